@@ -1,0 +1,82 @@
+/*
+ * syntropy_hip.h -- C ABI of the MI355X (gfx950) quantized-matmul and MoE kernels.
+ *
+ * Plain pointers and sizes only.  Device pointers are HIP device memory; `stream` is a
+ * hipStream_t (NULL = the default stream).  Every call only enqueues work on `stream`; it
+ * never synchronizes and never allocates device memory.  Each function returns SYN_OK (0)
+ * or an error code; the message of the last error on the calling thread is returned by
+ * syn_last_error().  A refused call enqueues nothing.
+ *
+ * Weight types are ggml's type ids: SYN_Q4_0 = 2, SYN_Q8_0 = 8, SYN_Q4_K = 12.  Weights are in
+ * GGUF's own block layout, one output row after another (LayoutVersion::SOURCE).
+ *
+ * Each entry point names the reference interface whose value it computes (paths relative to
+ * the reference repository root).  The provider-table boundary the reference's loader binds,
+ * `syntropy_provider_entry_v1`, is declared in syntropy_provider.h and is built on these.
+ */
+#ifndef SYNTROPY_HIP_H
+#define SYNTROPY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SYN_OK 0
+#define SYN_E_INVALID 1      /* malformed arguments: shape, type, alignment, null pointer */
+#define SYN_E_UNSUPPORTED 2  /* a weight type or shape these kernels do not take */
+#define SYN_E_WORKSPACE 3    /* the workspace is smaller than the call needs */
+#define SYN_E_DEVICE 4       /* the HIP runtime refused the launch */
+
+#define SYN_Q4_0 2
+#define SYN_Q8_0 8
+#define SYN_Q4_K 12
+
+/* The message of the last failed call on this thread ("" if none). */
+const char* syn_last_error(void);
+/* Library version: major * 10000 + minor * 100 + patch. */
+int syn_version(void);
+
+/* ---- Gemv -------------------------------------------------------------------------------
+ * Workspace bytes one syn_gemv call of `rows` activation rows of width `k_in` needs for the
+ * quantized activations.  Replaces crates/kernels-cpu/src/gemv/act.rs:108-111
+ * (workspace_bytes) as planned by crates/kernels-cpu/src/gemv/entry.rs:68-77. */
+int syn_gemv_workspace_bytes(int32_t wtype, uint32_t rows, uint32_t k_in, uint64_t* bytes);
+
+/* Quantizes x F32 [rows, k_in] into the workspace: Q8_0 blocks for Q4_0/Q8_0 weights, Q8_K
+ * for Q4_K.  Replaces crates/kernels-cpu/src/gemv/act.rs:122-167 (quantize_into).
+ * x: 16-byte aligned; ws: 256-byte aligned. */
+int syn_act_quantize(int32_t wtype, const float* x, uint32_t rows, uint32_t k_in, void* ws,
+                     uint64_t ws_bytes, void* stream);
+
+/* y F32 [rows, n_out] = W [n_out, k_in] x (activations already quantized into ws by
+ * syn_act_quantize for the same wtype, rows and k_in).  Replaces
+ * crates/kernels-cpu/src/gemv.rs:435-492 (gemv over every output row). */
+int syn_gemv_quantized(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                       uint32_t k_in, const void* ws, uint64_t ws_bytes, uint32_t rows,
+                       float* y, void* stream);
+
+/* The Gemv op: quantize x F32 [rows, k_in], then y F32 [rows, n_out] = W x.  Bit-identical to
+ * the reference CPU provider's launch, crates/kernels-cpu/src/gemv/entry.rs:167-247 (run). */
+int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uint32_t k_in,
+             const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
+             void* stream);
+
+/* ---- Weight packing ---------------------------------------------------------------------
+ * x F32 [n] -> GGUF blocks of wtype, byte-identical to ggml's reference quantizers
+ * (third_party/ggml/src/ggml-quants.c:113-140, 276-297, 1458-1528, wrapped by
+ * crates/kernels-ggml/src/lib.rs:268 quantize).  n must be whole blocks; the caller checks
+ * that every value is finite and at most 65504 in magnitude, as that wrapper does. */
+int syn_quantize(int32_t wtype, const float* x, uint64_t n, void* out, uint64_t out_bytes,
+                 void* stream);
+
+/* GGUF blocks -> F32, exact (crates/kernels/src/reference/dequant.rs:195-229). */
+int syn_dequantize(int32_t wtype, const void* src, uint64_t src_bytes, float* out,
+                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

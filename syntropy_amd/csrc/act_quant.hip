@@ -1,0 +1,146 @@
+// Activation quantization on gfx950: F32 rows -> the 8-bit blocks the GEMV kernels read.
+//
+// Q8_0 follows crates/kernels-cpu/src/gemv/act.rs:323-342 (ggml's arm64 quantizer, ties to
+// even, F16-rounded scale); Q8_K follows act.rs:351-373 (signed maximum, first on ties,
+// ggml's nearest_int).  A block holding a NaN or an infinity gets scale NaN and zero codes.
+// Both kernels also write the exact I32 sum of every 32 codes.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace syn {
+
+// One wavefront per 256-value block; lane l holds values 4l..4l+3.
+__global__ __launch_bounds__(256) void k_quant_q8k(const float* __restrict__ x, uint64_t nblk,
+                                                   int8_t* __restrict__ codes,
+                                                   float* __restrict__ dout,
+                                                   int32_t* __restrict__ sums) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t blk = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= nblk) return;
+    const float4 v4 = reinterpret_cast<const float4*>(x + blk * 256)[lane];
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    bool fin = finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]);
+    const bool all_finite = __all(fin);
+    // Largest magnitude, the first index on a tie: (amax desc, index asc).
+    float amax = 0.0f, mx = 0.0f;
+    int idx = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float a = __builtin_fabsf(v[i]);
+        if (a > amax) {
+            amax = a;
+            mx = v[i];
+            idx = lane * 4 + i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        float oa = __shfl_xor(amax, off);
+        float om = __shfl_xor(mx, off);
+        int oi = __shfl_xor(idx, off);
+        if (oa > amax || (oa == amax && oi < idx)) {
+            amax = oa;
+            mx = om;
+            idx = oi;
+        }
+    }
+    float d = 0.0f;
+    int q[4] = {0, 0, 0, 0};
+    if (!all_finite) {
+        d = __builtin_nanf("");
+    } else if (amax != 0.0f) {
+        const float iscale = -127.0f / mx;
+        if (finite_f(iscale)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                int t = nearest_int(iscale * v[i]);
+                q[i] = t < 127 ? t : 127;
+            }
+        }
+        d = 1.0f / iscale;
+    }
+    uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+                      ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
+    reinterpret_cast<uint32_t*>(codes + blk * 256)[lane] = packed;
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if ((lane & 7) == 0) sums[blk * 8 + (lane >> 3)] = s;
+    if (lane == 0) dout[blk] = d;
+}
+
+// Eight lanes per 32-value block, eight blocks per wavefront.
+__global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x, uint64_t nblk,
+                                                    int8_t* __restrict__ codes,
+                                                    float* __restrict__ dout,
+                                                    int32_t* __restrict__ sums) {
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint64_t blk = t >> 3;
+    const int sub = threadIdx.x & 7;
+    const bool live = blk < nblk;
+    float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) v4 = reinterpret_cast<const float4*>(x + blk * 32)[sub];
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    int bad = !(finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]));
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float a = __builtin_fabsf(v[i]);
+        amax = amax > a ? amax : a;
+    }
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1) {
+        float o = __shfl_xor(amax, off);
+        amax = amax > o ? amax : o;
+        bad |= __shfl_xor(bad, off);
+    }
+    int q[4] = {0, 0, 0, 0};
+    float dused;
+    if (bad) {
+        dused = __builtin_nanf("");
+    } else {
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        if (finite_f(id)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = (int)__builtin_rintf(v[i] * id);
+        }
+        dused = f16_to_f32(f16_bits(d));
+    }
+    if (!live) return;
+    uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+                      ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
+    reinterpret_cast<uint32_t*>(codes + blk * 32)[sub] = packed;
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if (sub == 0) {
+        sums[blk] = s;
+        dout[blk] = dused;
+    }
+}
+
+// The Q8_0 kernel leaves no per-32 sums for Q8_K; Q8_K's sums come from its own kernel.
+void launch_act_quant(int kind, const float* x, uint64_t rows, uint64_t k, uint8_t* ws,
+                      hipStream_t stream) {
+    const ActLayout L = act_layout(kind, rows, k);
+    int8_t* codes = reinterpret_cast<int8_t*>(ws + L.codes);
+    float* d = reinterpret_cast<float*>(ws + L.d);
+    int32_t* sums = reinterpret_cast<int32_t*>(ws + L.sums);
+    const uint64_t n = rows * k;
+    if (kind == ACT_Q8K) {
+        const uint64_t nblk = n / 256;
+        if (nblk == 0) return;
+        hipLaunchKernelGGL(k_quant_q8k, dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, stream, x,
+                           nblk, codes, d, sums);
+    } else if (kind == ACT_Q8_0) {
+        const uint64_t nblk = n / 32;
+        if (nblk == 0) return;
+        hipLaunchKernelGGL(k_quant_q8_0, dim3((unsigned)((nblk + 31) / 32)), dim3(256), 0, stream,
+                           x, nblk, codes, d, sums);
+    }
+}
+
+}  // namespace syn

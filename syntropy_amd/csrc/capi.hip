@@ -1,0 +1,151 @@
+// The C ABI (include/syntropy_hip.h): argument checks, then the kernel launchers.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/syntropy_hip.h"
+#include "kernels.hpp"
+
+#define SYN_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(SYN_E_DEVICE, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return SYN_OK;
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+bool gemv_type(int32_t t) { return t == SYN_Q4_0 || t == SYN_Q8_0 || t == SYN_Q4_K; }
+
+int check_gemv_shape(const char* what, int32_t wtype, uint32_t rows, uint32_t k_in) {
+    if (!gemv_type(wtype)) return fail(SYN_E_UNSUPPORTED, "%s: weight type %d is not Q4_0, Q8_0 or Q4_K", what, wtype);
+    const int be = syn::block_elems(wtype);
+    if (k_in % (uint32_t)be)
+        return fail(SYN_E_INVALID, "%s: a row of %u weights is not whole %d-weight blocks", what, k_in, be);
+    if ((uint64_t)rows * k_in > (1ull << 40)) return fail(SYN_E_INVALID, "%s: rows * k_in too large", what);
+    return SYN_OK;
+}
+
+}  // namespace
+
+SYN_EXPORT const char* syn_last_error(void) { return g_last_error.c_str(); }
+SYN_EXPORT int syn_version(void) { return 100; }
+
+SYN_EXPORT int syn_gemv_workspace_bytes(int32_t wtype, uint32_t rows, uint32_t k_in,
+                                        uint64_t* bytes) {
+    if (int rc = check_gemv_shape("syn_gemv_workspace_bytes", wtype, rows, k_in)) return rc;
+    if (!bytes) return fail(SYN_E_INVALID, "syn_gemv_workspace_bytes: null output");
+    *bytes = syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
+    return SYN_OK;
+}
+
+SYN_EXPORT int syn_act_quantize(int32_t wtype, const float* x, uint32_t rows, uint32_t k_in,
+                                void* ws, uint64_t ws_bytes, void* stream) {
+    const char* W = "syn_act_quantize";
+    if (int rc = check_gemv_shape(W, wtype, rows, k_in)) return rc;
+    const uint64_t need = syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
+    if ((uint64_t)rows * k_in == 0) return SYN_OK;
+    if (!x || !ws) return fail(SYN_E_INVALID, "%s: null x or workspace", W);
+    if (!aligned(x, 16) || !aligned(ws, 256))
+        return fail(SYN_E_INVALID, "%s: x must be 16-byte and the workspace 256-byte aligned", W);
+    if (ws_bytes < need)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)need);
+    syn::launch_act_quant(syn::act_kind(wtype), x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_gemv_quantized(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                                  uint32_t k_in, const void* ws, uint64_t ws_bytes, uint32_t rows,
+                                  float* y, void* stream) {
+    const char* W = "syn_gemv_quantized";
+    if (int rc = check_gemv_shape(W, wtype, rows, k_in)) return rc;
+    if (rows == 0 || n_out == 0) return SYN_OK;
+    if (n_out > (1u << 30)) return fail(SYN_E_INVALID, "%s: n_out too large", W);
+    const uint64_t row_bytes = (uint64_t)k_in / syn::block_elems(wtype) * syn::block_bytes(wtype);
+    const uint64_t need_w = row_bytes * n_out;
+    const uint64_t need_ws = syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
+    if (!y || (need_w && !w) || (need_ws && !ws)) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (w_bytes < need_w)
+        return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
+                    (unsigned long long)w_bytes, (unsigned long long)need_w);
+    if (ws_bytes < need_ws)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)need_ws);
+    if (!aligned(ws, 256) || !aligned(y, 4))
+        return fail(SYN_E_INVALID, "%s: the workspace must be 256-byte and y 4-byte aligned", W);
+    syn::launch_gemv_q(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows,
+                       y, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                        uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws,
+                        uint64_t ws_bytes, void* stream) {
+    const char* W = "syn_gemv";
+    if (int rc = check_gemv_shape(W, wtype, rows, k_in)) return rc;
+    if (rows == 0 || n_out == 0) return SYN_OK;
+    const uint64_t row_bytes = (uint64_t)k_in / syn::block_elems(wtype) * syn::block_bytes(wtype);
+    const uint64_t need_ws = syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
+    if (!y || (row_bytes * n_out && !w)) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (w_bytes < row_bytes * n_out)
+        return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
+                    (unsigned long long)w_bytes, (unsigned long long)(row_bytes * n_out));
+    if (ws_bytes < need_ws)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)need_ws);
+    if (k_in && (!x || !ws)) return fail(SYN_E_INVALID, "%s: null x or workspace", W);
+    if ((k_in && (!aligned(x, 16) || !aligned(ws, 256))) || !aligned(y, 4))
+        return fail(SYN_E_INVALID, "%s: x must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
+    if (k_in) {
+        syn::launch_act_quant(syn::act_kind(wtype), x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
+        if (int rc = check_launch(W)) return rc;
+    }
+    syn::launch_gemv_q(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows,
+                       y, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_quantize(int32_t wtype, const float* x, uint64_t n, void* out,
+                            uint64_t out_bytes, void* stream) {
+    const char* W = "syn_quantize";
+    if (!gemv_type(wtype)) return fail(SYN_E_UNSUPPORTED, "%s: weight type %d", W, wtype);
+    const int be = syn::block_elems(wtype);
+    if (n % (uint64_t)be) return fail(SYN_E_INVALID, "%s: %llu values are not whole %d-value blocks", W, (unsigned long long)n, be);
+    const uint64_t need = n / be * syn::block_bytes(wtype);
+    if (out_bytes < need) return fail(SYN_E_INVALID, "%s: output holds %llu bytes, needs %llu", W, (unsigned long long)out_bytes, (unsigned long long)need);
+    if (n == 0) return SYN_OK;
+    if (!x || !out) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!aligned(x, 4) || !aligned(out, 2)) return fail(SYN_E_INVALID, "%s: misaligned operand", W);
+    syn::launch_quantize(wtype, x, n, (uint8_t*)out, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_dequantize(int32_t wtype, const void* src, uint64_t src_bytes, float* out,
+                              void* stream) {
+    const char* W = "syn_dequantize";
+    if (!gemv_type(wtype)) return fail(SYN_E_UNSUPPORTED, "%s: weight type %d", W, wtype);
+    const int bb = syn::block_bytes(wtype);
+    if (src_bytes % (uint64_t)bb) return fail(SYN_E_INVALID, "%s: %llu bytes are not whole %d-byte blocks", W, (unsigned long long)src_bytes, bb);
+    if (src_bytes == 0) return SYN_OK;
+    if (!src || !out) return fail(SYN_E_INVALID, "%s: null operand", W);
+    syn::launch_dequantize(wtype, (const uint8_t*)src, src_bytes / bb * syn::block_elems(wtype), out,
+                           (hipStream_t)stream);
+    return check_launch(W);
+}

@@ -1,0 +1,127 @@
+// Device helpers shared by the gfx950 kernels of the quantized-matmul path.
+//
+// Every float operation here is one IEEE F32 operation: the library is compiled with
+// -ffp-contract=off, correctly rounded division and square root, and F32/F16 denormals kept,
+// so each helper gives the same bits as the reference function it cites.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SYN_DEV __device__ __forceinline__
+
+namespace syn {
+
+// GGUF type ids (ggml's enum ggml_type values).
+enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_BF16 = 30 };
+// Activation block kinds (crates/kernels-cpu/src/gemv/act.rs:31-39).
+enum : int { ACT_F32 = 0, ACT_Q8_0 = 1, ACT_Q8K = 2 };
+
+constexpr int WAVE = 64;
+
+SYN_DEV uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+SYN_DEV float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+SYN_DEV bool finite_f(float v) { return (f2u(v) & 0x7F800000u) != 0x7F800000u; }
+
+// Exact F16 -> F32 (v_cvt_f32_f16 with F16 denormals kept): the value of
+// crates/kernels/src/reference/act_quant.rs:448-467 for every non-NaN pattern.
+SYN_DEV float f16_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
+}
+
+// F32 -> F16 bits, round to nearest even with subnormals, NaN -> sign|0x7E00
+// (crates/kernels/src/reference/act_quant.rs:400-446), in integer arithmetic.
+SYN_DEV uint32_t f16_bits(float x) {
+    uint32_t b = f2u(x);
+    uint32_t sign = (b >> 16) & 0x8000u;
+    uint32_t a = b & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return sign | 0x7E00u;
+    if (a >= 0x477FF000u) return sign | 0x7C00u;
+    int e = (int)(a >> 23) - 127;
+    uint32_t mant = a & 0x007FFFFFu;
+    if (e >= -14) {
+        uint32_t base = ((uint32_t)(e + 15) << 10) | (mant >> 13);
+        uint32_t rem = mant & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (base & 1u))) base += 1;
+        return sign | base;
+    }
+    if (a < 0x00800000u) return sign;
+    uint32_t shift = (uint32_t)(-e - 1);
+    if (shift >= 40) return sign;
+    uint64_t sig = (uint64_t)(mant | 0x00800000u);
+    uint64_t base = sig >> shift;
+    uint64_t r = sig & ((1ull << shift) - 1);
+    uint64_t h = 1ull << (shift - 1);
+    if (r > h || (r == h && (base & 1))) base += 1;
+    return sign | (uint32_t)base;
+}
+
+// ggml's nearest_int (ggml-quants.c:621-626; kernels-cpu/src/gemv/act.rs:345-348).
+SYN_DEV int nearest_int(float f) {
+    float v = f + 12582912.f;
+    return (int)(f2u(v) & 0x007FFFFFu) - 0x00400000;
+}
+
+// get_scale_min_k4 (crates/kernels-cpu/src/gemv.rs:528-537) from the 12 packed bytes held in
+// three little-endian words.
+SYN_DEV void scales_k4(uint32_t w0, uint32_t w1, uint32_t w2, int* sc, int* mn) {
+    // bytes q[0..3] = w0, q[4..7] = w1, q[8..11] = w2
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t qj = (w0 >> (8 * j)) & 0xFFu;
+        uint32_t qj4 = (w1 >> (8 * j)) & 0xFFu;
+        uint32_t qj8 = (w2 >> (8 * j)) & 0xFFu;
+        sc[j] = (int)(qj & 63u);
+        mn[j] = (int)(qj4 & 63u);
+        sc[j + 4] = (int)((qj8 & 0xFu) | ((qj >> 6) << 4));
+        mn[j + 4] = (int)((qj8 >> 4) | ((qj4 >> 6) << 4));
+    }
+}
+
+// The reference's software exp (crates/kernels/src/reference/math.rs:45-75).
+SYN_DEV float pow2i(int k) { return u2f((uint32_t)(k + 127) << 23); }
+SYN_DEV float ref_exp(float x) {
+    const float LOG2_E = 1.44269504088896340736f;
+    const float LN2_HI = __builtin_bit_cast(float, 0x3F317200u);
+    const float LN2_LO = 1.4286068e-6f;
+    if (x != x) return x + x;
+    if (x > 88.72284f) return __builtin_inff();
+    if (x < -103.97208f) return 0.0f;
+    float kf = __builtin_rintf(x * LOG2_E);
+    float r = (x - kf * LN2_HI) - kf * LN2_LO;
+    float p = 1.0f / 5040.0f;
+    p = p * r + 1.0f / 720.0f;
+    p = p * r + 1.0f / 120.0f;
+    p = p * r + 1.0f / 24.0f;
+    p = p * r + 1.0f / 6.0f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    int k = (int)kf;
+    int k1 = k >> 1;  // floor division by 2 (Rust div_euclid(2)): arithmetic shift
+    return (p * pow2i(k1)) * pow2i(k - k1);
+}
+// silu(x) = x / (1 + exp(-x)) (math.rs:82-84).
+SYN_DEV float ref_silu(float x) { return x / (1.0f + ref_exp(-x)); }
+
+SYN_DEV int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Lane rotation by one inside groups of P lanes (the in-order fold hands its running sum to
+// the next lane of the group): quad_perm [3,0,1,2], row_ror:1, or wave_ror:1.
+template <int P>
+SYN_DEV float rot1(float v) {
+    int i = __builtin_bit_cast(int, v);
+    if constexpr (P == 4) {
+        i = __builtin_amdgcn_update_dpp(i, i, 0x93, 0xF, 0xF, false);
+    } else if constexpr (P == 16) {
+        i = __builtin_amdgcn_update_dpp(i, i, 0x121, 0xF, 0xF, false);
+    } else {
+        static_assert(P == 64, "P must be 4, 16 or 64");
+        i = __builtin_amdgcn_update_dpp(i, i, 0x13C, 0xF, 0xF, false);
+    }
+    return __builtin_bit_cast(float, i);
+}
+
+}  // namespace syn

@@ -1,0 +1,58 @@
+// Host-side geometry of the path: GGUF block sizes and the layout of the quantized
+// activations the GEMV kernels read.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace syn {
+
+inline int block_elems(int ty) {
+    switch (ty) {
+    case 1: case 30: return 1;     // F16, BF16
+    case 2: case 8: return 32;     // Q4_0, Q8_0
+    case 12: return 256;           // Q4_K
+    default: return 0;
+    }
+}
+inline int block_bytes(int ty) {
+    switch (ty) {
+    case 1: case 30: return 2;
+    case 2: return 18;
+    case 8: return 34;
+    case 12: return 144;
+    default: return 0;
+    }
+}
+// The activation block a product over weight type `ty` quantizes to
+// (crates/kernels-cpu/src/gemv.rs:145-151): Q8_0 for Q8_0/Q4_0, Q8_K for Q4_K.
+inline int act_kind(int ty) {
+    switch (ty) {
+    case 2: case 8: return 1;
+    case 12: return 2;
+    default: return 0;
+    }
+}
+inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+// Quantized activations of `rows` rows of `k` values in device memory.  The provider owns
+// this layout (the workspace is provider-declared scratch): codes first, then one F32 scale
+// per block, then one I32 code sum per 32 values; each section starts on 256 bytes.
+//   kind 1 (Q8_0): scale per 32 values; sums feed Q4_0's offset-8 term.
+//   kind 2 (Q8_K): scale per 256 values; sums feed Q4_K's minimum term.
+struct ActLayout {
+    uint64_t codes, d, sums, bytes;
+};
+inline ActLayout act_layout(int kind, uint64_t rows, uint64_t k) {
+    ActLayout l{0, 0, 0, 0};
+    if (kind == 0) return l;
+    uint64_t n = rows * k;
+    uint64_t nd = kind == 1 ? n / 32 : n / 256;
+    l.codes = 0;
+    l.d = align_up(n, 256);
+    l.sums = align_up(l.d + 4 * nd, 256);
+    l.bytes = align_up(l.sums + 4 * (n / 32), 256);
+    return l;
+}
+
+}  // namespace syn

@@ -1,0 +1,151 @@
+"""Decode GEMV on the MI355X, mirroring the reference CPU provider's `gemv` module
+(crates/kernels-cpu/src/gemv.rs, gemv/act.rs, gemv/entry.rs): the same names, argument
+meaning and refusals, over device tensors.  Every call runs the HIP kernels through the C ABI;
+there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from enum import IntEnum
+
+import torch
+
+from ._lib import SynError, call, lib
+
+
+class WeightType(IntEnum):
+    """A weight type this module computes (gemv.rs:87-151), by ggml type id."""
+
+    Q4_0 = 2
+    Q8_0 = 8
+    Q4K = 12
+
+    def block_elems(self) -> int:
+        return 256 if self is WeightType.Q4K else 32
+
+    def block_bytes(self) -> int:
+        return {WeightType.Q4_0: 18, WeightType.Q8_0: 34, WeightType.Q4K: 144}[self]
+
+    def act(self) -> str:
+        """The activation block a product over this type quantizes to (gemv.rs:145-151)."""
+        return "Q8K" if self is WeightType.Q4K else "Q8_0"
+
+
+class GemvError(ValueError):
+    """Why a GEMV call refused its inputs (gemv.rs:226-279).  A refused call writes nothing."""
+
+    def __init__(self, kind: str, msg: str):
+        super().__init__(f"Gemv: {msg}")
+        self.kind = kind
+
+
+@dataclass
+class Weights:
+    """`n_out` rows of `k_in` weights of type `ty` in GGUF block layout, in device memory
+    (gemv.rs:157-224).  `bytes` is a uint8 device tensor holding exactly the matrix."""
+
+    ty: WeightType
+    bytes: torch.Tensor
+    n_out: int
+    k_in: int
+
+    def __post_init__(self):
+        self.ty = WeightType(self.ty)
+        if self.k_in % self.ty.block_elems():
+            raise GemvError("RowLength", f"a row of {self.k_in} weights is not whole "
+                            f"{self.ty.block_elems()}-weight {self.ty.name} blocks")
+        need = self.row_bytes() * self.n_out
+        if self.bytes.dtype != torch.uint8 or self.bytes.numel() != need:
+            raise GemvError("Len", f"`weights` holds {self.bytes.numel()} values, the op needs {need}")
+
+    def row_bytes(self) -> int:
+        return self.k_in // self.ty.block_elems() * self.ty.block_bytes()
+
+
+def workspace_bytes(ty: WeightType, rows: int, k: int) -> int:
+    """Scratch bytes of one call's quantized activations (act.rs:108-111; the provider's own
+    layout: codes, scales, 32-value sums)."""
+    out = C.c_uint64()
+    call("syn_gemv_workspace_bytes", int(ty), rows, k, C.byref(out))
+    return out.value
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return getattr(stream, "cuda_stream", stream)
+
+
+def _check_x(x: torch.Tensor, rows: int, k: int):
+    if not (x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()):
+        raise GemvError("Len", "x must be a contiguous F32 device tensor")
+    if x.numel() < rows * k:
+        raise GemvError("Len", f"`x` holds {x.numel()} values, the op needs {rows * k}")
+
+
+def new_workspace(ty: WeightType, rows: int, k: int, device="cuda") -> torch.Tensor:
+    return torch.empty(max(workspace_bytes(ty, rows, k), 256), dtype=torch.uint8, device=device)
+
+
+def quantize_into(ty: WeightType, x: torch.Tensor, rows: int, k: int, ws: torch.Tensor,
+                  stream=None) -> None:
+    """Quantizes the first `rows` rows of x (k values each) into `ws` (act.rs:122-167)."""
+    ty = WeightType(ty)
+    if k % ty.block_elems():
+        raise GemvError("Activations", "k is not whole activation blocks")
+    _check_x(x, rows, k)
+    call("syn_act_quantize", int(ty), x.data_ptr(), rows, k, ws.data_ptr(), ws.numel(), _stream(stream))
+
+
+def gemv_quantized(w: Weights, ws: torch.Tensor, rows: int, y: torch.Tensor, stream=None) -> None:
+    """y[r][o] for every row r < rows and every output o (gemv.rs:435-492)."""
+    need = rows * w.n_out
+    if y.numel() < need:
+        raise GemvError("Len", f"`y` holds {y.numel()} values, the op needs {need}")
+    call("syn_gemv_quantized", int(w.ty), w.bytes.data_ptr(), w.bytes.numel(), w.n_out, w.k_in,
+         ws.data_ptr(), ws.numel(), rows, y.data_ptr(), _stream(stream))
+
+
+def gemv(w: Weights, x: torch.Tensor, rows: int, y: torch.Tensor | None = None,
+         ws: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """The Gemv op (gemv/entry.rs:167-247): quantize x F32 [rows, k_in], then
+    y F32 [rows, n_out] = W x, bit-identical to the reference CPU provider."""
+    _check_x(x, rows, w.k_in)
+    if y is None:
+        y = torch.empty(rows, w.n_out, dtype=torch.float32, device=x.device)
+    elif y.numel() < rows * w.n_out:
+        raise GemvError("Len", f"`y` holds {y.numel()} values, the op needs {rows * w.n_out}")
+    if ws is None:
+        ws = new_workspace(w.ty, rows, w.k_in, x.device)
+    call("syn_gemv", int(w.ty), w.bytes.data_ptr(), w.bytes.numel(), w.n_out, w.k_in,
+         x.data_ptr(), rows, y.data_ptr(), ws.data_ptr(), ws.numel(), _stream(stream))
+    return y
+
+
+def quantize(ty: WeightType, x: torch.Tensor, stream=None) -> torch.Tensor:
+    """F32 values -> GGUF blocks, byte-identical to ggml's reference quantizers
+    (crates/kernels-ggml/src/lib.rs:268 quantize).  Like that wrapper, refuses non-finite
+    values and magnitudes above 65504 (checked on the device, one reduction)."""
+    ty = WeightType(ty)
+    x = x.contiguous()
+    if x.numel() % ty.block_elems():
+        raise GemvError("RowLength", f"{x.numel()} values are not whole {ty.block_elems()}-value blocks")
+    if x.numel() and not bool(torch.isfinite(x).all() and x.abs().max() <= 65504.0):
+        raise GemvError("OutOfRange", "a value is not finite or is out of the type's range")
+    out = torch.empty(x.numel() // ty.block_elems() * ty.block_bytes(), dtype=torch.uint8, device=x.device)
+    call("syn_quantize", int(ty), x.data_ptr(), x.numel(), out.data_ptr(), out.numel(), _stream(stream))
+    return out
+
+
+def dequantize(ty: WeightType, src: torch.Tensor, stream=None) -> torch.Tensor:
+    """GGUF blocks -> F32, exact (dequant.rs:195-229)."""
+    ty = WeightType(ty)
+    out = torch.empty(src.numel() // ty.block_bytes() * ty.block_elems(), dtype=torch.float32,
+                      device=src.device)
+    call("syn_dequantize", int(ty), src.data_ptr(), src.numel(), out.data_ptr(), _stream(stream))
+    return out
+
+
+__all__ = ["WeightType", "Weights", "GemvError", "SynError", "workspace_bytes", "quantize_into",
+           "gemv_quantized", "gemv", "quantize", "dequantize", "new_workspace", "lib"]

@@ -1,0 +1,55 @@
+"""The C-ABI library loads and exports every function its public headers declare.
+
+CPU-only: loads the shared object and resolves symbols; makes no compute calls.
+"""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "syntropy_amd", "libsyntropy_hip.so")
+
+
+def declared_functions():
+    names = []
+    for h in sorted(glob.glob(os.path.join(ROOT, "include", "*.h"))):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\**\s*\**\s*([a-z][a-z0-9_]*)\s*\(",
+                             text, flags=re.M):
+            names.append(m.group(1))
+    return sorted(set(names))
+
+
+def test_headers_declare_functions():
+    names = declared_functions()
+    assert "syn_gemv" in names and "syn_last_error" in names
+
+
+def test_library_exports_every_declared_function():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} is not built: run python -m syntropy_amd.build")
+    import torch  # noqa: F401  one HIP runtime in the process
+    lib = ctypes.CDLL(LIB)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_version_and_errors_without_a_gpu():
+    import torch  # noqa: F401
+    lib = ctypes.CDLL(LIB)
+    lib.syn_version.restype = ctypes.c_int
+    assert lib.syn_version() >= 100
+    lib.syn_last_error.restype = ctypes.c_char_p
+    out = ctypes.c_uint64()
+    # a refused call (Q4_K rows of 100 values) reports through syn_last_error, touching no device
+    lib.syn_gemv_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32,
+                                             ctypes.POINTER(ctypes.c_uint64)]
+    assert lib.syn_gemv_workspace_bytes(12, 1, 100, ctypes.byref(out)) == 1
+    assert b"256" in lib.syn_last_error()
+    assert lib.syn_gemv_workspace_bytes(12, 1, 4096, ctypes.byref(out)) == 0
+    assert out.value >= 4096 + 16 * 4 + 128 * 4
+    assert lib.syn_gemv_workspace_bytes(7, 1, 4096, ctypes.byref(out)) == 2
