@@ -1,0 +1,247 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-matmul path on one MI355X.
+
+Headline workload: one Q4_K decode layer's matmuls at Llama-3-8B shapes, batch 1 (QKV
+6144x4096, O 4096x4096, gate and up 14336x4096, down 4096x14336).  One step quantizes each
+GEMV's F32 activation row to Q8_K and runs the five GEMVs: the reference's `Gemv` op five
+times.  Weights are N(0, 0.02) quantized by the GPU Q4_K packer (byte-identical to ggml's),
+in COPIES distinct copies that the steps rotate through, so the weights come from HBM and not
+from the 256 MB Infinity Cache.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only layer|copy] [--no-cpu]
+
+Prints one JSON line: whole-step weight GB/s (value), the roofline of the GEMV kernel from
+HIP events on its stream, and the CPU oracle timed on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q4_K GEMV weight GB/s (% HBM peak); MoE layer tokens/s at 64-token decode"
+HBM_PEAK_GBS = 8000.0
+LAYER = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate", 14336, 4096), ("up", 14336, 4096),
+         ("down", 4096, 14336)]
+Q4K = 12
+COPIES = 5
+
+
+def q4k_bytes(n_out, k):
+    return n_out * (k // 256) * 144
+
+
+def act_bytes(k):
+    # Q8_K codes + one F32 scale per 256 + one I32 sum per 32, read by the GEMV
+    return k + 4 * (k // 256) + 4 * (k // 32)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--only", choices=["layer", "copy"], default=None)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    return p.parse_args()
+
+
+def build_layer(torch, S, seed_base):
+    gen = torch.Generator(device="cuda")
+    copies = []
+    for c in range(COPIES):
+        mats = {}
+        for i, (name, n_out, k) in enumerate(LAYER):
+            gen.manual_seed(seed_base + 100 * c + i)
+            w = torch.randn(n_out * k, generator=gen, device="cuda", dtype=torch.float32) * 0.02
+            mats[name] = S.Weights(S.WeightType.Q4K, S.quantize(S.WeightType.Q4K, w), n_out, k)
+            del w
+        copies.append(mats)
+    gen.manual_seed(seed_base + 7)
+    xs = {name: torch.randn(k, generator=gen, device="cuda", dtype=torch.float32)
+          for name, _, k in LAYER}
+    ys = {name: torch.empty(n_out, device="cuda", dtype=torch.float32) for name, n_out, _ in LAYER}
+    wss = {name: S.new_workspace(S.WeightType.Q4K, 1, k) for name, _, k in LAYER}
+    return copies, xs, ys, wss
+
+
+def run_step_batched(batch, stream):
+    """One decode layer as one grouped launch pair (batched Q8_K quantization + grouped GEMV)."""
+    batch(stream=stream)
+
+
+def run_step(S, mats, xs, ys, wss, stream, events=None):
+    """One decode layer: five Gemv ops (F32 row in, Q8_K quantization fused, F32 row out)."""
+    for name, _, k in LAYER:
+        if events is not None:
+            events[name][0].record()
+        S.gemv(mats[name], xs[name], 1, y=ys[name], ws=wss[name], stream=stream)
+        if events is not None:
+            events[name][1].record()
+
+
+def cpu_baseline(torch, copies, xs, seconds):
+    """The oracle (C restatement of crates/kernels-cpu, multi-threaded by the reference's row
+    partition) over the same layer: bounded sample of `seconds` of repeated layers."""
+    from oracle import oracle as o
+    threads = min(16, os.cpu_count() or 1)
+    mats = copies[0]
+    w = {name: mats[name].bytes.cpu().numpy() for name, _, _ in LAYER}
+    x = {name: xs[name].cpu().numpy() for name, _, _ in LAYER}
+    total_w = sum(q4k_bytes(n, k) for _, n, k in LAYER)
+
+    def layer():
+        for name, n_out, k in LAYER:
+            o.gemv(o.Q4_K, w[name], n_out, k, x[name], 1, threads=threads)
+
+    layer()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        layer()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    t1 = time.perf_counter()
+    layer_single = None
+    for name, n_out, k in LAYER:  # one pass at one thread, for reference
+        o.gemv(o.Q4_K, w[name], n_out, k, x[name], 1, threads=1)
+    layer_single = time.perf_counter() - t1
+    return {
+        "value": round(total_w * n / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} Q4_K decode layers (5 GEMVs incl. Q8_K activation quantization) in "
+                  f"{dt:.1f} s on {threads} threads; one layer at 1 thread: "
+                  f"{layer_single * 1e3:.1f} ms",
+        "ms_per_layer": round(dt / n * 1e3, 3),
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one MI355X; --gpus {a.gpus} is not supported "
+              "(this build runs on one GPU only)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import syntropy_amd.gemv as S
+
+    assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+
+    if a.only == "copy":
+        # a plain copy of known size: calibrates the HBM byte counters
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel(), "launches": 5}))
+        return
+
+    copies, xs, ys, wss = build_layer(torch, S, 0x51A10003)
+    names = [name for name, _, _ in LAYER]
+    batches = [S.GemvBatch([c[n] for n in names], [xs[n] for n in names], [ys[n] for n in names])
+               for c in copies]
+    weight_bytes = sum(q4k_bytes(n, k) for _, n, k in LAYER)
+
+    # Headline: the layer's five Gemv ops as one grouped launch pair per step.
+    for i in range(a.warmup):
+        run_step_batched(batches[i % COPIES], stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        run_step_batched(batches[i % COPIES], stream)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    value = weight_bytes * a.steps / dt / 1e9
+
+    # The same five ops launched one by one (one launch each, quantization fused).
+    for i in range(a.warmup):
+        run_step(S, copies[i % COPIES], xs, ys, wss, stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for i in range(a.steps):
+        run_step(S, copies[i % COPIES], xs, ys, wss, stream)
+    torch.cuda.synchronize()
+    dt_ops = time.perf_counter() - t1
+
+    # Per-launch durations from HIP events on the launching stream: the grouped GEMV launch
+    # (the dominant kernel) and, for the one-by-one path, each Gemv op.
+    nrep = max(20, min(a.steps, 100))
+    evb = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(nrep)]
+    for i in range(nrep):
+        evb[i][0].record()
+        run_step_batched(batches[i % COPIES], stream)
+        evb[i][1].record()
+    torch.cuda.synchronize()
+    batch_ms = sum(e0.elapsed_time(e1) for e0, e1 in evb) / nrep
+    ev = [{name: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for name, _, _ in LAYER} for _ in range(nrep)]
+    for i in range(nrep):
+        run_step(S, copies[i % COPIES], xs, ys, wss, stream, events=ev[i])
+    torch.cuda.synchronize()
+    per = {name: sum(ev[i][name][0].elapsed_time(ev[i][name][1]) for i in range(nrep)) / nrep
+           for name, _, _ in LAYER}  # ms
+    # algorithmic bytes of the layer: weights + the F32 activation rows + the F32 outputs
+    alg_bytes = sum(q4k_bytes(n, k) + 4 * k + 4 * n for _, n, k in LAYER)
+    achieved = alg_bytes / (batch_ms * 1e-3) / 1e9
+
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "traffic_q4k_gemv_decode_layer.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(dt / a.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8xi8->i32, f32 terms",
+        "data": "synthetic: W ~ N(0,0.02) -> Q4_K (GPU packer, ggml-exact); x ~ N(0,1) F32",
+        "config": {
+            "workload": "Q4_K decode layer matmuls, Llama-3-8B shapes, batch 1: QKV 6144x4096, "
+                        "O 4096x4096, gate/up 14336x4096, down 4096x14336; Q8_K act quant + "
+                        "5 GEMVs per step",
+            "launch": "grouped: one batched Q8_K quantization + one grouped GEMV (syn_gemv_batch)",
+            "weight_bytes_per_step": weight_bytes,
+            "weight_copies_rotated": COPIES,
+            "hbm_fraction_of_peak": round(value / HBM_PEAK_GBS, 4),
+            "one_op_per_launch_gbs": round(weight_bytes * a.steps / dt_ops / 1e9, 2),
+            "one_op_per_launch_us": {k: round(v * 1e3, 3) for k, v in per.items()},
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_quant_q8k_batch + k_gemv_q4k_batch (one syn_gemv_batch call)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "alg_bytes_per_launch": alg_bytes,
+            "avg_launch_us": round(batch_ms * 1e3, 3),
+        },
+    }
+    if not a.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(torch, copies, xs, a.cpu_seconds)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

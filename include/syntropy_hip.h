@@ -64,6 +64,19 @@ int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uin
              const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
              void* stream);
 
+/* ---- Grouped decode -----------------------------------------------------------------------
+ * Up to 8 independent single-row Q4_K Gemv ops in two launches (one batched Q8_K quantization,
+ * one grouped GEMV): y[i] F32 [n_out[i]] = W[i] [n_out[i], k_in[i]] x[i], each bit-identical to
+ * syn_gemv on the same operands.  It computes what that many separate calls of the reference's
+ * Gemv launch compute (crates/kernels-cpu/src/gemv/entry.rs:167-247); the reference has no
+ * grouped form.  Host arrays of n entries; every wtypes[i] must be SYN_Q4_K and every k_in[i]
+ * at most 16384.  syn_gemv_batch_workspace_bytes gives the workspace the call needs. */
+int syn_gemv_batch_workspace_bytes(uint32_t n, const uint32_t* k_in, uint64_t* bytes);
+int syn_gemv_batch(uint32_t n, const int32_t* wtypes, const void* const* w,
+                   const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
+                   const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
+                   void* stream);
+
 /* ---- Weight packing ---------------------------------------------------------------------
  * x F32 [n] -> GGUF blocks of wtype, byte-identical to ggml's reference quantizers
  * (third_party/ggml/src/ggml-quants.c:113-140, 276-297, 1458-1528, wrapped by

@@ -43,6 +43,8 @@ def lib():
         "syn_gemv_quantized": [i32, vp, u64, u32, u32, vp, u64, u32, fp, vp],
         "syn_gemv": [i32, vp, u64, u32, u32, fp, u32, fp, vp, u64, vp],
         "syn_quantize": [i32, fp, u64, vp, u64, vp],
+        "syn_gemv_batch_workspace_bytes": [u32, vp, C.POINTER(C.c_uint64)],
+        "syn_gemv_batch": [u32, vp, vp, vp, vp, vp, vp, vp, vp, u64, vp],
         "syn_dequantize": [i32, vp, u64, fp, vp],
     }
     for name, args in sigs.items():

@@ -9,24 +9,19 @@
 
 namespace syn {
 
-// One wavefront per 256-value block; lane l holds values 4l..4l+3.
-__global__ __launch_bounds__(256) void k_quant_q8k(const float* __restrict__ x, uint64_t nblk,
-                                                   int8_t* __restrict__ codes,
-                                                   float* __restrict__ dout,
-                                                   int32_t* __restrict__ sums) {
-    const int lane = threadIdx.x & 63;
-    const uint64_t blk = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (blk >= nblk) return;
-    const float4 v4 = reinterpret_cast<const float4*>(x + blk * 256)[lane];
+// One 256-value block by one wavefront; lane l holds values 4l..4l+3.
+SYN_DEV void q8k_block_wave(const float* __restrict__ xb, int8_t* __restrict__ codes,
+                            float* __restrict__ dout, int32_t* __restrict__ sums, int lane) {
+    const float4 v4 = reinterpret_cast<const float4*>(xb)[lane];
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    bool fin = finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]);
+    const bool fin = finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]);
     const bool all_finite = __all(fin);
     // Largest magnitude, the first index on a tie: (amax desc, index asc).
     float amax = 0.0f, mx = 0.0f;
     int idx = 0x7FFFFFFF;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        float a = __builtin_fabsf(v[i]);
+        const float a = __builtin_fabsf(v[i]);
         if (a > amax) {
             amax = a;
             mx = v[i];
@@ -35,9 +30,9 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float* __restrict__ x, 
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
-        float oa = __shfl_xor(amax, off);
-        float om = __shfl_xor(mx, off);
-        int oi = __shfl_xor(idx, off);
+        const float oa = __shfl_xor(amax, off);
+        const float om = __shfl_xor(mx, off);
+        const int oi = __shfl_xor(idx, off);
         if (oa > amax || (oa == amax && oi < idx)) {
             amax = oa;
             mx = om;
@@ -53,21 +48,30 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float* __restrict__ x, 
         if (finite_f(iscale)) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                int t = nearest_int(iscale * v[i]);
+                const int t = nearest_int(iscale * v[i]);
                 q[i] = t < 127 ? t : 127;
             }
         }
         d = 1.0f / iscale;
     }
-    uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
-                      ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
-    reinterpret_cast<uint32_t*>(codes + blk * 256)[lane] = packed;
+    const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+                            ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
+    reinterpret_cast<uint32_t*>(codes)[lane] = packed;
     int s = q[0] + q[1] + q[2] + q[3];
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
     s += __shfl_xor(s, 4);
-    if ((lane & 7) == 0) sums[blk * 8 + (lane >> 3)] = s;
-    if (lane == 0) dout[blk] = d;
+    if ((lane & 7) == 0) sums[lane >> 3] = s;
+    if (lane == 0) *dout = d;
+}
+
+__global__ __launch_bounds__(256) void k_quant_q8k(const float* __restrict__ x, uint64_t nblk,
+                                                   int8_t* __restrict__ codes,
+                                                   float* __restrict__ dout,
+                                                   int32_t* __restrict__ sums) {
+    const uint64_t blk = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= nblk) return;
+    q8k_block_wave(x + blk * 256, codes + blk * 256, dout + blk, sums + blk * 8, threadIdx.x & 63);
 }
 
 // Eight lanes per 32-value block, eight blocks per wavefront.
@@ -120,6 +124,46 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x,
         sums[blk] = s;
         dout[blk] = dused;
     }
+}
+
+// Several single rows at once: problem p takes workgroups [wg_begin[p], wg_begin[p+1]), one
+// wavefront per 256-value block, each into its own workspace.
+struct QuantBatch {
+    const float* x[SYN_BATCH];
+    uint8_t* ws[SYN_BATCH];
+    int nblk[SYN_BATCH];
+    int wg_begin[SYN_BATCH + 1];
+    int np;
+};
+
+__global__ __launch_bounds__(256) void k_quant_q8k_batch(QuantBatch qb) {
+    int p = 0;
+    while (p + 1 < qb.np && (int)blockIdx.x >= qb.wg_begin[p + 1]) ++p;
+    const int blk = ((int)blockIdx.x - qb.wg_begin[p]) * 4 + (threadIdx.x >> 6);
+    const int nblk = qb.nblk[p];
+    if (blk >= nblk) return;
+    const ActLayout L = act_layout(ACT_Q8K, 1, (uint64_t)nblk * 256);
+    uint8_t* ws = qb.ws[p];
+    q8k_block_wave(qb.x[p] + (int64_t)blk * 256, reinterpret_cast<int8_t*>(ws + L.codes) + (int64_t)blk * 256,
+                   reinterpret_cast<float*>(ws + L.d) + blk,
+                   reinterpret_cast<int32_t*>(ws + L.sums) + (int64_t)blk * 8, threadIdx.x & 63);
+}
+
+void launch_act_quant_batch(int np, const float* const* x, const int* k, uint8_t* const* ws,
+                            hipStream_t stream) {
+    QuantBatch qb{};
+    qb.np = np;
+    int wg = 0;
+    for (int p = 0; p < np; ++p) {
+        qb.x[p] = x[p];
+        qb.ws[p] = ws[p];
+        qb.nblk[p] = k[p] / 256;
+        qb.wg_begin[p] = wg;
+        wg += (qb.nblk[p] + 3) / 4;
+    }
+    qb.wg_begin[np] = wg;
+    if (wg == 0) return;
+    hipLaunchKernelGGL(k_quant_q8k_batch, dim3(wg), dim3(256), 0, stream, qb);
 }
 
 // The Q8_0 kernel leaves no per-32 sums for Q8_K; Q8_K's sums come from its own kernel.

@@ -90,8 +90,12 @@ SYN_EXPORT int syn_gemv_quantized(int32_t wtype, const void* w, uint64_t w_bytes
                     (unsigned long long)ws_bytes, (unsigned long long)need_ws);
     if (!aligned(ws, 256) || !aligned(y, 4))
         return fail(SYN_E_INVALID, "%s: the workspace must be 256-byte and y 4-byte aligned", W);
-    syn::launch_gemv_q(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows,
-                       y, (hipStream_t)stream);
+    if (wtype == SYN_Q4_K && rows == 1 && k_in > 0 && syn::q4k_dec_supported((int)k_in) && aligned(w, 16))
+        syn::launch_gemv_q4k_dec_ws((const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, y,
+                                    (hipStream_t)stream);
+    else
+        syn::launch_gemv_q(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws,
+                           (int)rows, y, (hipStream_t)stream);
     return check_launch(W);
 }
 
@@ -113,12 +117,76 @@ SYN_EXPORT int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t
     if (k_in && (!x || !ws)) return fail(SYN_E_INVALID, "%s: null x or workspace", W);
     if ((k_in && (!aligned(x, 16) || !aligned(ws, 256))) || !aligned(y, 4))
         return fail(SYN_E_INVALID, "%s: x must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
+    if (wtype == SYN_Q4_K && rows == 1 && k_in > 0 && syn::q4k_dec_supported((int)k_in) && aligned(w, 16)) {
+        // one launch: the workgroups quantize the row into LDS themselves
+        syn::launch_gemv_q4k_dec_f32((const uint8_t*)w, (int)n_out, (int)k_in, x, y, (hipStream_t)stream);
+        return check_launch(W);
+    }
     if (k_in) {
         syn::launch_act_quant(syn::act_kind(wtype), x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
         if (int rc = check_launch(W)) return rc;
     }
     syn::launch_gemv_q(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows,
                        y, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_gemv_batch_workspace_bytes(uint32_t n, const uint32_t* k_in, uint64_t* bytes) {
+    const char* W = "syn_gemv_batch_workspace_bytes";
+    if (n > SYN_BATCH) return fail(SYN_E_UNSUPPORTED, "%s: at most %d problems", W, SYN_BATCH);
+    if (!bytes || (n && !k_in)) return fail(SYN_E_INVALID, "%s: null argument", W);
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (k_in[i] % 256) return fail(SYN_E_INVALID, "%s: k_in[%u] = %u is not whole 256-weight blocks", W, i, k_in[i]);
+        total += syn::act_layout(syn::ACT_Q8K, 1, k_in[i]).bytes;
+    }
+    *bytes = total;
+    return SYN_OK;
+}
+
+SYN_EXPORT int syn_gemv_batch(uint32_t n, const int32_t* wtypes, const void* const* w,
+                              const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
+                              const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
+                              void* stream) {
+    const char* W = "syn_gemv_batch";
+    if (n == 0) return SYN_OK;
+    if (n > SYN_BATCH) return fail(SYN_E_UNSUPPORTED, "%s: at most %d problems", W, SYN_BATCH);
+    if (!wtypes || !w || !w_bytes || !n_out || !k_in || !x || !y)
+        return fail(SYN_E_INVALID, "%s: null argument array", W);
+    uint64_t need = 0;
+    if (int rc = syn_gemv_batch_workspace_bytes(n, k_in, &need)) return rc;
+    if (ws_bytes < need)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)need);
+    if (!ws || !aligned(ws, 256)) return fail(SYN_E_INVALID, "%s: the workspace must be 256-byte aligned", W);
+    const uint8_t* wp[SYN_BATCH];
+    const uint8_t* wsp[SYN_BATCH];
+    uint8_t* wsm[SYN_BATCH];
+    const float* xp[SYN_BATCH];
+    float* yp[SYN_BATCH];
+    int no[SYN_BATCH], kk[SYN_BATCH];
+    uint64_t off = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (wtypes[i] != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: problem %u is not Q4_K", W, i);
+        if (k_in[i] == 0 || k_in[i] > 16384) return fail(SYN_E_UNSUPPORTED, "%s: k_in[%u] = %u (1..16384)", W, i, k_in[i]);
+        if (n_out[i] == 0 || n_out[i] > (1u << 28)) return fail(SYN_E_INVALID, "%s: n_out[%u] = %u", W, i, n_out[i]);
+        const uint64_t need_w = (uint64_t)k_in[i] / 256 * 144 * n_out[i];
+        if (w_bytes[i] < need_w) return fail(SYN_E_INVALID, "%s: weight %u holds %llu bytes, the matrix %llu", W, i, (unsigned long long)w_bytes[i], (unsigned long long)need_w);
+        if (!w[i] || !x[i] || !y[i]) return fail(SYN_E_INVALID, "%s: null operand in problem %u", W, i);
+        if (!aligned(w[i], 16) || !aligned(x[i], 16) || !aligned(y[i], 4))
+            return fail(SYN_E_INVALID, "%s: problem %u: W and x must be 16-byte, y 4-byte aligned", W, i);
+        wp[i] = (const uint8_t*)w[i];
+        wsm[i] = (uint8_t*)ws + off;
+        wsp[i] = wsm[i];
+        xp[i] = x[i];
+        yp[i] = y[i];
+        no[i] = (int)n_out[i];
+        kk[i] = (int)k_in[i];
+        off += syn::act_layout(syn::ACT_Q8K, 1, k_in[i]).bytes;
+    }
+    syn::launch_act_quant_batch((int)n, xp, kk, wsm, (hipStream_t)stream);
+    if (int rc = check_launch(W)) return rc;
+    syn::launch_gemv_q4k_batch((int)n, wp, no, kk, wsp, yp, (hipStream_t)stream);
     return check_launch(W);
 }
 

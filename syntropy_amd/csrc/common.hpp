@@ -8,14 +8,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "layout.hpp"
+
 #define SYN_DEV __device__ __forceinline__
 
 namespace syn {
-
-// GGUF type ids (ggml's enum ggml_type values).
-enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_BF16 = 30 };
-// Activation block kinds (crates/kernels-cpu/src/gemv/act.rs:31-39).
-enum : int { ACT_F32 = 0, ACT_Q8_0 = 1, ACT_Q8K = 2 };
 
 constexpr int WAVE = 64;
 

@@ -1,0 +1,342 @@
+// Decode GEMV for Q4_K weights, one activation row: the path's headline kernel.
+//
+// Value: crates/kernels-cpu/src/gemv.rs:539-547 (q4k_term) folded in ascending super-block
+// order from +0.0 (gemv/portable.rs:114-190), bit for bit.
+//
+// Design (gfx950):
+//  * A wavefront owns one 4-row group: 16 lanes per output row, lane j takes super-blocks
+//    j, j+16, j+32, ... ("rounds") of its row.  Each lane loads its 144-byte super-block straight
+//    into registers with nine 16-byte loads; with more than one round the next round's block is
+//    loaded into the other half of a register ping-pong before the current one is computed.
+//    The rounds are unrolled and every load is unconditional (an idle lane reloads the matrix's
+//    first block), so the compiler's wait counts stay exact and a wavefront always has a block
+//    in flight.
+//  * The weight loads of the first round are issued before the workgroup prepares the
+//    activation row, so HBM latency overlaps that prologue.
+//  * The activation row lives in LDS for the whole workgroup: quantized to Q8_K in the
+//    prologue (FUSE = 1: the Gemv op, F32 row in, one launch) or copied from a workspace
+//    quantized earlier (FUSE = 0).  Column c's codes sit at c*272 bytes (a 16-byte skew per
+//    column), so the 16 columns a wavefront reads at once fall in distinct banks.
+//  * The 16 terms of a row are folded in order by passing the running sum from lane to lane
+//    with DPP row_ror:1, once per round.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace syn {
+
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr int COL = 272;  // LDS bytes per activation column (256 codes + 16-byte skew)
+constexpr int SUMW = 48;  // LDS bytes per column of 32-value sums (8 ints + skew)
+
+SYN_DEV int xs_off(int nb) { return nb * COL; }
+SYN_DEV int xd_off(int nb) { return nb * (COL + SUMW); }
+
+template <int NT>
+SYN_DEV v4u ldw(const uint8_t* p) {
+    if constexpr (NT)
+        return __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    else
+        return *reinterpret_cast<const v4u*>(p);
+}
+
+// Q8_K of the activation row into LDS (crates/kernels-cpu/src/gemv/act.rs:351-373): 16 lanes
+// per 256-value super-block, 16 values per lane.  Largest magnitude, first index on ties.
+SYN_DEV void quant_row_to_lds(const float* __restrict__ x, int nb, uint8_t* lds) {
+    const int t = threadIdx.x;
+    for (int c = t; c < nb * 16; c += 256) {  // the 16 lanes of a super-block stay together
+        const int sb = c >> 4, part = c & 15;
+        const float4* src = reinterpret_cast<const float4*>(x + (int64_t)sb * 256 + part * 16);
+        const float4 a0 = src[0], a1 = src[1], a2 = src[2], a3 = src[3];
+        const float v[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                             a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+        bool fin = true;
+        float amax = 0.0f, mx = 0.0f;
+        int idx = 0x7FFFFFFF;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            fin = fin && finite_f(v[i]);
+            const float av = __builtin_fabsf(v[i]);
+            if (av > amax) {
+                amax = av;
+                mx = v[i];
+                idx = part * 16 + i;
+            }
+        }
+        int bad = !fin;
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) {
+            const float oa = __shfl_xor(amax, off);
+            const float om = __shfl_xor(mx, off);
+            const int oi = __shfl_xor(idx, off);
+            bad |= __shfl_xor(bad, off);
+            if (oa > amax || (oa == amax && oi < idx)) {
+                amax = oa;
+                mx = om;
+                idx = oi;
+            }
+        }
+        float d = 0.0f;
+        int q[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) q[i] = 0;
+        if (bad) {
+            d = __builtin_nanf("");
+        } else if (amax != 0.0f) {
+            const float iscale = -127.0f / mx;
+            if (finite_f(iscale)) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int n = nearest_int(iscale * v[i]);
+                    q[i] = n < 127 ? n : 127;
+                }
+            }
+            d = 1.0f / iscale;
+        }
+        uint32_t w[4];
+        int s = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            w[k] = (uint32_t)(q[4 * k] & 0xFF) | ((uint32_t)(q[4 * k + 1] & 0xFF) << 8) |
+                   ((uint32_t)(q[4 * k + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * k + 3] & 0xFF) << 24);
+            s += q[4 * k] + q[4 * k + 1] + q[4 * k + 2] + q[4 * k + 3];
+        }
+        v4u pk = {w[0], w[1], w[2], w[3]};
+        *reinterpret_cast<v4u*>(lds + sb * COL + part * 16) = pk;
+        s += __shfl_xor(s, 1);  // the two 16-value halves of a 32-value group
+        if ((part & 1) == 0) reinterpret_cast<int*>(lds + xs_off(nb) + sb * SUMW)[part >> 1] = s;
+        if (part == 0) reinterpret_cast<float*>(lds + xd_off(nb))[sb] = d;
+    }
+}
+
+SYN_DEV void copy_row_to_lds(const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                             const int32_t* __restrict__ xs, int nb, uint8_t* lds) {
+    for (int i = threadIdx.x; i < nb * 16; i += 256) {
+        const int c = i >> 4, p = i & 15;
+        *reinterpret_cast<v4u*>(lds + c * COL + p * 16) =
+            *reinterpret_cast<const v4u*>(xq + (int64_t)c * 256 + p * 16);
+    }
+    for (int i = threadIdx.x; i < nb * 2; i += 256) {
+        const int c = i >> 1, p = i & 1;
+        *reinterpret_cast<v4u*>(lds + xs_off(nb) + c * SUMW + p * 16) =
+            *reinterpret_cast<const v4u*>(xs + (int64_t)c * 8 + p * 4);
+    }
+    for (int i = threadIdx.x; i < nb; i += 256) reinterpret_cast<float*>(lds + xd_off(nb))[i] = xd[i];
+}
+
+// One super-block's term from its nine 16-byte words and activation column b in LDS.
+SYN_DEV float q4k_term_lds(const v4u* wv, const uint8_t* lds, int nb, int b) {
+    uint32_t wb[36];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+        wb[4 * i] = wv[i].x;
+        wb[4 * i + 1] = wv[i].y;
+        wb[4 * i + 2] = wv[i].z;
+        wb[4 * i + 3] = wv[i].w;
+    }
+    int sc[8], mn[8];
+    scales_k4(wb[1], wb[2], wb[3], sc, mn);
+    const float d = f16_to_f32(wb[0]), dmin = f16_to_f32(wb[0] >> 16);
+    const uint8_t* xc = lds + b * COL;
+    int s1 = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const v4u xl0 = *reinterpret_cast<const v4u*>(xc + 64 * g);
+        const v4u xl1 = *reinterpret_cast<const v4u*>(xc + 64 * g + 16);
+        const v4u xh0 = *reinterpret_cast<const v4u*>(xc + 64 * g + 32);
+        const v4u xh1 = *reinterpret_cast<const v4u*>(xc + 64 * g + 48);
+        const uint32_t xl[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
+        const uint32_t xh[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t q = wb[4 + 8 * g + t];
+            lo = sdot4(q & 0x0F0F0F0Fu, xl[t], lo);
+            hi = sdot4((q >> 4) & 0x0F0F0F0Fu, xh[t], hi);
+        }
+        s1 += sc[2 * g] * lo + sc[2 * g + 1] * hi;
+    }
+    const int4 sa = *reinterpret_cast<const int4*>(lds + xs_off(nb) + b * SUMW);
+    const int4 sb = *reinterpret_cast<const int4*>(lds + xs_off(nb) + b * SUMW + 16);
+    const float dx = reinterpret_cast<const float*>(lds + xd_off(nb))[b];
+    const int s2 = mn[0] * sa.x + mn[1] * sa.y + mn[2] * sa.z + mn[3] * sa.w + mn[4] * sb.x +
+                   mn[5] * sb.y + mn[6] * sb.z + mn[7] * sb.w;
+    return (d * dx) * (float)s1 - (dmin * dx) * (float)s2;
+}
+
+}  // namespace
+
+// The 4-row group of one wavefront: rows row0 + lane/16.  NR = ceil(nb / 16) rounds, fixed at
+// compile time so the body is straight-line code.  `A` holds round 0, already in flight.
+template <int NT, int NR>
+SYN_DEV void rowgroup_body(const uint8_t* __restrict__ W, int n_out, int nb, int row,
+                           const uint8_t* lds, v4u* A, float* __restrict__ y) {
+    const int j = threadIdx.x & 15;
+    const int64_t row_bytes = (int64_t)nb * 144;
+    const bool row_ok = row < n_out;
+    auto blk = [&](int r) {
+        const int b = r * 16 + j;
+        const bool ok = row_ok && b < nb;
+        return ok ? W + (int64_t)row * row_bytes + (int64_t)b * 144 : W;
+    };
+    v4u B[9];
+    float acc = 0.0f;
+    auto consume = [&](const v4u* buf, int r) {
+        const int b = r * 16 + j;
+        const bool ok = row_ok && b < nb;
+        const float t = q4k_term_lds(buf, lds, nb, ok ? b : 0);
+        const float tv = ok ? t : 0.0f;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            acc = rot1<16>(acc);
+            acc = acc + ((j == s) ? tv : 0.0f);
+        }
+    };
+#pragma unroll
+    for (int r = 0; r < NR; r += 2) {
+        if (r + 1 < NR) {
+            const uint8_t* p = blk(r + 1);
+#pragma unroll
+            for (int i = 0; i < 9; ++i) B[i] = ldw<NT>(p + 16 * i);
+        }
+        consume(A, r);
+        if (r + 2 < NR) {
+            const uint8_t* p = blk(r + 2);
+#pragma unroll
+            for (int i = 0; i < 9; ++i) A[i] = ldw<NT>(p + 16 * i);
+        }
+        if (r + 1 < NR) consume(B, r + 1);
+    }
+    if (j == 15 && row_ok) y[row] = acc;
+}
+
+template <int NT>
+SYN_DEV void load_round0(const uint8_t* __restrict__ W, int n_out, int nb, int row, v4u* A) {
+    const int j = threadIdx.x & 15;
+    const bool ok = row < n_out && j < nb;
+    const uint8_t* p = ok ? W + (int64_t)row * nb * 144 + (int64_t)j * 144 : W;
+#pragma unroll
+    for (int i = 0; i < 9; ++i) A[i] = ldw<NT>(p + 16 * i);
+}
+
+template <int FUSE, int NT, int NR>
+__global__ __launch_bounds__(256) void k_gemv_q4k_dec(const uint8_t* __restrict__ W, int n_out,
+                                                      int nb, const float* __restrict__ xf,
+                                                      const int8_t* __restrict__ xq,
+                                                      const float* __restrict__ xd,
+                                                      const int32_t* __restrict__ xs,
+                                                      float* __restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = (blockIdx.x * 4 + wave) * 4 + (lane >> 4);
+    v4u A[9];
+    load_round0<NT>(W, n_out, nb, row, A);  // in flight while the activation row is prepared
+    if constexpr (FUSE)
+        quant_row_to_lds(xf, nb, lds);
+    else
+        copy_row_to_lds(xq, xd, xs, nb, lds);
+    __syncthreads();
+    rowgroup_body<NT, NR>(W, n_out, nb, row, lds, A, y);
+}
+
+// Up to SYN_BATCH independent single-row GEMVs in one launch: problem p takes workgroups
+// [wg_begin[p], wg_begin[p+1]); its activation row was quantized into ws[p] beforehand.
+struct DecBatch {
+    const uint8_t* W[SYN_BATCH];
+    const uint8_t* ws[SYN_BATCH];
+    float* y[SYN_BATCH];
+    int n_out[SYN_BATCH];
+    int nb[SYN_BATCH];
+    int wg_begin[SYN_BATCH + 1];
+    int np;
+};
+
+template <int NT>
+__global__ __launch_bounds__(256) void k_gemv_q4k_batch(DecBatch bt) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    int p = 0;
+    while (p + 1 < bt.np && (int)blockIdx.x >= bt.wg_begin[p + 1]) ++p;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint8_t* W = bt.W[p];
+    const int n_out = bt.n_out[p], nb = bt.nb[p];
+    const int row = (((int)blockIdx.x - bt.wg_begin[p]) * 4 + wave) * 4 + (lane >> 4);
+    v4u A[9];
+    load_round0<NT>(W, n_out, nb, row, A);
+    const ActLayout L = act_layout(ACT_Q8K, 1, (uint64_t)nb * 256);
+    copy_row_to_lds(reinterpret_cast<const int8_t*>(bt.ws[p] + L.codes),
+                    reinterpret_cast<const float*>(bt.ws[p] + L.d),
+                    reinterpret_cast<const int32_t*>(bt.ws[p] + L.sums), nb, lds);
+    __syncthreads();
+    if (nb <= 16)
+        rowgroup_body<NT, 1>(W, n_out, nb, row, lds, A, bt.y[p]);
+    else if (nb <= 32)
+        rowgroup_body<NT, 2>(W, n_out, nb, row, lds, A, bt.y[p]);
+    else if (nb <= 64)
+        rowgroup_body<NT, 4>(W, n_out, nb, row, lds, A, bt.y[p]);
+    else
+        rowgroup_body<NT, 8>(W, n_out, nb, row, lds, A, bt.y[p]);
+}
+
+static size_t q4k_dec_lds(int nb) { return (size_t)nb * (COL + SUMW + 4); }
+
+// K up to 32768: at most 8 rounds, and the activation row within 41 KB of LDS.
+bool q4k_dec_supported(int k) { return k % 256 == 0 && k > 0 && k <= 32768; }
+
+template <int FUSE>
+static void launch_dec(const uint8_t* W, int n_out, int nb, const float* xf, const int8_t* xq,
+                       const float* xd, const int32_t* xs, float* y, hipStream_t stream) {
+    const int total_rg = (n_out + 3) / 4;
+    const dim3 grid((unsigned)((total_rg + 3) / 4));
+    const size_t lds = q4k_dec_lds(nb);
+#define SYN_DEC(NR)                                                                         \
+    hipLaunchKernelGGL((k_gemv_q4k_dec<FUSE, 0, NR>), grid, dim3(256), lds, stream, W, n_out, nb, \
+                       xf, xq, xd, xs, y)
+    switch ((nb + 15) / 16) {
+    case 1: SYN_DEC(1); break;
+    case 2: SYN_DEC(2); break;
+    case 3: SYN_DEC(3); break;
+    case 4: SYN_DEC(4); break;
+    case 5: SYN_DEC(5); break;
+    case 6: SYN_DEC(6); break;
+    case 7: SYN_DEC(7); break;
+    default: SYN_DEC(8); break;
+    }
+#undef SYN_DEC
+}
+
+void launch_gemv_q4k_dec_f32(const uint8_t* W, int n_out, int k, const float* x, float* y,
+                             hipStream_t stream) {
+    launch_dec<1>(W, n_out, k / 256, x, nullptr, nullptr, nullptr, y, stream);
+}
+
+void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* ws, float* y,
+                            hipStream_t stream) {
+    const ActLayout L = act_layout(ACT_Q8K, 1, (uint64_t)k);
+    launch_dec<0>(W, n_out, k / 256, nullptr, reinterpret_cast<const int8_t*>(ws + L.codes),
+                  reinterpret_cast<const float*>(ws + L.d),
+                  reinterpret_cast<const int32_t*>(ws + L.sums), y, stream);
+}
+
+void launch_gemv_q4k_batch(int np, const uint8_t* const* W, const int* n_out, const int* k,
+                           const uint8_t* const* ws, float* const* y, hipStream_t stream) {
+    DecBatch bt{};
+    bt.np = np;
+    int wg = 0, max_nb = 0;
+    for (int p = 0; p < np; ++p) {
+        bt.W[p] = W[p];
+        bt.ws[p] = ws[p];
+        bt.y[p] = y[p];
+        bt.n_out[p] = n_out[p];
+        bt.nb[p] = k[p] / 256;
+        bt.wg_begin[p] = wg;
+        wg += ((n_out[p] + 3) / 4 + 3) / 4;
+        if (bt.nb[p] > max_nb) max_nb = bt.nb[p];
+    }
+    bt.wg_begin[np] = wg;
+    if (wg == 0) return;
+    hipLaunchKernelGGL((k_gemv_q4k_batch<0>), dim3(wg), dim3(256), q4k_dec_lds(max_nb), stream, bt);
+}
+
+}  // namespace syn

@@ -5,7 +5,18 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#if defined(__HIPCC__)
+#define SYN_HD __host__ __device__
+#else
+#define SYN_HD
+#endif
+
 namespace syn {
+
+// GGUF type ids (ggml's enum ggml_type values).
+enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_BF16 = 30 };
+// Activation block kinds (crates/kernels-cpu/src/gemv/act.rs:31-39).
+enum : int { ACT_F32 = 0, ACT_Q8_0 = 1, ACT_Q8K = 2 };
 
 inline int block_elems(int ty) {
     switch (ty) {
@@ -33,7 +44,7 @@ inline int act_kind(int ty) {
     default: return 0;
     }
 }
-inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+SYN_HD inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
 // Quantized activations of `rows` rows of `k` values in device memory.  The provider owns
 // this layout (the workspace is provider-declared scratch): codes first, then one F32 scale
@@ -43,7 +54,7 @@ inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 struct ActLayout {
     uint64_t codes, d, sums, bytes;
 };
-inline ActLayout act_layout(int kind, uint64_t rows, uint64_t k) {
+SYN_HD inline ActLayout act_layout(int kind, uint64_t rows, uint64_t k) {
     ActLayout l{0, 0, 0, 0};
     if (kind == 0) return l;
     uint64_t n = rows * k;

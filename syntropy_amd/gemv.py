@@ -123,6 +123,42 @@ def gemv(w: Weights, x: torch.Tensor, rows: int, y: torch.Tensor | None = None,
     return y
 
 
+class GemvBatch:
+    """Up to 8 independent single-row Q4_K Gemv ops launched together (one batched Q8_K
+    quantization, one grouped GEMV): each y[i] equals gemv(ws[i], x[i], 1) bit for bit.  The
+    argument arrays are built once; `__call__` launches."""
+
+    def __init__(self, weights: list[Weights], xs: list[torch.Tensor], ys: list[torch.Tensor],
+                 ws: torch.Tensor | None = None):
+        n = len(weights)
+        if not (n == len(xs) == len(ys)) or n > 8:
+            raise GemvError("Len", "GemvBatch takes up to 8 (weights, x, y) triples")
+        for w, x, y in zip(weights, xs, ys):
+            if w.ty is not WeightType.Q4K:
+                raise GemvError("Activations", "GemvBatch takes Q4_K weights")
+            _check_x(x, 1, w.k_in)
+            if y.numel() < w.n_out:
+                raise GemvError("Len", f"`y` holds {y.numel()} values, the op needs {w.n_out}")
+        self.n = n
+        u32 = C.c_uint32 * n
+        self.k = u32(*[w.k_in for w in weights])
+        self.n_out = u32(*[w.n_out for w in weights])
+        self.ty = (C.c_int32 * n)(*[int(w.ty) for w in weights])
+        self.w = (C.c_void_p * n)(*[w.bytes.data_ptr() for w in weights])
+        self.wb = (C.c_uint64 * n)(*[w.bytes.numel() for w in weights])
+        self.x = (C.c_void_p * n)(*[x.data_ptr() for x in xs])
+        self.y = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
+        need = C.c_uint64()
+        call("syn_gemv_batch_workspace_bytes", n, self.k, C.byref(need))
+        self.ws = ws if ws is not None else torch.empty(max(need.value, 256), dtype=torch.uint8,
+                                                        device=xs[0].device)
+        self._keep = (weights, xs, ys)
+
+    def __call__(self, stream=None) -> None:
+        call("syn_gemv_batch", self.n, self.ty, self.w, self.wb, self.n_out, self.k, self.x,
+             self.y, self.ws.data_ptr(), self.ws.numel(), _stream(stream))
+
+
 def quantize(ty: WeightType, x: torch.Tensor, stream=None) -> torch.Tensor:
     """F32 values -> GGUF blocks, byte-identical to ggml's reference quantizers
     (crates/kernels-ggml/src/lib.rs:268 quantize).  Like that wrapper, refuses non-finite
@@ -147,5 +183,5 @@ def dequantize(ty: WeightType, src: torch.Tensor, stream=None) -> torch.Tensor:
     return out
 
 
-__all__ = ["WeightType", "Weights", "GemvError", "SynError", "workspace_bytes", "quantize_into",
+__all__ = ["WeightType", "Weights", "GemvError", "SynError", "GemvBatch", "workspace_bytes", "quantize_into",
            "gemv_quantized", "gemv", "quantize", "dequantize", "new_workspace", "lib"]

@@ -134,17 +134,18 @@ def test_gemv_unaligned_weights(S, ty):
     """gemv/tests.rs:799-817: weights at an odd address give the same bits."""
     rng = GemvRng(13)
     k = gemv_widths(ty)[2]
-    n_out, rows = 9, 3
+    n_out = 9
     w = gemv_weights(rng, ty, n_out, k, o.f16_bits, o.round_bf16)
-    x = gemv_activations(rng, rows, k)
-    want = o.gemv(ty, w, n_out, k, x, rows)
-    xd = dev(x)
-    for shift in (1, 2, 3):
-        announce(f"gemv unaligned ty={ty} shift={shift}")
-        buf = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda")
-        buf[shift:shift + w.size] = dev(w)
-        W = S.Weights(ty, buf[shift:shift + w.size], n_out, k)
-        assert_same(host(S.gemv(W, xd, rows)), want, f"shift {shift}")
+    for rows in (1, 3):
+        x = gemv_activations(rng, rows, k)
+        want = o.gemv(ty, w, n_out, k, x, rows)
+        xd = dev(x)
+        for shift in (1, 2, 3, 16):
+            announce(f"gemv unaligned ty={ty} rows={rows} shift={shift}")
+            buf = torch.zeros(w.size + 32, dtype=torch.uint8, device="cuda")
+            buf[shift:shift + w.size] = dev(w)
+            W = S.Weights(ty, buf[shift:shift + w.size], n_out, k)
+            assert_same(host(S.gemv(W, xd, rows)), want, f"rows {rows} shift {shift}")
 
 
 def test_gemv_edge_cases(S):
@@ -218,6 +219,47 @@ def test_gemv_config_shapes_bit_exact(S, name, ty, n_out, k, rowss):
         want = o.gemv(ty, w, n_out, k, x, rows, threads=8)
         got = host(S.gemv(S.Weights(ty, wd, n_out, k), dev(x), rows))
         assert_same(got, want, f"{name} rows {rows}")
+
+
+@pytest.mark.parametrize("k", [256, 1536, 4096, 14336])
+def test_gemv_q4k_decode_paths_agree(S, k):
+    """The one-launch Q4_K decode path (activation row quantized in LDS) and the two-launch
+    path (quantize into the workspace, then GEMV) equal the oracle, for every K of the configs."""
+    n_out = 300
+    w = normal_weights(o.Q4_K, n_out, k, 0x51A30000 + k)
+    x = o.normal(0x51A40000 + k, 1.0, k)
+    want = o.gemv(o.Q4_K, w, n_out, k, x, 1)
+    W = S.Weights(S.WeightType.Q4K, dev(w), n_out, k)
+    announce(f"q4k decode fused k={k}")
+    assert_same(host(S.gemv(W, dev(x), 1)), want, "fused")
+    ws = S.new_workspace(S.WeightType.Q4K, 1, k)
+    S.quantize_into(S.WeightType.Q4K, dev(x), 1, k, ws)
+    y = torch.empty(n_out, device="cuda")
+    announce(f"q4k decode ws k={k}")
+    S.gemv_quantized(W, ws, 1, y)
+    assert_same(host(y), want, "workspace")
+
+
+def test_gemv_batch_layer_shapes(S):
+    """The grouped decode launch equals the oracle on every problem of a Q4_K decode layer
+    (Llama-3-8B shapes, output rows cut to keep the oracle quick) plus odd shapes."""
+    shapes = [(6144, 4096), (4096, 4096), (14336, 4096), (14336, 4096), (4096, 14336),
+              (37, 256), (5, 1536), (1, 16384)]
+    Ws, xs, ys, want = [], [], [], []
+    for i, (n_out, k) in enumerate(shapes):
+        n = min(n_out, 1024)
+        w = normal_weights(o.Q4_K, n, k, 0x51A50000 + i)
+        x = o.normal(0x51A60000 + i, 1.0, k)
+        want.append(o.gemv(o.Q4_K, w, n, k, x, 1))
+        Ws.append(S.Weights(S.WeightType.Q4K, dev(w), n, k))
+        xs.append(dev(x))
+        ys.append(torch.full((n,), float("nan"), device="cuda"))
+    announce("gemv batch layer")
+    batch = S.GemvBatch(Ws, xs, ys)
+    for rep in range(3):
+        batch()
+        for i in range(len(shapes)):
+            assert_same(host(ys[i]), want[i], f"problem {i} rep {rep}")
 
 
 # ---- weight packing and dequant ----------------------------------------------------------
