@@ -77,6 +77,50 @@ int syn_gemv_batch(uint32_t n, const int32_t* wtypes, const void* const* w,
                    const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
                    void* stream);
 
+/* ---- MoE layer ----------------------------------------------------------------------------
+ * MoeRoute{Softmax}: ids I32 [rows, top_k] and weights F32 [rows, top_k] from x F32
+ * [rows, hidden] and the router F32 [n_experts, hidden].  Logits are F32Fixed dot products
+ * (crates/kernels/src/reference/reduce.rs:30-90), softmax subtracts the row maximum and uses the
+ * reference's software exp (crates/kernels/src/reference/math.rs:45-75), top-k by probability
+ * with the lower expert index on ties, then each selected probability is divided by their
+ * in-order sum when `renormalize`.  The reference has no code for this op: it is its
+ * specification (plan/rfcs/RFC-0042-quantization-and-numerical-fidelity.md:232,281; the op
+ * kind crates/kernels/src/op/kind.rs:35-42, IR signature crates/graph/src/ir/signature.rs:149).
+ * probs (optional, F32 [rows, n_experts]) receives the softmax. */
+int syn_moe_route(const float* router, const float* x, uint32_t rows, uint32_t hidden,
+                  uint32_t n_experts, uint32_t top_k, int32_t renormalize, int32_t* ids, float* w,
+                  float* probs, void* stream);
+
+/* Packing of the rows*top_k route slots by expert, stable in slot order: offsets u32
+ * [n_experts + 1] and slots u32 [rows * top_k], bit-identical to the counting sort of
+ * crates/kernels-cpu/src/moe.rs:431-457.  err (device u32[2]): err[0] is 1 when an id is
+ * outside [0, n_experts), else 0; err[1] is the largest expert's slot count. */
+int syn_moe_pack(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
+                 uint32_t* offsets, uint32_t* slots, uint32_t* err, void* stream);
+
+/* MoeGrouped: out F32 [rows, top_k, hidden], each slot its expert's SwiGLU FFN of its row
+ * alone, bit-identical to crates/kernels-cpu/src/moe.rs:402-551 (moe_grouped) for Q4_K experts.
+ * gate, up: [n_experts][inter, hidden] and down: [n_experts][hidden, inter], GGUF Q4_K, stacked
+ * by expert (ffn_*_exps); expert_bytes_each is the size of one stacked matrix.  Binding:
+ * crates/kernels-cpu/src/moe/entry.rs:6-27.  An id outside [0, n_experts) writes nothing and
+ * sets *status (device u32, optional) to 1, as the reference refuses the call
+ * (moe.rs:433-441). */
+int syn_moe_grouped_workspace_bytes(int32_t wtype, uint32_t n_experts, uint32_t top_k,
+                                    uint32_t hidden, uint32_t inter, uint32_t rows,
+                                    uint64_t* bytes);
+int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, const void* down,
+                    uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k,
+                    uint32_t hidden, uint32_t inter, const float* x, const int32_t* ids,
+                    uint32_t rows, float* out, void* ws, uint64_t ws_bytes, uint32_t* status,
+                    void* stream);
+
+/* MoeCombine: y F32 [rows, hidden] = per row, the slots of out F32 [rows, top_k, hidden] in
+ * ascending expert id, y += w * v from +0.0 without fused multiply-add
+ * (crates/kernels-cpu/src/moe/tests.rs:541-556; IR signature
+ * crates/graph/src/ir/signature.rs:153). */
+int syn_moe_combine(const float* out, const int32_t* ids, const float* w, uint32_t rows,
+                    uint32_t top_k, uint32_t hidden, float* y, void* stream);
+
 /* ---- Weight packing ---------------------------------------------------------------------
  * x F32 [n] -> GGUF blocks of wtype, byte-identical to ggml's reference quantizers
  * (third_party/ggml/src/ggml-quants.c:113-140, 276-297, 1458-1528, wrapped by

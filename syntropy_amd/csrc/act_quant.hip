@@ -9,62 +9,6 @@
 
 namespace syn {
 
-// One 256-value block by one wavefront; lane l holds values 4l..4l+3.
-SYN_DEV void q8k_block_wave(const float* __restrict__ xb, int8_t* __restrict__ codes,
-                            float* __restrict__ dout, int32_t* __restrict__ sums, int lane) {
-    const float4 v4 = reinterpret_cast<const float4*>(xb)[lane];
-    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    const bool fin = finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]);
-    const bool all_finite = __all(fin);
-    // Largest magnitude, the first index on a tie: (amax desc, index asc).
-    float amax = 0.0f, mx = 0.0f;
-    int idx = 0x7FFFFFFF;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = __builtin_fabsf(v[i]);
-        if (a > amax) {
-            amax = a;
-            mx = v[i];
-            idx = lane * 4 + i;
-        }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float oa = __shfl_xor(amax, off);
-        const float om = __shfl_xor(mx, off);
-        const int oi = __shfl_xor(idx, off);
-        if (oa > amax || (oa == amax && oi < idx)) {
-            amax = oa;
-            mx = om;
-            idx = oi;
-        }
-    }
-    float d = 0.0f;
-    int q[4] = {0, 0, 0, 0};
-    if (!all_finite) {
-        d = __builtin_nanf("");
-    } else if (amax != 0.0f) {
-        const float iscale = -127.0f / mx;
-        if (finite_f(iscale)) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = nearest_int(iscale * v[i]);
-                q[i] = t < 127 ? t : 127;
-            }
-        }
-        d = 1.0f / iscale;
-    }
-    const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
-                            ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
-    reinterpret_cast<uint32_t*>(codes)[lane] = packed;
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
-    if ((lane & 7) == 0) sums[lane >> 3] = s;
-    if (lane == 0) *dout = d;
-}
-
 __global__ __launch_bounds__(256) void k_quant_q8k(const float* __restrict__ x, uint64_t nblk,
                                                    int8_t* __restrict__ codes,
                                                    float* __restrict__ dout,

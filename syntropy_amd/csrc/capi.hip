@@ -217,3 +217,142 @@ SYN_EXPORT int syn_dequantize(int32_t wtype, const void* src, uint64_t src_bytes
                            (hipStream_t)stream);
     return check_launch(W);
 }
+
+// ============================================================================================
+// MoE
+// ============================================================================================
+
+namespace {
+
+// Workspace of syn_moe_grouped: offsets, slots, the error word, the packed entries' Q8_K
+// activations, the entries' h rows and their Q8_K; every section on 256 bytes.
+struct MoeWs {
+    uint64_t offsets, slots, err, xq, h, hq, bytes;
+};
+MoeWs moe_ws(uint32_t n_experts, uint32_t top_k, uint32_t hidden, uint32_t inter, uint32_t rows) {
+    MoeWs m{};
+    const uint64_t ent = (uint64_t)rows * top_k;
+    uint64_t o = 0;
+    m.offsets = o;
+    o = syn::align_up(o + 4ull * (n_experts + 1), 256);
+    m.slots = o;
+    o = syn::align_up(o + 4ull * ent, 256);
+    m.err = o;  // error word, then the largest expert's entry count
+    o = syn::align_up(o + 8, 256);
+    m.xq = o;
+    o += syn::act_layout(syn::ACT_Q8K, ent, hidden).bytes;
+    m.h = o;
+    o = syn::align_up(o + 4ull * ent * inter, 256);
+    m.hq = o;
+    o += syn::act_layout(syn::ACT_Q8K, ent, inter).bytes;
+    m.bytes = syn::align_up(o, 256);
+    return m;
+}
+
+int check_moe_shape(const char* W, uint32_t n_experts, uint32_t top_k, uint32_t hidden,
+                    uint32_t inter, uint32_t rows) {
+    if (n_experts == 0 || n_experts > 256) return fail(SYN_E_UNSUPPORTED, "%s: n_experts %u (1..256)", W, n_experts);
+    if (top_k == 0 || top_k > n_experts || top_k > 32) return fail(SYN_E_UNSUPPORTED, "%s: top_k %u (1..min(n_experts, 32))", W, top_k);
+    if (hidden % 256 || inter % 256 || hidden == 0 || inter == 0)
+        return fail(SYN_E_INVALID, "%s: hidden %u and inter %u must be whole 256-weight blocks", W, hidden, inter);
+    if (hidden > 65536 || inter > 65536) return fail(SYN_E_UNSUPPORTED, "%s: hidden/inter above 65536", W);
+    if ((uint64_t)rows * top_k > 65536) return fail(SYN_E_UNSUPPORTED, "%s: rows * top_k above 65536", W);
+    return SYN_OK;
+}
+
+}  // namespace
+
+SYN_EXPORT int syn_moe_route(const float* router, const float* x, uint32_t rows, uint32_t hidden,
+                             uint32_t n_experts, uint32_t top_k, int32_t renormalize,
+                             int32_t* ids, float* w, float* probs, void* stream) {
+    const char* W = "syn_moe_route";
+    if (n_experts == 0 || n_experts > 256) return fail(SYN_E_UNSUPPORTED, "%s: n_experts %u (1..256)", W, n_experts);
+    if (top_k == 0 || top_k > n_experts || top_k > 32) return fail(SYN_E_UNSUPPORTED, "%s: top_k %u", W, top_k);
+    if (hidden % 32 || hidden == 0 || hidden > 16384) return fail(SYN_E_UNSUPPORTED, "%s: hidden %u (whole 32-blocks, at most 16384)", W, hidden);
+    if (rows == 0) return SYN_OK;
+    if (!router || !x || !ids || !w) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!aligned(router, 16) || !aligned(x, 4)) return fail(SYN_E_INVALID, "%s: router must be 16-byte aligned", W);
+    syn::launch_moe_route(router, x, (int)rows, (int)hidden, (int)n_experts, (int)top_k, renormalize != 0,
+                          ids, w, probs, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_moe_pack(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
+                            uint32_t* offsets, uint32_t* slots, uint32_t* err, void* stream) {
+    const char* W = "syn_moe_pack";
+    if (n_experts == 0 || n_experts > 256) return fail(SYN_E_UNSUPPORTED, "%s: n_experts %u (1..256)", W, n_experts);
+    if ((uint64_t)rows * top_k > 65536) return fail(SYN_E_UNSUPPORTED, "%s: rows * top_k above 65536", W);
+    if (!ids || !offsets || !slots || !err) return fail(SYN_E_INVALID, "%s: null operand", W);
+    syn::launch_moe_pack(ids, (int)(rows * top_k), (int)n_experts, offsets, slots, err, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_moe_grouped_workspace_bytes(int32_t wtype, uint32_t n_experts, uint32_t top_k,
+                                               uint32_t hidden, uint32_t inter, uint32_t rows,
+                                               uint64_t* bytes) {
+    const char* W = "syn_moe_grouped_workspace_bytes";
+    if (wtype != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: expert weight type %d (Q4_K)", W, wtype);
+    if (int rc = check_moe_shape(W, n_experts, top_k, hidden, inter, rows)) return rc;
+    if (!bytes) return fail(SYN_E_INVALID, "%s: null output", W);
+    *bytes = moe_ws(n_experts, top_k, hidden, inter, rows).bytes;
+    return SYN_OK;
+}
+
+SYN_EXPORT int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, const void* down,
+                               uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k,
+                               uint32_t hidden, uint32_t inter, const float* x, const int32_t* ids,
+                               uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
+                               uint32_t* status, void* stream) {
+    const char* W = "syn_moe_grouped";
+    if (wtype != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: expert weight type %d (Q4_K)", W, wtype);
+    if (int rc = check_moe_shape(W, n_experts, top_k, hidden, inter, rows)) return rc;
+    if (rows == 0) return SYN_OK;
+    const uint64_t mat = (uint64_t)inter * (hidden / 256) * 144;  // gate/up; down is the same size
+    if (expert_bytes_each < mat * n_experts)
+        return fail(SYN_E_INVALID, "%s: each stacked matrix holds %llu bytes, the experts need %llu", W,
+                    (unsigned long long)expert_bytes_each, (unsigned long long)(mat * n_experts));
+    const MoeWs m = moe_ws(n_experts, top_k, hidden, inter, rows);
+    if (ws_bytes < m.bytes)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)m.bytes);
+    if (!gate || !up || !down || !x || !ids || !out || !ws) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!aligned(gate, 16) || !aligned(up, 16) || !aligned(down, 16) || !aligned(x, 16) || !aligned(ws, 256) || !aligned(out, 4))
+        return fail(SYN_E_INVALID, "%s: weights and x must be 16-byte, the workspace 256-byte aligned", W);
+    uint8_t* base = (uint8_t*)ws;
+    uint32_t* offsets = (uint32_t*)(base + m.offsets);
+    uint32_t* slots = (uint32_t*)(base + m.slots);
+    uint32_t* err = (uint32_t*)(base + m.err);
+    const int ent = (int)(rows * top_k);
+    hipStream_t st = (hipStream_t)stream;
+    syn::launch_moe_pack(ids, ent, (int)n_experts, offsets, slots, err, st);
+    const syn::ActLayout LX = syn::act_layout(syn::ACT_Q8K, ent, hidden);
+    const syn::ActLayout LH = syn::act_layout(syn::ACT_Q8K, ent, inter);
+    syn::QAct ax{(const int8_t*)(base + m.xq + LX.codes), (const float*)(base + m.xq + LX.d),
+                 (const int32_t*)(base + m.xq + LX.sums)};
+    syn::QAct ah{(const int8_t*)(base + m.hq + LH.codes), (const float*)(base + m.hq + LH.d),
+                 (const int32_t*)(base + m.hq + LH.sums)};
+    syn::launch_moe_gather_q8k(x, slots, ent, (int)top_k, (int)hidden, err, (int8_t*)ax.codes, (float*)ax.d,
+                               (int32_t*)ax.sums, 1, st);
+    float* h = (float*)(base + m.h);
+    syn::launch_moe_gateup((const uint8_t*)gate, (const uint8_t*)up, (int)n_experts, (int)hidden, (int)inter,
+                           offsets, ent, ax, err, h, st);
+    syn::launch_moe_gather_q8k(h, slots, ent, (int)top_k, (int)inter, err, (int8_t*)ah.codes, (float*)ah.d,
+                               (int32_t*)ah.sums, 0, st);
+    syn::launch_moe_down((const uint8_t*)down, (int)n_experts, (int)hidden, (int)inter, offsets, ent, ah,
+                         slots, err, out, st);
+    if (status) {
+        hipError_t e = hipMemcpyAsync(status, err, 4, hipMemcpyDeviceToDevice, st);
+        if (e != hipSuccess) return fail(SYN_E_DEVICE, "%s: status copy: %s", W, hipGetErrorString(e));
+    }
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_moe_combine(const float* out, const int32_t* ids, const float* w, uint32_t rows,
+                               uint32_t top_k, uint32_t hidden, float* y, void* stream) {
+    const char* W = "syn_moe_combine";
+    if (top_k == 0 || top_k > 64) return fail(SYN_E_UNSUPPORTED, "%s: top_k %u (1..64)", W, top_k);
+    if (rows == 0 || hidden == 0) return SYN_OK;
+    if (!out || !ids || !w || !y) return fail(SYN_E_INVALID, "%s: null operand", W);
+    syn::launch_moe_combine(out, ids, w, (int)rows, (int)top_k, (int)hidden, y, (hipStream_t)stream);
+    return check_launch(W);
+}

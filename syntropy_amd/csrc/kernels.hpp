@@ -26,6 +26,28 @@ void launch_gemv_q4k_batch(int np, const uint8_t* const* W, const int* n_out, co
                            const uint8_t* const* ws, float* const* y, hipStream_t stream);
 void launch_act_quant_batch(int np, const float* const* x, const int* k, uint8_t* const* ws,
                             hipStream_t stream);
+// moe.hip
+struct QAct {  // Q8_K activations of the packed entries, entry-major
+    const int8_t* codes;
+    const float* d;
+    const int32_t* sums;
+};
+void launch_moe_route(const float* router, const float* x, int rows, int hidden, int n_experts,
+                      int top_k, int renorm, int32_t* ids, float* w, float* probs,
+                      hipStream_t stream);
+void launch_moe_pack(const int32_t* ids, int nslots, int n_experts, uint32_t* offsets,
+                     uint32_t* slots, uint32_t* err, hipStream_t stream);
+void launch_moe_gather_q8k(const float* x, const uint32_t* slots, int nentries, int top_k, int k,
+                           const uint32_t* err, int8_t* codes, float* d, int32_t* sums, int gather,
+                           hipStream_t stream);
+void launch_moe_gateup(const uint8_t* gate, const uint8_t* up, int n_experts, int hidden,
+                       int inter, const uint32_t* offsets, int nentries, QAct a,
+                       const uint32_t* err, float* h, hipStream_t stream);
+void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
+                     const uint32_t* offsets, int nentries, QAct a, const uint32_t* slots,
+                     const uint32_t* err, float* out, hipStream_t stream);
+void launch_moe_combine(const float* out, const int32_t* ids, const float* w, int rows, int top_k,
+                        int hidden, float* y, hipStream_t stream);
 // quant.hip
 void launch_quantize(int ty, const float* x, uint64_t n, uint8_t* out, hipStream_t stream);
 void launch_dequantize(int ty, const uint8_t* src, uint64_t n, float* out, hipStream_t stream);

@@ -1,0 +1,137 @@
+"""The MoE layer on the MI355X, mirroring the reference CPU provider's `moe` module
+(crates/kernels-cpu/src/moe.rs) and the MoeRoute / MoeCombine ops (crates/kernels/src/op/kind.rs,
+crates/graph/src/blocks/ffn.rs:127-200): route -> pack -> grouped expert FFN -> combine, every
+step a HIP kernel behind the C ABI.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from ._lib import call
+from .gemv import GemvError, WeightType, _stream
+
+
+@dataclass(frozen=True)
+class MoeShape:
+    """The layer's MoE shape: MoeGrouped's dims [n_experts, top_k, hidden, inter]
+    (crates/kernels-cpu/src/moe.rs:89-101)."""
+
+    n_experts: int
+    top_k: int
+    hidden: int
+    inter: int
+
+
+class MoeError(ValueError):
+    """Why a MoE call refused its inputs (moe.rs:148-166).  A refused call writes nothing."""
+
+
+@dataclass
+class Experts:
+    """One layer's experts in GGUF block layout, stacked by expert (ffn_gate_exps,
+    ffn_up_exps, ffn_down_exps): gate/up [n_experts][inter, hidden], down
+    [n_experts][hidden, inter], uint8 device tensors of one weight type."""
+
+    ty: WeightType
+    gate: torch.Tensor
+    up: torch.Tensor
+    down: torch.Tensor
+
+    def check(self, s: MoeShape):
+        ty = WeightType(self.ty)
+        if ty is not WeightType.Q4K:
+            raise MoeError("MoeGrouped on the GPU takes Q4_K experts")
+        need = s.n_experts * s.inter * (s.hidden // 256) * 144
+        for name, t in (("gate", self.gate), ("up", self.up), ("down", self.down)):
+            if t.dtype != torch.uint8 or t.numel() != need:
+                raise MoeError(f"`{name}` holds {t.numel()} bytes, the experts need {need}")
+
+
+def route(router: torch.Tensor, x: torch.Tensor, top_k: int, renormalize: bool = True,
+          probs: bool = False, stream=None):
+    """MoeRoute{Softmax}: (ids I32 [rows, k], weights F32 [rows, k][, probs])."""
+    n_experts, hidden = router.shape
+    rows = x.shape[0]
+    ids = torch.empty(rows, top_k, dtype=torch.int32, device=x.device)
+    w = torch.empty(rows, top_k, dtype=torch.float32, device=x.device)
+    p = torch.empty(rows, n_experts, dtype=torch.float32, device=x.device) if probs else None
+    call("syn_moe_route", router.data_ptr(), x.data_ptr(), rows, hidden, n_experts, top_k,
+         int(renormalize), ids.data_ptr(), w.data_ptr(), p.data_ptr() if p is not None else None,
+         _stream(stream))
+    return (ids, w, p) if probs else (ids, w)
+
+
+def pack(ids: torch.Tensor, n_experts: int, stream=None):
+    """(offsets u32 [E+1], slots u32 [rows*k], err u32 [2]) as int32 tensors: err[0] = bad id,
+    err[1] = the largest expert's slot count."""
+    rows, top_k = ids.shape
+    offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=ids.device)
+    slots = torch.empty(rows * top_k, dtype=torch.int32, device=ids.device)
+    err = torch.empty(2, dtype=torch.int32, device=ids.device)
+    call("syn_moe_pack", ids.data_ptr(), rows, top_k, n_experts, offsets.data_ptr(),
+         slots.data_ptr(), err.data_ptr(), _stream(stream))
+    return offsets, slots, err
+
+
+def workspace_bytes(s: MoeShape, rows: int, ty: WeightType = WeightType.Q4K) -> int:
+    out = C.c_uint64()
+    call("syn_moe_grouped_workspace_bytes", int(ty), s.n_experts, s.top_k, s.hidden, s.inter, rows,
+         C.byref(out))
+    return out.value
+
+
+def moe_grouped(s: MoeShape, experts: Experts, x: torch.Tensor, ids: torch.Tensor,
+                out: torch.Tensor | None = None, ws: torch.Tensor | None = None,
+                status: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """MoeGrouped (moe.rs:402-518): out F32 [rows, top_k, hidden]."""
+    experts.check(s)
+    rows = ids.shape[0]
+    if ids.shape != (rows, s.top_k) or ids.dtype != torch.int32:
+        raise MoeError("ids must be I32 [rows, top_k]")
+    if x.dtype != torch.float32 or x.numel() < rows * s.hidden or not x.is_contiguous():
+        raise MoeError("x must be contiguous F32 [rows, hidden]")
+    if out is None:
+        out = torch.empty(rows, s.top_k, s.hidden, dtype=torch.float32, device=x.device)
+    if ws is None:
+        ws = torch.empty(max(workspace_bytes(s, rows), 256), dtype=torch.uint8, device=x.device)
+    call("syn_moe_grouped", int(experts.ty), experts.gate.data_ptr(), experts.up.data_ptr(),
+         experts.down.data_ptr(), experts.gate.numel(), s.n_experts, s.top_k, s.hidden, s.inter,
+         x.data_ptr(), ids.data_ptr(), rows, out.data_ptr(), ws.data_ptr(), ws.numel(),
+         status.data_ptr() if status is not None else None, _stream(stream))
+    return out
+
+
+def combine(out: torch.Tensor, ids: torch.Tensor, w: torch.Tensor, y: torch.Tensor | None = None,
+            stream=None) -> torch.Tensor:
+    """MoeCombine: y F32 [rows, hidden] (moe/tests.rs:541-556)."""
+    rows, top_k, hidden = out.shape
+    if y is None:
+        y = torch.empty(rows, hidden, dtype=torch.float32, device=out.device)
+    call("syn_moe_combine", out.data_ptr(), ids.data_ptr(), w.data_ptr(), rows, top_k, hidden,
+         y.data_ptr(), _stream(stream))
+    return y
+
+
+class MoeLayer:
+    """route -> MoeGrouped -> combine for one layer, with its workspace held."""
+
+    def __init__(self, s: MoeShape, router: torch.Tensor, experts: Experts, max_rows: int):
+        self.s, self.router, self.experts = s, router, experts
+        self.ws = torch.empty(max(workspace_bytes(s, max_rows), 256), dtype=torch.uint8,
+                              device=router.device)
+        self.max_rows = max_rows
+
+    def __call__(self, x: torch.Tensor, stream=None):
+        rows = x.shape[0]
+        if rows > self.max_rows:
+            raise MoeError(f"{rows} rows above the layer's {self.max_rows}")
+        ids, w = route(self.router, x, self.s.top_k, True, stream=stream)
+        out = moe_grouped(self.s, self.experts, x, ids, ws=self.ws, stream=stream)
+        return combine(out, ids, w, stream=stream), ids, w, out
+
+
+__all__ = ["MoeShape", "MoeError", "Experts", "route", "pack", "workspace_bytes", "moe_grouped",
+           "combine", "MoeLayer", "GemvError"]

@@ -1,0 +1,204 @@
+"""GPU parity of the MoE layer (route, pack, grouped expert FFN, combine) against the CPU oracle:
+bit-exact ids, lists and outputs."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce, assert_same, dev, host, require_gpu
+from oracle import oracle as o
+from refgen import MoeRng, moe_activations, moe_matrix, moe_route_ids
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def M():
+    require_gpu()
+    import syntropy_amd.moe as M
+    return M
+
+
+def random_q4k_experts(seed, n_experts, hidden, inter):
+    """Stacked Q4_K experts as the reference's MoE tests build them (random codes, F16 scales in
+    [2^-9, 2^-5]; crates/kernels-cpu/src/moe/tests.rs:40-74)."""
+    rng = MoeRng(seed)
+    gate = moe_matrix(rng, o.Q4_K, n_experts * inter, hidden, o.f16_bits)
+    up = moe_matrix(rng, o.Q4_K, n_experts * inter, hidden, o.f16_bits)
+    down = moe_matrix(rng, o.Q4_K, n_experts * hidden, inter, o.f16_bits)
+    return gate, up, down
+
+
+def fast_q4k_experts(seed, n_experts, hidden, inter):
+    """The same distribution generated vectorized (for the layer-size cases)."""
+    rs = np.random.default_rng(seed)
+
+    def mat(n_out, k):
+        nb = n_out * k // 256
+        b = rs.integers(0, 256, (nb, 144), dtype=np.uint8)
+        # F16 scales in [2^-10, 2^-5): biased exponent 5..9, random mantissa
+        h = ((rs.integers(5, 10, (nb, 2), dtype=np.uint16) << 10)
+             | rs.integers(0, 1024, (nb, 2), dtype=np.uint16)).astype(np.uint16)
+        b[:, 0:4] = h.view(np.uint8).reshape(nb, 4)
+        return b.ravel()
+
+    return mat(n_experts * inter, hidden), mat(n_experts * inter, hidden), mat(n_experts * hidden, inter)
+
+
+# ---- route ----------------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,hidden,n_experts,top_k", [(37, 256, 16, 4), (64, 4096, 128, 8),
+                                                         (5, 1024, 60, 6), (600, 512, 32, 2)])
+def test_route_bit_exact(M, rows, hidden, n_experts, top_k):
+    router = o.normal(0x51A30004 + hidden, 0.02, n_experts * hidden).reshape(n_experts, hidden)
+    x = o.normal(0x51A20004 + rows, 1.0, rows * hidden).reshape(rows, hidden)
+    announce(f"route rows={rows} hidden={hidden} E={n_experts} k={top_k}")
+    ids, w, probs = M.route(dev(router), dev(x), top_k, True, probs=True)
+    wids, ww, wprobs = o.moe_route(router, x, n_experts, top_k, True)
+    assert_same(host(probs), wprobs, "probs")
+    assert (host(ids) == wids).all()
+    assert_same(host(w), ww, "weights")
+
+
+def test_route_ties_go_to_the_lower_index(M):
+    hidden, n_experts = 256, 16
+    router = o.normal(3, 0.02, n_experts * hidden).reshape(n_experts, hidden)
+    router[9] = router[2]
+    router[11] = router[2]
+    router[5] = router[14]
+    x = o.normal(4, 1.0, 8 * hidden).reshape(8, hidden)
+    announce("route ties")
+    ids, w = M.route(dev(router), dev(x), 6, True)
+    wids, ww, _ = o.moe_route(router, x, n_experts, 6, True)
+    assert (host(ids) == wids).all()
+    assert_same(host(w), ww)
+    # brute force: the selection is the stable descending sort of the probabilities
+    _, _, p = o.moe_route(router, x, n_experts, 6, True)
+    for r in range(8):
+        order = sorted(range(n_experts), key=lambda e: (-p[r, e], e))[:6]
+        assert list(host(ids)[r]) == order
+
+
+# ---- pack -------------------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,top_k,n_experts", [(1, 1, 4), (64, 8, 128), (2048, 8, 128),
+                                                   (300, 3, 7), (17, 2, 256)])
+def test_pack_bit_exact(M, rows, top_k, n_experts):
+    rs = np.random.default_rng(rows * 31 + top_k)
+    ids = rs.integers(0, n_experts, (rows, top_k)).astype(np.int32)
+    if rows >= 64:  # skew: a few experts take many slots
+        ids[: rows // 2, 0] = 3
+    announce(f"pack rows={rows} k={top_k} E={n_experts}")
+    offsets, slots, err = M.pack(dev(ids), n_experts)
+    wo, ws = o.moe_pack(ids, n_experts)
+    assert host(err)[0] == 0
+    assert (host(offsets).view(np.uint32) == wo).all()
+    assert (host(slots).view(np.uint32) == ws).all()
+
+
+def test_pack_refuses_bad_ids(M):
+    ids = np.zeros((8, 2), np.int32)
+    ids[5, 1] = 9
+    announce("pack bad id")
+    _, _, err = M.pack(dev(ids), 9)
+    assert host(err)[0] == 1
+
+
+# ---- grouped expert FFN ------------------------------------------------------------------------
+def run_grouped(M, shape, gate, up, down, x, ids):
+    ex = M.Experts(12, dev(gate), dev(up), dev(down))
+    out = torch.full((ids.shape[0], shape.top_k, shape.hidden), float("nan"), device="cuda")
+    st = torch.full((1,), 7, dtype=torch.int32, device="cuda")
+    M.moe_grouped(shape, ex, dev(x), dev(ids), out=out, status=st)
+    return host(out), int(host(st)[0])
+
+
+@pytest.mark.parametrize("rows", [1, 2, 5, 8, 9, 17, 40])
+def test_grouped_equals_oracle_reference_shape(M, rows):
+    """crates/kernels-cpu/src/moe/tests.rs:227-236 shape: 6 experts, top-2, hidden 256, inter 512."""
+    s = M.MoeShape(6, 2, 256, 512)
+    gate, up, down = random_q4k_experts(1, s.n_experts, s.hidden, s.inter)
+    rng = MoeRng(100 + rows)
+    x = moe_activations(rng, rows * s.hidden).reshape(rows, s.hidden)
+    ids = moe_route_ids(rng, rows, s.top_k, s.n_experts)
+    announce(f"grouped ref-shape rows={rows}")
+    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, 6, 2, 256, 512, gate, up, down, x, ids)
+    assert st == 0
+    assert_same(got, want, f"rows {rows}")
+
+
+def test_grouped_layer_shape_64_tokens(M):
+    """Qwen3-235B-A22B MoE shape at 64 decode tokens: 128 experts, top-8, hidden 4096, inter 1536,
+    routed by the GPU router on N(0,1) rows; every slot bit-exact against the oracle."""
+    s = M.MoeShape(128, 8, 4096, 1536)
+    gate, up, down = fast_q4k_experts(7, s.n_experts, s.hidden, s.inter)
+    router = o.normal(0x51A30004, 0.02, s.n_experts * s.hidden).reshape(s.n_experts, s.hidden)
+    x = o.normal(0x51A20004, 1.0, 64 * s.hidden).reshape(64, s.hidden)
+    announce("grouped layer shape 64 tokens")
+    ids_d, w_d = M.route(dev(router), dev(x), s.top_k, True)
+    ids = host(ids_d)
+    wids, ww, _ = o.moe_route(router, x, s.n_experts, s.top_k, True)
+    assert (ids == wids).all()
+    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    assert st == 0
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, 128, 8, 4096, 1536, gate, up, down, x, ids, threads=16)
+    assert_same(got, want, "layer slots")
+    y = host(M.combine(dev(got), dev(ids), dev(ww)))
+    assert_same(y, o.moe_combine(want, ids, ww), "combined")
+
+
+def test_grouped_skewed_loads(M):
+    """One expert takes most rows (more entries than one work item holds)."""
+    s = M.MoeShape(8, 2, 512, 256)
+    gate, up, down = random_q4k_experts(5, s.n_experts, s.hidden, s.inter)
+    rows = 150
+    rng = MoeRng(9)
+    x = moe_activations(rng, rows * s.hidden).reshape(rows, s.hidden)
+    ids = moe_route_ids(rng, rows, s.top_k, s.n_experts)
+    ids[:120, 0] = 6
+    ids[:120, 1] = np.where(ids[:120, 1] == 6, 2, ids[:120, 1])
+    announce("grouped skewed")
+    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, 8, 2, 512, 256, gate, up, down, x, ids)
+    assert st == 0
+    assert_same(got, want)
+
+
+def test_grouped_row_permutation(M):
+    """moe/tests.rs:497-539: permuting rows permutes the per-slot and combined outputs."""
+    s = M.MoeShape(6, 2, 256, 512)
+    gate, up, down = random_q4k_experts(2, s.n_experts, s.hidden, s.inter)
+    rng = MoeRng(5)
+    rows = 12
+    x = moe_activations(rng, rows * s.hidden).reshape(rows, s.hidden)
+    ids = moe_route_ids(rng, rows, s.top_k, s.n_experts)
+    w = np.array([abs(rng.unit()) for _ in range(rows * s.top_k)], np.float32).reshape(rows, s.top_k)
+    perm = [(rows - 1 - i) for i in range(rows)]
+    perm = perm[rows // 3:] + perm[:rows // 3]
+    announce("grouped permutation")
+    out, _ = run_grouped(M, s, gate, up, down, x, ids)
+    outp, _ = run_grouped(M, s, gate, up, down, x[perm], ids[perm])
+    assert_same(outp, out[perm])
+    y = host(M.combine(dev(out), dev(ids), dev(w)))
+    yp = host(M.combine(dev(outp), dev(ids[perm]), dev(w[perm])))
+    assert_same(yp, y[perm])
+
+
+def test_grouped_refusal_writes_nothing(M):
+    s = M.MoeShape(6, 2, 256, 512)
+    gate, up, down = random_q4k_experts(3, s.n_experts, s.hidden, s.inter)
+    x = np.ones((3, 256), np.float32)
+    ids = np.array([[0, 1], [2, 6], [3, 4]], np.int32)
+    announce("grouped bad id")
+    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    assert st == 1
+    assert np.isnan(got).all()
+
+
+# ---- combine ------------------------------------------------------------------------------------
+def test_combine_bit_exact(M):
+    rs = np.random.default_rng(4)
+    rows, k, hidden = 33, 8, 1000
+    out = rs.standard_normal((rows, k, hidden)).astype(np.float32)
+    ids = np.stack([rs.permutation(64)[:k] for _ in range(rows)]).astype(np.int32)
+    w = rs.random((rows, k)).astype(np.float32)
+    announce("combine")
+    assert_same(host(M.combine(dev(out), dev(ids), dev(w))), o.moe_combine(out, ids, w))
