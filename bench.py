@@ -48,7 +48,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", choices=["layer", "copy"], default=None)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-seconds", type=float, default=8.0)
+    p.add_argument("--no-moe", action="store_true")
     return p.parse_args()
 
 
@@ -125,6 +126,89 @@ def cpu_baseline(torch, copies, xs, seconds):
     }
 
 
+MOE = dict(n_experts=128, top_k=8, hidden=4096, inter=1536, tokens=64)
+
+
+def build_moe(torch, S, M, seed):
+    """Qwen3-235B-A22B MoE layer shape: router F32 N(0,0.02); 128 experts of gate/up [1536,4096]
+    and down [4096,1536], N(0,0.02) quantized to Q4_K by the GPU packer; x N(0,1)."""
+    c = MOE
+    gen = torch.Generator(device="cuda")
+    mats = []
+    for m, (n_out, k) in enumerate([(c["inter"], c["hidden"]), (c["inter"], c["hidden"]),
+                                    (c["hidden"], c["inter"])]):
+        parts = []
+        for e in range(c["n_experts"]):
+            gen.manual_seed(seed + 1000 * m + e)
+            w = torch.randn(n_out * k, generator=gen, device="cuda", dtype=torch.float32) * 0.02
+            parts.append(S.quantize(S.WeightType.Q4K, w))
+        mats.append(torch.cat(parts))
+        del parts
+    gen.manual_seed(seed + 7)
+    router = torch.randn(c["n_experts"], c["hidden"], generator=gen, device="cuda") * 0.02
+    x = torch.randn(c["tokens"], c["hidden"], generator=gen, device="cuda")
+    shape = M.MoeShape(c["n_experts"], c["top_k"], c["hidden"], c["inter"])
+    layer = M.MoeLayer(shape, router, M.Experts(12, *mats), c["tokens"])
+    return layer, x
+
+
+def bench_moe(torch, S, M, steps, warmup, cpu_seconds):
+    c = MOE
+    layer, x = build_moe(torch, S, M, 0x51A40000)
+    for _ in range(warmup):
+        layer(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        y, ids, w, out = layer(x)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ids_h = ids.cpu().numpy()
+    e_t = len(set(ids_h.ravel().tolist()))
+    loads = [int((ids_h == e).sum()) for e in range(c["n_experts"])]
+    expert_bytes = 3 * c["inter"] * (c["hidden"] // 256) * 144
+    alg = e_t * expert_bytes + c["n_experts"] * c["hidden"] * 4 + 2 * c["tokens"] * c["hidden"] * 4
+    ms = dt / steps * 1e3
+    res = {
+        "metric": "MoE layer tokens/s at 64-token decode",
+        "value": round(c["tokens"] * steps / dt, 1),
+        "unit": "tokens/s",
+        "ms_per_step": round(ms, 4),
+        "workload": "Qwen3-235B-A22B MoE FFN shape: 64 decode tokens, hidden 4096, 128 Q4_K experts "
+                    "(SwiGLU inter 1536), softmax top-8 renormalized; route + pack + grouped FFN + combine",
+        "distinct_experts": e_t,
+        "max_over_avg_load": round(max(loads) / (sum(loads) / c["n_experts"]), 3),
+        "alg_bytes_per_step": alg,
+        "hbm_gbs": round(alg / (ms * 1e-3) / 1e9, 1),
+        "hbm_fraction_of_peak": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
+    if cpu_seconds > 0:
+        from oracle import oracle as o
+        threads = min(16, os.cpu_count() or 1)
+        ex = layer.experts
+        g, u, d = ex.gate.cpu().numpy(), ex.up.cpu().numpy(), ex.down.cpu().numpy()
+        r, xh = layer.router.cpu().numpy(), x.cpu().numpy()
+
+        def step():
+            ids_c, w_c, _ = o.moe_route(r, xh, c["n_experts"], c["top_k"], True)
+            out_c = o.moe_grouped(o.Q4_K, o.Q4_K, c["n_experts"], c["top_k"], c["hidden"],
+                                  c["inter"], g, u, d, xh, ids_c, threads=threads)
+            return o.moe_combine(out_c, ids_c, w_c)
+
+        step()
+        n, t1 = 0, time.perf_counter()
+        while True:
+            step()
+            n += 1
+            if time.perf_counter() - t1 >= cpu_seconds:
+                break
+        cdt = time.perf_counter() - t1
+        res["cpu_baseline"] = {"value": round(c["tokens"] * n / cdt, 1), "unit": "tokens/s",
+                               "cores": threads, "kind": "port",
+                               "sample": f"{n} MoE layers of 64 tokens in {cdt:.1f} s"}
+    return res
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -133,6 +217,7 @@ def main():
         sys.exit(2)
     import torch
     import syntropy_amd.gemv as S
+    import syntropy_amd.moe as M
 
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     torch.cuda.set_device(0)
@@ -240,6 +325,11 @@ def main():
     }
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, copies, xs, a.cpu_seconds)
+    del copies, batches
+    if not a.no_moe:
+        torch.cuda.empty_cache()
+        out["moe"] = bench_moe(torch, S, M, max(10, a.steps // 4), max(3, a.warmup // 4),
+                               0 if a.no_cpu else a.cpu_seconds)
     print(json.dumps(out))
 
 

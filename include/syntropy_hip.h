@@ -86,7 +86,9 @@ int syn_gemv_batch(uint32_t n, const int32_t* wtypes, const void* const* w,
  * in-order sum when `renormalize`.  The reference has no code for this op: it is its
  * specification (plan/rfcs/RFC-0042-quantization-and-numerical-fidelity.md:232,281; the op
  * kind crates/kernels/src/op/kind.rs:35-42, IR signature crates/graph/src/ir/signature.rs:149).
- * probs (optional, F32 [rows, n_experts]) receives the softmax. */
+ * probs (F32 [rows, n_experts], required) receives the softmax; the call stages the router
+ * logits there first.  Limits: n_experts <= 256, top_k <= min(n_experts, 32), hidden whole
+ * 32-value blocks and at most 8192; the router 16-byte aligned. */
 int syn_moe_route(const float* router, const float* x, uint32_t rows, uint32_t hidden,
                   uint32_t n_experts, uint32_t top_k, int32_t renormalize, int32_t* ids, float* w,
                   float* probs, void* stream);

@@ -240,11 +240,11 @@ MoeWs moe_ws(uint32_t n_experts, uint32_t top_k, uint32_t hidden, uint32_t inter
     m.err = o;  // error word, then the largest expert's entry count
     o = syn::align_up(o + 8, 256);
     m.xq = o;
-    o += syn::act_layout(syn::ACT_Q8K, ent, hidden).bytes;
+    o += syn::moe_act_bytes((int64_t)ent, (int)hidden);
     m.h = o;
     o = syn::align_up(o + 4ull * ent * inter, 256);
     m.hq = o;
-    o += syn::act_layout(syn::ACT_Q8K, ent, inter).bytes;
+    o += syn::moe_act_bytes((int64_t)ent, (int)inter);
     m.bytes = syn::align_up(o, 256);
     return m;
 }
@@ -257,6 +257,9 @@ int check_moe_shape(const char* W, uint32_t n_experts, uint32_t top_k, uint32_t 
         return fail(SYN_E_INVALID, "%s: hidden %u and inter %u must be whole 256-weight blocks", W, hidden, inter);
     if (hidden > 65536 || inter > 65536) return fail(SYN_E_UNSUPPORTED, "%s: hidden/inter above 65536", W);
     if ((uint64_t)rows * top_k > 65536) return fail(SYN_E_UNSUPPORTED, "%s: rows * top_k above 65536", W);
+    // the expert kernels address the entries' codes with 32-bit offsets
+    if ((uint64_t)rows * top_k * (hidden > inter ? hidden : inter) >= (1ull << 32))
+        return fail(SYN_E_UNSUPPORTED, "%s: rows * top_k * max(hidden, inter) reaches 2^32", W);
     return SYN_OK;
 }
 
@@ -268,12 +271,14 @@ SYN_EXPORT int syn_moe_route(const float* router, const float* x, uint32_t rows,
     const char* W = "syn_moe_route";
     if (n_experts == 0 || n_experts > 256) return fail(SYN_E_UNSUPPORTED, "%s: n_experts %u (1..256)", W, n_experts);
     if (top_k == 0 || top_k > n_experts || top_k > 32) return fail(SYN_E_UNSUPPORTED, "%s: top_k %u", W, top_k);
-    if (hidden % 32 || hidden == 0 || hidden > 16384) return fail(SYN_E_UNSUPPORTED, "%s: hidden %u (whole 32-blocks, at most 16384)", W, hidden);
+    if (hidden % 32 || hidden == 0 || hidden > 8192 || !syn::moe_route_supported((int)hidden))
+        return fail(SYN_E_UNSUPPORTED, "%s: hidden %u (whole 32-blocks, at most 8192)", W, hidden);
     if (rows == 0) return SYN_OK;
-    if (!router || !x || !ids || !w) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!router || !x || !ids || !w || !probs) return fail(SYN_E_INVALID, "%s: null operand", W);
     if (!aligned(router, 16) || !aligned(x, 4)) return fail(SYN_E_INVALID, "%s: router must be 16-byte aligned", W);
+    // the logits are staged in probs, row by row, before the softmax overwrites them
     syn::launch_moe_route(router, x, (int)rows, (int)hidden, (int)n_experts, (int)top_k, renormalize != 0,
-                          ids, w, probs, (hipStream_t)stream);
+                          ids, w, probs, probs, (hipStream_t)stream);
     return check_launch(W);
 }
 
@@ -325,19 +330,13 @@ SYN_EXPORT int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, 
     const int ent = (int)(rows * top_k);
     hipStream_t st = (hipStream_t)stream;
     syn::launch_moe_pack(ids, ent, (int)n_experts, offsets, slots, err, st);
-    const syn::ActLayout LX = syn::act_layout(syn::ACT_Q8K, ent, hidden);
-    const syn::ActLayout LH = syn::act_layout(syn::ACT_Q8K, ent, inter);
-    syn::QAct ax{(const int8_t*)(base + m.xq + LX.codes), (const float*)(base + m.xq + LX.d),
-                 (const int32_t*)(base + m.xq + LX.sums)};
-    syn::QAct ah{(const int8_t*)(base + m.hq + LH.codes), (const float*)(base + m.hq + LH.d),
-                 (const int32_t*)(base + m.hq + LH.sums)};
-    syn::launch_moe_gather_q8k(x, slots, ent, (int)top_k, (int)hidden, err, (int8_t*)ax.codes, (float*)ax.d,
-                               (int32_t*)ax.sums, 1, st);
+    const syn::MoeAct ax = syn::moe_act_at(base + m.xq, ent, (int)hidden);
+    const syn::MoeAct ah = syn::moe_act_at(base + m.hq, ent, (int)inter);
+    syn::launch_moe_gather_q8k(x, slots, ent, (int)top_k, (int)hidden, err, ax, 1, st);
     float* h = (float*)(base + m.h);
     syn::launch_moe_gateup((const uint8_t*)gate, (const uint8_t*)up, (int)n_experts, (int)hidden, (int)inter,
                            offsets, ent, ax, err, h, st);
-    syn::launch_moe_gather_q8k(h, slots, ent, (int)top_k, (int)inter, err, (int8_t*)ah.codes, (float*)ah.d,
-                               (int32_t*)ah.sums, 0, st);
+    syn::launch_moe_gather_q8k(h, slots, ent, (int)top_k, (int)inter, err, ah, 0, st);
     syn::launch_moe_down((const uint8_t*)down, (int)n_experts, (int)hidden, (int)inter, offsets, ent, ah,
                          slots, err, out, st);
     if (status) {

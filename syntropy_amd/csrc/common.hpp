@@ -133,9 +133,14 @@ SYN_DEV float rot1(float v) {
 
 // Q8_K of one 256-value block (crates/kernels-cpu/src/gemv/act.rs:351-373): largest
 // magnitude, first index on ties, ggml's nearest_int; non-finite block -> scale NaN, codes 0.
-// One wavefront; lane l holds values 4l..4l+3.
-SYN_DEV void q8k_block_wave(const float* __restrict__ xb, int8_t* __restrict__ codes,
-                            float* __restrict__ dout, int32_t* __restrict__ sums, int lane) {
+// One wavefront; lane l holds values 4l..4l+3 and gets their four codes (packed bytes), the
+// code sum of its 32-value sub-block l/8 (every lane of the sub-block) and the block scale.
+struct Q8KLane {
+    uint32_t packed;
+    int sum32;
+    float d;
+};
+SYN_DEV Q8KLane q8k_block_lane(const float* __restrict__ xb, int lane) {
     const float4 v4 = reinterpret_cast<const float4*>(xb)[lane];
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
     const bool fin = finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]);
@@ -178,15 +183,26 @@ SYN_DEV void q8k_block_wave(const float* __restrict__ xb, int8_t* __restrict__ c
         }
         d = 1.0f / iscale;
     }
-    const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
-                            ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
-    reinterpret_cast<uint32_t*>(codes)[lane] = packed;
+    Q8KLane r;
+    r.packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+               ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
     int s = q[0] + q[1] + q[2] + q[3];
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
     s += __shfl_xor(s, 4);
-    if ((lane & 7) == 0) sums[lane >> 3] = s;
-    if (lane == 0) *dout = d;
+    r.sum32 = s;
+    r.d = d;
+    return r;
+}
+
+// The same block in the row layout of the GEMV workspace: codes in order, the eight 32-value
+// sums, the scale.
+SYN_DEV void q8k_block_wave(const float* __restrict__ xb, int8_t* __restrict__ codes,
+                            float* __restrict__ dout, int32_t* __restrict__ sums, int lane) {
+    const Q8KLane r = q8k_block_lane(xb, lane);
+    reinterpret_cast<uint32_t*>(codes)[lane] = r.packed;
+    if ((lane & 7) == 0) sums[lane >> 3] = r.sum32;
+    if (lane == 0) *dout = r.d;
 }
 
 }  // namespace syn

@@ -27,24 +27,32 @@ void launch_gemv_q4k_batch(int np, const uint8_t* const* W, const int* n_out, co
 void launch_act_quant_batch(int np, const float* const* x, const int* k, uint8_t* const* ws,
                             hipStream_t stream);
 // moe.hip
-struct QAct {  // Q8_K activations of the packed entries, entry-major
-    const int8_t* codes;
-    const float* d;
-    const int32_t* sums;
-};
+bool moe_route_supported(int hidden);
 void launch_moe_route(const float* router, const float* x, int rows, int hidden, int n_experts,
-                      int top_k, int renorm, int32_t* ids, float* w, float* probs,
+                      int top_k, int renorm, int32_t* ids, float* w, float* probs, float* logits,
                       hipStream_t stream);
 void launch_moe_pack(const int32_t* ids, int nslots, int n_experts, uint32_t* offsets,
                      uint32_t* slots, uint32_t* err, hipStream_t stream);
+// Q8_K activations of the packed entries as the expert kernels read them, entry-major.  Each
+// 256-value block b of an entry is stored in the matrix-core operand order: byte
+// 256b + 64p + 8j + i holds code 32j + 8p + i (sub-block j, k part p), so that one lane reads
+// its A operand of all eight sub-blocks as 64 contiguous bytes.  lh holds, per block, the
+// sub-block code sums s_j = 128 h_j + l_j as bytes l_0..l_7 (0..127), h_0..h_7 (-32..31).
+struct MoeAct {
+    int8_t* codes;  // [entry][k]
+    float* d;       // [k / 256][entry] (block-major)
+    uint8_t* lh;    // [entry][k / 256][16]
+    int nentries;
+};
+size_t moe_act_bytes(int64_t nentries, int k);
+MoeAct moe_act_at(uint8_t* base, int64_t nentries, int k);
 void launch_moe_gather_q8k(const float* x, const uint32_t* slots, int nentries, int top_k, int k,
-                           const uint32_t* err, int8_t* codes, float* d, int32_t* sums, int gather,
-                           hipStream_t stream);
+                           const uint32_t* err, MoeAct a, int gather, hipStream_t stream);
 void launch_moe_gateup(const uint8_t* gate, const uint8_t* up, int n_experts, int hidden,
-                       int inter, const uint32_t* offsets, int nentries, QAct a,
+                       int inter, const uint32_t* offsets, int nentries, MoeAct a,
                        const uint32_t* err, float* h, hipStream_t stream);
 void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
-                     const uint32_t* offsets, int nentries, QAct a, const uint32_t* slots,
+                     const uint32_t* offsets, int nentries, MoeAct a, const uint32_t* slots,
                      const uint32_t* err, float* out, hipStream_t stream);
 void launch_moe_combine(const float* out, const int32_t* ids, const float* w, int rows, int top_k,
                         int hidden, float* y, hipStream_t stream);

@@ -57,10 +57,9 @@ def route(router: torch.Tensor, x: torch.Tensor, top_k: int, renormalize: bool =
     rows = x.shape[0]
     ids = torch.empty(rows, top_k, dtype=torch.int32, device=x.device)
     w = torch.empty(rows, top_k, dtype=torch.float32, device=x.device)
-    p = torch.empty(rows, n_experts, dtype=torch.float32, device=x.device) if probs else None
+    p = torch.empty(rows, n_experts, dtype=torch.float32, device=x.device)
     call("syn_moe_route", router.data_ptr(), x.data_ptr(), rows, hidden, n_experts, top_k,
-         int(renormalize), ids.data_ptr(), w.data_ptr(), p.data_ptr() if p is not None else None,
-         _stream(stream))
+         int(renormalize), ids.data_ptr(), w.data_ptr(), p.data_ptr(), _stream(stream))
     return (ids, w, p) if probs else (ids, w)
 
 

@@ -45,8 +45,12 @@ def fast_q4k_experts(seed, n_experts, hidden, inter):
 
 
 # ---- route ----------------------------------------------------------------------------------
-@pytest.mark.parametrize("rows,hidden,n_experts,top_k", [(37, 256, 16, 4), (64, 4096, 128, 8),
-                                                         (5, 1024, 60, 6), (600, 512, 32, 2)])
+@pytest.mark.parametrize("rows,hidden,n_experts,top_k", [
+    (37, 256, 16, 4), (64, 4096, 128, 8), (5, 1024, 60, 6), (600, 512, 32, 2),
+    # odd block counts at some tree level: 5 and 48 router blocks, 3 softmax blocks
+    (9, 160, 70, 5), (300, 1536, 70, 4),
+    # the widest rows (fewer experts per workgroup) and 256 experts
+    (3, 8192, 40, 3), (5, 7168, 256, 8)])
 def test_route_bit_exact(M, rows, hidden, n_experts, top_k):
     router = o.normal(0x51A30004 + hidden, 0.02, n_experts * hidden).reshape(n_experts, hidden)
     x = o.normal(0x51A20004 + rows, 1.0, rows * hidden).reshape(rows, hidden)
