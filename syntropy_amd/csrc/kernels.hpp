@@ -40,9 +40,10 @@ void launch_moe_pack(const int32_t* ids, int nslots, int n_experts, uint32_t* of
 // sub-block code sums s_j = 128 h_j + l_j as bytes l_0..l_7 (0..127), h_0..h_7 (-32..31).
 struct MoeAct {
     int8_t* codes;  // [entry][k]
-    float* d;       // [k / 256][entry] (block-major)
+    float* d;       // [k / 256][dstride] (block-major, rows padded to 4 entries)
     uint8_t* lh;    // [entry][k / 256][16]
     int nentries;
+    int dstride;
 };
 size_t moe_act_bytes(int64_t nentries, int k);
 MoeAct moe_act_at(uint8_t* base, int64_t nentries, int k);

@@ -357,8 +357,10 @@ void launch_moe_pack(const int32_t* ids, int nslots, int n_experts, uint32_t* of
 
 size_t moe_act_bytes(int64_t nentries, int k) {
     const int64_t nb = k / 256;
-    // the scales carry 64 bytes of pad: the expert kernels read four entries' scales at once
-    return align_up((size_t)(nentries * k), 256) + align_up((size_t)(nentries * nb * 4 + 64), 256) +
+    // scale rows padded to 4 entries, 64 bytes past the end: the expert kernels read 16-byte
+    // aligned windows of scales
+    return align_up((size_t)(nentries * k), 256) +
+           align_up((size_t)(align_up((size_t)nentries, 4) * nb * 4 + 64), 256) +
            align_up((size_t)(nentries * nb * 16), 256);
 }
 MoeAct moe_act_at(uint8_t* base, int64_t nentries, int k) {
@@ -366,13 +368,16 @@ MoeAct moe_act_at(uint8_t* base, int64_t nentries, int k) {
     MoeAct a;
     a.codes = (int8_t*)base;
     a.d = (float*)(base + align_up((size_t)(nentries * k), 256));
-    a.lh = (uint8_t*)a.d + align_up((size_t)(nentries * nb * 4 + 64), 256);
+    a.dstride = (int)align_up((size_t)nentries, 4);
+    a.lh = (uint8_t*)a.d + align_up((size_t)(a.dstride * nb * 4 + 64), 256);
     a.nentries = (int)nentries;
     return a;
 }
 
 // One wavefront per (entry, 256-value block).  Lane l quantizes values 4l..4l+3: sub-block
-// j = l/8, k part p = (l%8)/2, bytes 4(l%2)..+3 of that part.
+// j = l/8, k part p = (l%8)/2, bytes 4(l%2)..+3 of that part, stored at
+// 64p + 16(j%4) + 8(j/4): the two sub-blocks j and j + 4 that one expert-kernel lane multiplies
+// sit side by side.
 __global__ __launch_bounds__(256) void k_moe_gather_q8k(const float* __restrict__ x,
                                                         const uint32_t* __restrict__ slots,
                                                         int nentries, int top_k, int k,
@@ -387,14 +392,14 @@ __global__ __launch_bounds__(256) void k_moe_gather_q8k(const float* __restrict_
     const int64_t src_row = gather ? (int64_t)(slots[i] / (uint32_t)top_k) : i;
     const Q8KLane r = q8k_block_lane(x + src_row * k + (int64_t)b * 256, lane);
     const int j = lane >> 3, p = (lane & 7) >> 1;
-    *reinterpret_cast<uint32_t*>(a.codes + (int64_t)i * k + (int64_t)b * 256 + 64 * p + 8 * j +
-                                 4 * (lane & 1)) = r.packed;
+    *reinterpret_cast<uint32_t*>(a.codes + (int64_t)i * k + (int64_t)b * 256 + 64 * p +
+                                 16 * (j & 3) + 8 * (j >> 2) + 4 * (lane & 1)) = r.packed;
     uint8_t* lh = a.lh + ((int64_t)i * nb + b) * 16;
     if ((lane & 7) == 0) {
         lh[j] = (uint8_t)(r.sum32 & 127);
         lh[8 + j] = (uint8_t)(r.sum32 >> 7);
     }
-    if (lane == 0) a.d[(int64_t)b * nentries + i] = r.d;
+    if (lane == 0) a.d[(int64_t)b * a.dstride + i] = r.d;
 }
 
 void launch_moe_gather_q8k(const float* x, const uint32_t* slots, int nentries, int top_k, int k,
@@ -411,203 +416,260 @@ void launch_moe_gather_q8k(const float* x, const uint32_t* slots, int nentries, 
 //
 // A workgroup item is (expert, 64 consecutive weight rows, up to 16 consecutive entries of the
 // expert); each of its four wavefronts takes 16 of the rows and walks their super-blocks in
-// order with the next super-block's loads in flight.  The entries' codes of a super-block are
-// staged once in LDS for the four wavefronts.  Per 32-weight sub-block j, one
-// v_mfma_i32_16x16x32_i8: lane l = 16p + c holds weight row c (B operand: the row's 8 codes
-// k = 8p..8p+7 of the sub-block) and entry c (A operand: the entry's codes at the same k), and
-// receives D[entry 4p+i][row c], i = 0..3: the exact I32 sub-block sums of its row against
-// four entries.  S1 = sum_j sc_j * D_j follows on the vector ALU; S2 = sum_j m_j * s_j takes
-// two more products (the l and h bytes of the entry sums against the row's mins,
-// S2 = D_l + 128 D_h).  The lane then folds the super-block term of its row and four entries
-// into its accumulators (gemv.rs:539-547).
+// order.  The workgroup streams every super-block's operands - the 64 rows of each weight
+// matrix and the entries' codes, sums and scales - from global memory straight into LDS
+// (global_load_lds_dwordx4, no registers held while the loads fly), two super-blocks ahead of
+// the arithmetic, in a ring of three stages.
+//
+// The entries go four at a time (decode routes a few entries to each expert).  A product
+// v_mfma_i32_16x16x32_i8 has 16 A rows; row 4j' + t carries entry t's codes of sub-block
+// 4h + j' (zero in the other three products of the group), so four accumulating products
+// (sub-blocks 4h..4h+3) leave lane l = 16p + c holding the exact I32 sums D_h[t] of weight row c
+// and sub-block 4h + p against entries t = 0..3.  The lane scales them, s[t] = sc_p D_0[t] +
+// sc_{4+p} D_1[t]; summing s over the four lanes of the row (two lane swaps) gives S1 of entry
+// p, and S2 = sum_j m_j s_j of entry p comes from its packed sub-block sums with sdot4.  The
+// lane then folds the super-block term of (row c, entry p) into its accumulator
+// (gemv.rs:539-547).
 
-struct WStage {  // one super-block of the lane's weight row, as loaded
-    v4u hdr;     // d, dmin | 12 scale bytes
-    v4u x0, x1;  // code chunks (group 2(p&1), half p>>1) and (group 2(p&1)+1, half p>>1)
+// The shape of one expert kernel: NM weight matrices, WV wavefronts of 16 rows each, up to CH
+// entries (CH / 4 groups) per item.  One stage in LDS: NM weight tiles [16 WV rows][144 bytes],
+// the entries' codes [CH][256] (16-byte chunk q of entry t at position q ^ 4(t & 3), so the
+// sixteen lanes of one read fall in distinct banks), their sums [CH][16], then the
+// 16-byte-aligned window of CH + 4 scales holding theirs.
+template <int NM_, int WV_, int CH_>
+struct MoeCfg {
+    static constexpr int NM = NM_, WV = WV_, CH = CH_, NG = CH_ / 4;
+    static constexpr int THREADS = 64 * WV;
+    static constexpr int ROWS = 16 * WV;
+    static constexpr int W = ROWS * 144;
+    static constexpr int WCHUNKS = NM * ROWS * 9;        // 16-byte chunks of the weight tiles
+    static constexpr int WSLOTS = (WCHUNKS + 63) / 64;
+    static constexpr int CODES = NM * W;
+    static constexpr int LH = CODES + CH * 256;
+    static constexpr int DX = LH + CH * 16;
+    static constexpr int BYTES = DX + (CH / 4 + 1) * 16;
+    static constexpr int SLOTS = WSLOTS + NG + 1;         // wavefront loads per stage
+    static constexpr int PER_WAVE = (SLOTS + WV - 1) / WV;  // each wavefront issues as many
+    static_assert(CH % 4 == 0 && CH <= 16 && CH + CH / 4 + 1 <= 64, "entry chunk");
 };
-struct TStage {  // one super-block of the lane's entries, from global memory
-    v4u lh;         // sub-block sums of entry c: l bytes, h bytes
-    v4f dx;         // Q8_K scales of entries 4p + i
+constexpr int MOE_STAGES = 3;
+
+// s_waitcnt that waits for vector memory only: vmcnt n, expcnt and lgkmcnt left at their maxima.
+template <int N>
+SYN_DEV void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// The same for a wave-uniform n <= M.
+template <int M>
+SYN_DEV void wait_vm_n(int n) {
+    if constexpr (M > 0) {
+        if (n >= M) {
+            wait_vm<M>();
+            return;
+        }
+        wait_vm_n<M - 1>(n);
+    } else {
+        wait_vm<0>();
+    }
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// Workgroup barrier over LDS reads only: each wavefront's LDS reads have returned, then
+// s_barrier.  (The fence of __syncthreads would also wait for every load into LDS still in
+// flight, the next stages' included.)  The memory clobber keeps the compiler from moving
+// memory accesses across it.
+SYN_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One wavefront's load slot of a stage: the lane's global address of super-block 0 and its
+// step per super-block, whether the lane loads, and the slot's LDS offset inside the stage.
+// Every load is 16 bytes; lane L of a slot writes LDS offset + 16 L.
+struct Slot {
+    const uint8_t* src;
+    uint32_t step;
+    bool on;    // this lane loads
+    bool live;  // the slot loads at all (uniform): not padding, not an absent entry group
+    int lds;
 };
 
-// One super-block of the lane's row in three 16-byte loads: the header and two code chunks,
-// so the wavefront's loads cover its rows' 128 code bytes once.  A half-group holds k parts
-// 2h and 2h + 1; swapping the second part of even rows (p = 0, 2) with the first part of odd
-// rows (p = 1, 3) leaves every lane with k part p of all four groups.
-SYN_DEV void load_w(const uint8_t* __restrict__ base, uint32_t off, uint32_t coff, WStage& w) {
-    w.hdr = *reinterpret_cast<const v4u*>(base + off);
-    w.x0 = *reinterpret_cast<const v4u*>(base + (off + coff));
-    w.x1 = *reinterpret_cast<const v4u*>(base + (off + coff + 32));
-}
-// q[2g], q[2g + 1]: k part p of group g (odd rows' low words <-> even rows' high words, by
-// v_permlane16_swap)
-SYN_DEV void part_codes(const WStage& w, uint32_t (&q)[8]) {
-    const auto r0 = __builtin_amdgcn_permlane16_swap(w.x0.x, w.x0.z, false, false);
-    const auto r1 = __builtin_amdgcn_permlane16_swap(w.x0.y, w.x0.w, false, false);
-    const auto r2 = __builtin_amdgcn_permlane16_swap(w.x1.x, w.x1.z, false, false);
-    const auto r3 = __builtin_amdgcn_permlane16_swap(w.x1.y, w.x1.w, false, false);
-    q[0] = r0[0];
-    q[1] = r1[0];
-    q[2] = r2[0];
-    q[3] = r3[0];
-    q[4] = r0[1];
-    q[5] = r1[1];
-    q[6] = r2[1];
-    q[7] = r3[1];
+template <class C>
+SYN_DEV Slot make_slot(int s, const uint8_t* const (&bases)[C::NM], uint32_t row0_off, uint32_t rb,
+                       const MoeAct& a, int k, int ent0, int nent) {
+    const int lane = threadIdx.x & 63;
+    Slot r;
+    r.on = true;
+    r.live = s < C::SLOTS;
+    if (s >= C::SLOTS) s = C::SLOTS - 1;
+    if (s < C::WSLOTS) {
+        // chunk ci = 64 s + lane of the tiles: matrix ci / (9 ROWS), then row, then part of 9
+        const int ci0 = 64 * s + lane;
+        r.on = ci0 < C::WCHUNKS;
+        const int ci = r.on ? ci0 : 0;
+        const int m = ci / (9 * C::ROWS), rem = ci - m * (9 * C::ROWS);
+        r.src = bases[m] + (row0_off + (uint32_t)(rem / 9) * rb + 16u * (uint32_t)(rem % 9));
+        r.step = 144u;
+        r.lds = s * 1024;
+    } else if (s < C::WSLOTS + C::NG) {
+        // entries 4j..4j+3: position q of entry t holds its chunk q ^ 4(t & 3)
+        const int j = s - C::WSLOTS, t = 4 * j + (lane >> 4), q = lane & 15;
+        r.live = r.live && 4 * j < nent;
+        const int ec = ent0 + (t < nent ? t : nent - 1);
+        r.src = (const uint8_t*)a.codes + ((uint32_t)ec * (uint32_t)k + 16u * (uint32_t)(q ^ (4 * (t & 3))));
+        r.step = 256u;
+        r.lds = C::CODES + j * 1024;
+    } else if (lane < C::CH) {
+        // sums of entry `lane`
+        const int ec = ent0 + (lane < nent ? lane : nent - 1);
+        r.src = a.lh + (uint32_t)ec * (uint32_t)(k / 256) * 16u;
+        r.step = 16u;
+        r.lds = C::LH;
+    } else {
+        // the next lanes: the scales from ent0 rounded down to 4 (rows padded to 4 entries)
+        const int w = lane - C::CH;
+        r.on = w <= C::CH / 4;
+        r.src = (const uint8_t*)(a.d + (ent0 & ~3) + 4 * (r.on ? w : 0));
+        r.step = 4u * (uint32_t)a.dstride;
+        r.lds = C::LH;
+    }
+    return r;
 }
 
-SYN_DEV void load_t(const MoeAct& a, uint32_t lh_off, const float* __restrict__ d_row, TStage& t) {
-    t.lh = *reinterpret_cast<const v4u*>(a.lh + lh_off);
-    __builtin_memcpy(&t.dx, d_row, sizeof(t.dx));  // 4-byte aligned: the target picks the load width
-}
-
-// The entries' codes of one super-block in LDS: [entry c][k part p][sub-block j][8], rows of
-// 272 bytes (the 16-byte pad spreads the 16 entries over the banks).
-constexpr int TOK_STRIDE = 272;
-constexpr int TOK_BUF = 16 * TOK_STRIDE;
-
-SYN_DEV v4u tok_fetch(const MoeAct& a, int k, int b, int ent0, int nent) {
-    const int t = threadIdx.x, c = t >> 4, u = t & 15;
-    const int ec = ent0 + (c < nent ? c : nent - 1);
-    return *reinterpret_cast<const v4u*>(a.codes + ((uint32_t)ec * (uint32_t)k + 256u * (uint32_t)b + 16u * (uint32_t)u));
-}
-SYN_DEV void tok_put(uint8_t* buf, v4u v) {
-    const int t = threadIdx.x;
-    *reinterpret_cast<v4u*>(buf + (t >> 4) * TOK_STRIDE + 16 * (t & 15)) = v;
+// The load is written as assembly so the compiler does not track it: it would otherwise wait
+// for every load into LDS still in flight before each LDS read, the next stages' included.
+// The explicit waits of the ring order the stages instead.
+SYN_DEV void issue_slot(const Slot& sl, int b, uint8_t* stage) {
+    if (sl.live && sl.on) {
+        const uint8_t* src = sl.src + (uint64_t)sl.step * (uint32_t)b;
+        const uint32_t dst = (uint32_t)(uintptr_t)(lds_ptr)(stage + sl.lds);
+        // m0 (the LDS address) is reserved: the compiler keeps nothing in it across code
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                     :
+                     : "v"(src), "s"(dst)
+                     : "memory");
+    }
 }
 
 SYN_DEV long pack2(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
 
-SYN_DEV long q4k_codes(const uint32_t (&q)[8], int j) {
-    const uint32_t lo = q[2 * (j >> 1)], hi = q[2 * (j >> 1) + 1];
-    const uint32_t c0 = (j & 1) ? (lo >> 4) & 0x0F0F0F0Fu : lo & 0x0F0F0F0Fu;
-    const uint32_t c1 = (j & 1) ? (hi >> 4) & 0x0F0F0F0Fu : hi & 0x0F0F0F0Fu;
-    return pack2(c0, c1);
-}
-
-// One super-block of NM weight rows (gate and up: NM = 2) against the item's entries.  The
-// scheduling barriers and the pinned partial sums keep at most two sub-blocks' products
-// live: sub-block j's products issue while sub-block j - 1's are scaled.
-template <int NM>
-SYN_DEV void q4k_super(const WStage (&w)[NM], const TStage& t, const uint8_t* tok, int p,
-                       float (&acc)[NM][4]) {
-    const int c = threadIdx.x & 15;
-    v4u am[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) am[q] = *reinterpret_cast<const v4u*>(tok + c * TOK_STRIDE + 64 * p + 16 * q);
-    uint32_t qs[NM][8], scs[NM][2], mns[NM][2];
+// One super-block of the wavefront's 16 rows of NM matrices (gate and up: NM = 2) against the
+// item's entry groups, operands from the stage in LDS.  acc[m][g]: row c, entry 4g + p.
+template <class C>
+SYN_DEV void q4k_super(const uint8_t* st, int wave, int ent0, int ngroups, float (&acc)[C::NM][C::NG]) {
+    constexpr int NM = C::NM;
+    using L = C;
+    const int lane = threadIdx.x & 63, c = lane & 15, p = lane >> 4, jq = c >> 2;
+    v4u hdr[NM];
+    long bq[NM][8];  // B operands: the row's codes of sub-block j, k part p
+    uint32_t mns[NM][2];
+    int sc0[NM], sc1[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-        part_codes(w[m], qs[m]);
-        // get_scale_min_k4 (gemv.rs:528-537) on packed bytes: scales of sub-blocks 0-3 | 4-7,
+        const uint8_t* row = st + m * L::W + (16 * wave + c) * 144;
+        hdr[m] = *reinterpret_cast<const v4u*>(row);
+        uint32_t q[8];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint2 v = *reinterpret_cast<const uint2*>(row + 16 + 32 * g + 8 * p);
+            q[2 * g] = v.x;
+            q[2 * g + 1] = v.y;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t lo = q[2 * (j >> 1)], hi = q[2 * (j >> 1) + 1];
+            const uint32_t c0 = (j & 1) ? (lo >> 4) & 0x0F0F0F0Fu : lo & 0x0F0F0F0Fu;
+            const uint32_t c1 = (j & 1) ? (hi >> 4) & 0x0F0F0F0Fu : hi & 0x0F0F0F0Fu;
+            bq[m][j] = pack2(c0, c1);
+        }
+        // get_scale_min_k4 (gemv.rs:528-537) on packed bytes: scales of sub-blocks p and 4 + p,
         // mins of sub-blocks 0-3 | 4-7
-        const uint32_t w0 = w[m].hdr.y, w1 = w[m].hdr.z, w2 = w[m].hdr.w;
-        scs[m][0] = w0 & 0x3F3F3F3Fu;
-        scs[m][1] = (w2 & 0x0F0F0F0Fu) | ((w0 >> 2) & 0x30303030u);
+        const uint32_t w0 = hdr[m].y, w1 = hdr[m].z, w2 = hdr[m].w;
+        const uint32_t sc_lo = w0 & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (w2 & 0x0F0F0F0Fu) | ((w0 >> 2) & 0x30303030u);
+        sc0[m] = (int)((sc_lo >> (8 * p)) & 0xFFu);
+        sc1[m] = (int)((sc_hi >> (8 * p)) & 0xFFu);
         mns[m][0] = w1 & 0x3F3F3F3Fu;
         mns[m][1] = ((w2 >> 4) & 0x0F0F0F0Fu) | ((w1 >> 2) & 0x30303030u);
     }
     const v4i z = {0, 0, 0, 0};
-    int s1[NM][4];
-    v4i prev[NM];
 #pragma unroll
-    for (int j = 0; j <= 8; ++j) {
-        v4i cur[NM];
-        if (j < 8) {
-            const v4u aw = am[j >> 1];
-            const long av = (j & 1) ? pack2(aw.z, aw.w) : pack2(aw.x, aw.y);
+    for (int g = 0; g < C::NG; ++g) {
+        if (g >= ngroups) break;  // uniform
+        // entry 4g + (c & 3): its codes of sub-blocks jq and jq + 4, k part p
+        const int ta = 4 * g + (c & 3);
+        const v4u ap = *reinterpret_cast<const v4u*>(st + L::CODES + ta * 256 + 16 * ((4 * p + jq) ^ (4 * (c & 3))));
+        const int to = 4 * g + p;  // the lane's output entry
+        const v4u lh = *reinterpret_cast<const v4u*>(st + L::LH + 16 * to);
+        const float dx = reinterpret_cast<const float*>(st + L::DX)[(ent0 & 3) + to];
+        v4i d0[NM], d1[NM];
 #pragma unroll
-            for (int m = 0; m < NM; ++m)
-                cur[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, q4k_codes(qs[m], j), z, 0, 0, 0);
-        }
-        if (j > 0) {
-            const int jj = j - 1;
+        for (int m = 0; m < NM; ++m) d0[m] = d1[m] = z;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const long a0 = jj == jq ? pack2(ap.x, ap.y) : 0;
+            const long a1 = jj == jq ? pack2(ap.z, ap.w) : 0;
 #pragma unroll
             for (int m = 0; m < NM; ++m) {
-                const int sc = (int)((scs[m][jj >> 2] >> (8 * (jj & 3))) & 0xFFu);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    // |D| <= 32 * 15 * 127 fits 24 bits: one v_mad_i32_i24
-                    const int dv = (prev[m][i] << 8) >> 8;
-                    s1[m][i] = (jj ? s1[m][i] : 0) + sc * dv;
-                    asm volatile("" : "+v"(s1[m][i]));  // here, not re-associated to the end
-                }
+                d0[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bq[m][jj], d0[m], 0, 0, 0);
+                d1[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bq[m][4 + jj], d1[m], 0, 0, 0);
             }
         }
-        if (j < 8) {
 #pragma unroll
-            for (int m = 0; m < NM; ++m) prev[m] = cur[m];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    // S2: lanes of k part 0 carry the l (then h) bytes of their entry and the row's mins
-    const long al = p == 0 ? pack2(t.lh.x, t.lh.y) : 0;
-    const long ah = p == 0 ? pack2(t.lh.z, t.lh.w) : 0;
+        for (int m = 0; m < NM; ++m) {
+            // |D| <= 32 * 15 * 127 fits 24 bits: v_mad_i32_i24
+            int sv[4];
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-        const long bm = p == 0 ? pack2(mns[m][0], mns[m][1]) : 0;
-        const v4i dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bm, z, 0, 0, 0);
-        const v4i dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bm, z, 0, 0, 0);
-        const float d = f16_to_f32(w[m].hdr.x), dmin = f16_to_f32(w[m].hdr.x >> 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int s2 = dl[i] + 128 * dh[i];
-            const float dx = t.dx[i];
-            acc[m][i] = acc[m][i] + ((d * dx) * (float)s1[m][i] - (dmin * dx) * (float)s2);
+            for (int t = 0; t < 4; ++t) sv[t] = sc0[m] * ((d0[m][t] << 8) >> 8) + sc1[m] * ((d1[m][t] << 8) >> 8);
+            // sum over the row's four lanes, entry p left in lane p: rows p, p^1 exchange two
+            // values (odd rows' first <-> even rows' second), then lane halves one
+            const auto r0 = __builtin_amdgcn_permlane16_swap(sv[0], sv[1], false, false);
+            const auto r1 = __builtin_amdgcn_permlane16_swap(sv[2], sv[3], false, false);
+            const int z0 = (int)r0[0] + (int)r0[1], z1 = (int)r1[0] + (int)r1[1];
+            const auto r2 = __builtin_amdgcn_permlane32_swap(z0, z1, false, false);
+            const int s1 = (int)r2[0] + (int)r2[1];
+            const int s2 = sdot4(mns[m][0], lh.x, sdot4(mns[m][1], lh.y, 0)) +
+                           128 * sdot4(mns[m][0], lh.z, sdot4(mns[m][1], lh.w, 0));
+            const float d = f16_to_f32(hdr[m].x), dmin = f16_to_f32(hdr[m].x >> 16);
+            acc[m][g] = acc[m][g] + ((d * dx) * (float)s1 - (dmin * dx) * (float)s2);
         }
     }
 }
 
-// The super-blocks of NM weight rows against the item's entries, in order.  Weights and the
-// entries' sums and scales ping-pong between two register stages; the entries' codes between
-// two LDS buffers, each filled by the whole workgroup one super-block ahead.  bases: the
-// expert's matrices (wave-uniform); w_off: the lane's row.
-template <int NM>
-SYN_DEV void ffn_rows(const uint8_t* const (&bases)[NM], uint32_t w_off, const MoeAct& a, int k,
-                      int ent0, int nent, int p, uint8_t* tok, float (&acc)[NM][4]) {
+// The item's super-blocks in order through the three-stage LDS ring.  Each wavefront issues the
+// same loads for every stage (the entry groups the item has); before the arithmetic on
+// super-block b it waits until only the loads of b + 1 may still fly, then the barrier makes
+// the stage whole for the workgroup.
+template <class C>
+SYN_DEV void ffn_rows(const uint8_t* const (&bases)[C::NM], uint32_t row0_off, uint32_t rb,
+                      const MoeAct& a, int k, int ent0, int nent, int wave, uint8_t* lds,
+                      float (&acc)[C::NM][C::NG]) {
     const int nb = k / 256;
-    const int c = threadIdx.x & 15;
-    const int ent_a = ent0 + (c < nent ? c : nent - 1);
-    const uint32_t coff = 16u + 64u * (uint32_t)(p & 1) + 16u * (uint32_t)(p >> 1);
-    const uint32_t l0 = (uint32_t)ent_a * (uint32_t)nb * 16u;
-    const float* d0 = a.d + ent0 + 4 * p;  // four output entries; the array is padded past its end
-    const int64_t dstride = a.nentries;
-    uint8_t* const tb0 = tok;
-    uint8_t* const tb1 = tok + TOK_BUF;
-    WStage wa[NM], wb[NM];
-    TStage ta, tb;
-    tok_put(tb0, tok_fetch(a, k, 0, ent0, nent));
+    const int ngroups = (nent + 3) >> 2;
+    Slot sl[C::PER_WAVE];
+    int live = 0;  // loads this wavefront issues per stage
 #pragma unroll
-    for (int m = 0; m < NM; ++m) load_w(bases[m], w_off, coff, wa[m]);
-    load_t(a, l0, d0, ta);
-    __syncthreads();
-    // Pairs of super-blocks, every load and product unconditional inside the loop (a load
-    // whose only use sat under a branch would sink to that use and stop flying early); the
-    // odd last block, already in stage a, after it.
-#pragma unroll 1
-    for (int b = 0; b + 1 < nb; b += 2) {
-        const uint32_t b1 = (uint32_t)(b + 1);
-        const v4u n1 = tok_fetch(a, k, b1, ent0, nent);
-#pragma unroll
-        for (int m = 0; m < NM; ++m) load_w(bases[m], w_off + 144u * b1, coff, wb[m]);
-        load_t(a, l0 + 16u * b1, d0 + dstride * b1, tb);
-        __builtin_amdgcn_sched_barrier(0);
-        q4k_super<NM>(wa, ta, tb0, p, acc);
-        tok_put(tb1, n1);
-        __syncthreads();
-        // the next pair's first block; past the end, the last block again
-        const uint32_t b2 = (uint32_t)(b + 2 < nb ? b + 2 : nb - 1);
-        const v4u n2 = tok_fetch(a, k, b2, ent0, nent);
-#pragma unroll
-        for (int m = 0; m < NM; ++m) load_w(bases[m], w_off + 144u * b2, coff, wa[m]);
-        load_t(a, l0 + 16u * b2, d0 + dstride * b2, ta);
-        __builtin_amdgcn_sched_barrier(0);
-        q4k_super<NM>(wb, tb, tb1, p, acc);
-        tok_put(tb0, n2);
-        __syncthreads();
+    for (int i = 0; i < C::PER_WAVE; ++i) {
+        sl[i] = make_slot<C>(wave + C::WV * i, bases, row0_off, rb, a, k, ent0, nent);
+        live += sl[i].live ? 1 : 0;
     }
-    if (nb & 1) {
-        q4k_super<NM>(wa, ta, tb0, p, acc);
+#pragma unroll
+    for (int i = 0; i < C::PER_WAVE; ++i) issue_slot(sl[i], 0, lds);
+    if (nb > 1) {
+#pragma unroll
+        for (int i = 0; i < C::PER_WAVE; ++i) issue_slot(sl[i], 1, lds + C::BYTES);
+    }
+    int cur = 0;  // stage of super-block b
+#pragma unroll 1
+    for (int b = 0; b < nb; ++b) {
+        wait_vm_n<C::PER_WAVE>(b + 1 < nb ? live : 0);
+        lds_barrier();
+        if (b + 2 < nb) {
+            const int nxt = cur == 0 ? 2 : cur - 1;  // (cur + 2) % 3
+#pragma unroll
+            for (int i = 0; i < C::PER_WAVE; ++i) issue_slot(sl[i], b + 2, lds + nxt * C::BYTES);
+        }
+        q4k_super<C>(lds + cur * C::BYTES, wave, ent0, ngroups, acc);
+        cur = cur == 2 ? 0 : cur + 1;
     }
 }
 
@@ -615,16 +677,16 @@ SYN_DEV void ffn_rows(const uint8_t* const (&bases)[NM], uint32_t w_off, const M
 struct MoeItems {
     const uint32_t* offsets;
     int n_experts;
-    int row_groups;  // weight rows / 64
+    int row_groups;  // weight rows / rows per item
+    int chunk;       // entries per item
 };
-constexpr int MOE_CHUNK = 16;  // entries per item
 
 // Maps a flat item index to (expert, row group, entry chunk); items of an expert with fewer
 // entries are empty.  Items: expert-major, then entry chunk, then row group.  The item space,
 // n_experts * row_groups * max_chunks, is sized on the device from the largest expert.
-SYN_DEV int moe_max_chunks(const uint32_t* err) {
+SYN_DEV int moe_max_chunks(const MoeItems& it, const uint32_t* err) {
     const int most = (int)err[1];
-    return (most + MOE_CHUNK - 1) / MOE_CHUNK;
+    return (most + it.chunk - 1) / it.chunk;
 }
 SYN_DEV bool moe_item(const MoeItems& it, int item, int max_chunks, int& e, int& rg, int& ent0,
                       int& nent) {
@@ -635,92 +697,110 @@ SYN_DEV bool moe_item(const MoeItems& it, int item, int max_chunks, int& e, int&
     rg = r - ch * it.row_groups;
     if (e >= it.n_experts) return false;
     const int b0 = (int)it.offsets[e], b1 = (int)it.offsets[e + 1];
-    ent0 = b0 + ch * MOE_CHUNK;
+    ent0 = b0 + ch * it.chunk;
     if (ent0 >= b1) return false;
-    nent = b1 - ent0 < MOE_CHUNK ? b1 - ent0 : MOE_CHUNK;
+    nent = b1 - ent0 < it.chunk ? b1 - ent0 : it.chunk;
     return true;
 }
 
 // gate/up + SiLU: h[entry][row] = silu(gate_row . x) * (up_row . x) (moe.rs:466-499).
-__global__ __launch_bounds__(256, 3) void k_moe_gateup(const uint8_t* __restrict__ gate,
-                                                       const uint8_t* __restrict__ up, int inter,
-                                                       int hidden, MoeItems it, MoeAct a,
-                                                       const uint32_t* __restrict__ err,
-                                                       float* __restrict__ h) {
-    __shared__ __attribute__((aligned(16))) uint8_t tok[2 * TOK_BUF];
+template <int WV, int CH>
+__global__ __launch_bounds__(64 * WV) void k_moe_gateup(const uint8_t* __restrict__ gate,
+                                                        const uint8_t* __restrict__ up, int inter,
+                                                        int hidden, MoeItems it, MoeAct a,
+                                                        const uint32_t* __restrict__ err,
+                                                        float* __restrict__ h) {
+    using C = MoeCfg<2, WV, CH>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     if (err[0]) return;
-    const int max_chunks = moe_max_chunks(err);
+    const int max_chunks = moe_max_chunks(it, err);
     const int total = it.n_experts * it.row_groups * max_chunks;
     const int lane = threadIdx.x & 63, p = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t row_bytes = (uint32_t)(hidden / 256) * 144u;
+    const uint32_t rb = (uint32_t)(hidden / 256) * 144u;
     for (int item = blockIdx.x; item < total; item += gridDim.x) {
         int e, rg, ent0, nent;
         if (!moe_item(it, item, max_chunks, e, rg, ent0, nent)) continue;  // uniform per workgroup
-        const int row = rg * 64 + wave * 16 + (lane & 15);
-        const int64_t ebytes = (int64_t)inter * row_bytes;
+        const int64_t ebytes = (int64_t)inter * rb;
         const uint8_t* const bases[2] = {gate + e * ebytes, up + e * ebytes};
-        float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-        ffn_rows<2>(bases, (uint32_t)row * row_bytes, a, hidden, ent0, nent, p, tok, acc);
+        float acc[2][C::NG] = {};
+        ffn_rows<C>(bases, (uint32_t)(rg * C::ROWS) * rb, rb, a, hidden, ent0, nent, wave, lds, acc);
+        const int row = rg * C::ROWS + wave * 16 + (lane & 15);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (4 * p + i < nent)
-                h[(int64_t)(ent0 + 4 * p + i) * inter + row] = ref_silu(acc[0][i]) * acc[1][i];
-        __syncthreads();  // the LDS buffers are refilled by the next item
+        for (int g = 0; g < C::NG; ++g)
+            if (4 * g + p < nent)
+                h[(int64_t)(ent0 + 4 * g + p) * inter + row] = ref_silu(acc[0][g]) * acc[1][g];
+        lds_barrier();  // the ring is refilled by the next item
     }
 }
 
 // down: out[slot][row] = down_row . hq[entry], written to the entry's slot (the reference's
 // scatter, moe.rs:501-515).
-__global__ __launch_bounds__(256, 3) void k_moe_down(const uint8_t* __restrict__ down, int hidden,
-                                                     int inter, MoeItems it, MoeAct a,
-                                                     const uint32_t* __restrict__ slots,
-                                                     const uint32_t* __restrict__ err,
-                                                     float* __restrict__ out) {
-    __shared__ __attribute__((aligned(16))) uint8_t tok[2 * TOK_BUF];
+template <int WV, int CH>
+__global__ __launch_bounds__(64 * WV) void k_moe_down(const uint8_t* __restrict__ down, int hidden,
+                                                      int inter, MoeItems it, MoeAct a,
+                                                      const uint32_t* __restrict__ slots,
+                                                      const uint32_t* __restrict__ err,
+                                                      float* __restrict__ out) {
+    using C = MoeCfg<1, WV, CH>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     if (err[0]) return;
-    const int max_chunks = moe_max_chunks(err);
+    const int max_chunks = moe_max_chunks(it, err);
     const int total = it.n_experts * it.row_groups * max_chunks;
     const int lane = threadIdx.x & 63, p = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t row_bytes = (uint32_t)(inter / 256) * 144u;
+    const uint32_t rb = (uint32_t)(inter / 256) * 144u;
     for (int item = blockIdx.x; item < total; item += gridDim.x) {
         int e, rg, ent0, nent;
         if (!moe_item(it, item, max_chunks, e, rg, ent0, nent)) continue;  // uniform per workgroup
-        const int row = rg * 64 + wave * 16 + (lane & 15);
-        const uint8_t* const bases[1] = {down + e * ((int64_t)hidden * row_bytes)};
-        float acc[1][4] = {{0.0f, 0.0f, 0.0f, 0.0f}};
-        ffn_rows<1>(bases, (uint32_t)row * row_bytes, a, inter, ent0, nent, p, tok, acc);
+        const uint8_t* const bases[1] = {down + e * ((int64_t)hidden * rb)};
+        float acc[1][C::NG] = {};
+        ffn_rows<C>(bases, (uint32_t)(rg * C::ROWS) * rb, rb, a, inter, ent0, nent, wave, lds, acc);
+        const int row = rg * C::ROWS + wave * 16 + (lane & 15);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (4 * p + i < nent) out[(int64_t)slots[ent0 + 4 * p + i] * hidden + row] = acc[0][i];
-        __syncthreads();  // the LDS buffers are refilled by the next item
+        for (int g = 0; g < C::NG; ++g)
+            if (4 * g + p < nent) out[(int64_t)slots[ent0 + 4 * g + p] * hidden + row] = acc[0][g];
+        lds_barrier();  // the ring is refilled by the next item
     }
 }
 
 // The grid covers every item of the common case (the largest expert within one entry chunk)
 // with one workgroup each; larger item spaces, sized on the device, are walked grid-stride.
-static unsigned moe_grid(int n_experts, int row_groups, int nentries) {
-    int64_t items = (int64_t)n_experts * row_groups;
-    const int64_t cap = (int64_t)n_experts * row_groups * ((nentries + MOE_CHUNK - 1) / MOE_CHUNK);
+static unsigned moe_grid(const MoeItems& it, int nentries) {
+    int64_t items = (int64_t)it.n_experts * it.row_groups;
+    const int64_t cap = (int64_t)it.n_experts * it.row_groups * ((nentries + it.chunk - 1) / it.chunk);
     items = items < cap ? items : cap;
     return (unsigned)(items > 0 ? items : 1);
 }
 
+// gate/up: four wavefronts (64 rows), up to 16 entries per item; down: the same
+constexpr int GU_WV = 4, GU_CH = 16;
+constexpr int DN_WV = 4, DN_CH = 16;
+
 void launch_moe_gateup(const uint8_t* gate, const uint8_t* up, int n_experts, int hidden,
                        int inter, const uint32_t* offsets, int nentries, MoeAct a,
                        const uint32_t* err, float* h, hipStream_t stream) {
-    MoeItems it{offsets, n_experts, inter / 64};
-    hipLaunchKernelGGL(k_moe_gateup, dim3(moe_grid(n_experts, it.row_groups, nentries)), dim3(256), 0,
-                       stream, gate, up, inter, hidden, it, a, err, h);
+    using C = MoeCfg<2, GU_WV, GU_CH>;
+    const MoeItems it{offsets, n_experts, inter / C::ROWS, C::CH};
+    const int lds = MOE_STAGES * C::BYTES;
+    static const hipError_t lds_ok = hipFuncSetAttribute(
+        (const void*)k_moe_gateup<GU_WV, GU_CH>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    (void)lds_ok;  // a refusal shows as the launch's error
+    hipLaunchKernelGGL((k_moe_gateup<GU_WV, GU_CH>), dim3(moe_grid(it, nentries)), dim3(C::THREADS),
+                       lds, stream, gate, up, inter, hidden, it, a, err, h);
 }
 
 void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
                      const uint32_t* offsets, int nentries, MoeAct a, const uint32_t* slots,
                      const uint32_t* err, float* out, hipStream_t stream) {
-    MoeItems it{offsets, n_experts, hidden / 64};
-    hipLaunchKernelGGL(k_moe_down, dim3(moe_grid(n_experts, it.row_groups, nentries)), dim3(256), 0,
-                       stream, down, hidden, inter, it, a, slots, err, out);
+    using C = MoeCfg<1, DN_WV, DN_CH>;
+    const MoeItems it{offsets, n_experts, hidden / C::ROWS, C::CH};
+    const int lds = MOE_STAGES * C::BYTES;
+    static const hipError_t lds_ok = hipFuncSetAttribute(
+        (const void*)k_moe_down<DN_WV, DN_CH>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    (void)lds_ok;  // a refusal shows as the launch's error
+    hipLaunchKernelGGL((k_moe_down<DN_WV, DN_CH>), dim3(moe_grid(it, nentries)), dim3(C::THREADS),
+                       lds, stream, down, hidden, inter, it, a, slots, err, out);
 }
 
 // ============================================================================================
