@@ -77,6 +77,15 @@ int syn_gemv_batch(uint32_t n, const int32_t* wtypes, const void* const* w,
                    const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
                    void* stream);
 
+/* The two halves of syn_gemv_batch, for callers that quantize once and multiply later (the
+ * reference's Gemv launch does the same in two steps: act.rs:122-167, then gemv.rs:435-492):
+ * the n rows x[i] (F32 [k_in[i]]) to Q8_K in ws, then the grouped GEMV on ws. */
+int syn_act_quantize_batch(uint32_t n, const uint32_t* k_in, const float* const* x, void* ws,
+                           uint64_t ws_bytes, void* stream);
+int syn_gemv_batch_quantized(uint32_t n, const int32_t* wtypes, const void* const* w,
+                             const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
+                             const void* ws, uint64_t ws_bytes, float* const* y, void* stream);
+
 /* ---- MoE layer ----------------------------------------------------------------------------
  * MoeRoute{Softmax}: ids I32 [rows, top_k] and weights F32 [rows, top_k] from x F32
  * [rows, hidden] and the router F32 [n_experts, hidden].  Logits are F32Fixed dot products

@@ -45,6 +45,8 @@ def lib():
         "syn_quantize": [i32, fp, u64, vp, u64, vp],
         "syn_gemv_batch_workspace_bytes": [u32, vp, C.POINTER(C.c_uint64)],
         "syn_gemv_batch": [u32, vp, vp, vp, vp, vp, vp, vp, vp, u64, vp],
+        "syn_act_quantize_batch": [u32, vp, vp, vp, u64, vp],
+        "syn_gemv_batch_quantized": [u32, vp, vp, vp, vp, vp, vp, u64, vp, vp],
         "syn_dequantize": [i32, vp, u64, fp, vp],
         "syn_moe_route": [vp, vp, u32, u32, u32, u32, i32, vp, vp, vp, vp],
         "syn_moe_pack": [vp, u32, u32, u32, vp, vp, vp, vp],

@@ -144,50 +144,105 @@ SYN_EXPORT int syn_gemv_batch_workspace_bytes(uint32_t n, const uint32_t* k_in, 
     return SYN_OK;
 }
 
-SYN_EXPORT int syn_gemv_batch(uint32_t n, const int32_t* wtypes, const void* const* w,
-                              const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
-                              const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
-                              void* stream) {
-    const char* W = "syn_gemv_batch";
-    if (n == 0) return SYN_OK;
+namespace {
+
+// Shared checks of the grouped entry points: problem i's quantized row sits at ws + off[i].
+int batch_setup(const char* W, uint32_t n, const int32_t* wtypes, const void* const* w,
+                const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in, void* ws,
+                uint64_t ws_bytes, uint64_t* off) {
     if (n > SYN_BATCH) return fail(SYN_E_UNSUPPORTED, "%s: at most %d problems", W, SYN_BATCH);
-    if (!wtypes || !w || !w_bytes || !n_out || !k_in || !x || !y)
-        return fail(SYN_E_INVALID, "%s: null argument array", W);
+    if (!k_in || (w && (!wtypes || !w_bytes || !n_out))) return fail(SYN_E_INVALID, "%s: null argument array", W);
     uint64_t need = 0;
     if (int rc = syn_gemv_batch_workspace_bytes(n, k_in, &need)) return rc;
     if (ws_bytes < need)
         return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
                     (unsigned long long)ws_bytes, (unsigned long long)need);
     if (!ws || !aligned(ws, 256)) return fail(SYN_E_INVALID, "%s: the workspace must be 256-byte aligned", W);
+    uint64_t o = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (k_in[i] == 0 || k_in[i] > 16384) return fail(SYN_E_UNSUPPORTED, "%s: k_in[%u] = %u (1..16384)", W, i, k_in[i]);
+        if (w) {
+            if (wtypes[i] != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: problem %u is not Q4_K", W, i);
+            if (n_out[i] == 0 || n_out[i] > (1u << 28)) return fail(SYN_E_INVALID, "%s: n_out[%u] = %u", W, i, n_out[i]);
+            const uint64_t need_w = (uint64_t)k_in[i] / 256 * 144 * n_out[i];
+            if (w_bytes[i] < need_w) return fail(SYN_E_INVALID, "%s: weight %u holds %llu bytes, the matrix %llu", W, i, (unsigned long long)w_bytes[i], (unsigned long long)need_w);
+            if (!w[i] || !aligned(w[i], 16)) return fail(SYN_E_INVALID, "%s: problem %u: W must be a 16-byte aligned pointer", W, i);
+        }
+        off[i] = o;
+        o += syn::act_layout(syn::ACT_Q8K, 1, k_in[i]).bytes;
+    }
+    return SYN_OK;
+}
+
+int batch_quantize(const char* W, uint32_t n, const uint32_t* k_in, const float* const* x,
+                   uint8_t* ws, const uint64_t* off, hipStream_t st) {
+    const float* xp[SYN_BATCH];
+    uint8_t* wsm[SYN_BATCH];
+    int kk[SYN_BATCH];
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!x[i] || !aligned(x[i], 16)) return fail(SYN_E_INVALID, "%s: x[%u] must be a 16-byte aligned pointer", W, i);
+        xp[i] = x[i];
+        wsm[i] = ws + off[i];
+        kk[i] = (int)k_in[i];
+    }
+    syn::launch_act_quant_batch((int)n, xp, kk, wsm, st);
+    return check_launch(W);
+}
+
+int batch_gemv(const char* W, uint32_t n, const void* const* w, const uint32_t* n_out,
+               const uint32_t* k_in, const uint8_t* ws, const uint64_t* off, float* const* y,
+               hipStream_t st) {
     const uint8_t* wp[SYN_BATCH];
     const uint8_t* wsp[SYN_BATCH];
-    uint8_t* wsm[SYN_BATCH];
-    const float* xp[SYN_BATCH];
     float* yp[SYN_BATCH];
     int no[SYN_BATCH], kk[SYN_BATCH];
-    uint64_t off = 0;
     for (uint32_t i = 0; i < n; ++i) {
-        if (wtypes[i] != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: problem %u is not Q4_K", W, i);
-        if (k_in[i] == 0 || k_in[i] > 16384) return fail(SYN_E_UNSUPPORTED, "%s: k_in[%u] = %u (1..16384)", W, i, k_in[i]);
-        if (n_out[i] == 0 || n_out[i] > (1u << 28)) return fail(SYN_E_INVALID, "%s: n_out[%u] = %u", W, i, n_out[i]);
-        const uint64_t need_w = (uint64_t)k_in[i] / 256 * 144 * n_out[i];
-        if (w_bytes[i] < need_w) return fail(SYN_E_INVALID, "%s: weight %u holds %llu bytes, the matrix %llu", W, i, (unsigned long long)w_bytes[i], (unsigned long long)need_w);
-        if (!w[i] || !x[i] || !y[i]) return fail(SYN_E_INVALID, "%s: null operand in problem %u", W, i);
-        if (!aligned(w[i], 16) || !aligned(x[i], 16) || !aligned(y[i], 4))
-            return fail(SYN_E_INVALID, "%s: problem %u: W and x must be 16-byte, y 4-byte aligned", W, i);
+        if (!y[i] || !aligned(y[i], 4)) return fail(SYN_E_INVALID, "%s: y[%u] must be a 4-byte aligned pointer", W, i);
         wp[i] = (const uint8_t*)w[i];
-        wsm[i] = (uint8_t*)ws + off;
-        wsp[i] = wsm[i];
-        xp[i] = x[i];
+        wsp[i] = ws + off[i];
         yp[i] = y[i];
         no[i] = (int)n_out[i];
         kk[i] = (int)k_in[i];
-        off += syn::act_layout(syn::ACT_Q8K, 1, k_in[i]).bytes;
     }
-    syn::launch_act_quant_batch((int)n, xp, kk, wsm, (hipStream_t)stream);
-    if (int rc = check_launch(W)) return rc;
-    syn::launch_gemv_q4k_batch((int)n, wp, no, kk, wsp, yp, (hipStream_t)stream);
+    syn::launch_gemv_q4k_batch((int)n, wp, no, kk, wsp, yp, st);
     return check_launch(W);
+}
+
+}  // namespace
+
+SYN_EXPORT int syn_act_quantize_batch(uint32_t n, const uint32_t* k_in, const float* const* x,
+                                      void* ws, uint64_t ws_bytes, void* stream) {
+    const char* W = "syn_act_quantize_batch";
+    if (n == 0) return SYN_OK;
+    if (!x) return fail(SYN_E_INVALID, "%s: null argument array", W);
+    uint64_t off[SYN_BATCH];
+    if (int rc = batch_setup(W, n, nullptr, nullptr, nullptr, nullptr, k_in, ws, ws_bytes, off)) return rc;
+    return batch_quantize(W, n, k_in, x, (uint8_t*)ws, off, (hipStream_t)stream);
+}
+
+SYN_EXPORT int syn_gemv_batch_quantized(uint32_t n, const int32_t* wtypes, const void* const* w,
+                                        const uint64_t* w_bytes, const uint32_t* n_out,
+                                        const uint32_t* k_in, const void* ws, uint64_t ws_bytes,
+                                        float* const* y, void* stream) {
+    const char* W = "syn_gemv_batch_quantized";
+    if (n == 0) return SYN_OK;
+    if (!w || !y) return fail(SYN_E_INVALID, "%s: null argument array", W);
+    uint64_t off[SYN_BATCH];
+    if (int rc = batch_setup(W, n, wtypes, w, w_bytes, n_out, k_in, (void*)ws, ws_bytes, off)) return rc;
+    return batch_gemv(W, n, w, n_out, k_in, (const uint8_t*)ws, off, y, (hipStream_t)stream);
+}
+
+SYN_EXPORT int syn_gemv_batch(uint32_t n, const int32_t* wtypes, const void* const* w,
+                              const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
+                              const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
+                              void* stream) {
+    const char* W = "syn_gemv_batch";
+    if (n == 0) return SYN_OK;
+    if (!w || !x || !y) return fail(SYN_E_INVALID, "%s: null argument array", W);
+    uint64_t off[SYN_BATCH];
+    if (int rc = batch_setup(W, n, wtypes, w, w_bytes, n_out, k_in, ws, ws_bytes, off)) return rc;
+    if (int rc = batch_quantize(W, n, k_in, x, (uint8_t*)ws, off, (hipStream_t)stream)) return rc;
+    return batch_gemv(W, n, w, n_out, k_in, (const uint8_t*)ws, off, y, (hipStream_t)stream);
 }
 
 SYN_EXPORT int syn_quantize(int32_t wtype, const float* x, uint64_t n, void* out,

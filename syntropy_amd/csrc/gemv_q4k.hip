@@ -31,6 +31,7 @@ namespace {
 constexpr int COL = 272;  // LDS bytes per activation column (256 codes + 16-byte skew)
 constexpr int SUMW = 48;  // LDS bytes per column of 32-value sums (8 ints + skew)
 
+SYN_HD inline size_t q4k_dec_lds(int nb) { return (size_t)nb * (COL + SUMW + 4); }
 SYN_DEV int xs_off(int nb) { return nb * COL; }
 SYN_DEV int xd_off(int nb) { return nb * (COL + SUMW); }
 
@@ -42,73 +43,76 @@ SYN_DEV v4u ldw(const uint8_t* p) {
         return *reinterpret_cast<const v4u*>(p);
 }
 
+// Lane `part` = c % 16 of super-block c / 16's group of 16 lanes: values 16 part .. +15.
+SYN_DEV void quant_block16(const float* __restrict__ x, int c, int nb, uint8_t* lds) {
+    const int sb = c >> 4, part = c & 15;
+    const float4* src = reinterpret_cast<const float4*>(x + (int64_t)sb * 256 + part * 16);
+    const float4 a0 = src[0], a1 = src[1], a2 = src[2], a3 = src[3];
+    const float v[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                         a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+    bool fin = true;
+    float amax = 0.0f, mx = 0.0f;
+    int idx = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        fin = fin && finite_f(v[i]);
+        const float av = __builtin_fabsf(v[i]);
+        if (av > amax) {
+            amax = av;
+            mx = v[i];
+            idx = part * 16 + i;
+        }
+    }
+    int bad = !fin;
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {
+        const float oa = __shfl_xor(amax, off);
+        const float om = __shfl_xor(mx, off);
+        const int oi = __shfl_xor(idx, off);
+        bad |= __shfl_xor(bad, off);
+        if (oa > amax || (oa == amax && oi < idx)) {
+            amax = oa;
+            mx = om;
+            idx = oi;
+        }
+    }
+    float d = 0.0f;
+    int q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = 0;
+    if (bad) {
+        d = __builtin_nanf("");
+    } else if (amax != 0.0f) {
+        const float iscale = -127.0f / mx;
+        if (finite_f(iscale)) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int n = nearest_int(iscale * v[i]);
+                q[i] = n < 127 ? n : 127;
+            }
+        }
+        d = 1.0f / iscale;
+    }
+    uint32_t w[4];
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        w[k] = (uint32_t)(q[4 * k] & 0xFF) | ((uint32_t)(q[4 * k + 1] & 0xFF) << 8) |
+               ((uint32_t)(q[4 * k + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * k + 3] & 0xFF) << 24);
+        s += q[4 * k] + q[4 * k + 1] + q[4 * k + 2] + q[4 * k + 3];
+    }
+    v4u pk = {w[0], w[1], w[2], w[3]};
+    *reinterpret_cast<v4u*>(lds + sb * COL + part * 16) = pk;
+    s += __shfl_xor(s, 1);  // the two 16-value halves of a 32-value group
+    if ((part & 1) == 0) reinterpret_cast<int*>(lds + xs_off(nb) + sb * SUMW)[part >> 1] = s;
+    if (part == 0) reinterpret_cast<float*>(lds + xd_off(nb))[sb] = d;
+}
+
 // Q8_K of the activation row into LDS (crates/kernels-cpu/src/gemv/act.rs:351-373): 16 lanes
 // per 256-value super-block, 16 values per lane.  Largest magnitude, first index on ties.
 SYN_DEV void quant_row_to_lds(const float* __restrict__ x, int nb, uint8_t* lds) {
-    const int t = threadIdx.x;
-    for (int c = t; c < nb * 16; c += 256) {  // the 16 lanes of a super-block stay together
-        const int sb = c >> 4, part = c & 15;
-        const float4* src = reinterpret_cast<const float4*>(x + (int64_t)sb * 256 + part * 16);
-        const float4 a0 = src[0], a1 = src[1], a2 = src[2], a3 = src[3];
-        const float v[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
-                             a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
-        bool fin = true;
-        float amax = 0.0f, mx = 0.0f;
-        int idx = 0x7FFFFFFF;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            fin = fin && finite_f(v[i]);
-            const float av = __builtin_fabsf(v[i]);
-            if (av > amax) {
-                amax = av;
-                mx = v[i];
-                idx = part * 16 + i;
-            }
-        }
-        int bad = !fin;
-#pragma unroll
-        for (int off = 8; off >= 1; off >>= 1) {
-            const float oa = __shfl_xor(amax, off);
-            const float om = __shfl_xor(mx, off);
-            const int oi = __shfl_xor(idx, off);
-            bad |= __shfl_xor(bad, off);
-            if (oa > amax || (oa == amax && oi < idx)) {
-                amax = oa;
-                mx = om;
-                idx = oi;
-            }
-        }
-        float d = 0.0f;
-        int q[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) q[i] = 0;
-        if (bad) {
-            d = __builtin_nanf("");
-        } else if (amax != 0.0f) {
-            const float iscale = -127.0f / mx;
-            if (finite_f(iscale)) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int n = nearest_int(iscale * v[i]);
-                    q[i] = n < 127 ? n : 127;
-                }
-            }
-            d = 1.0f / iscale;
-        }
-        uint32_t w[4];
-        int s = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            w[k] = (uint32_t)(q[4 * k] & 0xFF) | ((uint32_t)(q[4 * k + 1] & 0xFF) << 8) |
-                   ((uint32_t)(q[4 * k + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * k + 3] & 0xFF) << 24);
-            s += q[4 * k] + q[4 * k + 1] + q[4 * k + 2] + q[4 * k + 3];
-        }
-        v4u pk = {w[0], w[1], w[2], w[3]};
-        *reinterpret_cast<v4u*>(lds + sb * COL + part * 16) = pk;
-        s += __shfl_xor(s, 1);  // the two 16-value halves of a 32-value group
-        if ((part & 1) == 0) reinterpret_cast<int*>(lds + xs_off(nb) + sb * SUMW)[part >> 1] = s;
-        if (part == 0) reinterpret_cast<float*>(lds + xd_off(nb))[sb] = d;
-    }
+    for (int c = threadIdx.x; c < nb * 16; c += blockDim.x)  // the 16 lanes of a super-block stay together
+        quant_block16(x, c, nb, lds);
 }
 
 SYN_DEV void copy_row_to_lds(const int8_t* __restrict__ xq, const float* __restrict__ xd,
@@ -242,7 +246,11 @@ __global__ __launch_bounds__(256) void k_gemv_q4k_dec(const uint8_t* __restrict_
 }
 
 // Up to SYN_BATCH independent single-row GEMVs in one launch: problem p takes workgroups
-// [wg_begin[p], wg_begin[p+1]); its activation row was quantized into ws[p] beforehand.
+// [wg_begin[p], wg_begin[p+1]); its activation row was quantized into ws[p] beforehand.  A row
+// takes P lanes (P = 16, 32 or 64, the smallest holding all nb <= 64 of its super-blocks), lane
+// j its super-block j, so every lane loads exactly one block and no wavefront holds a second
+// block's registers: the kernel keeps enough wavefronts resident to cover HBM latency.  Each
+// row's terms are folded in order by one lane from LDS.
 struct DecBatch {
     const uint8_t* W[SYN_BATCH];
     const uint8_t* ws[SYN_BATCH];
@@ -253,33 +261,50 @@ struct DecBatch {
     int np;
 };
 
-template <int NT>
-__global__ __launch_bounds__(256) void k_gemv_q4k_batch(DecBatch bt) {
+SYN_DEV int lanes_per_row(int nb) { return nb <= 16 ? 16 : nb <= 32 ? 32 : 64; }
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6)))
+void k_gemv_q4k_batch(DecBatch bt) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int p = 0;
     while (p + 1 < bt.np && (int)blockIdx.x >= bt.wg_begin[p + 1]) ++p;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint8_t* W = bt.W[p];
     const int n_out = bt.n_out[p], nb = bt.nb[p];
-    const int row = (((int)blockIdx.x - bt.wg_begin[p]) * 4 + wave) * 4 + (lane >> 4);
+    const int P = lanes_per_row(nb);
+    const int rows_per_wave = 64 / P;
+    const int row = (((int)blockIdx.x - bt.wg_begin[p]) * 4 + wave) * rows_per_wave + lane / P;
+    const int b = lane % P;
+    const bool ok = row < n_out && b < nb;
+    // the lane's block, in flight while the activation row is copied
+    const uint8_t* src = ok ? W + (int64_t)row * nb * 144 + (int64_t)b * 144 : W;
     v4u A[9];
-    load_round0<NT>(W, n_out, nb, row, A);
+#pragma unroll
+    for (int i = 0; i < 9; ++i) A[i] = *reinterpret_cast<const v4u*>(src + 16 * i);
     const ActLayout L = act_layout(ACT_Q8K, 1, (uint64_t)nb * 256);
     copy_row_to_lds(reinterpret_cast<const int8_t*>(bt.ws[p] + L.codes),
                     reinterpret_cast<const float*>(bt.ws[p] + L.d),
                     reinterpret_cast<const int32_t*>(bt.ws[p] + L.sums), nb, lds);
     __syncthreads();
-    if (nb <= 16)
-        rowgroup_body<NT, 1>(W, n_out, nb, row, lds, A, bt.y[p]);
-    else if (nb <= 32)
-        rowgroup_body<NT, 2>(W, n_out, nb, row, lds, A, bt.y[p]);
-    else if (nb <= 64)
-        rowgroup_body<NT, 4>(W, n_out, nb, row, lds, A, bt.y[p]);
-    else
-        rowgroup_body<NT, 8>(W, n_out, nb, row, lds, A, bt.y[p]);
+    const float t = q4k_term_lds(A, lds, nb, ok ? b : 0);
+    // in-order fold: the row's P terms (+0.0 past its nb blocks, which leaves a sum that
+    // started from +0.0 unchanged) added by the row's first lane
+    float* terms = reinterpret_cast<float*>(lds + align_up(q4k_dec_lds(nb), 16)) + wave * 64;
+    terms[lane] = ok ? t : 0.0f;
+    wave_lds_sync();
+    if (b == 0 && row < n_out) {
+        const float4* tv = reinterpret_cast<const float4*>(terms + lane);
+        float acc = 0.0f;
+        for (int q = 0; q < P / 4; ++q) {
+            const float4 v = tv[q];
+            acc = acc + v.x;
+            acc = acc + v.y;
+            acc = acc + v.z;
+            acc = acc + v.w;
+        }
+        bt.y[p][row] = acc;
+    }
 }
-
-static size_t q4k_dec_lds(int nb) { return (size_t)nb * (COL + SUMW + 4); }
 
 // K up to 32768: at most 8 rounds, and the activation row within 41 KB of LDS.
 bool q4k_dec_supported(int k) { return k % 256 == 0 && k > 0 && k <= 32768; }
@@ -331,12 +356,16 @@ void launch_gemv_q4k_batch(int np, const uint8_t* const* W, const int* n_out, co
         bt.n_out[p] = n_out[p];
         bt.nb[p] = k[p] / 256;
         bt.wg_begin[p] = wg;
-        wg += ((n_out[p] + 3) / 4 + 3) / 4;
-        if (bt.nb[p] > max_nb) max_nb = bt.nb[p];
+        const int nb = bt.nb[p];
+        const int rows_per_wg = 4 * (64 / (nb <= 16 ? 16 : nb <= 32 ? 32 : 64));
+        wg += (n_out[p] + rows_per_wg - 1) / rows_per_wg;
+        if (nb > max_nb) max_nb = nb;
     }
     bt.wg_begin[np] = wg;
     if (wg == 0) return;
-    hipLaunchKernelGGL((k_gemv_q4k_batch<0>), dim3(wg), dim3(256), q4k_dec_lds(max_nb), stream, bt);
+    // the activation row, then 64 fold terms per wavefront
+    hipLaunchKernelGGL(k_gemv_q4k_batch, dim3(wg), dim3(256), align_up(q4k_dec_lds(max_nb), 16) + 4 * 64 * 4,
+                       stream, bt);
 }
 
 }  // namespace syn

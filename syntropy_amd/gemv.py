@@ -158,6 +158,16 @@ class GemvBatch:
         call("syn_gemv_batch", self.n, self.ty, self.w, self.wb, self.n_out, self.k, self.x,
              self.y, self.ws.data_ptr(), self.ws.numel(), _stream(stream))
 
+    def quantize(self, stream=None) -> None:
+        """The first half of __call__: every x[i] to Q8_K in the held workspace."""
+        call("syn_act_quantize_batch", self.n, self.k, self.x, self.ws.data_ptr(), self.ws.numel(),
+             _stream(stream))
+
+    def gemv_quantized(self, stream=None) -> None:
+        """The second half: every y[i] from the workspace quantize() filled."""
+        call("syn_gemv_batch_quantized", self.n, self.ty, self.w, self.wb, self.n_out, self.k,
+             self.ws.data_ptr(), self.ws.numel(), self.y, _stream(stream))
+
 
 def quantize(ty: WeightType, x: torch.Tensor, stream=None) -> torch.Tensor:
     """F32 values -> GGUF blocks, byte-identical to ggml's reference quantizers

@@ -245,6 +245,7 @@ def test_gemv_batch_layer_shapes(S):
     (Llama-3-8B shapes, output rows cut to keep the oracle quick) plus odd shapes."""
     shapes = [(6144, 4096), (4096, 4096), (14336, 4096), (14336, 4096), (4096, 14336),
               (37, 256), (5, 1536), (1, 16384)]
+    # every row width the kernel picks: 16 lanes (K <= 4096), 32 (<= 8192), 64 (<= 16384)
     Ws, xs, ys, want = [], [], [], []
     for i, (n_out, k) in enumerate(shapes):
         n = min(n_out, 1024)
@@ -260,6 +261,30 @@ def test_gemv_batch_layer_shapes(S):
         batch()
         for i in range(len(shapes)):
             assert_same(host(ys[i]), want[i], f"problem {i} rep {rep}")
+    # the two halves (quantize, then the GEMV on the Q8_K rows) give the same bits
+    for y in ys:
+        y.fill_(float("nan"))
+    batch.quantize()
+    batch.gemv_quantized()
+    for i in range(len(shapes)):
+        assert_same(host(ys[i]), want[i], f"problem {i} split")
+
+
+def test_gemv_batch_row_widths(S):
+    """K of 17..32 and 33..64 super-blocks (32- and 64-lane rows) and ragged row counts."""
+    shapes = [(50, 5120), (3, 8192), (65, 8448), (9, 12288), (130, 2048)]
+    Ws, xs, ys, want = [], [], [], []
+    for i, (n, k) in enumerate(shapes):
+        w = normal_weights(o.Q4_K, n, k, 0x51A70000 + i)
+        x = o.normal(0x51A80000 + i, 1.0, k)
+        want.append(o.gemv(o.Q4_K, w, n, k, x, 1))
+        Ws.append(S.Weights(S.WeightType.Q4K, dev(w), n, k))
+        xs.append(dev(x))
+        ys.append(torch.full((n,), float("nan"), device="cuda"))
+    announce("gemv batch row widths")
+    S.GemvBatch(Ws, xs, ys)()
+    for i in range(len(shapes)):
+        assert_same(host(ys[i]), want[i], f"problem {i}")
 
 
 # ---- weight packing and dequant ----------------------------------------------------------
