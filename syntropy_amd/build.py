@@ -1,9 +1,10 @@
-"""Builds libsyntropy_hip.so for gfx950 in-tree with hipcc.
+"""Builds libsyntropy_hip.so and libsyntropy_provider.so for gfx950 in-tree with hipcc.
 
     python -m syntropy_amd.build          # compile every source, link the library
 
-The library is C-ABI only (include/syntropy_hip.h, include/syntropy_provider.h); nothing in
-it links PyTorch.
+Two libraries, both C-ABI only and linking nothing of PyTorch: libsyntropy_hip.so (the
+kernels' entry points, include/syntropy_hip.h) and libsyntropy_provider.so (the same kernels
+behind the provider-library boundary, include/syntropy_provider.h).
 """
 from __future__ import annotations
 
@@ -19,6 +20,10 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsyntropy_hip.so")
+# The provider library: the same kernels behind the one symbol syntropy_provider_entry_v1
+# (include/syntropy_provider.h), everything else local, linked -Bsymbolic.
+PROVIDER_LIB = os.path.join(HERE, "libsyntropy_provider.so")
+PROVIDER_MAP = os.path.join(HERE, "provider.map")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -61,17 +66,24 @@ def _compile(src: str) -> str:
     return obj
 
 
+def _link(out: str, objs, extra=()) -> None:
+    tmp = out + ".tmp"
+    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, *extra],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link of {out} failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, out)
+
+
 def build(jobs: int = 8) -> str:
     os.makedirs(OBJ, exist_ok=True)
     srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=min(jobs, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
-    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs],
-                       capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+    provider = [o for o in objs if os.path.basename(o).startswith("provider.")]
+    kernels = [o for o in objs if o not in provider]
+    _link(LIB, kernels)
+    _link(PROVIDER_LIB, objs, [f"-Wl,--version-script={PROVIDER_MAP}", "-Wl,-Bsymbolic"])
     shutil.rmtree(OBJ, ignore_errors=True)
     return LIB
 

@@ -1,0 +1,984 @@
+// The provider-library boundary for MI355X: syntropy_provider_entry_v1 and its "hip" provider
+// (include/syntropy_provider.h).  The reference's module side is crates/kernels/src/abi/
+// (guest.rs: the thunks, export.rs: the table); its host side, kernels_loader::ModuleProvider
+// (crates/kernels-loader/src/provider.rs), calls this table unchanged.
+//
+// Behaviour kept from the reference's guest:
+//  * every entry runs under a catch-all; a caught exception returns Internal / ProviderPanicked
+//    (16) and makes the provider sticky, after which every entry but health, free and close_ctx
+//    returns Device / DeviceSticky (8) (guest.rs:184-230);
+//  * the message of the last failure is kept per thread and read with last_error
+//    (guest.rs:240-265);
+//  * a context lives in a per-thread table: a handle used on another thread is refused
+//    (guest.rs:267-280);
+//  * query answers with CapsWire JSON or nothing (len 0) for an op it does not serve
+//    (wire.rs:762-830); the JSON it reads is serde's form of OpKey and ShapeSig.
+//
+// The hot entries (launch, record, wait, poll, copy, copy_batch, replay, health) take no lock
+// and allocate nothing: they look up handles in the calling thread's context and enqueue.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/syntropy_hip.h"
+#include "../../include/syntropy_provider.h"
+
+#define SYN_PROVIDER_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+// ============================================================================================
+// Status, messages, stickiness
+// ============================================================================================
+
+struct Fail {
+    uint32_t cls;
+    uint16_t code;
+    std::string msg;
+};
+
+thread_local std::string t_message;
+std::atomic<uint16_t> g_sticky{0};
+
+SynStatus status(uint32_t cls, uint16_t code) {
+    SynStatus s;
+    s.cls = cls;
+    s.domain = SYN_DOMAIN_KERNELS;
+    s.code = code;
+    s.retry = 0;
+    return s;
+}
+const SynStatus OK = status(SYN_CLASS_OK, 0);
+
+[[noreturn]] void fail(uint32_t cls, uint16_t code, std::string msg) { throw Fail{cls, code, std::move(msg)}; }
+[[noreturn]] void internal(std::string msg) { fail(SYN_CLASS_INTERNAL, 0, std::move(msg)); }
+[[noreturn]] void unsupported(std::string msg) { fail(SYN_CLASS_UNSUPPORTED, SYN_CODE_OP_UNSUPPORTED, std::move(msg)); }
+
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) fail(SYN_CLASS_DEVICE, 0, std::string(what) + ": " + hipGetErrorString(e));
+}
+void check_syn(int rc, const char* what) {
+    if (rc == SYN_OK) return;
+    const std::string m = std::string(what) + ": " + syn_last_error();
+    if (rc == SYN_E_UNSUPPORTED) unsupported(m);
+    if (rc == SYN_E_WORKSPACE) fail(SYN_CLASS_INTERNAL, SYN_CODE_WORKSPACE_EXCEEDED, m);
+    if (rc == SYN_E_DEVICE) fail(SYN_CLASS_DEVICE, 0, m);
+    internal(m);
+}
+
+// Runs one entry: the sticky gate, the catch-all, the per-thread message.
+template <class F>
+SynStatus call(const char* name, bool allowed_when_sticky, F&& f) {
+    const uint16_t sticky = g_sticky.load(std::memory_order_acquire);
+    if (sticky && !allowed_when_sticky) {
+        t_message = std::string("`") + name + "` refused: the provider is sticky after code " +
+                    std::to_string(sticky);
+        return status(SYN_CLASS_DEVICE, SYN_CODE_DEVICE_STICKY);
+    }
+    try {
+        f();
+        return OK;
+    } catch (const Fail& e) {
+        t_message = e.msg;
+        return status(e.cls, e.code);
+    } catch (const std::exception& e) {
+        g_sticky.store(SYN_CODE_PROVIDER_PANICKED, std::memory_order_release);
+        t_message = std::string("the provider failed in `") + name + "`: " + e.what();
+        return status(SYN_CLASS_INTERNAL, SYN_CODE_PROVIDER_PANICKED);
+    } catch (...) {
+        g_sticky.store(SYN_CODE_PROVIDER_PANICKED, std::memory_order_release);
+        t_message = std::string("the provider failed in `") + name + "` with an unknown exception";
+        return status(SYN_CLASS_INTERNAL, SYN_CODE_PROVIDER_PANICKED);
+    }
+}
+
+void put(SynOutBuf* out, const std::string& s) {
+    if (!out) internal("null output buffer");
+    out->len = s.size();
+    if (s.size() <= out->cap && out->ptr) std::memcpy(out->ptr, s.data(), s.size());
+}
+
+// ============================================================================================
+// JSON: the serde forms of OpKey and ShapeSig (a small reader; objects keep their order)
+// ============================================================================================
+
+struct Json {
+    enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
+    double num = 0;
+    bool b = false;
+    std::string str;
+    std::vector<Json> arr;
+    std::vector<std::pair<std::string, Json>> obj;
+    const Json* get(const char* key) const {
+        for (const auto& kv : obj)
+            if (kv.first == key) return &kv.second;
+        return nullptr;
+    }
+};
+
+struct Reader {
+    const char* p;
+    const char* end;
+    void ws() {
+        while (p < end && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) ++p;
+    }
+    [[noreturn]] void bad(const char* what) { fail(SYN_CLASS_INVALID_REQUEST, 0, std::string("JSON: ") + what); }
+    std::string string() {
+        if (p >= end || *p != '"') bad("expected a string");
+        ++p;
+        std::string s;
+        while (p < end && *p != '"') {
+            if (*p == '\\') {
+                ++p;
+                if (p >= end) bad("unterminated escape");
+                const char c = *p;
+                s.push_back(c == 'n' ? '\n' : c == 't' ? '\t' : c == 'r' ? '\r' : c);
+                if (c == 'u') bad("\\u escapes are not used by these records");
+            } else {
+                s.push_back(*p);
+            }
+            ++p;
+        }
+        if (p >= end) bad("unterminated string");
+        ++p;
+        return s;
+    }
+    Json value(int depth = 0) {
+        if (depth > 32) bad("nested too deeply");
+        ws();
+        if (p >= end) bad("unexpected end");
+        Json v;
+        if (*p == '{') {
+            ++p;
+            v.kind = Json::Obj;
+            ws();
+            if (p < end && *p == '}') {
+                ++p;
+                return v;
+            }
+            for (;;) {
+                ws();
+                std::string k = string();
+                ws();
+                if (p >= end || *p != ':') bad("expected ':'");
+                ++p;
+                v.obj.emplace_back(std::move(k), value(depth + 1));
+                ws();
+                if (p < end && *p == ',') {
+                    ++p;
+                    continue;
+                }
+                if (p < end && *p == '}') {
+                    ++p;
+                    return v;
+                }
+                bad("expected ',' or '}'");
+            }
+        }
+        if (*p == '[') {
+            ++p;
+            v.kind = Json::Arr;
+            ws();
+            if (p < end && *p == ']') {
+                ++p;
+                return v;
+            }
+            for (;;) {
+                v.arr.push_back(value(depth + 1));
+                ws();
+                if (p < end && *p == ',') {
+                    ++p;
+                    continue;
+                }
+                if (p < end && *p == ']') {
+                    ++p;
+                    return v;
+                }
+                bad("expected ',' or ']'");
+            }
+        }
+        if (*p == '"') {
+            v.kind = Json::Str;
+            v.str = string();
+            return v;
+        }
+        if (end - p >= 4 && !std::strncmp(p, "true", 4)) {
+            p += 4;
+            v.kind = Json::Bool;
+            v.b = true;
+            return v;
+        }
+        if (end - p >= 5 && !std::strncmp(p, "false", 5)) {
+            p += 5;
+            v.kind = Json::Bool;
+            return v;
+        }
+        if (end - p >= 4 && !std::strncmp(p, "null", 4)) {
+            p += 4;
+            return v;
+        }
+        const char* s = p;
+        while (p < end && (std::strchr("+-.eE", *p) || (*p >= '0' && *p <= '9'))) ++p;
+        if (p == s) bad("unexpected character");
+        v.kind = Json::Num;
+        v.num = std::strtod(std::string(s, p).c_str(), nullptr);
+        return v;
+    }
+};
+
+Json parse(const uint8_t* data, size_t len) {
+    if (!data && len) internal("null JSON");
+    Reader r{reinterpret_cast<const char*>(data), reinterpret_cast<const char*>(data) + len};
+    Json v = r.value();
+    r.ws();
+    if (r.p != r.end) r.bad("trailing bytes");
+    return v;
+}
+
+uint32_t u32_of(const Json* v, const char* what) {
+    if (!v || v->kind != Json::Num || v->num < 0 || v->num > 4294967295.0 || v->num != (double)(uint64_t)v->num)
+        fail(SYN_CLASS_INVALID_REQUEST, 0, std::string("JSON: ") + what + " must be an unsigned integer");
+    return (uint32_t)v->num;
+}
+
+// ============================================================================================
+// Ops served: keys, shapes, capabilities
+// ============================================================================================
+
+enum class Op { Gemv, MoeGrouped, MoeRoute, MoeCombine, Other };
+
+struct Key {
+    Op op = Op::Other;
+    bool softmax = false;       // MoeRoute's norm
+    int weight = -1;            // ggml type id of schemes[0] when it is a Ggml scheme
+    bool rest_plain_f32 = true;  // every other scheme is Plain(F32)
+    size_t n_schemes = 0;
+    uint32_t layout = 0, variant = 0;
+};
+
+int ggml_id(const std::string& name) {
+    if (name == "Q4_0") return SYN_Q4_0;
+    if (name == "Q8_0") return SYN_Q8_0;
+    if (name == "Q4_K") return SYN_Q4_K;
+    return -2;  // a ggml type this provider does not compute
+}
+
+Key parse_key(const uint8_t* data, size_t len) {
+    const Json j = parse(data, len);
+    if (j.kind != Json::Obj) fail(SYN_CLASS_INVALID_REQUEST, 0, "OpKey: not an object");
+    Key k;
+    const Json* op = j.get("op");
+    if (!op) fail(SYN_CLASS_INVALID_REQUEST, 0, "OpKey: no op");
+    if (op->kind == Json::Str) {
+        if (op->str == "Gemv") k.op = Op::Gemv;
+        else if (op->str == "MoeGrouped") k.op = Op::MoeGrouped;
+        else if (op->str == "MoeCombine") k.op = Op::MoeCombine;
+    } else if (op->kind == Json::Obj && op->obj.size() == 1 && op->obj[0].first == "MoeRoute") {
+        k.op = Op::MoeRoute;
+        const Json* norm = op->obj[0].second.get("norm");
+        k.softmax = norm && norm->kind == Json::Str && norm->str == "Softmax";
+    }
+    const Json* schemes = j.get("schemes");
+    if (!schemes || schemes->kind != Json::Arr) fail(SYN_CLASS_INVALID_REQUEST, 0, "OpKey: no schemes");
+    k.n_schemes = schemes->arr.size();
+    for (size_t i = 0; i < schemes->arr.size(); ++i) {
+        const Json& s = schemes->arr[i];
+        const bool plain_f32 = s.kind == Json::Obj && s.obj.size() == 1 && s.obj[0].first == "Plain" &&
+                               s.obj[0].second.kind == Json::Str && s.obj[0].second.str == "F32";
+        if (i == 0 && s.kind == Json::Obj && s.obj.size() == 1 && s.obj[0].first == "Ggml" &&
+            s.obj[0].second.kind == Json::Str)
+            k.weight = ggml_id(s.obj[0].second.str);
+        else if (!plain_f32)
+            k.rest_plain_f32 = false;
+    }
+    k.layout = u32_of(j.get("layout"), "layout");
+    k.variant = u32_of(j.get("variant"), "variant");
+    return k;
+}
+
+struct Shape {
+    uint32_t rows = 0;
+    std::vector<uint32_t> dims;
+};
+
+Shape parse_shape(const uint8_t* data, size_t len) {
+    const Json j = parse(data, len);
+    if (j.kind != Json::Obj) fail(SYN_CLASS_INVALID_REQUEST, 0, "ShapeSig: not an object");
+    Shape s;
+    s.rows = u32_of(j.get("rows"), "rows");
+    const Json* dims = j.get("dims");
+    if (!dims || dims->kind != Json::Arr) fail(SYN_CLASS_INVALID_REQUEST, 0, "ShapeSig: no dims");
+    for (const Json& d : dims->arr) s.dims.push_back(u32_of(&d, "dims"));
+    return s;
+}
+
+// What one prepared (key, shape) computes.
+struct Plan {
+    Op op = Op::Other;
+    int weight = 0;
+    uint32_t rows = 0;
+    uint32_t dims[4] = {0, 0, 0, 0};
+    uint64_t workspace = 0;  // bytes the executor provides (incl. 256 of alignment slack)
+    uint32_t max_block = 0;
+    uint32_t act_in = 0;  // NumericsWire codes: 0 none, 2 Q8Block32, 3 Q8K256
+};
+
+uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+// The plan of a key and shape this provider serves, or false (query answers None).  Gemv and
+// MoeGrouped follow the reference's bindings (kernels-cpu/src/gemv/entry.rs:35-66,
+// moe/entry.rs:33-56); MoeRoute and MoeCombine their IR signatures
+// (crates/graph/src/ir/signature.rs:149,153).
+bool plan_of(const Key& k, const Shape& s, Plan& p) {
+    if (k.layout != 0 || k.variant != 0 || !k.rest_plain_f32) return false;
+    p.op = k.op;
+    p.rows = s.rows;
+    switch (k.op) {
+    case Op::Gemv: {
+        if (k.weight < 0 || k.n_schemes < 1 || k.n_schemes > 3 || s.dims.size() != 2) return false;
+        const uint32_t n_out = s.dims[0], k_in = s.dims[1];
+        uint64_t ws = 0;
+        if (syn_gemv_workspace_bytes(k.weight, s.rows, k_in, &ws) != SYN_OK) return false;
+        p.weight = k.weight;
+        p.dims[0] = n_out;
+        p.dims[1] = k_in;
+        p.workspace = round_up(ws, 64) + 256;
+        p.max_block = k.weight == SYN_Q4_K ? 256 : 32;
+        p.act_in = k.weight == SYN_Q4_K ? 3 : 2;
+        return true;
+    }
+    case Op::MoeGrouped: {
+        if (k.weight != SYN_Q4_K || k.n_schemes > 3 || s.dims.size() != 4) return false;
+        uint64_t ws = 0;
+        if (syn_moe_grouped_workspace_bytes(k.weight, s.dims[0], s.dims[1], s.dims[2], s.dims[3],
+                                            s.rows, &ws) != SYN_OK)
+            return false;
+        p.weight = k.weight;
+        for (int i = 0; i < 4; ++i) p.dims[i] = s.dims[i];
+        p.workspace = round_up(ws, 64) + 256;
+        p.max_block = 256;
+        p.act_in = 3;
+        return true;
+    }
+    case Op::MoeRoute: {
+        // dims [n_experts, top_k, hidden] (crates/kernels/src/op/kind.rs:242); the router is F32
+        if (!k.softmax || k.weight != -1 || s.dims.size() != 3) return false;
+        const uint32_t e = s.dims[0], top_k = s.dims[1], hidden = s.dims[2];
+        if (e == 0 || e > 256 || top_k == 0 || top_k > e || top_k > 32 || hidden == 0 ||
+            hidden % 32 || hidden > 8192)
+            return false;
+        for (int i = 0; i < 3; ++i) p.dims[i] = s.dims[i];
+        // the softmax rows, staged in the workspace (the op's outputs are ids and weights)
+        p.workspace = round_up(4ull * s.rows * e, 64) + 256;
+        return true;
+    }
+    case Op::MoeCombine: {
+        // dims [top_k, hidden]
+        if (k.weight != -1 || s.dims.size() != 2 || s.dims[0] == 0 || s.dims[0] > 64) return false;
+        p.dims[0] = s.dims[0];
+        p.dims[1] = s.dims[1];
+        p.workspace = 0;
+        return true;
+    }
+    default:
+        return false;
+    }
+}
+
+std::string caps_json(const Plan& p) {
+    // CapsWire (wire.rs:762-771) with NumericsWire (:677-686); kernel_hash and source_key are
+    // zero: uncertified, as the reference's own kernels until certification
+    std::string zeros = "[";
+    for (int i = 0; i < 32; ++i) zeros += i ? ",0" : "0";
+    zeros += "]";
+    const bool route = p.op == Op::MoeRoute, combine = p.op == Op::MoeCombine;
+    char num[256];
+    std::snprintf(num, sizeof num,
+                  "{\"accumulate\":%u,\"max_block\":%u,\"act_in\":%u,\"group\":0,\"out\":0,"
+                  "\"softmax_f32\":%s,\"state_f32\":false}",
+                  route || combine ? 0u : 1u, p.max_block, p.act_in, route ? "true" : "false");
+    return std::string("{\"workspace\":") + std::to_string(p.workspace) +
+           ",\"est\":null,\"layout\":0,\"capture_safe\":true,\"deterministic\":true,\"numerics\":" + num +
+           ",\"kernel_hash\":" + zeros + ",\"source_key\":" + zeros + "}";
+}
+
+const char* OPS_JSON =
+    "["
+    "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q4_K\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
+    "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q8_0\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
+    "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q4_0\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
+    "{\"op\":\"MoeGrouped\",\"schemes\":[{\"Ggml\":\"Q4_K\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
+    "{\"op\":{\"MoeRoute\":{\"norm\":\"Softmax\"}},\"schemes\":[{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
+    "{\"op\":\"MoeCombine\",\"schemes\":[{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0}"
+    "]";
+
+// ============================================================================================
+// Contexts
+// ============================================================================================
+
+struct Buf {
+    void* ptr;
+    uint64_t bytes;
+};
+
+struct Ctx {
+    int device = 0;
+    std::unordered_map<uint64_t, Buf> bufs;
+    std::unordered_map<uint64_t, hipStream_t> streams;
+    std::unordered_map<uint64_t, hipEvent_t> events;
+    std::unordered_map<uint64_t, hipGraphExec_t> graphs;
+    std::unordered_map<uint64_t, Plan> plans;
+    uint64_t next = 1;
+    uint64_t handle() { return next++; }
+};
+
+std::atomic<uint64_t> g_next_ctx{1};
+thread_local std::unordered_map<uint64_t, Ctx*> t_ctx;
+
+Ctx& ctx_of(uint64_t h) {
+    auto it = t_ctx.find(h);
+    if (it == t_ctx.end())
+        internal("context " + std::to_string(h) +
+                 " is not open on this thread: a context is used on the thread that opened it");
+    check_hip(hipSetDevice(it->second->device), "hipSetDevice");
+    return *it->second;
+}
+
+hipStream_t stream_of(Ctx& c, uint64_t s) {
+    auto it = c.streams.find(s);
+    if (it == c.streams.end()) internal("unknown stream " + std::to_string(s));
+    return it->second;
+}
+hipEvent_t event_of(Ctx& c, uint64_t e) {
+    auto it = c.events.find(e);
+    if (it == c.events.end()) internal("unknown event " + std::to_string(e));
+    return it->second;
+}
+// The device address of a slice, checked against its buffer.
+uint8_t* addr_of(Ctx& c, const SynSlice& s) {
+    auto it = c.bufs.find(s.buffer);
+    if (it == c.bufs.end()) internal("unknown buffer " + std::to_string(s.buffer));
+    if (s.offset > it->second.bytes || s.bytes > it->second.bytes - s.offset)
+        internal("a slice runs past its buffer");
+    return static_cast<uint8_t*>(it->second.ptr) + s.offset;
+}
+
+// A packed tensor argument: dtype, dims [d0, d1, d2, d3] with row-major element strides
+// (crates/kernels/src/op/args.rs:85-96), its slice holding the span.
+uint8_t* tensor(Ctx& c, const SynTensorArg& t, uint32_t dtype, uint32_t d0, uint32_t d1, uint32_t d2,
+                uint32_t elem, const char* what) {
+    const uint32_t want[4] = {d0, d1, d2, 1};
+    for (int i = 0; i < 4; ++i)
+        if (t.dims[i] != want[i])
+            internal(std::string(what) + ": dims [" + std::to_string(t.dims[0]) + "," +
+                     std::to_string(t.dims[1]) + "," + std::to_string(t.dims[2]) + "," +
+                     std::to_string(t.dims[3]) + "] are not the plan's");
+    if (t.dtype != dtype) internal(std::string(what) + ": dtype code " + std::to_string(t.dtype));
+    // packed: strides[3] = 1 and each stride the product of the extents inside it
+    if (t.strides[3] != 1 || t.strides[2] != 1 || t.strides[1] != d2 || t.strides[0] != d1 * d2)
+        internal(std::string(what) + " is not packed");
+    const uint64_t need = (uint64_t)d0 * d1 * d2 * elem;
+    if (t.buf.bytes < need) internal(std::string(what) + ": the slice is shorter than the tensor");
+    return addr_of(c, t.buf);
+}
+
+uint8_t* workspace_of(Ctx& c, const SynOpArgs& a, const Plan& p) {
+    if (p.workspace == 0) return nullptr;
+    if (!a.has_workspace || a.workspace.bytes < p.workspace)
+        fail(SYN_CLASS_INTERNAL, SYN_CODE_WORKSPACE_EXCEEDED, "the workspace is smaller than the op's caps");
+    uint8_t* w = addr_of(c, a.workspace);
+    return reinterpret_cast<uint8_t*>(round_up(reinterpret_cast<uintptr_t>(w), 256));
+}
+
+const SynBufferView& weight(const SynOpArgs& a, size_t i, uint64_t need, const char* what) {
+    if (i >= a.n_weights || !a.weights) internal(std::string(what) + ": missing weight view");
+    const SynBufferView& w = a.weights[i];
+    if (w.len < need) internal(std::string(what) + ": the weight view is shorter than the matrix");
+    return w;
+}
+
+void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
+    const uint32_t rows = p.rows;
+    switch (p.op) {
+    case Op::Gemv: {
+        const uint32_t n_out = p.dims[0], k_in = p.dims[1];
+        if (a.n_inputs != 1 || a.n_outputs != 1 || a.n_weights != 1 || a.n_statics != 0)
+            internal("Gemv binds one input, one output, one weight and no constants");
+        const uint8_t* x = tensor(c, a.inputs[0], 0, rows, k_in, 1, 4, "Gemv x");
+        uint8_t* y = tensor(c, a.outputs[0], 0, rows, n_out, 1, 4, "Gemv y");
+        const int be = p.weight == SYN_Q4_K ? 256 : 32, bb = p.weight == SYN_Q4_K ? 144 : p.weight == SYN_Q8_0 ? 34 : 18;
+        const uint64_t wbytes = (uint64_t)k_in / be * bb * n_out;
+        const SynBufferView& w = weight(a, 0, wbytes, "Gemv");
+        uint8_t* ws = workspace_of(c, a, p);
+        check_syn(syn_gemv(p.weight, (const void*)w.addr, wbytes, n_out, k_in, (const float*)x, rows,
+                           (float*)y, ws, p.workspace - 256, st),
+                  "Gemv");
+        return;
+    }
+    case Op::MoeGrouped: {
+        const uint32_t e = p.dims[0], top_k = p.dims[1], hidden = p.dims[2], inter = p.dims[3];
+        if (a.n_inputs < 2 || a.n_inputs > 3 || a.n_outputs != 1 || a.n_weights != 3)
+            internal("MoeGrouped binds x, ids (and an optional site), one output and three weights");
+        if (a.n_inputs == 3) unsupported("MoeGrouped: the site input (per-expert residency) is not served");
+        const uint8_t* x = tensor(c, a.inputs[0], 0, rows, hidden, 1, 4, "MoeGrouped x");
+        const uint8_t* ids = tensor(c, a.inputs[1], 7, rows, top_k, 1, 4, "MoeGrouped ids");
+        uint8_t* out = tensor(c, a.outputs[0], 0, rows, top_k, hidden, 4, "MoeGrouped out");
+        const uint64_t mat = (uint64_t)inter * (hidden / 256) * 144 * e;
+        const SynBufferView& g = weight(a, 0, mat, "MoeGrouped gate");
+        const SynBufferView& u = weight(a, 1, mat, "MoeGrouped up");
+        const SynBufferView& d = weight(a, 2, mat, "MoeGrouped down");
+        uint8_t* ws = workspace_of(c, a, p);
+        check_syn(syn_moe_grouped(p.weight, (const void*)g.addr, (const void*)u.addr, (const void*)d.addr,
+                                  mat, e, top_k, hidden, inter, (const float*)x, (const int32_t*)ids, rows,
+                                  (float*)out, ws, p.workspace - 256, nullptr, st),
+                  "MoeGrouped");
+        return;
+    }
+    case Op::MoeRoute: {
+        const uint32_t e = p.dims[0], top_k = p.dims[1], hidden = p.dims[2];
+        if (a.n_inputs != 1 || a.n_outputs != 2 || a.n_weights != 1 || a.n_statics > 1)
+            internal("MoeRoute binds x, two outputs (ids, weights), the router and at most one constant");
+        // the node's `renormalize` attribute as an I32 or U32 constant; true without one (the
+        // Qwen3-MoE norm_topk_prob)
+        int renorm = 1;
+        if (a.n_statics == 1) {
+            if (a.statics[0].tag != 1 && a.statics[0].tag != 2) internal("MoeRoute: renormalize must be an integer constant");
+            renorm = a.statics[0].bits != 0;
+        }
+        const uint8_t* x = tensor(c, a.inputs[0], 0, rows, hidden, 1, 4, "MoeRoute x");
+        uint8_t* ids = tensor(c, a.outputs[0], 7, rows, top_k, 1, 4, "MoeRoute ids");
+        uint8_t* w = tensor(c, a.outputs[1], 0, rows, top_k, 1, 4, "MoeRoute weights");
+        const SynBufferView& r = weight(a, 0, 4ull * e * hidden, "MoeRoute router");
+        uint8_t* ws = workspace_of(c, a, p);
+        check_syn(syn_moe_route((const float*)r.addr, (const float*)x, rows, hidden, e, top_k, renorm,
+                                (int32_t*)ids, (float*)w, (float*)ws, st),
+                  "MoeRoute");
+        return;
+    }
+    case Op::MoeCombine: {
+        const uint32_t top_k = p.dims[0], hidden = p.dims[1];
+        if (a.n_inputs != 3 || a.n_outputs != 1)
+            internal("MoeCombine binds the per-slot outputs, their weights and ids, and one output");
+        const uint8_t* per = tensor(c, a.inputs[0], 0, rows, top_k, hidden, 4, "MoeCombine outputs");
+        const uint8_t* w = tensor(c, a.inputs[1], 0, rows, top_k, 1, 4, "MoeCombine weights");
+        const uint8_t* ids = tensor(c, a.inputs[2], 7, rows, top_k, 1, 4, "MoeCombine ids");
+        uint8_t* y = tensor(c, a.outputs[0], 0, rows, hidden, 1, 4, "MoeCombine y");
+        check_syn(syn_moe_combine((const float*)per, (const int32_t*)ids, (const float*)w, rows, top_k,
+                                  hidden, (float*)y, st),
+                  "MoeCombine");
+        return;
+    }
+    default:
+        internal("a prepared op of no kind");
+    }
+}
+
+// ============================================================================================
+// The table's entries
+// ============================================================================================
+
+SynStatus e_build(void*, SynOutBuf* out) {
+    return call("build", false, [&] {
+        int rt = 0;
+        (void)hipRuntimeGetVersion(&rt);
+        put(out, "{\"version\":1,\"module\":null,\"toolchain\":[[\"hip\",\"" + std::to_string(rt) +
+                     "\"],[\"target\",\"gfx950\"]],\"driver\":null}");
+    });
+}
+
+SynStatus e_enumerate(void*, SynOutBuf* out) {
+    return call("enumerate", false, [&] {
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+        std::string s = "[";
+        for (int i = 0; i < n; ++i) {
+            hipDeviceProp_t prop{};
+            check_hip(hipGetDeviceProperties(&prop, i), "hipGetDeviceProperties");
+            size_t free_b = 0, total_b = 0;
+            check_hip(hipSetDevice(i), "hipSetDevice");
+            check_hip(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+            char rec[768];
+            std::snprintf(rec, sizeof rec,
+                          "%s{\"local\":%d,\"uuid\":null,\"pci\":{\"domain\":%d,\"bus\":%d,\"device\":%d,\"function\":0},"
+                          "\"kind\":\"DiscreteGpu\",\"name\":\"%s\",\"class\":{\"Hip\":{\"gfx\":%d}},\"features\":0,"
+                          "\"memory\":{\"total\":%zu,\"free\":%zu,\"budget\":null,\"host_visible_device_local\":null,"
+                          "\"max_alloc\":%zu,\"unified\":false},\"numa\":null}",
+                          i ? "," : "", i, prop.pciDomainID, prop.pciBusID, prop.pciDeviceID, "AMD Instinct MI355X",
+                          0x950, total_b, free_b, total_b);
+            s += rec;
+        }
+        put(out, s + "]");
+    });
+}
+
+SynStatus e_open(void*, const SynDeviceId* dev, const SynOpenOptions*, uint64_t* ctx) {
+    return call("open", false, [&] {
+        if (!dev || !ctx) internal("open: null argument");
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n == 0) fail(SYN_CLASS_DEVICE, 0, "open: no HIP device");
+        if ((int)dev->ordinal >= n) fail(SYN_CLASS_INVALID_REQUEST, 0, "open: no device " + std::to_string(dev->ordinal));
+        check_hip(hipSetDevice((int)dev->ordinal), "hipSetDevice");
+        Ctx* c = new Ctx();
+        c->device = (int)dev->ordinal;
+        const uint64_t h = g_next_ctx.fetch_add(1);
+        t_ctx[h] = c;
+        *ctx = h;
+    });
+}
+
+SynStatus e_close_ctx(void*, uint64_t ctx) {
+    return call("close_ctx", true, [&] {
+        auto it = t_ctx.find(ctx);
+        if (it == t_ctx.end())
+            internal("context " + std::to_string(ctx) + " is not open on this thread, so it was not closed");
+        Ctx* c = it->second;
+        (void)hipSetDevice(c->device);
+        for (auto& g : c->graphs) (void)hipGraphExecDestroy(g.second);
+        for (auto& e : c->events) (void)hipEventDestroy(e.second);
+        for (auto& s : c->streams) (void)hipStreamDestroy(s.second);
+        for (auto& b : c->bufs) (void)hipFree(b.second.ptr);
+        delete c;
+        t_ctx.erase(it);
+    });
+}
+
+SynStatus e_memory_info(void*, uint64_t ctx, SynMemoryInfo* out) {
+    return call("memory_info", false, [&] {
+        ctx_of(ctx);
+        size_t free_b = 0, total_b = 0;
+        check_hip(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+        SynMemoryInfo m{};
+        m.total = total_b;
+        m.free = free_b;
+        m.max_alloc = total_b;
+        *out = m;
+    });
+}
+
+SynStatus e_ops(void*, SynOutBuf* out) {
+    return call("ops", false, [&] { put(out, OPS_JSON); });
+}
+
+SynStatus e_query(void*, uint64_t ctx, const uint8_t* op, size_t op_len, const uint8_t* shape,
+                  size_t shape_len, SynOutBuf* out) {
+    return call("query", false, [&] {
+        ctx_of(ctx);
+        const Key k = parse_key(op, op_len);
+        const Shape s = parse_shape(shape, shape_len);
+        Plan p;
+        put(out, plan_of(k, s, p) ? caps_json(p) : std::string());
+    });
+}
+
+SynStatus e_alloc(void*, uint64_t ctx, const SynAllocRequest* req, SynBuffer* out) {
+    return call("alloc", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        if (!req || !out) internal("alloc: null argument");
+        if (req->kind != 0 || req->reserve_only) unsupported("alloc: only plain device memory is served");
+        if (req->align > 256 && (req->align & (req->align - 1))) internal("alloc: alignment is not a power of two");
+        void* p = nullptr;
+        if (hipMalloc(&p, req->bytes ? req->bytes : 1) != hipSuccess)
+            fail(SYN_CLASS_CAPACITY, SYN_CODE_ALLOC_FAILED, "alloc: " + std::to_string(req->bytes) + " bytes");
+        const uint64_t h = c.handle();
+        c.bufs[h] = Buf{p, req->bytes};
+        SynBuffer b{};
+        b.addr = reinterpret_cast<uint64_t>(p);
+        b.bytes = req->bytes;
+        b.handle = h;
+        *out = b;
+    });
+}
+
+SynStatus e_free(void*, uint64_t ctx, const SynBuffer* buf) {
+    return call("free", true, [&] {
+        Ctx& c = ctx_of(ctx);
+        if (!buf) internal("free: null buffer");
+        auto it = c.bufs.find(buf->handle);
+        if (it == c.bufs.end()) internal("free: unknown buffer " + std::to_string(buf->handle));
+        check_hip(hipFree(it->second.ptr), "hipFree");
+        c.bufs.erase(it);
+    });
+}
+
+#define SYN_UNSERVED(name, ...)                                                   \
+    SynStatus e_##name(__VA_ARGS__) {                                             \
+        return call(#name, false, [&] { unsupported("`" #name "` is not served by the hip provider"); }); \
+    }
+SYN_UNSERVED(map_segment, void*, uint64_t, const SynBuffer*, uint64_t, uint64_t, SynSegment*)
+SYN_UNSERVED(unmap_segment, void*, uint64_t, const SynSegment*)
+SYN_UNSERVED(register_host, void*, uint64_t, SynHostRegion, SynRegistration*)
+SYN_UNSERVED(host_registrar, void*, uint64_t, SynRegistrarVtbl*)
+SYN_UNSERVED(import, void*, uint64_t, SynHostRegion, SynBuffer*)
+SYN_UNSERVED(signal_host, void*, uint64_t, uint64_t, uint32_t, uint32_t)
+SYN_UNSERVED(wait_host, void*, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t)
+SYN_UNSERVED(arm_wake, void*, uint64_t, uint64_t, uint32_t, uint64_t)
+#undef SYN_UNSERVED
+
+SynStatus e_set_resident(void*, uint64_t ctx, const SynBuffer*, size_t, uint32_t) {
+    // device memory is always resident
+    return call("set_resident", false, [&] { ctx_of(ctx); });
+}
+
+// Weights stay in their GGUF layout (LayoutVersion SOURCE): nothing to repack.
+SynStatus e_repack(void*, const uint8_t*, size_t, const uint8_t*, size_t, uint8_t*, size_t,
+                   uint32_t* present, uint32_t* layout) {
+    return call("repack", false, [&] {
+        if (present) *present = 0;
+        if (layout) *layout = 0;
+    });
+}
+SynStatus e_repacked_len(void*, const uint8_t*, size_t, uint64_t, uint32_t* present, uint64_t* out) {
+    return call("repacked_len", false, [&] {
+        if (present) *present = 0;
+        if (out) *out = 0;
+    });
+}
+
+SynStatus e_stream(void*, uint64_t ctx, uint32_t prio, uint64_t* out) {
+    return call("stream", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        if (prio > 4) internal("stream: unknown priority code " + std::to_string(prio));
+        // every stream at the default priority: the priority code only names the stream's role
+        hipStream_t s = nullptr;
+        check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+        const uint64_t h = c.handle();
+        c.streams[h] = s;
+        *out = h;
+    });
+}
+
+SynStatus e_event(void*, uint64_t ctx, uint64_t* out) {
+    return call("event", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        hipEvent_t e = nullptr;
+        check_hip(hipEventCreate(&e), "hipEventCreate");
+        const uint64_t h = c.handle();
+        c.events[h] = e;
+        *out = h;
+    });
+}
+
+SynStatus e_record(void*, uint64_t ctx, uint64_t s, uint64_t e) {
+    return call("record", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        check_hip(hipEventRecord(event_of(c, e), stream_of(c, s)), "hipEventRecord");
+    });
+}
+
+SynStatus e_wait(void*, uint64_t ctx, uint64_t s, uint64_t e) {
+    return call("wait", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        check_hip(hipStreamWaitEvent(stream_of(c, s), event_of(c, e), 0), "hipStreamWaitEvent");
+    });
+}
+
+SynStatus e_poll(void*, uint64_t ctx, uint64_t e, uint32_t* done) {
+    return call("poll", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        const hipError_t r = hipEventQuery(event_of(c, e));
+        if (r == hipSuccess) *done = 1;
+        else if (r == hipErrorNotReady) *done = 0;
+        else check_hip(r, "hipEventQuery");
+    });
+}
+
+SynStatus e_elapsed(void*, uint64_t ctx, uint64_t start, uint64_t end, uint32_t* present, uint64_t* nanos) {
+    return call("elapsed", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        float ms = 0.0f;
+        const hipError_t r = hipEventElapsedTime(&ms, event_of(c, start), event_of(c, end));
+        if (r == hipSuccess) {
+            *present = 1;
+            *nanos = (uint64_t)((double)ms * 1e6);
+        } else {
+            *present = 0;
+            *nanos = 0;
+        }
+    });
+}
+
+SynStatus e_synchronize(void*, uint64_t ctx, uint64_t s) {
+    return call("synchronize", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        check_hip(hipStreamSynchronize(stream_of(c, s)), "hipStreamSynchronize");
+    });
+}
+
+void copy_one(Ctx& c, hipStream_t st, const SynSlice& src, const SynSlice& dst) {
+    if (src.bytes != dst.bytes) internal("copy: the slices differ in length");
+    check_hip(hipMemcpyAsync(addr_of(c, dst), addr_of(c, src), src.bytes, hipMemcpyDeviceToDevice, st),
+              "hipMemcpyAsync");
+}
+
+SynStatus e_copy(void*, uint64_t ctx, uint64_t s, const SynSlice* src, const SynSlice* dst) {
+    return call("copy", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        copy_one(c, stream_of(c, s), *src, *dst);
+    });
+}
+
+SynStatus e_copy_batch(void*, uint64_t ctx, uint64_t s, const SynSlicePair* pairs, size_t n) {
+    return call("copy_batch", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        hipStream_t st = stream_of(c, s);
+        for (size_t i = 0; i < n; ++i) copy_one(c, st, pairs[i].src, pairs[i].dst);
+    });
+}
+
+SynStatus e_prepare(void*, uint64_t ctx, const uint8_t* op, size_t op_len, const uint8_t* shape,
+                    size_t shape_len, SynPreparedOp* out) {
+    return call("prepare", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        const Key k = parse_key(op, op_len);
+        const Shape s = parse_shape(shape, shape_len);
+        Plan p;
+        if (!plan_of(k, s, p)) unsupported("prepare: an op or shape the hip provider does not serve");
+        const uint64_t h = c.handle();
+        c.plans[h] = p;
+        SynPreparedOp r;
+        r.workspace = p.workspace;
+        r.handle = h;
+        *out = r;
+    });
+}
+
+SynStatus e_launch(void*, uint64_t ctx, uint64_t s, const SynPreparedOp* op, const SynOpArgs* args) {
+    return call("launch", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        if (!op || !args) internal("launch: null argument");
+        auto it = c.plans.find(op->handle);
+        if (it == c.plans.end()) internal("launch: unknown prepared op " + std::to_string(op->handle));
+        launch_op(c, stream_of(c, s), it->second, *args);
+    });
+}
+
+SynStatus e_begin_capture(void*, uint64_t ctx, uint64_t s) {
+    return call("begin_capture", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        check_hip(hipStreamBeginCapture(stream_of(c, s), hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    });
+}
+
+SynStatus e_end_capture(void*, uint64_t ctx, uint64_t s, uint64_t* out) {
+    return call("end_capture", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        hipGraph_t g = nullptr;
+        check_hip(hipStreamEndCapture(stream_of(c, s), &g), "hipStreamEndCapture");
+        hipGraphExec_t ex = nullptr;
+        const hipError_t r = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        check_hip(r, "hipGraphInstantiate");
+        const uint64_t h = c.handle();
+        c.graphs[h] = ex;
+        *out = h;
+    });
+}
+
+SynStatus e_replay(void*, uint64_t ctx, uint64_t s, uint64_t g) {
+    return call("replay", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        auto it = c.graphs.find(g);
+        if (it == c.graphs.end()) internal("replay: unknown graph " + std::to_string(g));
+        check_hip(hipGraphLaunch(it->second, stream_of(c, s)), "hipGraphLaunch");
+    });
+}
+
+SynStatus e_health(void*, uint64_t ctx, SynHealth* out) {
+    return call("health", true, [&] {
+        (void)ctx;
+        SynHealth h{};
+        const uint16_t sticky = g_sticky.load(std::memory_order_acquire);
+        if (sticky) {  // Sticky, in the Kernels domain, with the code that made it so
+            h.kind = 3;
+            h.domain = SYN_DOMAIN_KERNELS;
+            h.detail = sticky;
+        }
+        *out = h;
+    });
+}
+
+SynStatus e_last_error(void*, uint64_t, uint8_t* buf, size_t cap, size_t* len) {
+    // never refused: it reports why the last call failed
+    const std::string& m = t_message;
+    if (len) *len = m.size();
+    if (buf) std::memcpy(buf, m.data(), m.size() < cap ? m.size() : cap);
+    return OK;
+}
+
+SynStatus e_shutdown() { return OK; }
+
+SynHeader header(uint32_t size) {
+    SynHeader h{};
+    std::memcpy(h.magic, SYN_PROVIDER_MAGIC, 8);
+    h.abi_major = SYN_ABI_MAJOR;
+    h.abi_minor = SYN_ABI_MINOR;
+    // build id: zero, so the core accepts the module under kernels.dev_modules only
+    h.struct_size = size;
+    return h;
+}
+
+SynProviderVtbl make_vtbl() {
+    SynProviderVtbl v{};
+    v.struct_size = sizeof(SynProviderVtbl);
+    v.id = "hip";
+    v.backend = SYN_BACKEND_HIP;
+    v.domain = SYN_MEMDOMAIN_HIP;
+    v.build = e_build;
+    v.enumerate = e_enumerate;
+    v.open = e_open;
+    v.close_ctx = e_close_ctx;
+    v.memory_info = e_memory_info;
+    v.ops = e_ops;
+    v.query = e_query;
+    v.alloc = e_alloc;
+    v.free = e_free;
+    v.map_segment = e_map_segment;
+    v.unmap_segment = e_unmap_segment;
+    v.register_host = e_register_host;
+    v.host_registrar = e_host_registrar;
+    v.import = e_import;
+    v.set_resident = e_set_resident;
+    v.repack = e_repack;
+    v.repacked_len = e_repacked_len;
+    v.stream = e_stream;
+    v.event = e_event;
+    v.record = e_record;
+    v.wait = e_wait;
+    v.signal_host = e_signal_host;
+    v.wait_host = e_wait_host;
+    v.arm_wake = e_arm_wake;
+    v.poll = e_poll;
+    v.elapsed = e_elapsed;
+    v.synchronize = e_synchronize;
+    v.copy = e_copy;
+    v.copy_batch = e_copy_batch;
+    v.prepare = e_prepare;
+    v.launch = e_launch;
+    v.begin_capture = e_begin_capture;
+    v.end_capture = e_end_capture;
+    v.replay = e_replay;
+    v.health = e_health;
+    v.last_error = e_last_error;
+    v.slf = nullptr;
+    v.health_size = sizeof(SynHealth);
+    return v;
+}
+
+const SynProviderVtbl g_vtbl = make_vtbl();
+const SynModule g_module = {header(sizeof(SynModule)), 1, &g_vtbl, e_shutdown};
+
+}  // namespace
+
+SYN_PROVIDER_EXPORT const SynModule* syntropy_provider_entry_v1(const SynHostApi* host) {
+    // the module checks the host's magic, major and size (RFC-0040 §10.4; module.rs:26-40)
+    if (!host || std::memcmp(host->h.magic, SYN_PROVIDER_MAGIC, 8) != 0 ||
+        host->h.abi_major != SYN_ABI_MAJOR || host->h.struct_size < sizeof(SynHostApi))
+        return nullptr;
+    return &g_module;
+}

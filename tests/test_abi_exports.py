@@ -11,14 +11,19 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB = os.path.join(ROOT, "syntropy_amd", "libsyntropy_hip.so")
+PROVIDER_LIB = os.path.join(ROOT, "syntropy_amd", "libsyntropy_provider.so")
+# which library exports what each header declares
+HEADER_LIB = {"syntropy_hip.h": LIB, "syntropy_provider.h": PROVIDER_LIB}
 
 
-def declared_functions():
+def declared_functions(header=None):
     names = []
     for h in sorted(glob.glob(os.path.join(ROOT, "include", "*.h"))):
+        if header is not None and os.path.basename(h) != header:
+            continue
         text = open(h).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\**\s*\**\s*([a-z][a-z0-9_]*)\s*\(",
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*(?:\s+\**|\s*\*+)\s*\**\s*([a-z][a-z0-9_]*)\s*\(",
                              text, flags=re.M):
             names.append(m.group(1))
     return sorted(set(names))
@@ -29,12 +34,21 @@ def test_headers_declare_functions():
     assert "syn_gemv" in names and "syn_last_error" in names
 
 
-def test_library_exports_every_declared_function():
-    if not os.path.exists(LIB):
-        pytest.fail(f"{LIB} is not built: run python -m syntropy_amd.build")
+def test_every_header_has_its_library():
+    headers = sorted(os.path.basename(h) for h in glob.glob(os.path.join(ROOT, "include", "*.h")))
+    assert headers == sorted(HEADER_LIB)
+
+
+@pytest.mark.parametrize("header", sorted(HEADER_LIB))
+def test_library_exports_every_declared_function(header):
+    path = HEADER_LIB[header]
+    if not os.path.exists(path):
+        pytest.fail(f"{path} is not built: run python -m syntropy_amd.build")
     import torch  # noqa: F401  one HIP runtime in the process
-    lib = ctypes.CDLL(LIB)
-    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    lib = ctypes.CDLL(path)
+    names = declared_functions(header)
+    assert names
+    missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
 
 

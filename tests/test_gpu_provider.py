@@ -1,0 +1,253 @@
+"""GPU parity through the provider-library boundary: the core's calling sequence (open, stream,
+alloc, query, prepare, launch, synchronize) on the hip provider, each op's outputs bit-exact
+against the oracle; stream capture and replay; the workspace and argument checks.
+
+The sequence is kernels_loader::ModuleProvider's (crates/kernels-loader/src/provider.rs) and the
+argument binding is the executor's (crates/kernels/src/op/args.rs:85-96: packed tensors, weight
+views, the workspace slice)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce, assert_same, dev, require_gpu
+from oracle import oracle as o
+from refgen import GemvRng, MoeRng, gemv_activations, gemv_weights, moe_matrix
+
+pytestmark = pytest.mark.gpu
+
+H2D, D2H = 1, 2
+
+
+class Ctx:
+    """One open context and a stream; host data moves in and out with hipMemcpy."""
+
+    def __init__(self):
+        require_gpu()
+        from syntropy_amd import provider as P
+        self.P = P
+        self.pr = P.Provider()
+        self.hip = C.CDLL("libamdhip64.so.7")  # the runtime torch and the provider already share
+        self.hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        self.hip.hipMemcpy.restype = C.c_int
+        self.hip.hipDeviceSynchronize.restype = C.c_int
+        self.ctx = self.pr.open(0)
+        self.s = self.pr.stream(self.ctx)
+        self.bufs = []
+
+    def upload(self, addr: int, a):
+        """A host-to-device copy complete before the provider's stream runs again."""
+        assert self.hip.hipMemcpy(addr, a.ctypes.data, a.nbytes, H2D) == 0
+        assert self.hip.hipDeviceSynchronize() == 0
+
+    def put(self, a) -> "object":
+        a = np.ascontiguousarray(a)
+        b = self.pr.alloc(self.ctx, max(a.nbytes, 1))
+        if a.nbytes:
+            self.upload(b.addr, a)
+        self.bufs.append(b)
+        return b
+
+    def empty(self, nbytes: int, fill: int = 0x7F):
+        return self.put(np.full(nbytes, fill, np.uint8))
+
+    def get(self, b, dtype, shape):
+        self.pr.synchronize(self.ctx, self.s)
+        out = np.empty(shape, dtype)
+        assert self.hip.hipMemcpy(out.ctypes.data, b.addr, out.nbytes, D2H) == 0
+        return out
+
+    def workspace(self, op):
+        if op.workspace == 0:
+            return None
+        ws = self.empty(op.workspace, 0)
+        return self.P.Slice(ws.handle, 0, op.workspace)
+
+    def close(self):
+        self.pr.close(self.ctx)
+
+
+@pytest.fixture(scope="module")
+def cx():
+    c = Ctx()
+    yield c
+    c.close()
+
+
+def gemv_key(ty):
+    name = {o.Q4_K: "Q4_K", o.Q8_0: "Q8_0", o.Q4_0: "Q4_0"}[ty]
+    return {"op": "Gemv", "schemes": [{"Ggml": name}, {"Plain": "F32"}, {"Plain": "F32"}], "layout": 0,
+            "variant": 0}
+
+
+def shape(rows, *dims, cls="Decode"):
+    return {"class": cls, "rows": rows, "dims": list(dims)}
+
+
+@pytest.mark.parametrize("ty,rows,n_out,k", [(o.Q4_K, 1, 4096, 4096), (o.Q4_K, 7, 1536, 2048),
+                                             (o.Q8_0, 3, 1000, 4096), (o.Q4_0, 2, 513, 1024)])
+def test_gemv_through_the_provider(cx, ty, rows, n_out, k):
+    P, pr = cx.P, cx.pr
+    rng = GemvRng(ty * 1000 + rows)
+    w = gemv_weights(rng, ty, n_out, k, o.f16_bits, o.round_bf16)
+    x = gemv_activations(rng, rows, k)
+    announce(f"provider gemv ty={ty} rows={rows} n_out={n_out} k={k}")
+    caps = pr.query(cx.ctx, gemv_key(ty), shape(rows, n_out, k))
+    assert caps is not None and caps["deterministic"] and caps["capture_safe"]
+    op = pr.prepare(cx.ctx, gemv_key(ty), shape(rows, n_out, k))
+    assert op.workspace == caps["workspace"]
+    wd = dev(w)
+    xb, yb = cx.put(x.astype(np.float32)), cx.empty(4 * rows * n_out)
+    args = P.op_args([P.packed(xb, P.DT_F32, [rows, k])], [P.packed(yb, P.DT_F32, [rows, n_out])],
+                     [P.view(wd.data_ptr(), w.nbytes)], cx.workspace(op))
+    pr.launch(cx.ctx, cx.s, op, args)
+    got = cx.get(yb, np.float32, (rows, n_out))
+    assert_same(got, o.gemv(ty, w, n_out, k, x, rows, threads=8), "provider gemv")
+
+
+def test_query_answers_none_for_unserved_shapes(cx):
+    pr = cx.pr
+    assert pr.query(cx.ctx, gemv_key(o.Q4_K), shape(1, 64, 100)) is None  # k not whole super-blocks
+    key = dict(gemv_key(o.Q4_K), schemes=[{"Ggml": "Q6_K"}, {"Plain": "F32"}, {"Plain": "F32"}])
+    assert pr.query(cx.ctx, key, shape(1, 64, 256)) is None
+    assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=3), shape(1, 64, 256)) is None
+    assert pr.query(cx.ctx, {"op": "Attention", "schemes": [], "layout": 0, "variant": 0},
+                    shape(1, 64, 256)) is None
+    with pytest.raises(cx.P.ProviderError) as e:
+        pr.prepare(cx.ctx, gemv_key(o.Q4_K), shape(1, 64, 100))
+    assert (e.value.cls, e.value.code) == (2, 1)
+
+
+def test_launch_checks_workspace_and_arguments(cx):
+    P, pr = cx.P, cx.pr
+    rows, n_out, k = 2, 256, 512
+    op = pr.prepare(cx.ctx, gemv_key(o.Q4_K), shape(rows, n_out, k))
+    w = torch.zeros(n_out * k // 256 * 144, dtype=torch.uint8, device="cuda")
+    xb, yb = cx.empty(4 * rows * k, 0), cx.empty(4 * rows * n_out)
+    small = cx.empty(64, 0)
+    announce("provider launch refusals")
+    x_arg, y_arg = P.packed(xb, P.DT_F32, [rows, k]), P.packed(yb, P.DT_F32, [rows, n_out])
+    wv = [P.view(w.data_ptr(), w.numel())]
+    with pytest.raises(P.ProviderError) as e:
+        pr.launch(cx.ctx, cx.s, op, P.op_args([x_arg], [y_arg], wv, P.Slice(small.handle, 0, 64)))
+    assert (e.value.cls, e.value.code) == (13, 14)
+    ws = cx.workspace(op)
+    with pytest.raises(P.ProviderError) as e:  # dims not the plan's
+        pr.launch(cx.ctx, cx.s, op, P.op_args([P.packed(xb, P.DT_F32, [rows, k // 2])], [y_arg], wv, ws))
+    assert "dims" in e.value.message
+    with pytest.raises(P.ProviderError) as e:  # a short weight view
+        pr.launch(cx.ctx, cx.s, op, P.op_args([x_arg], [y_arg], [P.view(w.data_ptr(), 100)], ws))
+    assert "weight view" in e.value.message
+    # nothing was written by the refused launches
+    assert (cx.get(yb, np.uint8, 4 * rows * n_out) == 0x7F).all()
+
+
+def test_moe_layer_through_the_provider(cx):
+    """Route, grouped experts, combine: three prepared ops on one stream, every output bit-exact."""
+    P, pr = cx.P, cx.pr
+    E, top_k, hidden, inter, rows = 16, 4, 512, 256, 37
+    rng = MoeRng(77)
+    gate = moe_matrix(rng, o.Q4_K, E * inter, hidden, o.f16_bits)
+    up = moe_matrix(rng, o.Q4_K, E * inter, hidden, o.f16_bits)
+    down = moe_matrix(rng, o.Q4_K, E * hidden, inter, o.f16_bits)
+    router = o.normal(0x51A30004, 0.02, E * hidden).reshape(E, hidden)
+    x = o.normal(0x51A20004, 1.0, rows * hidden).reshape(rows, hidden)
+    announce(f"provider moe E={E} k={top_k} hidden={hidden} inter={inter} rows={rows}")
+
+    route_key = {"op": {"MoeRoute": {"norm": "Softmax"}}, "schemes": [{"Plain": "F32"}, {"Plain": "F32"}],
+                 "layout": 0, "variant": 0}
+    grouped_key = {"op": "MoeGrouped", "schemes": [{"Ggml": "Q4_K"}, {"Plain": "F32"}, {"Plain": "F32"}],
+                   "layout": 0, "variant": 0}
+    combine_key = {"op": "MoeCombine", "schemes": [{"Plain": "F32"}], "layout": 0, "variant": 0}
+    caps = pr.query(cx.ctx, route_key, shape(rows, E, top_k, hidden))
+    assert caps["numerics"]["softmax_f32"]
+    r_op = pr.prepare(cx.ctx, route_key, shape(rows, E, top_k, hidden))
+    g_op = pr.prepare(cx.ctx, grouped_key, shape(rows, E, top_k, hidden, inter))
+    c_op = pr.prepare(cx.ctx, combine_key, shape(rows, top_k, hidden))
+
+    rd, gd, ud, dd = dev(router), dev(gate), dev(up), dev(down)
+    xb = cx.put(x)
+    ids_b, w_b = cx.empty(4 * rows * top_k), cx.empty(4 * rows * top_k)
+    per_b, y_b = cx.empty(4 * rows * top_k * hidden), cx.empty(4 * rows * hidden)
+    x_arg = P.packed(xb, P.DT_F32, [rows, hidden])
+    ids_arg = P.packed(ids_b, P.DT_I32, [rows, top_k])
+    w_arg = P.packed(w_b, P.DT_F32, [rows, top_k])
+    per_arg = P.packed(per_b, P.DT_F32, [rows, top_k, hidden])
+    y_arg = P.packed(y_b, P.DT_F32, [rows, hidden])
+    pr.launch(cx.ctx, cx.s, r_op, P.op_args([x_arg], [ids_arg, w_arg], [P.view(rd.data_ptr(), router.nbytes)],
+                                            cx.workspace(r_op), [P.Scalar(1, 1)]))
+    views = [P.view(t.data_ptr(), t.numel()) for t in (gd, ud, dd)]
+    pr.launch(cx.ctx, cx.s, g_op, P.op_args([x_arg, ids_arg], [per_arg], views, cx.workspace(g_op)))
+    pr.launch(cx.ctx, cx.s, c_op, P.op_args([per_arg, w_arg, ids_arg], [y_arg], []))
+
+    wids, ww, _ = o.moe_route(router, x, E, top_k, True)
+    assert (cx.get(ids_b, np.int32, (rows, top_k)) == wids).all()
+    assert_same(cx.get(w_b, np.float32, (rows, top_k)), ww, "route weights")
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, E, top_k, hidden, inter, gate, up, down, x, wids, threads=8)
+    assert_same(cx.get(per_b, np.float32, (rows, top_k, hidden)), want, "grouped")
+    assert_same(cx.get(y_b, np.float32, (rows, hidden)), o.moe_combine(want, wids, ww), "combined")
+
+
+def test_route_without_renormalization(cx):
+    P, pr = cx.P, cx.pr
+    E, top_k, hidden, rows = 8, 2, 256, 5
+    router = o.normal(11, 0.02, E * hidden).reshape(E, hidden)
+    x = o.normal(12, 1.0, rows * hidden).reshape(rows, hidden)
+    key = {"op": {"MoeRoute": {"norm": "Softmax"}}, "schemes": [{"Plain": "F32"}, {"Plain": "F32"}],
+           "layout": 0, "variant": 0}
+    announce("provider route renormalize=0")
+    op = pr.prepare(cx.ctx, key, shape(rows, E, top_k, hidden))
+    rd = dev(router)
+    xb, ids_b, w_b = cx.put(x), cx.empty(4 * rows * top_k), cx.empty(4 * rows * top_k)
+    pr.launch(cx.ctx, cx.s, op, P.op_args([P.packed(xb, P.DT_F32, [rows, hidden])],
+                                          [P.packed(ids_b, P.DT_I32, [rows, top_k]),
+                                           P.packed(w_b, P.DT_F32, [rows, top_k])],
+                                          [P.view(rd.data_ptr(), router.nbytes)], cx.workspace(op),
+                                          [P.Scalar(2, 0)]))
+    wids, ww, _ = o.moe_route(router, x, E, top_k, False)
+    assert (cx.get(ids_b, np.int32, (rows, top_k)) == wids).all()
+    assert_same(cx.get(w_b, np.float32, (rows, top_k)), ww)
+
+
+def test_capture_and_replay(cx):
+    """A captured Q4_K GEMV replayed three times over new inputs written between replays; every
+    replay equals the oracle."""
+    P, pr = cx.P, cx.pr
+    rows, n_out, k = 4, 768, 2048
+    rng = GemvRng(4242)
+    w = gemv_weights(rng, o.Q4_K, n_out, k, o.f16_bits, o.round_bf16)
+    op = pr.prepare(cx.ctx, gemv_key(o.Q4_K), shape(rows, n_out, k))
+    wd = dev(w)
+    xb, yb = cx.empty(4 * rows * k, 0), cx.empty(4 * rows * n_out)
+    args = P.op_args([P.packed(xb, P.DT_F32, [rows, k])], [P.packed(yb, P.DT_F32, [rows, n_out])],
+                     [P.view(wd.data_ptr(), w.nbytes)], cx.workspace(op))
+    announce("provider capture/replay")
+    pr.begin_capture(cx.ctx, cx.s)
+    pr.launch(cx.ctx, cx.s, op, args)
+    g = pr.end_capture(cx.ctx, cx.s)
+    for i in range(3):
+        x = gemv_activations(rng, rows, k).astype(np.float32)
+        cx.upload(xb.addr, x)
+        pr.replay(cx.ctx, cx.s, g)
+        got = cx.get(yb, np.float32, (rows, n_out))
+        assert_same(got, o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=8), f"replay {i}")
+
+
+def test_events_and_device_copy(cx):
+    P, pr = cx.P, cx.pr
+    a = np.arange(1 << 16, dtype=np.uint32)
+    src, dst = cx.put(a), cx.empty(a.nbytes, 0)
+    e0, e1 = pr.event(cx.ctx), pr.event(cx.ctx)
+    announce("provider copy + events")
+    pr.record(cx.ctx, cx.s, e0)
+    pr.copy(cx.ctx, cx.s, P.Slice(src.handle, 0, a.nbytes), P.Slice(dst.handle, 0, a.nbytes))
+    pr.record(cx.ctx, cx.s, e1)
+    assert (cx.get(dst, np.uint32, a.size) == a).all()
+    assert pr.poll(cx.ctx, e1)
+    mi = pr.memory_info(cx.ctx)
+    assert mi.total > 200 << 30 and 0 < mi.free <= mi.total
+    devs = pr.enumerate()
+    assert devs and devs[0]["class"] == {"Hip": {"gfx": 0x950}}
+    with pytest.raises(P.ProviderError):  # a slice past its buffer
+        pr.copy(cx.ctx, cx.s, P.Slice(src.handle, 8, a.nbytes), P.Slice(dst.handle, 0, a.nbytes))

@@ -1,0 +1,181 @@
+"""The provider-library boundary on the CPU: the one exported symbol, the header handshake, the
+table's identity and layout, the JSON the core reads (ops, query), and the error protocol
+(status classes and codes, per-thread messages, per-thread contexts, stickiness).  No device call
+reaches a kernel: on a host without a GPU `open` fails with a Device status.
+
+The reference's own checks of a module: crates/kernels-loader/src/module.rs:26-40 (header),
+crates/kernels/src/abi/guest.rs:184-280 (status, messages, contexts)."""
+import ctypes as C
+import json
+import os
+import subprocess
+import threading
+
+import pytest
+
+import torch  # noqa: F401  one HIP runtime in the process
+
+from syntropy_amd import provider as P
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def pr():
+    if not os.path.exists(P.PROVIDER_LIB):
+        pytest.fail(f"{P.PROVIDER_LIB} is not built: run python -m syntropy_amd.build")
+    return P.Provider()
+
+
+def test_exports_exactly_the_entry_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", P.PROVIDER_LIB], capture_output=True, text=True,
+                         check=True).stdout
+    syms = [l.split()[-1] for l in out.splitlines() if l.split() and l.split()[-2] in "TtDdBbRrWwVv"]
+    syms = [s for s in syms if not s.startswith("SYNTROPY_PROVIDER_1")]
+    assert syms == ["syntropy_provider_entry_v1@@SYNTROPY_PROVIDER_1"], syms
+
+
+def test_struct_sizes_match_the_reference_layout():
+    # repr(C) sizes of crates/kernels/src/abi/types.rs on x86-64
+    assert C.sizeof(P.Header) == 52
+    assert C.sizeof(P.Status) == 12
+    assert C.sizeof(P.TensorArg) == 64
+    assert C.sizeof(P.BufferView) == 56
+    assert C.sizeof(P.OpArgs) == 120
+    assert C.sizeof(P.Health) == P.HEALTH_SIZE
+    assert C.sizeof(P.Vtbl) == 24 + 36 * 8 + 8 + 8  # head, 36 entries, slf, health_size (padded)
+
+
+def test_python_mirror_matches_the_c_header(tmp_path):
+    """Every field offset of the ctypes mirror equals the C header's (compiled here with gcc)."""
+    pairs = [("SynHeader", P.Header), ("SynStatus", P.Status), ("SynHostApi", P.HostApi),
+             ("SynMemoryInfo", P.MemoryInfo), ("SynBuffer", P.Buffer), ("SynSlice", P.Slice),
+             ("SynTensorArg", P.TensorArg), ("SynBufferView", P.BufferView), ("SynOpArgs", P.OpArgs),
+             ("SynOutBuf", P.OutBuf), ("SynProviderVtbl", P.Vtbl), ("SynModule", P.Module),
+             ("SynOpenOptions", P.OpenOptions), ("SynDeviceId", P.DeviceId)]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "syntropy_provider.h"', "int main(void){"]
+    want = []
+    for cname, py in pairs:
+        lines.append(f'printf("%zu\\n", sizeof({cname}));')
+        want.append(C.sizeof(py))
+        for f, _ in py._fields_:
+            lines.append(f'printf("%zu\\n", offsetof({cname}, {f}));')
+            want.append(getattr(py, f).offset)
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got == want
+
+
+def test_refuses_a_foreign_host_header():
+    for kw in ({"magic": b"SYNPROV2"}, {"major": 2}, {"size": 16}):
+        m, _, _ = P.load(host=P.host_api(**kw))
+        assert m is None, kw
+    m, _, _ = P.load()
+    assert m is not None and bytes(m.h.magic) == P.MAGIC
+
+
+def test_module_and_table_identity(pr):
+    m, vt = pr.module, pr.vt
+    assert (m.h.abi_major, m.h.abi_minor, m.n_providers) == (1, 0, 1)
+    assert m.h.struct_size == C.sizeof(P.Module)
+    assert vt.struct_size == C.sizeof(P.Vtbl)
+    assert pr.id() == "hip" and vt.backend == P.BACKEND_HIP and vt.domain == P.MEMDOMAIN_HIP
+    assert vt.health_size == 12
+    assert m.shutdown().cls == 0
+
+
+def test_build_and_ops_json(pr):
+    b = pr.build()
+    assert b["version"] == 1 and ["target", "gfx950"] in b["toolchain"]
+    ops = pr.ops()
+    got = {(json.dumps(k["op"]), k["schemes"][0].get("Ggml")) for k in ops}
+    assert got == {('"Gemv"', "Q4_K"), ('"Gemv"', "Q8_0"), ('"Gemv"', "Q4_0"), ('"MoeGrouped"', "Q4_K"),
+                   ('{"MoeRoute": {"norm": "Softmax"}}', None), ('"MoeCombine"', None)}
+    for k in ops:
+        assert k["layout"] == 0 and k["variant"] == 0
+
+
+def test_outbuf_retry_protocol(pr):
+    """A too-small buffer gets only the length (types.rs SynOutBuf)."""
+    buf = (C.c_uint8 * 4)(9, 9, 9, 9)
+    out = P.OutBuf(C.cast(buf, C.POINTER(C.c_uint8)), 4, 0)
+    assert pr.vt.ops(pr.vt.slf, C.byref(out)).cls == 0
+    assert out.len > 4 and list(buf) == [9, 9, 9, 9]
+
+
+def test_unserved_entries_are_unsupported(pr):
+    vt, slf = pr.vt, pr.vt.slf
+    calls = {
+        "map_segment": lambda: vt.map_segment(slf, 1, None, 0, 0, None),
+        "unmap_segment": lambda: vt.unmap_segment(slf, 1, None),
+        "register_host": lambda: vt.register_host(slf, 1, P.HostRegion(0, 0), None),
+        "host_registrar": lambda: vt.host_registrar(slf, 1, None),
+        "import": lambda: getattr(vt, "import")(slf, 1, P.HostRegion(0, 0), None),
+        "signal_host": lambda: vt.signal_host(slf, 1, 1, 0, 1),
+        "wait_host": lambda: vt.wait_host(slf, 1, 1, 0, 1, 0, 0, 0),
+        "arm_wake": lambda: vt.arm_wake(slf, 1, 1, 0, 0),
+    }
+    for name, f in calls.items():
+        st = f()
+        assert (st.cls, st.code, st.domain) == (2, 1, 1), name
+        assert name in pr.message(), name
+
+
+def test_repack_reports_no_repacked_layout(pr):
+    present, layout, n = C.c_uint32(7), C.c_uint32(7), C.c_uint64(7)
+    assert pr.vt.repack(pr.vt.slf, None, 0, None, 0, None, 0, C.byref(present), C.byref(layout)).cls == 0
+    assert (present.value, layout.value) == (0, 0)
+    assert pr.vt.repacked_len(pr.vt.slf, None, 0, 4096, C.byref(present), C.byref(n)).cls == 0
+    assert (present.value, n.value) == (0, 0)
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the behaviour on a host without a GPU")
+def test_open_without_a_device_is_a_device_error(pr):
+    with pytest.raises(P.ProviderError) as e:
+        pr.open(0)
+    assert e.value.cls == 6 and "no HIP device" in e.value.message
+    assert pr.enumerate() == []
+
+
+def test_unknown_context_is_refused(pr):
+    with pytest.raises(P.ProviderError) as e:
+        pr.query(987654, {"op": "Gemv"}, {})
+    assert e.value.cls == 13 and "not open on this thread" in e.value.message
+    with pytest.raises(P.ProviderError):
+        pr.stream(987654)
+    with pytest.raises(P.ProviderError):
+        pr.close(987654)
+
+
+def test_messages_are_per_thread(pr):
+    with pytest.raises(P.ProviderError):
+        pr.stream(5551)
+    mine = pr.message()
+    seen = {}
+
+    def other():
+        seen["before"] = pr.message()
+        st = pr.vt.signal_host(pr.vt.slf, 1, 1, 0, 1)
+        seen["cls"] = st.cls
+        seen["after"] = pr.message()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert "5551" in mine
+    assert seen["before"] == "" and seen["cls"] == 2 and "signal_host" in seen["after"]
+    assert pr.message() == mine
+
+
+def test_health_is_healthy(pr):
+    h = pr.health()
+    assert (h.kind, h.domain, h.detail) == (0, 0, 0)
+
+
+def test_header_declares_the_entry():
+    text = open(os.path.join(ROOT, "include", "syntropy_provider.h")).read()
+    assert "const SynModule* syntropy_provider_entry_v1(const SynHostApi* host);" in text
