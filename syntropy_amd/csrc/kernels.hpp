@@ -35,8 +35,9 @@ void launch_moe_pack(const int32_t* ids, int nslots, int n_experts, uint32_t* of
                      uint32_t* slots, uint32_t* err, hipStream_t stream);
 // Q8_K activations of the packed entries as the expert kernels read them, entry-major.  Each
 // 256-value block b of an entry is stored in the matrix-core operand order: byte
-// 256b + 64p + 8j + i holds code 32j + 8p + i (sub-block j, k part p), so that one lane reads
-// its A operand of all eight sub-blocks as 64 contiguous bytes.  lh holds, per block, the
+// 256b + 64p + 16(j%4) + 8(j/4) + i holds code 32j + 8p + i (sub-block j, k part p), so that
+// one lane reads its A operand of all eight sub-blocks as 64 contiguous bytes, the two
+// sub-blocks j and j + 4 it multiplies together side by side.  lh holds, per block, the
 // sub-block code sums s_j = 128 h_j + l_j as bytes l_0..l_7 (0..127), h_0..h_7 (-32..31).
 struct MoeAct {
     int8_t* codes;  // [entry][k]
