@@ -64,6 +64,23 @@ int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uin
              const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
              void* stream);
 
+/* ---- Prefill GEMM ---------------------------------------------------------------------------
+ * Q4_K weights times many activation rows on the matrix cores, each output bit-identical to
+ * syn_gemv (which takes this path itself for Q4_K calls of 32 rows or more).  The reference
+ * computes the same value with its Gemv kernel over row groups (crates/kernels-cpu/src/gemv.rs:
+ * 435-492; its Gemm kind is Gemv at a larger bucket, crates/kernels/src/reference/linear.rs:
+ * 11-13).  k_in must be whole 256-weight super-blocks.
+ * syn_gemm_workspace_bytes: the activation workspace for `rows` rows of width k_in.
+ * syn_gemm_act_quantize: x F32 [rows, k_in] to Q8_K in the GEMM's layout (x 16-byte, ws
+ *   256-byte aligned); the values of crates/kernels-cpu/src/gemv/act.rs:351-373.
+ * syn_gemm_q4k_quantized: y F32 [rows, n_out] = W [n_out, k_in] x from that workspace
+ *   (w 16-byte aligned). */
+int syn_gemm_workspace_bytes(uint32_t rows, uint32_t k_in, uint64_t* bytes);
+int syn_gemm_act_quantize(const float* x, uint32_t rows, uint32_t k_in, void* ws, uint64_t ws_bytes,
+                          void* stream);
+int syn_gemm_q4k_quantized(const void* w, uint64_t w_bytes, uint32_t n_out, uint32_t k_in,
+                           const void* ws, uint64_t ws_bytes, uint32_t rows, float* y, void* stream);
+
 /* ---- Grouped decode -----------------------------------------------------------------------
  * Up to 8 independent single-row Q4_K Gemv ops in two launches (one batched Q8_K quantization,
  * one grouped GEMV): y[i] F32 [n_out[i]] = W[i] [n_out[i], k_in[i]] x[i], each bit-identical to

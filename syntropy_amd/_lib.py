@@ -48,6 +48,9 @@ def lib():
         "syn_act_quantize_batch": [u32, vp, vp, vp, u64, vp],
         "syn_gemv_batch_quantized": [u32, vp, vp, vp, vp, vp, vp, u64, vp, vp],
         "syn_dequantize": [i32, vp, u64, fp, vp],
+        "syn_gemm_workspace_bytes": [u32, u32, C.POINTER(C.c_uint64)],
+        "syn_gemm_act_quantize": [vp, u32, u32, vp, u64, vp],
+        "syn_gemm_q4k_quantized": [vp, u64, u32, u32, vp, u64, u32, vp, vp],
         "syn_moe_route": [vp, vp, u32, u32, u32, u32, i32, vp, vp, vp, vp],
         "syn_moe_pack": [vp, u32, u32, u32, vp, vp, vp, vp],
         "syn_moe_grouped_workspace_bytes": [i32, u32, u32, u32, u32, u32, C.POINTER(C.c_uint64)],

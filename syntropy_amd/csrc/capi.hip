@@ -42,6 +42,34 @@ int check_gemv_shape(const char* what, int32_t wtype, uint32_t rows, uint32_t k_
     return SYN_OK;
 }
 
+// Q4_K calls of at least this many activation rows run on the matrix cores (k_gemm_q4k); the
+// value of every output is the same either way.
+constexpr uint32_t GEMM_MIN_ROWS = 32;
+
+uint64_t gemm_tpad(uint32_t rows) { return ((uint64_t)rows + 63) / 64 * 64; }
+
+bool use_gemm(int32_t wtype, uint32_t rows, uint32_t n_out, uint32_t k_in) {
+    return wtype == SYN_Q4_K && rows >= GEMM_MIN_ROWS && syn::gemm_q4k_supported((int)n_out, (int)k_in) &&
+           gemm_tpad(rows) * (k_in / 256) < (1ull << 31);
+}
+
+// Workspace of a Gemv call: the larger of the two activation layouts when the call may take
+// the matrix-core path (the bytes do not depend on n_out, which the workspace query lacks).
+uint64_t gemv_ws_bytes(int32_t wtype, uint32_t rows, uint32_t k_in) {
+    uint64_t b = syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
+    if (use_gemm(wtype, rows, 1, k_in)) {
+        const uint64_t g = syn::gemm_act_bytes((int64_t)gemm_tpad(rows), (int)k_in);
+        if (g > b) b = g;
+    }
+    return b;
+}
+
+int check_gemm_shape(const char* what, uint32_t rows, uint32_t k_in) {
+    if (k_in == 0 || k_in % 256) return fail(SYN_E_INVALID, "%s: k_in %u is not whole 256-weight super-blocks", what, k_in);
+    if (gemm_tpad(rows) * (k_in / 256) >= (1ull << 31)) return fail(SYN_E_INVALID, "%s: rows * k_in too large", what);
+    return SYN_OK;
+}
+
 }  // namespace
 
 SYN_EXPORT const char* syn_last_error(void) { return g_last_error.c_str(); }
@@ -51,7 +79,7 @@ SYN_EXPORT int syn_gemv_workspace_bytes(int32_t wtype, uint32_t rows, uint32_t k
                                         uint64_t* bytes) {
     if (int rc = check_gemv_shape("syn_gemv_workspace_bytes", wtype, rows, k_in)) return rc;
     if (!bytes) return fail(SYN_E_INVALID, "syn_gemv_workspace_bytes: null output");
-    *bytes = syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
+    *bytes = gemv_ws_bytes(wtype, rows, k_in);
     return SYN_OK;
 }
 
@@ -106,7 +134,9 @@ SYN_EXPORT int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t
     if (int rc = check_gemv_shape(W, wtype, rows, k_in)) return rc;
     if (rows == 0 || n_out == 0) return SYN_OK;
     const uint64_t row_bytes = (uint64_t)k_in / syn::block_elems(wtype) * syn::block_bytes(wtype);
-    const uint64_t need_ws = syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
+    const bool gemm = use_gemm(wtype, rows, n_out, k_in) && aligned(w, 16);
+    const uint64_t need_ws = gemm ? syn::gemm_act_bytes((int64_t)gemm_tpad(rows), (int)k_in)
+                                  : syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
     if (!y || (row_bytes * n_out && !w)) return fail(SYN_E_INVALID, "%s: null operand", W);
     if (w_bytes < row_bytes * n_out)
         return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
@@ -122,12 +152,69 @@ SYN_EXPORT int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t
         syn::launch_gemv_q4k_dec_f32((const uint8_t*)w, (int)n_out, (int)k_in, x, y, (hipStream_t)stream);
         return check_launch(W);
     }
+    if (gemm) {
+        const syn::GemmAct a = syn::gemm_act_at((uint8_t*)ws, (int64_t)gemm_tpad(rows), (int)k_in);
+        syn::launch_gemm_act(x, (int)rows, (int)k_in, a, (hipStream_t)stream);
+        if (int rc = check_launch(W)) return rc;
+        syn::launch_gemm_q4k((const uint8_t*)w, (int)n_out, (int)k_in, a, (int)rows, y, (hipStream_t)stream);
+        return check_launch(W);
+    }
     if (k_in) {
         syn::launch_act_quant(syn::act_kind(wtype), x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
         if (int rc = check_launch(W)) return rc;
     }
     syn::launch_gemv_q(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows,
                        y, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_gemm_workspace_bytes(uint32_t rows, uint32_t k_in, uint64_t* bytes) {
+    const char* W = "syn_gemm_workspace_bytes";
+    if (int rc = check_gemm_shape(W, rows, k_in)) return rc;
+    if (!bytes) return fail(SYN_E_INVALID, "%s: null output", W);
+    *bytes = syn::gemm_act_bytes((int64_t)gemm_tpad(rows), (int)k_in);
+    return SYN_OK;
+}
+
+SYN_EXPORT int syn_gemm_act_quantize(const float* x, uint32_t rows, uint32_t k_in, void* ws,
+                                     uint64_t ws_bytes, void* stream) {
+    const char* W = "syn_gemm_act_quantize";
+    if (int rc = check_gemm_shape(W, rows, k_in)) return rc;
+    if (rows == 0) return SYN_OK;
+    const uint64_t need = syn::gemm_act_bytes((int64_t)gemm_tpad(rows), (int)k_in);
+    if (!x || !ws) return fail(SYN_E_INVALID, "%s: null x or workspace", W);
+    if (!aligned(x, 16) || !aligned(ws, 256))
+        return fail(SYN_E_INVALID, "%s: x must be 16-byte and the workspace 256-byte aligned", W);
+    if (ws_bytes < need)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)need);
+    syn::launch_gemm_act(x, (int)rows, (int)k_in,
+                         syn::gemm_act_at((uint8_t*)ws, (int64_t)gemm_tpad(rows), (int)k_in), (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_gemm_q4k_quantized(const void* w, uint64_t w_bytes, uint32_t n_out, uint32_t k_in,
+                                      const void* ws, uint64_t ws_bytes, uint32_t rows, float* y,
+                                      void* stream) {
+    const char* W = "syn_gemm_q4k_quantized";
+    if (int rc = check_gemm_shape(W, rows, k_in)) return rc;
+    if (rows == 0 || n_out == 0) return SYN_OK;
+    if (!syn::gemm_q4k_supported((int)n_out, (int)k_in))
+        return fail(SYN_E_UNSUPPORTED, "%s: a %u x %u matrix is larger than 4 GiB", W, n_out, k_in);
+    const uint64_t need_w = (uint64_t)n_out * (k_in / 256) * 144;
+    const uint64_t need = syn::gemm_act_bytes((int64_t)gemm_tpad(rows), (int)k_in);
+    if (!w || !ws || !y) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (w_bytes < need_w)
+        return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
+                    (unsigned long long)w_bytes, (unsigned long long)need_w);
+    if (ws_bytes < need)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)need);
+    if (!aligned(w, 16) || !aligned(ws, 256) || !aligned(y, 4))
+        return fail(SYN_E_INVALID, "%s: w must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
+    syn::launch_gemm_q4k((const uint8_t*)w, (int)n_out, (int)k_in,
+                         syn::gemm_act_at((uint8_t*)ws, (int64_t)gemm_tpad(rows), (int)k_in), (int)rows, y,
+                         (hipStream_t)stream);
     return check_launch(W);
 }
 

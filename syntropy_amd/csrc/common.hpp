@@ -205,4 +205,37 @@ SYN_DEV void q8k_block_wave(const float* __restrict__ xb, int8_t* __restrict__ c
     if (lane == 0) *dout = r.d;
 }
 
+// ---- LDS staging helpers of the matrix-core kernels ----------------------------------------
+
+// s_waitcnt that waits for vector memory only: vmcnt n, expcnt and lgkmcnt left at their maxima.
+template <int N>
+SYN_DEV void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// The same for a wave-uniform n <= M.
+template <int M>
+SYN_DEV void wait_vm_n(int n) {
+    if constexpr (M > 0) {
+        if (n >= M) {
+            wait_vm<M>();
+            return;
+        }
+        wait_vm_n<M - 1>(n);
+    } else {
+        wait_vm<0>();
+    }
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// Workgroup barrier over LDS reads only: each wavefront's LDS reads have returned, then
+// s_barrier.  (The fence of __syncthreads would also wait for every load into LDS still in
+// flight, the next stages' included.)  The memory clobber keeps the compiler from moving
+// memory accesses across it.
+SYN_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// The LDS address (M0 form) of a pointer into shared memory.
+SYN_DEV uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_ptr)(p); }
+
 }  // namespace syn

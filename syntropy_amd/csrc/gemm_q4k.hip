@@ -1,0 +1,374 @@
+// Prefill Q4_K GEMM on the gfx950 matrix cores: Y[t][n] for many activation rows t, each
+// output the exact Gemv value (crates/kernels-cpu/src/gemv.rs:435-547: per super-block the
+// term (d*dx)*S1 - (dmin*dx)*S2 with S1 = sum_j sc_j D_j and S2 = sum_j m_j s_j exact, folded
+// in super-block order from +0.0).  The reference's Gemm is the same value (its Gemm kind is
+// Gemv at a larger bucket, crates/kernels/src/reference/linear.rs:11-13).
+//
+// Exact sums on F16 matrix cores.  v_mfma_f32_16x16x32_f16 multiplies F16 operands exactly and
+// accumulates in F32; when every operand is an integer and every partial sum stays below 2^24
+// in magnitude, the F32 result is the exact integer whatever the order of the additions.  Per
+// super-block the kernel feeds, for k = 0..255:
+//   A[t][k] = x code (Q8_K, |x| <= 127, written as F16 by k_gemm_act);
+//   B[k][n] = sc_j(k) * q_k - 472   (|B| <= 473, exact F16: the 6-bit scale folded into the
+//                                     4-bit code, centred so that 256 * 127 * 473 < 2^24)
+// so one accumulator holds D = S1 - 472 X exactly, X = sum_k x_k (a per-token integer the
+// activation kernel stores), and fma(472, X, D) = fl(S1): one rounding of the exact S1, which
+// is the reference's `S1 as f32`.  S2 comes from a second product per tile: A = (l_j, 64 h_j)
+// with s_j = 64 h_j + l_j, B = (m_j, m_j), also exact.  The term and the fold are plain F32
+// operations in the reference's order.
+//
+// B from the packed nibbles, two codes per instruction: a dword shifted so that a nibble of each
+// 16-bit half sits at bits 4-7, masked and ORed with 0x6400 in each half, is the F16 pair
+// (1024 + 16 q0, 1024 + 16 q1), and one v_pk_fma_f16 with (sc/16, -(64 sc + 472)) gives
+// sc*q - 472 exactly (every constant is an exact F16 and the FMA rounds once, to an exact
+// integer).  The k order inside
+// a super-block is free (the sum is exact), so each lane's eight k slots of an instruction are
+// the codes of four consecutive bytes, low nibbles then high: k_gemm_act writes the activations
+// in the same order.
+//
+// Tiling.  A workgroup computes 64 tokens x 256 rows; each of its 4 wavefronts 64 tokens x 64
+// rows as 4 x 4 tiles of 16 x 16, so each A operand serves four rows tiles and each B operand four
+// token tiles.  Per super-block the weight rows (144 bytes each), the 64 tokens' codes and their
+// sums, scales and X stream from global memory into LDS with global_load_lds_dwordx4 (no
+// registers held while they fly), one stage ahead, in a ring of two 72 KB stages.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace syn {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// ============================================================================================
+// Activation layout (GemmAct)
+// ============================================================================================
+//
+// For tpad = T rounded up to 64 and nb = k / 256 super-blocks:
+//   codes [nb][tpad][256] F16: chunk c = 8p + s (8 codes) of token t holds the values
+//         64p + 4s + {0, 2, 1, 3, 32, 34, 33, 35} and sits at chunk position c ^ (t & 15), so the
+//         16 lanes of a read touch 16 distinct 16-byte bank groups;
+//   tail  [nb][ s2: tpad x 16 F16 | dx: tpad x F32 | X: tpad x F32 ]: s2 = (l_0..l_7,
+//         64 h_0..64 h_7) with s_j = 64 h_j + l_j, 0 <= l_j < 64; dx the Q8_K scale; X the sum
+//         of the block's 256 codes.
+// Rows t >= T are zero.
+constexpr int GM_TAIL_ROW = 40;  // tail bytes per token per super-block
+
+size_t gemm_act_bytes(int64_t tpad, int k) {
+    const int64_t nb = k / 256;
+    return align_up((uint64_t)(nb * tpad * 512), 256) + align_up((uint64_t)(nb * tpad * GM_TAIL_ROW), 256);
+}
+
+GemmAct gemm_act_at(uint8_t* base, int64_t tpad, int k) {
+    const int64_t nb = k / 256;
+    GemmAct a;
+    a.codes = base;
+    a.tail = base + align_up((uint64_t)(nb * tpad * 512), 256);
+    a.tpad = (int)tpad;
+    return a;
+}
+
+// One wavefront per (super-block b, token t): the Q8_K block of crates/kernels-cpu/src/gemv/
+// act.rs:351-373 (q8k_block_lane), written in the GEMM order.  Lane l holds values 4l..4l+3:
+// sub-block j = l / 8, k part p = l / 16, nibble half h = (l / 8) & 1, dword s = l & 7.
+__global__ __launch_bounds__(256) void k_gemm_act(const float* __restrict__ x, int T, int k, GemmAct a) {
+    const int nb = k / 256, lane = threadIdx.x & 63;
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= (int64_t)nb * a.tpad) return;
+    const int b = (int)(item / a.tpad), t = (int)(item - (int64_t)b * a.tpad);
+    uint32_t q = 0;
+    int sum32 = 0, xsum = 0;
+    float d = 0.0f;
+    if (t < T) {  // uniform over the wavefront
+        const Q8KLane r = q8k_block_lane(x + (int64_t)t * k + (int64_t)b * 256, lane);
+        q = r.packed;
+        sum32 = r.sum32;
+        d = r.d;
+        xsum = sum32;
+        xsum += __shfl_xor(xsum, 8);
+        xsum += __shfl_xor(xsum, 16);
+        xsum += __shfl_xor(xsum, 32);
+    }
+    const int p = lane >> 4, h = (lane >> 3) & 1, s = lane & 7;
+    auto code = [&](int i) { return (_Float16)(float)(int8_t)(q >> (8 * i)); };
+    h2 lo = {code(0), code(2)}, hi = {code(1), code(3)};
+    const int pos = (8 * p + s) ^ (t & 15);
+    uint8_t* dst = a.codes + ((int64_t)b * a.tpad + t) * 512 + pos * 16 + 8 * h;
+    uint2 v;
+    v.x = __builtin_bit_cast(uint32_t, lo);
+    v.y = __builtin_bit_cast(uint32_t, hi);
+    *reinterpret_cast<uint2*>(dst) = v;
+    uint8_t* tail = a.tail + (int64_t)b * a.tpad * GM_TAIL_ROW;
+    if ((lane & 7) == 0) {
+        const int j = lane >> 3;
+        const int hj = sum32 >> 6;  // floor: s = 64 h + l with 0 <= l < 64
+        const int lj = sum32 - 64 * hj;
+        _Float16* s2 = reinterpret_cast<_Float16*>(tail + (int64_t)t * 32);
+        s2[j] = (_Float16)(float)lj;
+        s2[8 + j] = (_Float16)(float)(64 * hj);
+    }
+    if (lane == 0) {
+        reinterpret_cast<float*>(tail + (int64_t)a.tpad * 32)[t] = d;
+        reinterpret_cast<float*>(tail + (int64_t)a.tpad * 36)[t] = (float)xsum;
+    }
+}
+
+void launch_gemm_act(const float* x, int T, int k, GemmAct a, hipStream_t stream) {
+    const int64_t items = (int64_t)(k / 256) * a.tpad;
+    if (items == 0) return;
+    hipLaunchKernelGGL(k_gemm_act, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, x, T, k, a);
+}
+
+// ============================================================================================
+// The GEMM
+// ============================================================================================
+
+constexpr int GM_TT = 64;                           // tokens per workgroup
+constexpr int GM_NT = 4;                            // 16-row tiles per wavefront
+constexpr int GM_MT = 4;                            // 16-token tiles per wavefront
+constexpr int GM_ROWS = 4 * 16 * GM_NT;             // rows per workgroup
+constexpr int GM_WB = GM_ROWS * 144;                // weight bytes per stage
+constexpr int GM_AB = GM_TT * 512;                  // code bytes per stage
+constexpr int GM_TB = GM_TT * GM_TAIL_ROW;          // s2 | dx | X bytes per stage
+constexpr int GM_STAGE = GM_WB + GM_AB + GM_TB;
+constexpr int GM_WSLOT = GM_WB / 1024;              // wavefront loads (64 x 16 bytes) of each part
+constexpr int GM_ASLOT = GM_AB / 1024;
+constexpr int GM_TSLOT = (GM_TB + 1023) / 1024;
+constexpr int GM_SLOTS = GM_WSLOT + GM_ASLOT + GM_TSLOT;
+constexpr int GM_PER_WAVE = (GM_SLOTS + 3) / 4;
+static_assert(GM_WB % 1024 == 0 && GM_AB % 1024 == 0, "wavefront-sized weight and code parts");
+static_assert(GM_STAGE % 16 == 0 && 2 * GM_STAGE <= 160 * 1024, "two stages in LDS");
+
+struct GemmArgs {
+    const uint8_t* W;
+    const uint8_t* codes;
+    const uint8_t* tail;
+    float* y;
+    int N, T, nb, tpad;
+    uint32_t rb;  // weight row bytes
+};
+
+// The lane's 32-bit offsets of its loads of one stage, relative to the part's base of the
+// super-block (weights: W + 144 b; codes: codes + (b tpad + t0) 512; tail: tail + b tpad 40).
+struct GemmSlots {
+    uint32_t woff[(GM_WSLOT + 3) / 4];
+    uint32_t toff;
+    int nw, nt;     // weight and tail slots of this wavefront (uniform)
+    bool ton;       // this lane's tail chunk exists
+};
+
+SYN_DEV GemmSlots gemm_slots(const GemmArgs& g, int wave, int lane, int n0, int t0) {
+    GemmSlots s;
+    s.nw = 0;
+#pragma unroll
+    for (int u = 0; u < (GM_WSLOT + 3) / 4; ++u) {
+        const int gs = wave + 4 * u;
+        const int ci = 64 * gs + lane, row = ci / 9, part = ci - 9 * (ci / 9);
+        const int r = n0 + row < g.N ? n0 + row : g.N - 1;
+        s.woff[u] = (uint32_t)r * g.rb + 16u * (uint32_t)part;
+        if (gs < GM_WSLOT) s.nw = u + 1;
+    }
+    // tail slot: wave w takes tail part w if it exists
+    s.nt = wave < GM_TSLOT ? 1 : 0;
+    const int ti = 64 * wave + lane;
+    s.ton = s.nt && ti < GM_TB / 16;
+    if (ti < GM_TT * 2)
+        s.toff = (uint32_t)t0 * 32u + 16u * (uint32_t)ti;
+    else if (ti < GM_TT * 2 + GM_TT / 4)
+        s.toff = (uint32_t)g.tpad * 32u + (uint32_t)t0 * 4u + 16u * (uint32_t)(ti - GM_TT * 2);
+    else
+        s.toff = (uint32_t)g.tpad * 36u + (uint32_t)t0 * 4u + 16u * (uint32_t)(ti - GM_TT * 2 - GM_TT / 4);
+    return s;
+}
+
+SYN_DEV void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
+    // m0 (the LDS address) is reserved: the compiler keeps nothing in it across code
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "memory");
+}
+
+// Issues the wavefront's loads of super-block b into `stage`.  Slot order: weight parts
+// wave, wave + 4, ..; code parts wave, wave + 4, ..; tail part `wave`.
+SYN_DEV void gemm_issue(const GemmArgs& g, const GemmSlots& s, int wave, int lane, int b, int t0,
+                        uint8_t* stage) {
+    const uint8_t* wb = g.W + 144 * (size_t)b;
+    const uint8_t* ab = g.codes + ((size_t)b * g.tpad + t0) * 512;
+    const uint8_t* tb = g.tail + (size_t)b * g.tpad * GM_TAIL_ROW;
+    const uint32_t st = lds_addr(stage);
+#pragma unroll
+    for (int u = 0; u < (GM_WSLOT + 3) / 4; ++u)
+        if (u < s.nw) dma16(s.woff[u], wb, st + 1024u * (uint32_t)(wave + 4 * u));
+#pragma unroll
+    for (int u = 0; u < GM_ASLOT / 4; ++u) {
+        const int gs = wave + 4 * u;
+        dma16(16u * (uint32_t)lane, ab + 1024 * gs, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
+    }
+    if (s.ton) dma16(s.toff, tb, st + (uint32_t)(GM_WB + GM_AB) + 1024u * (uint32_t)wave);
+}
+
+// The F16 pair (1024 + 16 q0, 1024 + 16 q1) etc. from the nibbles under `mask`.
+SYN_DEV h2 magic_pair(uint32_t v, uint32_t mask) {
+    return __builtin_bit_cast(h2, (v & mask) | 0x64006400u);
+}
+
+SYN_DEV h2 bcast(_Float16 v) { return h2{v, v}; }
+
+// One super-block of the wavefront's 64 tokens x 64 rows from the stage in LDS.
+SYN_DEV void gemm_super(const uint8_t* st, int wave, int lane, v4f (&acc)[GM_MT][GM_NT]) {
+    const int c = lane & 15, p = lane >> 4;
+    const uint8_t* wt = st + (64 * wave) * 144;
+    const uint8_t* at = st + GM_WB;
+    const uint8_t* tl = st + GM_WB + GM_AB;
+
+    // per row tile: scales, the B-operand constants, the S2 operand
+    float dd[GM_NT], dm[GM_NT];
+    h2 ka[GM_NT], kb[GM_NT];  // (sc/16, -(64 sc + 472)) of sub-blocks 2p and 2p + 1
+    v8h bm[GM_NT];
+#pragma unroll
+    for (int nt = 0; nt < GM_NT; ++nt) {
+        const v4u hdr = *reinterpret_cast<const v4u*>(wt + (16 * nt + c) * 144);
+        dd[nt] = f16_to_f32(hdr.x);
+        dm[nt] = f16_to_f32(hdr.x >> 16);
+        // get_scale_min_k4 (gemv.rs:528-537) on packed bytes
+        const uint32_t w0 = hdr.y, w1 = hdr.z, w2 = hdr.w;
+        const uint32_t sc_lo = w0 & 0x3F3F3F3Fu;                                 // sc_0..3
+        const uint32_t sc_hi = (w2 & 0x0F0F0F0Fu) | ((w0 >> 2) & 0x30303030u);   // sc_4..7
+        const uint32_t mn_lo = w1 & 0x3F3F3F3Fu;                                 // m_0..3
+        const uint32_t mn_hi = ((w2 >> 4) & 0x0F0F0F0Fu) | ((w1 >> 2) & 0x30303030u);  // m_4..7
+        // this lane group's sub-blocks: 2p (low nibbles) and 2p + 1 (high nibbles)
+        const uint32_t scw = p < 2 ? sc_lo : sc_hi;
+        const int sa = (int)((scw >> (16 * (p & 1))) & 0xFFu), sb = (int)((scw >> (16 * (p & 1) + 8)) & 0xFFu);
+        const float fa = (float)sa, fb = (float)sb;
+        ka[nt] = h2{(_Float16)(fa * 0.0625f), (_Float16)(-(64.0f * fa + 472.0f))};
+        kb[nt] = h2{(_Float16)(fb * 0.0625f), (_Float16)(-(64.0f * fb + 472.0f))};
+        // S2 operand: m_0..m_7 in lane groups 0 and 1 (against l_j and 64 h_j), zero in 2 and 3
+        const _Float16 on = p < 2 ? (_Float16)1.0f : (_Float16)0.0f;
+        const h2 k1 = bcast(on), k0 = bcast((_Float16)(-1024.0f) * on);
+        // bytes b0, b1 of a word into the low bits of two halves
+        const h2 m01 = __builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, mn_lo, 0x0c010c00u) | 0x64006400u), k1, k0);
+        const h2 m23 = __builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, mn_lo, 0x0c030c02u) | 0x64006400u), k1, k0);
+        const h2 m45 = __builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, mn_hi, 0x0c010c00u) | 0x64006400u), k1, k0);
+        const h2 m67 = __builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, mn_hi, 0x0c030c02u) | 0x64006400u), k1, k0);
+        bm[nt] = v8h{m01.x, m01.y, m23.x, m23.y, m45.x, m45.y, m67.x, m67.y};
+    }
+
+    v4f dacc[GM_MT][GM_NT];
+#pragma unroll
+    for (int mt = 0; mt < GM_MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < GM_NT; ++nt) dacc[mt][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        v8h bq[GM_NT];
+#pragma unroll
+        for (int nt = 0; nt < GM_NT; ++nt) {
+            // bytes 32p + 4s .. +3 of the row's codes: sub-block 2p (low) and 2p + 1 (high)
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(wt + (16 * nt + c) * 144 + 16 + 32 * p + 4 * s);
+            // (b0, b2) low nibbles, (b1, b3) low, (b0, b2) high, (b1, b3) high
+            const h2 y3 = __builtin_elementwise_fma(magic_pair(v << 4, 0x00F000F0u), bcast(ka[nt].x), bcast(ka[nt].y));
+            const h2 y2 = __builtin_elementwise_fma(magic_pair(v >> 4, 0x00F000F0u), bcast(ka[nt].x), bcast(ka[nt].y));
+            const h2 y1 = __builtin_elementwise_fma(magic_pair(v, 0x00F000F0u), bcast(kb[nt].x), bcast(kb[nt].y));
+            const h2 y4 = __builtin_elementwise_fma(magic_pair(v >> 8, 0x00F000F0u), bcast(kb[nt].x), bcast(kb[nt].y));
+            bq[nt] = v8h{y3.x, y3.y, y2.x, y2.y, y1.x, y1.y, y4.x, y4.y};
+        }
+#pragma unroll
+        for (int mt = 0; mt < GM_MT; ++mt) {
+            const int t = 16 * mt + c;
+            const v8h a = *reinterpret_cast<const v8h*>(at + t * 512 + (((8 * p + s) ^ c) << 4));
+#pragma unroll
+            for (int nt = 0; nt < GM_NT; ++nt)
+                dacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[nt], dacc[mt][nt], 0, 0, 0);
+        }
+    }
+
+    // S2, then the super-block terms folded into the accumulators
+    const v8h zero8 = {};
+#pragma unroll
+    for (int mt = 0; mt < GM_MT; ++mt) {
+        const v8h as = p < 2 ? *reinterpret_cast<const v8h*>(tl + (16 * mt + c) * 32 + 16 * p) : zero8;
+        const v4f dx = *reinterpret_cast<const v4f*>(tl + GM_TT * 32 + (16 * mt + 4 * p) * 4);
+        const v4f xs = *reinterpret_cast<const v4f*>(tl + GM_TT * 36 + (16 * mt + 4 * p) * 4);
+#pragma unroll
+        for (int nt = 0; nt < GM_NT; ++nt) {
+            const v4f s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bm[nt], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float s1 = __builtin_fmaf(472.0f, xs[i], dacc[mt][nt][i]);  // fl(S1), exact operands
+                const float a1 = (dd[nt] * dx[i]) * s1;
+                const float a2 = (dm[nt] * dx[i]) * s2[i];
+                acc[mt][nt][i] = acc[mt][nt][i] + (a1 - a2);
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_gemm_q4k(GemmArgs g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: slot choices in SGPRs
+    const int n0 = blockIdx.x * GM_ROWS, t0 = blockIdx.y * GM_TT;
+    const GemmSlots sl = gemm_slots(g, wave, lane, n0, t0);
+    const int live = sl.nw + GM_ASLOT / 4 + sl.nt;  // loads per stage of this wavefront
+    v4f acc[GM_MT][GM_NT];
+#pragma unroll
+    for (int mt = 0; mt < GM_MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < GM_NT; ++nt) acc[mt][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    gemm_issue(g, sl, wave, lane, 0, t0, smem);
+    if (g.nb > 1) gemm_issue(g, sl, wave, lane, 1, t0, smem + GM_STAGE);
+    for (int b = 0; b < g.nb; ++b) {
+        uint8_t* stage = smem + (b & 1) * GM_STAGE;
+        // this lane's loads of b have landed once at most those of b + 1 are in flight
+        wait_vm_n<GM_PER_WAVE>(b + 1 < g.nb ? live : 0);
+        lds_barrier();
+        gemm_super(stage, wave, lane, acc);
+        lds_barrier();
+        if (b + 2 < g.nb) gemm_issue(g, sl, wave, lane, b + 2, t0, stage);
+    }
+
+    const int c = lane & 15, p = lane >> 4;
+#pragma unroll
+    for (int mt = 0; mt < GM_MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < GM_NT; ++nt) {
+            const int n = n0 + 64 * wave + 16 * nt + c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = t0 + 16 * mt + 4 * p + i;
+                if (t < g.T && n < g.N) g.y[(int64_t)t * g.N + n] = acc[mt][nt][i];
+            }
+        }
+}
+
+bool gemm_q4k_supported(int n_out, int k) {
+    return k >= 256 && k % 256 == 0 && n_out > 0 &&
+           (uint64_t)n_out * (uint64_t)(k / 256) * 144u < (1ull << 32);
+}
+
+void launch_gemm_q4k(const uint8_t* W, int n_out, int k, GemmAct a, int T, float* y, hipStream_t stream) {
+    GemmArgs g;
+    g.W = W;
+    g.codes = a.codes;
+    g.tail = a.tail;
+    g.y = y;
+    g.N = n_out;
+    g.T = T;
+    g.nb = k / 256;
+    g.tpad = a.tpad;
+    g.rb = (uint32_t)(k / 256) * 144u;
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void*)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  2 * GM_STAGE);
+        attr = true;
+    }
+    const dim3 grid((unsigned)((n_out + GM_ROWS - 1) / GM_ROWS), (unsigned)(a.tpad / GM_TT));
+    hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(256), 2 * GM_STAGE, stream, g);
+}
+
+}  // namespace syn

@@ -58,6 +58,19 @@ void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
                      const uint32_t* err, float* out, hipStream_t stream);
 void launch_moe_combine(const float* out, const int32_t* ids, const float* w, int rows, int top_k,
                         int hidden, float* y, hipStream_t stream);
+// gemm_q4k.hip: the prefill Q4_K GEMM on the F16 matrix cores.  Activations are quantized to
+// Q8_K into the GEMM's own layout (codes as F16 in the matrix-core operand order, then per
+// super-block the sub-block sums, scales and block sums); tpad = rows rounded up to 64.
+struct GemmAct {
+    uint8_t* codes;
+    uint8_t* tail;
+    int tpad;
+};
+size_t gemm_act_bytes(int64_t tpad, int k);
+GemmAct gemm_act_at(uint8_t* base, int64_t tpad, int k);
+void launch_gemm_act(const float* x, int T, int k, GemmAct a, hipStream_t stream);
+bool gemm_q4k_supported(int n_out, int k);
+void launch_gemm_q4k(const uint8_t* W, int n_out, int k, GemmAct a, int T, float* y, hipStream_t stream);
 // quant.hip
 void launch_quantize(int ty, const float* x, uint64_t n, uint8_t* out, hipStream_t stream);
 void launch_dequantize(int ty, const uint8_t* src, uint64_t n, float* out, hipStream_t stream);

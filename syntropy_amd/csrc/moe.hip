@@ -454,34 +454,6 @@ struct MoeCfg {
 };
 constexpr int MOE_STAGES = 3;
 
-// s_waitcnt that waits for vector memory only: vmcnt n, expcnt and lgkmcnt left at their maxima.
-template <int N>
-SYN_DEV void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-// The same for a wave-uniform n <= M.
-template <int M>
-SYN_DEV void wait_vm_n(int n) {
-    if constexpr (M > 0) {
-        if (n >= M) {
-            wait_vm<M>();
-            return;
-        }
-        wait_vm_n<M - 1>(n);
-    } else {
-        wait_vm<0>();
-    }
-}
-
-typedef __attribute__((address_space(3))) void* lds_ptr;
-
-// Workgroup barrier over LDS reads only: each wavefront's LDS reads have returned, then
-// s_barrier.  (The fence of __syncthreads would also wait for every load into LDS still in
-// flight, the next stages' included.)  The memory clobber keeps the compiler from moving
-// memory accesses across it.
-SYN_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // One wavefront's load slot of a stage: the lane's global address of super-block 0 and its
 // step per super-block, whether the lane loads, and the slot's LDS offset inside the stage.
 // Every load is 16 bytes; lane L of a slot writes LDS offset + 16 L.

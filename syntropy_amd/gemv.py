@@ -169,6 +169,30 @@ class GemvBatch:
              self.ws.data_ptr(), self.ws.numel(), self.y, _stream(stream))
 
 
+def gemm_workspace(rows: int, k: int, device="cuda") -> torch.Tensor:
+    """Workspace of the prefill GEMM's activations (rows x k, Q8_K in the GEMM layout)."""
+    out = C.c_uint64()
+    call("syn_gemm_workspace_bytes", rows, k, C.byref(out))
+    return torch.empty(max(out.value, 256), dtype=torch.uint8, device=device)
+
+
+def gemm_quantize_into(x: torch.Tensor, rows: int, k: int, ws: torch.Tensor, stream=None) -> None:
+    """The first `rows` rows of x to Q8_K in the prefill GEMM's layout (act.rs:351-373 values)."""
+    _check_x(x, rows, k)
+    call("syn_gemm_act_quantize", x.data_ptr(), rows, k, ws.data_ptr(), ws.numel(), _stream(stream))
+
+
+def gemm_quantized(w: Weights, ws: torch.Tensor, rows: int, y: torch.Tensor, stream=None) -> None:
+    """y[r][o] for every row r < rows from a workspace gemm_quantize_into filled: the Q4_K
+    matrix-core GEMM, every output the Gemv value (gemv.rs:435-547)."""
+    if w.ty is not WeightType.Q4K:
+        raise GemvError("Activations", "the prefill GEMM takes Q4_K weights")
+    if y.numel() < rows * w.n_out:
+        raise GemvError("Len", f"`y` holds {y.numel()} values, the op needs {rows * w.n_out}")
+    call("syn_gemm_q4k_quantized", w.bytes.data_ptr(), w.bytes.numel(), w.n_out, w.k_in, ws.data_ptr(),
+         ws.numel(), rows, y.data_ptr(), _stream(stream))
+
+
 def quantize(ty: WeightType, x: torch.Tensor, stream=None) -> torch.Tensor:
     """F32 values -> GGUF blocks, byte-identical to ggml's reference quantizers
     (crates/kernels-ggml/src/lib.rs:268 quantize).  Like that wrapper, refuses non-finite
@@ -194,4 +218,5 @@ def dequantize(ty: WeightType, src: torch.Tensor, stream=None) -> torch.Tensor:
 
 
 __all__ = ["WeightType", "Weights", "GemvError", "SynError", "GemvBatch", "workspace_bytes", "quantize_into",
-           "gemv_quantized", "gemv", "quantize", "dequantize", "new_workspace", "lib"]
+           "gemv_quantized", "gemv", "quantize", "dequantize", "new_workspace", "gemm_workspace",
+           "gemm_quantize_into", "gemm_quantized", "lib"]
