@@ -11,7 +11,9 @@ from the 256 MB Infinity Cache.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only layer|copy] [--no-cpu]
 
 Prints one JSON line: whole-step weight GB/s (value), the roofline of the GEMV kernel from
-HIP events on its stream, and the CPU oracle timed on this host's cores.
+HIP events on its stream, and the CPU oracle timed on this host's cores; beside it the MoE layer
+at 64 decode tokens ("moe") and the 2048-token prefill ("prefill": the dense GEMMs on the matrix
+cores and the skewed MoE layer).
 """
 from __future__ import annotations
 
@@ -50,6 +52,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=8.0)
     p.add_argument("--no-moe", action="store_true")
+    p.add_argument("--no-prefill", action="store_true")
     return p.parse_args()
 
 
@@ -209,6 +212,120 @@ def bench_moe(torch, S, M, steps, warmup, cpu_seconds):
     return res
 
 
+PREFILL = dict(tokens=2048, dense=[("gate", 14336, 4096), ("down", 4096, 14336)], skew_rows=(3, 50, 97),
+               skew_scale=3.0)
+F16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(torch, S, M, steps, warmup, cpu_seconds, moe_layer_parts=None):
+    """Prefill at 2048 tokens: the dense Q4_K GEMMs (2048x4096 activations, BF16-valued, times
+    gate 14336x4096 and down 4096x14336) on the matrix cores, and the MoE layer at 2048 tokens
+    with three router rows scaled so their experts take several times the average load."""
+    c = PREFILL
+    T = c["tokens"]
+    gen = torch.Generator(device="cuda")
+    mats, xs, wss, ys = {}, {}, {}, {}
+    for i, (name, n_out, k) in enumerate(c["dense"]):
+        gen.manual_seed(0x51A10005 + i)
+        w = torch.randn(n_out * k, generator=gen, device="cuda") * 0.02
+        mats[name] = S.Weights(S.WeightType.Q4K, S.quantize(S.WeightType.Q4K, w), n_out, k)
+        del w
+        gen.manual_seed(0x51A20005 + i)
+        xs[name] = torch.randn(T, k, generator=gen, device="cuda").to(torch.bfloat16).float()
+        wss[name] = S.gemm_workspace(T, k)
+        ys[name] = torch.empty(T, n_out, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def dense_step():
+        for name, _, k in c["dense"]:
+            S.gemm_quantize_into(xs[name], T, k, wss[name], stream=stream)
+            S.gemm_quantized(mats[name], wss[name], T, ys[name], stream=stream)
+
+    for _ in range(warmup):
+        dense_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dense_step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    flops = sum(2.0 * T * n * k for _, n, k in c["dense"])
+    # the GEMM kernel alone, HIP events on its stream
+    per = {}
+    for name, _, k in c["dense"]:
+        S.gemm_quantize_into(xs[name], T, k, wss[name], stream=stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            S.gemm_quantized(mats[name], wss[name], T, ys[name], stream=stream)
+        e1.record()
+        torch.cuda.synchronize()
+        per[name] = e0.elapsed_time(e1) / steps  # ms
+    gemm_s = sum(per.values()) * 1e-3
+    res = {
+        "workload": "prefill, 2048 tokens: X 2048x4096 (BF16 values) x Q4_K gate 14336x4096, "
+                    "X' 2048x14336 x Q4_K down 4096x14336; Q8_K activation quantization + GEMM each",
+        "dense_tokens_per_s": round(T / dt, 1),
+        "dense_ms_per_step": round(dt * 1e3, 4),
+        "dense_tflops": round(flops / dt / 1e12, 1),
+        "roofline": {"bound": "mfma", "kernel": "k_gemm_q4k (F16 MFMA, exact integer sums)",
+                     "achieved": round(flops / gemm_s / 1e12, 1), "peak": F16_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flops / gemm_s / 1e12 / F16_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": None, "avg_launch_us": {k: round(v * 1e3, 1) for k, v in per.items()}},
+    }
+    del mats, xs, wss, ys
+    torch.cuda.empty_cache()
+    # MoE at 2048 tokens, skewed
+    mc = MOE
+    layer, _ = build_moe(torch, S, M, 0x51A40000) if moe_layer_parts is None else moe_layer_parts
+    router = layer.router.clone()
+    for r in c["skew_rows"]:
+        router[r] *= c["skew_scale"]
+    gen.manual_seed(0x51A20006)
+    x = torch.randn(T, mc["hidden"], generator=gen, device="cuda")
+    big = M.MoeLayer(layer.s, router, layer.experts, T)
+    for _ in range(max(1, warmup // 2)):
+        big(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        y, ids, w, out = big(x)
+    torch.cuda.synchronize()
+    mdt = (time.perf_counter() - t0) / steps
+    ids_h = ids.cpu().numpy()
+    loads = sorted((int((ids_h == e).sum()) for e in range(mc["n_experts"])), reverse=True)
+    avg = T * mc["top_k"] / mc["n_experts"]
+    moe_flops = 2.0 * T * mc["top_k"] * 3 * mc["inter"] * mc["hidden"]
+    res["moe"] = {"tokens_per_s": round(T / mdt, 1), "ms_per_step": round(mdt * 1e3, 3),
+                  "tflops": round(moe_flops / mdt / 1e12, 1),
+                  "top_loads_over_avg": [round(v / avg, 2) for v in loads[:4]],
+                  "skew": f"router rows {list(c['skew_rows'])} scaled by {c['skew_scale']}"}
+    if cpu_seconds > 0:
+        from oracle import oracle as o
+        threads = min(16, os.cpu_count() or 1)
+        rows = 16
+        gen.manual_seed(0x51A10005)
+        sample = []
+        for i, (name, n_out, k) in enumerate(c["dense"]):
+            gen.manual_seed(0x51A10005 + i)
+            w = torch.randn(n_out * k, generator=gen, device="cuda") * 0.02
+            wb = S.quantize(S.WeightType.Q4K, w).cpu().numpy()
+            xh = torch.randn(rows, k, device="cuda").cpu().numpy()
+            sample.append((wb, n_out, k, xh))
+        n, t1 = 0, time.perf_counter()
+        while True:
+            for wb, n_out, k, xh in sample:
+                o.gemv(o.Q4_K, wb, n_out, k, xh, rows, threads=threads)
+            n += 1
+            if time.perf_counter() - t1 >= cpu_seconds:
+                break
+        cdt = time.perf_counter() - t1
+        res["cpu_baseline"] = {"value": round(rows * n / cdt, 1), "unit": "tokens/s (dense gate+down)",
+                               "cores": threads, "kind": "port",
+                               "sample": f"{n} x {rows} token rows through gate and down in {cdt:.1f} s"}
+    return res
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -334,6 +451,10 @@ def main():
         torch.cuda.empty_cache()
         out["moe"] = bench_moe(torch, S, M, max(10, a.steps // 4), max(3, a.warmup // 4),
                                0 if a.no_cpu else a.cpu_seconds)
+    if not a.no_prefill:
+        torch.cuda.empty_cache()
+        out["prefill"] = bench_prefill(torch, S, M, max(5, a.steps // 20), max(2, a.warmup // 10),
+                                       0 if a.no_cpu else min(a.cpu_seconds, 5.0))
     print(json.dumps(out))
 
 
