@@ -34,6 +34,9 @@ extern "C" {
 #define SYN_Q8_0 8
 #define SYN_Q4_K 12
 
+#define SYN_LAYOUT_SOURCE 0 /* the GGUF order */
+#define SYN_LAYOUT_X8 1     /* Q4_K runs of eight super-blocks stored chunk-major */
+
 /* The message of the last failed call on this thread ("" if none). */
 const char* syn_last_error(void);
 /* Library version: major * 10000 + minor * 100 + patch. */
@@ -63,6 +66,34 @@ int syn_gemv_quantized(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t 
 int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uint32_t k_in,
              const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
              void* stream);
+
+/* ---- Weight layouts ---------------------------------------------------------------------------
+ * Layout 1 (X8) of a Q4_K matrix is a permutation of its bytes: each run of eight consecutive
+ * 144-byte super-blocks is stored chunk-major (16-byte chunk q of the run's block i at 128 q +
+ * 16 i; a final run of m < 8 blocks with stride 16 m).  It needs only the byte count, as the
+ * reference's repack does (crates/kernels/src/provider.rs:326-336, repack / repacked_len: the
+ * repacked form is the same length).  Decode then reads whole 128-byte lines per load.
+ * syn_q4k_repack: on the device (src and dst distinct, 16-byte aligned); inverse = 1 restores
+ *   the GGUF order.  syn_q4k_repack_host: the same on host memory.
+ * syn_gemv_layout(_workspace_bytes): the Gemv op over a matrix in `layout` (0 is syn_gemv); for
+ *   layout 1 one row runs the grouped decode kernel (k_in <= 16384), more rows the matrix-core
+ *   GEMM (k_in a multiple of 2048).
+ * syn_gemv_batch_layout / syn_gemv_batch_quantized_layout: the grouped decode of every problem
+ *   in `layout`. */
+int syn_q4k_repack(uint32_t layout, const void* src, void* dst, uint64_t bytes, int32_t inverse, void* stream);
+int syn_q4k_repack_host(uint32_t layout, const void* src, void* dst, uint64_t bytes, int32_t inverse);
+int syn_gemv_layout_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t rows, uint32_t k_in,
+                                    uint64_t* bytes);
+int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                    uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
+                    void* stream);
+int syn_gemv_batch_layout(uint32_t layout, uint32_t n, const int32_t* wtypes, const void* const* w,
+                          const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
+                          const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
+                          void* stream);
+int syn_gemv_batch_quantized_layout(uint32_t layout, uint32_t n, const int32_t* wtypes, const void* const* w,
+                                    const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
+                                    const void* ws, uint64_t ws_bytes, float* const* y, void* stream);
 
 /* ---- Prefill GEMM ---------------------------------------------------------------------------
  * Q4_K weights times many activation rows on the matrix cores, each output bit-identical to

@@ -51,6 +51,12 @@ def lib():
         "syn_gemm_workspace_bytes": [u32, u32, C.POINTER(C.c_uint64)],
         "syn_gemm_act_quantize": [vp, u32, u32, vp, u64, vp],
         "syn_gemm_q4k_quantized": [vp, u64, u32, u32, vp, u64, u32, vp, vp],
+        "syn_q4k_repack": [u32, vp, vp, u64, i32, vp],
+        "syn_q4k_repack_host": [u32, vp, vp, u64, i32],
+        "syn_gemv_layout_workspace_bytes": [u32, i32, u32, u32, C.POINTER(C.c_uint64)],
+        "syn_gemv_layout": [u32, i32, vp, u64, u32, u32, vp, u32, vp, vp, u64, vp],
+        "syn_gemv_batch_layout": [u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, u64, vp],
+        "syn_gemv_batch_quantized_layout": [u32, u32, vp, vp, vp, vp, vp, vp, u64, vp, vp],
         "syn_moe_route": [vp, vp, u32, u32, u32, u32, i32, vp, vp, vp, vp],
         "syn_moe_pack": [vp, u32, u32, u32, vp, vp, vp, vp],
         "syn_moe_grouped_workspace_bytes": [i32, u32, u32, u32, u32, u32, C.POINTER(C.c_uint64)],

@@ -1,6 +1,7 @@
 // The C ABI (include/syntropy_hip.h): argument checks, then the kernel launchers.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
 
 #include <string>
 
@@ -156,7 +157,8 @@ SYN_EXPORT int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t
         const syn::GemmAct a = syn::gemm_act_at((uint8_t*)ws, (int64_t)gemm_tpad(rows), (int)k_in);
         syn::launch_gemm_act(x, (int)rows, (int)k_in, a, (hipStream_t)stream);
         if (int rc = check_launch(W)) return rc;
-        syn::launch_gemm_q4k((const uint8_t*)w, (int)n_out, (int)k_in, a, (int)rows, y, (hipStream_t)stream);
+        syn::launch_gemm_q4k(SYN_LAYOUT_SOURCE, (const uint8_t*)w, (int)n_out, (int)k_in, a, (int)rows, y,
+                             (hipStream_t)stream);
         return check_launch(W);
     }
     if (k_in) {
@@ -212,7 +214,7 @@ SYN_EXPORT int syn_gemm_q4k_quantized(const void* w, uint64_t w_bytes, uint32_t 
                     (unsigned long long)ws_bytes, (unsigned long long)need);
     if (!aligned(w, 16) || !aligned(ws, 256) || !aligned(y, 4))
         return fail(SYN_E_INVALID, "%s: w must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
-    syn::launch_gemm_q4k((const uint8_t*)w, (int)n_out, (int)k_in,
+    syn::launch_gemm_q4k(SYN_LAYOUT_SOURCE, (const uint8_t*)w, (int)n_out, (int)k_in,
                          syn::gemm_act_at((uint8_t*)ws, (int64_t)gemm_tpad(rows), (int)k_in), (int)rows, y,
                          (hipStream_t)stream);
     return check_launch(W);
@@ -276,9 +278,11 @@ int batch_quantize(const char* W, uint32_t n, const uint32_t* k_in, const float*
     return check_launch(W);
 }
 
-int batch_gemv(const char* W, uint32_t n, const void* const* w, const uint32_t* n_out,
+int batch_gemv(const char* W, int layout, uint32_t n, const void* const* w, const uint32_t* n_out,
                const uint32_t* k_in, const uint8_t* ws, const uint64_t* off, float* const* y,
                hipStream_t st) {
+    if (layout != SYN_LAYOUT_SOURCE && layout != SYN_LAYOUT_X8)
+        return fail(SYN_E_UNSUPPORTED, "%s: weight layout %d", W, layout);
     const uint8_t* wp[SYN_BATCH];
     const uint8_t* wsp[SYN_BATCH];
     float* yp[SYN_BATCH];
@@ -291,7 +295,7 @@ int batch_gemv(const char* W, uint32_t n, const void* const* w, const uint32_t* 
         no[i] = (int)n_out[i];
         kk[i] = (int)k_in[i];
     }
-    syn::launch_gemv_q4k_batch((int)n, wp, no, kk, wsp, yp, st);
+    syn::launch_gemv_q4k_batch(layout, (int)n, wp, no, kk, wsp, yp, st);
     return check_launch(W);
 }
 
@@ -307,29 +311,137 @@ SYN_EXPORT int syn_act_quantize_batch(uint32_t n, const uint32_t* k_in, const fl
     return batch_quantize(W, n, k_in, x, (uint8_t*)ws, off, (hipStream_t)stream);
 }
 
-SYN_EXPORT int syn_gemv_batch_quantized(uint32_t n, const int32_t* wtypes, const void* const* w,
-                                        const uint64_t* w_bytes, const uint32_t* n_out,
-                                        const uint32_t* k_in, const void* ws, uint64_t ws_bytes,
-                                        float* const* y, void* stream) {
+SYN_EXPORT int syn_gemv_batch_quantized_layout(uint32_t layout, uint32_t n, const int32_t* wtypes,
+                                               const void* const* w, const uint64_t* w_bytes,
+                                               const uint32_t* n_out, const uint32_t* k_in, const void* ws,
+                                               uint64_t ws_bytes, float* const* y, void* stream) {
     const char* W = "syn_gemv_batch_quantized";
     if (n == 0) return SYN_OK;
     if (!w || !y) return fail(SYN_E_INVALID, "%s: null argument array", W);
     uint64_t off[SYN_BATCH];
     if (int rc = batch_setup(W, n, wtypes, w, w_bytes, n_out, k_in, (void*)ws, ws_bytes, off)) return rc;
-    return batch_gemv(W, n, w, n_out, k_in, (const uint8_t*)ws, off, y, (hipStream_t)stream);
+    return batch_gemv(W, (int)layout, n, w, n_out, k_in, (const uint8_t*)ws, off, y, (hipStream_t)stream);
+}
+
+SYN_EXPORT int syn_gemv_batch_quantized(uint32_t n, const int32_t* wtypes, const void* const* w,
+                                        const uint64_t* w_bytes, const uint32_t* n_out,
+                                        const uint32_t* k_in, const void* ws, uint64_t ws_bytes,
+                                        float* const* y, void* stream) {
+    return syn_gemv_batch_quantized_layout(SYN_LAYOUT_SOURCE, n, wtypes, w, w_bytes, n_out, k_in, ws, ws_bytes,
+                                           y, stream);
+}
+
+SYN_EXPORT int syn_gemv_batch_layout(uint32_t layout, uint32_t n, const int32_t* wtypes, const void* const* w,
+                                     const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
+                                     const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
+                                     void* stream) {
+    const char* W = "syn_gemv_batch";
+    if (n == 0) return SYN_OK;
+    if (!w || !x || !y) return fail(SYN_E_INVALID, "%s: null argument array", W);
+    if (layout != SYN_LAYOUT_SOURCE && layout != SYN_LAYOUT_X8)
+        return fail(SYN_E_UNSUPPORTED, "%s: weight layout %u", W, layout);
+    uint64_t off[SYN_BATCH];
+    if (int rc = batch_setup(W, n, wtypes, w, w_bytes, n_out, k_in, ws, ws_bytes, off)) return rc;
+    if (int rc = batch_quantize(W, n, k_in, x, (uint8_t*)ws, off, (hipStream_t)stream)) return rc;
+    return batch_gemv(W, (int)layout, n, w, n_out, k_in, (const uint8_t*)ws, off, y, (hipStream_t)stream);
 }
 
 SYN_EXPORT int syn_gemv_batch(uint32_t n, const int32_t* wtypes, const void* const* w,
                               const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
                               const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
                               void* stream) {
-    const char* W = "syn_gemv_batch";
-    if (n == 0) return SYN_OK;
-    if (!w || !x || !y) return fail(SYN_E_INVALID, "%s: null argument array", W);
-    uint64_t off[SYN_BATCH];
-    if (int rc = batch_setup(W, n, wtypes, w, w_bytes, n_out, k_in, ws, ws_bytes, off)) return rc;
-    if (int rc = batch_quantize(W, n, k_in, x, (uint8_t*)ws, off, (hipStream_t)stream)) return rc;
-    return batch_gemv(W, n, w, n_out, k_in, (const uint8_t*)ws, off, y, (hipStream_t)stream);
+    return syn_gemv_batch_layout(SYN_LAYOUT_SOURCE, n, wtypes, w, w_bytes, n_out, k_in, x, y, ws, ws_bytes,
+                                 stream);
+}
+
+// ---- weight layouts -----------------------------------------------------------------------------
+
+namespace {
+int check_repack(const char* W, uint32_t layout, const void* src, void* dst, uint64_t bytes) {
+    if (layout != SYN_LAYOUT_X8) return fail(SYN_E_UNSUPPORTED, "%s: layout %u (1: X8)", W, layout);
+    if (bytes % 144) return fail(SYN_E_INVALID, "%s: %llu bytes are not whole Q4_K super-blocks", W, (unsigned long long)bytes);
+    if (bytes && (!src || !dst)) return fail(SYN_E_INVALID, "%s: null buffer", W);
+    if (bytes && src == dst) return fail(SYN_E_INVALID, "%s: the repack is not in place", W);
+    return SYN_OK;
+}
+}  // namespace
+
+SYN_EXPORT int syn_q4k_repack(uint32_t layout, const void* src, void* dst, uint64_t bytes, int32_t inverse,
+                              void* stream) {
+    const char* W = "syn_q4k_repack";
+    if (int rc = check_repack(W, layout, src, dst, bytes)) return rc;
+    if (!aligned(src, 16) || !aligned(dst, 16)) return fail(SYN_E_INVALID, "%s: buffers must be 16-byte aligned", W);
+    syn::launch_q4k_x8((const uint8_t*)src, (uint8_t*)dst, bytes / 144, inverse != 0, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_q4k_repack_host(uint32_t layout, const void* src, void* dst, uint64_t bytes, int32_t inverse) {
+    const char* W = "syn_q4k_repack_host";
+    if (int rc = check_repack(W, layout, src, dst, bytes)) return rc;
+    const uint64_t nblocks = bytes / 144;
+    const uint8_t* s = (const uint8_t*)src;
+    uint8_t* d = (uint8_t*)dst;
+    for (uint64_t g = 0; g < nblocks; ++g)
+        for (int q = 0; q < 9; ++q) {
+            const uint64_t to = syn::x8_chunk_offset(g, q, nblocks), from = g * 144 + 16 * (uint64_t)q;
+            memcpy(d + (inverse ? from : to), s + (inverse ? to : from), 16);
+        }
+    return SYN_OK;
+}
+
+// Gemv over Q4_K weights in a repacked layout: one row runs the grouped decode kernel, more rows
+// the matrix-core GEMM (which needs rows of whole 8-block runs: k_in a multiple of 2048).
+SYN_EXPORT int syn_gemv_layout_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t rows, uint32_t k_in,
+                                               uint64_t* bytes) {
+    const char* W = "syn_gemv_layout_workspace_bytes";
+    if (layout == SYN_LAYOUT_SOURCE) return syn_gemv_workspace_bytes(wtype, rows, k_in, bytes);
+    if (layout != SYN_LAYOUT_X8 || wtype != SYN_Q4_K)
+        return fail(SYN_E_UNSUPPORTED, "%s: layout %u of weight type %d", W, layout, wtype);
+    if (!bytes) return fail(SYN_E_INVALID, "%s: null output", W);
+    if (rows <= 1) {
+        if (k_in == 0 || k_in % 256 || k_in > 16384) return fail(SYN_E_UNSUPPORTED, "%s: k_in %u (256..16384, whole super-blocks)", W, k_in);
+        *bytes = syn::act_layout(syn::ACT_Q8K, 1, k_in).bytes;
+        return SYN_OK;
+    }
+    if (k_in % 2048) return fail(SYN_E_UNSUPPORTED, "%s: the layout-1 GEMM takes k_in in multiples of 2048, not %u", W, k_in);
+    if (int rc = check_gemm_shape(W, rows, k_in)) return rc;
+    *bytes = syn::gemm_act_bytes((int64_t)gemm_tpad(rows), (int)k_in);
+    return SYN_OK;
+}
+
+SYN_EXPORT int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                               uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
+                               void* stream) {
+    const char* W = "syn_gemv_layout";
+    if (layout == SYN_LAYOUT_SOURCE) return syn_gemv(wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, ws_bytes, stream);
+    uint64_t need = 0;
+    if (int rc = syn_gemv_layout_workspace_bytes(layout, wtype, rows, k_in, &need)) return rc;
+    if (rows == 0 || n_out == 0) return SYN_OK;
+    if (rows == 1) {
+        const float* xs[1] = {x};
+        float* ys[1] = {y};
+        const void* ws_[1] = {w};
+        const int32_t ts[1] = {wtype};
+        const uint64_t wb[1] = {w_bytes};
+        return syn_gemv_batch_layout(layout, 1, ts, ws_, wb, &n_out, &k_in, xs, ys, ws, ws_bytes, stream);
+    }
+    if (!syn::gemm_q4k_supported((int)n_out, (int)k_in))
+        return fail(SYN_E_UNSUPPORTED, "%s: a %u x %u matrix is larger than 4 GiB", W, n_out, k_in);
+    const uint64_t need_w = (uint64_t)n_out * (k_in / 256) * 144;
+    if (!w || !x || !ws || !y) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (w_bytes < need_w)
+        return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
+                    (unsigned long long)w_bytes, (unsigned long long)need_w);
+    if (ws_bytes < need)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)need);
+    if (!aligned(w, 16) || !aligned(x, 16) || !aligned(ws, 256) || !aligned(y, 4))
+        return fail(SYN_E_INVALID, "%s: w and x must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
+    const syn::GemmAct a = syn::gemm_act_at((uint8_t*)ws, (int64_t)gemm_tpad(rows), (int)k_in);
+    syn::launch_gemm_act(x, (int)rows, (int)k_in, a, (hipStream_t)stream);
+    if (int rc = check_launch(W)) return rc;
+    syn::launch_gemm_q4k(SYN_LAYOUT_X8, (const uint8_t*)w, (int)n_out, (int)k_in, a, (int)rows, y, (hipStream_t)stream);
+    return check_launch(W);
 }
 
 SYN_EXPORT int syn_quantize(int32_t wtype, const float* x, uint64_t n, void* out,

@@ -238,4 +238,15 @@ SYN_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::
 // The LDS address (M0 form) of a pointer into shared memory.
 SYN_DEV uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_ptr)(p); }
 
+// 16 bytes per active lane from sbase + voff to LDS address lds + 16 * lane, with no registers
+// held while the load flies.  Written as assembly so the compiler does not track it (it would
+// otherwise wait for every load into LDS in flight before each LDS read); the caller waits with
+// wait_vm.  m0 (the LDS address) is reserved: the compiler keeps nothing in it across code.
+SYN_DEV void lds_dma16(uint32_t voff, const void* sbase, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "memory");
+}
+
 }  // namespace syn

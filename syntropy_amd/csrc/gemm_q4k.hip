@@ -26,9 +26,9 @@
 // the codes of four consecutive bytes, low nibbles then high: k_gemm_act writes the activations
 // in the same order.
 //
-// Tiling.  A workgroup computes 64 tokens x 256 rows; each of its 4 wavefronts 64 tokens x 64
-// rows as 4 x 4 tiles of 16 x 16, so each A operand serves four rows tiles and each B operand four
-// token tiles.  Per super-block the weight rows (144 bytes each), the 64 tokens' codes and their
+// Tiling.  A workgroup computes 64 tokens x 256 rows; each of its 8 wavefronts 64 tokens x 32
+// rows as 4 x 2 tiles of 16 x 16 (two wavefronts per SIMD hide each other's LDS and matrix-core
+// latencies), so each A operand serves two row tiles and each B operand four token tiles.  Per super-block the weight rows (144 bytes each), the 64 tokens' codes and their
 // sums, scales and X stream from global memory into LDS with global_load_lds_dwordx4 (no
 // registers held while they fly), one stage ahead, in a ring of two 72 KB stages.
 #include "common.hpp"
@@ -125,9 +125,10 @@ void launch_gemm_act(const float* x, int T, int k, GemmAct a, hipStream_t stream
 // ============================================================================================
 
 constexpr int GM_TT = 64;                           // tokens per workgroup
-constexpr int GM_NT = 4;                            // 16-row tiles per wavefront
+constexpr int GM_WAVES = 8;                         // wavefronts per workgroup
+constexpr int GM_NT = 2;                            // 16-row tiles per wavefront
 constexpr int GM_MT = 4;                            // 16-token tiles per wavefront
-constexpr int GM_ROWS = 4 * 16 * GM_NT;             // rows per workgroup
+constexpr int GM_ROWS = GM_WAVES * 16 * GM_NT;      // rows per workgroup
 constexpr int GM_WB = GM_ROWS * 144;                // weight bytes per stage
 constexpr int GM_AB = GM_TT * 512;                  // code bytes per stage
 constexpr int GM_TB = GM_TT * GM_TAIL_ROW;          // s2 | dx | X bytes per stage
@@ -135,13 +136,15 @@ constexpr int GM_STAGE = GM_WB + GM_AB + GM_TB;
 constexpr int GM_WSLOT = GM_WB / 1024;              // wavefront loads (64 x 16 bytes) of each part
 constexpr int GM_ASLOT = GM_AB / 1024;
 constexpr int GM_TSLOT = (GM_TB + 1023) / 1024;
-constexpr int GM_SLOTS = GM_WSLOT + GM_ASLOT + GM_TSLOT;
-constexpr int GM_PER_WAVE = (GM_SLOTS + 3) / 4;
+constexpr int GM_WPW = (GM_WSLOT + GM_WAVES - 1) / GM_WAVES;  // weight slots per wavefront (at most)
+constexpr int GM_PER_WAVE = GM_WPW + GM_ASLOT / GM_WAVES + 1;
+static_assert(GM_ASLOT % GM_WAVES == 0 && GM_TSLOT <= GM_WAVES, "slot split");
 static_assert(GM_WB % 1024 == 0 && GM_AB % 1024 == 0, "wavefront-sized weight and code parts");
 static_assert(GM_STAGE % 16 == 0 && 2 * GM_STAGE <= 160 * 1024, "two stages in LDS");
 
 struct GemmArgs {
     const uint8_t* W;
+    int layout;  // LAYOUT_SOURCE or LAYOUT_X8 (rows of whole 8-block runs)
     const uint8_t* codes;
     const uint8_t* tail;
     float* y;
@@ -152,7 +155,7 @@ struct GemmArgs {
 // The lane's 32-bit offsets of its loads of one stage, relative to the part's base of the
 // super-block (weights: W + 144 b; codes: codes + (b tpad + t0) 512; tail: tail + b tpad 40).
 struct GemmSlots {
-    uint32_t woff[(GM_WSLOT + 3) / 4];
+    uint32_t woff[GM_WPW];
     uint32_t toff;
     int nw, nt;     // weight and tail slots of this wavefront (uniform)
     bool ton;       // this lane's tail chunk exists
@@ -162,11 +165,12 @@ SYN_DEV GemmSlots gemm_slots(const GemmArgs& g, int wave, int lane, int n0, int 
     GemmSlots s;
     s.nw = 0;
 #pragma unroll
-    for (int u = 0; u < (GM_WSLOT + 3) / 4; ++u) {
-        const int gs = wave + 4 * u;
+    for (int u = 0; u < GM_WPW; ++u) {
+        const int gs = wave + GM_WAVES * u;
         const int ci = 64 * gs + lane, row = ci / 9, part = ci - 9 * (ci / 9);
         const int r = n0 + row < g.N ? n0 + row : g.N - 1;
-        s.woff[u] = (uint32_t)r * g.rb + 16u * (uint32_t)part;
+        // chunk `part` of the row's block: 16 bytes on in GGUF order, 128 (a run's chunk row) in X8
+        s.woff[u] = (uint32_t)r * g.rb + (g.layout == LAYOUT_X8 ? 128u : 16u) * (uint32_t)part;
         if (gs < GM_WSLOT) s.nw = u + 1;
     }
     // tail slot: wave w takes tail part w if it exists
@@ -182,31 +186,26 @@ SYN_DEV GemmSlots gemm_slots(const GemmArgs& g, int wave, int lane, int n0, int 
     return s;
 }
 
-SYN_DEV void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
-    // m0 (the LDS address) is reserved: the compiler keeps nothing in it across code
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-                 :
-                 : "v"(voff), "s"(sbase), "s"(lds)
-                 : "memory");
-}
 
 // Issues the wavefront's loads of super-block b into `stage`.  Slot order: weight parts
-// wave, wave + 4, ..; code parts wave, wave + 4, ..; tail part `wave`.
+// wave, wave + 8, ..; code parts wave, wave + 8, ..; tail part `wave`.
 SYN_DEV void gemm_issue(const GemmArgs& g, const GemmSlots& s, int wave, int lane, int b, int t0,
                         uint8_t* stage) {
-    const uint8_t* wb = g.W + 144 * (size_t)b;
+    // super-block b of row 0: in X8 block b sits in run b / 8 at position b % 8
+    const uint8_t* wb = g.layout == LAYOUT_X8 ? g.W + 1152 * (size_t)(b >> 3) + 16 * (size_t)(b & 7)
+                                                  : g.W + 144 * (size_t)b;
     const uint8_t* ab = g.codes + ((size_t)b * g.tpad + t0) * 512;
     const uint8_t* tb = g.tail + (size_t)b * g.tpad * GM_TAIL_ROW;
     const uint32_t st = lds_addr(stage);
 #pragma unroll
-    for (int u = 0; u < (GM_WSLOT + 3) / 4; ++u)
-        if (u < s.nw) dma16(s.woff[u], wb, st + 1024u * (uint32_t)(wave + 4 * u));
+    for (int u = 0; u < GM_WPW; ++u)
+        if (u < s.nw) lds_dma16(s.woff[u], wb, st + 1024u * (uint32_t)(wave + GM_WAVES * u));
 #pragma unroll
-    for (int u = 0; u < GM_ASLOT / 4; ++u) {
-        const int gs = wave + 4 * u;
-        dma16(16u * (uint32_t)lane, ab + 1024 * gs, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
+    for (int u = 0; u < GM_ASLOT / GM_WAVES; ++u) {
+        const int gs = wave + GM_WAVES * u;
+        lds_dma16(16u * (uint32_t)lane, ab + 1024 * gs, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
     }
-    if (s.ton) dma16(s.toff, tb, st + (uint32_t)(GM_WB + GM_AB) + 1024u * (uint32_t)wave);
+    if (s.ton) lds_dma16(s.toff, tb, st + (uint32_t)(GM_WB + GM_AB) + 1024u * (uint32_t)wave);
 }
 
 // The F16 pair (1024 + 16 q0, 1024 + 16 q1) etc. from the nibbles under `mask`.
@@ -216,10 +215,10 @@ SYN_DEV h2 magic_pair(uint32_t v, uint32_t mask) {
 
 SYN_DEV h2 bcast(_Float16 v) { return h2{v, v}; }
 
-// One super-block of the wavefront's 64 tokens x 64 rows from the stage in LDS.
+// One super-block of the wavefront's 64 tokens x 32 rows from the stage in LDS.
 SYN_DEV void gemm_super(const uint8_t* st, int wave, int lane, v4f (&acc)[GM_MT][GM_NT]) {
     const int c = lane & 15, p = lane >> 4;
-    const uint8_t* wt = st + (64 * wave) * 144;
+    const uint8_t* wt = st + (16 * GM_NT * wave) * 144;
     const uint8_t* at = st + GM_WB;
     const uint8_t* tl = st + GM_WB + GM_AB;
 
@@ -306,13 +305,13 @@ SYN_DEV void gemm_super(const uint8_t* st, int wave, int lane, v4f (&acc)[GM_MT]
     }
 }
 
-__global__ __launch_bounds__(256) void k_gemm_q4k(GemmArgs g) {
+__global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_q4k(GemmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: slot choices in SGPRs
     const int n0 = blockIdx.x * GM_ROWS, t0 = blockIdx.y * GM_TT;
     const GemmSlots sl = gemm_slots(g, wave, lane, n0, t0);
-    const int live = sl.nw + GM_ASLOT / 4 + sl.nt;  // loads per stage of this wavefront
+    const int live = sl.nw + GM_ASLOT / GM_WAVES + sl.nt;  // loads per stage of this wavefront
     v4f acc[GM_MT][GM_NT];
 #pragma unroll
     for (int mt = 0; mt < GM_MT; ++mt)
@@ -336,7 +335,7 @@ __global__ __launch_bounds__(256) void k_gemm_q4k(GemmArgs g) {
     for (int mt = 0; mt < GM_MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < GM_NT; ++nt) {
-            const int n = n0 + 64 * wave + 16 * nt + c;
+            const int n = n0 + 16 * GM_NT * wave + 16 * nt + c;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = t0 + 16 * mt + 4 * p + i;
@@ -350,9 +349,11 @@ bool gemm_q4k_supported(int n_out, int k) {
            (uint64_t)n_out * (uint64_t)(k / 256) * 144u < (1ull << 32);
 }
 
-void launch_gemm_q4k(const uint8_t* W, int n_out, int k, GemmAct a, int T, float* y, hipStream_t stream) {
+void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, int T, float* y,
+                     hipStream_t stream) {
     GemmArgs g;
     g.W = W;
+    g.layout = layout;
     g.codes = a.codes;
     g.tail = a.tail;
     g.y = y;
@@ -368,7 +369,7 @@ void launch_gemm_q4k(const uint8_t* W, int n_out, int k, GemmAct a, int T, float
         attr = true;
     }
     const dim3 grid((unsigned)((n_out + GM_ROWS - 1) / GM_ROWS), (unsigned)(a.tpad / GM_TT));
-    hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(256), 2 * GM_STAGE, stream, g);
+    hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(64 * GM_WAVES), 2 * GM_STAGE, stream, g);
 }
 
 }  // namespace syn

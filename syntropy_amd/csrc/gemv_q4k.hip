@@ -29,7 +29,7 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr int COL = 272;  // LDS bytes per activation column (256 codes + 16-byte skew)
-constexpr int SUMW = 48;  // LDS bytes per column of 32-value sums (8 ints + skew)
+constexpr int SUMW = 32;  // LDS bytes per column of 32-value sums (8 ints)
 
 SYN_HD inline size_t q4k_dec_lds(int nb) { return (size_t)nb * (COL + SUMW + 4); }
 SYN_DEV int xs_off(int nb) { return nb * COL; }
@@ -117,17 +117,17 @@ SYN_DEV void quant_row_to_lds(const float* __restrict__ x, int nb, uint8_t* lds)
 
 SYN_DEV void copy_row_to_lds(const int8_t* __restrict__ xq, const float* __restrict__ xd,
                              const int32_t* __restrict__ xs, int nb, uint8_t* lds) {
-    for (int i = threadIdx.x; i < nb * 16; i += 256) {
+    for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
         const int c = i >> 4, p = i & 15;
         *reinterpret_cast<v4u*>(lds + c * COL + p * 16) =
             *reinterpret_cast<const v4u*>(xq + (int64_t)c * 256 + p * 16);
     }
-    for (int i = threadIdx.x; i < nb * 2; i += 256) {
+    for (int i = threadIdx.x; i < nb * 2; i += blockDim.x) {
         const int c = i >> 1, p = i & 1;
         *reinterpret_cast<v4u*>(lds + xs_off(nb) + c * SUMW + p * 16) =
             *reinterpret_cast<const v4u*>(xs + (int64_t)c * 8 + p * 4);
     }
-    for (int i = threadIdx.x; i < nb; i += 256) reinterpret_cast<float*>(lds + xd_off(nb))[i] = xd[i];
+    for (int i = threadIdx.x; i < nb; i += blockDim.x) reinterpret_cast<float*>(lds + xd_off(nb))[i] = xd[i];
 }
 
 // One super-block's term from its nine 16-byte words and activation column b in LDS.
@@ -263,9 +263,19 @@ struct DecBatch {
 
 SYN_DEV int lanes_per_row(int nb) { return nb <= 16 ? 16 : nb <= 32 ? 32 : 64; }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6)))
+// Wavefronts per workgroup of k_gemv_q4k_batch for each weight layout.
+template <int LAYOUT>
+constexpr int dec_waves() { return LAYOUT == LAYOUT_X8 ? 8 : 4; }
+
+// LAYOUT 0 (the GGUF order): each lane reads its 144-byte super-block with nine 16-byte loads.
+// LAYOUT 1 (x8): chunk q of the blocks of eight consecutive super-blocks sits together (see
+// layout.hpp), so the nine loads of a wavefront each read whole 128-byte lines, which streams at
+// a higher rate with non-temporal loads (the weights are read once).
+template <int LAYOUT>
+__global__ __launch_bounds__(64 * dec_waves<LAYOUT>()) __attribute__((amdgpu_waves_per_eu(6)))
 void k_gemv_q4k_batch(DecBatch bt) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int WAVES = dec_waves<LAYOUT>();
     int p = 0;
     while (p + 1 < bt.np && (int)blockIdx.x >= bt.wg_begin[p + 1]) ++p;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -273,19 +283,52 @@ void k_gemv_q4k_batch(DecBatch bt) {
     const int n_out = bt.n_out[p], nb = bt.nb[p];
     const int P = lanes_per_row(nb);
     const int rows_per_wave = 64 / P;
-    const int row = (((int)blockIdx.x - bt.wg_begin[p]) * 4 + wave) * rows_per_wave + lane / P;
+    const int row = (((int)blockIdx.x - bt.wg_begin[p]) * WAVES + wave) * rows_per_wave + lane / P;
     const int b = lane % P;
     const bool ok = row < n_out && b < nb;
-    // the lane's block, in flight while the activation row is copied
-    const uint8_t* src = ok ? W + (int64_t)row * nb * 144 + (int64_t)b * 144 : W;
+    if constexpr (LAYOUT == LAYOUT_X8) {
+        // the activation row streams into LDS first, with no registers held (codes column by
+        // column, 16 lanes per column to keep the bank skew; sums and scales contiguous), so the
+        // block's loads below queue behind it and the row is in place when they land
+        const ActLayout L0 = act_layout(ACT_Q8K, 1, (uint64_t)nb * 256);
+        const uint8_t* wsp = bt.ws[p];
+        const uint32_t l0 = lds_addr(lds);
+        const int wv = __builtin_amdgcn_readfirstlane(wave);
+        for (int c = wv; c < nb; c += WAVES)
+            if (lane < 16) lds_dma16(16u * (uint32_t)lane, wsp + L0.codes + (size_t)c * 256, l0 + (uint32_t)(c * COL));
+        if (wv == 0) {
+            for (int u = 0; u * 64 < nb * 2; ++u)
+                if (u * 64 + lane < nb * 2)
+                    lds_dma16(16u * (uint32_t)lane, wsp + L0.sums + (size_t)u * 1024, l0 + (uint32_t)(xs_off(nb) + u * 1024));
+            // the scales' last chunk reads up to 12 bytes past them: workspace padding, and LDS up
+            // to the fold terms (which start at the 16-byte-aligned end of the row)
+            if (lane * 4 < nb) lds_dma16(16u * (uint32_t)lane, wsp + L0.d, l0 + (uint32_t)xd_off(nb));
+        }
+    }
+    // the lane's block
     v4u A[9];
+    if constexpr (LAYOUT == LAYOUT_X8) {
+        const uint64_t nblocks = (uint64_t)n_out * (uint64_t)nb;
+        const uint64_t g = ok ? (uint64_t)row * nb + b : 0;
+        const uint8_t* src = W + x8_chunk_offset(g, 0, nblocks);
+        const uint32_t step = 16u * x8_group_blocks(g, nblocks);
 #pragma unroll
-    for (int i = 0; i < 9; ++i) A[i] = *reinterpret_cast<const v4u*>(src + 16 * i);
-    const ActLayout L = act_layout(ACT_Q8K, 1, (uint64_t)nb * 256);
-    copy_row_to_lds(reinterpret_cast<const int8_t*>(bt.ws[p] + L.codes),
-                    reinterpret_cast<const float*>(bt.ws[p] + L.d),
-                    reinterpret_cast<const int32_t*>(bt.ws[p] + L.sums), nb, lds);
-    __syncthreads();
+        for (int i = 0; i < 9; ++i) A[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(src + step * i));
+    } else {
+        const uint8_t* src = ok ? W + (int64_t)row * nb * 144 + (int64_t)b * 144 : W;
+#pragma unroll
+        for (int i = 0; i < 9; ++i) A[i] = *reinterpret_cast<const v4u*>(src + 16 * i);
+    }
+    if constexpr (LAYOUT == LAYOUT_X8) {
+        wait_vm<9>();  // this wavefront's row loads, all older than the block's nine
+        lds_barrier();
+    } else {
+        const ActLayout L = act_layout(ACT_Q8K, 1, (uint64_t)nb * 256);
+        copy_row_to_lds(reinterpret_cast<const int8_t*>(bt.ws[p] + L.codes),
+                        reinterpret_cast<const float*>(bt.ws[p] + L.d),
+                        reinterpret_cast<const int32_t*>(bt.ws[p] + L.sums), nb, lds);
+        __syncthreads();
+    }
     const float t = q4k_term_lds(A, lds, nb, ok ? b : 0);
     // in-order fold: the row's P terms (+0.0 past its nb blocks, which leaves a sum that
     // started from +0.0 unchanged) added by the row's first lane
@@ -344,8 +387,10 @@ void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* w
                   reinterpret_cast<const int32_t*>(ws + L.sums), y, stream);
 }
 
-void launch_gemv_q4k_batch(int np, const uint8_t* const* W, const int* n_out, const int* k,
-                           const uint8_t* const* ws, float* const* y, hipStream_t stream) {
+template <int LAYOUT>
+static void launch_batch(int np, const uint8_t* const* W, const int* n_out, const int* k,
+                         const uint8_t* const* ws, float* const* y, hipStream_t stream) {
+    constexpr int WAVES = dec_waves<LAYOUT>();
     DecBatch bt{};
     bt.np = np;
     int wg = 0, max_nb = 0;
@@ -357,15 +402,42 @@ void launch_gemv_q4k_batch(int np, const uint8_t* const* W, const int* n_out, co
         bt.nb[p] = k[p] / 256;
         bt.wg_begin[p] = wg;
         const int nb = bt.nb[p];
-        const int rows_per_wg = 4 * (64 / (nb <= 16 ? 16 : nb <= 32 ? 32 : 64));
+        const int rows_per_wg = WAVES * (64 / (nb <= 16 ? 16 : nb <= 32 ? 32 : 64));
         wg += (n_out[p] + rows_per_wg - 1) / rows_per_wg;
         if (nb > max_nb) max_nb = nb;
     }
     bt.wg_begin[np] = wg;
     if (wg == 0) return;
     // the activation row, then 64 fold terms per wavefront
-    hipLaunchKernelGGL(k_gemv_q4k_batch, dim3(wg), dim3(256), align_up(q4k_dec_lds(max_nb), 16) + 4 * 64 * 4,
-                       stream, bt);
+    hipLaunchKernelGGL(k_gemv_q4k_batch<LAYOUT>, dim3(wg), dim3(64 * WAVES),
+                       align_up(q4k_dec_lds(max_nb), 16) + WAVES * 64 * 4, stream, bt);
+}
+
+void launch_gemv_q4k_batch(int layout, int np, const uint8_t* const* W, const int* n_out, const int* k,
+                           const uint8_t* const* ws, float* const* y, hipStream_t stream) {
+    if (layout == LAYOUT_X8)
+        launch_batch<LAYOUT_X8>(np, W, n_out, k, ws, y, stream);
+    else
+        launch_batch<LAYOUT_SOURCE>(np, W, n_out, k, ws, y, stream);
+}
+
+// ---- the x8 repack: a permutation of whole 16-byte chunks --------------------------------------
+__global__ __launch_bounds__(256) void k_q4k_x8(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                uint64_t nblocks, int inverse) {
+    const uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;  // source chunk (GGUF order)
+    if (c >= nblocks * 9) return;
+    const uint64_t g = c / 9, q = c - g * 9;
+    const uint64_t to = x8_chunk_offset(g, (int)q, nblocks);
+    const uint64_t from = c * 16;
+    const v4u v = *reinterpret_cast<const v4u*>(src + (inverse ? to : from));
+    *reinterpret_cast<v4u*>(dst + (inverse ? from : to)) = v;
+}
+
+void launch_q4k_x8(const uint8_t* src, uint8_t* dst, uint64_t nblocks, int inverse, hipStream_t stream) {
+    const uint64_t chunks = nblocks * 9;
+    if (chunks == 0) return;
+    hipLaunchKernelGGL(k_q4k_x8, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, src, dst, nblocks,
+                       inverse);
 }
 
 }  // namespace syn

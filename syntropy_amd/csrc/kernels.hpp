@@ -22,8 +22,10 @@ void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* w
                             hipStream_t stream);
 // The most problems one grouped launch takes.
 #define SYN_BATCH 8
-void launch_gemv_q4k_batch(int np, const uint8_t* const* W, const int* n_out, const int* k,
+void launch_gemv_q4k_batch(int layout, int np, const uint8_t* const* W, const int* n_out, const int* k,
                            const uint8_t* const* ws, float* const* y, hipStream_t stream);
+// The X8 repack of a Q4_K matrix of nblocks super-blocks (inverse = 1: back to the GGUF order).
+void launch_q4k_x8(const uint8_t* src, uint8_t* dst, uint64_t nblocks, int inverse, hipStream_t stream);
 void launch_act_quant_batch(int np, const float* const* x, const int* k, uint8_t* const* ws,
                             hipStream_t stream);
 // moe.hip
@@ -70,7 +72,7 @@ size_t gemm_act_bytes(int64_t tpad, int k);
 GemmAct gemm_act_at(uint8_t* base, int64_t tpad, int k);
 void launch_gemm_act(const float* x, int T, int k, GemmAct a, hipStream_t stream);
 bool gemm_q4k_supported(int n_out, int k);
-void launch_gemm_q4k(const uint8_t* W, int n_out, int k, GemmAct a, int T, float* y, hipStream_t stream);
+void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, int T, float* y, hipStream_t stream);
 // quant.hip
 void launch_quantize(int ty, const float* x, uint64_t n, uint8_t* out, hipStream_t stream);
 void launch_dequantize(int ty, const uint8_t* src, uint64_t n, float* out, hipStream_t stream);

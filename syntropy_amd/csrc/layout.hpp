@@ -66,4 +66,21 @@ SYN_HD inline ActLayout act_layout(int kind, uint64_t rows, uint64_t k) {
     return l;
 }
 
+// Weight layouts of Q4_K matrices (the OpKey's LayoutVersion).
+//  0 SOURCE: the GGUF order, 144-byte super-blocks one after the other.
+//  1 X8: the same bytes with each run of eight consecutive super-blocks (1152 bytes) stored
+//    chunk-major: 16-byte chunk q of the run's block i at 128 q + 16 i.  A final run of m < 8
+//    blocks is stored the same way with stride 16 m.  Shape-free (a permutation of the matrix
+//    bytes), so a repack needs only the byte count.
+enum : int { LAYOUT_SOURCE = 0, LAYOUT_X8 = 1 };
+SYN_HD inline uint32_t x8_group_blocks(uint64_t g, uint64_t nblocks) {
+    const uint64_t first = g & ~(uint64_t)7;
+    return nblocks - first < 8 ? (uint32_t)(nblocks - first) : 8u;
+}
+// Byte offset of chunk q (0..8) of super-block g in an X8 matrix of nblocks blocks.
+SYN_HD inline uint64_t x8_chunk_offset(uint64_t g, int q, uint64_t nblocks) {
+    const uint64_t first = g & ~(uint64_t)7;
+    return first * 144 + 16 * ((uint64_t)q * x8_group_blocks(g, nblocks) + (g - first));
+}
+
 }  // namespace syn

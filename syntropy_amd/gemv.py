@@ -40,15 +40,20 @@ class GemvError(ValueError):
         self.kind = kind
 
 
+LAYOUT_SOURCE, LAYOUT_X8 = 0, 1
+
+
 @dataclass
 class Weights:
     """`n_out` rows of `k_in` weights of type `ty` in GGUF block layout, in device memory
-    (gemv.rs:157-224).  `bytes` is a uint8 device tensor holding exactly the matrix."""
+    (gemv.rs:157-224).  `bytes` is a uint8 device tensor holding exactly the matrix; `layout` is
+    LAYOUT_SOURCE (the GGUF order) or, for Q4_K, LAYOUT_X8 (see repack)."""
 
     ty: WeightType
     bytes: torch.Tensor
     n_out: int
     k_in: int
+    layout: int = LAYOUT_SOURCE
 
     def __post_init__(self):
         self.ty = WeightType(self.ty)
@@ -107,6 +112,17 @@ def gemv_quantized(w: Weights, ws: torch.Tensor, rows: int, y: torch.Tensor, str
          ws.data_ptr(), ws.numel(), rows, y.data_ptr(), _stream(stream))
 
 
+def repack(w: Weights, layout: int = LAYOUT_X8, stream=None) -> Weights:
+    """The matrix in another layout (a permutation of its bytes, crates/kernels/src/provider.rs:
+    326-336 repack): LAYOUT_X8 stores each run of eight Q4_K super-blocks chunk-major, so the
+    decode kernel reads whole 128-byte lines."""
+    if w.ty is not WeightType.Q4K or layout != LAYOUT_X8 or w.layout != LAYOUT_SOURCE:
+        raise GemvError("Activations", "repack takes Q4_K weights in the source layout to LAYOUT_X8")
+    out = torch.empty_like(w.bytes)
+    call("syn_q4k_repack", layout, w.bytes.data_ptr(), out.data_ptr(), w.bytes.numel(), 0, _stream(stream))
+    return Weights(w.ty, out, w.n_out, w.k_in, layout)
+
+
 def gemv(w: Weights, x: torch.Tensor, rows: int, y: torch.Tensor | None = None,
          ws: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """The Gemv op (gemv/entry.rs:167-247): quantize x F32 [rows, k_in], then
@@ -116,6 +132,14 @@ def gemv(w: Weights, x: torch.Tensor, rows: int, y: torch.Tensor | None = None,
         y = torch.empty(rows, w.n_out, dtype=torch.float32, device=x.device)
     elif y.numel() < rows * w.n_out:
         raise GemvError("Len", f"`y` holds {y.numel()} values, the op needs {rows * w.n_out}")
+    if w.layout != LAYOUT_SOURCE:
+        if ws is None:
+            need = C.c_uint64()
+            call("syn_gemv_layout_workspace_bytes", w.layout, int(w.ty), rows, w.k_in, C.byref(need))
+            ws = torch.empty(max(need.value, 256), dtype=torch.uint8, device=x.device)
+        call("syn_gemv_layout", w.layout, int(w.ty), w.bytes.data_ptr(), w.bytes.numel(), w.n_out, w.k_in,
+             x.data_ptr(), rows, y.data_ptr(), ws.data_ptr(), ws.numel(), _stream(stream))
+        return y
     if ws is None:
         ws = new_workspace(w.ty, rows, w.k_in, x.device)
     call("syn_gemv", int(w.ty), w.bytes.data_ptr(), w.bytes.numel(), w.n_out, w.k_in,
@@ -139,6 +163,10 @@ class GemvBatch:
             _check_x(x, 1, w.k_in)
             if y.numel() < w.n_out:
                 raise GemvError("Len", f"`y` holds {y.numel()} values, the op needs {w.n_out}")
+        layouts = {w.layout for w in weights}
+        if len(layouts) > 1:
+            raise GemvError("Activations", "GemvBatch takes weights of one layout")
+        self.layout = layouts.pop() if layouts else LAYOUT_SOURCE
         self.n = n
         u32 = C.c_uint32 * n
         self.k = u32(*[w.k_in for w in weights])
@@ -155,8 +183,8 @@ class GemvBatch:
         self._keep = (weights, xs, ys)
 
     def __call__(self, stream=None) -> None:
-        call("syn_gemv_batch", self.n, self.ty, self.w, self.wb, self.n_out, self.k, self.x,
-             self.y, self.ws.data_ptr(), self.ws.numel(), _stream(stream))
+        call("syn_gemv_batch_layout", self.layout, self.n, self.ty, self.w, self.wb, self.n_out, self.k,
+             self.x, self.y, self.ws.data_ptr(), self.ws.numel(), _stream(stream))
 
     def quantize(self, stream=None) -> None:
         """The first half of __call__: every x[i] to Q8_K in the held workspace."""
@@ -165,8 +193,8 @@ class GemvBatch:
 
     def gemv_quantized(self, stream=None) -> None:
         """The second half: every y[i] from the workspace quantize() filled."""
-        call("syn_gemv_batch_quantized", self.n, self.ty, self.w, self.wb, self.n_out, self.k,
-             self.ws.data_ptr(), self.ws.numel(), self.y, _stream(stream))
+        call("syn_gemv_batch_quantized_layout", self.layout, self.n, self.ty, self.w, self.wb, self.n_out,
+             self.k, self.ws.data_ptr(), self.ws.numel(), self.y, _stream(stream))
 
 
 def gemm_workspace(rows: int, k: int, device="cuda") -> torch.Tensor:
@@ -218,5 +246,6 @@ def dequantize(ty: WeightType, src: torch.Tensor, stream=None) -> torch.Tensor:
 
 
 __all__ = ["WeightType", "Weights", "GemvError", "SynError", "GemvBatch", "workspace_bytes", "quantize_into",
+           "repack", "LAYOUT_SOURCE", "LAYOUT_X8",
            "gemv_quantized", "gemv", "quantize", "dequantize", "new_workspace", "gemm_workspace",
            "gemm_quantize_into", "gemm_quantized", "lib"]

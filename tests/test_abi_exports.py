@@ -67,3 +67,27 @@ def test_version_and_errors_without_a_gpu():
     assert lib.syn_gemv_workspace_bytes(12, 1, 4096, ctypes.byref(out)) == 0
     assert out.value >= 4096 + 16 * 4 + 128 * 4
     assert lib.syn_gemv_workspace_bytes(7, 1, 4096, ctypes.byref(out)) == 2
+
+
+def test_x8_host_repack_is_its_definition_and_inverts():
+    """The host repack of the X8 layout against its definition (chunk q of block i of a run of m
+    at 16 (q m + i)), and the inverse; no device involved."""
+    import numpy as np
+    import torch  # noqa: F401
+    lib = ctypes.CDLL(LIB)
+    lib.syn_q4k_repack_host.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                        ctypes.c_int32]
+    for nblk in (1, 7, 8, 9, 21, 64):
+        b = np.random.default_rng(nblk).integers(0, 256, nblk * 144, dtype=np.uint8)
+        want = np.empty_like(b)
+        for g0 in range(0, nblk, 8):
+            m = min(8, nblk - g0)
+            want[g0 * 144:(g0 + m) * 144] = b[g0 * 144:(g0 + m) * 144].reshape(m, 9, 16).transpose(1, 0, 2).ravel()
+        got = np.empty_like(b)
+        assert lib.syn_q4k_repack_host(1, b.ctypes.data, got.ctypes.data, b.size, 0) == 0
+        assert (got == want).all()
+        back = np.empty_like(b)
+        assert lib.syn_q4k_repack_host(1, got.ctypes.data, back.ctypes.data, b.size, 1) == 0
+        assert (back == b).all()
+    assert lib.syn_q4k_repack_host(2, b.ctypes.data, got.ctypes.data, b.size, 0) == 2
+    assert lib.syn_q4k_repack_host(1, b.ctypes.data, got.ctypes.data, 100, 0) == 1

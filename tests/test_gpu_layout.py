@@ -1,0 +1,94 @@
+"""The X8 weight layout (each run of eight Q4_K super-blocks stored chunk-major): the device and
+host repacks agree with the definition and invert exactly, and the decode kernel and the GEMM
+over repacked weights give the source layout's outputs bit for bit (the oracle's values)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce, assert_same, dev, host, require_gpu
+from oracle import oracle as o
+from test_gpu_gemm import random_q4k
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def S():
+    require_gpu()
+    import syntropy_amd.gemv as S
+    return S
+
+
+def x8_numpy(b: np.ndarray) -> np.ndarray:
+    """The layout's definition on host bytes: chunk q of block i of a run of m at 16 (q m + i)."""
+    nblk = b.size // 144
+    out = np.empty_like(b)
+    for g0 in range(0, nblk, 8):
+        m = min(8, nblk - g0)
+        run = b[g0 * 144:(g0 + m) * 144].reshape(m, 9, 16)
+        out[g0 * 144:(g0 + m) * 144] = run.transpose(1, 0, 2).reshape(-1)
+    return out
+
+
+@pytest.mark.parametrize("nblk", [8, 16, 13, 1, 7, 8 * 57 + 5])
+def test_repack_matches_definition_and_inverts(S, nblk):
+    rs = np.random.default_rng(nblk)
+    b = rs.integers(0, 256, nblk * 144, dtype=np.uint8)
+    W = S.Weights(S.WeightType.Q4K, dev(b), nblk, 256)
+    announce(f"x8 repack {nblk} blocks")
+    r = S.repack(W)
+    got = host(r.bytes)
+    assert (got == x8_numpy(b)).all()
+    back = torch.empty_like(r.bytes)
+    S.lib().syn_q4k_repack(1, r.bytes.data_ptr(), back.data_ptr(), r.bytes.numel(), 1, None)
+    assert (host(back) == b).all()
+    h = np.empty_like(b)
+    assert S.lib().syn_q4k_repack_host(1, b.ctypes.data, h.ctypes.data, b.size, 0) == 0
+    assert (h == got).all()
+
+
+@pytest.mark.parametrize("n_out,k", [(256, 4096), (96, 14336), (37, 3072), (50, 1536), (9, 16384), (5, 256)])
+def test_decode_x8_equals_oracle(S, n_out, k):
+    rs = np.random.default_rng(n_out + k)
+    w = random_q4k(rs, n_out, k)
+    x = o.normal(0xD0 + k, 1.0, k)
+    W = S.repack(S.Weights(S.WeightType.Q4K, dev(w), n_out, k))
+    announce(f"decode x8 {n_out}x{k}")
+    got = host(S.gemv(W, dev(x), 1))
+    assert_same(got, o.gemv(o.Q4_K, w, n_out, k, x, 1, threads=8), "x8 decode")
+
+
+def test_batch_x8_equals_source_layout(S):
+    shapes = [(6144, 4096), (4096, 4096), (1000, 14336), (37, 3072), (256, 1536)]
+    rs = np.random.default_rng(3)
+    Ws, Xs, Y0, Y1, W8 = [], [], [], [], []
+    for n, k in shapes:
+        w = S.Weights(S.WeightType.Q4K, dev(random_q4k(rs, n, k)), n, k)
+        Ws.append(w)
+        W8.append(S.repack(w))
+        Xs.append(dev(o.normal(n + k, 1.0, k)))
+        Y0.append(torch.empty(n, device="cuda"))
+        Y1.append(torch.full((n,), float("nan"), device="cuda"))
+    announce("batch x8 vs source")
+    S.GemvBatch(Ws, Xs, Y0)()
+    S.GemvBatch(W8, Xs, Y1)()
+    for a, b in zip(Y0, Y1):
+        assert_same(host(b), host(a), "x8 batch")
+
+
+@pytest.mark.parametrize("rows,n_out,k", [(2, 64, 2048), (64, 300, 4096), (100, 256, 14336)])
+def test_gemm_x8_equals_oracle(S, rows, n_out, k):
+    rs = np.random.default_rng(rows + n_out + k)
+    w = random_q4k(rs, n_out, k)
+    x = o.normal(0xE0 + rows, 1.0, rows * k).reshape(rows, k)
+    W = S.repack(S.Weights(S.WeightType.Q4K, dev(w), n_out, k))
+    announce(f"gemm x8 rows={rows} {n_out}x{k}")
+    got = host(S.gemv(W, dev(x), rows))
+    assert_same(got, o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=8), "x8 gemm")
+
+
+def test_x8_refusals(S):
+    W = S.repack(S.Weights(S.WeightType.Q4K, torch.zeros(64 * 6 * 144, dtype=torch.uint8, device="cuda"), 64, 1536))
+    x = torch.zeros(4, 1536, device="cuda")
+    with pytest.raises(S.SynError):  # the GEMM takes rows of whole 8-block runs only
+        S.gemv(W, x, 4)
