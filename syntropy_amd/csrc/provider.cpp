@@ -327,6 +327,7 @@ struct Plan {
     uint64_t workspace = 0;  // bytes the executor provides (incl. 256 of alignment slack)
     uint32_t max_block = 0;
     uint32_t act_in = 0;  // NumericsWire codes: 0 none, 2 Q8Block32, 3 Q8K256
+    uint32_t layout = 0;  // the weights' LayoutVersion
 };
 
 uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
@@ -336,15 +337,18 @@ uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 // moe/entry.rs:33-56); MoeRoute and MoeCombine their IR signatures
 // (crates/graph/src/ir/signature.rs:149,153).
 bool plan_of(const Key& k, const Shape& s, Plan& p) {
-    if (k.layout != 0 || k.variant != 0 || !k.rest_plain_f32) return false;
+    if (k.variant != 0 || !k.rest_plain_f32) return false;
+    // layout 1 (X8, from repack) is served for Q4_K Gemv weights only
+    if (k.layout != 0 && !(k.layout == SYN_LAYOUT_X8 && k.op == Op::Gemv && k.weight == SYN_Q4_K)) return false;
     p.op = k.op;
     p.rows = s.rows;
+    p.layout = k.layout;
     switch (k.op) {
     case Op::Gemv: {
         if (k.weight < 0 || k.n_schemes < 1 || k.n_schemes > 3 || s.dims.size() != 2) return false;
         const uint32_t n_out = s.dims[0], k_in = s.dims[1];
         uint64_t ws = 0;
-        if (syn_gemv_workspace_bytes(k.weight, s.rows, k_in, &ws) != SYN_OK) return false;
+        if (syn_gemv_layout_workspace_bytes(k.layout, k.weight, s.rows, k_in, &ws) != SYN_OK) return false;
         p.weight = k.weight;
         p.dims[0] = n_out;
         p.dims[1] = k_in;
@@ -403,14 +407,15 @@ std::string caps_json(const Plan& p) {
                   "{\"accumulate\":%u,\"max_block\":%u,\"act_in\":%u,\"group\":0,\"out\":0,"
                   "\"softmax_f32\":%s,\"state_f32\":false}",
                   route || combine ? 0u : 1u, p.max_block, p.act_in, route ? "true" : "false");
-    return std::string("{\"workspace\":") + std::to_string(p.workspace) +
-           ",\"est\":null,\"layout\":0,\"capture_safe\":true,\"deterministic\":true,\"numerics\":" + num +
+    return std::string("{\"workspace\":") + std::to_string(p.workspace) + ",\"est\":null,\"layout\":" +
+           std::to_string(p.layout) + ",\"capture_safe\":true,\"deterministic\":true,\"numerics\":" + num +
            ",\"kernel_hash\":" + zeros + ",\"source_key\":" + zeros + "}";
 }
 
 const char* OPS_JSON =
     "["
     "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q4_K\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
+    "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q4_K\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":1,\"variant\":0},"
     "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q8_0\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
     "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q4_0\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
     "{\"op\":\"MoeGrouped\",\"schemes\":[{\"Ggml\":\"Q4_K\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
@@ -516,8 +521,8 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         const uint64_t wbytes = (uint64_t)k_in / be * bb * n_out;
         const SynBufferView& w = weight(a, 0, wbytes, "Gemv");
         uint8_t* ws = workspace_of(c, a, p);
-        check_syn(syn_gemv(p.weight, (const void*)w.addr, wbytes, n_out, k_in, (const float*)x, rows,
-                           (float*)y, ws, p.workspace - 256, st),
+        check_syn(syn_gemv_layout(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in, (const float*)x,
+                                  rows, (float*)y, ws, p.workspace - 256, st),
                   "Gemv");
         return;
     }
@@ -725,18 +730,32 @@ SynStatus e_set_resident(void*, uint64_t ctx, const SynBuffer*, size_t, uint32_t
     return call("set_resident", false, [&] { ctx_of(ctx); });
 }
 
-// Weights stay in their GGUF layout (LayoutVersion SOURCE): nothing to repack.
-SynStatus e_repack(void*, const uint8_t*, size_t, const uint8_t*, size_t, uint8_t*, size_t,
-                   uint32_t* present, uint32_t* layout) {
+// Gemv's Q4_K weights are repacked to layout 1 (X8: each run of eight super-blocks stored
+// chunk-major, a permutation of the bytes, so the same length); every other op's weights keep
+// their GGUF layout (LayoutVersion SOURCE, `present` 0).
+bool repacks(const uint8_t* op, size_t op_len) {
+    const Key k = parse_key(op, op_len);
+    return k.op == Op::Gemv && k.weight == SYN_Q4_K && k.layout == 0;
+}
+SynStatus e_repack(void*, const uint8_t* op, size_t op_len, const uint8_t* src, size_t src_len, uint8_t* dst,
+                   size_t dst_len, uint32_t* present, uint32_t* layout) {
     return call("repack", false, [&] {
-        if (present) *present = 0;
-        if (layout) *layout = 0;
+        if (!present || !layout) internal("repack: null output");
+        *present = 0;
+        *layout = 0;
+        if (!repacks(op, op_len)) return;
+        if (src_len % 144) fail(SYN_CLASS_INVALID_REQUEST, 0, "repack: the bytes are not whole Q4_K super-blocks");
+        if (dst_len < src_len) fail(SYN_CLASS_INVALID_REQUEST, 0, "repack: the destination is shorter than the source");
+        check_syn(syn_q4k_repack_host(SYN_LAYOUT_X8, src, dst, src_len, 0), "repack");
+        *present = 1;
+        *layout = SYN_LAYOUT_X8;
     });
 }
-SynStatus e_repacked_len(void*, const uint8_t*, size_t, uint64_t, uint32_t* present, uint64_t* out) {
+SynStatus e_repacked_len(void*, const uint8_t* op, size_t op_len, uint64_t src, uint32_t* present, uint64_t* out) {
     return call("repacked_len", false, [&] {
-        if (present) *present = 0;
-        if (out) *out = 0;
+        if (!present || !out) internal("repacked_len: null output");
+        *present = repacks(op, op_len) ? 1 : 0;
+        *out = *present ? src : 0;
     });
 }
 

@@ -6,6 +6,7 @@ The sequence is kernels_loader::ModuleProvider's (crates/kernels-loader/src/prov
 argument binding is the executor's (crates/kernels/src/op/args.rs:85-96: packed tensors, weight
 views, the workspace slice)."""
 import ctypes as C
+import json
 
 import numpy as np
 import pytest
@@ -106,12 +107,44 @@ def test_gemv_through_the_provider(cx, ty, rows, n_out, k):
     assert_same(got, o.gemv(ty, w, n_out, k, x, rows, threads=8), "provider gemv")
 
 
+@pytest.mark.parametrize("rows,n_out,k", [(1, 4096, 4096), (1, 1000, 14336), (64, 256, 4096)])
+def test_gemv_x8_layout_through_the_provider(cx, rows, n_out, k):
+    """The core's path for repacked weights: repacked_len / repack on the host bytes, then the
+    Gemv key with the layout repack returned; outputs equal the oracle on the source bytes."""
+    P, pr = cx.P, cx.pr
+    rng = GemvRng(rows * 7 + n_out)
+    w = gemv_weights(rng, o.Q4_K, n_out, k, o.f16_bits, o.round_bf16)
+    x = gemv_activations(rng, rows, k)
+    src_key = gemv_key(o.Q4_K)
+    kb = json.dumps(src_key).encode()
+    kbuf = (C.c_uint8 * len(kb)).from_buffer_copy(kb)
+    present, layout = C.c_uint32(), C.c_uint32()
+    dst = np.zeros_like(w)
+    st = pr.vt.repack(pr.vt.slf, kbuf, len(kb), w.ctypes.data_as(C.POINTER(C.c_uint8)), w.size,
+                      dst.ctypes.data_as(C.POINTER(C.c_uint8)), dst.size, C.byref(present), C.byref(layout))
+    assert st.cls == 0 and (present.value, layout.value) == (1, 1)
+    key = dict(src_key, layout=layout.value)
+    announce(f"provider gemv x8 rows={rows} n_out={n_out} k={k}")
+    caps = pr.query(cx.ctx, key, shape(rows, n_out, k))
+    assert caps is not None and caps["layout"] == 1
+    op = pr.prepare(cx.ctx, key, shape(rows, n_out, k))
+    wd = dev(dst)
+    xb, yb = cx.put(x.astype(np.float32)), cx.empty(4 * rows * n_out)
+    args = P.op_args([P.packed(xb, P.DT_F32, [rows, k])], [P.packed(yb, P.DT_F32, [rows, n_out])],
+                     [P.view(wd.data_ptr(), dst.nbytes)], cx.workspace(op))
+    pr.launch(cx.ctx, cx.s, op, args)
+    got = cx.get(yb, np.float32, (rows, n_out))
+    assert_same(got, o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=8), "provider gemv x8")
+
+
 def test_query_answers_none_for_unserved_shapes(cx):
     pr = cx.pr
     assert pr.query(cx.ctx, gemv_key(o.Q4_K), shape(1, 64, 100)) is None  # k not whole super-blocks
     key = dict(gemv_key(o.Q4_K), schemes=[{"Ggml": "Q6_K"}, {"Plain": "F32"}, {"Plain": "F32"}])
     assert pr.query(cx.ctx, key, shape(1, 64, 256)) is None
     assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=3), shape(1, 64, 256)) is None
+    assert pr.query(cx.ctx, dict(gemv_key(o.Q8_0), layout=1), shape(1, 64, 256)) is None
+    assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(8, 64, 1536)) is None  # GEMM: k % 2048
     assert pr.query(cx.ctx, {"op": "Attention", "schemes": [], "layout": 0, "variant": 0},
                     shape(1, 64, 256)) is None
     with pytest.raises(cx.P.ProviderError) as e:

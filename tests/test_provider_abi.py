@@ -92,11 +92,12 @@ def test_build_and_ops_json(pr):
     b = pr.build()
     assert b["version"] == 1 and ["target", "gfx950"] in b["toolchain"]
     ops = pr.ops()
-    got = {(json.dumps(k["op"]), k["schemes"][0].get("Ggml")) for k in ops}
-    assert got == {('"Gemv"', "Q4_K"), ('"Gemv"', "Q8_0"), ('"Gemv"', "Q4_0"), ('"MoeGrouped"', "Q4_K"),
-                   ('{"MoeRoute": {"norm": "Softmax"}}', None), ('"MoeCombine"', None)}
+    got = {(json.dumps(k["op"]), k["schemes"][0].get("Ggml"), k["layout"]) for k in ops}
+    assert got == {('"Gemv"', "Q4_K", 0), ('"Gemv"', "Q4_K", 1), ('"Gemv"', "Q8_0", 0), ('"Gemv"', "Q4_0", 0),
+                   ('"MoeGrouped"', "Q4_K", 0), ('{"MoeRoute": {"norm": "Softmax"}}', None, 0),
+                   ('"MoeCombine"', None, 0)}
     for k in ops:
-        assert k["layout"] == 0 and k["variant"] == 0
+        assert k["variant"] == 0
 
 
 def test_outbuf_retry_protocol(pr):
@@ -125,12 +126,39 @@ def test_unserved_entries_are_unsupported(pr):
         assert name in pr.message(), name
 
 
-def test_repack_reports_no_repacked_layout(pr):
+def _key(op, weight, layout=0):
+    schemes = ([{"Ggml": weight}] if weight else []) + [{"Plain": "F32"}, {"Plain": "F32"}]
+    return json.dumps({"op": op, "schemes": schemes, "layout": layout, "variant": 0}).encode()
+
+
+def test_repack_of_q4k_gemv_is_the_x8_permutation(pr):
+    """Gemv's Q4_K weights repack to layout 1 (each run of eight super-blocks chunk-major, the
+    same length); every other op keeps the source layout (provider.rs:326-336)."""
+    import numpy as np
+    nblk = 21
+    src = np.random.default_rng(1).integers(0, 256, nblk * 144, dtype=np.uint8)
+    want = np.empty_like(src)
+    for g0 in range(0, nblk, 8):
+        m = min(8, nblk - g0)
+        want[g0 * 144:(g0 + m) * 144] = src[g0 * 144:(g0 + m) * 144].reshape(m, 9, 16).transpose(1, 0, 2).ravel()
     present, layout, n = C.c_uint32(7), C.c_uint32(7), C.c_uint64(7)
-    assert pr.vt.repack(pr.vt.slf, None, 0, None, 0, None, 0, C.byref(present), C.byref(layout)).cls == 0
-    assert (present.value, layout.value) == (0, 0)
-    assert pr.vt.repacked_len(pr.vt.slf, None, 0, 4096, C.byref(present), C.byref(n)).cls == 0
-    assert (present.value, n.value) == (0, 0)
+    key = _key("Gemv", "Q4_K")
+    kb = (C.c_uint8 * len(key)).from_buffer_copy(key)
+    assert pr.vt.repacked_len(pr.vt.slf, kb, len(key), src.size, C.byref(present), C.byref(n)).cls == 0
+    assert (present.value, n.value) == (1, src.size)
+    dst = np.zeros_like(src)
+    sp, dp = src.ctypes.data_as(C.POINTER(C.c_uint8)), dst.ctypes.data_as(C.POINTER(C.c_uint8))
+    assert pr.vt.repack(pr.vt.slf, kb, len(key), sp, src.size, dp, dst.size, C.byref(present), C.byref(layout)).cls == 0
+    assert (present.value, layout.value) == (1, 1)
+    assert (dst == want).all()
+    for other in (_key("Gemv", "Q8_0"), _key("MoeGrouped", "Q4_K"), _key("MoeCombine", None)):
+        ob = (C.c_uint8 * len(other)).from_buffer_copy(other)
+        assert pr.vt.repacked_len(pr.vt.slf, ob, len(other), 144, C.byref(present), C.byref(n)).cls == 0
+        assert (present.value, n.value) == (0, 0)
+        assert pr.vt.repack(pr.vt.slf, ob, len(other), sp, 144, dp, 144, C.byref(present), C.byref(layout)).cls == 0
+        assert (present.value, layout.value) == (0, 0)
+    bad = pr.vt.repack(pr.vt.slf, kb, len(key), sp, 100, dp, 100, C.byref(present), C.byref(layout))
+    assert bad.cls == 1 and "super-blocks" in pr.message()
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the behaviour on a host without a GPU")
