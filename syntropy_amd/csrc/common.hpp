@@ -249,4 +249,12 @@ SYN_DEV void lds_dma16(uint32_t voff, const void* sbase, uint32_t lds) {
                  : "memory");
 }
 
+// 4 bytes per active lane from sbase + voff to LDS address lds + 4 * lane (as lds_dma16).
+SYN_DEV void lds_dma4(uint32_t voff, const void* sbase, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "memory");
+}
+
 }  // namespace syn

@@ -35,94 +35,192 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // MoeRoute{Softmax}
 // ============================================================================================
 
-// Logits: one workgroup per (TT tokens, EC experts).  The block sums of the chunk go to LDS,
-// then the pairwise tree runs level by level in LDS (ping-pong), exactly as reduce.rs defines.
-// EC (at most 32) is sized so the tokens' rows and the sums fit 64 KB of LDS.
+// Logits: one workgroup per (RT_T tokens, RT_E experts), walking the hidden dimension in
+// chunks of RT_CB blocks of 32 values, double-buffered in LDS.  Each chunk of the tokens' rows and
+// the experts' router rows is copied into LDS by global_load_lds_dwordx4 (every wavefront load
+// reads whole 128-byte lines) while the previous chunk is computed; the 16-byte chunk q of
+// block b sits at position 8 b + (q ^ (b & 7)), so the lanes reading one chunk of their blocks
+// hit distinct banks.  Lane (b, token pair) of wavefront w computes the 32-term block sums of
+// experts 2w, 2w + 1 against tokens 2p, 2p + 1 (router and token blocks in registers); the block
+// sums go to LDS.
+//
+// The pairwise tree of reduce.rs, level by level over n values (a pair at each level, an odd
+// last value carried up), restricted to an aligned run of 2^m values is the same tree over that
+// run alone: at level L, value i covers [i 2^L, (i + 1) 2^L) clipped to n, and the run's
+// boundaries are multiples of 2^L.  So each of a pair's 8 threads folds its own run of the block
+// sums in registers, and one thread folds the 8 run results.
+constexpr int RT_T = 4, RT_E = 8, RT_PAIRS = RT_T * RT_E, RT_CB = 32;
+constexpr int RT_ROW = RT_CB * 128;                    // bytes of one row's chunk: 4 KB
+constexpr int RT_STAGE = (RT_T + RT_E) * RT_ROW;       // 48 KB; two stages
+constexpr int RT_MAXB = 256;                           // blocks per row: hidden <= 8192
 
-template <int TT>
-__global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ router,
-                                                    const float* __restrict__ x, int rows,
-                                                    int hidden, int n_experts, int EC,
-                                                    float* __restrict__ logits) {
-    extern __shared__ __attribute__((aligned(16))) float sm[];
-    const int tid = threadIdx.x;
-    const int t0 = blockIdx.x * TT;
-    const int e0 = blockIdx.y * EC;
-    const int ec = n_experts - e0 < EC ? n_experts - e0 : EC;
-    const int nblk = hidden / 32;
-    float* xs = sm;                              // [TT][hidden]
-    float* S0 = xs + TT * hidden;  // [TT][EC][nblk]
-    float* S1 = S0 + TT * EC * nblk;  // [TT][EC][nblk]
-    for (int i = tid; i < TT * hidden; i += 256) {
-        const int t = i / hidden, c = i - t * hidden;
-        xs[i] = (t0 + t < rows) ? x[(int64_t)(t0 + t) * hidden + c] : 0.0f;
-    }
-    __syncthreads();
-    for (int p = tid; p < ec * nblk; p += 256) {
-        const int e = p / nblk, b = p - e * nblk;
-        const float4* wr = reinterpret_cast<const float4*>(router + (int64_t)(e0 + e) * hidden + b * 32);
-        float wv[32];
+SYN_DEV float4 rt_chunk(const uint8_t* row, int b, int q) {
+    return *reinterpret_cast<const float4*>(row + 16 * (8 * b + (q ^ (b & 7))));
+}
+
+// The pairwise tree over v[0..n) (n <= N), in place; the result in v[0].
+template <int N>
+SYN_DEV float tree_fold(float (&v)[N], int n) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float4 f = wr[q];
-            wv[4 * q] = f.x;
-            wv[4 * q + 1] = f.y;
-            wv[4 * q + 2] = f.z;
-            wv[4 * q + 3] = f.w;
-        }
+    for (int len = N; len > 1; len = (len + 1) >> 1) {
+        // one level for every n in (len / 2, len]: the level's n is len' = min(n, len)
+        const int m = n < len ? n : len;
 #pragma unroll
-        for (int t = 0; t < TT; ++t) {
-            const float* xb = xs + t * hidden + b * 32;
-            float acc = 0.0f;
+        for (int i = 0; i < (len + 1) / 2; ++i)
+            if (i < (m + 1) / 2) v[i] = (2 * i + 1 < m) ? v[2 * i] + v[2 * i + 1] : v[2 * i];
+        n = (m + 1) / 2;
+    }
+    return v[0];
+}
+
+// Wavefront w issues, for chunk c0, row i of the stage (tokens 0-3, then experts 0-7), blocks
+// 8w .. 8w + 7: one 16-byte load a lane (token rows not 16-byte aligned: four 4-byte loads).
+template <bool X16>
+SYN_DEV void rt_issue(const float* x, const float* router, int rows, int hidden, int n_experts,
+                      int t0, int e0, int c0, int nblk, int wave, int lane, uint8_t* stage) {
 #pragma unroll
-            for (int i = 0; i < 32; ++i) acc = acc + wv[i] * xb[i];
-            S0[(t * EC + e) * nblk + b] = acc;
+    for (int r = 0; r < RT_T + RT_E; ++r) {
+        const uint32_t dst = lds_addr(stage + r * RT_ROW + 1024 * wave);
+        const float* base;
+        if (r < RT_T) {
+            const int t = t0 + r < rows ? t0 + r : rows - 1;
+            base = x + (int64_t)t * hidden;
+        } else {
+            const int e = e0 + r - RT_T < n_experts ? e0 + r - RT_T : n_experts - 1;
+            base = router + (int64_t)e * hidden;
         }
-    }
-    __syncthreads();
-    float* src = S0;
-    float* dst = S1;
-    for (int n = nblk; n > 1; n = (n + 1) >> 1) {
-        const int half = (n + 1) >> 1;
-        for (int p = tid; p < TT * ec * half; p += 256) {
-            const int te = p / half, i = p - te * half;
-            const int t = te / ec, e = te - t * ec;
-            const float* sp = src + (t * EC + e) * nblk;
-            dst[(t * EC + e) * nblk + i] = (2 * i + 1 < n) ? sp[2 * i] + sp[2 * i + 1] : sp[2 * i];
+        if (X16 || r >= RT_T) {
+            const int bq = 64 * wave + lane, bl = bq >> 3, q = (bq & 7) ^ (bl & 7);
+            const int b = c0 + bl < nblk ? c0 + bl : nblk - 1;  // past the row: a valid block, unused
+            lds_dma16((uint32_t)(b * 128 + 16 * q), base, dst);
+        } else {
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const int bq = 64 * wave + 16 * s4 + (lane >> 2), bl = bq >> 3, q = (bq & 7) ^ (bl & 7);
+                const int b = c0 + bl < nblk ? c0 + bl : nblk - 1;
+                lds_dma4((uint32_t)(b * 128 + 16 * q + 4 * (lane & 3)), base, dst + 256 * s4);
+            }
         }
-        __syncthreads();
-        float* tmp = src;
-        src = dst;
-        dst = tmp;
-    }
-    for (int p = tid; p < TT * ec; p += 256) {
-        const int t = p / ec, e = p - t * ec;
-        if (t0 + t < rows) logits[(int64_t)(t0 + t) * n_experts + e0 + e] = src[(t * EC + e) * nblk];
     }
 }
 
-// Softmax and top-k: one wavefront per token (E <= 256, 4 experts per lane).
+template <bool X16>  // token rows 16-byte aligned (else they are copied 4 bytes a lane)
+__global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ router,
+                                                    const float* __restrict__ x, int rows,
+                                                    int hidden, int n_experts,
+                                                    float* __restrict__ logits) {
+    constexpr int LOADS = X16 ? RT_T + RT_E : 4 * RT_T + RT_E;  // loads per chunk per wavefront
+    extern __shared__ __attribute__((aligned(16))) uint8_t rt_lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.x * RT_T, e0 = blockIdx.y * RT_E;
+    const int nblk = hidden / 32;
+    float* S0 = reinterpret_cast<float*>(rt_lds + 2 * RT_STAGE);  // [RT_PAIRS][nblk]
+    rt_issue<X16>(x, router, rows, hidden, n_experts, t0, e0, 0, nblk, wave, lane, rt_lds);
+    const int bl = lane & 31, tp = lane >> 5;
+    for (int c0 = 0, cur = 0; c0 < nblk; c0 += RT_CB, cur ^= 1) {
+        if (c0 + RT_CB < nblk) {
+            rt_issue<X16>(x, router, rows, hidden, n_experts, t0, e0, c0 + RT_CB, nblk, wave, lane,
+                          rt_lds + (cur ^ 1) * RT_STAGE);
+            wait_vm<LOADS>();
+        } else {
+            wait_vm<0>();
+        }
+        lds_barrier();
+        const uint8_t* st = rt_lds + cur * RT_STAGE;
+        const int b = c0 + bl;
+        if (b < nblk) {
+            float xv[2][32], wv[2][32];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const float4 f = rt_chunk(st + (2 * tp + j) * RT_ROW, bl, q);
+                    const float4 g = rt_chunk(st + (RT_T + 2 * wave + j) * RT_ROW, bl, q);
+                    xv[j][4 * q] = f.x;
+                    xv[j][4 * q + 1] = f.y;
+                    xv[j][4 * q + 2] = f.z;
+                    xv[j][4 * q + 3] = f.w;
+                    wv[j][4 * q] = g.x;
+                    wv[j][4 * q + 1] = g.y;
+                    wv[j][4 * q + 2] = g.z;
+                    wv[j][4 * q + 3] = g.w;
+                }
+#pragma unroll
+            for (int je = 0; je < 2; ++je)
+#pragma unroll
+                for (int jt = 0; jt < 2; ++jt) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) acc = acc + wv[je][i] * xv[jt][i];
+                    S0[((2 * tp + jt) * RT_E + 2 * wave + je) * nblk + b] = acc;
+                }
+        }
+        lds_barrier();  // this stage is refilled two chunks on
+    }
+    // the tree: pair pr = tid / 8; thread sub = tid % 8 folds blocks [sub * cs, sub * cs + cs)
+    const int pr = tid >> 3, sub = tid & 7;
+    int cs = 1;
+    while (cs * 8 < nblk) cs <<= 1;  // <= 32
+    const int start = sub * cs;
+    const int cnt = nblk - start < 0 ? 0 : (nblk - start < cs ? nblk - start : cs);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = i < cnt ? S0[pr * nblk + start + i] : 0.0f;
+    const float run = tree_fold<32>(v, cnt);
+    float r8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r8[i] = __shfl(run, (lane & ~7) + i);
+    const int nrun = (nblk + cs - 1) / cs;
+    const float total = tree_fold<8>(r8, nrun);
+    if (sub == 0) {
+        const int t = pr / RT_E, e = pr - t * RT_E;
+        if (t0 + t < rows && e0 + e < n_experts) logits[(int64_t)(t0 + t) * n_experts + e0 + e] = total;
+    }
+}
+
+// Softmax and top-k: one wavefront per token (E <= 256, 4 experts per lane).  The selection
+// ranks every expert by (probability descending, index ascending), a NaN after every number
+// (the spec's order; with a NaN anywhere in a row every probability is NaN and the ranks are the
+// indices, as a first-best scan gives).  The order is that of one 64-bit key per expert:
+// (NaN ? 0 : |p| bits + 1) << 8 | (255 - e).  Probabilities are exp(.) / sum, never negative, so
+// the magnitude bits order them as the float comparison does.
+SYN_DEV uint64_t rank_key(float p, int e) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, p) & 0x7FFFFFFFu;
+    const uint64_t k = p != p ? 0ull : (uint64_t)b + 1ull;
+    return (k << 8) | (uint64_t)(255 - e);
+}
+
+template <int NQ>  // experts per lane: E <= 64 NQ
 __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logits, int rows,
                                                   int n_experts, int top_k, int renorm,
                                                   int32_t* __restrict__ ids,
                                                   float* __restrict__ wout,
                                                   float* __restrict__ probs_out) {
-    __shared__ float sp[4][256];
+    __shared__ __attribute__((aligned(16))) float sp[4][256];
+    __shared__ __attribute__((aligned(16))) uint64_t keys[4][256];
+    __shared__ __attribute__((aligned(16))) float selv[4][32];
+    __shared__ int seli[4][32];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wave;
     if (t >= rows) return;
     float* lg = sp[wave];
     const float* src = logits + (int64_t)t * n_experts;
-    float m = -__builtin_inff();
+    // the row maximum as a first-best scan finds it: logit 0, then any strictly larger one
+    float m = -__builtin_inff(), l0 = 0.0f;
     for (int e = lane; e < n_experts; e += 64) {
-        lg[e] = src[e];
-        m = lg[e] > m ? lg[e] : m;
+        const float v = src[e];
+        lg[e] = v;
+        l0 = e == 0 ? v : l0;
+        m = v > m ? v : m;
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         const float o = __shfl_xor(m, off);
         m = o > m ? o : m;
     }
+    l0 = __shfl(l0, 0);
+    if (l0 != l0) m = l0;
     for (int e = lane; e < n_experts; e += 64) lg[e] = ref_exp(lg[e] - m);
     wave_lds_sync();
     // F32Fixed sum of the E exponentials: 32-term blocks in order (one lane each), then the
@@ -130,8 +228,15 @@ __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logi
     const int nbk = (n_experts + 31) >> 5;  // <= 8
     float bsum = 0.0f;
     if (lane < nbk) {
-        const int s1 = n_experts < lane * 32 + 32 ? n_experts : lane * 32 + 32;
-        for (int i = lane * 32; i < s1; ++i) bsum = bsum + lg[i];
+        if (lane * 32 + 32 <= n_experts) {
+            float4 q[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[i] = reinterpret_cast<const float4*>(lg + lane * 32)[i];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) bsum = (((bsum + q[i].x) + q[i].y) + q[i].z) + q[i].w;
+        } else {
+            for (int i = lane * 32; i < n_experts; ++i) bsum = bsum + lg[i];
+        }
     }
     float b8[8];
 #pragma unroll
@@ -148,87 +253,88 @@ __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logi
         }
         total = nbk > 0 ? b8[0] : 0.0f;
     }
-    for (int e = lane; e < n_experts; e += 64) lg[e] = lg[e] / total;
-    wave_lds_sync();
-    if (probs_out)
-        for (int e = lane; e < n_experts; e += 64) probs_out[(int64_t)t * n_experts + e] = lg[e];
-    // top-k: k rounds of (probability desc, index asc) over the lane's experts
-    float v[4];
-    int vi[4];
+    uint64_t* kw = keys[wave];
+    float v[NQ];
+    uint64_t kv[NQ];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < NQ; ++q) {
         const int e = lane + 64 * q;
-        v[q] = e < n_experts ? lg[e] : 0.0f;
-        vi[q] = e < n_experts ? e : 0x7FFFFFFF;
+        v[q] = e < n_experts ? lg[e] / total : 0.0f;
+        kv[q] = rank_key(v[q], e);
+        if (e < n_experts) {
+            kw[e] = kv[q];
+            if (probs_out) probs_out[(int64_t)t * n_experts + e] = v[q];
+        }
     }
+    // keys past E, up to a multiple of 8, rank after every real one
+    const int e8 = (n_experts + 7) & ~7;
+    if (lane < e8 - n_experts) kw[n_experts + lane] = 0ull;
+    wave_lds_sync();
+    // rank of each of the lane's experts: how many keys are larger
+    int rk[NQ] = {};
+    for (int f = 0; f < e8; f += 8) {
+        ulonglong2 u[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) u[i] = reinterpret_cast<const ulonglong2*>(kw + f)[i];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rk[q] += (u[i].x > kv[q] ? 1 : 0) + (u[i].y > kv[q] ? 1 : 0);
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        if (lane + 64 * q < n_experts && rk[q] < top_k) {
+            selv[wave][rk[q]] = v[q];
+            seli[wave][rk[q]] = lane + 64 * q;
+        }
+    }
+    wave_lds_sync();
+    // the k selected, in rank order from +0 (one block: k <= 32)
     float tsum = 0.0f;
-    float myw = 0.0f;
-    int myid = 0;
-    for (int j = 0; j < top_k; ++j) {
-        float bv = 0.0f;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (vi[q] != 0x7FFFFFFF && (bi == 0x7FFFFFFF || v[q] > bv)) {
-                bv = v[q];
-                bi = vi[q];
-            }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            if (oi != 0x7FFFFFFF && (bi == 0x7FFFFFFF || ov > bv || (ov == bv && oi < bi))) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (vi[q] == bi) vi[q] = 0x7FFFFFFF;  // taken
-        tsum = tsum + bv;  // the k selected, in rank order from +0 (one block: k <= 32)
-        if (lane == j) {
-            myw = bv;
-            myid = bi;
-        }
+    for (int j = 0; j < top_k; j += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(&selv[wave][j]);
+        tsum = tsum + q.x;
+        if (j + 1 < top_k) tsum = tsum + q.y;
+        if (j + 2 < top_k) tsum = tsum + q.z;
+        if (j + 3 < top_k) tsum = tsum + q.w;
     }
     if (lane < top_k) {
-        ids[(int64_t)t * top_k + lane] = myid;
+        const float myw = selv[wave][lane];
+        ids[(int64_t)t * top_k + lane] = seli[wave][lane];
         wout[(int64_t)t * top_k + lane] = renorm ? myw / tsum : myw;
     }
 }
 
-constexpr size_t ROUTE_LDS = 64 * 1024;
+// Two staging areas and the block sums.
+size_t moe_logits_lds(int hidden) { return 2ull * RT_STAGE + (size_t)RT_PAIRS * (hidden / 32) * sizeof(float); }
 
-// Experts per workgroup for TT tokens of `hidden` values: up to 32, as many as fit the LDS.
-int moe_logits_ec(int tt, int hidden) {
-    const int64_t rest = (int64_t)ROUTE_LDS - 4ll * tt * hidden;
-    const int64_t ec = rest > 0 ? rest / (8ll * tt * (hidden / 32)) : 0;
-    return (int)(ec < 32 ? ec : 32);
-}
-size_t moe_logits_lds(int tt, int hidden, int ec) {
-    return sizeof(float) * ((size_t)tt * hidden + 2ull * tt * ec * (hidden / 32));
-}
-
-bool moe_route_supported(int hidden) { return moe_logits_ec(1, hidden) >= 1; }
+bool moe_route_supported(int hidden) { return hidden > 0 && hidden % 32 == 0 && hidden / 32 <= RT_MAXB; }
 
 void launch_moe_route(const float* router, const float* x, int rows, int hidden, int n_experts,
                       int top_k, int renorm, int32_t* ids, float* w, float* probs, float* logits,
                       hipStream_t stream) {
-    // Two tokens per workgroup share each router block once there are enough tokens and a
-    // full chunk of experts still fits.
-    const int ec2 = moe_logits_ec(2, hidden);
-    if (rows >= 256 && ec2 >= 32) {
-        hipLaunchKernelGGL((k_moe_logits<2>), dim3((rows + 1) / 2, (n_experts + ec2 - 1) / ec2),
-                           dim3(256), moe_logits_lds(2, hidden, ec2), stream, router, x, rows, hidden,
-                           n_experts, ec2, logits);
-    } else {
-        const int ec = moe_logits_ec(1, hidden);
-        hipLaunchKernelGGL((k_moe_logits<1>), dim3(rows, (n_experts + ec - 1) / ec), dim3(256),
-                           moe_logits_lds(1, hidden, ec), stream, router, x, rows, hidden, n_experts,
-                           ec, logits);
-    }
-    hipLaunchKernelGGL(k_moe_topk, dim3((rows + 3) / 4), dim3(256), 0, stream, logits, rows,
-                       n_experts, top_k, renorm, ids, w, probs);
+    const dim3 grid((rows + RT_T - 1) / RT_T, (n_experts + RT_E - 1) / RT_E);
+    const size_t lds = moe_logits_lds(hidden);
+    static const hipError_t lds_ok =
+        hipFuncSetAttribute((const void*)k_moe_logits<true>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    static const hipError_t lds_ok4 =
+        hipFuncSetAttribute((const void*)k_moe_logits<false>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)lds_ok;  // a refusal shows as the launch's error
+    (void)lds_ok4;
+    if (((uintptr_t)x & 15) == 0)
+        hipLaunchKernelGGL(k_moe_logits<true>, grid, dim3(256), lds, stream, router, x, rows, hidden, n_experts, logits);
+    else
+        hipLaunchKernelGGL(k_moe_logits<false>, grid, dim3(256), lds, stream, router, x, rows, hidden, n_experts,
+                           logits);
+    const dim3 tg((rows + 3) / 4);
+    if (n_experts <= 64)
+        hipLaunchKernelGGL(k_moe_topk<1>, tg, dim3(256), 0, stream, logits, rows, n_experts, top_k, renorm, ids, w, probs);
+    else if (n_experts <= 128)
+        hipLaunchKernelGGL(k_moe_topk<2>, tg, dim3(256), 0, stream, logits, rows, n_experts, top_k, renorm, ids, w, probs);
+    else if (n_experts <= 192)
+        hipLaunchKernelGGL(k_moe_topk<3>, tg, dim3(256), 0, stream, logits, rows, n_experts, top_k, renorm, ids, w, probs);
+    else
+        hipLaunchKernelGGL(k_moe_topk<4>, tg, dim3(256), 0, stream, logits, rows, n_experts, top_k, renorm, ids, w, probs);
 }
 
 // ============================================================================================

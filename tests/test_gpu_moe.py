@@ -62,6 +62,50 @@ def test_route_bit_exact(M, rows, hidden, n_experts, top_k):
     assert_same(host(w), ww, "weights")
 
 
+@pytest.mark.parametrize("rows,hidden,n_experts", [(7, 2080, 19), (130, 4096, 128)])
+def test_route_token_rows_not_16_byte_aligned(M, rows, hidden, n_experts):
+    """Token rows at a 4-byte offset take the 4-byte copy path; a hidden size of 65 blocks
+    leaves a one-block last chunk."""
+    router = o.normal(0x51A30004 + hidden, 0.02, n_experts * hidden).reshape(n_experts, hidden)
+    x = o.normal(0x51A20004 + rows, 1.0, rows * hidden).reshape(rows, hidden)
+    flat = torch.empty(rows * hidden + 1, dtype=torch.float32, device="cuda")
+    xs = flat[1:].view(rows, hidden)
+    xs.copy_(torch.from_numpy(x))
+    assert xs.data_ptr() % 16 == 4
+    announce(f"route misaligned rows={rows} hidden={hidden} E={n_experts}")
+    ids, w, probs = M.route(dev(router), xs, 4, True, probs=True)
+    wids, ww, wprobs = o.moe_route(router, x, n_experts, 4, True)
+    assert_same(host(probs), wprobs, "probs")
+    assert (host(ids) == wids).all()
+    assert_same(host(w), ww, "weights")
+
+
+def test_route_nan_rows_match_the_first_best_scan(M):
+    """A NaN logit makes every probability of its row NaN (the F32Fixed sum is NaN); the
+    selection is then experts 0..k-1, as the oracle's first-best scan gives, and the weights
+    are NaN.  Rows without NaN are unaffected."""
+    hidden, n_experts, rows = 256, 40, 9
+    router = o.normal(21, 0.02, n_experts * hidden).reshape(n_experts, hidden)
+    x = o.normal(22, 1.0, rows * hidden).reshape(rows, hidden)
+    x[2, 7] = np.nan
+    router[0, 3] = np.nan  # logit 0 NaN in every row: the row maximum itself is NaN
+    x2 = x.copy()
+    announce("route nan")
+    for r in (router, router * np.float32(1)):
+        ids, w, probs = M.route(dev(r), dev(x2), 5, True, probs=True)
+        wids, ww, wprobs = o.moe_route(r, x2, n_experts, 5, True)
+        assert (host(ids) == wids).all()
+        assert_same(host(w), ww, "weights")
+        assert_same(host(probs), wprobs, "probs")
+    r = router.copy()
+    r[0, 3] = 0.5
+    ids, w, probs = M.route(dev(r), dev(x), 5, True, probs=True)
+    wids, ww, wprobs = o.moe_route(r, x, n_experts, 5, True)
+    assert (host(ids) == wids).all() and (wids[2] == np.arange(5)).all()
+    assert_same(host(w), ww, "weights")
+    assert np.isnan(host(w)[2]).all() and not np.isnan(host(w)[[0, 1, 3]]).any()
+
+
 def test_route_ties_go_to_the_lower_index(M):
     hidden, n_experts = 256, 16
     router = o.normal(3, 0.02, n_experts * hidden).reshape(n_experts, hidden)
