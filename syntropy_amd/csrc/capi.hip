@@ -331,19 +331,51 @@ SYN_EXPORT int syn_gemv_batch_quantized(uint32_t n, const int32_t* wtypes, const
                                            y, stream);
 }
 
-SYN_EXPORT int syn_gemv_batch_layout(uint32_t layout, uint32_t n, const int32_t* wtypes, const void* const* w,
-                                     const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
-                                     const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
-                                     void* stream) {
-    const char* W = "syn_gemv_batch";
+namespace {
+
+// The grouped Gemv on F32 rows.  fuse = 0: one batched Q8_K quantization into the workspace,
+// then the grouped GEMV (the faster pair for a whole layer); fuse = 1: one launch whose
+// workgroups quantize their problem's row into LDS themselves (one launch fewer, for a lone
+// Gemv); the workspace is still sized and checked.
+int gemv_batch_f32(const char* W, uint32_t layout, uint32_t n, const int32_t* wtypes, const void* const* w,
+                   const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in, const float* const* x,
+                   float* const* y, void* ws, uint64_t ws_bytes, void* stream, bool fuse) {
     if (n == 0) return SYN_OK;
     if (!w || !x || !y) return fail(SYN_E_INVALID, "%s: null argument array", W);
     if (layout != SYN_LAYOUT_SOURCE && layout != SYN_LAYOUT_X8)
         return fail(SYN_E_UNSUPPORTED, "%s: weight layout %u", W, layout);
     uint64_t off[SYN_BATCH];
     if (int rc = batch_setup(W, n, wtypes, w, w_bytes, n_out, k_in, ws, ws_bytes, off)) return rc;
-    if (int rc = batch_quantize(W, n, k_in, x, (uint8_t*)ws, off, (hipStream_t)stream)) return rc;
-    return batch_gemv(W, (int)layout, n, w, n_out, k_in, (const uint8_t*)ws, off, y, (hipStream_t)stream);
+    if (!fuse || layout != SYN_LAYOUT_X8) {
+        if (int rc = batch_quantize(W, n, k_in, x, (uint8_t*)ws, off, (hipStream_t)stream)) return rc;
+        return batch_gemv(W, (int)layout, n, w, n_out, k_in, (const uint8_t*)ws, off, y, (hipStream_t)stream);
+    }
+    const uint8_t* wp[SYN_BATCH];
+    const float* xp[SYN_BATCH];
+    float* yp[SYN_BATCH];
+    int no[SYN_BATCH], kk[SYN_BATCH];
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!x[i] || !aligned(x[i], 16)) return fail(SYN_E_INVALID, "%s: x[%u] must be a 16-byte aligned pointer", W, i);
+        if (!y[i] || !aligned(y[i], 4)) return fail(SYN_E_INVALID, "%s: y[%u] must be a 4-byte aligned pointer", W, i);
+        if (!syn::gemv_q4k_batch_fusable((int)k_in[i])) return fail(SYN_E_UNSUPPORTED, "%s: k_in[%u] = %u", W, i, k_in[i]);
+        wp[i] = (const uint8_t*)w[i];
+        xp[i] = x[i];
+        yp[i] = y[i];
+        no[i] = (int)n_out[i];
+        kk[i] = (int)k_in[i];
+    }
+    syn::launch_gemv_q4k_batch_f32(wp, (int)n, no, kk, xp, yp, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+}  // namespace
+
+SYN_EXPORT int syn_gemv_batch_layout(uint32_t layout, uint32_t n, const int32_t* wtypes, const void* const* w,
+                                     const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
+                                     const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,
+                                     void* stream) {
+    return gemv_batch_f32("syn_gemv_batch", layout, n, wtypes, w, w_bytes, n_out, k_in, x, y, ws, ws_bytes, stream,
+                          false);
 }
 
 SYN_EXPORT int syn_gemv_batch(uint32_t n, const int32_t* wtypes, const void* const* w,
@@ -423,7 +455,7 @@ SYN_EXPORT int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, ui
         const void* ws_[1] = {w};
         const int32_t ts[1] = {wtype};
         const uint64_t wb[1] = {w_bytes};
-        return syn_gemv_batch_layout(layout, 1, ts, ws_, wb, &n_out, &k_in, xs, ys, ws, ws_bytes, stream);
+        return gemv_batch_f32(W, layout, 1, ts, ws_, wb, &n_out, &k_in, xs, ys, ws, ws_bytes, stream, true);
     }
     if (!syn::gemm_q4k_supported((int)n_out, (int)k_in))
         return fail(SYN_E_UNSUPPORTED, "%s: a %u x %u matrix is larger than 4 GiB", W, n_out, k_in);

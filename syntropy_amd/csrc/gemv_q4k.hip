@@ -44,12 +44,21 @@ SYN_DEV v4u ldw(const uint8_t* p) {
 }
 
 // Lane `part` = c % 16 of super-block c / 16's group of 16 lanes: values 16 part .. +15.
-SYN_DEV void quant_block16(const float* __restrict__ x, int c, int nb, uint8_t* lds) {
+SYN_DEV void load_block16(const float* __restrict__ x, int c, float (&v)[16]) {
     const int sb = c >> 4, part = c & 15;
     const float4* src = reinterpret_cast<const float4*>(x + (int64_t)sb * 256 + part * 16);
-    const float4 a0 = src[0], a1 = src[1], a2 = src[2], a3 = src[3];
-    const float v[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
-                         a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 a = src[q];
+        v[4 * q] = a.x;
+        v[4 * q + 1] = a.y;
+        v[4 * q + 2] = a.z;
+        v[4 * q + 3] = a.w;
+    }
+}
+
+SYN_DEV void quant16_to_lds(const float (&v)[16], int c, int nb, uint8_t* lds) {
+    const int sb = c >> 4, part = c & 15;
     bool fin = true;
     float amax = 0.0f, mx = 0.0f;
     int idx = 0x7FFFFFFF;
@@ -106,6 +115,12 @@ SYN_DEV void quant_block16(const float* __restrict__ x, int c, int nb, uint8_t* 
     s += __shfl_xor(s, 1);  // the two 16-value halves of a 32-value group
     if ((part & 1) == 0) reinterpret_cast<int*>(lds + xs_off(nb) + sb * SUMW)[part >> 1] = s;
     if (part == 0) reinterpret_cast<float*>(lds + xd_off(nb))[sb] = d;
+}
+
+SYN_DEV void quant_block16(const float* __restrict__ x, int c, int nb, uint8_t* lds) {
+    float v[16];
+    load_block16(x, c, v);
+    quant16_to_lds(v, c, nb, lds);
 }
 
 // Q8_K of the activation row into LDS (crates/kernels-cpu/src/gemv/act.rs:351-373): 16 lanes
@@ -253,7 +268,8 @@ __global__ __launch_bounds__(256) void k_gemv_q4k_dec(const uint8_t* __restrict_
 // row's terms are folded in order by one lane from LDS.
 struct DecBatch {
     const uint8_t* W[SYN_BATCH];
-    const uint8_t* ws[SYN_BATCH];
+    const uint8_t* ws[SYN_BATCH];  // FUSE = 0: the Q8_K row, quantized beforehand
+    const float* x[SYN_BATCH];     // FUSE = 1: the F32 row, quantized by every workgroup
     float* y[SYN_BATCH];
     int n_out[SYN_BATCH];
     int nb[SYN_BATCH];
@@ -271,8 +287,22 @@ constexpr int dec_waves() { return LAYOUT == LAYOUT_X8 ? 8 : 4; }
 // LAYOUT 1 (x8): chunk q of the blocks of eight consecutive super-blocks sits together (see
 // layout.hpp), so the nine loads of a wavefront each read whole 128-byte lines, which streams at
 // a higher rate with non-temporal loads (the weights are read once).
-template <int LAYOUT>
-__global__ __launch_bounds__(64 * dec_waves<LAYOUT>()) __attribute__((amdgpu_waves_per_eu(6)))
+// FUSE = 1 (X8 weights; a lone Gemv op on an F32 row, one launch): the workgroup loads its
+// problem's F32 row into registers before the block's loads, and quantizes it to Q8_K in LDS
+// while they fly (crates/kernels-cpu/src/gemv/act.rs:351-373, the same steps as the separate
+// quantizer).  Rows of at most 64 super-blocks: two 16-value pieces per thread at 512 threads.
+// For a whole layer the separate quantization launch is faster (each workgroup re-quantizing
+// its row costs more than the launch it saves).
+constexpr int FUSE_PIECES = 2;
+
+// Resident wavefronts per SIMD: 6 (80 registers); the fused form holds the row pieces too
+// (4: 128 registers, no spills).
+template <int LAYOUT, int FUSE>
+constexpr int dec_occupancy() { return FUSE ? 4 : 6; }
+
+template <int LAYOUT, int FUSE>
+__global__ __launch_bounds__(64 * dec_waves<LAYOUT>())
+__attribute__((amdgpu_waves_per_eu(dec_occupancy<LAYOUT, FUSE>())))
 void k_gemv_q4k_batch(DecBatch bt) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int WAVES = dec_waves<LAYOUT>();
@@ -286,7 +316,15 @@ void k_gemv_q4k_batch(DecBatch bt) {
     const int row = (((int)blockIdx.x - bt.wg_begin[p]) * WAVES + wave) * rows_per_wave + lane / P;
     const int b = lane % P;
     const bool ok = row < n_out && b < nb;
-    if constexpr (LAYOUT == LAYOUT_X8) {
+    static_assert(!FUSE || LAYOUT == LAYOUT_X8, "the fused form reads X8 weights");
+    float xv[FUSE ? FUSE_PIECES : 1][16];
+    if constexpr (FUSE) {
+#pragma unroll
+        for (int i = 0; i < FUSE_PIECES; ++i) {
+            const int c = (int)threadIdx.x + i * 64 * WAVES;
+            if (c < nb * 16) load_block16(bt.x[p], c, xv[i]);
+        }
+    } else if constexpr (LAYOUT == LAYOUT_X8) {
         // the activation row streams into LDS first, with no registers held (codes column by
         // column, 16 lanes per column to keep the bank skew; sums and scales contiguous), so the
         // block's loads below queue behind it and the row is in place when they land
@@ -319,7 +357,14 @@ void k_gemv_q4k_batch(DecBatch bt) {
 #pragma unroll
         for (int i = 0; i < 9; ++i) A[i] = *reinterpret_cast<const v4u*>(src + 16 * i);
     }
-    if constexpr (LAYOUT == LAYOUT_X8) {
+    if constexpr (FUSE) {
+#pragma unroll
+        for (int i = 0; i < FUSE_PIECES; ++i) {
+            const int c = (int)threadIdx.x + i * 64 * WAVES;
+            if (c < nb * 16) quant16_to_lds(xv[i], c, nb, lds);  // 16-lane groups stay whole
+        }
+        lds_barrier();
+    } else if constexpr (LAYOUT == LAYOUT_X8) {
         wait_vm<9>();  // this wavefront's row loads, all older than the block's nine
         lds_barrier();
     } else {
@@ -387,16 +432,18 @@ void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* w
                   reinterpret_cast<const int32_t*>(ws + L.sums), y, stream);
 }
 
-template <int LAYOUT>
+template <int LAYOUT, int FUSE>
 static void launch_batch(int np, const uint8_t* const* W, const int* n_out, const int* k,
-                         const uint8_t* const* ws, float* const* y, hipStream_t stream) {
+                         const uint8_t* const* ws, const float* const* x, float* const* y,
+                         hipStream_t stream) {
     constexpr int WAVES = dec_waves<LAYOUT>();
     DecBatch bt{};
     bt.np = np;
     int wg = 0, max_nb = 0;
     for (int p = 0; p < np; ++p) {
         bt.W[p] = W[p];
-        bt.ws[p] = ws[p];
+        bt.ws[p] = ws ? ws[p] : nullptr;
+        bt.x[p] = x ? x[p] : nullptr;
         bt.y[p] = y[p];
         bt.n_out[p] = n_out[p];
         bt.nb[p] = k[p] / 256;
@@ -409,16 +456,23 @@ static void launch_batch(int np, const uint8_t* const* W, const int* n_out, cons
     bt.wg_begin[np] = wg;
     if (wg == 0) return;
     // the activation row, then 64 fold terms per wavefront
-    hipLaunchKernelGGL(k_gemv_q4k_batch<LAYOUT>, dim3(wg), dim3(64 * WAVES),
+    hipLaunchKernelGGL((k_gemv_q4k_batch<LAYOUT, FUSE>), dim3(wg), dim3(64 * WAVES),
                        align_up(q4k_dec_lds(max_nb), 16) + WAVES * 64 * 4, stream, bt);
 }
 
 void launch_gemv_q4k_batch(int layout, int np, const uint8_t* const* W, const int* n_out, const int* k,
                            const uint8_t* const* ws, float* const* y, hipStream_t stream) {
     if (layout == LAYOUT_X8)
-        launch_batch<LAYOUT_X8>(np, W, n_out, k, ws, y, stream);
+        launch_batch<LAYOUT_X8, 0>(np, W, n_out, k, ws, nullptr, y, stream);
     else
-        launch_batch<LAYOUT_SOURCE>(np, W, n_out, k, ws, y, stream);
+        launch_batch<LAYOUT_SOURCE, 0>(np, W, n_out, k, ws, nullptr, y, stream);
+}
+
+bool gemv_q4k_batch_fusable(int k) { return k % 256 == 0 && k > 0 && k <= 64 * 256; }
+
+void launch_gemv_q4k_batch_f32(const uint8_t* const* W, int np, const int* n_out, const int* k,
+                               const float* const* x, float* const* y, hipStream_t stream) {
+    launch_batch<LAYOUT_X8, 1>(np, W, n_out, k, nullptr, x, y, stream);
 }
 
 // ---- the x8 repack: a permutation of whole 16-byte chunks --------------------------------------

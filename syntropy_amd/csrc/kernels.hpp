@@ -24,6 +24,10 @@ void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* w
 #define SYN_BATCH 8
 void launch_gemv_q4k_batch(int layout, int np, const uint8_t* const* W, const int* n_out, const int* k,
                            const uint8_t* const* ws, float* const* y, hipStream_t stream);
+// The same over X8 weights with the F32 rows quantized inside the grouped launch (k <= 16384).
+bool gemv_q4k_batch_fusable(int k);
+void launch_gemv_q4k_batch_f32(const uint8_t* const* W, int np, const int* n_out, const int* k,
+                               const float* const* x, float* const* y, hipStream_t stream);
 // The X8 repack of a Q4_K matrix of nblocks super-blocks (inverse = 1: back to the GGUF order).
 void launch_q4k_x8(const uint8_t* src, uint8_t* dst, uint64_t nblocks, int inverse, hipStream_t stream);
 void launch_act_quant_batch(int np, const float* const* x, const int* k, uint8_t* const* ws,
