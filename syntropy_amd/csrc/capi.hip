@@ -510,10 +510,24 @@ SYN_EXPORT int syn_dequantize(int32_t wtype, const void* src, uint64_t src_bytes
 
 namespace {
 
-// Workspace of syn_moe_grouped: offsets, slots, the error word, the packed entries' Q8_K
-// activations, the entries' h rows and their Q8_K; every section on 256 bytes.
+// The expert FFN runs on the prefill GEMM (entries padded to 64-entry tiles per expert) once the
+// experts average this many entries; below it, on the grouped decode kernels.
+constexpr uint64_t MOE_GEMM_MIN_AVG = 32;
+
+bool moe_use_gemm(uint32_t n_experts, uint32_t top_k, uint32_t hidden, uint32_t inter, uint32_t rows) {
+    return (uint64_t)rows * top_k >= MOE_GEMM_MIN_AVG * n_experts && syn::moe_gemm_supported((int)hidden, (int)inter);
+}
+
+// Workspace of syn_moe_grouped: offsets, slots, the error word, then
+//   decode kernels: the packed entries' Q8_K activations, the entries' h rows and their Q8_K;
+//   GEMM path: the tile table (padded offsets, tile experts, tile count), the entries' rows in
+//   the GEMM layout at their padded positions, h, and h in the GEMM layout;
+// every section on 256 bytes.
 struct MoeWs {
     uint64_t offsets, slots, err, xq, h, hq, bytes;
+    bool gemm;
+    uint64_t pad_off, tile_e, n_tiles;
+    int max_tiles;
 };
 MoeWs moe_ws(uint32_t n_experts, uint32_t top_k, uint32_t hidden, uint32_t inter, uint32_t rows) {
     MoeWs m{};
@@ -525,12 +539,30 @@ MoeWs moe_ws(uint32_t n_experts, uint32_t top_k, uint32_t hidden, uint32_t inter
     o = syn::align_up(o + 4ull * ent, 256);
     m.err = o;  // error word, then the largest expert's entry count
     o = syn::align_up(o + 8, 256);
-    m.xq = o;
-    o += syn::moe_act_bytes((int64_t)ent, (int)hidden);
-    m.h = o;
-    o = syn::align_up(o + 4ull * ent * inter, 256);
-    m.hq = o;
-    o += syn::moe_act_bytes((int64_t)ent, (int)inter);
+    m.gemm = moe_use_gemm(n_experts, top_k, hidden, inter, rows);
+    if (m.gemm) {
+        m.max_tiles = (int)((ent + 63) / 64 + n_experts);
+        const int64_t tpad = 64ll * m.max_tiles;
+        m.pad_off = o;
+        o = syn::align_up(o + 4ull * (n_experts + 1), 256);
+        m.tile_e = o;
+        o = syn::align_up(o + 4ull * m.max_tiles, 256);
+        m.n_tiles = o;
+        o = syn::align_up(o + 4, 256);
+        m.xq = o;
+        o = syn::align_up(o + syn::gemm_act_bytes(tpad, (int)hidden), 256);
+        m.h = o;
+        o = syn::align_up(o + 4ull * ent * inter, 256);
+        m.hq = o;
+        o = syn::align_up(o + syn::gemm_act_bytes(tpad, (int)inter), 256);
+    } else {
+        m.xq = o;
+        o += syn::moe_act_bytes((int64_t)ent, (int)hidden);
+        m.h = o;
+        o = syn::align_up(o + 4ull * ent * inter, 256);
+        m.hq = o;
+        o += syn::moe_act_bytes((int64_t)ent, (int)inter);
+    }
     m.bytes = syn::align_up(o, 256);
     return m;
 }
@@ -616,6 +648,26 @@ SYN_EXPORT int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, 
     const int ent = (int)(rows * top_k);
     hipStream_t st = (hipStream_t)stream;
     syn::launch_moe_pack(ids, ent, (int)n_experts, offsets, slots, err, st);
+    if (m.gemm) {
+        const syn::MoeTiles mt{(uint32_t*)(base + m.pad_off), (uint32_t*)(base + m.tile_e),
+                               (uint32_t*)(base + m.n_tiles)};
+        const int64_t tpad = 64ll * m.max_tiles;
+        const syn::GemmAct gx = syn::gemm_act_at(base + m.xq, tpad, (int)hidden);
+        const syn::GemmAct gh = syn::gemm_act_at(base + m.hq, tpad, (int)inter);
+        float* h = (float*)(base + m.h);
+        syn::launch_moe_tiles(offsets, (int)n_experts, err, mt, st);
+        syn::launch_moe_gemm_act(x, 1, slots, (int)top_k, (int)hidden, offsets, mt, err, gx, st);
+        syn::launch_moe_gemm(0, (const uint8_t*)gate, (const uint8_t*)up, (int)n_experts, (int)inter, (int)hidden,
+                             gx, m.max_tiles, offsets, mt, err, slots, h, st);
+        syn::launch_moe_gemm_act(h, 0, slots, (int)top_k, (int)inter, offsets, mt, err, gh, st);
+        syn::launch_moe_gemm(1, (const uint8_t*)down, nullptr, (int)n_experts, (int)hidden, (int)inter, gh,
+                             m.max_tiles, offsets, mt, err, slots, out, st);
+        if (status) {
+            hipError_t e = hipMemcpyAsync(status, err, 4, hipMemcpyDeviceToDevice, st);
+            if (e != hipSuccess) return fail(SYN_E_DEVICE, "%s: status copy: %s", W, hipGetErrorString(e));
+        }
+        return check_launch(W);
+    }
     const syn::MoeAct ax = syn::moe_act_at(base + m.xq, ent, (int)hidden);
     const syn::MoeAct ah = syn::moe_act_at(base + m.hq, ent, (int)inter);
     syn::launch_moe_gather_q8k(x, slots, ent, (int)top_k, (int)hidden, err, ax, 1, st);

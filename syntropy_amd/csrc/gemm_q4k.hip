@@ -72,16 +72,13 @@ GemmAct gemm_act_at(uint8_t* base, int64_t tpad, int k) {
 // One wavefront per (super-block b, token t): the Q8_K block of crates/kernels-cpu/src/gemv/
 // act.rs:351-373 (q8k_block_lane), written in the GEMM order.  Lane l holds values 4l..4l+3:
 // sub-block j = l / 8, k part p = l / 16, nibble half h = (l / 8) & 1, dword s = l & 7.
-__global__ __launch_bounds__(256) void k_gemm_act(const float* __restrict__ x, int T, int k, GemmAct a) {
-    const int nb = k / 256, lane = threadIdx.x & 63;
-    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= (int64_t)nb * a.tpad) return;
-    const int b = (int)(item / a.tpad), t = (int)(item - (int64_t)b * a.tpad);
+// A null row writes zeros (padding).
+SYN_DEV void gemm_act_block(const float* __restrict__ row, int b, int t, GemmAct a, int lane) {
     uint32_t q = 0;
     int sum32 = 0, xsum = 0;
     float d = 0.0f;
-    if (t < T) {  // uniform over the wavefront
-        const Q8KLane r = q8k_block_lane(x + (int64_t)t * k + (int64_t)b * 256, lane);
+    if (row) {  // uniform over the wavefront
+        const Q8KLane r = q8k_block_lane(row + (int64_t)b * 256, lane);
         q = r.packed;
         sum32 = r.sum32;
         d = r.d;
@@ -112,6 +109,14 @@ __global__ __launch_bounds__(256) void k_gemm_act(const float* __restrict__ x, i
         reinterpret_cast<float*>(tail + (int64_t)a.tpad * 32)[t] = d;
         reinterpret_cast<float*>(tail + (int64_t)a.tpad * 36)[t] = (float)xsum;
     }
+}
+
+__global__ __launch_bounds__(256) void k_gemm_act(const float* __restrict__ x, int T, int k, GemmAct a) {
+    const int nb = k / 256, lane = threadIdx.x & 63;
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= (int64_t)nb * a.tpad) return;
+    const int b = (int)(item / a.tpad), t = (int)(item - (int64_t)b * a.tpad);
+    gemm_act_block(t < T ? x + (int64_t)t * k : nullptr, b, t, a, lane);
 }
 
 void launch_gemm_act(const float* x, int T, int k, GemmAct a, hipStream_t stream) {
@@ -371,5 +376,246 @@ void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, 
     const dim3 grid((unsigned)((n_out + GM_ROWS - 1) / GM_ROWS), (unsigned)(a.tpad / GM_TT));
     hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(64 * GM_WAVES), 2 * GM_STAGE, stream, g);
 }
+
+// ============================================================================================
+// The MoE layer at many tokens: the grouped expert FFN on the same matrix cores
+// ============================================================================================
+//
+// Each expert's entries (the packed lists of k_moe_pack: offsets, slots) are padded to whole
+// 64-entry tiles: tile i belongs to expert tile_e[i], and its padded position p = 64 i + t holds
+// entry offsets[e] + p - pad_off[e] when that is below offsets[e + 1] (padding rows are zero and
+// their outputs are dropped).  The entries' rows are quantized to Q8_K in the GEMM layout at
+// their padded positions (each entry's row exactly as the expert quantizes it, moe.rs:479-492),
+// then:
+//   gate/up: a workgroup takes (tile, 128 weight rows); its 256-row weight tile is those 128
+//     rows of the tile's gate matrix followed by the same 128 rows of its up matrix, so
+//     wavefronts 0-3 hold g and wavefronts 4-7 hold u of the same outputs, and
+//     h = silu(g) * u per entry (moe.rs:529-551);
+//   down: (tile, 256 rows) of the expert's down matrix on h requantized the same way; each
+//     output goes to its entry's slot (moe.rs:500-515).
+// Every product is the Gemv value (the same exact sums and term fold as the dense GEMM).
+
+// One workgroup: an inclusive scan of the experts' tile counts (E <= 256).
+__global__ __launch_bounds__(256) void k_moe_tiles(const uint32_t* __restrict__ offsets, int n_experts,
+                                                   const uint32_t* __restrict__ err, MoeTiles mt) {
+    __shared__ uint32_t cnt[256];
+    const int e = threadIdx.x;
+    const bool bad = err[0] != 0;  // uniform: the layer writes nothing
+    const uint32_t n = (!bad && e < n_experts) ? offsets[e + 1] - offsets[e] : 0u;
+    const uint32_t tiles = (n + 63u) / 64u;
+    cnt[e] = tiles;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        const uint32_t v = e >= off ? cnt[e - off] : 0u;
+        __syncthreads();
+        cnt[e] += v;
+        __syncthreads();
+    }
+    const uint32_t end = cnt[e], begin = end - tiles;
+    if (e < n_experts) mt.pad_off[e] = 64u * begin;
+    if (e == n_experts - 1) {
+        mt.pad_off[n_experts] = 64u * end;
+        mt.n_tiles[0] = end;
+    }
+    for (uint32_t i = begin; i < end; ++i) mt.tile_e[i] = (uint32_t)e;
+}
+
+void launch_moe_tiles(const uint32_t* offsets, int n_experts, const uint32_t* err, MoeTiles mt,
+                      hipStream_t stream) {
+    hipLaunchKernelGGL(k_moe_tiles, dim3(1), dim3(256), 0, stream, offsets, n_experts, err, mt);
+}
+
+// The entries' rows at their padded positions: GATHER = 1 takes row slots[i] / top_k of x
+// (the entry's token), GATHER = 0 row i of h.  Positions in tiles past the used ones are not
+// written (no workgroup reads them).
+template <int GATHER>
+__global__ __launch_bounds__(256) void k_moe_gemm_act(const float* __restrict__ src,
+                                                      const uint32_t* __restrict__ slots, int top_k, int k,
+                                                      const uint32_t* __restrict__ offsets, MoeTiles mt,
+                                                      const uint32_t* __restrict__ err, GemmAct a) {
+    if (err[0]) return;
+    const int nb = k / 256, lane = threadIdx.x & 63;
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= (int64_t)nb * a.tpad) return;
+    const int b = (int)(item / a.tpad), pos = (int)(item - (int64_t)b * a.tpad);
+    const uint32_t tile = (uint32_t)pos / 64u;
+    if (tile >= mt.n_tiles[0]) return;
+    const uint32_t e = mt.tile_e[tile];
+    const uint32_t i = offsets[e] + ((uint32_t)pos - mt.pad_off[e]);
+    const float* row = nullptr;
+    if (i < offsets[e + 1]) row = GATHER ? src + (int64_t)(slots[i] / (uint32_t)top_k) * k : src + (int64_t)i * k;
+    gemm_act_block(row, b, pos, a, lane);
+}
+
+void launch_moe_gemm_act(const float* src, int gather, const uint32_t* slots, int top_k, int k,
+                         const uint32_t* offsets, MoeTiles mt, const uint32_t* err, GemmAct a,
+                         hipStream_t stream) {
+    const int64_t items = (int64_t)(k / 256) * a.tpad;
+    if (items == 0) return;
+    const dim3 grid((unsigned)((items + 3) / 4));
+    if (gather)
+        hipLaunchKernelGGL(k_moe_gemm_act<1>, grid, dim3(256), 0, stream, src, slots, top_k, k, offsets, mt, err, a);
+    else
+        hipLaunchKernelGGL(k_moe_gemm_act<0>, grid, dim3(256), 0, stream, src, slots, top_k, k, offsets, mt, err, a);
+}
+
+struct MoeGemmArgs {
+    const uint8_t* W0;  // gate (MODE 0) or down (MODE 1), stacked by expert
+    const uint8_t* W1;  // up (MODE 0)
+    uint64_t ebytes;    // bytes of one expert's matrix
+    GemmAct act;
+    int nb;             // super-blocks along k
+    uint32_t rb;        // weight row bytes
+    int row_tiles;      // workgroups per entry tile
+    const uint32_t* offsets;
+    MoeTiles mt;
+    const uint32_t* err;
+    const uint32_t* slots;
+    float* out;         // h [entries][cols] (MODE 0) or out [slots][cols] (MODE 1)
+    int cols;           // inter (MODE 0) or hidden (MODE 1)
+};
+
+// MODE 0 (gate/up, 128 weight rows of each per workgroup) or 1 (down, 256 rows).
+template <int MODE>
+__global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    if (g.err[0]) return;
+    const int tile = (int)blockIdx.x / g.row_tiles, rt = (int)blockIdx.x - tile * g.row_tiles;
+    if ((uint32_t)tile >= g.mt.n_tiles[0]) return;  // uniform per workgroup
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t e = g.mt.tile_e[tile];
+    const int t0 = 64 * tile;
+    const uint32_t i0 = g.offsets[e] + ((uint32_t)t0 - g.mt.pad_off[e]);
+    const uint32_t left = g.offsets[e + 1] - i0;
+    const int nvalid = left < 64u ? (int)left : 64;
+    constexpr int ROWS = MODE == 0 ? GM_ROWS / 2 : GM_ROWS;  // rows of each matrix
+    const uint8_t* b0 = g.W0 + (uint64_t)e * g.ebytes + (uint64_t)rt * ROWS * g.rb;
+    const uint8_t* b1 = MODE == 0 ? g.W1 + (uint64_t)e * g.ebytes + (uint64_t)rt * ROWS * g.rb : b0;
+    // the weight tile's 256 rows: MODE 0 rows 0-127 of b0 then rows 0-127 of b1 (slots
+    // 0..GM_WSLOT/2-1 hold exactly the first 128 rows: 128 * 9 chunks = 18 slots of 64)
+    GemmArgs ga{};
+    ga.layout = LAYOUT_SOURCE;
+    ga.N = GM_ROWS;
+    ga.rb = g.rb;
+    ga.codes = g.act.codes;
+    ga.tail = g.act.tail;
+    ga.tpad = g.act.tpad;
+    ga.nb = g.nb;
+    GemmSlots sl = gemm_slots(ga, wave, lane, 0, t0);
+    static_assert(GM_ROWS / 2 * 9 % 64 == 0, "gate and up halves on whole slots");
+    constexpr int HALF_SLOTS = GM_ROWS / 2 * 9 / 64;
+    bool upper[GM_WPW];
+#pragma unroll
+    for (int u = 0; u < GM_WPW; ++u) {
+        upper[u] = MODE == 0 && wave + GM_WAVES * u >= HALF_SLOTS;
+        if (upper[u]) sl.woff[u] -= (uint32_t)(GM_ROWS / 2) * g.rb;
+    }
+    const int live = sl.nw + GM_ASLOT / GM_WAVES + sl.nt;
+    auto issue = [&](int b, uint8_t* stage) {
+        const uint8_t* w0 = b0 + 144 * (size_t)b;
+        const uint8_t* w1 = b1 + 144 * (size_t)b;
+        const uint8_t* ab = g.act.codes + ((size_t)b * g.act.tpad + t0) * 512;
+        const uint8_t* tb = g.act.tail + (size_t)b * g.act.tpad * GM_TAIL_ROW;
+        const uint32_t st = lds_addr(stage);
+#pragma unroll
+        for (int u = 0; u < GM_WPW; ++u)
+            if (u < sl.nw) lds_dma16(sl.woff[u], upper[u] ? w1 : w0, st + 1024u * (uint32_t)(wave + GM_WAVES * u));
+#pragma unroll
+        for (int u = 0; u < GM_ASLOT / GM_WAVES; ++u) {
+            const int gs = wave + GM_WAVES * u;
+            lds_dma16(16u * (uint32_t)lane, ab + 1024 * gs, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
+        }
+        if (sl.ton) lds_dma16(sl.toff, tb, st + (uint32_t)(GM_WB + GM_AB) + 1024u * (uint32_t)wave);
+    };
+    v4f acc[GM_MT][GM_NT];
+#pragma unroll
+    for (int mt = 0; mt < GM_MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < GM_NT; ++nt) acc[mt][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    issue(0, smem);
+    if (g.nb > 1) issue(1, smem + GM_STAGE);
+    for (int b = 0; b < g.nb; ++b) {
+        uint8_t* stage = smem + (b & 1) * GM_STAGE;
+        wait_vm_n<GM_PER_WAVE>(b + 1 < g.nb ? live : 0);
+        lds_barrier();
+        gemm_super(stage, wave, lane, acc);
+        lds_barrier();
+        if (b + 2 < g.nb) issue(b + 2, stage);
+    }
+    const int c = lane & 15, p = lane >> 4;
+    if constexpr (MODE == 0) {
+        // u (wavefronts 4-7) through LDS to the wavefronts holding g of the same outputs
+        float* ux = reinterpret_cast<float*>(smem);  // [64 tokens][128 rows]
+        if (wave >= GM_WAVES / 2) {
+#pragma unroll
+            for (int mt = 0; mt < GM_MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < GM_NT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        ux[(16 * mt + 4 * p + i) * ROWS + 16 * GM_NT * (wave - GM_WAVES / 2) + 16 * nt + c] = acc[mt][nt][i];
+        }
+        lds_barrier();
+        if (wave < GM_WAVES / 2) {
+#pragma unroll
+            for (int mt = 0; mt < GM_MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < GM_NT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int t = 16 * mt + 4 * p + i, r = 16 * GM_NT * wave + 16 * nt + c;
+                        if (t < nvalid) {
+                            const float u = ux[t * ROWS + r];
+                            g.out[(int64_t)(i0 + t) * g.cols + rt * ROWS + r] = ref_silu(acc[mt][nt][i]) * u;
+                        }
+                    }
+        }
+    } else {
+#pragma unroll
+        for (int mt = 0; mt < GM_MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < GM_NT; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * mt + 4 * p + i, r = 16 * GM_NT * wave + 16 * nt + c;
+                    if (t < nvalid) g.out[(int64_t)g.slots[i0 + t] * g.cols + rt * ROWS + r] = acc[mt][nt][i];
+                }
+    }
+}
+
+void launch_moe_gemm(int mode, const uint8_t* w0, const uint8_t* w1, int n_experts, int rows, int k,
+                     GemmAct act, int max_tiles, const uint32_t* offsets, MoeTiles mt, const uint32_t* err,
+                     const uint32_t* slots, float* out, hipStream_t stream) {
+    MoeGemmArgs g;
+    g.W0 = w0;
+    g.W1 = w1;
+    g.nb = k / 256;
+    g.rb = (uint32_t)g.nb * 144u;
+    g.ebytes = (uint64_t)rows * g.rb;
+    g.act = act;
+    g.row_tiles = mode == 0 ? rows / (GM_ROWS / 2) : rows / GM_ROWS;
+    g.offsets = offsets;
+    g.mt = mt;
+    g.err = err;
+    g.slots = slots;
+    g.out = out;
+    g.cols = rows;
+    const dim3 grid((unsigned)(max_tiles * g.row_tiles));
+    if (mode == 0) {
+        static const hipError_t ok0 = hipFuncSetAttribute((const void*)k_moe_gemm<0>,
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize, 2 * GM_STAGE);
+        (void)ok0;  // a refusal shows as the launch's error
+        hipLaunchKernelGGL(k_moe_gemm<0>, grid, dim3(64 * GM_WAVES), 2 * GM_STAGE, stream, g);
+    } else {
+        static const hipError_t ok1 = hipFuncSetAttribute((const void*)k_moe_gemm<1>,
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize, 2 * GM_STAGE);
+        (void)ok1;
+        hipLaunchKernelGGL(k_moe_gemm<1>, grid, dim3(64 * GM_WAVES), 2 * GM_STAGE, stream, g);
+    }
+}
+
+// Row tiles: gate/up 128 rows, down 256.
+bool moe_gemm_supported(int hidden, int inter) { return hidden % GM_ROWS == 0 && inter % (GM_ROWS / 2) == 0; }
 
 }  // namespace syn

@@ -230,6 +230,59 @@ def test_grouped_row_permutation(M):
     assert_same(yp, y[perm])
 
 
+# ---- the grouped FFN on the prefill GEMM (experts averaging 32 or more entries) ---------------
+@pytest.mark.parametrize("rows", [96, 200, 333])
+def test_grouped_gemm_path_equals_oracle(M, rows):
+    """The reference test shape at token counts that take the matrix-core GEMM path: entries
+    padded to 64-entry tiles per expert, gate and up in one workgroup, down to the slots."""
+    s = M.MoeShape(6, 2, 256, 512)
+    gate, up, down = random_q4k_experts(2, s.n_experts, s.hidden, s.inter)
+    rng = MoeRng(300 + rows)
+    x = moe_activations(rng, rows * s.hidden).reshape(rows, s.hidden)
+    ids = moe_route_ids(rng, rows, s.top_k, s.n_experts)
+    announce(f"grouped gemm path rows={rows}")
+    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, 6, 2, 256, 512, gate, up, down, x, ids)
+    assert st == 0
+    assert_same(got, want, f"rows {rows}")
+
+
+def test_grouped_gemm_path_skewed_and_empty_experts(M):
+    """One expert takes 300 entries (five tiles, the last partial), four take none, and the
+    hidden size spans several 256-row down tiles and 128-row gate/up tiles."""
+    s = M.MoeShape(16, 4, 1024, 512)
+    gate, up, down = fast_q4k_experts(5, s.n_experts, s.hidden, s.inter)
+    rows = 160
+    rs = np.random.default_rng(9)
+    x = rs.standard_normal((rows, s.hidden)).astype(np.float32)
+    ids = np.stack([rs.permutation(12)[: s.top_k] for _ in range(rows)]).astype(np.int32)  # experts 12-15 empty
+    ids[:, 0] = np.where(np.arange(rows) < 150, 3, ids[:, 0])
+    for r in range(rows):  # distinct experts per row
+        for j in range(1, s.top_k):
+            if ids[r, j] in ids[r, :j]:
+                ids[r, j] = next(e for e in range(12) if e not in ids[r])
+    cnt = np.bincount(ids.ravel(), minlength=16)
+    assert cnt[3] >= 150 and (cnt[12:] == 0).all()
+    announce("grouped gemm path skewed")
+    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, 16, 4, 1024, 512, gate, up, down, x, ids, threads=8)
+    assert st == 0
+    assert_same(got, want, "skewed")
+
+
+def test_grouped_gemm_path_refusal_writes_nothing(M):
+    s = M.MoeShape(4, 2, 256, 256)
+    gate, up, down = random_q4k_experts(3, s.n_experts, s.hidden, s.inter)
+    rows = 80
+    x = np.ones((rows, 256), np.float32)
+    ids = np.tile(np.array([[0, 1]], np.int32), (rows, 1))
+    ids[41, 1] = 4
+    announce("grouped gemm path bad id")
+    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    assert st == 1
+    assert np.isnan(got).all()
+
+
 def test_grouped_refusal_writes_nothing(M):
     s = M.MoeShape(6, 2, 256, 512)
     gate, up, down = random_q4k_experts(3, s.n_experts, s.hidden, s.inter)
