@@ -95,6 +95,21 @@ int syn_gemv_batch_quantized_layout(uint32_t layout, uint32_t n, const int32_t* 
                                     const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
                                     const void* ws, uint64_t ws_bytes, float* const* y, void* stream);
 
+/* ---- GateUpAct{Silu} -------------------------------------------------------------------------
+ * y[r][i] = silu(gate_i . x_r) * (up_i . x_r) for the reference's GateUpAct
+ * (crates/kernels/src/reference/linear.rs:75-112), with w one matrix of 2 n_out rows of k_in,
+ * gate rows first, then up rows: the ggml provider's binding of the op
+ * (crates/kernels-ggml/src/mapping.rs:31).  Each dot is the Gemv value of syn_gemv_layout over
+ * the stacked matrix (any row count and layout it serves), silu uses the reference's software
+ * exp (crates/kernels/src/reference/math.rs:82-84) and the product is rounded once, as the MoE
+ * FFN's gated product (crates/kernels-cpu/src/moe.rs:529-551).  x [rows, k_in] and y
+ * [rows, n_out] F32; the workspace holds the Gemv's workspace and the [rows, 2 n_out] product. */
+int syn_gate_up_act_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t rows, uint32_t n_out,
+                                    uint32_t k_in, uint64_t* bytes);
+int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                    uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
+                    void* stream);
+
 /* ---- Prefill GEMM ---------------------------------------------------------------------------
  * Q4_K weights times many activation rows on the matrix cores, each output bit-identical to
  * syn_gemv (which takes this path itself for Q4_K calls of 32 rows or more).  The reference

@@ -21,6 +21,8 @@
  *                    q8_0/q8_1 ref, q8_K)
  *   or_gemv          pinned output bits of crates/kernels-cpu/src/gemv/tests.rs:739-777 and
  *                    the hand-computed cases at :407-458, plus the F64 derived bound
+ *   or_gate_up_act   or_gemv and or_silu composed; a one-hot Q8_0 gate/up pair pins the row
+ *                    order (gate rows first) and the product against the activation codes
  *   or_moe_*         packing against brute force; MoE slot = expert FFN of the row alone
  *                    (moe/tests.rs:315); combine against its definition; route ids against a
  *                    brute-force sort.  MoeRoute and MoeCombine have no reference code: their
@@ -922,6 +924,28 @@ int or_gemv_threads(int ty, const uint8_t* w, size_t n_out, size_t k, const floa
     free(st);
     free(ws);
     return 0;
+}
+
+/* ===================================================================================== */
+/* GateUpAct{Silu} on quantized weights.  kernels::reference defines the op as               */
+/* y[r][i] = silu(gate_i . x_r) * (up_i . x_r) (crates/kernels/src/reference/linear.rs:75-112); */
+/* the ggml provider binds one weight of 2 n_out rows, gate rows first, then up rows          */
+/* (crates/kernels-ggml/src/mapping.rs:31).  On quantized weights each dot is the Gemv value */
+/* and the gated product is the MoE FFN's (crates/kernels-cpu/src/moe.rs:529-551): silu with  */
+/* the software exp, the product rounded once.                                              */
+/* ===================================================================================== */
+
+int or_gate_up_act(int ty, const uint8_t* w, size_t n_out, size_t k, const float* x, size_t rows,
+                   float* y, int threads) {
+    float* y2 = (float*)malloc(rows * 2 * n_out * sizeof(float) + 1);
+    if (!y2) return -1;
+    int rc = or_gemv_threads(ty, w, 2 * n_out, k, x, rows, y2, threads);
+    if (!rc)
+        for (size_t r = 0; r < rows; ++r)
+            for (size_t i = 0; i < n_out; ++i)
+                y[r * n_out + i] = or_silu(y2[r * 2 * n_out + i]) * y2[r * 2 * n_out + n_out + i];
+    free(y2);
+    return rc;
 }
 
 /* ===================================================================================== */

@@ -82,6 +82,8 @@ int or_gemv(int ty, const uint8_t* w, size_t n_out, size_t k, const float* x, si
 /* the same, split over `threads` pthreads by the reference's partition (gemv.rs:402-421) */
 int or_gemv_threads(int ty, const uint8_t* w, size_t n_out, size_t k, const float* x,
                     size_t rows, float* y, int threads);
+int or_gate_up_act(int ty, const uint8_t* w, size_t n_out, size_t k, const float* x, size_t rows,
+                   float* y, int threads);
 void or_partition(int ty, size_t n_out, size_t k, size_t parts, size_t* starts, size_t* ends);
 
 /* ---- MoE (crates/kernels-cpu/src/moe.rs:402-551) ---- */

@@ -73,6 +73,7 @@ def lib():
         L.or_gemv_ws.argtypes = [i32, vp, sz, sz, vp, vp, sz, sz, sz, vp]
         L.or_gemv.argtypes = [i32, vp, sz, sz, vp, sz, vp]
         L.or_gemv_threads.argtypes = [i32, vp, sz, sz, vp, sz, vp, i32]
+        L.or_gate_up_act.argtypes = [i32, vp, sz, sz, vp, sz, vp, i32]
         L.or_partition.argtypes = [i32, sz, sz, sz, vp, vp]
         L.or_moe_workspace_bytes.restype = sz
         L.or_moe_workspace_bytes.argtypes = [sz, sz, sz, sz, sz]
@@ -214,6 +215,17 @@ def gemv(ty: int, w, n_out: int, k: int, x, rows: int, threads: int = 1) -> np.n
     y = np.full(rows * n_out, np.nan, dtype=np.float32)
     if lib().or_gemv_threads(ty, _p(w), n_out, k, _p(x), rows, _p(y), threads):
         raise ValueError("gemv refused")
+    return y.reshape(rows, n_out)
+
+
+def gate_up_act(ty: int, w, n_out: int, k: int, x, rows: int, threads: int = 1) -> np.ndarray:
+    """GateUpAct{Silu}: w holds 2 n_out rows, gate then up (oracle.c or_gate_up_act)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = _f32(x).ravel()
+    assert w.size == 2 * n_out * row_bytes(ty, k) and x.size >= rows * k
+    y = np.full(rows * n_out, np.nan, dtype=np.float32)
+    if lib().or_gate_up_act(ty, _p(w), n_out, k, _p(x), rows, _p(y), threads):
+        raise ValueError("gate_up_act refused")
     return y.reshape(rows, n_out)
 
 

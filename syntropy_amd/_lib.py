@@ -55,6 +55,8 @@ def lib():
         "syn_q4k_repack_host": [u32, vp, vp, u64, i32],
         "syn_gemv_layout_workspace_bytes": [u32, i32, u32, u32, C.POINTER(C.c_uint64)],
         "syn_gemv_layout": [u32, i32, vp, u64, u32, u32, vp, u32, vp, vp, u64, vp],
+        "syn_gate_up_act_workspace_bytes": [u32, i32, u32, u32, u32, vp],
+        "syn_gate_up_act": [u32, i32, vp, u64, u32, u32, vp, u32, vp, vp, u64, vp],
         "syn_gemv_batch_layout": [u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, u64, vp],
         "syn_gemv_batch_quantized_layout": [u32, u32, vp, vp, vp, vp, vp, vp, u64, vp, vp],
         "syn_moe_route": [vp, vp, u32, u32, u32, u32, i32, vp, vp, vp, vp],

@@ -476,6 +476,38 @@ SYN_EXPORT int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, ui
     return check_launch(W);
 }
 
+SYN_EXPORT int syn_gate_up_act_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t rows, uint32_t n_out,
+                                               uint32_t k_in, uint64_t* bytes) {
+    const char* W = "syn_gate_up_act_workspace_bytes";
+    if (!bytes) return fail(SYN_E_INVALID, "%s: null output", W);
+    uint64_t g = 0;
+    if (int rc = syn_gemv_layout_workspace_bytes(layout, wtype, rows, k_in, &g)) return rc;
+    // the Gemv's workspace, then the stacked product [rows][2 n_out]
+    *bytes = syn::align_up(g, 256) + 8ull * rows * n_out;
+    return SYN_OK;
+}
+
+SYN_EXPORT int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                               uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
+                               void* stream) {
+    const char* W = "syn_gate_up_act";
+    uint64_t need = 0;
+    if (int rc = syn_gate_up_act_workspace_bytes(layout, wtype, rows, n_out, k_in, &need)) return rc;
+    if (rows == 0 || n_out == 0) return SYN_OK;
+    if (n_out > (1u << 29)) return fail(SYN_E_INVALID, "%s: n_out too large", W);
+    if (ws_bytes < need)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)need);
+    if (!ws || !aligned(ws, 256) || !y || !aligned(y, 4))
+        return fail(SYN_E_INVALID, "%s: the workspace must be 256-byte and y 4-byte aligned", W);
+    uint64_t g = 0;
+    (void)syn_gemv_layout_workspace_bytes(layout, wtype, rows, k_in, &g);
+    float* y2 = (float*)((uint8_t*)ws + syn::align_up(g, 256));
+    if (int rc = syn_gemv_layout(layout, wtype, w, w_bytes, 2 * n_out, k_in, x, rows, y2, ws, g, stream)) return rc;
+    syn::launch_silu_mul(y2, (int)rows, (int)n_out, y, (hipStream_t)stream);
+    return check_launch(W);
+}
+
 SYN_EXPORT int syn_quantize(int32_t wtype, const float* x, uint64_t n, void* out,
                             uint64_t out_bytes, void* stream) {
     const char* W = "syn_quantize";

@@ -266,4 +266,26 @@ void launch_gemv_q(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws
     }
 }
 
+// GateUpAct{Silu}: y[r][i] = silu(y2[r][i]) * y2[r][n + i], y2 the Gemv of the stacked
+// [gate; up] weight (crates/kernels/src/reference/linear.rs:75-112 with the quantized dots of
+// the MoE FFN, crates/kernels-cpu/src/moe.rs:529-551: software-exp silu, the product rounded
+// once).  Four outputs per thread.
+__global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ y2, int rows, int n,
+                                                  float* __restrict__ y) {
+    const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int64_t i = i0 + q;
+        if (i >= (int64_t)rows * n) return;
+        const int64_t r = i / n, c = i - r * n;
+        y[i] = ref_silu(y2[r * 2 * n + c]) * y2[r * 2 * n + n + c];
+    }
+}
+
+void launch_silu_mul(const float* y2, int rows, int n, float* y, hipStream_t stream) {
+    const int64_t total = (int64_t)rows * n;
+    if (total == 0) return;
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((total + 1023) / 1024)), dim3(256), 0, stream, y2, rows, n, y);
+}
+
 }  // namespace syn

@@ -251,11 +251,17 @@ uint32_t u32_of(const Json* v, const char* what) {
 // Ops served: keys, shapes, capabilities
 // ============================================================================================
 
-enum class Op { Gemv, MoeGrouped, MoeRoute, MoeCombine, Other };
+// Gemv, Gemm and Logits share one binding (a matrix product: the ggml provider maps all three
+// to mul_mat, crates/kernels-ggml/src/mapping.rs:30); GateUpAct{Silu} takes the stacked
+// [gate; up] weight (:31).
+enum class Op { Gemv, Gemm, Logits, GateUpAct, MoeGrouped, MoeRoute, MoeCombine, Other };
+
+bool dense(Op op) { return op == Op::Gemv || op == Op::Gemm || op == Op::Logits || op == Op::GateUpAct; }
 
 struct Key {
     Op op = Op::Other;
     bool softmax = false;       // MoeRoute's norm
+    bool silu = false;          // GateUpAct's act
     int weight = -1;            // ggml type id of schemes[0] when it is a Ggml scheme
     bool rest_plain_f32 = true;  // every other scheme is Plain(F32)
     size_t n_schemes = 0;
@@ -277,12 +283,18 @@ Key parse_key(const uint8_t* data, size_t len) {
     if (!op) fail(SYN_CLASS_INVALID_REQUEST, 0, "OpKey: no op");
     if (op->kind == Json::Str) {
         if (op->str == "Gemv") k.op = Op::Gemv;
+        else if (op->str == "Gemm") k.op = Op::Gemm;
+        else if (op->str == "Logits") k.op = Op::Logits;
         else if (op->str == "MoeGrouped") k.op = Op::MoeGrouped;
         else if (op->str == "MoeCombine") k.op = Op::MoeCombine;
     } else if (op->kind == Json::Obj && op->obj.size() == 1 && op->obj[0].first == "MoeRoute") {
         k.op = Op::MoeRoute;
         const Json* norm = op->obj[0].second.get("norm");
         k.softmax = norm && norm->kind == Json::Str && norm->str == "Softmax";
+    } else if (op->kind == Json::Obj && op->obj.size() == 1 && op->obj[0].first == "GateUpAct") {
+        k.op = Op::GateUpAct;
+        const Json* act = op->obj[0].second.get("act");
+        k.silu = act && act->kind == Json::Str && act->str == "Silu";
     }
     const Json* schemes = j.get("schemes");
     if (!schemes || schemes->kind != Json::Arr) fail(SYN_CLASS_INVALID_REQUEST, 0, "OpKey: no schemes");
@@ -338,17 +350,27 @@ uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 // (crates/graph/src/ir/signature.rs:149,153).
 bool plan_of(const Key& k, const Shape& s, Plan& p) {
     if (k.variant != 0 || !k.rest_plain_f32) return false;
-    // layout 1 (X8, from repack) is served for Q4_K Gemv weights only
-    if (k.layout != 0 && !(k.layout == SYN_LAYOUT_X8 && k.op == Op::Gemv && k.weight == SYN_Q4_K)) return false;
+    // layout 1 (X8, from repack) is served for the dense products' Q4_K weights only
+    if (k.layout != 0 && !(k.layout == SYN_LAYOUT_X8 && dense(k.op) && k.weight == SYN_Q4_K)) return false;
     p.op = k.op;
     p.rows = s.rows;
     p.layout = k.layout;
     switch (k.op) {
-    case Op::Gemv: {
+    case Op::Gemv:
+    case Op::Gemm:
+    case Op::Logits:
+    case Op::GateUpAct: {
         if (k.weight < 0 || k.n_schemes < 1 || k.n_schemes > 3 || s.dims.size() != 2) return false;
+        if (k.op == Op::GateUpAct && !k.silu) return false;  // GELU gating: no reference form yet
         const uint32_t n_out = s.dims[0], k_in = s.dims[1];
         uint64_t ws = 0;
-        if (syn_gemv_layout_workspace_bytes(k.layout, k.weight, s.rows, k_in, &ws) != SYN_OK) return false;
+        if (k.op == Op::GateUpAct) {
+            if (n_out > (1u << 29) ||
+                syn_gate_up_act_workspace_bytes(k.layout, k.weight, s.rows, n_out, k_in, &ws) != SYN_OK)
+                return false;
+        } else if (syn_gemv_layout_workspace_bytes(k.layout, k.weight, s.rows, k_in, &ws) != SYN_OK) {
+            return false;
+        }
         p.weight = k.weight;
         p.dims[0] = n_out;
         p.dims[1] = k_in;
@@ -412,16 +434,26 @@ std::string caps_json(const Plan& p) {
            ",\"kernel_hash\":" + zeros + ",\"source_key\":" + zeros + "}";
 }
 
-const char* OPS_JSON =
-    "["
-    "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q4_K\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
-    "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q4_K\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":1,\"variant\":0},"
-    "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q8_0\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
-    "{\"op\":\"Gemv\",\"schemes\":[{\"Ggml\":\"Q4_0\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
-    "{\"op\":\"MoeGrouped\",\"schemes\":[{\"Ggml\":\"Q4_K\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
-    "{\"op\":{\"MoeRoute\":{\"norm\":\"Softmax\"}},\"schemes\":[{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
-    "{\"op\":\"MoeCombine\",\"schemes\":[{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0}"
-    "]";
+// ops(): every key served, as the executor's key catalogue (query still decides per shape).
+std::string ops_json() {
+    std::string out = "[";
+    const char* dense_ops[] = {"\"Gemv\"", "\"Gemm\"", "\"Logits\"", "{\"GateUpAct\":{\"act\":\"Silu\"}}"};
+    const char* weights[] = {"Q4_K", "Q8_0", "Q4_0"};
+    for (const char* op : dense_ops)
+        for (const char* w : weights)
+            for (int layout = 0; layout < 2; ++layout) {
+                if (layout == 1 && std::string(w) != "Q4_K") continue;
+                out += std::string("{\"op\":") + op + ",\"schemes\":[{\"Ggml\":\"" + w +
+                       "\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":" + std::to_string(layout) +
+                       ",\"variant\":0},";
+            }
+    out +=
+        "{\"op\":\"MoeGrouped\",\"schemes\":[{\"Ggml\":\"Q4_K\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
+        "{\"op\":{\"MoeRoute\":{\"norm\":\"Softmax\"}},\"schemes\":[{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
+        "{\"op\":\"MoeCombine\",\"schemes\":[{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0}"
+        "]";
+    return out;
+}
 
 // ============================================================================================
 // Contexts
@@ -511,19 +543,30 @@ const SynBufferView& weight(const SynOpArgs& a, size_t i, uint64_t need, const c
 void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
     const uint32_t rows = p.rows;
     switch (p.op) {
-    case Op::Gemv: {
+    case Op::Gemv:
+    case Op::Gemm:
+    case Op::Logits:
+    case Op::GateUpAct: {
+        const bool gated = p.op == Op::GateUpAct;
+        const char* name = gated ? "GateUpAct" : p.op == Op::Gemm ? "Gemm" : p.op == Op::Logits ? "Logits" : "Gemv";
         const uint32_t n_out = p.dims[0], k_in = p.dims[1];
         if (a.n_inputs != 1 || a.n_outputs != 1 || a.n_weights != 1 || a.n_statics != 0)
-            internal("Gemv binds one input, one output, one weight and no constants");
-        const uint8_t* x = tensor(c, a.inputs[0], 0, rows, k_in, 1, 4, "Gemv x");
-        uint8_t* y = tensor(c, a.outputs[0], 0, rows, n_out, 1, 4, "Gemv y");
+            internal(std::string(name) + " binds one input, one output, one weight and no constants");
+        const uint8_t* x = tensor(c, a.inputs[0], 0, rows, k_in, 1, 4, "x");
+        uint8_t* y = tensor(c, a.outputs[0], 0, rows, n_out, 1, 4, "y");
         const int be = p.weight == SYN_Q4_K ? 256 : 32, bb = p.weight == SYN_Q4_K ? 144 : p.weight == SYN_Q8_0 ? 34 : 18;
-        const uint64_t wbytes = (uint64_t)k_in / be * bb * n_out;
-        const SynBufferView& w = weight(a, 0, wbytes, "Gemv");
+        // GateUpAct's weight stacks the gate rows, then the up rows
+        const uint64_t wbytes = (uint64_t)k_in / be * bb * n_out * (gated ? 2 : 1);
+        const SynBufferView& w = weight(a, 0, wbytes, name);
         uint8_t* ws = workspace_of(c, a, p);
-        check_syn(syn_gemv_layout(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in, (const float*)x,
-                                  rows, (float*)y, ws, p.workspace - 256, st),
-                  "Gemv");
+        if (gated)
+            check_syn(syn_gate_up_act(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in, (const float*)x,
+                                      rows, (float*)y, ws, p.workspace - 256, st),
+                      name);
+        else
+            check_syn(syn_gemv_layout(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in, (const float*)x,
+                                      rows, (float*)y, ws, p.workspace - 256, st),
+                      name);
         return;
     }
     case Op::MoeGrouped: {
@@ -667,7 +710,10 @@ SynStatus e_memory_info(void*, uint64_t ctx, SynMemoryInfo* out) {
 }
 
 SynStatus e_ops(void*, SynOutBuf* out) {
-    return call("ops", false, [&] { put(out, OPS_JSON); });
+    return call("ops", false, [&] {
+        static const std::string ops = ops_json();
+        put(out, ops);
+    });
 }
 
 SynStatus e_query(void*, uint64_t ctx, const uint8_t* op, size_t op_len, const uint8_t* shape,
@@ -735,7 +781,7 @@ SynStatus e_set_resident(void*, uint64_t ctx, const SynBuffer*, size_t, uint32_t
 // their GGUF layout (LayoutVersion SOURCE, `present` 0).
 bool repacks(const uint8_t* op, size_t op_len) {
     const Key k = parse_key(op, op_len);
-    return k.op == Op::Gemv && k.weight == SYN_Q4_K && k.layout == 0;
+    return dense(k.op) && k.weight == SYN_Q4_K && k.layout == 0;
 }
 SynStatus e_repack(void*, const uint8_t* op, size_t op_len, const uint8_t* src, size_t src_len, uint8_t* dst,
                    size_t dst_len, uint32_t* present, uint32_t* layout) {

@@ -147,6 +147,27 @@ def gemv(w: Weights, x: torch.Tensor, rows: int, y: torch.Tensor | None = None,
     return y
 
 
+def gate_up_act(w: Weights, x: torch.Tensor, rows: int, y: torch.Tensor | None = None,
+                stream=None) -> torch.Tensor:
+    """GateUpAct{Silu} (crates/kernels/src/reference/linear.rs:75-112): `w` stacks the gate rows
+    then the up rows (w.n_out = 2 n), y F32 [rows, n] = silu(gate x) * (up x), each dot the
+    Gemv value, silu with the reference's software exp, the product rounded once."""
+    if w.n_out % 2:
+        raise GemvError("Len", f"a stacked gate/up matrix has an even row count, not {w.n_out}")
+    n = w.n_out // 2
+    _check_x(x, rows, w.k_in)
+    if y is None:
+        y = torch.empty(rows, n, dtype=torch.float32, device=x.device)
+    elif y.numel() < rows * n:
+        raise GemvError("Len", f"`y` holds {y.numel()} values, the op needs {rows * n}")
+    need = C.c_uint64()
+    call("syn_gate_up_act_workspace_bytes", w.layout, int(w.ty), rows, n, w.k_in, C.byref(need))
+    ws = torch.empty(max(need.value, 256), dtype=torch.uint8, device=x.device)
+    call("syn_gate_up_act", w.layout, int(w.ty), w.bytes.data_ptr(), w.bytes.numel(), n, w.k_in,
+         x.data_ptr(), rows, y.data_ptr(), ws.data_ptr(), ws.numel(), _stream(stream))
+    return y
+
+
 class GemvBatch:
     """Up to 8 independent single-row Q4_K Gemv ops launched together (one batched Q8_K
     quantization, one grouped GEMV): each y[i] equals gemv(ws[i], x[i], 1) bit for bit.  The
@@ -248,4 +269,4 @@ def dequantize(ty: WeightType, src: torch.Tensor, stream=None) -> torch.Tensor:
 __all__ = ["WeightType", "Weights", "GemvError", "SynError", "GemvBatch", "workspace_bytes", "quantize_into",
            "repack", "LAYOUT_SOURCE", "LAYOUT_X8",
            "gemv_quantized", "gemv", "quantize", "dequantize", "new_workspace", "gemm_workspace",
-           "gemm_quantize_into", "gemm_quantized", "lib"]
+           "gemm_quantize_into", "gemm_quantized", "gate_up_act", "lib"]

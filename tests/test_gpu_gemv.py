@@ -318,3 +318,29 @@ def test_every_f16_scale_converts_exactly(S):
     announce("f16 patterns")
     got = host(S.dequantize(o.Q8_0, dev(blocks.ravel()))).reshape(65536, 32)[:, 0]
     assert_same(got, o.dequantize(o.Q8_0, blocks.ravel()).reshape(65536, 32)[:, 0])
+
+
+# ---- GateUpAct{Silu}: the Gemv of the stacked [gate; up] weight, then silu(g) * u --------------
+@pytest.mark.parametrize("ty,rows,n,k", [(o.Q4_K, 1, 1536, 4096), (o.Q4_K, 5, 700, 2048),
+                                         (o.Q4_K, 96, 512, 4096), (o.Q8_0, 1, 1000, 4096),
+                                         (o.Q4_0, 9, 333, 1024)])
+def test_gate_up_act_equals_oracle(S, ty, rows, n, k):
+    rng = GemvRng(ty * 17 + rows * 3 + n)
+    w = gemv_weights(rng, ty, 2 * n, k, o.f16_bits, o.round_bf16)
+    x = gemv_activations(rng, rows, k)
+    announce(f"gate_up_act ty={ty} rows={rows} n={n} k={k}")
+    W = S.Weights(ty, dev(w), 2 * n, k)
+    got = host(S.gate_up_act(W, dev(x.astype(np.float32)), rows))
+    assert_same(got, o.gate_up_act(ty, w, n, k, x, rows, threads=8), "gate_up_act")
+
+
+def test_gate_up_act_x8_layout(S):
+    rng = GemvRng(4242)
+    n, k = 1024, 4096
+    w = gemv_weights(rng, o.Q4_K, 2 * n, k, o.f16_bits, o.round_bf16)
+    for rows in (1, 64):
+        x = gemv_activations(rng, rows, k)
+        announce(f"gate_up_act x8 rows={rows}")
+        W = S.repack(S.Weights(S.WeightType.Q4K, dev(w), 2 * n, k))
+        got = host(S.gate_up_act(W, dev(x.astype(np.float32)), rows))
+        assert_same(got, o.gate_up_act(o.Q4_K, w, n, k, x, rows, threads=8), f"x8 rows {rows}")

@@ -137,12 +137,70 @@ def test_gemv_x8_layout_through_the_provider(cx, rows, n_out, k):
     assert_same(got, o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=8), "provider gemv x8")
 
 
+def dense_key(op, ty, layout=0):
+    return dict(gemv_key(ty), op=op, layout=layout)
+
+
+@pytest.mark.parametrize("op,ty,rows,n_out,k", [
+    ("Gemm", o.Q4_K, 64, 512, 4096), ("Gemm", o.Q8_0, 20, 300, 1024),
+    ("Logits", o.Q4_K, 1, 3000, 2048), ("Logits", o.Q4_0, 2, 777, 512)])
+def test_gemm_and_logits_keys_take_the_gemv_binding(cx, op, ty, rows, n_out, k):
+    """Gemm and Logits are matrix products with Gemv's operands (the ggml provider maps all three
+    to mul_mat, crates/kernels-ggml/src/mapping.rs:30); their values are Gemv's."""
+    P, pr = cx.P, cx.pr
+    rng = GemvRng(ty * 77 + rows)
+    w = gemv_weights(rng, ty, n_out, k, o.f16_bits, o.round_bf16)
+    x = gemv_activations(rng, rows, k)
+    announce(f"provider {op} ty={ty} rows={rows} n_out={n_out} k={k}")
+    key = dense_key(op, ty)
+    assert pr.query(cx.ctx, key, shape(rows, n_out, k)) is not None
+    opp = pr.prepare(cx.ctx, key, shape(rows, n_out, k))
+    wd = dev(w)
+    xb, yb = cx.put(x.astype(np.float32)), cx.empty(4 * rows * n_out)
+    args = P.op_args([P.packed(xb, P.DT_F32, [rows, k])], [P.packed(yb, P.DT_F32, [rows, n_out])],
+                     [P.view(wd.data_ptr(), w.nbytes)], cx.workspace(opp))
+    pr.launch(cx.ctx, cx.s, opp, args)
+    assert_same(cx.get(yb, np.float32, (rows, n_out)), o.gemv(ty, w, n_out, k, x, rows, threads=8), op)
+
+
+@pytest.mark.parametrize("ty,rows,n,k,layout", [(o.Q4_K, 1, 1536, 4096, 0), (o.Q4_K, 40, 512, 2048, 0),
+                                                (o.Q4_K, 1, 1024, 4096, 1), (o.Q8_0, 3, 700, 1024, 0),
+                                                (o.Q4_0, 1, 256, 512, 0)])
+def test_gate_up_act_through_the_provider(cx, ty, rows, n, k, layout):
+    """GateUpAct{Silu}: one weight of 2 n rows, gate then up (mapping.rs:31); y [rows, n]."""
+    P, pr = cx.P, cx.pr
+    rng = GemvRng(ty * 55 + rows + n)
+    w = gemv_weights(rng, ty, 2 * n, k, o.f16_bits, o.round_bf16)
+    x = gemv_activations(rng, rows, k)
+    wl = w
+    if layout:
+        wl = np.zeros_like(w)
+        kb = json.dumps(dense_key({"GateUpAct": {"act": "Silu"}}, ty)).encode()
+        kbuf = (C.c_uint8 * len(kb)).from_buffer_copy(kb)
+        present, lay = C.c_uint32(), C.c_uint32()
+        st = pr.vt.repack(pr.vt.slf, kbuf, len(kb), w.ctypes.data_as(C.POINTER(C.c_uint8)), w.size,
+                          wl.ctypes.data_as(C.POINTER(C.c_uint8)), wl.size, C.byref(present), C.byref(lay))
+        assert st.cls == 0 and (present.value, lay.value) == (1, 1)
+    key = dense_key({"GateUpAct": {"act": "Silu"}}, ty, layout)
+    announce(f"provider gate_up_act ty={ty} rows={rows} n={n} k={k} layout={layout}")
+    assert pr.query(cx.ctx, key, shape(rows, n, k)) is not None
+    opp = pr.prepare(cx.ctx, key, shape(rows, n, k))
+    wd = dev(wl)
+    xb, yb = cx.put(x.astype(np.float32)), cx.empty(4 * rows * n)
+    args = P.op_args([P.packed(xb, P.DT_F32, [rows, k])], [P.packed(yb, P.DT_F32, [rows, n])],
+                     [P.view(wd.data_ptr(), wl.nbytes)], cx.workspace(opp))
+    pr.launch(cx.ctx, cx.s, opp, args)
+    assert_same(cx.get(yb, np.float32, (rows, n)), o.gate_up_act(ty, w, n, k, x, rows, threads=8), "gate_up_act")
+
+
 def test_query_answers_none_for_unserved_shapes(cx):
     pr = cx.pr
     assert pr.query(cx.ctx, gemv_key(o.Q4_K), shape(1, 64, 100)) is None  # k not whole super-blocks
     key = dict(gemv_key(o.Q4_K), schemes=[{"Ggml": "Q6_K"}, {"Plain": "F32"}, {"Plain": "F32"}])
     assert pr.query(cx.ctx, key, shape(1, 64, 256)) is None
     assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=3), shape(1, 64, 256)) is None
+    gelu = dense_key({"GateUpAct": {"act": "Gelu"}}, o.Q4_K)
+    assert pr.query(cx.ctx, gelu, shape(1, 64, 256)) is None  # no reference form of GELU gating
     assert pr.query(cx.ctx, dict(gemv_key(o.Q8_0), layout=1), shape(1, 64, 256)) is None
     assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(8, 64, 1536)) is None  # GEMM: k % 2048
     assert pr.query(cx.ctx, {"op": "Attention", "schemes": [], "layout": 0, "variant": 0},

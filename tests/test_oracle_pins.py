@@ -64,6 +64,26 @@ def test_gemv_hand_computed_cases():
     assert o.gemv(o.Q4_K, w, 1, 256, xk, 1)[0, 0] == 32.0 * 127.0
 
 
+def test_gate_up_act_one_hot_rows():
+    """GateUpAct{Silu} (linear.rs:75-112) on the stacked [gate; up] weight of the ggml binding
+    (kernels-ggml/src/mapping.rs:31): with one-hot Q8_0 rows each dot is one activation code
+    times its scale, so the output pins the row order (gate rows first) and silu(g) * u."""
+    one = o.f16_bits(1.0).to_bytes(2, "little")
+
+    def row(j):
+        return np.frombuffer(one + bytes(1 if i == j else 0 for i in range(32)), np.uint8)
+
+    x = np.linspace(-3.0, 2.5, 32).astype(np.float32)
+    picks = (3, 7, 20, 31)  # gate rows 0, 1; up rows 0, 1
+    w = np.concatenate([row(j) for j in picks])
+    y = o.gate_up_act(o.Q8_0, w, 2, 32, x, 1)[0]
+    dot = [np.float32(o.gemv(o.Q8_0, row(j), 1, 32, x, 1)[0, 0]) for j in picks]
+    want = [np.float32(o.silu(float(dot[i]))) * dot[2 + i] for i in range(2)]
+    assert bits(y).tolist() == bits(np.array(want, np.float32)).tolist()
+    swapped = [np.float32(o.silu(float(dot[2 + i]))) * dot[i] for i in range(2)]
+    assert bits(y).tolist() != bits(np.array(swapped, np.float32)).tolist()
+
+
 def test_gemv_zero_activations_give_positive_zero():
     """gemv/tests.rs:780-795."""
     rng = GemvRng(12)

@@ -93,9 +93,11 @@ def test_build_and_ops_json(pr):
     assert b["version"] == 1 and ["target", "gfx950"] in b["toolchain"]
     ops = pr.ops()
     got = {(json.dumps(k["op"]), k["schemes"][0].get("Ggml"), k["layout"]) for k in ops}
-    assert got == {('"Gemv"', "Q4_K", 0), ('"Gemv"', "Q4_K", 1), ('"Gemv"', "Q8_0", 0), ('"Gemv"', "Q4_0", 0),
-                   ('"MoeGrouped"', "Q4_K", 0), ('{"MoeRoute": {"norm": "Softmax"}}', None, 0),
-                   ('"MoeCombine"', None, 0)}
+    dense = {(op, w, l) for op in ('"Gemv"', '"Gemm"', '"Logits"', '{"GateUpAct": {"act": "Silu"}}')
+             for w, l in (("Q4_K", 0), ("Q4_K", 1), ("Q8_0", 0), ("Q4_0", 0))}
+    assert got == dense | {('"MoeGrouped"', "Q4_K", 0), ('{"MoeRoute": {"norm": "Softmax"}}', None, 0),
+                           ('"MoeCombine"', None, 0)}
+    assert len(ops) == len(got)
     for k in ops:
         assert k["variant"] == 0
 
@@ -151,6 +153,11 @@ def test_repack_of_q4k_gemv_is_the_x8_permutation(pr):
     assert pr.vt.repack(pr.vt.slf, kb, len(key), sp, src.size, dp, dst.size, C.byref(present), C.byref(layout)).cls == 0
     assert (present.value, layout.value) == (1, 1)
     assert (dst == want).all()
+    for dense_op in ("Gemm", "Logits", {"GateUpAct": {"act": "Silu"}}):
+        kd = _key(dense_op, "Q4_K")
+        db = (C.c_uint8 * len(kd)).from_buffer_copy(kd)
+        assert pr.vt.repacked_len(pr.vt.slf, db, len(kd), src.size, C.byref(present), C.byref(n)).cls == 0
+        assert (present.value, n.value) == (1, src.size)
     for other in (_key("Gemv", "Q8_0"), _key("MoeGrouped", "Q4_K"), _key("MoeCombine", None)):
         ob = (C.c_uint8 * len(other)).from_buffer_copy(other)
         assert pr.vt.repacked_len(pr.vt.slf, ob, len(other), 144, C.byref(present), C.byref(n)).cls == 0
