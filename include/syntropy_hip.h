@@ -30,6 +30,8 @@ extern "C" {
 #define SYN_E_WORKSPACE 3    /* the workspace is smaller than the call needs */
 #define SYN_E_DEVICE 4       /* the HIP runtime refused the launch */
 
+#define SYN_F16 1
+#define SYN_BF16 30
 #define SYN_Q4_0 2
 #define SYN_Q8_0 8
 #define SYN_Q4_K 12

@@ -33,9 +33,11 @@ int check_launch(const char* what) {
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
 bool gemv_type(int32_t t) { return t == SYN_Q4_0 || t == SYN_Q8_0 || t == SYN_Q4_K; }
+bool float_type(int32_t t) { return t == SYN_F16 || t == SYN_BF16; }
 
 int check_gemv_shape(const char* what, int32_t wtype, uint32_t rows, uint32_t k_in) {
-    if (!gemv_type(wtype)) return fail(SYN_E_UNSUPPORTED, "%s: weight type %d is not Q4_0, Q8_0 or Q4_K", what, wtype);
+    if (!gemv_type(wtype) && !float_type(wtype))
+        return fail(SYN_E_UNSUPPORTED, "%s: weight type %d is not F16, BF16, Q4_0, Q8_0 or Q4_K", what, wtype);
     const int be = syn::block_elems(wtype);
     if (k_in % (uint32_t)be)
         return fail(SYN_E_INVALID, "%s: a row of %u weights is not whole %d-weight blocks", what, k_in, be);
@@ -88,6 +90,7 @@ SYN_EXPORT int syn_act_quantize(int32_t wtype, const float* x, uint32_t rows, ui
                                 void* ws, uint64_t ws_bytes, void* stream) {
     const char* W = "syn_act_quantize";
     if (int rc = check_gemv_shape(W, wtype, rows, k_in)) return rc;
+    if (float_type(wtype)) return fail(SYN_E_UNSUPPORTED, "%s: F16 and BF16 products take F32 activations", W);
     const uint64_t need = syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
     if ((uint64_t)rows * k_in == 0) return SYN_OK;
     if (!x || !ws) return fail(SYN_E_INVALID, "%s: null x or workspace", W);
@@ -105,6 +108,7 @@ SYN_EXPORT int syn_gemv_quantized(int32_t wtype, const void* w, uint64_t w_bytes
                                   float* y, void* stream) {
     const char* W = "syn_gemv_quantized";
     if (int rc = check_gemv_shape(W, wtype, rows, k_in)) return rc;
+    if (float_type(wtype)) return fail(SYN_E_UNSUPPORTED, "%s: F16 and BF16 products take F32 activations", W);
     if (rows == 0 || n_out == 0) return SYN_OK;
     if (n_out > (1u << 30)) return fail(SYN_E_INVALID, "%s: n_out too large", W);
     const uint64_t row_bytes = (uint64_t)k_in / syn::block_elems(wtype) * syn::block_bytes(wtype);
@@ -145,7 +149,14 @@ SYN_EXPORT int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t
     if (ws_bytes < need_ws)
         return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
                     (unsigned long long)ws_bytes, (unsigned long long)need_ws);
-    if (k_in && (!x || !ws)) return fail(SYN_E_INVALID, "%s: null x or workspace", W);
+    if (k_in && (!x || (!ws && !float_type(wtype)))) return fail(SYN_E_INVALID, "%s: null x or workspace", W);
+    if (float_type(wtype)) {
+        // F32 activations straight into the FMA accumulators: no workspace
+        if ((k_in && (!x || !aligned(x, 4) || !aligned(w, 2))) || !aligned(y, 4))
+            return fail(SYN_E_INVALID, "%s: x and y must be 4-byte and w 2-byte aligned", W);
+        syn::launch_gemv_float(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, x, (int)rows, y, (hipStream_t)stream);
+        return check_launch(W);
+    }
     if ((k_in && (!aligned(x, 16) || !aligned(ws, 256))) || !aligned(y, 4))
         return fail(SYN_E_INVALID, "%s: x must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
     if (wtype == SYN_Q4_K && rows == 1 && k_in > 0 && syn::q4k_dec_supported((int)k_in) && aligned(w, 16)) {

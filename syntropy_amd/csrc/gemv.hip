@@ -266,6 +266,91 @@ void launch_gemv_q(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws
     }
 }
 
+// F16 and BF16 weights (crates/kernels-cpu/src/gemv/portable.rs:30-45 float_rows with the fold
+// of gemv.rs:506-516): per output, 32 F32 accumulators; element i goes into accumulator i % 32
+// with one fused multiply-add, in increasing i; then the halving fold acc[j] += acc[j + h] for
+// h = 16, 8, 4, 2, 1.  Four lanes per weight row: lane j holds accumulators 8j .. 8j + 7 and
+// reads the row's elements 32m + 8j .. + 7 (16 bytes, or one element at a time when k is not a
+// multiple of 8); 64 rows per workgroup.  Activation rows go FR at a time, each weight chunk
+// read once per group.  The activations stay F32 (no quantization).
+template <int BF16, int VEC, int FR>
+__global__ __launch_bounds__(256) void k_gemv_float(const uint8_t* __restrict__ W, int n_out, int k,
+                                                    const float* __restrict__ x, int rows,
+                                                    float* __restrict__ y) {
+    const int j = threadIdx.x & 3;
+    const int row = (int)((blockIdx.x * 256u + threadIdx.x) >> 2);
+    const bool ok = row < n_out;
+    const uint16_t* wr = reinterpret_cast<const uint16_t*>(W + (int64_t)(ok ? row : 0) * k * 2);
+    auto cvt = [](uint32_t h) { return BF16 ? __builtin_bit_cast(float, h << 16) : f16_to_f32(h); };
+    for (int r0 = 0; r0 < rows; r0 += FR) {  // uniform
+        float acc[FR][8];
+#pragma unroll
+        for (int t = 0; t < FR; ++t)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[t][e] = 0.0f;
+        for (int i0 = 8 * j; i0 < k; i0 += 32) {
+            float w[8];
+            if constexpr (VEC) {
+                const uint4 v = *reinterpret_cast<const uint4*>(wr + i0);
+                const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    w[2 * e] = cvt(u[e] & 0xFFFFu);
+                    w[2 * e + 1] = cvt(u[e] >> 16);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) w[e] = i0 + e < k ? cvt(wr[i0 + e]) : 0.0f;
+            }
+#pragma unroll
+            for (int t = 0; t < FR; ++t) {
+                if (r0 + t >= rows) break;  // uniform
+                const float* xr = x + (int64_t)(r0 + t) * k + i0;
+                if constexpr (VEC) {
+                    const float4 a = reinterpret_cast<const float4*>(xr)[0];
+                    const float4 b = reinterpret_cast<const float4*>(xr)[1];
+                    const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[t][e] = __builtin_fmaf(w[e], xv[e], acc[t][e]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (i0 + e < k) acc[t][e] = __builtin_fmaf(w[e], xr[e], acc[t][e]);
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < FR; ++t) {
+            // h = 16: accumulators 8j + e (j < 2) take 8(j + 2) + e; h = 8: lane 0 takes lane 1's
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v16 = __shfl_xor(acc[t][e], 2);
+                if (j < 2) acc[t][e] = acc[t][e] + v16;
+                const float v8 = __shfl_xor(acc[t][e], 1);
+                if (j == 0) acc[t][e] = acc[t][e] + v8;
+            }
+            // h = 4, 2, 1 inside the lane
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[t][e] = acc[t][e] + acc[t][e + 4];
+            acc[t][0] = acc[t][0] + acc[t][2];
+            acc[t][1] = acc[t][1] + acc[t][3];
+            acc[t][0] = acc[t][0] + acc[t][1];
+            if (j == 0 && ok && r0 + t < rows) y[(int64_t)(r0 + t) * n_out + row] = acc[t][0];
+        }
+    }
+}
+
+void launch_gemv_float(int ty, const uint8_t* W, int n_out, int k, const float* x, int rows, float* y,
+                       hipStream_t stream) {
+    const dim3 grid((unsigned)((n_out + 63) / 64));
+    const bool vec = k % 8 == 0 && ((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0;
+    const bool bf = ty == T_BF16;
+    if (vec && bf) hipLaunchKernelGGL((k_gemv_float<1, 1, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y);
+    else if (vec) hipLaunchKernelGGL((k_gemv_float<0, 1, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y);
+    else if (bf) hipLaunchKernelGGL((k_gemv_float<1, 0, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y);
+    else hipLaunchKernelGGL((k_gemv_float<0, 0, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y);
+}
+
 // GateUpAct{Silu}: y[r][i] = silu(y2[r][i]) * y2[r][n + i], y2 the Gemv of the stacked
 // [gate; up] weight (crates/kernels/src/reference/linear.rs:75-112 with the quantized dots of
 // the MoE FFN, crates/kernels-cpu/src/moe.rs:529-551: software-exp silu, the product rounded

@@ -24,6 +24,9 @@ void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* w
 #define SYN_BATCH 8
 void launch_gemv_q4k_batch(int layout, int np, const uint8_t* const* W, const int* n_out, const int* k,
                            const uint8_t* const* ws, float* const* y, hipStream_t stream);
+// Gemv over F16 / BF16 weights (F32 activations, 32 FMA accumulators and the halving fold).
+void launch_gemv_float(int ty, const uint8_t* W, int n_out, int k, const float* x, int rows, float* y,
+                       hipStream_t stream);
 // GateUpAct{Silu}'s gated product over the Gemv of the stacked [gate; up] weight.
 void launch_silu_mul(const float* y2, int rows, int n, float* y, hipStream_t stream);
 // The same over X8 weights with the F32 rows quantized inside the grouped launch (k <= 16384).

@@ -269,6 +269,8 @@ struct Key {
 };
 
 int ggml_id(const std::string& name) {
+    if (name == "F16") return SYN_F16;
+    if (name == "BF16") return SYN_BF16;
     if (name == "Q4_0") return SYN_Q4_0;
     if (name == "Q8_0") return SYN_Q8_0;
     if (name == "Q4_K") return SYN_Q4_K;
@@ -303,9 +305,13 @@ Key parse_key(const uint8_t* data, size_t len) {
         const Json& s = schemes->arr[i];
         const bool plain_f32 = s.kind == Json::Obj && s.obj.size() == 1 && s.obj[0].first == "Plain" &&
                                s.obj[0].second.kind == Json::Str && s.obj[0].second.str == "F32";
+        const bool plain = s.kind == Json::Obj && s.obj.size() == 1 && s.obj[0].first == "Plain" &&
+                           s.obj[0].second.kind == Json::Str;
         if (i == 0 && s.kind == Json::Obj && s.obj.size() == 1 && s.obj[0].first == "Ggml" &&
             s.obj[0].second.kind == Json::Str)
             k.weight = ggml_id(s.obj[0].second.str);
+        else if (i == 0 && plain && (s.obj[0].second.str == "F16" || s.obj[0].second.str == "BF16"))
+            k.weight = s.obj[0].second.str == "F16" ? SYN_F16 : SYN_BF16;  // gemv/entry.rs:41-47
         else if (!plain_f32)
             k.rest_plain_f32 = false;
     }
@@ -338,6 +344,7 @@ struct Plan {
     uint32_t dims[4] = {0, 0, 0, 0};
     uint64_t workspace = 0;  // bytes the executor provides (incl. 256 of alignment slack)
     uint32_t max_block = 0;
+    uint32_t accumulate = 1;  // NumericsWire codes: 0 F32, 1 I32ThenF32
     uint32_t act_in = 0;  // NumericsWire codes: 0 none, 2 Q8Block32, 3 Q8K256
     uint32_t layout = 0;  // the weights' LayoutVersion
 };
@@ -375,8 +382,11 @@ bool plan_of(const Key& k, const Shape& s, Plan& p) {
         p.dims[0] = n_out;
         p.dims[1] = k_in;
         p.workspace = round_up(ws, 64) + 256;
-        p.max_block = k.weight == SYN_Q4_K ? 256 : 32;
-        p.act_in = k.weight == SYN_Q4_K ? 3 : 2;
+        const bool fl = k.weight == SYN_F16 || k.weight == SYN_BF16;
+        // F16 / BF16: F32 accumulation of F32 activations (gemv/entry.rs:89-90)
+        p.accumulate = fl ? 0 : 1;
+        p.max_block = fl ? 0 : k.weight == SYN_Q4_K ? 256 : 32;
+        p.act_in = fl ? 0 : k.weight == SYN_Q4_K ? 3 : 2;
         return true;
     }
     case Op::MoeGrouped: {
@@ -428,7 +438,7 @@ std::string caps_json(const Plan& p) {
     std::snprintf(num, sizeof num,
                   "{\"accumulate\":%u,\"max_block\":%u,\"act_in\":%u,\"group\":0,\"out\":0,"
                   "\"softmax_f32\":%s,\"state_f32\":false}",
-                  route || combine ? 0u : 1u, p.max_block, p.act_in, route ? "true" : "false");
+                  route || combine ? 0u : p.accumulate, p.max_block, p.act_in, route ? "true" : "false");
     return std::string("{\"workspace\":") + std::to_string(p.workspace) + ",\"est\":null,\"layout\":" +
            std::to_string(p.layout) + ",\"capture_safe\":true,\"deterministic\":true,\"numerics\":" + num +
            ",\"kernel_hash\":" + zeros + ",\"source_key\":" + zeros + "}";
@@ -438,13 +448,15 @@ std::string caps_json(const Plan& p) {
 std::string ops_json() {
     std::string out = "[";
     const char* dense_ops[] = {"\"Gemv\"", "\"Gemm\"", "\"Logits\"", "{\"GateUpAct\":{\"act\":\"Silu\"}}"};
-    const char* weights[] = {"Q4_K", "Q8_0", "Q4_0"};
+    const char* weights[] = {"{\"Ggml\":\"Q4_K\"}", "{\"Ggml\":\"Q8_0\"}", "{\"Ggml\":\"Q4_0\"}",
+                             "{\"Ggml\":\"F16\"}", "{\"Ggml\":\"BF16\"}", "{\"Plain\":\"F16\"}",
+                             "{\"Plain\":\"BF16\"}"};
     for (const char* op : dense_ops)
         for (const char* w : weights)
             for (int layout = 0; layout < 2; ++layout) {
-                if (layout == 1 && std::string(w) != "Q4_K") continue;
-                out += std::string("{\"op\":") + op + ",\"schemes\":[{\"Ggml\":\"" + w +
-                       "\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":" + std::to_string(layout) +
+                if (layout == 1 && std::string(w) != "{\"Ggml\":\"Q4_K\"}") continue;
+                out += std::string("{\"op\":") + op + ",\"schemes\":[" + w +
+                       ",{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":" + std::to_string(layout) +
                        ",\"variant\":0},";
             }
     out +=
@@ -554,7 +566,9 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
             internal(std::string(name) + " binds one input, one output, one weight and no constants");
         const uint8_t* x = tensor(c, a.inputs[0], 0, rows, k_in, 1, 4, "x");
         uint8_t* y = tensor(c, a.outputs[0], 0, rows, n_out, 1, 4, "y");
-        const int be = p.weight == SYN_Q4_K ? 256 : 32, bb = p.weight == SYN_Q4_K ? 144 : p.weight == SYN_Q8_0 ? 34 : 18;
+        const bool fl = p.weight == SYN_F16 || p.weight == SYN_BF16;
+        const int be = fl ? 1 : p.weight == SYN_Q4_K ? 256 : 32;
+        const int bb = fl ? 2 : p.weight == SYN_Q4_K ? 144 : p.weight == SYN_Q8_0 ? 34 : 18;
         // GateUpAct's weight stacks the gate rows, then the up rows
         const uint64_t wbytes = (uint64_t)k_in / be * bb * n_out * (gated ? 2 : 1);
         const SynBufferView& w = weight(a, 0, wbytes, name);

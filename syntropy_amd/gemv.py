@@ -17,18 +17,24 @@ from ._lib import SynError, call, lib
 class WeightType(IntEnum):
     """A weight type this module computes (gemv.rs:87-151), by ggml type id."""
 
+    F16 = 1
     Q4_0 = 2
     Q8_0 = 8
     Q4K = 12
+    BF16 = 30
 
     def block_elems(self) -> int:
-        return 256 if self is WeightType.Q4K else 32
+        return {WeightType.F16: 1, WeightType.BF16: 1, WeightType.Q4K: 256}.get(self, 32)
 
     def block_bytes(self) -> int:
-        return {WeightType.Q4_0: 18, WeightType.Q8_0: 34, WeightType.Q4K: 144}[self]
+        return {WeightType.F16: 2, WeightType.BF16: 2, WeightType.Q4_0: 18, WeightType.Q8_0: 34,
+                WeightType.Q4K: 144}[self]
 
     def act(self) -> str:
-        """The activation block a product over this type quantizes to (gemv.rs:145-151)."""
+        """The activation block a product over this type quantizes to (gemv.rs:145-151); F16 and
+        BF16 products take the F32 activations as they are."""
+        if self in (WeightType.F16, WeightType.BF16):
+            return "F32"
         return "Q8K" if self is WeightType.Q4K else "Q8_0"
 
 

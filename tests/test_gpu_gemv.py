@@ -344,3 +344,31 @@ def test_gate_up_act_x8_layout(S):
         W = S.repack(S.Weights(S.WeightType.Q4K, dev(w), 2 * n, k))
         got = host(S.gate_up_act(W, dev(x.astype(np.float32)), rows))
         assert_same(got, o.gate_up_act(o.Q4_K, w, n, k, x, rows, threads=8), f"x8 rows {rows}")
+
+
+# ---- F16 / BF16 weights: 32 FMA accumulators and the halving fold (portable.rs:30-45) ----------
+@pytest.mark.parametrize("ty", [o.F16, o.BF16])
+@pytest.mark.parametrize("rows,n_out,k", [(1, 4096, 4096), (3, 1000, 1024), (9, 64, 4096),
+                                          (7, 513, 40), (2, 100, 33), (1, 5, 7)])
+def test_float_gemv_equals_oracle(S, ty, rows, n_out, k):
+    """Rows of 8-element-aligned k take 16-byte loads, others one element at a time; more than
+    four activation rows run in groups of four over the same weight chunks."""
+    rng = GemvRng(ty * 31 + rows * 7 + k)
+    w = gemv_weights(rng, ty, n_out, k, o.f16_bits, o.round_bf16)
+    x = gemv_activations(rng, rows, k)
+    announce(f"float gemv ty={ty} rows={rows} n_out={n_out} k={k}")
+    got = gpu_gemv(S, ty, w, n_out, k, x, rows)
+    assert_same(got, o.gemv(ty, w, n_out, k, x, rows, threads=8), f"ty {ty}")
+
+
+def test_float_gemv_golden_case(S):
+    """The pinned output bits of crates/kernels-cpu/src/gemv/tests.rs:726-777 on the device."""
+    from test_oracle_pins import PINNED
+    for ty in (o.F16, o.BF16):
+        rng = GemvRng(11)
+        k = gemv_widths(ty)[1]
+        w = gemv_weights(rng, ty, 3, k, o.f16_bits, o.round_bf16)
+        x = gemv_activations(rng, 2, k)
+        announce(f"float gemv golden ty={ty}")
+        got = gpu_gemv(S, ty, w, 3, k, x, 2)
+        assert bits(got).ravel().tolist() == PINNED[ty]

@@ -193,6 +193,28 @@ def test_gate_up_act_through_the_provider(cx, ty, rows, n, k, layout):
     assert_same(cx.get(yb, np.float32, (rows, n)), o.gate_up_act(ty, w, n, k, x, rows, threads=8), "gate_up_act")
 
 
+@pytest.mark.parametrize("scheme,ty", [({"Plain": "F16"}, o.F16), ({"Ggml": "BF16"}, o.BF16)])
+def test_float_gemv_through_the_provider(cx, scheme, ty):
+    """Plain and GGUF F16/BF16 weights (gemv/entry.rs:41-47): F32 accumulation, no workspace
+    beyond the alignment slack, no activation quantization."""
+    P, pr = cx.P, cx.pr
+    rows, n_out, k = 2, 777, 1024
+    rng = GemvRng(ty * 13)
+    w = gemv_weights(rng, ty, n_out, k, o.f16_bits, o.round_bf16)
+    x = gemv_activations(rng, rows, k)
+    key = {"op": "Gemv", "schemes": [scheme, {"Plain": "F32"}, {"Plain": "F32"}], "layout": 0, "variant": 0}
+    caps = pr.query(cx.ctx, key, shape(rows, n_out, k))
+    assert caps is not None and caps["numerics"]["accumulate"] == 0 and caps["numerics"]["act_in"] == 0
+    announce(f"provider float gemv {scheme}")
+    op = pr.prepare(cx.ctx, key, shape(rows, n_out, k))
+    wd = dev(w)
+    xb, yb = cx.put(x.astype(np.float32)), cx.empty(4 * rows * n_out)
+    args = P.op_args([P.packed(xb, P.DT_F32, [rows, k])], [P.packed(yb, P.DT_F32, [rows, n_out])],
+                     [P.view(wd.data_ptr(), w.nbytes)], cx.workspace(op))
+    pr.launch(cx.ctx, cx.s, op, args)
+    assert_same(cx.get(yb, np.float32, (rows, n_out)), o.gemv(ty, w, n_out, k, x, rows, threads=8), "float")
+
+
 def test_query_answers_none_for_unserved_shapes(cx):
     pr = cx.pr
     assert pr.query(cx.ctx, gemv_key(o.Q4_K), shape(1, 64, 100)) is None  # k not whole super-blocks

@@ -92,11 +92,14 @@ def test_build_and_ops_json(pr):
     b = pr.build()
     assert b["version"] == 1 and ["target", "gfx950"] in b["toolchain"]
     ops = pr.ops()
-    got = {(json.dumps(k["op"]), k["schemes"][0].get("Ggml"), k["layout"]) for k in ops}
+    got = {(json.dumps(k["op"]), json.dumps(k["schemes"][0]), k["layout"]) for k in ops}
+    weights = [('{"Ggml": "Q4_K"}', 0), ('{"Ggml": "Q4_K"}', 1), ('{"Ggml": "Q8_0"}', 0), ('{"Ggml": "Q4_0"}', 0),
+               ('{"Ggml": "F16"}', 0), ('{"Ggml": "BF16"}', 0), ('{"Plain": "F16"}', 0), ('{"Plain": "BF16"}', 0)]
     dense = {(op, w, l) for op in ('"Gemv"', '"Gemm"', '"Logits"', '{"GateUpAct": {"act": "Silu"}}')
-             for w, l in (("Q4_K", 0), ("Q4_K", 1), ("Q8_0", 0), ("Q4_0", 0))}
-    assert got == dense | {('"MoeGrouped"', "Q4_K", 0), ('{"MoeRoute": {"norm": "Softmax"}}', None, 0),
-                           ('"MoeCombine"', None, 0)}
+             for w, l in weights}
+    assert got == dense | {('"MoeGrouped"', '{"Ggml": "Q4_K"}', 0),
+                           ('{"MoeRoute": {"norm": "Softmax"}}', '{"Plain": "F32"}', 0),
+                           ('"MoeCombine"', '{"Plain": "F32"}', 0)}
     assert len(ops) == len(got)
     for k in ops:
         assert k["variant"] == 0
