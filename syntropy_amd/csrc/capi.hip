@@ -6,6 +6,7 @@
 #include <string>
 
 #include "../../include/syntropy_hip.h"
+#include "capi_rows.hpp"
 #include "kernels.hpp"
 
 #define SYN_EXPORT extern "C" __attribute__((visibility("default")))
@@ -132,9 +133,9 @@ SYN_EXPORT int syn_gemv_quantized(int32_t wtype, const void* w, uint64_t w_bytes
     return check_launch(W);
 }
 
-SYN_EXPORT int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+int syn_gemv_rows(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
                         uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws,
-                        uint64_t ws_bytes, void* stream) {
+                        uint64_t ws_bytes, void* stream, const uint32_t* active) {
     const char* W = "syn_gemv";
     if (int rc = check_gemv_shape(W, wtype, rows, k_in)) return rc;
     if (rows == 0 || n_out == 0) return SYN_OK;
@@ -154,22 +155,23 @@ SYN_EXPORT int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t
         // F32 activations straight into the FMA accumulators: no workspace
         if ((k_in && (!x || !aligned(x, 4) || !aligned(w, 2))) || !aligned(y, 4))
             return fail(SYN_E_INVALID, "%s: x and y must be 4-byte and w 2-byte aligned", W);
-        syn::launch_gemv_float(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, x, (int)rows, y, (hipStream_t)stream);
+        syn::launch_gemv_float(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, x, (int)rows, y, (hipStream_t)stream,
+                                active);
         return check_launch(W);
     }
     if ((k_in && (!aligned(x, 16) || !aligned(ws, 256))) || !aligned(y, 4))
         return fail(SYN_E_INVALID, "%s: x must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
     if (wtype == SYN_Q4_K && rows == 1 && k_in > 0 && syn::q4k_dec_supported((int)k_in) && aligned(w, 16)) {
         // one launch: the workgroups quantize the row into LDS themselves
-        syn::launch_gemv_q4k_dec_f32((const uint8_t*)w, (int)n_out, (int)k_in, x, y, (hipStream_t)stream);
+        syn::launch_gemv_q4k_dec_f32((const uint8_t*)w, (int)n_out, (int)k_in, x, y, (hipStream_t)stream, active);
         return check_launch(W);
     }
     if (gemm) {
         const syn::GemmAct a = syn::gemm_act_at((uint8_t*)ws, (int64_t)gemm_tpad(rows), (int)k_in);
-        syn::launch_gemm_act(x, (int)rows, (int)k_in, a, (hipStream_t)stream);
+        syn::launch_gemm_act(x, (int)rows, (int)k_in, a, (hipStream_t)stream, active);
         if (int rc = check_launch(W)) return rc;
         syn::launch_gemm_q4k(SYN_LAYOUT_SOURCE, (const uint8_t*)w, (int)n_out, (int)k_in, a, (int)rows, y,
-                             (hipStream_t)stream);
+                             (hipStream_t)stream, active);
         return check_launch(W);
     }
     if (k_in) {
@@ -177,8 +179,14 @@ SYN_EXPORT int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t
         if (int rc = check_launch(W)) return rc;
     }
     syn::launch_gemv_q(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows,
-                       y, (hipStream_t)stream);
+                       y, (hipStream_t)stream, active);
     return check_launch(W);
+}
+
+SYN_EXPORT int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                        uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws,
+                        uint64_t ws_bytes, void* stream) {
+    return syn_gemv_rows(wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, ws_bytes, stream, nullptr);
 }
 
 SYN_EXPORT int syn_gemm_workspace_bytes(uint32_t rows, uint32_t k_in, uint64_t* bytes) {
@@ -350,7 +358,8 @@ namespace {
 // Gemv); the workspace is still sized and checked.
 int gemv_batch_f32(const char* W, uint32_t layout, uint32_t n, const int32_t* wtypes, const void* const* w,
                    const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in, const float* const* x,
-                   float* const* y, void* ws, uint64_t ws_bytes, void* stream, bool fuse) {
+                   float* const* y, void* ws, uint64_t ws_bytes, void* stream, bool fuse,
+                   const uint32_t* active = nullptr) {
     if (n == 0) return SYN_OK;
     if (!w || !x || !y) return fail(SYN_E_INVALID, "%s: null argument array", W);
     if (layout != SYN_LAYOUT_SOURCE && layout != SYN_LAYOUT_X8)
@@ -375,7 +384,7 @@ int gemv_batch_f32(const char* W, uint32_t layout, uint32_t n, const int32_t* wt
         no[i] = (int)n_out[i];
         kk[i] = (int)k_in[i];
     }
-    syn::launch_gemv_q4k_batch_f32(wp, (int)n, no, kk, xp, yp, (hipStream_t)stream);
+    syn::launch_gemv_q4k_batch_f32(wp, (int)n, no, kk, xp, yp, (hipStream_t)stream, active);
     return check_launch(W);
 }
 
@@ -452,11 +461,12 @@ SYN_EXPORT int syn_gemv_layout_workspace_bytes(uint32_t layout, int32_t wtype, u
     return SYN_OK;
 }
 
-SYN_EXPORT int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
                                uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
-                               void* stream) {
+                               void* stream, const uint32_t* active) {
     const char* W = "syn_gemv_layout";
-    if (layout == SYN_LAYOUT_SOURCE) return syn_gemv(wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, ws_bytes, stream);
+    if (layout == SYN_LAYOUT_SOURCE)
+        return syn_gemv_rows(wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, ws_bytes, stream, active);
     uint64_t need = 0;
     if (int rc = syn_gemv_layout_workspace_bytes(layout, wtype, rows, k_in, &need)) return rc;
     if (rows == 0 || n_out == 0) return SYN_OK;
@@ -466,7 +476,7 @@ SYN_EXPORT int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, ui
         const void* ws_[1] = {w};
         const int32_t ts[1] = {wtype};
         const uint64_t wb[1] = {w_bytes};
-        return gemv_batch_f32(W, layout, 1, ts, ws_, wb, &n_out, &k_in, xs, ys, ws, ws_bytes, stream, true);
+        return gemv_batch_f32(W, layout, 1, ts, ws_, wb, &n_out, &k_in, xs, ys, ws, ws_bytes, stream, true, active);
     }
     if (!syn::gemm_q4k_supported((int)n_out, (int)k_in))
         return fail(SYN_E_UNSUPPORTED, "%s: a %u x %u matrix is larger than 4 GiB", W, n_out, k_in);
@@ -481,10 +491,17 @@ SYN_EXPORT int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, ui
     if (!aligned(w, 16) || !aligned(x, 16) || !aligned(ws, 256) || !aligned(y, 4))
         return fail(SYN_E_INVALID, "%s: w and x must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
     const syn::GemmAct a = syn::gemm_act_at((uint8_t*)ws, (int64_t)gemm_tpad(rows), (int)k_in);
-    syn::launch_gemm_act(x, (int)rows, (int)k_in, a, (hipStream_t)stream);
+    syn::launch_gemm_act(x, (int)rows, (int)k_in, a, (hipStream_t)stream, active);
     if (int rc = check_launch(W)) return rc;
-    syn::launch_gemm_q4k(SYN_LAYOUT_X8, (const uint8_t*)w, (int)n_out, (int)k_in, a, (int)rows, y, (hipStream_t)stream);
+    syn::launch_gemm_q4k(SYN_LAYOUT_X8, (const uint8_t*)w, (int)n_out, (int)k_in, a, (int)rows, y, (hipStream_t)stream,
+                         active);
     return check_launch(W);
+}
+
+SYN_EXPORT int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                               uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
+                               void* stream) {
+    return syn_gemv_layout_rows(layout, wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, ws_bytes, stream, nullptr);
 }
 
 SYN_EXPORT int syn_gate_up_act_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t rows, uint32_t n_out,
@@ -498,9 +515,9 @@ SYN_EXPORT int syn_gate_up_act_workspace_bytes(uint32_t layout, int32_t wtype, u
     return SYN_OK;
 }
 
-SYN_EXPORT int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+int syn_gate_up_act_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
                                uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
-                               void* stream) {
+                               void* stream, const uint32_t* active) {
     const char* W = "syn_gate_up_act";
     uint64_t need = 0;
     if (int rc = syn_gate_up_act_workspace_bytes(layout, wtype, rows, n_out, k_in, &need)) return rc;
@@ -514,9 +531,16 @@ SYN_EXPORT int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, ui
     uint64_t g = 0;
     (void)syn_gemv_layout_workspace_bytes(layout, wtype, rows, k_in, &g);
     float* y2 = (float*)((uint8_t*)ws + syn::align_up(g, 256));
-    if (int rc = syn_gemv_layout(layout, wtype, w, w_bytes, 2 * n_out, k_in, x, rows, y2, ws, g, stream)) return rc;
-    syn::launch_silu_mul(y2, (int)rows, (int)n_out, y, (hipStream_t)stream);
+    if (int rc = syn_gemv_layout_rows(layout, wtype, w, w_bytes, 2 * n_out, k_in, x, rows, y2, ws, g, stream, active))
+        return rc;
+    syn::launch_silu_mul(y2, (int)rows, (int)n_out, y, (hipStream_t)stream, active);
     return check_launch(W);
+}
+
+SYN_EXPORT int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                               uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
+                               void* stream) {
+    return syn_gate_up_act_rows(layout, wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, ws_bytes, stream, nullptr);
 }
 
 SYN_EXPORT int syn_quantize(int32_t wtype, const float* x, uint64_t n, void* out,
@@ -626,9 +650,9 @@ int check_moe_shape(const char* W, uint32_t n_experts, uint32_t top_k, uint32_t 
 
 }  // namespace
 
-SYN_EXPORT int syn_moe_route(const float* router, const float* x, uint32_t rows, uint32_t hidden,
+int syn_moe_route_rows(const float* router, const float* x, uint32_t rows, uint32_t hidden,
                              uint32_t n_experts, uint32_t top_k, int32_t renormalize,
-                             int32_t* ids, float* w, float* probs, void* stream) {
+                             int32_t* ids, float* w, float* probs, void* stream, const uint32_t* active) {
     const char* W = "syn_moe_route";
     if (n_experts == 0 || n_experts > 256) return fail(SYN_E_UNSUPPORTED, "%s: n_experts %u (1..256)", W, n_experts);
     if (top_k == 0 || top_k > n_experts || top_k > 32) return fail(SYN_E_UNSUPPORTED, "%s: top_k %u", W, top_k);
@@ -639,8 +663,14 @@ SYN_EXPORT int syn_moe_route(const float* router, const float* x, uint32_t rows,
     if (!aligned(router, 16) || !aligned(x, 4)) return fail(SYN_E_INVALID, "%s: router must be 16-byte aligned", W);
     // the logits are staged in probs, row by row, before the softmax overwrites them
     syn::launch_moe_route(router, x, (int)rows, (int)hidden, (int)n_experts, (int)top_k, renormalize != 0,
-                          ids, w, probs, probs, (hipStream_t)stream);
+                          ids, w, probs, probs, (hipStream_t)stream, active);
     return check_launch(W);
+}
+
+SYN_EXPORT int syn_moe_route(const float* router, const float* x, uint32_t rows, uint32_t hidden,
+                             uint32_t n_experts, uint32_t top_k, int32_t renormalize,
+                             int32_t* ids, float* w, float* probs, void* stream) {
+    return syn_moe_route_rows(router, x, rows, hidden, n_experts, top_k, renormalize, ids, w, probs, stream, nullptr);
 }
 
 SYN_EXPORT int syn_moe_pack(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
@@ -664,11 +694,11 @@ SYN_EXPORT int syn_moe_grouped_workspace_bytes(int32_t wtype, uint32_t n_experts
     return SYN_OK;
 }
 
-SYN_EXPORT int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, const void* down,
+int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const void* down,
                                uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k,
                                uint32_t hidden, uint32_t inter, const float* x, const int32_t* ids,
                                uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
-                               uint32_t* status, void* stream) {
+                               uint32_t* status, void* stream, const uint32_t* active) {
     const char* W = "syn_moe_grouped";
     if (wtype != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: expert weight type %d (Q4_K)", W, wtype);
     if (int rc = check_moe_shape(W, n_experts, top_k, hidden, inter, rows)) return rc;
@@ -690,7 +720,7 @@ SYN_EXPORT int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, 
     uint32_t* err = (uint32_t*)(base + m.err);
     const int ent = (int)(rows * top_k);
     hipStream_t st = (hipStream_t)stream;
-    syn::launch_moe_pack(ids, ent, (int)n_experts, offsets, slots, err, st);
+    syn::launch_moe_pack(ids, ent, (int)n_experts, offsets, slots, err, st, active, (int)top_k);
     if (m.gemm) {
         const syn::MoeTiles mt{(uint32_t*)(base + m.pad_off), (uint32_t*)(base + m.tile_e),
                                (uint32_t*)(base + m.n_tiles)};
@@ -713,11 +743,11 @@ SYN_EXPORT int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, 
     }
     const syn::MoeAct ax = syn::moe_act_at(base + m.xq, ent, (int)hidden);
     const syn::MoeAct ah = syn::moe_act_at(base + m.hq, ent, (int)inter);
-    syn::launch_moe_gather_q8k(x, slots, ent, (int)top_k, (int)hidden, err, ax, 1, st);
+    syn::launch_moe_gather_q8k(x, slots, ent, (int)top_k, (int)hidden, err, ax, 1, st, offsets + n_experts);
     float* h = (float*)(base + m.h);
     syn::launch_moe_gateup((const uint8_t*)gate, (const uint8_t*)up, (int)n_experts, (int)hidden, (int)inter,
                            offsets, ent, ax, err, h, st);
-    syn::launch_moe_gather_q8k(h, slots, ent, (int)top_k, (int)inter, err, ah, 0, st);
+    syn::launch_moe_gather_q8k(h, slots, ent, (int)top_k, (int)inter, err, ah, 0, st, offsets + n_experts);
     syn::launch_moe_down((const uint8_t*)down, (int)n_experts, (int)hidden, (int)inter, offsets, ent, ah,
                          slots, err, out, st);
     if (status) {
@@ -727,12 +757,25 @@ SYN_EXPORT int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, 
     return check_launch(W);
 }
 
-SYN_EXPORT int syn_moe_combine(const float* out, const int32_t* ids, const float* w, uint32_t rows,
-                               uint32_t top_k, uint32_t hidden, float* y, void* stream) {
+SYN_EXPORT int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, const void* down,
+                               uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k,
+                               uint32_t hidden, uint32_t inter, const float* x, const int32_t* ids,
+                               uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
+                               uint32_t* status, void* stream) {
+    return syn_moe_grouped_rows(wtype, gate, up, down, expert_bytes_each, n_experts, top_k, hidden, inter, x, ids, rows, out, ws, ws_bytes, status, stream, nullptr);
+}
+
+int syn_moe_combine_rows(const float* out, const int32_t* ids, const float* w, uint32_t rows,
+                               uint32_t top_k, uint32_t hidden, float* y, void* stream, const uint32_t* active) {
     const char* W = "syn_moe_combine";
     if (top_k == 0 || top_k > 64) return fail(SYN_E_UNSUPPORTED, "%s: top_k %u (1..64)", W, top_k);
     if (rows == 0 || hidden == 0) return SYN_OK;
     if (!out || !ids || !w || !y) return fail(SYN_E_INVALID, "%s: null operand", W);
-    syn::launch_moe_combine(out, ids, w, (int)rows, (int)top_k, (int)hidden, y, (hipStream_t)stream);
+    syn::launch_moe_combine(out, ids, w, (int)rows, (int)top_k, (int)hidden, y, (hipStream_t)stream, active);
     return check_launch(W);
+}
+
+SYN_EXPORT int syn_moe_combine(const float* out, const int32_t* ids, const float* w, uint32_t rows,
+                               uint32_t top_k, uint32_t hidden, float* y, void* stream) {
+    return syn_moe_combine_rows(out, ids, w, rows, top_k, hidden, y, stream, nullptr);
 }

@@ -111,7 +111,9 @@ SYN_DEV void gemm_act_block(const float* __restrict__ row, int b, int t, GemmAct
     }
 }
 
-__global__ __launch_bounds__(256) void k_gemm_act(const float* __restrict__ x, int T, int k, GemmAct a) {
+__global__ __launch_bounds__(256) void k_gemm_act(const float* __restrict__ x, int T, int k, GemmAct a,
+                                                  const uint32_t* __restrict__ active) {
+    T = active_rows(active, 0, T);  // inactive rows are written as padding
     const int nb = k / 256, lane = threadIdx.x & 63;
     const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (item >= (int64_t)nb * a.tpad) return;
@@ -119,10 +121,10 @@ __global__ __launch_bounds__(256) void k_gemm_act(const float* __restrict__ x, i
     gemm_act_block(t < T ? x + (int64_t)t * k : nullptr, b, t, a, lane);
 }
 
-void launch_gemm_act(const float* x, int T, int k, GemmAct a, hipStream_t stream) {
+void launch_gemm_act(const float* x, int T, int k, GemmAct a, hipStream_t stream, const uint32_t* active) {
     const int64_t items = (int64_t)(k / 256) * a.tpad;
     if (items == 0) return;
-    hipLaunchKernelGGL(k_gemm_act, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, x, T, k, a);
+    hipLaunchKernelGGL(k_gemm_act, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, x, T, k, a, active);
 }
 
 // ============================================================================================
@@ -155,6 +157,7 @@ struct GemmArgs {
     float* y;
     int N, T, nb, tpad;
     uint32_t rb;  // weight row bytes
+    const uint32_t* active;  // a step descriptor's rows_active, or null
 };
 
 // The lane's 32-bit offsets of its loads of one stage, relative to the part's base of the
@@ -315,6 +318,8 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_q4k(GemmArgs g) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: slot choices in SGPRs
     const int n0 = blockIdx.x * GM_ROWS, t0 = blockIdx.y * GM_TT;
+    const int T = active_rows(g.active, 0, g.T);
+    if (t0 >= T) return;  // uniform: a token tile past the step's active rows
     const GemmSlots sl = gemm_slots(g, wave, lane, n0, t0);
     const int live = sl.nw + GM_ASLOT / GM_WAVES + sl.nt;  // loads per stage of this wavefront
     v4f acc[GM_MT][GM_NT];
@@ -344,7 +349,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_q4k(GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = t0 + 16 * mt + 4 * p + i;
-                if (t < g.T && n < g.N) g.y[(int64_t)t * g.N + n] = acc[mt][nt][i];
+                if (t < T && n < g.N) g.y[(int64_t)t * g.N + n] = acc[mt][nt][i];
             }
         }
 }
@@ -355,8 +360,9 @@ bool gemm_q4k_supported(int n_out, int k) {
 }
 
 void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, int T, float* y,
-                     hipStream_t stream) {
-    GemmArgs g;
+                     hipStream_t stream, const uint32_t* active) {
+    GemmArgs g{};
+    g.active = active;
     g.W = W;
     g.layout = layout;
     g.codes = a.codes;

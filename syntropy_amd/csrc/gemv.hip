@@ -115,7 +115,10 @@ SYN_DEV float q32_term(uint32_t dw16, const uint32_t* qs, const ActPtrs& a, int 
 template <int FMT, int P, int R, int VEC>
 __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W, int n_out, int nb,
                                               int64_t row_bytes, ActPtrs act, int rows,
-                                              float* __restrict__ y, int64_t y_stride) {
+                                              float* __restrict__ y, int64_t y_stride,
+                                              const uint32_t* __restrict__ active, int first) {
+    rows = active_rows(active, first, rows);
+    if (rows == 0) return;  // uniform
     using F = Fmt<FMT>;
     using Gm = Geo<FMT, P>;
     constexpr int G = Gm::G, C = Gm::C, BB = F::BB;
@@ -207,7 +210,7 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W, int
 
 template <int FMT, int P, int R>
 static void launch_fmt(const uint8_t* W, int n_out, int k, const ActPtrs& a, int rows, float* y,
-                       int64_t y_stride, hipStream_t stream) {
+                       int64_t y_stride, const uint32_t* active, int first, hipStream_t stream) {
     const int nb = k / Fmt<FMT>::BE;
     const int64_t row_bytes = (int64_t)nb * Fmt<FMT>::BB;
     constexpr int G = Geo<FMT, P>::G;
@@ -215,39 +218,39 @@ static void launch_fmt(const uint8_t* W, int n_out, int k, const ActPtrs& a, int
     const bool vec16 = (row_bytes % 16 == 0) && ((uintptr_t)W % 16 == 0);
     if (vec16)
         hipLaunchKernelGGL((k_gemv<FMT, P, R, 16>), grid, dim3(256), 0, stream, W, n_out, nb,
-                           row_bytes, a, rows, y, y_stride);
+                           row_bytes, a, rows, y, y_stride, active, first);
     else
         hipLaunchKernelGGL((k_gemv<FMT, P, R, 1>), grid, dim3(256), 0, stream, W, n_out, nb,
-                           row_bytes, a, rows, y, y_stride);
+                           row_bytes, a, rows, y, y_stride, active, first);
 }
 
 template <int FMT, int P>
 static void launch_rows(const uint8_t* W, int n_out, int k, const ActPtrs& a, int rows, float* y,
-                        int64_t y_stride, hipStream_t stream) {
+                        int64_t y_stride, const uint32_t* active, int first, hipStream_t stream) {
     if (rows <= 1)
-        launch_fmt<FMT, P, 1>(W, n_out, k, a, rows, y, y_stride, stream);
+        launch_fmt<FMT, P, 1>(W, n_out, k, a, rows, y, y_stride, active, first, stream);
     else if (rows <= 2)
-        launch_fmt<FMT, P, 2>(W, n_out, k, a, rows, y, y_stride, stream);
+        launch_fmt<FMT, P, 2>(W, n_out, k, a, rows, y, y_stride, active, first, stream);
     else if (rows <= 4)
-        launch_fmt<FMT, P, 4>(W, n_out, k, a, rows, y, y_stride, stream);
+        launch_fmt<FMT, P, 4>(W, n_out, k, a, rows, y, y_stride, active, first, stream);
     else
-        launch_fmt<FMT, P, 8>(W, n_out, k, a, rows, y, y_stride, stream);
+        launch_fmt<FMT, P, 8>(W, n_out, k, a, rows, y, y_stride, active, first, stream);
 }
 
 template <int FMT>
 static void launch_p(const uint8_t* W, int n_out, int k, const ActPtrs& a, int rows, float* y,
-                     int64_t y_stride, hipStream_t stream) {
+                     int64_t y_stride, const uint32_t* active, int first, hipStream_t stream) {
     const int nb = k / Fmt<FMT>::BE;
     if (nb >= 12)
-        launch_rows<FMT, 16>(W, n_out, k, a, rows, y, y_stride, stream);
+        launch_rows<FMT, 16>(W, n_out, k, a, rows, y, y_stride, active, first, stream);
     else
-        launch_rows<FMT, 4>(W, n_out, k, a, rows, y, y_stride, stream);
+        launch_rows<FMT, 4>(W, n_out, k, a, rows, y, y_stride, active, first, stream);
 }
 
 // y[r][o] for r < rows, o < n_out, from activations already quantized into `ws` (layout
 // act_layout(act_kind(ty), rows, k)).  Rows are taken 8 at a time.
 void launch_gemv_q(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws, int rows,
-                   float* y, hipStream_t stream) {
+                   float* y, hipStream_t stream, const uint32_t* active) {
     const ActLayout L = act_layout(act_kind(ty), (uint64_t)rows, (uint64_t)k);
     for (int r0 = 0; r0 < rows; r0 += 8) {
         const int nr = rows - r0 < 8 ? rows - r0 : 8;
@@ -258,9 +261,9 @@ void launch_gemv_q(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws
         a.s = reinterpret_cast<const int32_t*>(ws + L.sums) + (int64_t)r0 * (k / 32);
         float* yr = y + (int64_t)r0 * n_out;
         switch (ty) {
-        case T_Q4_K: launch_p<T_Q4_K>(W, n_out, k, a, nr, yr, n_out, stream); break;
-        case T_Q4_0: launch_p<T_Q4_0>(W, n_out, k, a, nr, yr, n_out, stream); break;
-        case T_Q8_0: launch_p<T_Q8_0>(W, n_out, k, a, nr, yr, n_out, stream); break;
+        case T_Q4_K: launch_p<T_Q4_K>(W, n_out, k, a, nr, yr, n_out, active, r0, stream); break;
+        case T_Q4_0: launch_p<T_Q4_0>(W, n_out, k, a, nr, yr, n_out, active, r0, stream); break;
+        case T_Q8_0: launch_p<T_Q8_0>(W, n_out, k, a, nr, yr, n_out, active, r0, stream); break;
         default: break;
         }
     }
@@ -276,7 +279,9 @@ void launch_gemv_q(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws
 template <int BF16, int VEC, int FR>
 __global__ __launch_bounds__(256) void k_gemv_float(const uint8_t* __restrict__ W, int n_out, int k,
                                                     const float* __restrict__ x, int rows,
-                                                    float* __restrict__ y) {
+                                                    float* __restrict__ y,
+                                                    const uint32_t* __restrict__ active) {
+    rows = active_rows(active, 0, rows);
     const int j = threadIdx.x & 3;
     const int row = (int)((blockIdx.x * 256u + threadIdx.x) >> 2);
     const bool ok = row < n_out;
@@ -341,14 +346,18 @@ __global__ __launch_bounds__(256) void k_gemv_float(const uint8_t* __restrict__ 
 }
 
 void launch_gemv_float(int ty, const uint8_t* W, int n_out, int k, const float* x, int rows, float* y,
-                       hipStream_t stream) {
+                       hipStream_t stream, const uint32_t* active) {
     const dim3 grid((unsigned)((n_out + 63) / 64));
     const bool vec = k % 8 == 0 && ((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0;
     const bool bf = ty == T_BF16;
-    if (vec && bf) hipLaunchKernelGGL((k_gemv_float<1, 1, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y);
-    else if (vec) hipLaunchKernelGGL((k_gemv_float<0, 1, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y);
-    else if (bf) hipLaunchKernelGGL((k_gemv_float<1, 0, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y);
-    else hipLaunchKernelGGL((k_gemv_float<0, 0, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y);
+    if (vec && bf)
+        hipLaunchKernelGGL((k_gemv_float<1, 1, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y, active);
+    else if (vec)
+        hipLaunchKernelGGL((k_gemv_float<0, 1, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y, active);
+    else if (bf)
+        hipLaunchKernelGGL((k_gemv_float<1, 0, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y, active);
+    else
+        hipLaunchKernelGGL((k_gemv_float<0, 0, 4>), grid, dim3(256), 0, stream, W, n_out, k, x, rows, y, active);
 }
 
 // GateUpAct{Silu}: y[r][i] = silu(y2[r][i]) * y2[r][n + i], y2 the Gemv of the stacked
@@ -356,7 +365,8 @@ void launch_gemv_float(int ty, const uint8_t* W, int n_out, int k, const float* 
 // the MoE FFN, crates/kernels-cpu/src/moe.rs:529-551: software-exp silu, the product rounded
 // once).  Four outputs per thread.
 __global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ y2, int rows, int n,
-                                                  float* __restrict__ y) {
+                                                  float* __restrict__ y, const uint32_t* __restrict__ active) {
+    rows = active_rows(active, 0, rows);
     const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -367,10 +377,11 @@ __global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ y2, 
     }
 }
 
-void launch_silu_mul(const float* y2, int rows, int n, float* y, hipStream_t stream) {
+void launch_silu_mul(const float* y2, int rows, int n, float* y, hipStream_t stream, const uint32_t* active) {
     const int64_t total = (int64_t)rows * n;
     if (total == 0) return;
-    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((total + 1023) / 1024)), dim3(256), 0, stream, y2, rows, n, y);
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((total + 1023) / 1024)), dim3(256), 0, stream, y2, rows, n, y,
+                       active);
 }
 
 }  // namespace syn

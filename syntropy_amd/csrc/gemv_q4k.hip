@@ -246,7 +246,9 @@ __global__ __launch_bounds__(256) void k_gemv_q4k_dec(const uint8_t* __restrict_
                                                       const int8_t* __restrict__ xq,
                                                       const float* __restrict__ xd,
                                                       const int32_t* __restrict__ xs,
-                                                      float* __restrict__ y) {
+                                                      float* __restrict__ y,
+                                                      const uint32_t* __restrict__ active) {
+    if (active_rows(active, 0, 1) == 0) return;  // a step with no active row
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = (blockIdx.x * 4 + wave) * 4 + (lane >> 4);
@@ -270,6 +272,7 @@ struct DecBatch {
     const uint8_t* W[SYN_BATCH];
     const uint8_t* ws[SYN_BATCH];  // FUSE = 0: the Q8_K row, quantized beforehand
     const float* x[SYN_BATCH];     // FUSE = 1: the F32 row, quantized by every workgroup
+    const uint32_t* active;        // FUSE = 1: a step descriptor's rows_active (0: skip), or null
     float* y[SYN_BATCH];
     int n_out[SYN_BATCH];
     int nb[SYN_BATCH];
@@ -304,6 +307,7 @@ template <int LAYOUT, int FUSE>
 __global__ __launch_bounds__(64 * dec_waves<LAYOUT>())
 __attribute__((amdgpu_waves_per_eu(dec_occupancy<LAYOUT, FUSE>())))
 void k_gemv_q4k_batch(DecBatch bt) {
+    if (active_rows(bt.active, 0, 1) == 0) return;  // a step with no active row
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int WAVES = dec_waves<LAYOUT>();
     int p = 0;
@@ -399,13 +403,14 @@ bool q4k_dec_supported(int k) { return k % 256 == 0 && k > 0 && k <= 32768; }
 
 template <int FUSE>
 static void launch_dec(const uint8_t* W, int n_out, int nb, const float* xf, const int8_t* xq,
-                       const float* xd, const int32_t* xs, float* y, hipStream_t stream) {
+                       const float* xd, const int32_t* xs, float* y, hipStream_t stream,
+                       const uint32_t* active = nullptr) {
     const int total_rg = (n_out + 3) / 4;
     const dim3 grid((unsigned)((total_rg + 3) / 4));
     const size_t lds = q4k_dec_lds(nb);
 #define SYN_DEC(NR)                                                                         \
     hipLaunchKernelGGL((k_gemv_q4k_dec<FUSE, 0, NR>), grid, dim3(256), lds, stream, W, n_out, nb, \
-                       xf, xq, xd, xs, y)
+                       xf, xq, xd, xs, y, active)
     switch ((nb + 15) / 16) {
     case 1: SYN_DEC(1); break;
     case 2: SYN_DEC(2); break;
@@ -420,8 +425,8 @@ static void launch_dec(const uint8_t* W, int n_out, int nb, const float* xf, con
 }
 
 void launch_gemv_q4k_dec_f32(const uint8_t* W, int n_out, int k, const float* x, float* y,
-                             hipStream_t stream) {
-    launch_dec<1>(W, n_out, k / 256, x, nullptr, nullptr, nullptr, y, stream);
+                             hipStream_t stream, const uint32_t* active) {
+    launch_dec<1>(W, n_out, k / 256, x, nullptr, nullptr, nullptr, y, stream, active);
 }
 
 void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* ws, float* y,
@@ -435,10 +440,11 @@ void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* w
 template <int LAYOUT, int FUSE>
 static void launch_batch(int np, const uint8_t* const* W, const int* n_out, const int* k,
                          const uint8_t* const* ws, const float* const* x, float* const* y,
-                         hipStream_t stream) {
+                         hipStream_t stream, const uint32_t* active = nullptr) {
     constexpr int WAVES = dec_waves<LAYOUT>();
     DecBatch bt{};
     bt.np = np;
+    bt.active = active;
     int wg = 0, max_nb = 0;
     for (int p = 0; p < np; ++p) {
         bt.W[p] = W[p];
@@ -471,8 +477,9 @@ void launch_gemv_q4k_batch(int layout, int np, const uint8_t* const* W, const in
 bool gemv_q4k_batch_fusable(int k) { return k % 256 == 0 && k > 0 && k <= 64 * 256; }
 
 void launch_gemv_q4k_batch_f32(const uint8_t* const* W, int np, const int* n_out, const int* k,
-                               const float* const* x, float* const* y, hipStream_t stream) {
-    launch_batch<LAYOUT_X8, 1>(np, W, n_out, k, nullptr, x, y, stream);
+                               const float* const* x, float* const* y, hipStream_t stream,
+                               const uint32_t* active) {
+    launch_batch<LAYOUT_X8, 1>(np, W, n_out, k, nullptr, x, y, stream, active);
 }
 
 // ---- the x8 repack: a permutation of whole 16-byte chunks --------------------------------------

@@ -13,11 +13,11 @@ void launch_act_quant(int kind, const float* x, uint64_t rows, uint64_t k, uint8
                       hipStream_t stream);
 // gemv.hip
 void launch_gemv_q(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws, int rows,
-                   float* y, hipStream_t stream);
+                   float* y, hipStream_t stream, const uint32_t* active = nullptr);
 // gemv_q4k.hip: the Q4_K single-row decode kernel (activation row in LDS)
 bool q4k_dec_supported(int k);
 void launch_gemv_q4k_dec_f32(const uint8_t* W, int n_out, int k, const float* x, float* y,
-                             hipStream_t stream);
+                             hipStream_t stream, const uint32_t* active = nullptr);
 void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* ws, float* y,
                             hipStream_t stream);
 // The most problems one grouped launch takes.
@@ -26,13 +26,14 @@ void launch_gemv_q4k_batch(int layout, int np, const uint8_t* const* W, const in
                            const uint8_t* const* ws, float* const* y, hipStream_t stream);
 // Gemv over F16 / BF16 weights (F32 activations, 32 FMA accumulators and the halving fold).
 void launch_gemv_float(int ty, const uint8_t* W, int n_out, int k, const float* x, int rows, float* y,
-                       hipStream_t stream);
+                       hipStream_t stream, const uint32_t* active = nullptr);
 // GateUpAct{Silu}'s gated product over the Gemv of the stacked [gate; up] weight.
-void launch_silu_mul(const float* y2, int rows, int n, float* y, hipStream_t stream);
+void launch_silu_mul(const float* y2, int rows, int n, float* y, hipStream_t stream, const uint32_t* active = nullptr);
 // The same over X8 weights with the F32 rows quantized inside the grouped launch (k <= 16384).
 bool gemv_q4k_batch_fusable(int k);
 void launch_gemv_q4k_batch_f32(const uint8_t* const* W, int np, const int* n_out, const int* k,
-                               const float* const* x, float* const* y, hipStream_t stream);
+                               const float* const* x, float* const* y, hipStream_t stream,
+                               const uint32_t* active = nullptr);
 // The X8 repack of a Q4_K matrix of nblocks super-blocks (inverse = 1: back to the GGUF order).
 void launch_q4k_x8(const uint8_t* src, uint8_t* dst, uint64_t nblocks, int inverse, hipStream_t stream);
 void launch_act_quant_batch(int np, const float* const* x, const int* k, uint8_t* const* ws,
@@ -41,9 +42,9 @@ void launch_act_quant_batch(int np, const float* const* x, const int* k, uint8_t
 bool moe_route_supported(int hidden);
 void launch_moe_route(const float* router, const float* x, int rows, int hidden, int n_experts,
                       int top_k, int renorm, int32_t* ids, float* w, float* probs, float* logits,
-                      hipStream_t stream);
+                      hipStream_t stream, const uint32_t* active = nullptr);
 void launch_moe_pack(const int32_t* ids, int nslots, int n_experts, uint32_t* offsets,
-                     uint32_t* slots, uint32_t* err, hipStream_t stream);
+                     uint32_t* slots, uint32_t* err, hipStream_t stream, const uint32_t* active = nullptr, int top_k = 1);
 // Q8_K activations of the packed entries as the expert kernels read them, entry-major.  Each
 // 256-value block b of an entry is stored in the matrix-core operand order: byte
 // 256b + 64p + 16(j%4) + 8(j/4) + i holds code 32j + 8p + i (sub-block j, k part p), so that
@@ -60,7 +61,7 @@ struct MoeAct {
 size_t moe_act_bytes(int64_t nentries, int k);
 MoeAct moe_act_at(uint8_t* base, int64_t nentries, int k);
 void launch_moe_gather_q8k(const float* x, const uint32_t* slots, int nentries, int top_k, int k,
-                           const uint32_t* err, MoeAct a, int gather, hipStream_t stream);
+                           const uint32_t* err, MoeAct a, int gather, hipStream_t stream, const uint32_t* total = nullptr);
 void launch_moe_gateup(const uint8_t* gate, const uint8_t* up, int n_experts, int hidden,
                        int inter, const uint32_t* offsets, int nentries, MoeAct a,
                        const uint32_t* err, float* h, hipStream_t stream);
@@ -68,7 +69,7 @@ void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
                      const uint32_t* offsets, int nentries, MoeAct a, const uint32_t* slots,
                      const uint32_t* err, float* out, hipStream_t stream);
 void launch_moe_combine(const float* out, const int32_t* ids, const float* w, int rows, int top_k,
-                        int hidden, float* y, hipStream_t stream);
+                        int hidden, float* y, hipStream_t stream, const uint32_t* active = nullptr);
 // gemm_q4k.hip: the prefill Q4_K GEMM on the F16 matrix cores.  Activations are quantized to
 // Q8_K into the GEMM's own layout (codes as F16 in the matrix-core operand order, then per
 // super-block the sub-block sums, scales and block sums); tpad = rows rounded up to 64.
@@ -79,9 +80,10 @@ struct GemmAct {
 };
 size_t gemm_act_bytes(int64_t tpad, int k);
 GemmAct gemm_act_at(uint8_t* base, int64_t tpad, int k);
-void launch_gemm_act(const float* x, int T, int k, GemmAct a, hipStream_t stream);
+void launch_gemm_act(const float* x, int T, int k, GemmAct a, hipStream_t stream, const uint32_t* active = nullptr);
 bool gemm_q4k_supported(int n_out, int k);
-void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, int T, float* y, hipStream_t stream);
+void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, int T, float* y, hipStream_t stream,
+                     const uint32_t* active = nullptr);
 // The MoE expert FFN at many tokens on the same kernels: entries padded to 64-entry tiles per
 // expert (pad_off [E+1], tile_e [max_tiles], n_tiles [1], built on the device from the packed
 // offsets), quantized into the GEMM layout at their padded positions, then gate/up -> h and

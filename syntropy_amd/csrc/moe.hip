@@ -108,12 +108,15 @@ template <bool X16>  // token rows 16-byte aligned (else they are copied 4 bytes
 __global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ router,
                                                     const float* __restrict__ x, int rows,
                                                     int hidden, int n_experts,
-                                                    float* __restrict__ logits) {
+                                                    float* __restrict__ logits,
+                                                    const uint32_t* __restrict__ active) {
     constexpr int LOADS = X16 ? RT_T + RT_E : 4 * RT_T + RT_E;  // loads per chunk per wavefront
     extern __shared__ __attribute__((aligned(16))) uint8_t rt_lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t0 = blockIdx.x * RT_T, e0 = blockIdx.y * RT_E;
+    rows = active_rows(active, 0, rows);
+    if (t0 >= rows) return;  // uniform: tokens past the step's active rows
     const int nblk = hidden / 32;
     float* S0 = reinterpret_cast<float*>(rt_lds + 2 * RT_STAGE);  // [RT_PAIRS][nblk]
     rt_issue<X16>(x, router, rows, hidden, n_experts, t0, e0, 0, nblk, wave, lane, rt_lds);
@@ -196,7 +199,9 @@ __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logi
                                                   int n_experts, int top_k, int renorm,
                                                   int32_t* __restrict__ ids,
                                                   float* __restrict__ wout,
-                                                  float* __restrict__ probs_out) {
+                                                  float* __restrict__ probs_out,
+                                                  const uint32_t* __restrict__ active) {
+    rows = active_rows(active, 0, rows);
     __shared__ __attribute__((aligned(16))) float sp[4][256];
     __shared__ __attribute__((aligned(16))) uint64_t keys[4][256];
     __shared__ __attribute__((aligned(16))) float selv[4][32];
@@ -312,7 +317,7 @@ bool moe_route_supported(int hidden) { return hidden > 0 && hidden % 32 == 0 && 
 
 void launch_moe_route(const float* router, const float* x, int rows, int hidden, int n_experts,
                       int top_k, int renorm, int32_t* ids, float* w, float* probs, float* logits,
-                      hipStream_t stream) {
+                      hipStream_t stream, const uint32_t* active) {
     const dim3 grid((rows + RT_T - 1) / RT_T, (n_experts + RT_E - 1) / RT_E);
     const size_t lds = moe_logits_lds(hidden);
     static const hipError_t lds_ok =
@@ -322,19 +327,24 @@ void launch_moe_route(const float* router, const float* x, int rows, int hidden,
     (void)lds_ok;  // a refusal shows as the launch's error
     (void)lds_ok4;
     if (((uintptr_t)x & 15) == 0)
-        hipLaunchKernelGGL(k_moe_logits<true>, grid, dim3(256), lds, stream, router, x, rows, hidden, n_experts, logits);
+        hipLaunchKernelGGL(k_moe_logits<true>, grid, dim3(256), lds, stream, router, x, rows, hidden, n_experts, logits,
+                           active);
     else
         hipLaunchKernelGGL(k_moe_logits<false>, grid, dim3(256), lds, stream, router, x, rows, hidden, n_experts,
-                           logits);
+                           logits, active);
     const dim3 tg((rows + 3) / 4);
+#define SYN_TOPK(NQ)                                                                                           \
+    hipLaunchKernelGGL(k_moe_topk<NQ>, tg, dim3(256), 0, stream, logits, rows, n_experts, top_k, renorm, ids, w, \
+                       probs, active)
     if (n_experts <= 64)
-        hipLaunchKernelGGL(k_moe_topk<1>, tg, dim3(256), 0, stream, logits, rows, n_experts, top_k, renorm, ids, w, probs);
+        SYN_TOPK(1);
     else if (n_experts <= 128)
-        hipLaunchKernelGGL(k_moe_topk<2>, tg, dim3(256), 0, stream, logits, rows, n_experts, top_k, renorm, ids, w, probs);
+        SYN_TOPK(2);
     else if (n_experts <= 192)
-        hipLaunchKernelGGL(k_moe_topk<3>, tg, dim3(256), 0, stream, logits, rows, n_experts, top_k, renorm, ids, w, probs);
+        SYN_TOPK(3);
     else
-        hipLaunchKernelGGL(k_moe_topk<4>, tg, dim3(256), 0, stream, logits, rows, n_experts, top_k, renorm, ids, w, probs);
+        SYN_TOPK(4);
+#undef SYN_TOPK
 }
 
 // ============================================================================================
@@ -349,7 +359,9 @@ void launch_moe_route(const float* router, const float* x, int rows, int hidden,
 __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ ids, int nslots,
                                                    int n_experts, uint32_t* __restrict__ offsets,
                                                    uint32_t* __restrict__ slots,
-                                                   uint32_t* __restrict__ err) {
+                                                   uint32_t* __restrict__ err,
+                                                   const uint32_t* __restrict__ active, int top_k) {
+    if (active) nslots = active_rows(active, 0, nslots / top_k) * top_k;  // the active rows' slots
     extern __shared__ uint32_t cnt[];  // [16][n_experts]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int per = (nslots + 15) / 16;
@@ -452,9 +464,9 @@ __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ i
 }
 
 void launch_moe_pack(const int32_t* ids, int nslots, int n_experts, uint32_t* offsets,
-                     uint32_t* slots, uint32_t* err, hipStream_t stream) {
+                     uint32_t* slots, uint32_t* err, hipStream_t stream, const uint32_t* active, int top_k) {
     hipLaunchKernelGGL(k_moe_pack, dim3(1), dim3(1024), sizeof(uint32_t) * 16 * n_experts, stream,
-                       ids, nslots, n_experts, offsets, slots, err);
+                       ids, nslots, n_experts, offsets, slots, err, active, top_k);
 }
 
 // ============================================================================================
@@ -488,8 +500,10 @@ __global__ __launch_bounds__(256) void k_moe_gather_q8k(const float* __restrict_
                                                         const uint32_t* __restrict__ slots,
                                                         int nentries, int top_k, int k,
                                                         const uint32_t* __restrict__ err,
-                                                        MoeAct a, int gather) {
+                                                        MoeAct a, int gather,
+                                                        const uint32_t* __restrict__ total) {
     if (err[0]) return;
+    if (total) nentries = (int)(*total < (uint32_t)nentries ? *total : (uint32_t)nentries);  // packed entries
     const int nb = k / 256;
     const int lane = threadIdx.x & 63;
     const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -509,11 +523,11 @@ __global__ __launch_bounds__(256) void k_moe_gather_q8k(const float* __restrict_
 }
 
 void launch_moe_gather_q8k(const float* x, const uint32_t* slots, int nentries, int top_k, int k,
-                           const uint32_t* err, MoeAct a, int gather, hipStream_t stream) {
+                           const uint32_t* err, MoeAct a, int gather, hipStream_t stream, const uint32_t* total) {
     const int64_t items = (int64_t)nentries * (k / 256);
     if (items == 0) return;
     hipLaunchKernelGGL(k_moe_gather_q8k, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, x,
-                       slots, nentries, top_k, k, err, a, gather);
+                       slots, nentries, top_k, k, err, a, gather, total);
 }
 
 // ============================================================================================
@@ -890,9 +904,11 @@ void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
 __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ out,
                                                      const int32_t* __restrict__ ids,
                                                      const float* __restrict__ w, int top_k,
-                                                     int hidden, float* __restrict__ y) {
+                                                     int hidden, float* __restrict__ y,
+                                                     const uint32_t* __restrict__ active) {
     __shared__ int order[64];
     const int r = blockIdx.y;
+    if (r >= active_rows(active, 0, (int)gridDim.y)) return;  // uniform: a row past the active ones
     if (threadIdx.x == 0) {
         for (int j = 0; j < top_k; ++j) order[j] = j;
         for (int a2 = 1; a2 < top_k; ++a2) {  // stable insertion sort by id
@@ -918,10 +934,10 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ o
 }
 
 void launch_moe_combine(const float* out, const int32_t* ids, const float* w, int rows, int top_k,
-                        int hidden, float* y, hipStream_t stream) {
+                        int hidden, float* y, hipStream_t stream, const uint32_t* active) {
     if (rows == 0 || hidden == 0) return;
     hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((hidden + 1023) / 1024), (unsigned)rows),
-                       dim3(256), 0, stream, out, ids, w, top_k, hidden, y);
+                       dim3(256), 0, stream, out, ids, w, top_k, hidden, y, active);
 }
 
 }  // namespace syn

@@ -28,6 +28,7 @@
 
 #include "../../include/syntropy_hip.h"
 #include "../../include/syntropy_provider.h"
+#include "capi_rows.hpp"
 
 #define SYN_PROVIDER_EXPORT extern "C" __attribute__((visibility("default")))
 
@@ -545,6 +546,18 @@ uint8_t* workspace_of(Ctx& c, const SynOpArgs& a, const Plan& p) {
     return reinterpret_cast<uint8_t*>(round_up(reinterpret_cast<uintptr_t>(w), 256));
 }
 
+// The step descriptor's rows_active (byte offset 8 of syn_step_desc,
+// crates/kernels/include/syntropy/step_desc.h:53-57) as a device address the kernels read at
+// run time, so that a captured graph follows the value the host writes before each replay; null
+// for an empty step slice, which computes the whole bucket (crates/kernels-cpu/src/launch.rs:
+// 320-340 reads it the same way on the host).
+const uint32_t* step_rows(Ctx& c, const SynOpArgs& a) {
+    if (a.step.bytes == 0) return nullptr;
+    if (a.step.bytes < 12)
+        internal("a " + std::to_string(a.step.bytes) + "-byte step descriptor has no rows_active");
+    return reinterpret_cast<const uint32_t*>(addr_of(c, a.step) + 8);
+}
+
 const SynBufferView& weight(const SynOpArgs& a, size_t i, uint64_t need, const char* what) {
     if (i >= a.n_weights || !a.weights) internal(std::string(what) + ": missing weight view");
     const SynBufferView& w = a.weights[i];
@@ -554,6 +567,7 @@ const SynBufferView& weight(const SynOpArgs& a, size_t i, uint64_t need, const c
 
 void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
     const uint32_t rows = p.rows;
+    const uint32_t* active = step_rows(c, a);
     switch (p.op) {
     case Op::Gemv:
     case Op::Gemm:
@@ -574,12 +588,12 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         const SynBufferView& w = weight(a, 0, wbytes, name);
         uint8_t* ws = workspace_of(c, a, p);
         if (gated)
-            check_syn(syn_gate_up_act(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in, (const float*)x,
-                                      rows, (float*)y, ws, p.workspace - 256, st),
+            check_syn(syn_gate_up_act_rows(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in,
+                                           (const float*)x, rows, (float*)y, ws, p.workspace - 256, st, active),
                       name);
         else
-            check_syn(syn_gemv_layout(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in, (const float*)x,
-                                      rows, (float*)y, ws, p.workspace - 256, st),
+            check_syn(syn_gemv_layout_rows(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in,
+                                           (const float*)x, rows, (float*)y, ws, p.workspace - 256, st, active),
                       name);
         return;
     }
@@ -596,9 +610,9 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         const SynBufferView& u = weight(a, 1, mat, "MoeGrouped up");
         const SynBufferView& d = weight(a, 2, mat, "MoeGrouped down");
         uint8_t* ws = workspace_of(c, a, p);
-        check_syn(syn_moe_grouped(p.weight, (const void*)g.addr, (const void*)u.addr, (const void*)d.addr,
-                                  mat, e, top_k, hidden, inter, (const float*)x, (const int32_t*)ids, rows,
-                                  (float*)out, ws, p.workspace - 256, nullptr, st),
+        check_syn(syn_moe_grouped_rows(p.weight, (const void*)g.addr, (const void*)u.addr, (const void*)d.addr,
+                                       mat, e, top_k, hidden, inter, (const float*)x, (const int32_t*)ids, rows,
+                                       (float*)out, ws, p.workspace - 256, nullptr, st, active),
                   "MoeGrouped");
         return;
     }
@@ -618,8 +632,8 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         uint8_t* w = tensor(c, a.outputs[1], 0, rows, top_k, 1, 4, "MoeRoute weights");
         const SynBufferView& r = weight(a, 0, 4ull * e * hidden, "MoeRoute router");
         uint8_t* ws = workspace_of(c, a, p);
-        check_syn(syn_moe_route((const float*)r.addr, (const float*)x, rows, hidden, e, top_k, renorm,
-                                (int32_t*)ids, (float*)w, (float*)ws, st),
+        check_syn(syn_moe_route_rows((const float*)r.addr, (const float*)x, rows, hidden, e, top_k, renorm,
+                                     (int32_t*)ids, (float*)w, (float*)ws, st, active),
                   "MoeRoute");
         return;
     }
@@ -631,8 +645,8 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         const uint8_t* w = tensor(c, a.inputs[1], 0, rows, top_k, 1, 4, "MoeCombine weights");
         const uint8_t* ids = tensor(c, a.inputs[2], 7, rows, top_k, 1, 4, "MoeCombine ids");
         uint8_t* y = tensor(c, a.outputs[0], 0, rows, hidden, 1, 4, "MoeCombine y");
-        check_syn(syn_moe_combine((const float*)per, (const int32_t*)ids, (const float*)w, rows, top_k,
-                                  hidden, (float*)y, st),
+        check_syn(syn_moe_combine_rows((const float*)per, (const int32_t*)ids, (const float*)w, rows, top_k,
+                                       hidden, (float*)y, st, active),
                   "MoeCombine");
         return;
     }

@@ -350,13 +350,16 @@ def packed(buf: Buffer, dtype: int, dims, offset: int = 0, elem: int = 4) -> Ten
     return TensorArg(Slice(buf.handle, offset, n), dtype, 0, (u32 * 4)(*d), (u32 * 4)(*st))
 
 
-def op_args(inputs, outputs, weights, workspace: Slice | None = None, statics=()) -> OpArgs:
+def op_args(inputs, outputs, weights, workspace: Slice | None = None, statics=(),
+            step: Slice | None = None) -> OpArgs:
+    """SynOpArgs (types.rs:267-292).  `step` is the step descriptor's slice (its rows_active
+    bounds the rows computed); none computes the whole bucket."""
     ins = (TensorArg * max(1, len(inputs)))(*inputs)
     outs = (TensorArg * max(1, len(outputs)))(*outputs)
     ws = (BufferView * max(1, len(weights)))(*weights)
     st = (Scalar * max(1, len(statics)))(*statics)
     a = OpArgs(C.sizeof(OpArgs), 1 if workspace is not None else 0, ins, len(inputs), outs, len(outputs),
-               ws, len(weights), Slice(), workspace or Slice(), st, len(statics))
+               ws, len(weights), step or Slice(), workspace or Slice(), st, len(statics))
     a._keep = (ins, outs, ws, st)
     return a
 
