@@ -180,15 +180,17 @@ int syn_moe_pack(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_e
  * by expert (ffn_*_exps); expert_bytes_each is the size of one stacked matrix.  Binding:
  * crates/kernels-cpu/src/moe/entry.rs:6-27.  An id outside [0, n_experts) writes nothing and
  * sets *status (device u32, optional) to 1, as the reference refuses the call
- * (moe.rs:433-441). */
+ * (moe.rs:433-441).  site (device I32 [n_experts], optional, MoeGrouped's input 2): a nonzero
+ * entry marks an expert this call computes; the slots of the other experts keep their values
+ * (entry.rs:13-16, 25, 297-300).  Null: every expert is computed. */
 int syn_moe_grouped_workspace_bytes(int32_t wtype, uint32_t n_experts, uint32_t top_k,
                                     uint32_t hidden, uint32_t inter, uint32_t rows,
                                     uint64_t* bytes);
 int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, const void* down,
                     uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k,
                     uint32_t hidden, uint32_t inter, const float* x, const int32_t* ids,
-                    uint32_t rows, float* out, void* ws, uint64_t ws_bytes, uint32_t* status,
-                    void* stream);
+                    const int32_t* site, uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
+                    uint32_t* status, void* stream);
 
 /* MoeCombine: y F32 [rows, hidden] = per row, the slots of out F32 [rows, top_k, hidden] in
  * ascending expert id, y += w * v from +0.0 without fused multiply-add

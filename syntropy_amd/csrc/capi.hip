@@ -697,7 +697,7 @@ SYN_EXPORT int syn_moe_grouped_workspace_bytes(int32_t wtype, uint32_t n_experts
 int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const void* down,
                                uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k,
                                uint32_t hidden, uint32_t inter, const float* x, const int32_t* ids,
-                               uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
+                               const int32_t* site, uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
                                uint32_t* status, void* stream, const uint32_t* active) {
     const char* W = "syn_moe_grouped";
     if (wtype != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: expert weight type %d (Q4_K)", W, wtype);
@@ -712,6 +712,7 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
         return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
                     (unsigned long long)ws_bytes, (unsigned long long)m.bytes);
     if (!gate || !up || !down || !x || !ids || !out || !ws) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (site && !aligned(site, 4)) return fail(SYN_E_INVALID, "%s: the site mask must be 4-byte aligned", W);
     if (!aligned(gate, 16) || !aligned(up, 16) || !aligned(down, 16) || !aligned(x, 16) || !aligned(ws, 256) || !aligned(out, 4))
         return fail(SYN_E_INVALID, "%s: weights and x must be 16-byte, the workspace 256-byte aligned", W);
     uint8_t* base = (uint8_t*)ws;
@@ -720,7 +721,7 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
     uint32_t* err = (uint32_t*)(base + m.err);
     const int ent = (int)(rows * top_k);
     hipStream_t st = (hipStream_t)stream;
-    syn::launch_moe_pack(ids, ent, (int)n_experts, offsets, slots, err, st, active, (int)top_k);
+    syn::launch_moe_pack(ids, ent, (int)n_experts, offsets, slots, err, st, active, (int)top_k, site);
     if (m.gemm) {
         const syn::MoeTiles mt{(uint32_t*)(base + m.pad_off), (uint32_t*)(base + m.tile_e),
                                (uint32_t*)(base + m.n_tiles)};
@@ -760,9 +761,10 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
 SYN_EXPORT int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, const void* down,
                                uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k,
                                uint32_t hidden, uint32_t inter, const float* x, const int32_t* ids,
-                               uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
+                               const int32_t* site, uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
                                uint32_t* status, void* stream) {
-    return syn_moe_grouped_rows(wtype, gate, up, down, expert_bytes_each, n_experts, top_k, hidden, inter, x, ids, rows, out, ws, ws_bytes, status, stream, nullptr);
+    return syn_moe_grouped_rows(wtype, gate, up, down, expert_bytes_each, n_experts, top_k, hidden, inter, x, ids,
+                                site, rows, out, ws, ws_bytes, status, stream, nullptr);
 }
 
 int syn_moe_combine_rows(const float* out, const int32_t* ids, const float* w, uint32_t rows,

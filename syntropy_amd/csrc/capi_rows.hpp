@@ -17,7 +17,8 @@ int syn_moe_route_rows(const float* router, const float* x, uint32_t rows, uint3
                        const uint32_t* active);
 int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const void* down,
                          uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k, uint32_t hidden,
-                         uint32_t inter, const float* x, const int32_t* ids, uint32_t rows, float* out, void* ws,
+                         uint32_t inter, const float* x, const int32_t* ids, const int32_t* site, uint32_t rows,
+                         float* out, void* ws,
                          uint64_t ws_bytes, uint32_t* status, void* stream, const uint32_t* active);
 int syn_moe_combine_rows(const float* out, const int32_t* ids, const float* w, uint32_t rows, uint32_t top_k,
                          uint32_t hidden, float* y, void* stream, const uint32_t* active);

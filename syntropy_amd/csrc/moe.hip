@@ -360,8 +360,11 @@ __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ i
                                                    int n_experts, uint32_t* __restrict__ offsets,
                                                    uint32_t* __restrict__ slots,
                                                    uint32_t* __restrict__ err,
-                                                   const uint32_t* __restrict__ active, int top_k) {
+                                                   const uint32_t* __restrict__ active, int top_k,
+                                                   const int32_t* __restrict__ site) {
     if (active) nslots = active_rows(active, 0, nslots / top_k) * top_k;  // the active rows' slots
+    // Every id is checked; a slot whose expert the site mask leaves out is neither counted nor
+    // packed, so no later kernel computes or writes it.
     extern __shared__ uint32_t cnt[];  // [16][n_experts]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int per = (nslots + 15) / 16;
@@ -375,7 +378,7 @@ __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ i
         const int e = ids[s];
         if (e < 0 || e >= n_experts)
             atomicOr(&bad, 1u);
-        else
+        else if (!site || site[e] != 0)
             atomicAdd(&cnt[wave * n_experts + e], 1u);
     }
     __syncthreads();
@@ -440,8 +443,8 @@ __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ i
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (int c0 = s_begin; c0 < s_end; c0 += 64) {
         const int s = c0 + lane;
-        const bool live = s < s_end;
-        const int e = live ? ids[s] : -1;
+        const int e = s < s_end ? ids[s] : -1;
+        const bool live = e >= 0 && (!site || site[e] != 0);
         // lanes holding the same expert
         uint64_t same = __ballot(live);
 #pragma unroll
@@ -464,9 +467,10 @@ __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ i
 }
 
 void launch_moe_pack(const int32_t* ids, int nslots, int n_experts, uint32_t* offsets,
-                     uint32_t* slots, uint32_t* err, hipStream_t stream, const uint32_t* active, int top_k) {
+                     uint32_t* slots, uint32_t* err, hipStream_t stream, const uint32_t* active, int top_k,
+                     const int32_t* site) {
     hipLaunchKernelGGL(k_moe_pack, dim3(1), dim3(1024), sizeof(uint32_t) * 16 * n_experts, stream,
-                       ids, nslots, n_experts, offsets, slots, err, active, top_k);
+                       ids, nslots, n_experts, offsets, slots, err, active, top_k, site);
 }
 
 // ============================================================================================

@@ -601,9 +601,10 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         const uint32_t e = p.dims[0], top_k = p.dims[1], hidden = p.dims[2], inter = p.dims[3];
         if (a.n_inputs < 2 || a.n_inputs > 3 || a.n_outputs != 1 || a.n_weights != 3)
             internal("MoeGrouped binds x, ids (and an optional site), one output and three weights");
-        if (a.n_inputs == 3) unsupported("MoeGrouped: the site input (per-expert residency) is not served");
         const uint8_t* x = tensor(c, a.inputs[0], 0, rows, hidden, 1, 4, "MoeGrouped x");
         const uint8_t* ids = tensor(c, a.inputs[1], 7, rows, top_k, 1, 4, "MoeGrouped ids");
+        // input 2, the site mask: packed I32 [n_experts, 1], nonzero = computed here
+        const uint8_t* site = a.n_inputs == 3 ? tensor(c, a.inputs[2], 7, e, 1, 1, 4, "MoeGrouped site") : nullptr;
         uint8_t* out = tensor(c, a.outputs[0], 0, rows, top_k, hidden, 4, "MoeGrouped out");
         const uint64_t mat = (uint64_t)inter * (hidden / 256) * 144 * e;
         const SynBufferView& g = weight(a, 0, mat, "MoeGrouped gate");
@@ -611,7 +612,8 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         const SynBufferView& d = weight(a, 2, mat, "MoeGrouped down");
         uint8_t* ws = workspace_of(c, a, p);
         check_syn(syn_moe_grouped_rows(p.weight, (const void*)g.addr, (const void*)u.addr, (const void*)d.addr,
-                                       mat, e, top_k, hidden, inter, (const float*)x, (const int32_t*)ids, rows,
+                                       mat, e, top_k, hidden, inter, (const float*)x, (const int32_t*)ids,
+                                       (const int32_t*)site, rows,
                                        (float*)out, ws, p.workspace - 256, nullptr, st, active),
                   "MoeGrouped");
         return;

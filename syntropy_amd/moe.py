@@ -84,21 +84,28 @@ def workspace_bytes(s: MoeShape, rows: int, ty: WeightType = WeightType.Q4K) -> 
 
 def moe_grouped(s: MoeShape, experts: Experts, x: torch.Tensor, ids: torch.Tensor,
                 out: torch.Tensor | None = None, ws: torch.Tensor | None = None,
-                status: torch.Tensor | None = None, stream=None) -> torch.Tensor:
-    """MoeGrouped (moe.rs:402-518): out F32 [rows, top_k, hidden]."""
+                status: torch.Tensor | None = None, stream=None,
+                site: torch.Tensor | None = None) -> torch.Tensor:
+    """MoeGrouped (moe.rs:402-518): out F32 [rows, top_k, hidden].  site (I32 [n_experts],
+    optional): experts marked zero are not computed and their slots of out keep their values
+    (moe/entry.rs:13-16, 297-300)."""
     experts.check(s)
     rows = ids.shape[0]
     if ids.shape != (rows, s.top_k) or ids.dtype != torch.int32:
         raise MoeError("ids must be I32 [rows, top_k]")
     if x.dtype != torch.float32 or x.numel() < rows * s.hidden or not x.is_contiguous():
         raise MoeError("x must be contiguous F32 [rows, hidden]")
+    if site is not None and (site.dtype != torch.int32 or site.numel() != s.n_experts
+                             or not site.is_contiguous() or site.device != x.device):
+        raise MoeError("site must be contiguous I32 [n_experts] on x's device")
     if out is None:
         out = torch.empty(rows, s.top_k, s.hidden, dtype=torch.float32, device=x.device)
     if ws is None:
         ws = torch.empty(max(workspace_bytes(s, rows), 256), dtype=torch.uint8, device=x.device)
     call("syn_moe_grouped", int(experts.ty), experts.gate.data_ptr(), experts.up.data_ptr(),
          experts.down.data_ptr(), experts.gate.numel(), s.n_experts, s.top_k, s.hidden, s.inter,
-         x.data_ptr(), ids.data_ptr(), rows, out.data_ptr(), ws.data_ptr(), ws.numel(),
+         x.data_ptr(), ids.data_ptr(), site.data_ptr() if site is not None else None, rows,
+         out.data_ptr(), ws.data_ptr(), ws.numel(),
          status.data_ptr() if status is not None else None, _stream(stream))
     return out
 

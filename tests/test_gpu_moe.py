@@ -294,6 +294,43 @@ def test_grouped_refusal_writes_nothing(M):
     assert np.isnan(got).all()
 
 
+# ---- the site mask (MoeGrouped's input 2) ------------------------------------------------------
+SENTINEL = 0x7FC0DEAD
+
+
+@pytest.mark.parametrize("rows,n_experts,top_k,hidden,inter", [
+    (6, 6, 2, 256, 512),       # moe/tests.rs:559-590, on the decode kernels
+    (64, 128, 8, 4096, 1536),  # the 64-token layer shape, decode kernels
+    (200, 6, 2, 256, 512),     # the many-token GEMM path
+    (160, 16, 4, 1024, 512)])  # GEMM path, several row tiles
+def test_grouped_site_mask(M, rows, n_experts, top_k, hidden, inter):
+    """Experts the site mask leaves out are not computed: their slots keep their bits, the rest
+    equal the oracle's; the complementary call on the same output completes the unmasked one."""
+    s = M.MoeShape(n_experts, top_k, hidden, inter)
+    gate, up, down = fast_q4k_experts(11, n_experts, hidden, inter)
+    rs = np.random.default_rng(rows)
+    x = rs.standard_normal((rows, hidden)).astype(np.float32)
+    ids = np.stack([rs.permutation(n_experts)[:top_k] for _ in range(rows)]).astype(np.int32)
+    site = (rs.random(n_experts) < 0.5).astype(np.int32)
+    site[ids[0, 0]] = 1
+    site[ids[0, 1]] = 0
+    ex = M.Experts(12, dev(gate), dev(up), dev(down))
+    out = torch.full((rows, top_k, hidden), SENTINEL, dtype=torch.int32, device="cuda").view(torch.float32)
+    st = torch.full((1,), 7, dtype=torch.int32, device="cuda")
+    announce(f"grouped site rows={rows} E={n_experts} k={top_k} hidden={hidden} inter={inter}")
+    M.moe_grouped(s, ex, dev(x), dev(ids), out=out, status=st, site=dev(site))
+    got = host(out)
+    assert int(host(st)[0]) == 0
+    args = (o.Q4_K, o.Q4_K, n_experts, top_k, hidden, inter, gate, up, down, x, ids)
+    want = o.moe_grouped(*args, site=site, threads=8,
+                         out=np.full(rows * top_k * hidden, SENTINEL, np.uint32).view(np.float32))
+    assert_same(got, want, "masked")
+    kept = site[ids] == 0
+    assert (got[kept].view(np.uint32) == SENTINEL).all()
+    M.moe_grouped(s, ex, dev(x), dev(ids), out=out, status=st, site=dev(1 - site))
+    assert_same(host(out), o.moe_grouped(*args, threads=8), "both sites")
+
+
 # ---- combine ------------------------------------------------------------------------------------
 def test_combine_bit_exact(M):
     rs = np.random.default_rng(4)

@@ -302,6 +302,41 @@ def test_moe_layer_through_the_provider(cx):
     assert_same(cx.get(y_b, np.float32, (rows, hidden)), o.moe_combine(want, wids, ww), "combined")
 
 
+def test_moe_grouped_site_input_through_the_provider(cx):
+    """MoeGrouped's input 2, packed I32 [n_experts, 1] (crates/kernels-cpu/src/moe/entry.rs:13-16,
+    158-160): a zero leaves the expert's slots as they were."""
+    P, pr = cx.P, cx.pr
+    E, top_k, hidden, inter, rows = 8, 2, 256, 512, 5
+    rng = MoeRng(78)
+    gate = moe_matrix(rng, o.Q4_K, E * inter, hidden, o.f16_bits)
+    up = moe_matrix(rng, o.Q4_K, E * inter, hidden, o.f16_bits)
+    down = moe_matrix(rng, o.Q4_K, E * hidden, inter, o.f16_bits)
+    x = o.normal(0x51A20005, 1.0, rows * hidden).reshape(rows, hidden)
+    ids = np.array([[0, 1], [2, 3], [4, 5], [6, 7], [1, 6]], np.int32)
+    site = np.array([1, 0, 1, 1, 0, 0, 1, 0], np.int32)
+    announce(f"provider moe site E={E} rows={rows}")
+    key = {"op": "MoeGrouped", "schemes": [{"Ggml": "Q4_K"}, {"Plain": "F32"}, {"Plain": "F32"}],
+           "layout": 0, "variant": 0}
+    op = pr.prepare(cx.ctx, key, shape(rows, E, top_k, hidden, inter))
+    gd, ud, dd = dev(gate), dev(up), dev(down)
+    xb, ib, sb = cx.put(x), cx.put(ids), cx.put(site)
+    per_b = cx.put(np.full(rows * top_k * hidden, 0x7FC0DEAD, np.uint32))
+    views = [P.view(t.data_ptr(), t.numel()) for t in (gd, ud, dd)]
+    ins = [P.packed(xb, P.DT_F32, [rows, hidden]), P.packed(ib, P.DT_I32, [rows, top_k])]
+    per_arg = P.packed(per_b, P.DT_F32, [rows, top_k, hidden])
+    # a site tensor of the wrong shape is refused before anything runs
+    with pytest.raises(P.ProviderError):
+        pr.launch(cx.ctx, cx.s, op, P.op_args(ins + [P.packed(sb, P.DT_I32, [E - 1, 1])], [per_arg], views,
+                                              cx.workspace(op)))
+    pr.launch(cx.ctx, cx.s, op, P.op_args(ins + [P.packed(sb, P.DT_I32, [E, 1])], [per_arg], views,
+                                          cx.workspace(op)))
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, E, top_k, hidden, inter, gate, up, down, x, ids, site=site,
+                         out=np.full(rows * top_k * hidden, 0x7FC0DEAD, np.uint32).view(np.float32))
+    got = cx.get(per_b, np.float32, (rows, top_k, hidden))
+    assert_same(got, want, "site")
+    assert (got[site[ids] == 0].view(np.uint32) == 0x7FC0DEAD).all()
+
+
 def test_route_without_renormalization(cx):
     P, pr = cx.P, cx.pr
     E, top_k, hidden, rows = 8, 2, 256, 5

@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 
 from oracle import oracle as o
-from refgen import (GemvRng, gemv_activations, gemv_weights, gemv_widths, quant_values)
+from refgen import (GemvRng, MoeRng, gemv_activations, gemv_weights, gemv_widths, moe_activations,
+                    moe_matrix, moe_route_ids, quant_values)
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 TYPES = [o.F16, o.BF16, o.Q8_0, o.Q4_0, o.Q4_K]
@@ -349,3 +350,67 @@ def test_f32fixed_sum_equals_the_level_by_level_tree():
         assert bits(o.fsum(xs)) == bits(level_by_level(xs)), n
         b = rs.standard_normal(n).astype(np.float32)
         assert bits(o.fdot(xs, b)) == bits(level_by_level(xs * b)), n
+
+
+# ---- crates/kernels-cpu/src/moe/tests.rs: the grouped expert FFN --------------------------------
+MOE = (6, 2, 256, 512)  # n_experts, top_k, hidden, inter (moe/tests.rs:227-236)
+SENTINEL = 0x7FC0DEAD
+
+
+def moe_layer(seed):
+    e, _, hidden, inter = MOE
+    rng = MoeRng(seed)
+    gate = moe_matrix(rng, o.Q4_K, e * inter, hidden, o.f16_bits)
+    up = moe_matrix(rng, o.Q4_K, e * inter, hidden, o.f16_bits)
+    down = moe_matrix(rng, o.Q4_K, e * hidden, inter, o.f16_bits)
+    return rng, gate, up, down
+
+
+def ffn_alone(gate, up, down, e, x):
+    """moe/tests.rs:300-313: one row through expert e's gate/up Gemv, silu(g) * u, down Gemv,
+    from the pinned Gemv and activation quantizer."""
+    _, _, hidden, inter = MOE
+    gb, db = inter * o.row_bytes(o.Q4_K, hidden), hidden * o.row_bytes(o.Q4_K, inter)
+    g = o.gemv(o.Q4_K, gate[e * gb:(e + 1) * gb], inter, hidden, x, 1)[0]
+    u = o.gemv(o.Q4_K, up[e * gb:(e + 1) * gb], inter, hidden, x, 1)[0]
+    h = np.array([np.float32(o.silu(float(a))) * b for a, b in zip(g, u)], np.float32)
+    return o.gemv(o.Q4_K, down[e * db:(e + 1) * db], hidden, inter, h, 1)[0]
+
+
+def test_moe_every_slot_is_its_experts_ffn_of_the_row_alone():
+    """moe/tests.rs:315-337."""
+    rng, gate, up, down = moe_layer(1)
+    n_experts, top_k, hidden, inter = MOE
+    for rows in [1, 2, 5, 8, 9, 17]:
+        x = moe_activations(rng, rows * hidden).reshape(rows, hidden)
+        ids = moe_route_ids(rng, rows, top_k, n_experts)
+        out = o.moe_grouped(o.Q4_K, o.Q4_K, n_experts, top_k, hidden, inter, gate, up, down, x, ids)
+        for r in range(rows):
+            for j in range(top_k):
+                want = ffn_alone(gate, up, down, int(ids[r, j]), x[r])
+                assert (bits(out[r, j]) == bits(want)).all(), (rows, r, j)
+
+
+def test_moe_slots_of_other_sites_keep_their_values():
+    """moe/tests.rs:559-590: with the site mask on the even experts, their slots equal the
+    unmasked call's and every other slot keeps its bits; the odd experts' call on the same output
+    then completes it."""
+    rng, gate, up, down = moe_layer(6)
+    n_experts, top_k, hidden, inter = MOE
+    rows = 6
+    x = moe_activations(rng, rows * hidden).reshape(rows, hidden)
+    ids = moe_route_ids(rng, rows, top_k, n_experts)
+    args = (o.Q4_K, o.Q4_K, n_experts, top_k, hidden, inter, gate, up, down, x, ids)
+    every = o.moe_grouped(*args)
+    even = np.arange(n_experts, dtype=np.int32) % 2 == 0
+    out = np.full(rows * top_k * hidden, SENTINEL, np.uint32).view(np.float32)
+    got = o.moe_grouped(*args, site=even.astype(np.int32), out=out)
+    for r in range(rows):
+        for j in range(top_k):
+            if ids[r, j] % 2 == 0:
+                assert (bits(got[r, j]) == bits(every[r, j])).all(), (r, j)
+            else:
+                assert (bits(got[r, j]) == SENTINEL).all(), (r, j)
+    assert (ids % 2 == 1).any() and (ids % 2 == 0).any()
+    done = o.moe_grouped(*args, site=(~even).astype(np.int32), out=out)
+    assert (bits(done) == bits(every)).all()
