@@ -199,6 +199,57 @@ int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, const void*
 int syn_moe_combine(const float* out, const int32_t* ids, const float* w, uint32_t rows,
                     uint32_t top_k, uint32_t hidden, float* y, void* stream);
 
+/* ---- MoE residency split --------------------------------------------------------------------
+ * The doorbell layer a router op writes and the split rule every site evaluates from it
+ * (plan/rfcs/RFC-0040-kernel-providers-and-backends.md:380-403; RFC-0023 sections 2 and 6).
+ * Layouts and codes are those of crates/kernels/include/syntropy/moe_doorbell.h (ABI version 1):
+ * a layer is the 8-byte header { u32 seq; u16 n_route; u16 n_pred }, then route[max_union] of
+ * 8-byte { u16 expert; u16 tokens; u32 cache_slot } entries, then the predictions, all
+ * little-endian. */
+#define SYN_MOE_MISS 4294967295u /* cache_slot of an expert not in the device's cache */
+#define SYN_MOE_HIT 4294967295u  /* code: computed from its cache slot */
+#define SYN_MOE_CPU 4294967294u  /* code: computed in place by the CPU pools; below it: copy slot */
+
+/* The doorbell layer of one pass (RFC-0040 ...md:390): seq, then one route entry per distinct
+ * expert of ids I32 [rows, top_k], in ascending expert index, tokens = the rows that selected it,
+ * cache_slot = slot_of[expert] (device u32 [n_experts], the slot_of table of RFC-0040 ...md:384;
+ * null: every expert misses); n_pred = 0 and the prediction part is not written.  step_desc
+ * (device syn_step_desc, optional): seq is the low 32 bits of its step and its rows_active
+ * bounds the rows, both read on the device; without it, seq is the argument.  status (device
+ * u32, optional): 0; 1 for an id outside [0, n_experts); 2 when the distinct experts exceed
+ * max_union (DoorbellError::TooManyRoutes, crates/kernels/src/moe/doorbell.rs:17); the layer
+ * is written only with status 0.  Limits: n_experts <= 8192, top_k <= 32, rows <= 65535; the
+ * layer 8-byte aligned. */
+int syn_moe_doorbell(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
+                     const uint32_t* slot_of, const void* step_desc, uint32_t seq, void* layer,
+                     uint32_t max_union, uint32_t* status, void* stream);
+
+/* The split rule, bit-identical to syn_moe_assign of crates/kernels/include/syntropy/
+ * moe_assign.h:29-61 (crates/kernels/src/moe.rs:110-160 assign_into): out[i] (device u32) is
+ * SYN_MOE_HIT for a hit; for a miss marked in eligible (bit e % 32 of word e / 32, for e below
+ * n_experts), copy slot c, its rank among such misses ordered by tokens descending, expert
+ * ascending, then entry, while c < copy_slots and (c + 1) * expert_bytes <= b_copy; SYN_MOE_CPU
+ * otherwise.  route: device entries as above, 8-byte aligned; n_route <= 65535. */
+int syn_moe_assign(const void* route, uint32_t n_route, const uint32_t* eligible, uint32_t n_experts,
+                   uint32_t b_copy, uint64_t expert_bytes, uint32_t copy_slots, uint32_t* out,
+                   void* stream);
+
+/* The same over a doorbell layer, every input read on the device (so that a captured graph
+ * follows the step): n_route from its header (a header above max_union writes no code, as
+ * DoorbellLayer::read refuses it, doorbell.rs:326-340), b_copy from the device word b_copy (the
+ * step descriptor's moe_balance entry of the layer, step_desc.h:85-87).  Codes past n_route are
+ * not written. */
+int syn_moe_assign_layer(const void* layer, uint32_t max_union, const uint32_t* eligible,
+                         uint32_t n_experts, const uint32_t* b_copy, uint64_t expert_bytes,
+                         uint32_t copy_slots, uint32_t* out, void* stream);
+
+/* site I32 [n_experts] = 1 for the experts of the layer's route whose code is of class `which`
+ * (0 HIT, 1 COPY, 2 CPU), 0 for all others: MoeGrouped's site input for that class's launch
+ * (crates/kernels-cpu/src/moe/entry.rs:13-16).  No reference counterpart: the glue between the
+ * codes and the site mask. */
+int syn_moe_site_mask(const void* layer, uint32_t max_union, const uint32_t* codes, uint32_t n_experts,
+                      int32_t which, int32_t* site, void* stream);
+
 /* ---- Weight packing ---------------------------------------------------------------------
  * x F32 [n] -> GGUF blocks of wtype, byte-identical to ggml's reference quantizers
  * (third_party/ggml/src/ggml-quants.c:113-140, 276-297, 1458-1528, wrapped by

@@ -27,6 +27,12 @@
  *                    (moe/tests.rs:315); combine against its definition; route ids against a
  *                    brute-force sort.  MoeRoute and MoeCombine have no reference code: their
  *                    values are pinned by the specification and invariants only.
+ *   or_moe_assign    the reference's generated split rule (moe_assign.h), compiled into
+ *                    oracle/_ref, on 10^6 generated inputs; the hand-worked cases of
+ *                    crates/kernels/src/moe/tests.rs:801-922
+ *   or_moe_doorbell  struct layout against moe_doorbell.h compiled into oracle/_ref; the
+ *                    byte example of moe/tests.rs:938-961; the route list against a brute-force
+ *                    count of the ids
  */
 #include "oracle.h"
 
@@ -1207,4 +1213,108 @@ uint64_t or_fnv1a(const uint8_t* bytes, size_t n) {
 int or_num_threads_default(void) {
     long n = sysconf(_SC_NPROCESSORS_ONLN);
     return n > 0 ? (int)n : 1;
+}
+
+/* ============================================================================================
+ * The residency split
+ * ========================================================================================== */
+
+/* Stable merge sort of miss indices by tokens descending, then expert ascending. */
+static int miss_before(const struct or_route_slot* r, uint32_t a, uint32_t b) {
+    if (r[a].tokens != r[b].tokens) return r[a].tokens > r[b].tokens;
+    return r[a].expert < r[b].expert;
+}
+static void sort_misses(const struct or_route_slot* r, uint32_t* v, uint32_t* tmp, uint32_t n) {
+    for (uint32_t w = 1; w < n; w *= 2) {
+        for (uint32_t lo = 0; lo < n; lo += 2 * w) {
+            uint32_t mid = lo + w < n ? lo + w : n, hi = lo + 2 * w < n ? lo + 2 * w : n;
+            uint32_t i = lo, j = mid, k = lo;
+            /* the left run wins ties: stable */
+            while (i < mid && j < hi) tmp[k++] = miss_before(r, v[j], v[i]) ? v[j++] : v[i++];
+            while (i < mid) tmp[k++] = v[i++];
+            while (j < hi) tmp[k++] = v[j++];
+        }
+        memcpy(v, tmp, (size_t)n * 4);
+    }
+}
+
+/* RFC-0040 ...md:392-403 (RFC-0023 section 6), the split function as written there: the misses
+ * ordered by tokens descending, then expert index ascending (entries of one expert, which a
+ * well-formed doorbell never repeats, in entry order), walked; a miss marked in the eligibility
+ * bitmap (bit e % 32 of word e / 32, for e below n_experts) is copied while its bytes keep the
+ * copied total at or below b_copy and a copy slot is left, taking the next copy-slot index;
+ * hits are HIT, every other miss CPU.  The doc of crates/kernels/src/moe.rs:110-125 states the
+ * same rule. */
+void or_moe_assign(const struct or_route_slot* route, uint32_t n_route, const uint32_t* eligible,
+                   uint32_t n_experts, uint32_t b_copy, uint64_t expert_bytes, uint32_t copy_slots,
+                   uint32_t* out) {
+    uint32_t* miss = (uint32_t*)malloc((size_t)(n_route + 1) * 4);
+    uint32_t* tmp = (uint32_t*)malloc((size_t)(n_route + 1) * 4);
+    uint32_t m = 0;
+    for (uint32_t i = 0; i < n_route; ++i) {
+        if (route[i].cache_slot != OR_MOE_MISS) {
+            out[i] = OR_MOE_HIT;
+        } else {
+            out[i] = OR_MOE_CPU;
+            miss[m++] = i;
+        }
+    }
+    sort_misses(route, miss, tmp, m);
+    uint32_t copied = 0;
+    uint64_t bytes = 0; /* never above b_copy */
+    for (uint32_t t = 0; t < m; ++t) {
+        const uint32_t i = miss[t], e = route[i].expert;
+        const int marked = e < n_experts && ((eligible[e / 32] >> (e % 32)) & 1u);
+        const int fits = expert_bytes <= (uint64_t)b_copy - bytes;
+        if (marked && fits && copied < copy_slots) {
+            out[i] = copied++;
+            bytes += expert_bytes;
+        }
+    }
+    free(miss);
+    free(tmp);
+}
+
+/* RFC-0040 ...md:390 and RFC-0023 section 2: the router op's doorbell layer, the step's seq, then
+ * one RouteSlot { expert, tokens, cache_slot } per distinct expert the pass selected, tokens the
+ * rows that selected it; n_pred = 0 (no predictions), the pred part untouched.  Entries are in
+ * ascending expert index (the split rule does not depend on their order,
+ * crates/kernels/src/moe/tests.rs:612-627).  Layout: moe_doorbell.h, little-endian. */
+int or_moe_doorbell(const int32_t* ids, size_t rows, size_t top_k, uint32_t n_experts,
+                    const uint32_t* slot_of, uint32_t seq, uint32_t max_union, uint8_t* layer) {
+    uint32_t* cnt = (uint32_t*)calloc((size_t)n_experts + 1, 4);
+    for (size_t r = 0; r < rows; ++r) {
+        for (size_t j = 0; j < top_k; ++j) {
+            const int32_t e = ids[r * top_k + j];
+            if (e < 0 || (uint32_t)e >= n_experts) {
+                free(cnt);
+                return -1;
+            }
+            int again = 0;
+            for (size_t q = 0; q < j; ++q) again |= ids[r * top_k + q] == e;
+            if (!again) cnt[e] += 1;
+        }
+    }
+    uint32_t n = 0;
+    for (uint32_t e = 0; e < n_experts; ++e) n += cnt[e] != 0;
+    if (n > max_union) {
+        free(cnt);
+        return -2;
+    }
+    const uint16_t n_route = (uint16_t)n, n_pred = 0;
+    memcpy(layer + 0, &seq, 4);
+    memcpy(layer + 4, &n_route, 2);
+    memcpy(layer + 6, &n_pred, 2);
+    uint32_t i = 0;
+    for (uint32_t e = 0; e < n_experts; ++e) {
+        if (!cnt[e]) continue;
+        const uint16_t ex = (uint16_t)e, tok = (uint16_t)cnt[e];
+        const uint32_t slot = slot_of ? slot_of[e] : OR_MOE_MISS;
+        uint8_t* p = layer + 8 + 8 * (size_t)i++;
+        memcpy(p + 0, &ex, 2);
+        memcpy(p + 2, &tok, 2);
+        memcpy(p + 4, &slot, 4);
+    }
+    free(cnt);
+    return 0;
 }

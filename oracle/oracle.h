@@ -107,6 +107,25 @@ int or_moe_route(const float* router, const float* x, size_t rows, size_t hidden
 int or_moe_combine(const float* out, const int32_t* ids, const float* w, size_t rows,
                    size_t top_k, size_t hidden, float* y);
 
+/* ---- The residency split: doorbell layer and split rule
+ * (crates/kernels/include/syntropy/moe_doorbell.h, moe_assign.h; RFC-0040 ...md:380-403) ---- */
+#define OR_MOE_MISS 0xFFFFFFFFu
+#define OR_MOE_HIT 0xFFFFFFFFu
+#define OR_MOE_CPU 0xFFFFFFFEu
+struct or_route_slot {
+    uint16_t expert;
+    uint16_t tokens;
+    uint32_t cache_slot;
+};
+void or_moe_assign(const struct or_route_slot* route, uint32_t n_route, const uint32_t* eligible,
+                   uint32_t n_experts, uint32_t b_copy, uint64_t expert_bytes, uint32_t copy_slots,
+                   uint32_t* out);
+/* The doorbell layer (header, then route[max_union]) of one pass: -1 for an id outside
+ * [0, n_experts), -2 when the distinct experts exceed max_union; the layer is untouched then. */
+int or_moe_doorbell(const int32_t* ids, size_t rows, size_t top_k, uint32_t n_experts,
+                    const uint32_t* slot_of /* optional */, uint32_t seq, uint32_t max_union,
+                    uint8_t* layer);
+
 /* ---- seeded generators (SplitMix64 + Box-Muller, for the synthetic workloads) ---- */
 void or_normal_f32(uint64_t seed, float sigma, float* out, size_t n);
 

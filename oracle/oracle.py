@@ -16,6 +16,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "liboracle.so")
 REF_LIB = os.path.join(HERE, "_ref", "libggmlref.so")
+MOE_REF_LIB = os.path.join(HERE, "_ref", "libmoeref.so")
 
 F32, F16, Q4_0, Q8_0, Q4_K, BF16 = 0, 1, 2, 8, 12, 30
 ACT_F32, ACT_Q8_0, ACT_Q8K = 0, 1, 2
@@ -25,6 +26,7 @@ ACT_KIND = {F16: ACT_F32, BF16: ACT_F32, Q8_0: ACT_Q8_0, Q4_0: ACT_Q8_0, Q4_K: A
 
 _lib = None
 _ref = None
+_moe_ref = None
 
 
 def build() -> None:
@@ -81,12 +83,30 @@ def lib():
         L.or_moe_grouped.argtypes = [i32, i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, vp, i32]
         L.or_moe_route.argtypes = [vp, vp, sz, sz, sz, sz, i32, vp, vp, vp]
         L.or_moe_combine.argtypes = [vp, vp, vp, sz, sz, sz, vp]
+        L.or_moe_assign.argtypes = [vp, C.c_uint32, vp, C.c_uint32, C.c_uint32, u64, C.c_uint32, vp]
+        L.or_moe_assign.restype = None
+        L.or_moe_doorbell.argtypes = [vp, sz, sz, C.c_uint32, vp, C.c_uint32, C.c_uint32, vp]
+        L.or_moe_doorbell.restype = i32
         L.or_normal_f32.argtypes = [u64, C.c_float, vp, sz]
         L.or_fnv1a.restype = u64
         L.or_fnv1a.argtypes = [vp, sz]
         L.or_num_threads_default.restype = i32
         _lib = L
     return _lib
+
+
+def moe_ref_lib():
+    """The reference's split rule and doorbell headers compiled (oracle/_ref), or None."""
+    global _moe_ref
+    if _moe_ref is None and os.path.exists(MOE_REF_LIB):
+        R = C.CDLL(MOE_REF_LIB)
+        R.ref_moe_assign.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32,
+                                     C.c_uint64, C.c_uint32, C.c_void_p]
+        R.ref_doorbell_layout.argtypes = [C.c_void_p]
+        R.ref_moe_assign_compare.argtypes = [C.c_uint64, C.c_uint64, C.c_void_p, C.c_void_p, C.c_void_p]
+        R.ref_moe_assign_compare.restype = C.c_int64
+        _moe_ref = R
+    return _moe_ref
 
 
 def ref_lib():
@@ -282,6 +302,40 @@ def moe_combine(out, ids, w) -> np.ndarray:
     y = np.zeros((rows, hidden), dtype=np.float32)
     assert lib().or_moe_combine(_p(out), _p(ids), _p(w), rows, top_k, hidden, _p(y)) == 0
     return y
+
+
+# ---- the residency split ------------------------------------------------------------------
+# syn_route_slot of moe_doorbell.h
+ROUTE_SLOT = np.dtype([("expert", "<u2"), ("tokens", "<u2"), ("cache_slot", "<u4")])
+MOE_MISS, MOE_HIT, MOE_CPU = 0xFFFFFFFF, 0xFFFFFFFF, 0xFFFFFFFE
+DOORBELL_HEADER = 8
+
+
+def route_slots(entries) -> np.ndarray:
+    """[(expert, tokens, cache_slot), ...] as syn_route_slot records."""
+    return np.array([tuple(e) for e in entries], dtype=ROUTE_SLOT)
+
+
+def moe_assign(route, eligible, n_experts: int, b_copy: int, expert_bytes: int,
+               copy_slots: int) -> np.ndarray:
+    """The split rule: one u32 code per route entry (MOE_HIT, MOE_CPU or a copy-slot index)."""
+    route = np.ascontiguousarray(route, dtype=ROUTE_SLOT)
+    words = np.ascontiguousarray(eligible if eligible is not None else [], dtype=np.uint32)
+    out = np.zeros(len(route), np.uint32)
+    lib().or_moe_assign(_p(route), len(route), _p(words) if words.size else None, n_experts,
+                        b_copy, expert_bytes, copy_slots, _p(out))
+    return out
+
+
+def moe_doorbell(ids, n_experts: int, max_union: int, slot_of=None, seq: int = 0):
+    """The doorbell layer's header and route part (bytes), or None when refused."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    rows, top_k = ids.shape
+    layer = np.zeros(DOORBELL_HEADER + 8 * max_union, np.uint8)
+    so = None if slot_of is None else np.ascontiguousarray(slot_of, dtype=np.uint32)
+    rc = lib().or_moe_doorbell(_p(ids), rows, top_k, n_experts, _p(so) if so is not None else None,
+                               seq, max_union, _p(layer))
+    return None if rc else layer
 
 
 # ---- data ------------------------------------------------------------------------------

@@ -781,3 +781,65 @@ SYN_EXPORT int syn_moe_combine(const float* out, const int32_t* ids, const float
                                uint32_t top_k, uint32_t hidden, float* y, void* stream) {
     return syn_moe_combine_rows(out, ids, w, rows, top_k, hidden, y, stream, nullptr);
 }
+
+// ============================================================================================
+// The residency split
+// ============================================================================================
+
+SYN_EXPORT int syn_moe_doorbell(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
+                                const uint32_t* slot_of, const void* step_desc, uint32_t seq, void* layer,
+                                uint32_t max_union, uint32_t* status, void* stream) {
+    const char* W = "syn_moe_doorbell";
+    if (n_experts == 0 || n_experts > 8192) return fail(SYN_E_UNSUPPORTED, "%s: n_experts %u (1..8192)", W, n_experts);
+    if (top_k == 0 || top_k > 32) return fail(SYN_E_UNSUPPORTED, "%s: top_k %u (1..32)", W, top_k);
+    if (rows > 65535) return fail(SYN_E_UNSUPPORTED, "%s: %u rows; a route entry counts at most 65535 tokens", W, rows);
+    if (max_union > 65535) return fail(SYN_E_INVALID, "%s: max_union %u above 65535", W, max_union);
+    if (!layer || (rows && !ids)) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!aligned(layer, 8) || !aligned(step_desc, 8))
+        return fail(SYN_E_INVALID, "%s: the layer and the step descriptor must be 8-byte aligned", W);
+    syn::launch_moe_doorbell(ids, (int)rows, (int)top_k, (int)n_experts, slot_of, step_desc, seq, (uint8_t*)layer,
+                             max_union, status, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_moe_assign(const void* route, uint32_t n_route, const uint32_t* eligible, uint32_t n_experts,
+                              uint32_t b_copy, uint64_t expert_bytes, uint32_t copy_slots, uint32_t* out,
+                              void* stream) {
+    const char* W = "syn_moe_assign";
+    if (n_route > 65535) return fail(SYN_E_INVALID, "%s: %u route entries; a doorbell holds at most 65535", W, n_route);
+    if (n_route == 0) return SYN_OK;
+    if (!route || !out || (n_experts && !eligible)) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!aligned(route, 8) || !aligned(out, 4) || !aligned(eligible, 4))
+        return fail(SYN_E_INVALID, "%s: the route entries must be 8-byte aligned", W);
+    syn::launch_moe_assign((const uint8_t*)route, n_route, eligible, n_experts, b_copy, expert_bytes, copy_slots,
+                           out, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_moe_assign_layer(const void* layer, uint32_t max_union, const uint32_t* eligible,
+                                    uint32_t n_experts, const uint32_t* b_copy, uint64_t expert_bytes,
+                                    uint32_t copy_slots, uint32_t* out, void* stream) {
+    const char* W = "syn_moe_assign_layer";
+    if (max_union > 65535) return fail(SYN_E_INVALID, "%s: max_union %u above 65535", W, max_union);
+    if (!layer || !b_copy || (max_union && !out) || (n_experts && !eligible))
+        return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!aligned(layer, 8) || !aligned(b_copy, 4) || !aligned(out, 4) || !aligned(eligible, 4))
+        return fail(SYN_E_INVALID, "%s: the layer must be 8-byte aligned", W);
+    syn::launch_moe_assign_layer((const uint8_t*)layer, max_union, eligible, n_experts, b_copy, expert_bytes,
+                                 copy_slots, out, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_moe_site_mask(const void* layer, uint32_t max_union, const uint32_t* codes, uint32_t n_experts,
+                                 int32_t which, int32_t* site, void* stream) {
+    const char* W = "syn_moe_site_mask";
+    if (which < 0 || which > 2) return fail(SYN_E_INVALID, "%s: class %d (0 HIT, 1 COPY, 2 CPU)", W, which);
+    if (max_union > 65535) return fail(SYN_E_INVALID, "%s: max_union %u above 65535", W, max_union);
+    if (n_experts == 0) return SYN_OK;
+    if (!layer || !site || (max_union && !codes)) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!aligned(layer, 8) || !aligned(codes, 4) || !aligned(site, 4))
+        return fail(SYN_E_INVALID, "%s: the layer must be 8-byte aligned", W);
+    syn::launch_moe_site_mask((const uint8_t*)layer, max_union, codes, (int)n_experts, which, site,
+                              (hipStream_t)stream);
+    return check_launch(W);
+}

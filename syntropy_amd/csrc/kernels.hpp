@@ -71,6 +71,18 @@ void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
                      const uint32_t* err, float* out, hipStream_t stream);
 void launch_moe_combine(const float* out, const int32_t* ids, const float* w, int rows, int top_k,
                         int hidden, float* y, hipStream_t stream, const uint32_t* active = nullptr);
+// moe_split.hip: the residency split (doorbell layer, split rule, site masks)
+void launch_moe_assign(const uint8_t* route, uint32_t n_route, const uint32_t* eligible, uint32_t n_experts,
+                       uint32_t b_copy, uint64_t expert_bytes, uint32_t copy_slots, uint32_t* out,
+                       hipStream_t stream);
+void launch_moe_assign_layer(const uint8_t* layer, uint32_t max_union, const uint32_t* eligible,
+                             uint32_t n_experts, const uint32_t* b_copy, uint64_t expert_bytes,
+                             uint32_t copy_slots, uint32_t* out, hipStream_t stream);
+void launch_moe_doorbell(const int32_t* ids, int rows, int top_k, int n_experts, const uint32_t* slot_of,
+                         const void* desc, uint32_t seq, uint8_t* layer, uint32_t max_union, uint32_t* status,
+                         hipStream_t stream);
+void launch_moe_site_mask(const uint8_t* layer, uint32_t max_union, const uint32_t* codes, int n_experts,
+                          int which, int32_t* site, hipStream_t stream);
 // gemm_q4k.hip: the prefill Q4_K GEMM on the F16 matrix cores.  Activations are quantized to
 // Q8_K into the GEMM's own layout (codes as F16 in the matrix-core operand order, then per
 // super-block the sub-block sums, scales and block sums); tpad = rows rounded up to 64.

@@ -139,5 +139,64 @@ class MoeLayer:
         return combine(out, ids, w, stream=stream), ids, w, out
 
 
+# ---- the residency split (doorbell layer, split rule, site masks) ------------------------------
+HIT, COPY, CPU = 0, 1, 2  # site-mask classes
+
+
+def doorbell_bytes(max_union: int) -> int:
+    """Header and route part of a doorbell layer (moe_doorbell.h: 8 + 8 * MAX_UNION)."""
+    return 8 + 8 * max_union
+
+
+def doorbell(ids: torch.Tensor, n_experts: int, max_union: int, slot_of: torch.Tensor | None = None,
+             seq: int = 0, step_desc: torch.Tensor | None = None, layer: torch.Tensor | None = None,
+             status: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """The pass's doorbell layer (RFC-0040 3.4): seq, then one route entry per distinct expert of
+    ids, ascending.  Returns the layer as uint8 [8 + 8 * max_union]."""
+    rows, top_k = ids.shape
+    if layer is None:
+        layer = torch.zeros(doorbell_bytes(max_union), dtype=torch.uint8, device=ids.device)
+    if layer.numel() < doorbell_bytes(max_union):
+        raise MoeError("the layer is shorter than its route part")
+    call("syn_moe_doorbell", ids.data_ptr(), rows, top_k, n_experts,
+         slot_of.data_ptr() if slot_of is not None else None,
+         step_desc.data_ptr() if step_desc is not None else None, seq, layer.data_ptr(), max_union,
+         status.data_ptr() if status is not None else None, _stream(stream))
+    return layer
+
+
+def assign(route: torch.Tensor, n_route: int, eligible: torch.Tensor | None, n_experts: int, b_copy: int,
+           expert_bytes: int, copy_slots: int, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """The split rule (moe_assign.h): one code per route entry, as int32 (HIT = -1, CPU = -2)."""
+    if out is None:
+        out = torch.empty(max(n_route, 1), dtype=torch.int32, device=route.device)
+    call("syn_moe_assign", route.data_ptr(), n_route, eligible.data_ptr() if eligible is not None else None,
+         n_experts, b_copy, expert_bytes, copy_slots, out.data_ptr(), _stream(stream))
+    return out
+
+
+def assign_layer(layer: torch.Tensor, max_union: int, eligible: torch.Tensor | None, n_experts: int,
+                 b_copy: torch.Tensor, expert_bytes: int, copy_slots: int, out: torch.Tensor | None = None,
+                 stream=None) -> torch.Tensor:
+    """The split rule over a doorbell layer, n_route and b_copy read on the device."""
+    if out is None:
+        out = torch.empty(max(max_union, 1), dtype=torch.int32, device=layer.device)
+    call("syn_moe_assign_layer", layer.data_ptr(), max_union,
+         eligible.data_ptr() if eligible is not None else None, n_experts, b_copy.data_ptr(), expert_bytes,
+         copy_slots, out.data_ptr(), _stream(stream))
+    return out
+
+
+def site_mask(layer: torch.Tensor, max_union: int, codes: torch.Tensor, n_experts: int, which: int,
+              site: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """I32 [n_experts]: 1 for the route's experts whose code is of class `which` (HIT, COPY, CPU)."""
+    if site is None:
+        site = torch.empty(n_experts, dtype=torch.int32, device=layer.device)
+    call("syn_moe_site_mask", layer.data_ptr(), max_union, codes.data_ptr(), n_experts, which, site.data_ptr(),
+         _stream(stream))
+    return site
+
+
 __all__ = ["MoeShape", "MoeError", "Experts", "route", "pack", "workspace_bytes", "moe_grouped",
-           "combine", "MoeLayer", "GemvError"]
+           "combine", "MoeLayer", "GemvError", "doorbell", "doorbell_bytes", "assign", "assign_layer",
+           "site_mask", "HIT", "COPY", "CPU"]
