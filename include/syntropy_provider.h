@@ -4,8 +4,9 @@
  * version only appends.  Each side frees what it allocated; variable-size results go through a
  * caller buffer (SynOutBuf); handles are opaque 64-bit values.
  *
- * libsyntropy_provider.so exports exactly syntropy_provider_entry_v1, under the version node
- * SYNTROPY_PROVIDER_1 (the reference's ci/link/provider.map), and is linked -Bsymbolic. */
+ * libsyntropy_provider.so exports syntropy_provider_entry_v1, under the version node
+ * SYNTROPY_PROVIDER_1 (the reference's ci/link/provider.map), and the doorbell flag accessor
+ * syntropy_provider_flag_v1 beside it, and is linked -Bsymbolic. */
 #ifndef SYNTROPY_PROVIDER_H
 #define SYNTROPY_PROVIDER_H
 
@@ -31,6 +32,7 @@ enum {
     SYN_CLASS_UNSUPPORTED = 2,
     SYN_CLASS_CAPACITY = 3,
     SYN_CLASS_DEVICE = 6,
+    SYN_CLASS_TIMEOUT = 10,
     SYN_CLASS_INTERNAL = 13
 };
 enum {
@@ -276,6 +278,13 @@ typedef struct SynModule {
  * module has one provider: id "hip", backend Hip, domain Hip, serving Gemv (Q4_0, Q8_0, Q4_K),
  * MoeGrouped (Q4_K), MoeRoute{Softmax} and MoeCombine on AMD gfx950 devices. */
 const SynModule* syntropy_provider_entry_v1(const SynHostApi* host);
+
+/* The host address of doorbell flag `flag` (page << 16 | slot) of context `ctx`: a 4-byte word on
+ * a 64-byte line of its own in pinned host memory, which signal_host writes and wait_host reads
+ * from the device.  No counterpart in the reference's ABI, which leaves the host side of a
+ * module's flags open; the CPU provider gives the same address as Doorbells::flag
+ * (crates/kernels-cpu/src/doorbell.rs:76-81).  Called on the thread that opened the context. */
+SynStatus syntropy_provider_flag_v1(uint64_t ctx, uint32_t flag, uint32_t** host);
 
 #ifdef __cplusplus
 }

@@ -83,6 +83,10 @@ void launch_moe_doorbell(const int32_t* ids, int rows, int top_k, int n_experts,
                          hipStream_t stream);
 void launch_moe_site_mask(const uint8_t* layer, uint32_t max_union, const uint32_t* codes, int n_experts,
                           int which, int32_t* site, hipStream_t stream);
+// doorbell.hip: the device halves of the host <-> device flags (a bounded wait)
+void launch_bell_signal(uint32_t* flag, uint32_t value, hipStream_t stream);
+void launch_bell_wait(uint32_t* flag, uint32_t value, int geq, int has_reset, uint32_t reset, uint64_t max_ticks,
+                      uint32_t* status, uint32_t tag, hipStream_t stream);
 // gemm_q4k.hip: the prefill Q4_K GEMM on the F16 matrix cores.  Activations are quantized to
 // Q8_K into the GEMM's own layout (codes as F16 in the matrix-core operand order, then per
 // super-block the sub-block sums, scales and block sums); tpad = rows rounded up to 64.

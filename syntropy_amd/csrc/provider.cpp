@@ -20,6 +20,7 @@
 
 #include <atomic>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <exception>
 #include <string>
@@ -29,6 +30,7 @@
 #include "../../include/syntropy_hip.h"
 #include "../../include/syntropy_provider.h"
 #include "capi_rows.hpp"
+#include "kernels.hpp"
 
 #define SYN_PROVIDER_EXPORT extern "C" __attribute__((visibility("default")))
 
@@ -477,8 +479,22 @@ struct Buf {
     uint64_t bytes;
 };
 
+// Doorbell flags: 64 to a 4 KiB page, each on a 64-byte line of its own, in pinned host memory
+// both sides address (RFC-0040 ...md:545-547; crates/kernels-cpu/src/doorbell.rs:1-27).  The line
+// after the pages holds the wait-timeout word: 1 + the flag index of the first wait that passed
+// its spin limit.
+constexpr uint32_t FLAGS_PER_PAGE = 64;
+constexpr uint32_t FLAG_WORDS = 16;
+constexpr uint32_t MAX_FLAG_PAGES = 1024;
+constexpr uint64_t DEFAULT_SPIN_US = 2000000;
+
 struct Ctx {
     int device = 0;
+    uint32_t* bells = nullptr;      // host address
+    uint32_t* bells_dev = nullptr;  // the same memory as the device addresses it
+    uint32_t n_bells = 0;
+    uint64_t spin_us = DEFAULT_SPIN_US;
+    uint64_t spin_ticks = 0;
     std::unordered_map<uint64_t, Buf> bufs;
     std::unordered_map<uint64_t, hipStream_t> streams;
     std::unordered_map<uint64_t, hipEvent_t> events;
@@ -510,6 +526,28 @@ hipEvent_t event_of(Ctx& c, uint64_t e) {
     if (it == c.events.end()) internal("unknown event " + std::to_string(e));
     return it->second;
 }
+// The index of `flag` (page << 16 | slot), checked against the context's flags.
+uint32_t flag_index(Ctx& c, uint32_t flag) {
+    const uint32_t page = flag >> 16, slot = flag & 0xFFFFu;
+    if (slot >= FLAGS_PER_PAGE || (uint64_t)page * FLAGS_PER_PAGE + slot >= c.n_bells)
+        internal("no doorbell (page " + std::to_string(page) + ", slot " + std::to_string(slot) + ") on this device");
+    return page * FLAGS_PER_PAGE + slot;
+}
+
+// A wait that passed its spin limit since the last check: reported once, as a Timeout.
+void check_bells(Ctx& c) {
+    if (!c.bells) return;
+    uint32_t* st = c.bells + (size_t)c.n_bells * FLAG_WORDS;
+    const uint32_t tag = __atomic_exchange_n(st, 0u, __ATOMIC_ACQ_REL);
+    if (tag) {
+        const uint32_t i = tag - 1;
+        fail(SYN_CLASS_TIMEOUT, 0,
+             "wait_host on the doorbell (page " + std::to_string(i / FLAGS_PER_PAGE) + ", slot " +
+                 std::to_string(i % FLAGS_PER_PAGE) + ") passed its spin limit of " + std::to_string(c.spin_us) +
+                 " us without the host's reply; the stream ran on past it");
+    }
+}
+
 // The device address of a slice, checked against its buffer.
 uint8_t* addr_of(Ctx& c, const SynSlice& s) {
     auto it = c.bufs.find(s.buffer);
@@ -695,15 +733,48 @@ SynStatus e_enumerate(void*, SynOutBuf* out) {
     });
 }
 
-SynStatus e_open(void*, const SynDeviceId* dev, const SynOpenOptions*, uint64_t* ctx) {
+SynStatus e_open(void*, const SynDeviceId* dev, const SynOpenOptions* opts, uint64_t* ctx) {
     return call("open", false, [&] {
         if (!dev || !ctx) internal("open: null argument");
         int n = 0;
         if (hipGetDeviceCount(&n) != hipSuccess || n == 0) fail(SYN_CLASS_DEVICE, 0, "open: no HIP device");
         if ((int)dev->ordinal >= n) fail(SYN_CLASS_INVALID_REQUEST, 0, "open: no device " + std::to_string(dev->ordinal));
         check_hip(hipSetDevice((int)dev->ordinal), "hipSetDevice");
+        // doorbell_slots flags rounded up to whole pages, at least one (doorbell.rs:37-43)
+        const uint32_t want = opts ? opts->doorbell_slots : 0;
+        const uint32_t pages = want ? (uint32_t)(((uint64_t)want + FLAGS_PER_PAGE - 1) / FLAGS_PER_PAGE) : 1;
+        if (pages > MAX_FLAG_PAGES)
+            fail(SYN_CLASS_INVALID_REQUEST, 0, "open: " + std::to_string(want) + " doorbell slots (at most 65536)");
+        // the bound of one wait_host: SYNTROPY_SPIN_MAX_US (kernels.spin_kernel_max_us), default 2 s
+        uint64_t spin_us = DEFAULT_SPIN_US;
+        if (const char* e = std::getenv("SYNTROPY_SPIN_MAX_US")) {
+            char* end = nullptr;
+            const unsigned long long v = std::strtoull(e, &end, 10);
+            if (end == e || *end || v == 0 || v > 600000000ull)
+                fail(SYN_CLASS_INVALID_REQUEST, 0, "open: SYNTROPY_SPIN_MAX_US must be 1..600000000");
+            spin_us = v;
+        }
+        int khz = 0;
+        check_hip(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, (int)dev->ordinal),
+                  "hipDeviceGetAttribute(WallClockRate)");
+        if (khz <= 0) fail(SYN_CLASS_DEVICE, 0, "open: the device reports no wall-clock rate");
+        void* bells = nullptr;
+        const size_t bytes = (size_t)pages * 4096 + 64;
+        check_hip(hipHostMalloc(&bells, bytes, hipHostMallocMapped | hipHostMallocCoherent), "hipHostMalloc(doorbells)");
+        std::memset(bells, 0, bytes);
+        void* bells_dev = nullptr;
+        const hipError_t r = hipHostGetDevicePointer(&bells_dev, bells, 0);
+        if (r != hipSuccess) {
+            (void)hipHostFree(bells);
+            check_hip(r, "hipHostGetDevicePointer(doorbells)");
+        }
         Ctx* c = new Ctx();
         c->device = (int)dev->ordinal;
+        c->bells = static_cast<uint32_t*>(bells);
+        c->bells_dev = static_cast<uint32_t*>(bells_dev);
+        c->n_bells = pages * FLAGS_PER_PAGE;
+        c->spin_us = spin_us;
+        c->spin_ticks = spin_us * (uint64_t)khz / 1000u;
         const uint64_t h = g_next_ctx.fetch_add(1);
         t_ctx[h] = c;
         *ctx = h;
@@ -721,6 +792,7 @@ SynStatus e_close_ctx(void*, uint64_t ctx) {
         for (auto& e : c->events) (void)hipEventDestroy(e.second);
         for (auto& s : c->streams) (void)hipStreamDestroy(s.second);
         for (auto& b : c->bufs) (void)hipFree(b.second.ptr);
+        if (c->bells) (void)hipHostFree(c->bells);
         delete c;
         t_ctx.erase(it);
     });
@@ -796,8 +868,6 @@ SYN_UNSERVED(unmap_segment, void*, uint64_t, const SynSegment*)
 SYN_UNSERVED(register_host, void*, uint64_t, SynHostRegion, SynRegistration*)
 SYN_UNSERVED(host_registrar, void*, uint64_t, SynRegistrarVtbl*)
 SYN_UNSERVED(import, void*, uint64_t, SynHostRegion, SynBuffer*)
-SYN_UNSERVED(signal_host, void*, uint64_t, uint64_t, uint32_t, uint32_t)
-SYN_UNSERVED(wait_host, void*, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t)
 SYN_UNSERVED(arm_wake, void*, uint64_t, uint64_t, uint32_t, uint64_t)
 #undef SYN_UNSERVED
 
@@ -873,6 +943,34 @@ SynStatus e_wait(void*, uint64_t ctx, uint64_t s, uint64_t e) {
     });
 }
 
+// signal_host: a one-lane store kernel writes `value` to the flag when the stream reaches it
+// (provider.rs:346-356; RFC-0040 ...md:549-553, the store kernel).
+SynStatus e_signal_host(void*, uint64_t ctx, uint64_t s, uint32_t flag, uint32_t value) {
+    return call("signal_host", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        hipStream_t st = stream_of(c, s);
+        syn::launch_bell_signal(c.bells_dev + (size_t)flag_index(c, flag) * FLAG_WORDS, value, st);
+        check_hip(hipGetLastError(), "signal_host");
+    });
+}
+
+// wait_host: a one-wave kernel holds the stream until the flag compares Eq (cmp 0) or Geq (1)
+// with `value`, then writes `reset` when has_reset is 1 (provider.rs:357-377).  The wait gives up
+// after the spin limit; synchronize then reports a Timeout (RFC-0040 ...md:579-584).
+SynStatus e_wait_host(void*, uint64_t ctx, uint64_t s, uint32_t flag, uint32_t value, uint32_t cmp,
+                      uint32_t has_reset, uint32_t reset) {
+    return call("wait_host", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        if (cmp > 1) internal("wait_host: comparison code " + std::to_string(cmp) + " (0 Eq, 1 Geq)");
+        if (has_reset > 1) internal("wait_host: has_reset must be 0 or 1");
+        hipStream_t st = stream_of(c, s);
+        const uint32_t i = flag_index(c, flag);
+        syn::launch_bell_wait(c.bells_dev + (size_t)i * FLAG_WORDS, value, (int)cmp, (int)has_reset, reset,
+                              c.spin_ticks, c.bells_dev + (size_t)c.n_bells * FLAG_WORDS, i + 1, st);
+        check_hip(hipGetLastError(), "wait_host");
+    });
+}
+
 SynStatus e_poll(void*, uint64_t ctx, uint64_t e, uint32_t* done) {
     return call("poll", false, [&] {
         Ctx& c = ctx_of(ctx);
@@ -880,6 +978,7 @@ SynStatus e_poll(void*, uint64_t ctx, uint64_t e, uint32_t* done) {
         if (r == hipSuccess) *done = 1;
         else if (r == hipErrorNotReady) *done = 0;
         else check_hip(r, "hipEventQuery");
+        if (*done) check_bells(c);
     });
 }
 
@@ -902,6 +1001,7 @@ SynStatus e_synchronize(void*, uint64_t ctx, uint64_t s) {
     return call("synchronize", false, [&] {
         Ctx& c = ctx_of(ctx);
         check_hip(hipStreamSynchronize(stream_of(c, s)), "hipStreamSynchronize");
+        check_bells(c);
     });
 }
 
@@ -1069,6 +1169,17 @@ const SynProviderVtbl g_vtbl = make_vtbl();
 const SynModule g_module = {header(sizeof(SynModule)), 1, &g_vtbl, e_shutdown};
 
 }  // namespace
+
+// The host address of a doorbell flag of context `ctx`, for the host thread on the other side
+// of the doorbell (the CPU provider gives it as Doorbells::flag, crates/kernels-cpu/src/
+// doorbell.rs:76-81).  Called on the thread that opened the context.
+SYN_PROVIDER_EXPORT SynStatus syntropy_provider_flag_v1(uint64_t ctx, uint32_t flag, uint32_t** host) {
+    return call("flag", false, [&] {
+        Ctx& c = ctx_of(ctx);
+        if (!host) internal("flag: null output");
+        *host = c.bells + (size_t)flag_index(c, flag) * FLAG_WORDS;
+    });
+}
 
 SYN_PROVIDER_EXPORT const SynModule* syntropy_provider_entry_v1(const SynHostApi* host) {
     // the module checks the host's magic, major and size (RFC-0040 §10.4; module.rs:26-40)

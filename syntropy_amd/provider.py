@@ -262,9 +262,10 @@ class Provider:
     def ops(self) -> list:
         return json.loads(self._fetch("ops", self.vt.ops))
 
-    def open(self, ordinal: int = 0) -> int:
+    def open(self, ordinal: int = 0, doorbell_slots: int = 0) -> int:
         dev, opts, ctx = DeviceId(), OpenOptions(), u64(0)
         dev.ordinal = ordinal
+        opts.doorbell_slots = doorbell_slots
         self._ok("open", self.vt.open(self.vt.slf, C.byref(dev), C.byref(opts), C.byref(ctx)))
         return ctx.value
 
@@ -333,6 +334,24 @@ class Provider:
 
     def replay(self, ctx: int, s: int, g: int):
         self._ok("replay", self.vt.replay(self.vt.slf, ctx, s, g), ctx)
+
+    # -- doorbells (provider.rs:346-377; RFC-0040 4.2) --
+    def signal_host(self, ctx: int, s: int, page: int, slot: int, value: int = 1):
+        self._ok("signal_host", self.vt.signal_host(self.vt.slf, ctx, s, page << 16 | slot, value), ctx)
+
+    def wait_host(self, ctx: int, s: int, page: int, slot: int, value: int = 1, geq: bool = False,
+                  reset: int | None = 0):
+        self._ok("wait_host", self.vt.wait_host(self.vt.slf, ctx, s, page << 16 | slot, value, int(geq),
+                                                int(reset is not None), reset or 0), ctx)
+
+    def flag(self, ctx: int, page: int, slot: int) -> C.c_uint32:
+        """The host side of a doorbell flag, as a c_uint32 over its pinned word."""
+        f = self.lib.syntropy_provider_flag_v1
+        f.argtypes = [u64, u32, C.POINTER(C.POINTER(u32))]
+        f.restype = Status
+        p = C.POINTER(u32)()
+        self._ok("flag", f(ctx, page << 16 | slot, C.byref(p)), ctx)
+        return u32.from_address(C.addressof(p.contents))
 
     def health(self, ctx: int = 0) -> Health:
         h = Health()

@@ -1,0 +1,170 @@
+"""Doorbells through the provider boundary (crates/kernels/src/provider.rs:346-377; RFC-0040 4.2):
+signal_host raises a pinned host flag after the work before it, wait_host holds the stream until
+the host replies and then writes the consumer reset, a captured step runs the constant-valued
+handshake on every replay, and a wait that passes its spin limit ends on its own and is reported
+as a Timeout.  Every wait here is answered by the host except the one that tests the limit,
+which runs on a context opened with a 2 ms limit."""
+import os
+import time
+
+import numpy as np
+import pytest
+
+from gpu_util import announce
+from oracle import oracle as o
+from refgen import GemvRng, gemv_activations, gemv_weights
+from test_gpu_provider import Ctx, gemv_key, shape
+
+pytestmark = pytest.mark.gpu
+
+N_OUT, K, ROWS = 512, 1024, 2
+
+
+@pytest.fixture(scope="module")
+def cx():
+    c = Ctx()
+    yield c
+    c.close()
+
+
+def gemv_step(cx, seed):
+    """A prepared Q4_K Gemv with its buffers: (launch args, x buffer, y buffer, weights)."""
+    P, pr = cx.P, cx.pr
+    rng = GemvRng(seed)
+    w = gemv_weights(rng, o.Q4_K, N_OUT, K, o.f16_bits, o.round_bf16)
+    op = pr.prepare(cx.ctx, gemv_key(o.Q4_K), shape(ROWS, N_OUT, K))
+    wb = cx.put(w)
+    xb, yb = cx.empty(4 * ROWS * K, 0), cx.empty(4 * ROWS * N_OUT)
+    args = P.op_args([P.packed(xb, P.DT_F32, [ROWS, K])], [P.packed(yb, P.DT_F32, [ROWS, N_OUT])],
+                     [P.view(wb.addr, w.nbytes)], cx.workspace(op))
+    return op, args, xb, yb, w, rng
+
+
+def wait_for(flag, value, seconds=5.0):
+    end = time.monotonic() + seconds
+    while flag.value != value:
+        if time.monotonic() > end:
+            return False
+        time.sleep(0.0005)
+    return True
+
+
+def test_signal_host_follows_the_work_before_it(cx):
+    pr = cx.pr
+    op, args, xb, yb, w, rng = gemv_step(cx, 1)
+    x = gemv_activations(rng, ROWS, K).reshape(ROWS, K).astype(np.float32)
+    cx.upload(xb.addr, x)
+    flag = pr.flag(cx.ctx, 0, 1)
+    flag.value = 0
+    announce("signal_host")
+    pr.launch(cx.ctx, cx.s, op, args)
+    pr.signal_host(cx.ctx, cx.s, 0, 1, 1)
+    assert wait_for(flag, 1)
+    pr.synchronize(cx.ctx, cx.s)
+    got = cx.get(yb, np.float32, (ROWS, N_OUT))
+    assert (got.view(np.uint32) == o.gemv(o.Q4_K, w, N_OUT, K, x, ROWS).view(np.uint32)).all()
+    flag.value = 0
+
+
+def test_wait_host_holds_the_stream_until_the_host_replies(cx):
+    """wait_host(Eq 1, reset 0) -> Gemv -> signal_host: the done flag stays down while the host
+    has not replied, then rises; the reply flag is back at 0 and the output is the oracle's."""
+    pr = cx.pr
+    op, args, xb, yb, w, rng = gemv_step(cx, 2)
+    x = gemv_activations(rng, ROWS, K).reshape(ROWS, K).astype(np.float32)
+    cx.upload(xb.addr, x)
+    reply, done = pr.flag(cx.ctx, 0, 2), pr.flag(cx.ctx, 0, 3)
+    reply.value, done.value = 0, 0
+    announce("wait_host handshake")
+    pr.wait_host(cx.ctx, cx.s, 0, 2, 1, reset=0)
+    pr.launch(cx.ctx, cx.s, op, args)
+    pr.signal_host(cx.ctx, cx.s, 0, 3, 1)
+    time.sleep(0.1)
+    held = done.value
+    reply.value = 1
+    assert wait_for(done, 1)
+    pr.synchronize(cx.ctx, cx.s)
+    assert held == 0, "the stream ran past wait_host before the host replied"
+    assert reply.value == 0, "the consumer reset was not written"
+    got = cx.get(yb, np.float32, (ROWS, N_OUT))
+    assert (got.view(np.uint32) == o.gemv(o.Q4_K, w, N_OUT, K, x, ROWS).view(np.uint32)).all()
+    done.value = 0
+
+
+def test_wait_host_geq_and_no_reset(cx):
+    pr = cx.pr
+    reply, done = pr.flag(cx.ctx, 0, 4), pr.flag(cx.ctx, 0, 5)
+    reply.value, done.value = 3, 0
+    announce("wait_host geq")
+    pr.wait_host(cx.ctx, cx.s, 0, 4, 5, geq=True, reset=None)
+    pr.signal_host(cx.ctx, cx.s, 0, 5, 1)
+    time.sleep(0.05)
+    held = done.value
+    reply.value = 9
+    assert wait_for(done, 1)
+    pr.synchronize(cx.ctx, cx.s)
+    assert held == 0 and reply.value == 9
+    done.value = 0
+
+
+def test_captured_step_runs_the_handshake_on_every_replay(cx):
+    """One capture of wait_host(F = 1, reset 0) -> Gemv -> signal_host(D, 1), replayed three
+    times: per step the host writes x, raises F, waits for D, resets D (RFC-0040 4.2 rules 2-3)."""
+    pr = cx.pr
+    op, args, xb, yb, w, rng = gemv_step(cx, 3)
+    f, d = pr.flag(cx.ctx, 0, 6), pr.flag(cx.ctx, 0, 7)
+    f.value, d.value = 0, 0
+    announce("doorbell capture/replay")
+    pr.begin_capture(cx.ctx, cx.s)
+    pr.wait_host(cx.ctx, cx.s, 0, 6, 1, reset=0)
+    pr.launch(cx.ctx, cx.s, op, args)
+    pr.signal_host(cx.ctx, cx.s, 0, 7, 1)
+    g = pr.end_capture(cx.ctx, cx.s)
+    for step in range(3):
+        x = gemv_activations(rng, ROWS, K).reshape(ROWS, K).astype(np.float32)
+        cx.upload(xb.addr, x)
+        pr.replay(cx.ctx, cx.s, g)
+        time.sleep(0.02)
+        assert d.value == 0, f"step {step}: done before the reply"
+        f.value = 1
+        assert wait_for(d, 1), f"step {step}: no done flag"
+        d.value = 0
+        pr.synchronize(cx.ctx, cx.s)
+        assert f.value == 0
+        got = cx.get(yb, np.float32, (ROWS, N_OUT))
+        assert (got.view(np.uint32) == o.gemv(o.Q4_K, w, N_OUT, K, x, ROWS).view(np.uint32)).all(), step
+
+
+def test_flags_outside_the_pages_are_refused(cx):
+    P, pr = cx.P, cx.pr
+    for page, slot in [(0, 64), (1, 0), (65535, 63)]:
+        with pytest.raises(P.ProviderError):
+            pr.signal_host(cx.ctx, cx.s, page, slot, 1)
+        with pytest.raises(P.ProviderError):
+            pr.wait_host(cx.ctx, cx.s, page, slot, 1)
+    pr.synchronize(cx.ctx, cx.s)
+
+
+def test_a_wait_past_its_spin_limit_ends_and_is_reported():
+    """A context opened with a 2 ms limit: a wait the host never answers gives up on its own,
+    writes no reset, lets the stream run on (the next flag rises), and synchronize reports one
+    Timeout naming the flag; the next synchronize is clean."""
+    os.environ["SYNTROPY_SPIN_MAX_US"] = "2000"
+    try:
+        c = Ctx()
+    finally:
+        del os.environ["SYNTROPY_SPIN_MAX_US"]
+    try:
+        P, pr = c.P, c.pr
+        reply, after = pr.flag(c.ctx, 0, 9), pr.flag(c.ctx, 0, 10)
+        reply.value, after.value = 0, 0
+        announce("wait_host spin limit 2 ms")
+        pr.wait_host(c.ctx, c.s, 0, 9, 1, reset=5)
+        pr.signal_host(c.ctx, c.s, 0, 10, 1)
+        with pytest.raises(P.ProviderError) as e:
+            pr.synchronize(c.ctx, c.s)
+        assert e.value.cls == 10 and "slot 9" in str(e.value) and "spin limit of 2000" in str(e.value)
+        assert reply.value == 0 and after.value == 1
+        pr.synchronize(c.ctx, c.s)
+    finally:
+        c.close()

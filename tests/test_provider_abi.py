@@ -27,12 +27,13 @@ def pr():
     return P.Provider()
 
 
-def test_exports_exactly_the_entry_symbol():
+def test_exports_the_entry_symbol_and_the_flag_accessor_only():
     out = subprocess.run(["nm", "-D", "--defined-only", P.PROVIDER_LIB], capture_output=True, text=True,
                          check=True).stdout
     syms = [l.split()[-1] for l in out.splitlines() if l.split() and l.split()[-2] in "TtDdBbRrWwVv"]
-    syms = [s for s in syms if not s.startswith("SYNTROPY_PROVIDER_1")]
-    assert syms == ["syntropy_provider_entry_v1@@SYNTROPY_PROVIDER_1"], syms
+    syms = sorted(s for s in syms if not s.startswith("SYNTROPY_PROVIDER_1"))
+    assert syms == ["syntropy_provider_entry_v1@@SYNTROPY_PROVIDER_1",
+                    "syntropy_provider_flag_v1@@SYNTROPY_PROVIDER_1"], syms
 
 
 def test_struct_sizes_match_the_reference_layout():
@@ -121,14 +122,23 @@ def test_unserved_entries_are_unsupported(pr):
         "register_host": lambda: vt.register_host(slf, 1, P.HostRegion(0, 0), None),
         "host_registrar": lambda: vt.host_registrar(slf, 1, None),
         "import": lambda: getattr(vt, "import")(slf, 1, P.HostRegion(0, 0), None),
-        "signal_host": lambda: vt.signal_host(slf, 1, 1, 0, 1),
-        "wait_host": lambda: vt.wait_host(slf, 1, 1, 0, 1, 0, 0, 0),
         "arm_wake": lambda: vt.arm_wake(slf, 1, 1, 0, 0),
     }
     for name, f in calls.items():
         st = f()
         assert (st.cls, st.code, st.domain) == (2, 1, 1), name
         assert name in pr.message(), name
+
+
+def test_doorbell_entries_check_their_context(pr):
+    """signal_host and wait_host are served; on a context not open on this thread they refuse
+    with Internal before anything is enqueued (the CPU provider's flag_slot check,
+    crates/kernels-cpu/src/provider.rs:187-192, comes after its context check)."""
+    vt, slf = pr.vt, pr.vt.slf
+    for name, st in [("signal_host", vt.signal_host(slf, 987654, 1, 0, 1)),
+                     ("wait_host", vt.wait_host(slf, 987654, 1, 0, 1, 0, 1, 0))]:
+        assert st.cls == 13, name
+        assert "not open on this thread" in pr.message(), name
 
 
 def _key(op, weight, layout=0):
@@ -197,7 +207,7 @@ def test_messages_are_per_thread(pr):
 
     def other():
         seen["before"] = pr.message()
-        st = pr.vt.signal_host(pr.vt.slf, 1, 1, 0, 1)
+        st = pr.vt.arm_wake(pr.vt.slf, 1, 1, 0, 0)
         seen["cls"] = st.cls
         seen["after"] = pr.message()
 
@@ -205,7 +215,7 @@ def test_messages_are_per_thread(pr):
     t.start()
     t.join()
     assert "5551" in mine
-    assert seen["before"] == "" and seen["cls"] == 2 and "signal_host" in seen["after"]
+    assert seen["before"] == "" and seen["cls"] == 2 and "arm_wake" in seen["after"]
     assert pr.message() == mine
 
 
