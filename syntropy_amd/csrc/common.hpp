@@ -252,7 +252,7 @@ SYN_DEV void lds_dma16(uint32_t voff, const void* sbase, uint32_t lds) {
 // The rows a launch computes: `rows`, or fewer when `active` points at a step descriptor's
 // rows_active (crates/kernels/include/syntropy/step_desc.h:53-57), read on the device so that a
 // captured launch follows the value at each replay; `first` is the launch's first row.
-SYN_DEV inline int active_rows(const uint32_t* active, int first, int rows) {
+SYN_DEV int active_rows(const uint32_t* active, int first, int rows) {
     if (!active) return rows;
     const int64_t a = (int64_t)*active - first;
     return a <= 0 ? 0 : (a < rows ? (int)a : rows);
