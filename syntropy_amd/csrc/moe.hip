@@ -903,45 +903,69 @@ void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
 // MoeCombine (moe/tests.rs:541-556)
 // ============================================================================================
 
-// One workgroup per (row, 1024 columns); the row's slots are ordered by expert id (stable)
-// once in LDS, then each thread adds its columns in that order.
+// One workgroup per (row, 1024 columns).  The row's ids and weights go to LDS, each slot's rank
+// in (expert id, slot) order (a stable sort by id) is counted by its own thread, then each
+// thread adds its four columns over the slots in that order (float4 loads where the rows are
+// 16-byte aligned).
 __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ out,
                                                      const int32_t* __restrict__ ids,
                                                      const float* __restrict__ w, int top_k,
-                                                     int hidden, float* __restrict__ y,
+                                                     int hidden, int vec, float* __restrict__ y,
                                                      const uint32_t* __restrict__ active) {
     __shared__ int order[64];
-    const int r = blockIdx.y;
+    __shared__ int sid[64];
+    __shared__ float sw[64];
+    const int r = blockIdx.y, tid = threadIdx.x;
     if (r >= active_rows(active, 0, (int)gridDim.y)) return;  // uniform: a row past the active ones
-    if (threadIdx.x == 0) {
-        for (int j = 0; j < top_k; ++j) order[j] = j;
-        for (int a2 = 1; a2 < top_k; ++a2) {  // stable insertion sort by id
-            const int v = order[a2];
-            int b2 = a2;
-            while (b2 > 0 && ids[(int64_t)r * top_k + order[b2 - 1]] > ids[(int64_t)r * top_k + v]) {
-                order[b2] = order[b2 - 1];
-                --b2;
-            }
-            order[b2] = v;
-        }
+    if (tid < top_k) {
+        sid[tid] = ids[(int64_t)r * top_k + tid];
+        sw[tid] = w[(int64_t)r * top_k + tid];
     }
     __syncthreads();
-    for (int c = blockIdx.x * 1024 + threadIdx.x; c < hidden && c < (int)(blockIdx.x + 1) * 1024; c += 256) {
-        float acc = 0.0f;
+    if (tid < top_k) {
+        const int v = sid[tid];
+        int rank = 0;
+        for (int i = 0; i < top_k; ++i) {
+            const int u = sid[i];
+            rank += (u < v || (u == v && i < tid)) ? 1 : 0;
+        }
+        order[rank] = tid;
+    }
+    __syncthreads();
+    const int c = blockIdx.x * 1024 + 4 * tid;
+    if (c >= hidden) return;
+    const float* base = out + (int64_t)r * top_k * hidden;
+    if (vec) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (int a2 = 0; a2 < top_k; ++a2) {
             const int j = order[a2];
-            const float wj = w[(int64_t)r * top_k + j];
-            acc = acc + wj * out[((int64_t)r * top_k + j) * hidden + c];
+            const float wj = sw[j];
+            const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)j * hidden + c);
+            acc.x = acc.x + wj * v.x;
+            acc.y = acc.y + wj * v.y;
+            acc.z = acc.z + wj * v.z;
+            acc.w = acc.w + wj * v.w;
         }
-        y[(int64_t)r * hidden + c] = acc;
+        *reinterpret_cast<float4*>(y + (int64_t)r * hidden + c) = acc;
+    } else {
+        const int n = hidden - c < 4 ? hidden - c : 4;
+        for (int q = 0; q < n; ++q) {
+            float acc = 0.0f;
+            for (int a2 = 0; a2 < top_k; ++a2) {
+                const int j = order[a2];
+                acc = acc + sw[j] * base[(int64_t)j * hidden + c + q];
+            }
+            y[(int64_t)r * hidden + c + q] = acc;
+        }
     }
 }
 
 void launch_moe_combine(const float* out, const int32_t* ids, const float* w, int rows, int top_k,
                         int hidden, float* y, hipStream_t stream, const uint32_t* active) {
     if (rows == 0 || hidden == 0) return;
+    const int vec = hidden % 4 == 0 && (reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(y)) % 16 == 0;
     hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((hidden + 1023) / 1024), (unsigned)rows),
-                       dim3(256), 0, stream, out, ids, w, top_k, hidden, y, active);
+                       dim3(256), 0, stream, out, ids, w, top_k, hidden, vec, y, active);
 }
 
 }  // namespace syn

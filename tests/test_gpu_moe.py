@@ -332,11 +332,22 @@ def test_grouped_site_mask(M, rows, n_experts, top_k, hidden, inter):
 
 
 # ---- combine ------------------------------------------------------------------------------------
-def test_combine_bit_exact(M):
-    rs = np.random.default_rng(4)
-    rows, k, hidden = 33, 8, 1000
+@pytest.mark.parametrize("rows,k,hidden", [(33, 8, 1000), (5, 8, 1001), (64, 8, 4096), (3, 64, 130),
+                                          (7, 1, 4096), (2, 3, 2050)])
+def test_combine_bit_exact(M, rows, k, hidden):
+    """Float4 columns (hidden a multiple of 4) and the scalar tail; top_k 1 to 64; repeated ids
+    in a row keep their slot order (the stable sort of moe/tests.rs:541-556)."""
+    rs = np.random.default_rng(rows * 31 + hidden)
     out = rs.standard_normal((rows, k, hidden)).astype(np.float32)
-    ids = np.stack([rs.permutation(64)[:k] for _ in range(rows)]).astype(np.int32)
+    ids = np.stack([rs.permutation(max(64, k))[:k] for _ in range(rows)]).astype(np.int32)
+    if k > 2:
+        ids[0, 1] = ids[0, 0]
+        ids[-1, k - 1] = ids[-1, 0]
     w = rs.random((rows, k)).astype(np.float32)
-    announce("combine")
+    announce(f"combine rows={rows} k={k} hidden={hidden}")
     assert_same(host(M.combine(dev(out), dev(ids), dev(w))), o.moe_combine(out, ids, w))
+    # an output view 4 bytes into its buffer takes the scalar path
+    flat = torch.zeros(rows * k * hidden + 1, device="cuda")
+    flat[1:] = dev(out).reshape(-1)
+    view = flat[1:].view(rows, k, hidden)
+    assert_same(host(M.combine(view, dev(ids), dev(w))), o.moe_combine(out, ids, w), "unaligned")
