@@ -182,6 +182,109 @@ __global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ ro
     }
 }
 
+// Logits at many tokens: one workgroup per 16 tokens x 16 experts, one (token, expert) pair per
+// thread, so a wavefront's lanes read 4 token rows and 16 router rows (LDS broadcasts).  The
+// rows stream through LDS in chunks of 8 blocks (1 KB a row, padded by 16 bytes so the 16 router
+// rows of a read fall in distinct banks), double-buffered by DMA.  Each thread sums its pair's
+// 32-term blocks in order and keeps the pairwise tree as a binary stack: block j's sum merges
+// with the completed subtrees left of it (level L when bit L of j is set, left + right), and at
+// the end the subtrees of the set bits of nblk fold from the smallest up (left + right).  That is
+// reduce.rs's level-by-level tree with the odd value carried: the tree over n values is the tree
+// over the first 2^m (the largest power of two below n) plus the tree over the rest.
+constexpr int LT_T = 16, LT_E = 16, LT_CB = 8;
+constexpr int LT_ROW = LT_CB * 128 + 16;          // a row's chunk in LDS: 1,040 bytes
+constexpr int LT_STAGE = (LT_T + LT_E) * LT_ROW;  // 33,280 bytes; two stages
+constexpr int LT_LEVELS = 9;                      // nblk <= 256
+
+__global__ __launch_bounds__(256) void k_moe_logits_tile(const float* __restrict__ router,
+                                                         const float* __restrict__ x, int rows, int hidden,
+                                                         int n_experts, float* __restrict__ logits,
+                                                         const uint32_t* __restrict__ active) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lt_lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.x * LT_T, e0 = blockIdx.y * LT_E;
+    rows = active_rows(active, 0, rows);
+    if (t0 >= rows) return;  // uniform: tokens past the step's active rows
+    const int nblk = hidden / 32;
+    // wavefront w copies stage rows 8w .. 8w + 7 (tokens 0-15, then experts 0-15): lane l the
+    // 16 bytes l of the row's chunk, one copy per row (8 per chunk per wavefront)
+    auto issue = [&](int c0, uint8_t* stage) {
+        const int nb = nblk - c0 < LT_CB ? nblk - c0 : LT_CB;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 8 * wave + i;
+            const float* base;
+            if (r < LT_T) {
+                const int t = t0 + r < rows ? t0 + r : rows - 1;
+                base = x + (int64_t)t * hidden;
+            } else {
+                const int e = e0 + r - LT_T < n_experts ? e0 + r - LT_T : n_experts - 1;
+                base = router + (int64_t)e * hidden;
+            }
+            if (lane < 8 * nb) lds_dma16(16u * (uint32_t)lane + 128u * (uint32_t)c0, base, lds_addr(stage + r * LT_ROW));
+        }
+    };
+    const int tt = 4 * wave + (lane >> 4), ee = lane & 15;
+    float st[LT_LEVELS];
+#pragma unroll
+    for (int L = 0; L < LT_LEVELS; ++L) st[L] = 0.0f;
+    issue(0, lt_lds);
+    for (int c0 = 0, cur = 0; c0 < nblk; c0 += LT_CB, cur ^= 1) {
+        if (c0 + LT_CB < nblk) {
+            issue(c0 + LT_CB, lt_lds + (cur ^ 1) * LT_STAGE);
+            wait_vm<8>();  // this wavefront's copies of the current chunk, older than the next's
+        } else {
+            wait_vm<0>();
+        }
+        lds_barrier();
+        const uint8_t* stage = lt_lds + cur * LT_STAGE;
+        const float4* xr = reinterpret_cast<const float4*>(stage + tt * LT_ROW);
+        const float4* wr = reinterpret_cast<const float4*>(stage + (LT_T + ee) * LT_ROW);
+        const int nb = nblk - c0 < LT_CB ? nblk - c0 : LT_CB;
+        for (int bb = 0; bb < nb; ++bb) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 xv = xr[8 * bb + q], wv = wr[8 * bb + q];
+                acc = acc + wv.x * xv.x;
+                acc = acc + wv.y * xv.y;
+                acc = acc + wv.z * xv.z;
+                acc = acc + wv.w * xv.w;
+            }
+            // push block j = c0 + bb: merge with the left subtrees its set low bits complete
+            const int j = c0 + bb;
+            bool carry = true;
+#pragma unroll
+            for (int L = 0; L < LT_LEVELS; ++L) {
+                if (carry) {
+                    if ((j >> L) & 1) {
+                        acc = st[L] + acc;
+                    } else {
+                        st[L] = acc;
+                        carry = false;
+                    }
+                }
+            }
+        }
+        lds_barrier();  // this stage is refilled two chunks on
+    }
+    float total = 0.0f;
+    bool have = false;
+#pragma unroll
+    for (int L = 0; L < LT_LEVELS; ++L) {
+        if ((nblk >> L) & 1) {
+            total = have ? st[L] + total : st[L];
+            have = true;
+        }
+    }
+    if (t0 + tt < rows && e0 + ee < n_experts) logits[(int64_t)(t0 + tt) * n_experts + e0 + ee] = total;
+}
+
+// The many-token logits kernel from this many rows on (fewer: too few workgroups to fill the
+// chip); it copies 16-byte chunks, so the token rows must be 16-byte aligned.
+constexpr int LT_MIN_ROWS = 512;
+
 // Softmax and top-k: one wavefront per token (E <= 256, 4 experts per lane).  The selection
 // ranks every expert by (probability descending, index ascending), a NaN after every number
 // (the spec's order; with a NaN anywhere in a row every probability is NaN and the ranks are the
@@ -326,7 +429,14 @@ void launch_moe_route(const float* router, const float* x, int rows, int hidden,
         hipFuncSetAttribute((const void*)k_moe_logits<false>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     (void)lds_ok;  // a refusal shows as the launch's error
     (void)lds_ok4;
-    if (((uintptr_t)x & 15) == 0)
+    if (rows >= LT_MIN_ROWS && ((uintptr_t)x & 15) == 0 && ((uintptr_t)router & 15) == 0) {
+        static const hipError_t lt_ok = hipFuncSetAttribute((const void*)k_moe_logits_tile,
+                                                            hipFuncAttributeMaxDynamicSharedMemorySize, 2 * LT_STAGE);
+        (void)lt_ok;  // a refusal shows as the launch's error
+        const dim3 lg((rows + LT_T - 1) / LT_T, (n_experts + LT_E - 1) / LT_E);
+        hipLaunchKernelGGL(k_moe_logits_tile, lg, dim3(256), 2 * LT_STAGE, stream, router, x, rows, hidden, n_experts,
+                           logits, active);
+    } else if (((uintptr_t)x & 15) == 0)
         hipLaunchKernelGGL(k_moe_logits<true>, grid, dim3(256), lds, stream, router, x, rows, hidden, n_experts, logits,
                            active);
     else

@@ -50,7 +50,10 @@ def fast_q4k_experts(seed, n_experts, hidden, inter):
     # odd block counts at some tree level: 5 and 48 router blocks, 3 softmax blocks
     (9, 160, 70, 5), (300, 1536, 70, 4),
     # the widest rows (fewer experts per workgroup) and 256 experts
-    (3, 8192, 40, 3), (5, 7168, 256, 8)])
+    (3, 8192, 40, 3), (5, 7168, 256, 8),
+    # 512 rows and more: the many-token kernel (16 x 16 tiles, the tree as a binary stack):
+    # the prefill shape, 5 and 224 blocks, experts not a multiple of 16, 256 blocks (9 levels)
+    (2048, 4096, 128, 8), (700, 160, 70, 5), (513, 7168, 40, 3), (1000, 8192, 256, 8)])
 def test_route_bit_exact(M, rows, hidden, n_experts, top_k):
     router = o.normal(0x51A30004 + hidden, 0.02, n_experts * hidden).reshape(n_experts, hidden)
     x = o.normal(0x51A20004 + rows, 1.0, rows * hidden).reshape(rows, hidden)
