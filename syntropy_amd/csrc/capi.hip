@@ -726,16 +726,17 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
         const syn::MoeTiles mt{(uint32_t*)(base + m.pad_off), (uint32_t*)(base + m.tile_e),
                                (uint32_t*)(base + m.n_tiles)};
         const int64_t tpad = 64ll * m.max_tiles;
-        const syn::GemmAct gx = syn::gemm_act_at(base + m.xq, tpad, (int)hidden);
+        // the tokens' rows quantized once (the gate/up stage gathers each position's token)
+        const syn::GemmAct gx = syn::gemm_act_at(base + m.xq, (int64_t)syn::align_up(rows, 64), (int)hidden);
         const syn::GemmAct gh = syn::gemm_act_at(base + m.hq, tpad, (int)inter);
         float* h = (float*)(base + m.h);
         syn::launch_moe_tiles(offsets, (int)n_experts, err, mt, st);
-        syn::launch_moe_gemm_act(x, 1, slots, (int)top_k, (int)hidden, offsets, mt, err, gx, st);
+        syn::launch_gemm_act(x, (int)rows, (int)hidden, gx, st, active);
         syn::launch_moe_gemm(0, (const uint8_t*)gate, (const uint8_t*)up, (int)n_experts, (int)inter, (int)hidden,
-                             gx, m.max_tiles, offsets, mt, err, slots, h, st);
-        syn::launch_moe_gemm_act(h, 0, slots, (int)top_k, (int)inter, offsets, mt, err, gh, st);
+                             gx, m.max_tiles, offsets, mt, err, slots, h, st, (int)top_k);
+        syn::launch_moe_gemm_act(h, (int)inter, offsets, mt, err, gh, st);
         syn::launch_moe_gemm(1, (const uint8_t*)down, nullptr, (int)n_experts, (int)hidden, (int)inter, gh,
-                             m.max_tiles, offsets, mt, err, slots, out, st);
+                             m.max_tiles, offsets, mt, err, slots, out, st, (int)top_k);
         if (status) {
             hipError_t e = hipMemcpyAsync(status, err, 4, hipMemcpyDeviceToDevice, st);
             if (e != hipSuccess) return fail(SYN_E_DEVICE, "%s: status copy: %s", W, hipGetErrorString(e));

@@ -389,16 +389,17 @@ void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, 
 //
 // Each expert's entries (the packed lists of k_moe_pack: offsets, slots) are padded to whole
 // 64-entry tiles: tile i belongs to expert tile_e[i], and its padded position p = 64 i + t holds
-// entry offsets[e] + p - pad_off[e] when that is below offsets[e + 1] (padding rows are zero and
-// their outputs are dropped).  The entries' rows are quantized to Q8_K in the GEMM layout at
-// their padded positions (each entry's row exactly as the expert quantizes it, moe.rs:479-492),
-// then:
-//   gate/up: a workgroup takes (tile, 128 weight rows); its 256-row weight tile is those 128
-//     rows of the tile's gate matrix followed by the same 128 rows of its up matrix, so
-//     wavefronts 0-3 hold g and wavefronts 4-7 hold u of the same outputs, and
-//     h = silu(g) * u per entry (moe.rs:529-551);
-//   down: (tile, 256 rows) of the expert's down matrix on h requantized the same way; each
-//     output goes to its entry's slot (moe.rs:500-515).
+// entry offsets[e] + p - pad_off[e] when that is below offsets[e + 1] (padding positions'
+// outputs are dropped).  An entry's row is quantized exactly as the expert quantizes it
+// (moe.rs:479-492), which depends on the row alone, so:
+//   gate/up: the tokens' rows are quantized to Q8_K once, in the GEMM layout, and each stage
+//     gathers position p's row from its entry's token (slots[i] / top_k); a workgroup takes
+//     (tile, 128 weight rows); its 256-row weight tile is those 128 rows of the tile's gate
+//     matrix followed by the same 128 rows of its up matrix, so wavefronts 0-3 hold g and
+//     wavefronts 4-7 hold u of the same outputs, and h = silu(g) * u per entry
+//     (moe.rs:529-551);
+//   down: the entries' h rows quantized at their padded positions; (tile, 256 rows) of the
+//     expert's down matrix; each output goes to its entry's slot (moe.rs:500-515).
 // Every product is the Gemv value (the same exact sums and term fold as the dense GEMM).
 
 // One workgroup: an inclusive scan of the experts' tile counts (E <= 256).
@@ -431,12 +432,9 @@ void launch_moe_tiles(const uint32_t* offsets, int n_experts, const uint32_t* er
     hipLaunchKernelGGL(k_moe_tiles, dim3(1), dim3(256), 0, stream, offsets, n_experts, err, mt);
 }
 
-// The entries' rows at their padded positions: GATHER = 1 takes row slots[i] / top_k of x
-// (the entry's token), GATHER = 0 row i of h.  Positions in tiles past the used ones are not
-// written (no workgroup reads them).
-template <int GATHER>
-__global__ __launch_bounds__(256) void k_moe_gemm_act(const float* __restrict__ src,
-                                                      const uint32_t* __restrict__ slots, int top_k, int k,
+// The entries' h rows at their padded positions (row i of h for entry i).  Positions in tiles
+// past the used ones are not written (no workgroup reads them).
+__global__ __launch_bounds__(256) void k_moe_gemm_act(const float* __restrict__ h, int k,
                                                       const uint32_t* __restrict__ offsets, MoeTiles mt,
                                                       const uint32_t* __restrict__ err, GemmAct a) {
     if (err[0]) return;
@@ -448,21 +446,15 @@ __global__ __launch_bounds__(256) void k_moe_gemm_act(const float* __restrict__ 
     if (tile >= mt.n_tiles[0]) return;
     const uint32_t e = mt.tile_e[tile];
     const uint32_t i = offsets[e] + ((uint32_t)pos - mt.pad_off[e]);
-    const float* row = nullptr;
-    if (i < offsets[e + 1]) row = GATHER ? src + (int64_t)(slots[i] / (uint32_t)top_k) * k : src + (int64_t)i * k;
-    gemm_act_block(row, b, pos, a, lane);
+    gemm_act_block(i < offsets[e + 1] ? h + (int64_t)i * k : nullptr, b, pos, a, lane);
 }
 
-void launch_moe_gemm_act(const float* src, int gather, const uint32_t* slots, int top_k, int k,
-                         const uint32_t* offsets, MoeTiles mt, const uint32_t* err, GemmAct a,
-                         hipStream_t stream) {
+void launch_moe_gemm_act(const float* h, int k, const uint32_t* offsets, MoeTiles mt, const uint32_t* err,
+                         GemmAct a, hipStream_t stream) {
     const int64_t items = (int64_t)(k / 256) * a.tpad;
     if (items == 0) return;
-    const dim3 grid((unsigned)((items + 3) / 4));
-    if (gather)
-        hipLaunchKernelGGL(k_moe_gemm_act<1>, grid, dim3(256), 0, stream, src, slots, top_k, k, offsets, mt, err, a);
-    else
-        hipLaunchKernelGGL(k_moe_gemm_act<0>, grid, dim3(256), 0, stream, src, slots, top_k, k, offsets, mt, err, a);
+    hipLaunchKernelGGL(k_moe_gemm_act, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, h, k, offsets, mt,
+                       err, a);
 }
 
 struct MoeGemmArgs {
@@ -479,6 +471,8 @@ struct MoeGemmArgs {
     const uint32_t* slots;
     float* out;         // h [entries][cols] (MODE 0) or out [slots][cols] (MODE 1)
     int cols;           // inter (MODE 0) or hidden (MODE 1)
+    int top_k;          // MODE 0: act holds the tokens' rows, position p of a tile reads its
+                        // entry's token slots[i] / top_k
 };
 
 // MODE 0 (gate/up, 128 weight rows of each per workgroup) or 1 (down, 256 rows).
@@ -517,22 +511,60 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
         upper[u] = MODE == 0 && wave + GM_WAVES * u >= HALF_SLOTS;
         if (upper[u]) sl.woff[u] -= (uint32_t)(GM_ROWS / 2) * g.rb;
     }
-    const int live = sl.nw + GM_ASLOT / GM_WAVES + sl.nt;
+    // MODE 0 gathers each position's token row from the tokens' quantized rows: code slot u of
+    // this lane is 16-byte chunk q of position pa, which holds chunk q ^ (pa & 15) (the stage's
+    // bank skew) and sits in the token's row at chunk (q ^ (pa & 15)) ^ (tok & 15) (the row's
+    // own skew); tail: wavefronts 0-1 the s2 halves, 2 the scales, 3 the code sums, one position
+    // a lane (padding positions read token 0; their outputs are dropped)
+    const uint32_t tp = (uint32_t)g.act.tpad;
+    auto token_of = [&](int pa) -> uint32_t {
+        return pa < nvalid ? g.slots[i0 + (uint32_t)pa] / (uint32_t)g.top_k : 0u;
+    };
+    uint32_t aoff[GM_ASLOT / GM_WAVES];
+    uint32_t toff = 0;
+    if constexpr (MODE == 0) {
+#pragma unroll
+        for (int u = 0; u < GM_ASLOT / GM_WAVES; ++u) {
+            const int pa = 2 * (wave + GM_WAVES * u) + (lane >> 5), q = lane & 31;
+            const uint32_t tok = token_of(pa);
+            aoff[u] = tok * 512u + 16u * (uint32_t)((q ^ (pa & 15)) ^ (int)(tok & 15u));
+        }
+        if (wave < 2) {
+            toff = token_of((64 * wave + lane) >> 1) * 32u + 16u * (uint32_t)(lane & 1);
+        } else if (wave < 4) {
+            toff = tp * (wave == 2 ? 32u : 36u) + token_of(lane) * 4u;
+        }
+    }
+    const int live = sl.nw + GM_ASLOT / GM_WAVES + (MODE == 0 ? (wave < 4 ? 1 : 0) : sl.nt);
     auto issue = [&](int b, uint8_t* stage) {
         const uint8_t* w0 = b0 + 144 * (size_t)b;
         const uint8_t* w1 = b1 + 144 * (size_t)b;
-        const uint8_t* ab = g.act.codes + ((size_t)b * g.act.tpad + t0) * 512;
-        const uint8_t* tb = g.act.tail + (size_t)b * g.act.tpad * GM_TAIL_ROW;
         const uint32_t st = lds_addr(stage);
 #pragma unroll
         for (int u = 0; u < GM_WPW; ++u)
             if (u < sl.nw) lds_dma16(sl.woff[u], upper[u] ? w1 : w0, st + 1024u * (uint32_t)(wave + GM_WAVES * u));
+        if constexpr (MODE == 0) {
+            const uint32_t ab = (uint32_t)b * tp * 512u, tb = (uint32_t)b * tp * (uint32_t)GM_TAIL_ROW;
 #pragma unroll
-        for (int u = 0; u < GM_ASLOT / GM_WAVES; ++u) {
-            const int gs = wave + GM_WAVES * u;
-            lds_dma16(16u * (uint32_t)lane, ab + 1024 * gs, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
+            for (int u = 0; u < GM_ASLOT / GM_WAVES; ++u) {
+                const int gs = wave + GM_WAVES * u;
+                lds_dma16(ab + aoff[u], g.act.codes, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
+            }
+            const uint32_t tl = st + (uint32_t)(GM_WB + GM_AB);
+            if (wave < 2)
+                lds_dma16(tb + toff, g.act.tail, tl + 1024u * (uint32_t)wave);
+            else if (wave < 4)
+                lds_dma4(tb + toff, g.act.tail, tl + (wave == 2 ? 2048u : 2304u));
+        } else {
+            const uint8_t* ab = g.act.codes + ((size_t)b * g.act.tpad + t0) * 512;
+            const uint8_t* tb = g.act.tail + (size_t)b * g.act.tpad * GM_TAIL_ROW;
+#pragma unroll
+            for (int u = 0; u < GM_ASLOT / GM_WAVES; ++u) {
+                const int gs = wave + GM_WAVES * u;
+                lds_dma16(16u * (uint32_t)lane, ab + 1024 * gs, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
+            }
+            if (sl.ton) lds_dma16(sl.toff, tb, st + (uint32_t)(GM_WB + GM_AB) + 1024u * (uint32_t)wave);
         }
-        if (sl.ton) lds_dma16(sl.toff, tb, st + (uint32_t)(GM_WB + GM_AB) + 1024u * (uint32_t)wave);
     };
     v4f acc[GM_MT][GM_NT];
 #pragma unroll
@@ -592,8 +624,9 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
 
 void launch_moe_gemm(int mode, const uint8_t* w0, const uint8_t* w1, int n_experts, int rows, int k,
                      GemmAct act, int max_tiles, const uint32_t* offsets, MoeTiles mt, const uint32_t* err,
-                     const uint32_t* slots, float* out, hipStream_t stream) {
+                     const uint32_t* slots, float* out, hipStream_t stream, int top_k) {
     MoeGemmArgs g;
+    g.top_k = top_k;
     g.W0 = w0;
     g.W1 = w1;
     g.nb = k / 256;

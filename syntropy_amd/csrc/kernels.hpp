@@ -103,8 +103,8 @@ void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, 
                      const uint32_t* active = nullptr);
 // The MoE expert FFN at many tokens on the same kernels: entries padded to 64-entry tiles per
 // expert (pad_off [E+1], tile_e [max_tiles], n_tiles [1], built on the device from the packed
-// offsets), quantized into the GEMM layout at their padded positions, then gate/up -> h and
-// down -> the slots.
+// offsets); gate/up -> h on the tokens' rows quantized once (launch_gemm_act) and gathered per
+// position, then down -> the slots on h quantized at the padded positions.
 struct MoeTiles {
     uint32_t* pad_off;
     uint32_t* tile_e;
@@ -112,11 +112,13 @@ struct MoeTiles {
 };
 bool moe_gemm_supported(int hidden, int inter);
 void launch_moe_tiles(const uint32_t* offsets, int n_experts, const uint32_t* err, MoeTiles mt, hipStream_t stream);
-void launch_moe_gemm_act(const float* src, int gather, const uint32_t* slots, int top_k, int k,
-                         const uint32_t* offsets, MoeTiles mt, const uint32_t* err, GemmAct a, hipStream_t stream);
+void launch_moe_gemm_act(const float* h, int k, const uint32_t* offsets, MoeTiles mt, const uint32_t* err,
+                         GemmAct a, hipStream_t stream);
+// mode 0 (gate/up): act holds the tokens' rows (launch_gemm_act of x), gathered per position;
+// mode 1 (down): act holds the entries' h rows at their padded positions.
 void launch_moe_gemm(int mode, const uint8_t* w0, const uint8_t* w1, int n_experts, int rows, int k,
                      GemmAct act, int max_tiles, const uint32_t* offsets, MoeTiles mt, const uint32_t* err,
-                     const uint32_t* slots, float* out, hipStream_t stream);
+                     const uint32_t* slots, float* out, hipStream_t stream, int top_k);
 // quant.hip
 void launch_quantize(int ty, const float* x, uint64_t n, uint8_t* out, hipStream_t stream);
 void launch_dequantize(int ty, const uint8_t* src, uint64_t n, float* out, hipStream_t stream);
