@@ -242,27 +242,40 @@ __global__ __launch_bounds__(256) void k_moe_logits_tile(const float* __restrict
         const float4* xr = reinterpret_cast<const float4*>(stage + tt * LT_ROW);
         const float4* wr = reinterpret_cast<const float4*>(stage + (LT_T + ee) * LT_ROW);
         const int nb = nblk - c0 < LT_CB ? nblk - c0 : LT_CB;
-        for (int bb = 0; bb < nb; ++bb) {
-            float acc = 0.0f;
+        // four blocks' sums at a time (independent chains), pushed in block order: block j's sum
+        // merges with the left subtrees its set low bits complete
+        for (int b4 = 0; b4 < nb; b4 += 4) {
+            float acc[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[u] = 0.0f;
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const float4 xv = xr[8 * bb + q], wv = wr[8 * bb + q];
-                acc = acc + wv.x * xv.x;
-                acc = acc + wv.y * xv.y;
-                acc = acc + wv.z * xv.z;
-                acc = acc + wv.w * xv.w;
-            }
-            // push block j = c0 + bb: merge with the left subtrees its set low bits complete
-            const int j = c0 + bb;
-            bool carry = true;
 #pragma unroll
-            for (int L = 0; L < LT_LEVELS; ++L) {
-                if (carry) {
-                    if ((j >> L) & 1) {
-                        acc = st[L] + acc;
-                    } else {
-                        st[L] = acc;
-                        carry = false;
+                for (int u = 0; u < 4; ++u) {
+                    const int bb = b4 + u < nb ? b4 + u : b4;  // past the chunk: a valid block, unused
+                    const float4 xv = xr[8 * bb + q], wv = wr[8 * bb + q];
+                    acc[u] = acc[u] + wv.x * xv.x;
+                    acc[u] = acc[u] + wv.y * xv.y;
+                    acc[u] = acc[u] + wv.z * xv.z;
+                    acc[u] = acc[u] + wv.w * xv.w;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (b4 + u < nb) {
+                    const int j = c0 + b4 + u;
+                    float v = acc[u];
+                    bool carry = true;
+#pragma unroll
+                    for (int L = 0; L < LT_LEVELS; ++L) {
+                        if (carry) {
+                            if ((j >> L) & 1) {
+                                v = st[L] + v;
+                            } else {
+                                st[L] = v;
+                                carry = false;
+                            }
+                        }
                     }
                 }
             }
