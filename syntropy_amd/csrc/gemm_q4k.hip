@@ -373,12 +373,10 @@ void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, 
     g.nb = k / 256;
     g.tpad = a.tpad;
     g.rb = (uint32_t)(k / 256) * 144u;
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute((const void*)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  2 * GM_STAGE);
-        attr = true;
-    }
+    // once per process, thread-safe (a function-local static); a refusal shows as the launch's error
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * GM_STAGE);
+    (void)attr;
     const dim3 grid((unsigned)((n_out + GM_ROWS - 1) / GM_ROWS), (unsigned)(a.tpad / GM_TT));
     hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(64 * GM_WAVES), 2 * GM_STAGE, stream, g);
 }
