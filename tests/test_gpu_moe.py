@@ -53,7 +53,10 @@ def fast_q4k_experts(seed, n_experts, hidden, inter):
     (3, 8192, 40, 3), (5, 7168, 256, 8),
     # 512 rows and more: the many-token kernel (16 x 16 tiles, the tree as a binary stack):
     # the prefill shape, 5 and 224 blocks, experts not a multiple of 16, 256 blocks (9 levels)
-    (2048, 4096, 128, 8), (700, 160, 70, 5), (513, 7168, 40, 3), (1000, 8192, 256, 8)])
+    (2048, 4096, 128, 8), (700, 160, 70, 5), (513, 7168, 40, 3), (1000, 8192, 256, 8),
+    # one 32-value block (the tree is that block's sum), both kernels; 7 and 31 blocks (partial
+    # 8-block chunks of the many-token kernel)
+    (10, 32, 8, 2), (600, 32, 20, 3), (520, 224, 33, 4), (530, 992, 17, 1)])
 def test_route_bit_exact(M, rows, hidden, n_experts, top_k):
     router = o.normal(0x51A30004 + hidden, 0.02, n_experts * hidden).reshape(n_experts, hidden)
     x = o.normal(0x51A20004 + rows, 1.0, rows * hidden).reshape(rows, hidden)
@@ -295,6 +298,22 @@ def test_grouped_refusal_writes_nothing(M):
     got, st = run_grouped(M, s, gate, up, down, x, ids)
     assert st == 1
     assert np.isnan(got).all()
+
+
+@pytest.mark.parametrize("rows,n_experts,top_k", [(3, 256, 1), (40, 256, 8), (300, 4, 1)])
+def test_grouped_extreme_expert_counts(M, rows, n_experts, top_k):
+    """256 experts (the largest) with top-1 and top-8 at decode sizes, and top-1 over 4 experts
+    on the many-token path (75 entries per expert)."""
+    s = M.MoeShape(n_experts, top_k, 256, 256)
+    gate, up, down = fast_q4k_experts(13 + rows, n_experts, 256, 256)
+    rs = np.random.default_rng(rows + n_experts)
+    x = rs.standard_normal((rows, 256)).astype(np.float32)
+    ids = np.stack([rs.permutation(n_experts)[:top_k] for _ in range(rows)]).astype(np.int32)
+    announce(f"grouped E={n_experts} k={top_k} rows={rows}")
+    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    assert st == 0
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, n_experts, top_k, 256, 256, gate, up, down, x, ids, threads=8)
+    assert_same(got, want, "extreme experts")
 
 
 # ---- the site mask (MoeGrouped's input 2) ------------------------------------------------------
