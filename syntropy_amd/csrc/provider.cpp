@@ -17,11 +17,16 @@
 // The hot entries (launch, record, wait, poll, copy, copy_batch, replay, health) take no lock
 // and allocate nothing: they look up handles in the calling thread's context and enqueue.
 #include <hip/hip_runtime.h>
+#include <linux/futex.h>
+#include <sys/syscall.h>
+#include <unistd.h>
 
 #include <atomic>
+#include <climits>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <deque>
 #include <exception>
 #include <string>
 #include <unordered_map>
@@ -488,6 +493,27 @@ constexpr uint32_t FLAG_WORDS = 16;
 constexpr uint32_t MAX_FLAG_PAGES = 1024;
 constexpr uint64_t DEFAULT_SPIN_US = 2000000;
 
+// A host thread's wake target (RFC-0040 ...md:592-600, HostWaker): kind 0 a futex word at
+// `handle` that the waiter sets to 1 before it parks (FUTEX_WAIT on 1), kind 1 an eventfd.
+struct WakeTarget {
+    uint32_t kind;
+    uint64_t handle;
+};
+
+// The host-function node's body: clears an armed futex word and wakes its waiters, or adds 1 to
+// the eventfd.  No HIP call (it runs on the runtime's callback thread).
+void wake_target(void* p) {
+    const WakeTarget* w = static_cast<const WakeTarget*>(p);
+    if (w->kind == 0) {
+        uint32_t* word = reinterpret_cast<uint32_t*>(w->handle);
+        if (__atomic_exchange_n(word, 0u, __ATOMIC_ACQ_REL) == 1u)
+            (void)syscall(SYS_futex, word, FUTEX_WAKE, INT_MAX, nullptr, nullptr, 0);
+    } else {
+        const uint64_t one = 1;
+        (void)!write((int)w->handle, &one, sizeof one);
+    }
+}
+
 struct Ctx {
     int device = 0;
     uint32_t* bells = nullptr;      // host address
@@ -495,6 +521,12 @@ struct Ctx {
     uint32_t n_bells = 0;
     uint64_t spin_us = DEFAULT_SPIN_US;
     uint64_t spin_ticks = 0;
+    // arm_wake: per stream, the side stream its host-function nodes run on, whether a fork is
+    // still to be joined (at end_capture), the fork events, and the wake targets the nodes read
+    std::unordered_map<uint64_t, hipStream_t> side;
+    std::unordered_map<uint64_t, bool> forked;
+    std::vector<hipEvent_t> fork_events;
+    std::deque<WakeTarget> wakes;
     std::unordered_map<uint64_t, Buf> bufs;
     std::unordered_map<uint64_t, hipStream_t> streams;
     std::unordered_map<uint64_t, hipEvent_t> events;
@@ -790,6 +822,11 @@ SynStatus e_close_ctx(void*, uint64_t ctx) {
         (void)hipSetDevice(c->device);
         for (auto& g : c->graphs) (void)hipGraphExecDestroy(g.second);
         for (auto& e : c->events) (void)hipEventDestroy(e.second);
+        for (auto& s : c->side) {
+            (void)hipStreamSynchronize(s.second);  // pending wakes run before their targets go
+            (void)hipStreamDestroy(s.second);
+        }
+        for (auto& e : c->fork_events) (void)hipEventDestroy(e);
         for (auto& s : c->streams) (void)hipStreamDestroy(s.second);
         for (auto& b : c->bufs) (void)hipFree(b.second.ptr);
         if (c->bells) (void)hipHostFree(c->bells);
@@ -868,7 +905,6 @@ SYN_UNSERVED(unmap_segment, void*, uint64_t, const SynSegment*)
 SYN_UNSERVED(register_host, void*, uint64_t, SynHostRegion, SynRegistration*)
 SYN_UNSERVED(host_registrar, void*, uint64_t, SynRegistrarVtbl*)
 SYN_UNSERVED(import, void*, uint64_t, SynHostRegion, SynBuffer*)
-SYN_UNSERVED(arm_wake, void*, uint64_t, uint64_t, uint32_t, uint64_t)
 #undef SYN_UNSERVED
 
 SynStatus e_set_resident(void*, uint64_t ctx, const SynBuffer*, size_t, uint32_t) {
@@ -971,6 +1007,33 @@ SynStatus e_wait_host(void*, uint64_t ctx, uint64_t s, uint32_t flag, uint32_t v
     });
 }
 
+// arm_wake (provider.rs:378-384; RFC-0040 ...md:590-600, the HIP row): a host-function node on
+// a side branch forked from `s` at this point, so the wake follows the work enqueued so far
+// (normally a doorbell write) and `s` never waits for it; a captured branch is joined back at
+// end_capture, the step's end.  Kinds: 0 Futex (handle: the word's address), 1 EventFd
+// (handle: the descriptor); WinEvent and TimelineValue are not served.
+SynStatus e_arm_wake(void*, uint64_t ctx, uint64_t s, uint32_t kind, uint64_t handle) {
+    return call("arm_wake", false, [&] {
+        if (kind > 1) unsupported("arm_wake: wake kind " + std::to_string(kind) + " (Futex 0 and EventFd 1 only)");
+        Ctx& c = ctx_of(ctx);
+        if (kind == 0 && (handle == 0 || handle % 4)) internal("arm_wake: a futex word must be a 4-byte aligned address");
+        if (kind == 1 && handle > (uint64_t)INT_MAX) internal("arm_wake: not a file descriptor");
+        hipStream_t st = stream_of(c, s);
+        hipStream_t& side = c.side[s];
+        if (!side) check_hip(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "hipStreamCreate(arm_wake)");
+        hipEvent_t ev = nullptr;
+        check_hip(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate(arm_wake)");
+        c.fork_events.push_back(ev);
+        c.wakes.push_back(WakeTarget{kind, handle});
+        check_hip(hipEventRecord(ev, st), "hipEventRecord(arm_wake)");
+        check_hip(hipStreamWaitEvent(side, ev, 0), "hipStreamWaitEvent(arm_wake)");
+        check_hip(hipLaunchHostFunc(side, wake_target, &c.wakes.back()), "hipLaunchHostFunc(arm_wake)");
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        check_hip(hipStreamIsCapturing(st, &cap), "hipStreamIsCapturing");
+        if (cap == hipStreamCaptureStatusActive) c.forked[s] = true;  // joined at end_capture
+    });
+}
+
 SynStatus e_poll(void*, uint64_t ctx, uint64_t e, uint32_t* done) {
     return call("poll", false, [&] {
         Ctx& c = ctx_of(ctx);
@@ -1063,6 +1126,14 @@ SynStatus e_begin_capture(void*, uint64_t ctx, uint64_t s) {
 SynStatus e_end_capture(void*, uint64_t ctx, uint64_t s, uint64_t* out) {
     return call("end_capture", false, [&] {
         Ctx& c = ctx_of(ctx);
+        if (c.forked[s]) {  // join the wakes' branch back: the captured step ends after them
+            hipEvent_t ev = nullptr;
+            check_hip(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate(join)");
+            c.fork_events.push_back(ev);
+            check_hip(hipEventRecord(ev, c.side[s]), "hipEventRecord(join)");
+            check_hip(hipStreamWaitEvent(stream_of(c, s), ev, 0), "hipStreamWaitEvent(join)");
+            c.forked[s] = false;
+        }
         hipGraph_t g = nullptr;
         check_hip(hipStreamEndCapture(stream_of(c, s), &g), "hipStreamEndCapture");
         hipGraphExec_t ex = nullptr;

@@ -344,6 +344,11 @@ class Provider:
         self._ok("wait_host", self.vt.wait_host(self.vt.slf, ctx, s, page << 16 | slot, value, int(geq),
                                                 int(reset is not None), reset or 0), ctx)
 
+    def arm_wake(self, ctx: int, s: int, kind: int, handle: int):
+        """After the work enqueued so far on `s`, wake a host thread without `s` waiting:
+        kind 0 a futex word's address (cleared from 1 and woken), kind 1 an eventfd (+1)."""
+        self._ok("arm_wake", self.vt.arm_wake(self.vt.slf, ctx, s, kind, handle), ctx)
+
     def flag(self, ctx: int, page: int, slot: int) -> C.c_uint32:
         """The host side of a doorbell flag, as a c_uint32 over its pinned word."""
         f = self.lib.syntropy_provider_flag_v1

@@ -135,6 +135,93 @@ def test_captured_step_runs_the_handshake_on_every_replay(cx):
         assert (got.view(np.uint32) == o.gemv(o.Q4_K, w, N_OUT, K, x, ROWS).view(np.uint32)).all(), step
 
 
+def wait_readable(fd, seconds=5.0):
+    import select
+    r, _, _ = select.select([fd], [], [], seconds)
+    return bool(r)
+
+
+def test_arm_wake_eventfd_after_the_doorbell(cx):
+    """arm_wake after signal_host: the eventfd fires once the doorbell is up (the wake follows
+    the work before it) and the stream did not wait for it."""
+    pr = cx.pr
+    op, args, xb, yb, w, rng = gemv_step(cx, 4)
+    cx.upload(xb.addr, gemv_activations(rng, ROWS, K).reshape(ROWS, K).astype(np.float32))
+    d = pr.flag(cx.ctx, 0, 11)
+    d.value = 0
+    fd = os.eventfd(0, os.EFD_NONBLOCK)
+    try:
+        announce("arm_wake eventfd")
+        pr.launch(cx.ctx, cx.s, op, args)
+        pr.signal_host(cx.ctx, cx.s, 0, 11, 1)
+        pr.arm_wake(cx.ctx, cx.s, 1, fd)
+        assert wait_readable(fd), "no wake within 5 s"
+        assert d.value == 1, "the wake came before the doorbell"
+        assert os.eventfd_read(fd) == 1
+        pr.synchronize(cx.ctx, cx.s)
+    finally:
+        os.close(fd)
+        d.value = 0
+
+
+def test_arm_wake_futex_word_is_cleared_and_woken(cx):
+    """A futex word the waiter armed (1) is cleared by the wake, and a thread waiting on it in
+    FUTEX_WAIT returns before its timeout."""
+    import ctypes as C
+    import threading
+    pr = cx.pr
+    word = C.c_uint32(1)
+    libc = C.CDLL(None, use_errno=True)
+
+    class Timespec(C.Structure):
+        _fields_ = [("tv_sec", C.c_long), ("tv_nsec", C.c_long)]
+
+    out = {}
+
+    def waiter():
+        t0 = time.monotonic()
+        rc = libc.syscall(202, C.byref(word), 0, 1, C.byref(Timespec(5, 0)), None, 0)  # FUTEX_WAIT on 1
+        out["rc"], out["errno"], out["dt"] = rc, C.get_errno(), time.monotonic() - t0
+
+    th = threading.Thread(target=waiter)
+    th.start()
+    time.sleep(0.05)  # the waiter is in FUTEX_WAIT (or returns EAGAIN if the wake came first)
+    announce("arm_wake futex")
+    pr.arm_wake(cx.ctx, cx.s, 0, C.addressof(word))
+    th.join(10)
+    pr.synchronize(cx.ctx, cx.s)
+    assert word.value == 0
+    assert out["dt"] < 4.5, "the waiter slept until its timeout"
+    assert out["rc"] == 0 or out["errno"] == 11  # woken, or the word was already cleared
+
+
+def test_captured_arm_wake_fires_on_every_replay(cx):
+    pr = cx.pr
+    op, args, xb, yb, w, rng = gemv_step(cx, 5)
+    d = pr.flag(cx.ctx, 0, 12)
+    d.value = 0
+    fd = os.eventfd(0, os.EFD_NONBLOCK)
+    try:
+        announce("arm_wake capture/replay")
+        pr.begin_capture(cx.ctx, cx.s)
+        pr.launch(cx.ctx, cx.s, op, args)
+        pr.signal_host(cx.ctx, cx.s, 0, 12, 1)
+        pr.arm_wake(cx.ctx, cx.s, 1, fd)
+        g = pr.end_capture(cx.ctx, cx.s)
+        for step in range(3):
+            x = gemv_activations(rng, ROWS, K).reshape(ROWS, K).astype(np.float32)
+            cx.upload(xb.addr, x)
+            pr.replay(cx.ctx, cx.s, g)
+            assert wait_readable(fd), f"replay {step}: no wake"
+            assert d.value == 1 and os.eventfd_read(fd) == 1, step
+            d.value = 0
+            pr.synchronize(cx.ctx, cx.s)
+            got = cx.get(yb, np.float32, (ROWS, N_OUT))
+            assert (got.view(np.uint32) == o.gemv(o.Q4_K, w, N_OUT, K, x, ROWS).view(np.uint32)).all(), step
+    finally:
+        os.close(fd)
+
+
 def test_flags_outside_the_pages_are_refused(cx):
     P, pr = cx.P, cx.pr
     for page, slot in [(0, 64), (1, 0), (65535, 63)]:

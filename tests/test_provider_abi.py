@@ -122,12 +122,23 @@ def test_unserved_entries_are_unsupported(pr):
         "register_host": lambda: vt.register_host(slf, 1, P.HostRegion(0, 0), None),
         "host_registrar": lambda: vt.host_registrar(slf, 1, None),
         "import": lambda: getattr(vt, "import")(slf, 1, P.HostRegion(0, 0), None),
-        "arm_wake": lambda: vt.arm_wake(slf, 1, 1, 0, 0),
+        "arm_wake": lambda: vt.arm_wake(slf, 1, 1, 3, 0),  # TimelineValue: not served
     }
     for name, f in calls.items():
         st = f()
         assert (st.cls, st.code, st.domain) == (2, 1, 1), name
         assert name in pr.message(), name
+
+
+def test_arm_wake_serves_futex_and_eventfd_only(pr):
+    """WakeKind codes (crates/kernels/src/abi/wire.rs:180-197): Futex 0 and EventFd 1 are
+    served (checked against the context next), WinEvent 2 and TimelineValue 3 are Unsupported."""
+    vt, slf = pr.vt, pr.vt.slf
+    for kind in (2, 3):
+        st = vt.arm_wake(slf, 987654, 1, kind, 5)
+        assert (st.cls, st.code) == (2, 1), kind
+    for kind in (0, 1):
+        assert vt.arm_wake(slf, 987654, 1, kind, 64).cls == 13, kind
 
 
 def test_doorbell_entries_check_their_context(pr):
@@ -207,7 +218,7 @@ def test_messages_are_per_thread(pr):
 
     def other():
         seen["before"] = pr.message()
-        st = pr.vt.arm_wake(pr.vt.slf, 1, 1, 0, 0)
+        st = pr.vt.map_segment(pr.vt.slf, 1, None, 0, 0, None)
         seen["cls"] = st.cls
         seen["after"] = pr.message()
 
@@ -215,7 +226,7 @@ def test_messages_are_per_thread(pr):
     t.start()
     t.join()
     assert "5551" in mine
-    assert seen["before"] == "" and seen["cls"] == 2 and "arm_wake" in seen["after"]
+    assert seen["before"] == "" and seen["cls"] == 2 and "map_segment" in seen["after"]
     assert pr.message() == mine
 
 
