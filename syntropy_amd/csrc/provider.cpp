@@ -26,7 +26,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <deque>
+#include <map>
 #include <exception>
 #include <string>
 #include <unordered_map>
@@ -521,12 +521,14 @@ struct Ctx {
     uint32_t n_bells = 0;
     uint64_t spin_us = DEFAULT_SPIN_US;
     uint64_t spin_ticks = 0;
-    // arm_wake: per stream, the side stream its host-function nodes run on, whether a fork is
-    // still to be joined (at end_capture), the fork events, and the wake targets the nodes read
+    // arm_wake: per stream, the side stream its host-function nodes run on, its fork and join
+    // events (reused: a wait takes the event's state when it is enqueued), whether a captured
+    // fork is still to be joined (at end_capture); and the wake targets the nodes read, one per
+    // (kind, handle) at a stable address
     std::unordered_map<uint64_t, hipStream_t> side;
+    std::unordered_map<uint64_t, hipEvent_t> fork_ev, join_ev;
     std::unordered_map<uint64_t, bool> forked;
-    std::vector<hipEvent_t> fork_events;
-    std::deque<WakeTarget> wakes;
+    std::map<std::pair<uint32_t, uint64_t>, WakeTarget> wakes;
     std::unordered_map<uint64_t, Buf> bufs;
     std::unordered_map<uint64_t, hipStream_t> streams;
     std::unordered_map<uint64_t, hipEvent_t> events;
@@ -826,7 +828,8 @@ SynStatus e_close_ctx(void*, uint64_t ctx) {
             (void)hipStreamSynchronize(s.second);  // pending wakes run before their targets go
             (void)hipStreamDestroy(s.second);
         }
-        for (auto& e : c->fork_events) (void)hipEventDestroy(e);
+        for (auto& e : c->fork_ev) (void)hipEventDestroy(e.second);
+        for (auto& e : c->join_ev) (void)hipEventDestroy(e.second);
         for (auto& s : c->streams) (void)hipStreamDestroy(s.second);
         for (auto& b : c->bufs) (void)hipFree(b.second.ptr);
         if (c->bells) (void)hipHostFree(c->bells);
@@ -1021,13 +1024,12 @@ SynStatus e_arm_wake(void*, uint64_t ctx, uint64_t s, uint32_t kind, uint64_t ha
         hipStream_t st = stream_of(c, s);
         hipStream_t& side = c.side[s];
         if (!side) check_hip(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "hipStreamCreate(arm_wake)");
-        hipEvent_t ev = nullptr;
-        check_hip(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate(arm_wake)");
-        c.fork_events.push_back(ev);
-        c.wakes.push_back(WakeTarget{kind, handle});
+        hipEvent_t& ev = c.fork_ev[s];
+        if (!ev) check_hip(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate(arm_wake)");
+        WakeTarget& target = c.wakes.emplace(std::make_pair(kind, handle), WakeTarget{kind, handle}).first->second;
         check_hip(hipEventRecord(ev, st), "hipEventRecord(arm_wake)");
         check_hip(hipStreamWaitEvent(side, ev, 0), "hipStreamWaitEvent(arm_wake)");
-        check_hip(hipLaunchHostFunc(side, wake_target, &c.wakes.back()), "hipLaunchHostFunc(arm_wake)");
+        check_hip(hipLaunchHostFunc(side, wake_target, &target), "hipLaunchHostFunc(arm_wake)");
         hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
         check_hip(hipStreamIsCapturing(st, &cap), "hipStreamIsCapturing");
         if (cap == hipStreamCaptureStatusActive) c.forked[s] = true;  // joined at end_capture
@@ -1127,9 +1129,8 @@ SynStatus e_end_capture(void*, uint64_t ctx, uint64_t s, uint64_t* out) {
     return call("end_capture", false, [&] {
         Ctx& c = ctx_of(ctx);
         if (c.forked[s]) {  // join the wakes' branch back: the captured step ends after them
-            hipEvent_t ev = nullptr;
-            check_hip(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate(join)");
-            c.fork_events.push_back(ev);
+            hipEvent_t& ev = c.join_ev[s];
+            if (!ev) check_hip(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate(join)");
             check_hip(hipEventRecord(ev, c.side[s]), "hipEventRecord(join)");
             check_hip(hipStreamWaitEvent(stream_of(c, s), ev, 0), "hipStreamWaitEvent(join)");
             c.forked[s] = false;

@@ -159,6 +159,16 @@ def test_arm_wake_eventfd_after_the_doorbell(cx):
         assert d.value == 1, "the wake came before the doorbell"
         assert os.eventfd_read(fd) == 1
         pr.synchronize(cx.ctx, cx.s)
+        # many wakes of one target reuse the context's fork event and target record
+        for _ in range(100):
+            pr.arm_wake(cx.ctx, cx.s, 1, fd)
+        pr.synchronize(cx.ctx, cx.s)
+        end = time.monotonic() + 5
+        n = 0
+        while n < 100 and time.monotonic() < end:
+            if wait_readable(fd, 0.5):
+                n += os.eventfd_read(fd)
+        assert n == 100
     finally:
         os.close(fd)
         d.value = 0
