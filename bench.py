@@ -349,7 +349,7 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {a.gpus} is not supported "
-              "(this build runs on one GPU only)", file=sys.stderr)
+              "(one GPU only)", file=sys.stderr)
         sys.exit(2)
     import torch
     import syntropy_amd.gemv as S

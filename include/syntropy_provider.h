@@ -274,7 +274,7 @@ typedef struct SynModule {
 } SynModule;
 
 /* The entry point (crates/kernels/src/abi/mod.rs:64: ENTRY_SYMBOL; EntryFn).  Returns null when
- * the host's header is not "SYNPROV1", major 1, or shorter than this build's SynHostApi.  The
+ * the host's header is not "SYNPROV1", major 1, or shorter than this header's SynHostApi.  The
  * module has one provider: id "hip", backend Hip, domain Hip, serving Gemv (Q4_0, Q8_0, Q4_K),
  * MoeGrouped (Q4_K), MoeRoute{Softmax} and MoeCombine on AMD gfx950 devices. */
 const SynModule* syntropy_provider_entry_v1(const SynHostApi* host);

@@ -1,7 +1,7 @@
 /*
  * oracle.c -- CPU restatement of the reference's quantized-matmul and MoE path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels and the "port" CPU baseline.
+ * TEST INFRASTRUCTURE ONLY: what the HIP kernels are compared against, and the "port" CPU baseline.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
  *
  * Build with -ffp-contract=off and without fast-math: every float operation below is one IEEE

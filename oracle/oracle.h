@@ -1,7 +1,7 @@
 /*
  * oracle.h -- CPU restatement of the reference's quantized-matmul and MoE path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker the HIP path is compared against
+ * TEST INFRASTRUCTURE ONLY.  This library is what the HIP path is compared against
  * (and the "port" CPU baseline that bench.py times).  Only tests/, __graft_entry__.smoke()
  * and bench.py's cpu_baseline leg may load it; the product library never links or calls it.
  *

@@ -1,6 +1,6 @@
 """ctypes bindings of the C oracle (oracle/oracle.c) and of the reference ggml build.
 
-TEST INFRASTRUCTURE ONLY: the checker the HIP kernels are compared against, and the "port"
+TEST INFRASTRUCTURE ONLY: what the HIP kernels are compared against, and the "port"
 CPU baseline bench.py times.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
 leg may import it.  Each function mirrors the C function of the same name minus the `or_`
 prefix; the C file cites the reference function each one restates.

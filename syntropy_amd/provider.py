@@ -186,7 +186,7 @@ def _no_config(key):
 
 
 def host_api(magic: bytes = MAGIC, major: int = ABI_MAJOR, size: int | None = None) -> HostApi:
-    """The host's services with a header of this build's identity (zero build id)."""
+    """The host's services with a header of this library's identity (zero build id)."""
     h = Header()
     C.memmove(h.magic, magic, 8)
     h.abi_major, h.abi_minor = major, ABI_MINOR
