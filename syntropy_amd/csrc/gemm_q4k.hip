@@ -31,6 +31,7 @@
 // latencies), so each A operand serves two row tiles and each B operand four token tiles.  Per super-block the weight rows (144 bytes each), the 64 tokens' codes and their
 // sums, scales and X stream from global memory into LDS with global_load_lds_dwordx4 (no
 // registers held while they fly), one stage ahead, in a ring of two 72 KB stages.
+#include <type_traits>
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -195,10 +196,11 @@ SYN_DEV GemmSlots gemm_slots(const GemmArgs& g, int wave, int lane, int n0, int 
 }
 
 
-// Issues the wavefront's loads of super-block b into `stage`.  Slot order: weight parts
-// wave, wave + 8, ..; code parts wave, wave + 8, ..; tail part `wave`.
+// Issues the wavefront's loads of super-block b: weights and codes into `stage`, the tail into
+// `tail`.  Slot order: weight parts wave, wave + 8, ..; code parts wave, wave + 8, ..; tail part
+// `wave`.
 SYN_DEV void gemm_issue(const GemmArgs& g, const GemmSlots& s, int wave, int lane, int b, int t0,
-                        uint8_t* stage) {
+                        uint8_t* stage, uint8_t* tail) {
     // super-block b of row 0: in X8 block b sits in run b / 8 at position b % 8
     const uint8_t* wb = g.layout == LAYOUT_X8 ? g.W + 1152 * (size_t)(b >> 3) + 16 * (size_t)(b & 7)
                                                   : g.W + 144 * (size_t)b;
@@ -213,7 +215,7 @@ SYN_DEV void gemm_issue(const GemmArgs& g, const GemmSlots& s, int wave, int lan
         const int gs = wave + GM_WAVES * u;
         lds_dma16(16u * (uint32_t)lane, ab + 1024 * gs, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
     }
-    if (s.ton) lds_dma16(s.toff, tb, st + (uint32_t)(GM_WB + GM_AB) + 1024u * (uint32_t)wave);
+    if (s.ton) lds_dma16(s.toff, tb, lds_addr(tail) + 1024u * (uint32_t)wave);
 }
 
 // The F16 pair (1024 + 16 q0, 1024 + 16 q1) etc. from the nibbles under `mask`.
@@ -223,17 +225,22 @@ SYN_DEV h2 magic_pair(uint32_t v, uint32_t mask) {
 
 SYN_DEV h2 bcast(_Float16 v) { return h2{v, v}; }
 
-// One super-block of the wavefront's 64 tokens x 32 rows from the stage in LDS.
-SYN_DEV void gemm_super(const uint8_t* st, int wave, int lane, v4f (&acc)[GM_MT][GM_NT]) {
+// What the fold of a super-block needs from its row headers: d, dmin and the S2 operand.
+struct GemmHdr {
+    float dd[GM_NT], dm[GM_NT];
+    v8h bm[GM_NT];
+};
+
+// The matrix-core part of one super-block of the wavefront's 64 tokens x 32 rows, from the
+// weights and codes of the stage in LDS: dacc = S1 - 472 X exactly, and the row headers.
+SYN_DEV void gemm_mfma(const uint8_t* st, int wave, int lane, v4f (&dacc)[GM_MT][GM_NT], GemmHdr& h) {
     const int c = lane & 15, p = lane >> 4;
     const uint8_t* wt = st + (16 * GM_NT * wave) * 144;
     const uint8_t* at = st + GM_WB;
-    const uint8_t* tl = st + GM_WB + GM_AB;
-
-    // per row tile: scales, the B-operand constants, the S2 operand
-    float dd[GM_NT], dm[GM_NT];
+    float (&dd)[GM_NT] = h.dd;
+    float (&dm)[GM_NT] = h.dm;
+    v8h (&bm)[GM_NT] = h.bm;
     h2 ka[GM_NT], kb[GM_NT];  // (sc/16, -(64 sc + 472)) of sub-blocks 2p and 2p + 1
-    v8h bm[GM_NT];
 #pragma unroll
     for (int nt = 0; nt < GM_NT; ++nt) {
         const v4u hdr = *reinterpret_cast<const v4u*>(wt + (16 * nt + c) * 144);
@@ -262,7 +269,6 @@ SYN_DEV void gemm_super(const uint8_t* st, int wave, int lane, v4f (&acc)[GM_MT]
         bm[nt] = v8h{m01.x, m01.y, m23.x, m23.y, m45.x, m45.y, m67.x, m67.y};
     }
 
-    v4f dacc[GM_MT][GM_NT];
 #pragma unroll
     for (int mt = 0; mt < GM_MT; ++mt)
 #pragma unroll
@@ -291,8 +297,13 @@ SYN_DEV void gemm_super(const uint8_t* st, int wave, int lane, v4f (&acc)[GM_MT]
                 dacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[nt], dacc[mt][nt], 0, 0, 0);
         }
     }
+}
 
-    // S2, then the super-block terms folded into the accumulators
+// S2 from the tail's code sums, then the super-block's terms folded into the accumulators in
+// the reference's rounding order.
+SYN_DEV void gemm_fold(const uint8_t* tl, int lane, const v4f (&dacc)[GM_MT][GM_NT], const GemmHdr& h,
+                       v4f (&acc)[GM_MT][GM_NT]) {
+    const int c = lane & 15, p = lane >> 4;
     const v8h zero8 = {};
 #pragma unroll
     for (int mt = 0; mt < GM_MT; ++mt) {
@@ -301,17 +312,32 @@ SYN_DEV void gemm_super(const uint8_t* st, int wave, int lane, v4f (&acc)[GM_MT]
         const v4f xs = *reinterpret_cast<const v4f*>(tl + GM_TT * 36 + (16 * mt + 4 * p) * 4);
 #pragma unroll
         for (int nt = 0; nt < GM_NT; ++nt) {
-            const v4f s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bm[nt], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            const v4f s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, h.bm[nt], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float s1 = __builtin_fmaf(472.0f, xs[i], dacc[mt][nt][i]);  // fl(S1), exact operands
-                const float a1 = (dd[nt] * dx[i]) * s1;
-                const float a2 = (dm[nt] * dx[i]) * s2[i];
+                const float a1 = (h.dd[nt] * dx[i]) * s1;
+                const float a2 = (h.dm[nt] * dx[i]) * s2[i];
                 acc[mt][nt][i] = acc[mt][nt][i] + (a1 - a2);
             }
         }
     }
 }
+
+// One super-block from a stage that holds its tail after the weights and codes.
+SYN_DEV void gemm_super(const uint8_t* st, int wave, int lane, v4f (&acc)[GM_MT][GM_NT]) {
+    v4f dacc[GM_MT][GM_NT];
+    GemmHdr h;
+    gemm_mfma(st, wave, lane, dacc, h);
+    gemm_fold(st + GM_WB + GM_AB, lane, dacc, h, acc);
+}
+
+// The dense GEMM's LDS: two stages of weights and codes, then a three-slot ring of tails, so
+// that super-block b's fold can run after b + 1's matrix products (its weights and codes are
+// overwritten by then; its tail is not until b + 3 is issued).
+constexpr int GM_WA = GM_WB + GM_AB;
+constexpr int GM_DENSE_LDS = 2 * GM_WA + 3 * GM_TB;
+static_assert(GM_WA % 16 == 0 && GM_TB % 16 == 0 && GM_DENSE_LDS <= 160 * 1024, "dense GEMM LDS");
 
 __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_q4k(GemmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -328,16 +354,40 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_q4k(GemmArgs g) {
 #pragma unroll
         for (int nt = 0; nt < GM_NT; ++nt) acc[mt][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    gemm_issue(g, sl, wave, lane, 0, t0, smem);
-    if (g.nb > 1) gemm_issue(g, sl, wave, lane, 1, t0, smem + GM_STAGE);
-    for (int b = 0; b < g.nb; ++b) {
-        uint8_t* stage = smem + (b & 1) * GM_STAGE;
+    uint8_t* tails = smem + 2 * GM_WA;
+    gemm_issue(g, sl, wave, lane, 0, t0, smem, tails);
+    if (g.nb > 1) gemm_issue(g, sl, wave, lane, 1, t0, smem + GM_WA, tails + GM_TB);
+    // Super-block b's products, then b - 1's fold (independent work the wavefront can issue
+    // between the products), with the two sets of exact sums alternating by parity.  Super-block
+    // 0 has no fold before it, so it is peeled: the loop's products and fold are one straight
+    // run of code the scheduler can interleave.
+    v4f d0[GM_MT][GM_NT], d1[GM_MT][GM_NT];
+    GemmHdr h0, h1;
+    int slot = 0;  // tail ring slot of b
+    auto step = [&](auto fold, int b, v4f (&dc)[GM_MT][GM_NT], GemmHdr& hc, const v4f (&dp)[GM_MT][GM_NT],
+                    const GemmHdr& hp) __attribute__((always_inline)) {
+        uint8_t* stage = smem + (b & 1) * GM_WA;
+        const int prev = slot == 0 ? 2 : slot - 1;  // the slot of b - 1, and of b + 2 after the fold
         // this lane's loads of b have landed once at most those of b + 1 are in flight
         wait_vm_n<GM_PER_WAVE>(b + 1 < g.nb ? live : 0);
         lds_barrier();
-        gemm_super(stage, wave, lane, acc);
+        gemm_mfma(stage, wave, lane, dc, hc);
+        if constexpr (decltype(fold)::value) {
+            gemm_fold(tails + prev * GM_TB, lane, dp, hp, acc);
+        }
         lds_barrier();
-        if (b + 2 < g.nb) gemm_issue(g, sl, wave, lane, b + 2, t0, stage);
+        if (b + 2 < g.nb) gemm_issue(g, sl, wave, lane, b + 2, t0, stage, tails + prev * GM_TB);
+        slot = slot == 2 ? 0 : slot + 1;
+    };
+    step(std::false_type{}, 0, d0, h0, d1, h1);
+    for (int b = 1; b < g.nb; b += 2) {
+        step(std::true_type{}, b, d1, h1, d0, h0);
+        if (b + 1 < g.nb) step(std::true_type{}, b + 1, d0, h0, d1, h1);
+    }
+    {
+        const int last = slot == 0 ? 2 : slot - 1;  // the slot of nb - 1
+        if (g.nb & 1) gemm_fold(tails + last * GM_TB, lane, d0, h0, acc);
+        else gemm_fold(tails + last * GM_TB, lane, d1, h1, acc);
     }
 
     const int c = lane & 15, p = lane >> 4;
@@ -375,10 +425,10 @@ void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, 
     g.rb = (uint32_t)(k / 256) * 144u;
     // once per process, thread-safe (a function-local static); a refusal shows as the launch's error
     static const hipError_t attr =
-        hipFuncSetAttribute((const void*)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * GM_STAGE);
+        hipFuncSetAttribute((const void*)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, GM_DENSE_LDS);
     (void)attr;
     const dim3 grid((unsigned)((n_out + GM_ROWS - 1) / GM_ROWS), (unsigned)(a.tpad / GM_TT));
-    hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(64 * GM_WAVES), 2 * GM_STAGE, stream, g);
+    hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(64 * GM_WAVES), GM_DENSE_LDS, stream, g);
 }
 
 // ============================================================================================
