@@ -680,8 +680,9 @@ void launch_moe_gather_q8k(const float* x, const uint32_t* slots, int nentries, 
 
 // The shape of one expert kernel: NM weight matrices, WV wavefronts of 16 rows each, up to CH
 // entries (CH / 4 groups) per item.  One stage in LDS: NM weight tiles [16 WV rows][144 bytes],
-// the entries' codes [CH][256] (16-byte chunk q of entry t at position q ^ 4(t & 3), so the
-// sixteen lanes of one read fall in distinct banks), their sums [CH][16], then the
+// the entries' codes [CH][256] (16-byte chunk q of entry t at position q ^ (t & 3): a 16-byte
+// LDS read serves four lanes of each quarter-wave per pass, here entries c & 3 times chunks
+// 4p + jq, whose positions then differ), their sums [CH][16], then the
 // 16-byte-aligned window of CH + 4 scales holding theirs.
 template <int NM_, int WV_, int CH_>
 struct MoeCfg {
@@ -730,11 +731,11 @@ SYN_DEV Slot make_slot(int s, const uint8_t* const (&bases)[C::NM], uint32_t row
         r.step = 144u;
         r.lds = s * 1024;
     } else if (s < C::WSLOTS + C::NG) {
-        // entries 4j..4j+3: position q of entry t holds its chunk q ^ 4(t & 3)
+        // entries 4j..4j+3: position q of entry t holds its chunk q ^ (t & 3)
         const int j = s - C::WSLOTS, t = 4 * j + (lane >> 4), q = lane & 15;
         r.live = r.live && 4 * j < nent;
         const int ec = ent0 + (t < nent ? t : nent - 1);
-        r.src = (const uint8_t*)a.codes + ((uint32_t)ec * (uint32_t)k + 16u * (uint32_t)(q ^ (4 * (t & 3))));
+        r.src = (const uint8_t*)a.codes + ((uint32_t)ec * (uint32_t)k + 16u * (uint32_t)(q ^ (t & 3)));
         r.step = 256u;
         r.lds = C::CODES + j * 1024;
     } else if (lane < C::CH) {
@@ -816,7 +817,7 @@ SYN_DEV void q4k_super(const uint8_t* st, int wave, int ent0, int ngroups, float
         if (g >= ngroups) break;  // uniform
         // entry 4g + (c & 3): its codes of sub-blocks jq and jq + 4, k part p
         const int ta = 4 * g + (c & 3);
-        const v4u ap = *reinterpret_cast<const v4u*>(st + L::CODES + ta * 256 + 16 * ((4 * p + jq) ^ (4 * (c & 3))));
+        const v4u ap = *reinterpret_cast<const v4u*>(st + L::CODES + ta * 256 + 16 * ((4 * p + jq) ^ (c & 3)));
         const int to = 4 * g + p;  // the lane's output entry
         const v4u lh = *reinterpret_cast<const v4u*>(st + L::LH + 16 * to);
         const float dx = reinterpret_cast<const float*>(st + L::DX)[(ent0 & 3) + to];
