@@ -140,7 +140,6 @@ constexpr int GM_ROWS = GM_WAVES * 16 * GM_NT;      // rows per workgroup
 constexpr int GM_WB = GM_ROWS * 144;                // weight bytes per stage
 constexpr int GM_AB = GM_TT * 512;                  // code bytes per stage
 constexpr int GM_TB = GM_TT * GM_TAIL_ROW;          // s2 | dx | X bytes per stage
-constexpr int GM_STAGE = GM_WB + GM_AB + GM_TB;
 constexpr int GM_WSLOT = GM_WB / 1024;              // wavefront loads (64 x 16 bytes) of each part
 constexpr int GM_ASLOT = GM_AB / 1024;
 constexpr int GM_TSLOT = (GM_TB + 1023) / 1024;
@@ -148,7 +147,6 @@ constexpr int GM_WPW = (GM_WSLOT + GM_WAVES - 1) / GM_WAVES;  // weight slots pe
 constexpr int GM_PER_WAVE = GM_WPW + GM_ASLOT / GM_WAVES + 1;
 static_assert(GM_ASLOT % GM_WAVES == 0 && GM_TSLOT <= GM_WAVES, "slot split");
 static_assert(GM_WB % 1024 == 0 && GM_AB % 1024 == 0, "wavefront-sized weight and code parts");
-static_assert(GM_STAGE % 16 == 0 && 2 * GM_STAGE <= 160 * 1024, "two stages in LDS");
 
 struct GemmArgs {
     const uint8_t* W;
@@ -324,20 +322,53 @@ SYN_DEV void gemm_fold(const uint8_t* tl, int lane, const v4f (&dacc)[GM_MT][GM_
     }
 }
 
-// One super-block from a stage that holds its tail after the weights and codes.
-SYN_DEV void gemm_super(const uint8_t* st, int wave, int lane, v4f (&acc)[GM_MT][GM_NT]) {
-    v4f dacc[GM_MT][GM_NT];
-    GemmHdr h;
-    gemm_mfma(st, wave, lane, dacc, h);
-    gemm_fold(st + GM_WB + GM_AB, lane, dacc, h, acc);
-}
-
-// The dense GEMM's LDS: two stages of weights and codes, then a three-slot ring of tails, so
-// that super-block b's fold can run after b + 1's matrix products (its weights and codes are
+// The GEMMs' LDS: two stages of weights and codes, then a three-slot ring of tails, so that
+// super-block b's fold can run after b + 1's matrix products (its weights and codes are
 // overwritten by then; its tail is not until b + 3 is issued).
 constexpr int GM_WA = GM_WB + GM_AB;
-constexpr int GM_DENSE_LDS = 2 * GM_WA + 3 * GM_TB;
-static_assert(GM_WA % 16 == 0 && GM_TB % 16 == 0 && GM_DENSE_LDS <= 160 * 1024, "dense GEMM LDS");
+constexpr int GM_LOOP_LDS = 2 * GM_WA + 3 * GM_TB;
+static_assert(GM_WA % 16 == 0 && GM_TB % 16 == 0 && GM_LOOP_LDS <= 160 * 1024, "GEMM LDS");
+
+// The super-block loop of both GEMM kernels.  `issue(b, stage, tail)` issues the wavefront's
+// `live` loads of super-block b.  Super-block b's products run first, then b - 1's fold
+// (independent work the wavefront can issue between the products), with the two sets of exact
+// sums alternating by parity.  Super-block 0 has no fold before it, so it is peeled: the loop's
+// products and fold are one straight run of code the scheduler can interleave.
+template <class Issue>
+SYN_DEV void gemm_loop(int nb, int live, uint8_t* smem, int wave, int lane, Issue&& issue,
+                       v4f (&acc)[GM_MT][GM_NT]) {
+    uint8_t* tails = smem + 2 * GM_WA;
+    issue(0, smem, tails);
+    if (nb > 1) issue(1, smem + GM_WA, tails + GM_TB);
+    v4f d0[GM_MT][GM_NT], d1[GM_MT][GM_NT];
+    GemmHdr h0, h1;
+    int slot = 0;  // tail ring slot of b
+    auto step = [&](auto fold, int b, v4f (&dc)[GM_MT][GM_NT], GemmHdr& hc, const v4f (&dp)[GM_MT][GM_NT],
+                    const GemmHdr& hp) __attribute__((always_inline)) {
+        uint8_t* stage = smem + (b & 1) * GM_WA;
+        const int prev = slot == 0 ? 2 : slot - 1;  // the slot of b - 1, and of b + 2 after the fold
+        // this lane's loads of b have landed once at most those of b + 1 are in flight
+        wait_vm_n<GM_PER_WAVE>(b + 1 < nb ? live : 0);
+        lds_barrier();
+        gemm_mfma(stage, wave, lane, dc, hc);
+        if constexpr (decltype(fold)::value) {
+            gemm_fold(tails + prev * GM_TB, lane, dp, hp, acc);
+        }
+        lds_barrier();
+        if (b + 2 < nb) issue(b + 2, stage, tails + prev * GM_TB);
+        slot = slot == 2 ? 0 : slot + 1;
+    };
+    step(std::false_type{}, 0, d0, h0, d1, h1);
+    for (int b = 1; b < nb; b += 2) {
+        step(std::true_type{}, b, d1, h1, d0, h0);
+        if (b + 1 < nb) step(std::true_type{}, b + 1, d0, h0, d1, h1);
+    }
+    const int last = slot == 0 ? 2 : slot - 1;  // the slot of nb - 1
+    if (nb & 1)
+        gemm_fold(tails + last * GM_TB, lane, d0, h0, acc);
+    else
+        gemm_fold(tails + last * GM_TB, lane, d1, h1, acc);
+}
 
 __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_q4k(GemmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -354,41 +385,9 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_q4k(GemmArgs g) {
 #pragma unroll
         for (int nt = 0; nt < GM_NT; ++nt) acc[mt][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    uint8_t* tails = smem + 2 * GM_WA;
-    gemm_issue(g, sl, wave, lane, 0, t0, smem, tails);
-    if (g.nb > 1) gemm_issue(g, sl, wave, lane, 1, t0, smem + GM_WA, tails + GM_TB);
-    // Super-block b's products, then b - 1's fold (independent work the wavefront can issue
-    // between the products), with the two sets of exact sums alternating by parity.  Super-block
-    // 0 has no fold before it, so it is peeled: the loop's products and fold are one straight
-    // run of code the scheduler can interleave.
-    v4f d0[GM_MT][GM_NT], d1[GM_MT][GM_NT];
-    GemmHdr h0, h1;
-    int slot = 0;  // tail ring slot of b
-    auto step = [&](auto fold, int b, v4f (&dc)[GM_MT][GM_NT], GemmHdr& hc, const v4f (&dp)[GM_MT][GM_NT],
-                    const GemmHdr& hp) __attribute__((always_inline)) {
-        uint8_t* stage = smem + (b & 1) * GM_WA;
-        const int prev = slot == 0 ? 2 : slot - 1;  // the slot of b - 1, and of b + 2 after the fold
-        // this lane's loads of b have landed once at most those of b + 1 are in flight
-        wait_vm_n<GM_PER_WAVE>(b + 1 < g.nb ? live : 0);
-        lds_barrier();
-        gemm_mfma(stage, wave, lane, dc, hc);
-        if constexpr (decltype(fold)::value) {
-            gemm_fold(tails + prev * GM_TB, lane, dp, hp, acc);
-        }
-        lds_barrier();
-        if (b + 2 < g.nb) gemm_issue(g, sl, wave, lane, b + 2, t0, stage, tails + prev * GM_TB);
-        slot = slot == 2 ? 0 : slot + 1;
-    };
-    step(std::false_type{}, 0, d0, h0, d1, h1);
-    for (int b = 1; b < g.nb; b += 2) {
-        step(std::true_type{}, b, d1, h1, d0, h0);
-        if (b + 1 < g.nb) step(std::true_type{}, b + 1, d0, h0, d1, h1);
-    }
-    {
-        const int last = slot == 0 ? 2 : slot - 1;  // the slot of nb - 1
-        if (g.nb & 1) gemm_fold(tails + last * GM_TB, lane, d0, h0, acc);
-        else gemm_fold(tails + last * GM_TB, lane, d1, h1, acc);
-    }
+    gemm_loop(g.nb, live, smem, wave, lane,
+              [&](int b, uint8_t* stage, uint8_t* tail) { gemm_issue(g, sl, wave, lane, b, t0, stage, tail); },
+              acc);
 
     const int c = lane & 15, p = lane >> 4;
 #pragma unroll
@@ -425,10 +424,10 @@ void launch_gemm_q4k(int layout, const uint8_t* W, int n_out, int k, GemmAct a, 
     g.rb = (uint32_t)(k / 256) * 144u;
     // once per process, thread-safe (a function-local static); a refusal shows as the launch's error
     static const hipError_t attr =
-        hipFuncSetAttribute((const void*)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, GM_DENSE_LDS);
+        hipFuncSetAttribute((const void*)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, GM_LOOP_LDS);
     (void)attr;
     const dim3 grid((unsigned)((n_out + GM_ROWS - 1) / GM_ROWS), (unsigned)(a.tpad / GM_TT));
-    hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(64 * GM_WAVES), GM_DENSE_LDS, stream, g);
+    hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(64 * GM_WAVES), GM_LOOP_LDS, stream, g);
 }
 
 // ============================================================================================
@@ -584,7 +583,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
         }
     }
     const int live = sl.nw + GM_ASLOT / GM_WAVES + (MODE == 0 ? (wave < 4 ? 1 : 0) : sl.nt);
-    auto issue = [&](int b, uint8_t* stage) {
+    auto issue = [&](int b, uint8_t* stage, uint8_t* tail) {
         const uint8_t* w0 = b0 + 144 * (size_t)b;
         const uint8_t* w1 = b1 + 144 * (size_t)b;
         const uint32_t st = lds_addr(stage);
@@ -598,7 +597,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
                 const int gs = wave + GM_WAVES * u;
                 lds_dma16(ab + aoff[u], g.act.codes, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
             }
-            const uint32_t tl = st + (uint32_t)(GM_WB + GM_AB);
+            const uint32_t tl = lds_addr(tail);
             if (wave < 2)
                 lds_dma16(tb + toff, g.act.tail, tl + 1024u * (uint32_t)wave);
             else if (wave < 4)
@@ -611,7 +610,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
                 const int gs = wave + GM_WAVES * u;
                 lds_dma16(16u * (uint32_t)lane, ab + 1024 * gs, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
             }
-            if (sl.ton) lds_dma16(sl.toff, tb, st + (uint32_t)(GM_WB + GM_AB) + 1024u * (uint32_t)wave);
+            if (sl.ton) lds_dma16(sl.toff, tb, lds_addr(tail) + 1024u * (uint32_t)wave);
         }
     };
     v4f acc[GM_MT][GM_NT];
@@ -619,16 +618,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
     for (int mt = 0; mt < GM_MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < GM_NT; ++nt) acc[mt][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    issue(0, smem);
-    if (g.nb > 1) issue(1, smem + GM_STAGE);
-    for (int b = 0; b < g.nb; ++b) {
-        uint8_t* stage = smem + (b & 1) * GM_STAGE;
-        wait_vm_n<GM_PER_WAVE>(b + 1 < g.nb ? live : 0);
-        lds_barrier();
-        gemm_super(stage, wave, lane, acc);
-        lds_barrier();
-        if (b + 2 < g.nb) issue(b + 2, stage);
-    }
+    gemm_loop(g.nb, live, smem, wave, lane, issue, acc);
     const int c = lane & 15, p = lane >> 4;
     if constexpr (MODE == 0) {
         // u (wavefronts 4-7) through LDS to the wavefronts holding g of the same outputs
@@ -691,14 +681,14 @@ void launch_moe_gemm(int mode, const uint8_t* w0, const uint8_t* w1, int n_exper
     const dim3 grid((unsigned)(max_tiles * g.row_tiles));
     if (mode == 0) {
         static const hipError_t ok0 = hipFuncSetAttribute((const void*)k_moe_gemm<0>,
-                                                          hipFuncAttributeMaxDynamicSharedMemorySize, 2 * GM_STAGE);
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize, GM_LOOP_LDS);
         (void)ok0;  // a refusal shows as the launch's error
-        hipLaunchKernelGGL(k_moe_gemm<0>, grid, dim3(64 * GM_WAVES), 2 * GM_STAGE, stream, g);
+        hipLaunchKernelGGL(k_moe_gemm<0>, grid, dim3(64 * GM_WAVES), GM_LOOP_LDS, stream, g);
     } else {
         static const hipError_t ok1 = hipFuncSetAttribute((const void*)k_moe_gemm<1>,
-                                                          hipFuncAttributeMaxDynamicSharedMemorySize, 2 * GM_STAGE);
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize, GM_LOOP_LDS);
         (void)ok1;
-        hipLaunchKernelGGL(k_moe_gemm<1>, grid, dim3(64 * GM_WAVES), 2 * GM_STAGE, stream, g);
+        hipLaunchKernelGGL(k_moe_gemm<1>, grid, dim3(64 * GM_WAVES), GM_LOOP_LDS, stream, g);
     }
 }
 
