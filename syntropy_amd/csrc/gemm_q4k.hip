@@ -9,19 +9,20 @@
 // in magnitude, the F32 result is the exact integer whatever the order of the additions.  Per
 // super-block the kernel feeds, for k = 0..255:
 //   A[t][k] = x code (Q8_K, |x| <= 127, written as F16 by k_gemm_act);
-//   B[k][n] = sc_j(k) * q_k - 472   (|B| <= 473, exact F16: the 6-bit scale folded into the
-//                                     4-bit code, centred so that 256 * 127 * 473 < 2^24)
-// so one accumulator holds D = S1 - 472 X exactly, X = sum_k x_k (a per-token integer the
-// activation kernel stores), and fma(472, X, D) = fl(S1): one rounding of the exact S1, which
+//   B[k][n] = sc_j(k) * q_k - 512   (|B| <= 512, exact F16: the 6-bit scale folded into the
+//                                     4-bit code, offset so that 256 * 127 * 512 < 2^24)
+// so one accumulator holds D = S1 - 512 X exactly, X = sum_k x_k (a per-token integer the
+// activation kernel stores), and fma(512, X, D) = fl(S1): one rounding of the exact S1, which
 // is the reference's `S1 as f32`.  S2 comes from a second product per tile: A = (l_j, 64 h_j)
 // with s_j = 64 h_j + l_j, B = (m_j, m_j), also exact.  The term and the fold are plain F32
 // operations in the reference's order.
 //
-// B from the packed nibbles, two codes per instruction: a dword shifted so that a nibble of each
-// 16-bit half sits at bits 4-7, masked and ORed with 0x6400 in each half, is the F16 pair
-// (1024 + 16 q0, 1024 + 16 q1), and one v_pk_fma_f16 with (sc/16, -(64 sc + 472)) gives
-// sc*q - 472 exactly (every constant is an exact F16 and the FMA rounds once, to an exact
-// integer).  The k order inside
+// B from the packed nibbles, two codes per instruction: the code dword (or it shifted right by
+// 8) masked to the low nibbles of its 16-bit halves and ORed with 0x6400 in each half is the
+// F16 pair (1024 + q0, 1024 + q1), and one v_pk_fma_f16 with (sc, -(1024 sc + 512)) gives
+// sc*q - 512; masked to the high nibbles it is (1024 + 16 q0, 1024 + 16 q1), and the FMA takes
+// (sc/16, -(64 sc + 512)).  Both are exact: every constant is an exact F16 (1024 sc + 512 =
+// 512 (2 sc + 1)) and the FMA rounds once, to an exact integer.  The k order inside
 // a super-block is free (the sum is exact), so each lane's eight k slots of an instruction are
 // the codes of four consecutive bytes, low nibbles then high: k_gemm_act writes the activations
 // in the same order.
@@ -230,7 +231,7 @@ struct GemmHdr {
 };
 
 // The matrix-core part of one super-block of the wavefront's 64 tokens x 32 rows, from the
-// weights and codes of the stage in LDS: dacc = S1 - 472 X exactly, and the row headers.
+// weights and codes of the stage in LDS: dacc = S1 - 512 X exactly, and the row headers.
 SYN_DEV void gemm_mfma(const uint8_t* st, int wave, int lane, v4f (&dacc)[GM_MT][GM_NT], GemmHdr& h) {
     const int c = lane & 15, p = lane >> 4;
     const uint8_t* wt = st + (16 * GM_NT * wave) * 144;
@@ -238,7 +239,7 @@ SYN_DEV void gemm_mfma(const uint8_t* st, int wave, int lane, v4f (&dacc)[GM_MT]
     float (&dd)[GM_NT] = h.dd;
     float (&dm)[GM_NT] = h.dm;
     v8h (&bm)[GM_NT] = h.bm;
-    h2 ka[GM_NT], kb[GM_NT];  // (sc/16, -(64 sc + 472)) of sub-blocks 2p and 2p + 1
+    h2 ka[GM_NT], kb[GM_NT];  // (sc, -(1024 sc + 512)) of sub-block 2p, (sc/16, -(64 sc + 512)) of 2p + 1
 #pragma unroll
     for (int nt = 0; nt < GM_NT; ++nt) {
         const v4u hdr = *reinterpret_cast<const v4u*>(wt + (16 * nt + c) * 144);
@@ -254,8 +255,8 @@ SYN_DEV void gemm_mfma(const uint8_t* st, int wave, int lane, v4f (&dacc)[GM_MT]
         const uint32_t scw = p < 2 ? sc_lo : sc_hi;
         const int sa = (int)((scw >> (16 * (p & 1))) & 0xFFu), sb = (int)((scw >> (16 * (p & 1) + 8)) & 0xFFu);
         const float fa = (float)sa, fb = (float)sb;
-        ka[nt] = h2{(_Float16)(fa * 0.0625f), (_Float16)(-(64.0f * fa + 472.0f))};
-        kb[nt] = h2{(_Float16)(fb * 0.0625f), (_Float16)(-(64.0f * fb + 472.0f))};
+        ka[nt] = h2{(_Float16)fa, (_Float16)(-(1024.0f * fa + 512.0f))};
+        kb[nt] = h2{(_Float16)(fb * 0.0625f), (_Float16)(-(64.0f * fb + 512.0f))};
         // S2 operand: m_0..m_7 in lane groups 0 and 1 (against l_j and 64 h_j), zero in 2 and 3
         const _Float16 on = p < 2 ? (_Float16)1.0f : (_Float16)0.0f;
         const h2 k1 = bcast(on), k0 = bcast((_Float16)(-1024.0f) * on);
@@ -280,8 +281,8 @@ SYN_DEV void gemm_mfma(const uint8_t* st, int wave, int lane, v4f (&dacc)[GM_MT]
             // bytes 32p + 4s .. +3 of the row's codes: sub-block 2p (low) and 2p + 1 (high)
             const uint32_t v = *reinterpret_cast<const uint32_t*>(wt + (16 * nt + c) * 144 + 16 + 32 * p + 4 * s);
             // (b0, b2) low nibbles, (b1, b3) low, (b0, b2) high, (b1, b3) high
-            const h2 y3 = __builtin_elementwise_fma(magic_pair(v << 4, 0x00F000F0u), bcast(ka[nt].x), bcast(ka[nt].y));
-            const h2 y2 = __builtin_elementwise_fma(magic_pair(v >> 4, 0x00F000F0u), bcast(ka[nt].x), bcast(ka[nt].y));
+            const h2 y3 = __builtin_elementwise_fma(magic_pair(v, 0x000F000Fu), bcast(ka[nt].x), bcast(ka[nt].y));
+            const h2 y2 = __builtin_elementwise_fma(magic_pair(v >> 8, 0x000F000Fu), bcast(ka[nt].x), bcast(ka[nt].y));
             const h2 y1 = __builtin_elementwise_fma(magic_pair(v, 0x00F000F0u), bcast(kb[nt].x), bcast(kb[nt].y));
             const h2 y4 = __builtin_elementwise_fma(magic_pair(v >> 8, 0x00F000F0u), bcast(kb[nt].x), bcast(kb[nt].y));
             bq[nt] = v8h{y3.x, y3.y, y2.x, y2.y, y1.x, y1.y, y4.x, y4.y};
@@ -313,7 +314,7 @@ SYN_DEV void gemm_fold(const uint8_t* tl, int lane, const v4f (&dacc)[GM_MT][GM_
             const v4f s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, h.bm[nt], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float s1 = __builtin_fmaf(472.0f, xs[i], dacc[mt][nt][i]);  // fl(S1), exact operands
+                const float s1 = __builtin_fmaf(512.0f, xs[i], dacc[mt][nt][i]);  // fl(S1), exact operands
                 const float a1 = (h.dd[nt] * dx[i]) * s1;
                 const float a2 = (h.dm[nt] * dx[i]) * s2[i];
                 acc[mt][nt][i] = acc[mt][nt][i] + (a1 - a2);
