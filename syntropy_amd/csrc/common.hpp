@@ -241,11 +241,12 @@ SYN_DEV uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_ptr)
 // 16 bytes per active lane from sbase + voff to LDS address lds + 16 * lane, with no registers
 // held while the load flies.  Written as assembly so the compiler does not track it (it would
 // otherwise wait for every load into LDS in flight before each LDS read); the caller waits with
-// wait_vm.  m0 (the LDS address) is reserved: the compiler keeps nothing in it across code.
+// wait_vm.  The LDS address is an m0 operand, so the compiler sets m0 itself; the s_nop covers
+// the wait state between an SALU write of m0 and the LDS DMA.
 SYN_DEV void lds_dma16(uint32_t voff, const void* sbase, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                  :
-                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "v"(voff), "s"(sbase), "{m0}"(lds)
                  : "memory");
 }
 
@@ -260,9 +261,9 @@ SYN_DEV int active_rows(const uint32_t* active, int first, int rows) {
 
 // 4 bytes per active lane from sbase + voff to LDS address lds + 4 * lane (as lds_dma16).
 SYN_DEV void lds_dma4(uint32_t voff, const void* sbase, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
                  :
-                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "v"(voff), "s"(sbase), "{m0}"(lds)
                  : "memory");
 }
 

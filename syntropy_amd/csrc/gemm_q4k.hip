@@ -592,17 +592,20 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
         for (int u = 0; u < GM_WPW; ++u)
             if (u < sl.nw) lds_dma16(sl.woff[u], upper[u] ? w1 : w0, st + 1024u * (uint32_t)(wave + GM_WAVES * u));
         if constexpr (MODE == 0) {
-            const uint32_t ab = (uint32_t)b * tp * 512u, tb = (uint32_t)b * tp * (uint32_t)GM_TAIL_ROW;
+            // super-block bases in 64 bits (2 * hidden * tp bytes of codes may pass 2^32);
+            // the offsets within one super-block's rows stay below 2^25
+            const uint8_t* ab = g.act.codes + (size_t)b * tp * 512u;
+            const uint8_t* tb = g.act.tail + (size_t)b * tp * (uint32_t)GM_TAIL_ROW;
 #pragma unroll
             for (int u = 0; u < GM_ASLOT / GM_WAVES; ++u) {
                 const int gs = wave + GM_WAVES * u;
-                lds_dma16(ab + aoff[u], g.act.codes, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
+                lds_dma16(aoff[u], ab, st + (uint32_t)GM_WB + 1024u * (uint32_t)gs);
             }
             const uint32_t tl = lds_addr(tail);
             if (wave < 2)
-                lds_dma16(tb + toff, g.act.tail, tl + 1024u * (uint32_t)wave);
+                lds_dma16(toff, tb, tl + 1024u * (uint32_t)wave);
             else if (wave < 4)
-                lds_dma4(tb + toff, g.act.tail, tl + (wave == 2 ? 2048u : 2304u));
+                lds_dma4(toff, tb, tl + (wave == 2 ? 2048u : 2304u));
         } else {
             const uint8_t* ab = g.act.codes + ((size_t)b * g.act.tpad + t0) * 512;
             const uint8_t* tb = g.act.tail + (size_t)b * g.act.tpad * GM_TAIL_ROW;

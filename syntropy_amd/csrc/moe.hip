@@ -762,10 +762,10 @@ SYN_DEV void issue_slot(const Slot& sl, int b, uint8_t* stage) {
     if (sl.live && sl.on) {
         const uint8_t* src = sl.src + (uint64_t)sl.step * (uint32_t)b;
         const uint32_t dst = (uint32_t)(uintptr_t)(lds_ptr)(stage + sl.lds);
-        // m0 (the LDS address) is reserved: the compiler keeps nothing in it across code
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+        // the LDS address is an m0 operand (the compiler sets m0; s_nop is the wait state)
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                      :
-                     : "v"(src), "s"(dst)
+                     : "v"(src), "{m0}"(dst)
                      : "memory");
     }
 }

@@ -57,7 +57,7 @@ def test_gemm_equals_oracle(S, rows, n_out, k):
 
 def test_gemm_extreme_magnitudes(S):
     """Scales 63 and codes 15 against codes +-127 of one sign: the largest sums the exact F16
-    accumulation has to carry (256 * 127 * 473 < 2^24), and the smallest (codes 0)."""
+    accumulation has to carry (256 * 127 * 512 < 2^24), and the smallest (codes 0)."""
     rows, n_out, k = 64, 64, 1024
     rs = np.random.default_rng(11)
     w = random_q4k(rs, n_out, k).reshape(-1, 144)
@@ -109,7 +109,7 @@ def test_gemm_wide_scale_range(S):
 @pytest.mark.parametrize("n_out,k", [(14336, 4096), (4096, 14336)])
 def test_gemm_prefill_config_shapes(S, n_out, k):
     """The dense prefill shapes at 2048 tokens (X N(0,1) rounded to BF16 values): the GEMM equals
-    the row-group GEMV path on the whole output, and the oracle on 16 sampled rows."""
+    the oracle on the whole output, and so does the row-group GEMV path."""
     rows = 2048
     rs = np.random.default_rng(n_out + k)
     w = random_q4k(rs, n_out, k)
@@ -127,8 +127,6 @@ def test_gemm_prefill_config_shapes(S, n_out, k):
     S.quantize_into(S.WeightType.Q4K, xd, rows, k, ws2)
     y2 = torch.empty(rows, n_out, device="cuda")
     S.gemv_quantized(W, ws2, rows, y2)
-    got = host(y)
-    assert_same(got, host(y2), "gemm vs row-group gemv")
-    pick = [0, 1, 63, 64, 500, 1023, 1024, 1500, 2000, 2040, 2041, 2042, 2044, 2045, 2046, 2047]
-    want = o.gemv(o.Q4_K, w, n_out, k, np.ascontiguousarray(x[pick]), len(pick), threads=8)
-    assert_same(got[pick], want, "sampled rows vs oracle")
+    want = o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=16)
+    assert_same(host(y), want, "gemm vs oracle")
+    assert_same(host(y2), want, "row-group gemv vs oracle")

@@ -201,7 +201,7 @@ def normal_weights(ty, n_out, k, seed):
 
 CONFIG_SHAPES = [
     ("cfg1 Q4_0 4096x4096", o.Q4_0, 4096, 4096, [1]),
-    ("cfg2 Q8_0 14336x4096", o.Q8_0, 14336, 4096, [1, 8, 32]),
+    ("cfg2 Q8_0 14336x4096", o.Q8_0, 14336, 4096, [1, 8, 32, 128]),
     ("cfg3 QKV", o.Q4_K, 6144, 4096, [1]),
     ("cfg3 O", o.Q4_K, 4096, 4096, [1]),
     ("cfg3 gate", o.Q4_K, 14336, 4096, [1]),

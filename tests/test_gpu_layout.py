@@ -76,6 +76,31 @@ def test_batch_x8_equals_source_layout(S):
         assert_same(host(b), host(a), "x8 batch")
 
 
+def test_batch_layer_full_shapes_equal_oracle(S):
+    """The grouped decode launch over a whole Q4_K decode layer at Llama-3-8B shapes (QKV 6144x4096,
+    O 4096x4096, gate and up 14336x4096, down 4096x14336), every output row, in both weight
+    layouts, against the oracle."""
+    shapes = [(6144, 4096), (4096, 4096), (14336, 4096), (14336, 4096), (4096, 14336)]
+    rs = np.random.default_rng(0x51A1)
+    src, x8, xs, want = [], [], [], []
+    for i, (n, k) in enumerate(shapes):
+        w = random_q4k(rs, n, k)
+        x = o.normal(0x51A20003 + i, 1.0, k)
+        want.append(o.gemv(o.Q4_K, w, n, k, x, 1, threads=16))
+        W = S.Weights(S.WeightType.Q4K, dev(w), n, k)
+        src.append(W)
+        x8.append(S.repack(W))
+        xs.append(dev(x))
+    for name, ws in (("source", src), ("x8", x8)):
+        ys = [torch.full((n,), float("nan"), device="cuda") for n, _ in shapes]
+        announce(f"batch layer full shapes {name}")
+        batch = S.GemvBatch(ws, xs, ys)
+        for rep in range(2):
+            batch()
+            for i, y in enumerate(ys):
+                assert_same(host(y), want[i], f"{name} problem {i} rep {rep}")
+
+
 @pytest.mark.parametrize("rows,n_out,k", [(2, 64, 2048), (64, 300, 4096), (100, 256, 14336)])
 def test_gemm_x8_equals_oracle(S, rows, n_out, k):
     rs = np.random.default_rng(rows + n_out + k)

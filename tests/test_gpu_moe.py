@@ -34,7 +34,7 @@ def fast_q4k_experts(seed, n_experts, hidden, inter):
 
     def mat(n_out, k):
         nb = n_out * k // 256
-        b = rs.integers(0, 256, (nb, 144), dtype=np.uint8)
+        b = np.frombuffer(rs.bytes(nb * 144), np.uint8).reshape(nb, 144).copy()
         # F16 scales in [2^-10, 2^-5): biased exponent 5..9, random mantissa
         h = ((rs.integers(5, 10, (nb, 2), dtype=np.uint16) << 10)
              | rs.integers(0, 1024, (nb, 2), dtype=np.uint16)).astype(np.uint16)
@@ -195,6 +195,35 @@ def test_grouped_layer_shape_64_tokens(M):
     assert st == 0
     want = o.moe_grouped(o.Q4_K, o.Q4_K, 128, 8, 4096, 1536, gate, up, down, x, ids, threads=16)
     assert_same(got, want, "layer slots")
+    y = host(M.combine(dev(got), dev(ids), dev(ww)))
+    assert_same(y, o.moe_combine(want, ids, ww), "combined")
+
+
+def test_moe_layer_2048_skewed_tokens(M):
+    """The prefill MoE layer: 2048 tokens, 128 experts, top-8, hidden 4096, inter 1536, with
+    router rows 3, 50 and 97 scaled by 3 so those experts take over four times the average load.
+    Route, the grouped FFN (the many-token path) and the combine, every value against the oracle."""
+    s = M.MoeShape(128, 8, 4096, 1536)
+    T = 2048
+    gate, up, down = fast_q4k_experts(0x51A4, s.n_experts, s.hidden, s.inter)
+    router = o.normal(0x51A30004, 0.02, s.n_experts * s.hidden).reshape(s.n_experts, s.hidden)
+    for r in (3, 50, 97):
+        router[r] *= np.float32(3.0)
+    x = o.normal(0x51A20005, 1.0, T * s.hidden).reshape(T, s.hidden)
+    announce("moe layer 2048 skewed tokens: route")
+    ids_d, w_d = M.route(dev(router), dev(x), s.top_k, True)
+    wids, ww, _ = o.moe_route(router, x, s.n_experts, s.top_k, True)
+    ids = host(ids_d)
+    assert (ids == wids).all()
+    assert_same(host(w_d), ww, "weights")
+    loads = np.sort(np.bincount(ids.ravel(), minlength=s.n_experts))[::-1]
+    assert (loads[:3] >= 4 * T * s.top_k / s.n_experts).all(), loads[:4]
+    announce("moe layer 2048 skewed tokens: grouped")
+    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    assert st == 0
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, 128, 8, 4096, 1536, gate, up, down, x, ids, threads=16)
+    assert_same(got, want, "slots")
+    announce("moe layer 2048 skewed tokens: combine")
     y = host(M.combine(dev(got), dev(ids), dev(ww)))
     assert_same(y, o.moe_combine(want, ids, ww), "combined")
 
