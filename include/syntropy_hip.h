@@ -89,6 +89,17 @@ int syn_gemv_layout_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t row
 int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
                     uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
                     void* stream);
+/* syn_gemv_layout_noalloc: no counterpart in the reference.  The same Gemv as syn_gemv_layout
+ * (same outputs, bit for bit) for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the workspace is a
+ * per-device array inside the library, syn_gemv_layout_noalloc_max_workspace() bytes (8 MiB),
+ * held until the process ends.  A call whose workspace (syn_gemv_layout_workspace_bytes) is
+ * larger is refused with SYN_E_UNSUPPORTED.  It calls no allocator.  Every call on one device
+ * shares that device's array: calls that overlap on one device (two streams, two threads) race
+ * and must be serialised by the caller. */
+uint64_t syn_gemv_layout_noalloc_max_workspace(void);
+int syn_gemv_layout_noalloc(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                            uint32_t k_in, const float* x, uint32_t rows, float* y, void* stream);
 int syn_gemv_batch_layout(uint32_t layout, uint32_t n, const int32_t* wtypes, const void* const* w,
                           const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in,
                           const float* const* x, float* const* y, void* ws, uint64_t ws_bytes,

@@ -3,6 +3,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
 #include <string>
 
 #include "../../include/syntropy_hip.h"
@@ -502,6 +504,61 @@ SYN_EXPORT int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, ui
                                uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
                                void* stream) {
     return syn_gemv_layout_rows(layout, wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, ws_bytes, stream, nullptr);
+}
+
+// ---- syn_gemv_layout without a caller workspace ---------------------------------------------
+// The workspace lives in `scratch`, one array per device that holds it until the process ends.
+// Host code never passes the array's name to a kernel (that is a host-side stand-in, not a
+// device address): the device address comes from hipGetSymbolAddress, once per device, with
+// that device current, and every use goes through it.
+namespace {
+
+constexpr uint64_t SCRATCH_BYTES = 8ull << 20;
+constexpr int SCRATCH_DEVICES = 64;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+std::atomic<void*> g_scratch[SCRATCH_DEVICES];
+std::mutex g_scratch_init;
+
+// The current device's scratch address; null with the message set on failure.
+void* scratch_of_current_device(const char* W) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_DEVICES) {
+        fail(SYN_E_DEVICE, "%s: no current device below %d", W, SCRATCH_DEVICES);
+        return nullptr;
+    }
+    if (void* p = g_scratch[dev].load(std::memory_order_acquire)) return p;
+    std::lock_guard<std::mutex> lock(g_scratch_init);
+    if (void* p = g_scratch[dev].load(std::memory_order_acquire)) return p;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        fail(SYN_E_DEVICE, "%s: hipGetSymbolAddress(scratch) on device %d: %s", W, dev, hipGetErrorString(e));
+        return nullptr;
+    }
+    g_scratch[dev].store(p, std::memory_order_release);
+    return p;
+}
+
+}  // namespace
+
+SYN_EXPORT uint64_t syn_gemv_layout_noalloc_max_workspace(void) { return SCRATCH_BYTES; }
+
+SYN_EXPORT int syn_gemv_layout_noalloc(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes,
+                                       uint32_t n_out, uint32_t k_in, const float* x, uint32_t rows, float* y,
+                                       void* stream) {
+    const char* W = "syn_gemv_layout_noalloc";
+    uint64_t need = 0;
+    if (int rc = syn_gemv_layout_workspace_bytes(layout, wtype, rows, k_in, &need)) return rc;
+    if (need > SCRATCH_BYTES)
+        return fail(SYN_E_UNSUPPORTED, "%s: %u rows of %u need a %llu-byte workspace; the device scratch holds %llu",
+                    W, rows, k_in, (unsigned long long)need, (unsigned long long)SCRATCH_BYTES);
+    if (rows == 0 || n_out == 0) return SYN_OK;
+    void* ws = scratch_of_current_device(W);
+    if (!ws) return SYN_E_DEVICE;
+    // every byte the kernels read from the workspace is written earlier in the same call
+    return syn_gemv_layout_rows(layout, wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, SCRATCH_BYTES, stream,
+                                nullptr);
 }
 
 SYN_EXPORT int syn_gate_up_act_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t rows, uint32_t n_out,
