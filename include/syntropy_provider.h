@@ -4,9 +4,13 @@
  * version only appends.  Each side frees what it allocated; variable-size results go through a
  * caller buffer (SynOutBuf); handles are opaque 64-bit values.
  *
- * libsyntropy_provider.so exports syntropy_provider_entry_v1, under the version node
- * SYNTROPY_PROVIDER_1 (the reference's ci/link/provider.map), and the doorbell flag accessor
- * syntropy_provider_flag_v1 beside it, and is linked -Bsymbolic. */
+ * libsyntropy_provider.so exports exactly syntropy_provider_entry_v1, under the version node
+ * SYNTROPY_PROVIDER_1 (the reference's ci/link/provider.map), and is linked -Bsymbolic.
+ *
+ * Doorbell flags: signal_host and wait_host take `flag` = page << 16 | slot, naming the 4-byte
+ * word `slot` of a 4 KiB page of the HostMapped buffers (alloc kind 1) of the context.  Their
+ * pages are numbered in allocation order from 0 and never reused (RFC-0040 4.2, revised
+ * 2026-11-07).  A HostMapped buffer's `addr` is both its device and its host address. */
 #ifndef SYNTROPY_PROVIDER_H
 #define SYNTROPY_PROVIDER_H
 
@@ -39,6 +43,7 @@ enum {
     SYN_CODE_OP_UNSUPPORTED = 1,
     SYN_CODE_DEVICE_STICKY = 8,
     SYN_CODE_ALLOC_FAILED = 9,
+    SYN_CODE_DOORBELL_TIMEOUT = 11,
     SYN_CODE_WORKSPACE_EXCEEDED = 14,
     SYN_CODE_PROVIDER_PANICKED = 16
 };
@@ -275,16 +280,10 @@ typedef struct SynModule {
 
 /* The entry point (crates/kernels/src/abi/mod.rs:64: ENTRY_SYMBOL; EntryFn).  Returns null when
  * the host's header is not "SYNPROV1", major 1, or shorter than this header's SynHostApi.  The
- * module has one provider: id "hip", backend Hip, domain Hip, serving Gemv (Q4_0, Q8_0, Q4_K),
- * MoeGrouped (Q4_K), MoeRoute{Softmax} and MoeCombine on AMD gfx950 devices. */
+ * module has one provider: id "hip", backend Hip, domain Hip, serving Gemv, Gemm, Logits and
+ * GateUpAct{Silu} (Q4_0, Q8_0, Q4_K, F16, BF16), MoeGrouped (Q4_K, Q8_0), MoeRoute{Softmax} and
+ * MoeCombine on AMD gfx950 devices. */
 const SynModule* syntropy_provider_entry_v1(const SynHostApi* host);
-
-/* The host address of doorbell flag `flag` (page << 16 | slot) of context `ctx`: a 4-byte word on
- * a 64-byte line of its own in pinned host memory, which signal_host writes and wait_host reads
- * from the device.  No counterpart in the reference's ABI, which leaves the host side of a
- * module's flags open; the CPU provider gives the same address as Doorbells::flag
- * (crates/kernels-cpu/src/doorbell.rs:76-81).  Called on the thread that opened the context. */
-SynStatus syntropy_provider_flag_v1(uint64_t ctx, uint32_t flag, uint32_t** host);
 
 #ifdef __cplusplus
 }

@@ -755,7 +755,7 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
                                uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k,
                                uint32_t hidden, uint32_t inter, const float* x, const int32_t* ids,
                                const int32_t* site, uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
-                               uint32_t* status, void* stream, const uint32_t* active) {
+                               uint32_t* status, void* stream, const uint32_t* active, uint32_t* report) {
     const char* W = "syn_moe_grouped";
     if (wtype != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: expert weight type %d (Q4_K)", W, wtype);
     if (int rc = check_moe_shape(W, n_experts, top_k, hidden, inter, rows)) return rc;
@@ -778,7 +778,7 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
     uint32_t* err = (uint32_t*)(base + m.err);
     const int ent = (int)(rows * top_k);
     hipStream_t st = (hipStream_t)stream;
-    syn::launch_moe_pack(ids, ent, (int)n_experts, offsets, slots, err, st, active, (int)top_k, site);
+    syn::launch_moe_pack(ids, ent, (int)n_experts, offsets, slots, err, st, active, (int)top_k, site, report);
     if (m.gemm) {
         const syn::MoeTiles mt{(uint32_t*)(base + m.pad_off), (uint32_t*)(base + m.tile_e),
                                (uint32_t*)(base + m.n_tiles)};

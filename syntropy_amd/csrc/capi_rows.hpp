@@ -2,6 +2,9 @@
 // of a step descriptor's rows_active (crates/kernels/include/syntropy/step_desc.h:53-57), or
 // null for the whole bucket.  The kernels read it on the device, so a captured launch follows
 // the value the host writes before each replay; rows past it are neither computed nor written.
+// syn_moe_grouped_rows' `report`, when given, is three words of host-visible memory: the first
+// refused launch (an id that names no expert) writes 1 + the slot, the id and top_k, if word 0
+// is clear.
 #pragma once
 
 #include <stdint.h>
@@ -19,6 +22,7 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
                          uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k, uint32_t hidden,
                          uint32_t inter, const float* x, const int32_t* ids, const int32_t* site, uint32_t rows,
                          float* out, void* ws,
-                         uint64_t ws_bytes, uint32_t* status, void* stream, const uint32_t* active);
+                         uint64_t ws_bytes, uint32_t* status, void* stream, const uint32_t* active,
+                         uint32_t* report = nullptr);
 int syn_moe_combine_rows(const float* out, const int32_t* ids, const float* w, uint32_t rows, uint32_t top_k,
                          uint32_t hidden, float* y, void* stream, const uint32_t* active);

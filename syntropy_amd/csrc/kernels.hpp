@@ -45,7 +45,7 @@ void launch_moe_route(const float* router, const float* x, int rows, int hidden,
                       hipStream_t stream, const uint32_t* active = nullptr);
 void launch_moe_pack(const int32_t* ids, int nslots, int n_experts, uint32_t* offsets,
                      uint32_t* slots, uint32_t* err, hipStream_t stream, const uint32_t* active = nullptr, int top_k = 1,
-                     const int32_t* site = nullptr);
+                     const int32_t* site = nullptr, uint32_t* report = nullptr);
 // Q8_K activations of the packed entries as the expert kernels read them, entry-major.  Each
 // 256-value block b of an entry is stored in the matrix-core operand order: byte
 // 256b + 64p + 16(j%4) + 8(j/4) + i holds code 32j + 8p + i (sub-block j, k part p), so that

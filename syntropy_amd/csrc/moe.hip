@@ -484,7 +484,8 @@ __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ i
                                                    uint32_t* __restrict__ slots,
                                                    uint32_t* __restrict__ err,
                                                    const uint32_t* __restrict__ active, int top_k,
-                                                   const int32_t* __restrict__ site) {
+                                                   const int32_t* __restrict__ site,
+                                                   uint32_t* __restrict__ report) {
     if (active) nslots = active_rows(active, 0, nslots / top_k) * top_k;  // the active rows' slots
     // Every id is checked; a slot whose expert the site mask leaves out is neither counted nor
     // packed, so no later kernel computes or writes it.
@@ -494,19 +495,32 @@ __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ i
     const int s_begin = wave * per;
     const int s_end = s_begin + per < nslots ? s_begin + per : nslots;
     for (int i = tid; i < 16 * n_experts; i += 1024) cnt[i] = 0;
-    __shared__ uint32_t bad;
-    if (tid == 0) bad = 0;
+    __shared__ uint32_t bad;  // the first slot whose id names no expert, or ~0
+    if (tid == 0) bad = ~0u;
     __syncthreads();
     for (int s = s_begin + lane; s < s_end; s += 64) {
         const int e = ids[s];
         if (e < 0 || e >= n_experts)
-            atomicOr(&bad, 1u);
+            atomicMin(&bad, (uint32_t)s);
         else if (!site || site[e] != 0)
             atomicAdd(&cnt[wave * n_experts + e], 1u);
     }
     __syncthreads();
-    if (bad) {
-        if (tid == 0) *err = 1u;
+    if (bad != ~0u) {
+        if (tid == 0) {
+            *err = 1u;
+            // the caller's report words (host memory the host reads after the stream): the
+            // first failing launch since the host last cleared word 0 writes 1 + slot, the id
+            // and top_k
+            if (report) {
+                uint32_t none = 0;
+                if (__hip_atomic_compare_exchange_strong(report, &none, bad + 1u, __ATOMIC_RELAXED,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
+                    __hip_atomic_store(report + 1, (uint32_t)ids[bad], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    __hip_atomic_store(report + 2, (uint32_t)top_k, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+            }
+        }
         return;
     }
     // scan, expert-major then wave-minor: per-expert totals, an exclusive scan of the totals in
@@ -591,9 +605,9 @@ __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ i
 
 void launch_moe_pack(const int32_t* ids, int nslots, int n_experts, uint32_t* offsets,
                      uint32_t* slots, uint32_t* err, hipStream_t stream, const uint32_t* active, int top_k,
-                     const int32_t* site) {
+                     const int32_t* site, uint32_t* report) {
     hipLaunchKernelGGL(k_moe_pack, dim3(1), dim3(1024), sizeof(uint32_t) * 16 * n_experts, stream,
-                       ids, nslots, n_experts, offsets, slots, err, active, top_k, site);
+                       ids, nslots, n_experts, offsets, slots, err, active, top_k, site, report);
 }
 
 // ============================================================================================

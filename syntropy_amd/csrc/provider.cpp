@@ -14,6 +14,16 @@
 //  * query answers with CapsWire JSON or nothing (len 0) for an op it does not serve
 //    (wire.rs:762-830); the JSON it reads is serde's form of OpKey and ShapeSig.
 //
+//  * a sticky device error (an illegal address, a failed launch and the like, RFC-0040 ...md:861,
+//    933) seen by any entry makes the provider sticky with DeviceSticky (8);
+//  * the core's host services (crates/kernels/src/abi/types.rs:47-58) are kept: `config` gives
+//    kernels.spin_kernel_max_us at open and the fault-injection keys fixture.panic_in and
+//    fixture.device_fault_in (read once, when the entry symbol is called; the names follow the
+//    reference's test provider, crates/kernels-loader/examples/test_provider.rs:7-16), and `log`
+//    receives every failure that makes the provider sticky or that the device reports later (a
+//    doorbell timeout, a refused MoeGrouped).  The reference defines no metric ids for
+//    providers, so `metric` is not called.
+//
 // The hot entries (launch, record, wait, poll, copy, copy_batch, replay, health) take no lock
 // and allocate nothing: they look up handles in the calling thread's context and enqueue.
 #include <hip/hip_runtime.h>
@@ -27,6 +37,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <exception>
 #include <string>
 #include <unordered_map>
@@ -54,6 +65,25 @@ struct Fail {
 thread_local std::string t_message;
 std::atomic<uint16_t> g_sticky{0};
 
+// The core's services, copied when the entry symbol is called, and the fault-injection keys.
+struct HostServices {
+    SynHostApi api{};
+    bool present = false;
+    std::string panic_in;         // fixture.panic_in: the entry that throws
+    std::string device_fault_in;  // fixture.device_fault_in: the entry that meets a sticky device error
+};
+HostServices g_host;
+std::once_flag g_host_once;
+
+const char* host_config(const char* key) {
+    return g_host.present && g_host.api.config ? g_host.api.config(key) : nullptr;
+}
+
+// level: 0 error, 1 warn, 2 info (types.rs:50-52)
+void host_log(uint8_t level, const std::string& msg) {
+    if (g_host.present && g_host.api.log) g_host.api.log(level, "syntropy_amd::hip", msg.data(), msg.size());
+}
+
 SynStatus status(uint32_t cls, uint16_t code) {
     SynStatus s;
     s.cls = cls;
@@ -68,8 +98,32 @@ const SynStatus OK = status(SYN_CLASS_OK, 0);
 [[noreturn]] void internal(std::string msg) { fail(SYN_CLASS_INTERNAL, 0, std::move(msg)); }
 [[noreturn]] void unsupported(std::string msg) { fail(SYN_CLASS_UNSUPPORTED, SYN_CODE_OP_UNSUPPORTED, std::move(msg)); }
 
+// Errors after which the device cannot run further work in this process.
+bool sticky_error(hipError_t e) {
+    switch (e) {
+    case hipErrorIllegalAddress:
+    case hipErrorLaunchFailure:
+    case hipErrorPriorLaunchFailure:
+    case hipErrorAssert:
+    case hipErrorLaunchTimeOut:
+    case hipErrorECCNotCorrectable:
+        return true;
+    default:
+        return false;
+    }
+}
+
 void check_hip(hipError_t e, const char* what) {
-    if (e != hipSuccess) fail(SYN_CLASS_DEVICE, 0, std::string(what) + ": " + hipGetErrorString(e));
+    if (e == hipSuccess) return;
+    std::string msg = std::string(what) + ": " + hipGetErrorString(e);
+    if (sticky_error(e)) {
+        uint16_t none = 0;
+        g_sticky.compare_exchange_strong(none, SYN_CODE_DEVICE_STICKY, std::memory_order_acq_rel);
+        msg += " (the device is lost to this process: the provider is sticky)";
+        host_log(0, msg);
+        fail(SYN_CLASS_DEVICE, SYN_CODE_DEVICE_STICKY, std::move(msg));
+    }
+    fail(SYN_CLASS_DEVICE, 0, std::move(msg));
 }
 void check_syn(int rc, const char* what) {
     if (rc == SYN_OK) return;
@@ -90,6 +144,10 @@ SynStatus call(const char* name, bool allowed_when_sticky, F&& f) {
         return status(SYN_CLASS_DEVICE, SYN_CODE_DEVICE_STICKY);
     }
     try {
+        if (!g_host.panic_in.empty() && g_host.panic_in == name)
+            throw std::runtime_error("injected by fixture.panic_in");
+        if (!g_host.device_fault_in.empty() && g_host.device_fault_in == name)
+            check_hip(hipErrorIllegalAddress, "injected by fixture.device_fault_in");
         f();
         return OK;
     } catch (const Fail& e) {
@@ -98,10 +156,12 @@ SynStatus call(const char* name, bool allowed_when_sticky, F&& f) {
     } catch (const std::exception& e) {
         g_sticky.store(SYN_CODE_PROVIDER_PANICKED, std::memory_order_release);
         t_message = std::string("the provider failed in `") + name + "`: " + e.what();
+        host_log(0, t_message);
         return status(SYN_CLASS_INTERNAL, SYN_CODE_PROVIDER_PANICKED);
     } catch (...) {
         g_sticky.store(SYN_CODE_PROVIDER_PANICKED, std::memory_order_release);
         t_message = std::string("the provider failed in `") + name + "` with an unknown exception";
+        host_log(0, t_message);
         return status(SYN_CLASS_INTERNAL, SYN_CODE_PROVIDER_PANICKED);
     }
 }
@@ -479,19 +539,36 @@ std::string ops_json() {
 // Contexts
 // ============================================================================================
 
+// alloc's memory kinds (crates/kernels/src/memory.rs:33-40)
+constexpr uint32_t KIND_DEVICE = 0, KIND_HOST_MAPPED = 1;
+
 struct Buf {
     void* ptr;
     uint64_t bytes;
+    uint32_t kind;
+    uint32_t first_page;  // HostMapped: the number of its first doorbell page
 };
 
-// Doorbell flags: 64 to a 4 KiB page, each on a 64-byte line of its own, in pinned host memory
-// both sides address (RFC-0040 ...md:545-547; crates/kernels-cpu/src/doorbell.rs:1-27).  The line
-// after the pages holds the wait-timeout word: 1 + the flag index of the first wait that passed
-// its spin limit.
-constexpr uint32_t FLAGS_PER_PAGE = 64;
-constexpr uint32_t FLAG_WORDS = 16;
-constexpr uint32_t MAX_FLAG_PAGES = 1024;
+// Doorbell flags (RFC-0040 ...md:545-547 and its 2026-11-07 revision at :594): a HostFlag
+// {page, slot} names the 4-byte word `slot` of a 4 KiB page of the tier manager's HostMapped
+// buffers.  Their pages are numbered in allocation order on the context, from 0, and a number
+// is never reused, as the CUDA provider numbers them (crates/kernels-cuda/src/memory.rs:44-49,
+// 544-583).  A HostMapped buffer is pinned, mapped and coherent host memory whose device
+// address is its host address (ROCm's unified addressing, checked at alloc).
+constexpr uint64_t DOORBELL_PAGE = 4096;
+constexpr uint32_t MAX_DOORBELL_PAGES = 1u << 16;
 constexpr uint64_t DEFAULT_SPIN_US = 2000000;
+
+struct DoorbellPage {
+    uint32_t* addr = nullptr;  // host and device address of the page's first word
+    uint64_t bytes = 0;        // bytes of the buffer from this page on (the last page may be short)
+    bool live = false;
+};
+
+// The context's status page: 4 KiB of pinned host memory the kernels write and the host reads
+// with plain loads.  Word 0: 1 + (page << 16 | slot) of the first wait_host past its spin limit.
+// Words 16-18: the first refused MoeGrouped launch (1 + slot, id, top_k).
+constexpr uint32_t STATUS_BELL = 0, STATUS_MOE = 16;
 
 // A host thread's wake target (RFC-0040 ...md:592-600, HostWaker): kind 0 a futex word at
 // `handle` that the waiter sets to 1 before it parks (FUTEX_WAIT on 1), kind 1 an eventfd.
@@ -516,9 +593,8 @@ void wake_target(void* p) {
 
 struct Ctx {
     int device = 0;
-    uint32_t* bells = nullptr;      // host address
-    uint32_t* bells_dev = nullptr;  // the same memory as the device addresses it
-    uint32_t n_bells = 0;
+    uint32_t* status = nullptr;  // the status page (host and device address)
+    std::vector<DoorbellPage> pages;
     uint64_t spin_us = DEFAULT_SPIN_US;
     uint64_t spin_ticks = 0;
     // arm_wake: per stream, the side stream its host-function nodes run on, its fork and join
@@ -560,26 +636,44 @@ hipEvent_t event_of(Ctx& c, uint64_t e) {
     if (it == c.events.end()) internal("unknown event " + std::to_string(e));
     return it->second;
 }
-// The index of `flag` (page << 16 | slot), checked against the context's flags.
-uint32_t flag_index(Ctx& c, uint32_t flag) {
+// The word `flag` (page << 16 | slot) names, refused unless it lies in a live HostMapped page.
+uint32_t* flag_word(Ctx& c, uint32_t flag) {
     const uint32_t page = flag >> 16, slot = flag & 0xFFFFu;
-    if (slot >= FLAGS_PER_PAGE || (uint64_t)page * FLAGS_PER_PAGE + slot >= c.n_bells)
-        internal("no doorbell (page " + std::to_string(page) + ", slot " + std::to_string(slot) + ") on this device");
-    return page * FLAGS_PER_PAGE + slot;
+    if (page >= c.pages.size() || !c.pages[page].live || (uint64_t)slot * 4 + 4 > DOORBELL_PAGE ||
+        (uint64_t)slot * 4 + 4 > c.pages[page].bytes)
+        internal("no doorbell flag at page " + std::to_string(page) + " slot " + std::to_string(slot) +
+                 " on this device");
+    return c.pages[page].addr + slot;
 }
 
-// A wait that passed its spin limit since the last check: reported once, as a Timeout.
-void check_bells(Ctx& c) {
-    if (!c.bells) return;
-    uint32_t* st = c.bells + (size_t)c.n_bells * FLAG_WORDS;
-    const uint32_t tag = __atomic_exchange_n(st, 0u, __ATOMIC_ACQ_REL);
-    if (tag) {
-        const uint32_t i = tag - 1;
-        fail(SYN_CLASS_TIMEOUT, 0,
-             "wait_host on the doorbell (page " + std::to_string(i / FLAGS_PER_PAGE) + ", slot " +
-                 std::to_string(i % FLAGS_PER_PAGE) + ") passed its spin limit of " + std::to_string(c.spin_us) +
-                 " us without the host's reply; the stream ran on past it");
+// What the device reported since the last check, reported once: a wait past its spin limit as
+// Timeout / DoorbellTimeout (RFC-0040 ...md:1361), a refused MoeGrouped as Internal, as the CPU
+// provider reports MoeError::ExpertId (crates/kernels-cpu/src/moe.rs:433-441, moe/entry.rs:309).
+void check_status(Ctx& c) {
+    if (!c.status) return;
+    const uint32_t tag = __atomic_exchange_n(c.status + STATUS_BELL, 0u, __ATOMIC_ACQ_REL);
+    const uint32_t bad = __atomic_load_n(c.status + STATUS_MOE, __ATOMIC_ACQUIRE);
+    std::string moe;
+    if (bad) {
+        const uint32_t id = __atomic_load_n(c.status + STATUS_MOE + 1, __ATOMIC_ACQUIRE);
+        const uint32_t k = __atomic_load_n(c.status + STATUS_MOE + 2, __ATOMIC_ACQUIRE);
+        __atomic_store_n(c.status + STATUS_MOE, 0u, __ATOMIC_RELEASE);
+        const uint32_t slot = bad - 1;
+        moe = "MoeGrouped: row " + std::to_string(k ? slot / k : slot) + " rank " + std::to_string(k ? slot % k : 0) +
+              " routes to expert " + std::to_string((int32_t)id) +
+              ", which the layer lacks; the launch wrote nothing";
+        host_log(1, moe);
     }
+    if (tag) {
+        const uint32_t f = tag - 1;
+        std::string m = "wait_host on the doorbell flag at page " + std::to_string(f >> 16) + " slot " +
+                        std::to_string(f & 0xFFFFu) + " passed its spin limit of " + std::to_string(c.spin_us) +
+                        " us without the host's reply; the stream ran on past it";
+        host_log(1, m);
+        if (!moe.empty()) m += "; also " + moe;
+        fail(SYN_CLASS_TIMEOUT, SYN_CODE_DOORBELL_TIMEOUT, std::move(m));
+    }
+    if (!moe.empty()) internal(std::move(moe));
 }
 
 // The device address of a slice, checked against its buffer.
@@ -686,7 +780,8 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         check_syn(syn_moe_grouped_rows(p.weight, (const void*)g.addr, (const void*)u.addr, (const void*)d.addr,
                                        mat, e, top_k, hidden, inter, (const float*)x, (const int32_t*)ids,
                                        (const int32_t*)site, rows,
-                                       (float*)out, ws, p.workspace - 256, nullptr, st, active),
+                                       (float*)out, ws, p.workspace - 256, nullptr, st, active,
+                                       c.status + STATUS_MOE),
                   "MoeGrouped");
         return;
     }
@@ -770,49 +865,52 @@ SynStatus e_enumerate(void*, SynOutBuf* out) {
 SynStatus e_open(void*, const SynDeviceId* dev, const SynOpenOptions* opts, uint64_t* ctx) {
     return call("open", false, [&] {
         if (!dev || !ctx) internal("open: null argument");
+        (void)opts;  // doorbell pages are the tier manager's HostMapped buffers (RFC-0040 ...md:594)
         int n = 0;
         if (hipGetDeviceCount(&n) != hipSuccess || n == 0) fail(SYN_CLASS_DEVICE, 0, "open: no HIP device");
         if ((int)dev->ordinal >= n) fail(SYN_CLASS_INVALID_REQUEST, 0, "open: no device " + std::to_string(dev->ordinal));
         check_hip(hipSetDevice((int)dev->ordinal), "hipSetDevice");
-        // doorbell_slots flags rounded up to whole pages, at least one (doorbell.rs:37-43)
-        const uint32_t want = opts ? opts->doorbell_slots : 0;
-        const uint32_t pages = want ? (uint32_t)(((uint64_t)want + FLAGS_PER_PAGE - 1) / FLAGS_PER_PAGE) : 1;
-        if (pages > MAX_FLAG_PAGES)
-            fail(SYN_CLASS_INVALID_REQUEST, 0, "open: " + std::to_string(want) + " doorbell slots (at most 65536)");
-        // the bound of one wait_host: SYNTROPY_SPIN_MAX_US (kernels.spin_kernel_max_us), default 2 s
+        // the bound of one wait_host: the core's kernels.spin_kernel_max_us (RFC-0040 ...md:1342),
+        // 2 s when the core sets none
         uint64_t spin_us = DEFAULT_SPIN_US;
-        if (const char* e = std::getenv("SYNTROPY_SPIN_MAX_US")) {
+        if (const char* v = host_config("kernels.spin_kernel_max_us")) {
             char* end = nullptr;
-            const unsigned long long v = std::strtoull(e, &end, 10);
-            if (end == e || *end || v == 0 || v > 600000000ull)
-                fail(SYN_CLASS_INVALID_REQUEST, 0, "open: SYNTROPY_SPIN_MAX_US must be 1..600000000");
-            spin_us = v;
+            const unsigned long long u = std::strtoull(v, &end, 10);
+            if (end == v || *end || u == 0 || u > 600000000ull)
+                fail(SYN_CLASS_INVALID_REQUEST, 0,
+                     std::string("open: kernels.spin_kernel_max_us must be 1..600000000, not '") + v + "'");
+            spin_us = u;
         }
         int khz = 0;
         check_hip(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, (int)dev->ordinal),
                   "hipDeviceGetAttribute(WallClockRate)");
         if (khz <= 0) fail(SYN_CLASS_DEVICE, 0, "open: the device reports no wall-clock rate");
-        void* bells = nullptr;
-        const size_t bytes = (size_t)pages * 4096 + 64;
-        check_hip(hipHostMalloc(&bells, bytes, hipHostMallocMapped | hipHostMallocCoherent), "hipHostMalloc(doorbells)");
-        std::memset(bells, 0, bytes);
-        void* bells_dev = nullptr;
-        const hipError_t r = hipHostGetDevicePointer(&bells_dev, bells, 0);
-        if (r != hipSuccess) {
-            (void)hipHostFree(bells);
-            check_hip(r, "hipHostGetDevicePointer(doorbells)");
+        // the status page: the one allocation outside the tier manager's requests, 4 KiB per
+        // context, for the words the kernels report through
+        void* st = nullptr;
+        check_hip(hipHostMalloc(&st, DOORBELL_PAGE, hipHostMallocMapped | hipHostMallocCoherent),
+                  "hipHostMalloc(status page)");
+        std::memset(st, 0, DOORBELL_PAGE);
+        void* st_dev = nullptr;
+        const hipError_t r = hipHostGetDevicePointer(&st_dev, st, 0);
+        if (r != hipSuccess || st_dev != st) {
+            (void)hipHostFree(st);
+            check_hip(r == hipSuccess ? hipErrorInvalidValue : r, "hipHostGetDevicePointer(status page)");
         }
         Ctx* c = new Ctx();
         c->device = (int)dev->ordinal;
-        c->bells = static_cast<uint32_t*>(bells);
-        c->bells_dev = static_cast<uint32_t*>(bells_dev);
-        c->n_bells = pages * FLAGS_PER_PAGE;
+        c->status = static_cast<uint32_t*>(st);
         c->spin_us = spin_us;
         c->spin_ticks = spin_us * (uint64_t)khz / 1000u;
         const uint64_t h = g_next_ctx.fetch_add(1);
         t_ctx[h] = c;
         *ctx = h;
     });
+}
+
+void free_buf(const Buf& b) {
+    if (b.kind == KIND_HOST_MAPPED) (void)hipHostFree(b.ptr);
+    else (void)hipFree(b.ptr);
 }
 
 SynStatus e_close_ctx(void*, uint64_t ctx) {
@@ -831,8 +929,8 @@ SynStatus e_close_ctx(void*, uint64_t ctx) {
         for (auto& e : c->fork_ev) (void)hipEventDestroy(e.second);
         for (auto& e : c->join_ev) (void)hipEventDestroy(e.second);
         for (auto& s : c->streams) (void)hipStreamDestroy(s.second);
-        for (auto& b : c->bufs) (void)hipFree(b.second.ptr);
-        if (c->bells) (void)hipHostFree(c->bells);
+        for (auto& b : c->bufs) free_buf(b.second);
+        if (c->status) (void)hipHostFree(c->status);
         delete c;
         t_ctx.erase(it);
     });
@@ -869,21 +967,52 @@ SynStatus e_query(void*, uint64_t ctx, const uint8_t* op, size_t op_len, const u
     });
 }
 
+// alloc (RFC-0040 ...md §5.1): Device as hipMalloc; HostMapped as pinned, mapped, coherent host
+// pages (hipHostMalloc), zeroed, whose 4 KiB pages become the next doorbell pages.
 SynStatus e_alloc(void*, uint64_t ctx, const SynAllocRequest* req, SynBuffer* out) {
     return call("alloc", false, [&] {
         Ctx& c = ctx_of(ctx);
         if (!req || !out) internal("alloc: null argument");
-        if (req->kind != 0 || req->reserve_only) unsupported("alloc: only plain device memory is served");
+        if (req->reserve_only || (req->kind != KIND_DEVICE && req->kind != KIND_HOST_MAPPED))
+            unsupported("alloc: Device and HostMapped memory are served, without reservations");
         if (req->align > 256 && (req->align & (req->align - 1))) internal("alloc: alignment is not a power of two");
+        if (req->kind == KIND_HOST_MAPPED && req->align > DOORBELL_PAGE)
+            unsupported("alloc: HostMapped memory is aligned to 4 KiB pages");
         void* p = nullptr;
-        if (hipMalloc(&p, req->bytes ? req->bytes : 1) != hipSuccess)
-            fail(SYN_CLASS_CAPACITY, SYN_CODE_ALLOC_FAILED, "alloc: " + std::to_string(req->bytes) + " bytes");
+        uint32_t first_page = 0;
+        if (req->kind == KIND_DEVICE) {
+            if (hipMalloc(&p, req->bytes ? req->bytes : 1) != hipSuccess)
+                fail(SYN_CLASS_CAPACITY, SYN_CODE_ALLOC_FAILED, "alloc: " + std::to_string(req->bytes) + " bytes");
+        } else {
+            const uint64_t pages = req->bytes ? (req->bytes + DOORBELL_PAGE - 1) / DOORBELL_PAGE : 1;
+            if (c.pages.size() + pages > MAX_DOORBELL_PAGES)
+                fail(SYN_CLASS_CAPACITY, SYN_CODE_ALLOC_FAILED,
+                     "alloc: the context has numbered all 65536 doorbell pages");
+            if (hipHostMalloc(&p, pages * DOORBELL_PAGE, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+                fail(SYN_CLASS_CAPACITY, SYN_CODE_ALLOC_FAILED,
+                     "alloc: " + std::to_string(req->bytes) + " bytes of host-mapped memory");
+            void* d = nullptr;
+            if (hipHostGetDevicePointer(&d, p, 0) != hipSuccess || d != p) {
+                (void)hipHostFree(p);
+                fail(SYN_CLASS_DEVICE, 0, "alloc: host-mapped memory whose device address is not its host address");
+            }
+            std::memset(p, 0, pages * DOORBELL_PAGE);
+            first_page = (uint32_t)c.pages.size();
+            for (uint64_t i = 0; i < pages; ++i) {
+                DoorbellPage pg;
+                pg.addr = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p) + i * DOORBELL_PAGE);
+                pg.bytes = req->bytes > i * DOORBELL_PAGE ? req->bytes - i * DOORBELL_PAGE : 0;
+                pg.live = true;
+                c.pages.push_back(pg);
+            }
+        }
         const uint64_t h = c.handle();
-        c.bufs[h] = Buf{p, req->bytes};
+        c.bufs[h] = Buf{p, req->bytes, req->kind, first_page};
         SynBuffer b{};
         b.addr = reinterpret_cast<uint64_t>(p);
         b.bytes = req->bytes;
         b.handle = h;
+        b.kind = req->kind;
         *out = b;
     });
 }
@@ -894,7 +1023,14 @@ SynStatus e_free(void*, uint64_t ctx, const SynBuffer* buf) {
         if (!buf) internal("free: null buffer");
         auto it = c.bufs.find(buf->handle);
         if (it == c.bufs.end()) internal("free: unknown buffer " + std::to_string(buf->handle));
-        check_hip(hipFree(it->second.ptr), "hipFree");
+        const Buf b = it->second;
+        if (b.kind == KIND_HOST_MAPPED) {  // its page numbers retire, never renaming another flag
+            const uint64_t pages = b.bytes ? (b.bytes + DOORBELL_PAGE - 1) / DOORBELL_PAGE : 1;
+            for (uint64_t i = 0; i < pages; ++i) c.pages[b.first_page + i].live = false;
+            check_hip(hipHostFree(b.ptr), "hipHostFree");
+        } else {
+            check_hip(hipFree(b.ptr), "hipFree");
+        }
         c.bufs.erase(it);
     });
 }
@@ -988,7 +1124,7 @@ SynStatus e_signal_host(void*, uint64_t ctx, uint64_t s, uint32_t flag, uint32_t
     return call("signal_host", false, [&] {
         Ctx& c = ctx_of(ctx);
         hipStream_t st = stream_of(c, s);
-        syn::launch_bell_signal(c.bells_dev + (size_t)flag_index(c, flag) * FLAG_WORDS, value, st);
+        syn::launch_bell_signal(flag_word(c, flag), value, st);
         check_hip(hipGetLastError(), "signal_host");
     });
 }
@@ -1003,9 +1139,8 @@ SynStatus e_wait_host(void*, uint64_t ctx, uint64_t s, uint32_t flag, uint32_t v
         if (cmp > 1) internal("wait_host: comparison code " + std::to_string(cmp) + " (0 Eq, 1 Geq)");
         if (has_reset > 1) internal("wait_host: has_reset must be 0 or 1");
         hipStream_t st = stream_of(c, s);
-        const uint32_t i = flag_index(c, flag);
-        syn::launch_bell_wait(c.bells_dev + (size_t)i * FLAG_WORDS, value, (int)cmp, (int)has_reset, reset,
-                              c.spin_ticks, c.bells_dev + (size_t)c.n_bells * FLAG_WORDS, i + 1, st);
+        syn::launch_bell_wait(flag_word(c, flag), value, (int)cmp, (int)has_reset, reset, c.spin_ticks,
+                              c.status + STATUS_BELL, flag + 1u, st);
         check_hip(hipGetLastError(), "wait_host");
     });
 }
@@ -1043,7 +1178,7 @@ SynStatus e_poll(void*, uint64_t ctx, uint64_t e, uint32_t* done) {
         if (r == hipSuccess) *done = 1;
         else if (r == hipErrorNotReady) *done = 0;
         else check_hip(r, "hipEventQuery");
-        if (*done) check_bells(c);
+        if (*done) check_status(c);
     });
 }
 
@@ -1066,14 +1201,14 @@ SynStatus e_synchronize(void*, uint64_t ctx, uint64_t s) {
     return call("synchronize", false, [&] {
         Ctx& c = ctx_of(ctx);
         check_hip(hipStreamSynchronize(stream_of(c, s)), "hipStreamSynchronize");
-        check_bells(c);
+        check_status(c);
     });
 }
 
 void copy_one(Ctx& c, hipStream_t st, const SynSlice& src, const SynSlice& dst) {
     if (src.bytes != dst.bytes) internal("copy: the slices differ in length");
-    check_hip(hipMemcpyAsync(addr_of(c, dst), addr_of(c, src), src.bytes, hipMemcpyDeviceToDevice, st),
-              "hipMemcpyAsync");
+    // device and host-mapped buffers alike (one address space)
+    check_hip(hipMemcpyAsync(addr_of(c, dst), addr_of(c, src), src.bytes, hipMemcpyDefault, st), "hipMemcpyAsync");
 }
 
 SynStatus e_copy(void*, uint64_t ctx, uint64_t s, const SynSlice* src, const SynSlice* dst) {
@@ -1242,21 +1377,17 @@ const SynModule g_module = {header(sizeof(SynModule)), 1, &g_vtbl, e_shutdown};
 
 }  // namespace
 
-// The host address of a doorbell flag of context `ctx`, for the host thread on the other side
-// of the doorbell (the CPU provider gives it as Doorbells::flag, crates/kernels-cpu/src/
-// doorbell.rs:76-81).  Called on the thread that opened the context.
-SYN_PROVIDER_EXPORT SynStatus syntropy_provider_flag_v1(uint64_t ctx, uint32_t flag, uint32_t** host) {
-    return call("flag", false, [&] {
-        Ctx& c = ctx_of(ctx);
-        if (!host) internal("flag: null output");
-        *host = c.bells + (size_t)flag_index(c, flag) * FLAG_WORDS;
-    });
-}
-
 SYN_PROVIDER_EXPORT const SynModule* syntropy_provider_entry_v1(const SynHostApi* host) {
     // the module checks the host's magic, major and size (RFC-0040 §10.4; module.rs:26-40)
     if (!host || std::memcmp(host->h.magic, SYN_PROVIDER_MAGIC, 8) != 0 ||
         host->h.abi_major != SYN_ABI_MAJOR || host->h.struct_size < sizeof(SynHostApi))
         return nullptr;
+    // the services are kept for the module's life; the fault-injection keys are read now
+    std::call_once(g_host_once, [&] {
+        g_host.api = *host;
+        g_host.present = true;
+        if (const char* v = host_config("fixture.panic_in")) g_host.panic_in = v;
+        if (const char* v = host_config("fixture.device_fault_in")) g_host.device_fault_in = v;
+    });
     return &g_module;
 }

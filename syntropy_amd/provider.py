@@ -23,6 +23,12 @@ HEALTH_SIZE = 12
 BACKEND_HIP = MEMDOMAIN_HIP = 2
 # DType::ALL indices (crates/core/src/dtype.rs:55-71)
 DT_F32, DT_I32 = 0, 7
+# MemKind (crates/kernels/src/memory.rs:33-40); doorbell pages are 4 KiB of HostMapped buffers
+KIND_DEVICE, KIND_HOST_MAPPED = 0, 1
+DOORBELL_PAGE = 4096
+# status classes and Kernels-domain codes (RFC-0040 13)
+CLASS_DEVICE, CLASS_TIMEOUT, CLASS_INTERNAL = 6, 10, 13
+CODE_DEVICE_STICKY, CODE_DOORBELL_TIMEOUT, CODE_PROVIDER_PANICKED = 8, 11, 16
 
 u8, u16, u32, u64, sz, vp = C.c_uint8, C.c_uint16, C.c_uint32, C.c_uint64, C.c_size_t, C.c_void_p
 
@@ -36,9 +42,11 @@ class Status(C.Structure):
     _fields_ = [("cls", u32), ("domain", u32), ("code", u16), ("retry", u8)]
 
 
-LOGFN = C.CFUNCTYPE(None, u8, C.c_char_p, C.c_char_p, sz)
+LOGFN = C.CFUNCTYPE(None, u8, C.c_char_p, C.c_void_p, sz)
 METRICFN = C.CFUNCTYPE(None, u32, u64)
-CONFIGFN = C.CFUNCTYPE(C.c_char_p, C.c_char_p)
+# returns a NUL-terminated string the host keeps alive, or null (a c_void_p: ctypes would free a
+# returned bytes object)
+CONFIGFN = C.CFUNCTYPE(C.c_void_p, C.c_char_p)
 
 
 class HostApi(C.Structure):
@@ -173,16 +181,33 @@ class ProviderError(RuntimeError):
         self.message = message
 
 
-def _noop_log(level, target, msg, n):
+# The host's services, as the core's loader provides them (crates/kernels-loader/src/host.rs):
+# process-wide and alive for the module's life.  CONFIG holds the config keys the module reads
+# (kernels.spin_kernel_max_us, and the fault-injection keys fixture.panic_in and
+# fixture.device_fault_in, which the module reads once, at its entry); LOG collects
+# (level, target, message) of every log call.
+CONFIG: dict = {}
+LOG: list = []
+_config_strings: dict = {}
+
+
+def _log(level, target, msg, n):
+    LOG.append((int(level), target.decode(errors="replace"), C.string_at(msg, n).decode(errors="replace")))
+
+
+def _metric(i, v):
     return None
 
 
-def _noop_metric(i, v):
-    return None
+def _config(key):
+    v = CONFIG.get(key.decode())
+    if v is None:
+        return None
+    buf = _config_strings.setdefault(v, C.create_string_buffer(str(v).encode()))
+    return C.addressof(buf)
 
 
-def _no_config(key):
-    return None
+_CALLBACKS = (LOGFN(_log), METRICFN(_metric), CONFIGFN(_config))
 
 
 def host_api(magic: bytes = MAGIC, major: int = ABI_MAJOR, size: int | None = None) -> HostApi:
@@ -191,8 +216,10 @@ def host_api(magic: bytes = MAGIC, major: int = ABI_MAJOR, size: int | None = No
     C.memmove(h.magic, magic, 8)
     h.abi_major, h.abi_minor = major, ABI_MINOR
     h.struct_size = C.sizeof(HostApi) if size is None else size
-    api = HostApi(h, LOGFN(_noop_log), METRICFN(_noop_metric), CONFIGFN(_no_config))
-    return api
+    return HostApi(h, *_CALLBACKS)
+
+
+_HOST = host_api()
 
 
 def load(path: str = PROVIDER_LIB, host: HostApi | None = None):
@@ -201,7 +228,7 @@ def load(path: str = PROVIDER_LIB, host: HostApi | None = None):
     entry = lib.syntropy_provider_entry_v1
     entry.argtypes = [C.POINTER(HostApi)]
     entry.restype = C.POINTER(Module)
-    host = host if host is not None else host_api()
+    host = host if host is not None else _HOST
     m = entry(C.byref(host))
     return (m.contents if m else None), lib, host
 
@@ -224,6 +251,7 @@ class Provider:
             raise RuntimeError(f"{m.n_providers} providers in the module")
         self.module = m
         self.vt = m.providers[0]
+        self._pages = {}  # per context: the next doorbell page number
         if self.vt.health_size != HEALTH_SIZE:
             raise RuntimeError("health_size is not 12")
 
@@ -288,10 +316,14 @@ class Provider:
         self._ok("prepare", self.vt.prepare(self.vt.slf, ctx, ob, on, sb, sn, C.byref(p)), ctx)
         return p
 
-    def alloc(self, ctx: int, nbytes: int, align: int = 256) -> Buffer:
+    def alloc(self, ctx: int, nbytes: int, align: int = 256, kind: int = KIND_DEVICE) -> Buffer:
         b = Buffer()
-        self._ok("alloc", self.vt.alloc(self.vt.slf, ctx, C.byref(AllocRequest(nbytes, align, 0, 0)),
+        self._ok("alloc", self.vt.alloc(self.vt.slf, ctx, C.byref(AllocRequest(nbytes, align, kind, 0)),
                                         C.byref(b)), ctx)
+        if kind == KIND_HOST_MAPPED:  # the core numbers the doorbell pages in allocation order
+            n = self._pages.get(ctx, 0)
+            b.first_page = n
+            self._pages[ctx] = n + max(1, -(-nbytes // DOORBELL_PAGE))
         return b
 
     def free(self, ctx: int, b: Buffer):
@@ -349,19 +381,19 @@ class Provider:
         kind 0 a futex word's address (cleared from 1 and woken), kind 1 an eventfd (+1)."""
         self._ok("arm_wake", self.vt.arm_wake(self.vt.slf, ctx, s, kind, handle), ctx)
 
-    def flag(self, ctx: int, page: int, slot: int) -> C.c_uint32:
-        """The host side of a doorbell flag, as a c_uint32 over its pinned word."""
-        f = self.lib.syntropy_provider_flag_v1
-        f.argtypes = [u64, u32, C.POINTER(C.POINTER(u32))]
-        f.restype = Status
-        p = C.POINTER(u32)()
-        self._ok("flag", f(ctx, page << 16 | slot, C.byref(p)), ctx)
-        return u32.from_address(C.addressof(p.contents))
-
     def health(self, ctx: int = 0) -> Health:
         h = Health()
         self._ok("health", self.vt.health(self.vt.slf, ctx, C.byref(h)), ctx)
         return h
+
+
+def host_flag(buf: Buffer, offset: int):
+    """(page, slot) of the doorbell flag at byte `offset` of a HostMapped buffer, and the host's
+    c_uint32 over it (the buffer's addr is also its host address)."""
+    assert offset % 4 == 0 and 0 <= offset < buf.bytes
+    page = buf.first_page + offset // DOORBELL_PAGE
+    slot = offset % DOORBELL_PAGE // 4
+    return page, slot, u32.from_address(buf.addr + offset)
 
 
 def packed(buf: Buffer, dtype: int, dims, offset: int = 0, elem: int = 4) -> TensorArg:
@@ -394,5 +426,6 @@ def view(addr: int, nbytes: int) -> BufferView:
     return v
 
 
-__all__ = ["Provider", "ProviderError", "load", "host_api", "packed", "op_args", "view", "Slice",
-           "Buffer", "PreparedOp", "Scalar", "DT_F32", "DT_I32", "PROVIDER_LIB", "MAGIC"]
+__all__ = ["Provider", "ProviderError", "load", "host_api", "host_flag", "packed", "op_args", "view",
+           "Slice", "Buffer", "PreparedOp", "Scalar", "DT_F32", "DT_I32", "PROVIDER_LIB", "MAGIC", "CONFIG",
+           "LOG", "KIND_DEVICE", "KIND_HOST_MAPPED"]

@@ -1,9 +1,12 @@
-"""Doorbells through the provider boundary (crates/kernels/src/provider.rs:346-377; RFC-0040 4.2):
-signal_host raises a pinned host flag after the work before it, wait_host holds the stream until
-the host replies and then writes the consumer reset, a captured step runs the constant-valued
-handshake on every replay, and a wait that passes its spin limit ends on its own and is reported
-as a Timeout.  Every wait here is answered by the host except the one that tests the limit,
-which runs on a context opened with a 2 ms limit."""
+"""Doorbells through the provider boundary (crates/kernels/src/provider.rs:346-377; RFC-0040 4.2
+and its 2026-11-07 revision): flags are 4-byte words of the 4 KiB pages of HostMapped buffers
+the host allocated through `alloc`, numbered in allocation order.  signal_host raises a flag
+after the work before it, wait_host holds the stream until the host replies and then writes the
+consumer reset, a captured step runs the constant-valued handshake on every replay, and a wait
+that passes its spin limit ends on its own and is reported as a DoorbellTimeout.  Every wait here
+is answered by the host except the one that tests the limit, which runs on a context opened with
+kernels.spin_kernel_max_us = 2000.  Each flag sits on a 64-byte line of its own, as the host's
+rule asks (RFC-0040 4.2)."""
 import os
 import time
 
@@ -23,8 +26,14 @@ N_OUT, K, ROWS = 512, 1024, 2
 @pytest.fixture(scope="module")
 def cx():
     c = Ctx()
+    c.bells = c.pr.alloc(c.ctx, 4096, kind=c.P.KIND_HOST_MAPPED)
     yield c
     c.close()
+
+
+def bell(cx, i):
+    """Flag i of the context's doorbell buffer: (page, slot, host word), on line i."""
+    return cx.P.host_flag(cx.bells, 64 * i)
 
 
 def gemv_step(cx, seed):
@@ -54,11 +63,11 @@ def test_signal_host_follows_the_work_before_it(cx):
     op, args, xb, yb, w, rng = gemv_step(cx, 1)
     x = gemv_activations(rng, ROWS, K).reshape(ROWS, K).astype(np.float32)
     cx.upload(xb.addr, x)
-    flag = pr.flag(cx.ctx, 0, 1)
+    page, slot, flag = bell(cx, 1)
     flag.value = 0
     announce("signal_host")
     pr.launch(cx.ctx, cx.s, op, args)
-    pr.signal_host(cx.ctx, cx.s, 0, 1, 1)
+    pr.signal_host(cx.ctx, cx.s, page, slot, 1)
     assert wait_for(flag, 1)
     pr.synchronize(cx.ctx, cx.s)
     got = cx.get(yb, np.float32, (ROWS, N_OUT))
@@ -73,12 +82,12 @@ def test_wait_host_holds_the_stream_until_the_host_replies(cx):
     op, args, xb, yb, w, rng = gemv_step(cx, 2)
     x = gemv_activations(rng, ROWS, K).reshape(ROWS, K).astype(np.float32)
     cx.upload(xb.addr, x)
-    reply, done = pr.flag(cx.ctx, 0, 2), pr.flag(cx.ctx, 0, 3)
+    (rp, rs, reply), (dp, ds, done) = bell(cx, 2), bell(cx, 3)
     reply.value, done.value = 0, 0
     announce("wait_host handshake")
-    pr.wait_host(cx.ctx, cx.s, 0, 2, 1, reset=0)
+    pr.wait_host(cx.ctx, cx.s, rp, rs, 1, reset=0)
     pr.launch(cx.ctx, cx.s, op, args)
-    pr.signal_host(cx.ctx, cx.s, 0, 3, 1)
+    pr.signal_host(cx.ctx, cx.s, dp, ds, 1)
     time.sleep(0.1)
     held = done.value
     reply.value = 1
@@ -93,11 +102,11 @@ def test_wait_host_holds_the_stream_until_the_host_replies(cx):
 
 def test_wait_host_geq_and_no_reset(cx):
     pr = cx.pr
-    reply, done = pr.flag(cx.ctx, 0, 4), pr.flag(cx.ctx, 0, 5)
+    (rp, rs, reply), (dp, ds, done) = bell(cx, 4), bell(cx, 5)
     reply.value, done.value = 3, 0
     announce("wait_host geq")
-    pr.wait_host(cx.ctx, cx.s, 0, 4, 5, geq=True, reset=None)
-    pr.signal_host(cx.ctx, cx.s, 0, 5, 1)
+    pr.wait_host(cx.ctx, cx.s, rp, rs, 5, geq=True, reset=None)
+    pr.signal_host(cx.ctx, cx.s, dp, ds, 1)
     time.sleep(0.05)
     held = done.value
     reply.value = 9
@@ -112,13 +121,13 @@ def test_captured_step_runs_the_handshake_on_every_replay(cx):
     times: per step the host writes x, raises F, waits for D, resets D (RFC-0040 4.2 rules 2-3)."""
     pr = cx.pr
     op, args, xb, yb, w, rng = gemv_step(cx, 3)
-    f, d = pr.flag(cx.ctx, 0, 6), pr.flag(cx.ctx, 0, 7)
+    (fp, fs, f), (dp, ds, d) = bell(cx, 6), bell(cx, 7)
     f.value, d.value = 0, 0
     announce("doorbell capture/replay")
     pr.begin_capture(cx.ctx, cx.s)
-    pr.wait_host(cx.ctx, cx.s, 0, 6, 1, reset=0)
+    pr.wait_host(cx.ctx, cx.s, fp, fs, 1, reset=0)
     pr.launch(cx.ctx, cx.s, op, args)
-    pr.signal_host(cx.ctx, cx.s, 0, 7, 1)
+    pr.signal_host(cx.ctx, cx.s, dp, ds, 1)
     g = pr.end_capture(cx.ctx, cx.s)
     for step in range(3):
         x = gemv_activations(rng, ROWS, K).reshape(ROWS, K).astype(np.float32)
@@ -147,13 +156,13 @@ def test_arm_wake_eventfd_after_the_doorbell(cx):
     pr = cx.pr
     op, args, xb, yb, w, rng = gemv_step(cx, 4)
     cx.upload(xb.addr, gemv_activations(rng, ROWS, K).reshape(ROWS, K).astype(np.float32))
-    d = pr.flag(cx.ctx, 0, 11)
+    dp, ds, d = bell(cx, 11)
     d.value = 0
     fd = os.eventfd(0, os.EFD_NONBLOCK)
     try:
         announce("arm_wake eventfd")
         pr.launch(cx.ctx, cx.s, op, args)
-        pr.signal_host(cx.ctx, cx.s, 0, 11, 1)
+        pr.signal_host(cx.ctx, cx.s, dp, ds, 1)
         pr.arm_wake(cx.ctx, cx.s, 1, fd)
         assert wait_readable(fd), "no wake within 5 s"
         assert d.value == 1, "the wake came before the doorbell"
@@ -208,14 +217,14 @@ def test_arm_wake_futex_word_is_cleared_and_woken(cx):
 def test_captured_arm_wake_fires_on_every_replay(cx):
     pr = cx.pr
     op, args, xb, yb, w, rng = gemv_step(cx, 5)
-    d = pr.flag(cx.ctx, 0, 12)
+    dp, ds, d = bell(cx, 12)
     d.value = 0
     fd = os.eventfd(0, os.EFD_NONBLOCK)
     try:
         announce("arm_wake capture/replay")
         pr.begin_capture(cx.ctx, cx.s)
         pr.launch(cx.ctx, cx.s, op, args)
-        pr.signal_host(cx.ctx, cx.s, 0, 12, 1)
+        pr.signal_host(cx.ctx, cx.s, dp, ds, 1)
         pr.arm_wake(cx.ctx, cx.s, 1, fd)
         g = pr.end_capture(cx.ctx, cx.s)
         for step in range(3):
@@ -232,35 +241,70 @@ def test_captured_arm_wake_fires_on_every_replay(cx):
         os.close(fd)
 
 
-def test_flags_outside_the_pages_are_refused(cx):
+def test_pages_are_numbered_in_allocation_order(cx):
+    """Pages count across the context's HostMapped buffers in allocation order and are never
+    renumbered; a flag outside a live page, past a page or past its buffer's end is refused
+    before anything is enqueued; device memory holds no flags
+    (crates/kernels-cuda/src/capture/tests.rs:416-456)."""
     P, pr = cx.P, cx.pr
-    for page, slot in [(0, 64), (1, 0), (65535, 63)]:
-        with pytest.raises(P.ProviderError):
+    big = pr.alloc(cx.ctx, 3 * 4096, kind=P.KIND_HOST_MAPPED)
+    short = pr.alloc(cx.ctx, 100, kind=P.KIND_HOST_MAPPED)
+    assert big.first_page == cx.bells.first_page + 1 and short.first_page == big.first_page + 3
+    assert big.addr % 4096 == 0 and big.kind == P.KIND_HOST_MAPPED
+    page, slot, w = P.host_flag(big, 2 * 4096 + 8)
+    assert (page, slot) == (big.first_page + 2, 2)
+    w.value = 0
+    announce("doorbell page numbering")
+    pr.signal_host(cx.ctx, cx.s, page, slot, 7)
+    pr.synchronize(cx.ctx, cx.s)
+    assert w.value == 7
+    sp, ss, sw = P.host_flag(short, 96)  # the last whole word of the 100-byte buffer
+    pr.signal_host(cx.ctx, cx.s, sp, ss, 3)
+    pr.synchronize(cx.ctx, cx.s)
+    assert sw.value == 3
+    refused = [(short.first_page, 25),           # past the buffer's end
+               (cx.bells.first_page, 1024),      # past the page
+               (short.first_page + 1, 0),        # no such page yet
+               (65535, 0)]
+    pr.free(cx.ctx, big)
+    refused += [(big.first_page, 0), (big.first_page + 2, 2)]  # freed pages
+    for page, slot in refused:
+        with pytest.raises(P.ProviderError) as e:
             pr.signal_host(cx.ctx, cx.s, page, slot, 1)
+        assert e.value.cls == P.CLASS_INTERNAL and f"page {page} slot {slot}" in e.value.message
         with pytest.raises(P.ProviderError):
             pr.wait_host(cx.ctx, cx.s, page, slot, 1)
+    nxt = pr.alloc(cx.ctx, 4096, kind=P.KIND_HOST_MAPPED)
+    assert nxt.first_page == short.first_page + 1  # freed numbers are not reused
+    pr.signal_host(cx.ctx, cx.s, short.first_page, 0, 1)  # the short buffer's flags still work
     pr.synchronize(cx.ctx, cx.s)
+    pr.free(cx.ctx, short)
+    pr.free(cx.ctx, nxt)
 
 
 def test_a_wait_past_its_spin_limit_ends_and_is_reported():
-    """A context opened with a 2 ms limit: a wait the host never answers gives up on its own,
-    writes no reset, lets the stream run on (the next flag rises), and synchronize reports one
-    Timeout naming the flag; the next synchronize is clean."""
-    os.environ["SYNTROPY_SPIN_MAX_US"] = "2000"
+    """A context opened with kernels.spin_kernel_max_us = 2000: a wait the host never answers
+    gives up on its own, writes no reset, lets the stream run on (the next flag rises), and
+    synchronize reports one Timeout / DoorbellTimeout (11) naming the flag; the next synchronize
+    is clean (RFC-0040 ...md:1342, 1361)."""
+    from syntropy_amd import provider as P
+    P.CONFIG["kernels.spin_kernel_max_us"] = "2000"
     try:
         c = Ctx()
     finally:
-        del os.environ["SYNTROPY_SPIN_MAX_US"]
+        del P.CONFIG["kernels.spin_kernel_max_us"]
     try:
-        P, pr = c.P, c.pr
-        reply, after = pr.flag(c.ctx, 0, 9), pr.flag(c.ctx, 0, 10)
+        pr = c.pr
+        b = pr.alloc(c.ctx, 4096, kind=P.KIND_HOST_MAPPED)
+        (rp, rs, reply), (ap, as_, after) = P.host_flag(b, 9 * 64), P.host_flag(b, 10 * 64)
         reply.value, after.value = 0, 0
         announce("wait_host spin limit 2 ms")
-        pr.wait_host(c.ctx, c.s, 0, 9, 1, reset=5)
-        pr.signal_host(c.ctx, c.s, 0, 10, 1)
+        pr.wait_host(c.ctx, c.s, rp, rs, 1, reset=5)
+        pr.signal_host(c.ctx, c.s, ap, as_, 1)
         with pytest.raises(P.ProviderError) as e:
             pr.synchronize(c.ctx, c.s)
-        assert e.value.cls == 10 and "slot 9" in str(e.value) and "spin limit of 2000" in str(e.value)
+        assert (e.value.cls, e.value.code) == (P.CLASS_TIMEOUT, P.CODE_DOORBELL_TIMEOUT)
+        assert f"page {rp} slot {rs}" in str(e.value) and "spin limit of 2000" in str(e.value)
         assert reply.value == 0 and after.value == 1
         pr.synchronize(c.ctx, c.s)
     finally:

@@ -337,6 +337,53 @@ def test_moe_grouped_site_input_through_the_provider(cx):
     assert (got[site[ids] == 0].view(np.uint32) == 0x7FC0DEAD).all()
 
 
+@pytest.mark.parametrize("rows", [5, 120])
+def test_moe_grouped_refusal_is_reported_at_synchronize(rows):
+    """An id naming no expert: the launch writes nothing (the decode kernels at 5 rows, the
+    many-token path at 120), and the next synchronize reports the first such slot as Internal,
+    with the CPU provider's message (crates/kernels-cpu/src/moe.rs:433-441, moe/entry.rs:309);
+    the report is given once, and a clean launch after it runs."""
+    c = Ctx()
+    try:
+        P, pr = c.P, c.pr
+        E, top_k, hidden, inter = 6, 2, 256, 512
+        rng = MoeRng(79)
+        gate = moe_matrix(rng, o.Q4_K, E * inter, hidden, o.f16_bits)
+        up = moe_matrix(rng, o.Q4_K, E * inter, hidden, o.f16_bits)
+        down = moe_matrix(rng, o.Q4_K, E * hidden, inter, o.f16_bits)
+        x = o.normal(0x51A20006, 1.0, rows * hidden).reshape(rows, hidden)
+        ids = np.stack([np.arange(top_k) + r % (E - 1) for r in range(rows)]).astype(np.int32)
+        bad = ids.copy()
+        bad[rows - 2, 1] = E  # and a later one, which is not the first
+        bad[rows - 1, 0] = -3
+        key = {"op": "MoeGrouped", "schemes": [{"Ggml": "Q4_K"}, {"Plain": "F32"}, {"Plain": "F32"}],
+               "layout": 0, "variant": 0}
+        op = pr.prepare(c.ctx, key, shape(rows, E, top_k, hidden, inter))
+        gd, ud, dd = dev(gate), dev(up), dev(down)
+        views = [P.view(t.data_ptr(), t.numel()) for t in (gd, ud, dd)]
+        xb, bb, ib = c.put(x), c.put(bad), c.put(ids)
+        per_b = c.put(np.full(rows * top_k * hidden, 0x7FC0DEAD, np.uint32))
+        per_arg = P.packed(per_b, P.DT_F32, [rows, top_k, hidden])
+        ws = c.workspace(op)
+        announce(f"provider moe refusal rows={rows}")
+        pr.launch(c.ctx, c.s, op, P.op_args([P.packed(xb, P.DT_F32, [rows, hidden]),
+                                             P.packed(bb, P.DT_I32, [rows, top_k])], [per_arg], views, ws))
+        with pytest.raises(P.ProviderError) as e:
+            pr.synchronize(c.ctx, c.s)
+        assert e.value.cls == P.CLASS_INTERNAL
+        assert f"row {rows - 2} rank 1 routes to expert {E}" in e.value.message, e.value.message
+        assert any(f"routes to expert {E}" in m for _, _, m in P.LOG)
+        assert (c.get(per_b, np.uint32, rows * top_k * hidden) == 0x7FC0DEAD).all()
+        pr.synchronize(c.ctx, c.s)  # reported once
+        pr.launch(c.ctx, c.s, op, P.op_args([P.packed(xb, P.DT_F32, [rows, hidden]),
+                                             P.packed(ib, P.DT_I32, [rows, top_k])], [per_arg], views, ws))
+        pr.synchronize(c.ctx, c.s)
+        want = o.moe_grouped(o.Q4_K, o.Q4_K, E, top_k, hidden, inter, gate, up, down, x, ids, threads=8)
+        assert_same(c.get(per_b, np.float32, (rows, top_k, hidden)), want, "after the refusal")
+    finally:
+        c.close()
+
+
 def test_route_without_renormalization(cx):
     P, pr = cx.P, cx.pr
     E, top_k, hidden, rows = 8, 2, 256, 5

@@ -9,6 +9,7 @@ import ctypes as C
 import json
 import os
 import subprocess
+import sys
 import threading
 
 import pytest
@@ -27,13 +28,75 @@ def pr():
     return P.Provider()
 
 
-def test_exports_the_entry_symbol_and_the_flag_accessor_only():
+def test_the_dynamic_symbol_table_holds_exactly_the_entry_symbol():
+    """crates/kernels-loader/tests/exports.rs:48-70: `nm -D --defined-only` lists the entry symbol
+    and nothing else (the version node, when the linker lists it, is an absolute symbol); the
+    entry is under the version node SYNTROPY_PROVIDER_1."""
     out = subprocess.run(["nm", "-D", "--defined-only", P.PROVIDER_LIB], capture_output=True, text=True,
                          check=True).stdout
-    syms = [l.split()[-1] for l in out.splitlines() if l.split() and l.split()[-2] in "TtDdBbRrWwVv"]
-    syms = sorted(s for s in syms if not s.startswith("SYNTROPY_PROVIDER_1"))
-    assert syms == ["syntropy_provider_entry_v1@@SYNTROPY_PROVIDER_1",
-                    "syntropy_provider_flag_v1@@SYNTROPY_PROVIDER_1"], syms
+    lines = [l for l in out.splitlines() if l.split() and not l.rstrip().endswith("A SYNTROPY_PROVIDER_1")]
+    names = [l.split()[-1] for l in lines]
+    assert [n.split("@")[0] for n in names] == ["syntropy_provider_entry_v1"], out
+    assert names[0].endswith("@@SYNTROPY_PROVIDER_1"), out
+
+
+STICKY_SCRIPT = r"""
+import json, sys
+import torch  # one HIP runtime in the process
+from syntropy_amd import provider as P
+P.CONFIG.update(json.loads(sys.argv[1]))
+pr = P.Provider()
+res = {}
+def run(name, f):
+    st = f()
+    res[name] = [st.cls, st.code, st.domain, pr.message()]
+run("ops", lambda: pr.vt.ops(pr.vt.slf, P.OutBuf()))
+run("build", lambda: pr.vt.build(pr.vt.slf, P.OutBuf()))
+h = P.Health()
+run("health", lambda: pr.vt.health(pr.vt.slf, 0, h))
+res["health_state"] = [h.kind, h.domain, h.detail]
+res["log"] = P.LOG
+print(json.dumps(res))
+"""
+
+
+def sticky_run(config):
+    r = subprocess.run([sys.executable, "-c", STICKY_SCRIPT, json.dumps(config)], capture_output=True, text=True,
+                       cwd=ROOT, timeout=300)
+    assert r.returncode == 0, r.stderr
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def test_a_caught_panic_makes_the_provider_sticky():
+    """fixture.panic_in names an entry that throws (the reference's test provider key,
+    crates/kernels-loader/examples/test_provider.rs:7-16): that call returns Internal /
+    ProviderPanicked (16); every later entry but health, free and close_ctx returns Device /
+    DeviceSticky (8); health reports Sticky (kind 3) with code 16; the host's log has the error
+    (crates/kernels/src/abi/guest.rs:184-230)."""
+    r = sticky_run({"fixture.panic_in": "ops"})
+    assert r["ops"][:3] == [P.CLASS_INTERNAL, P.CODE_PROVIDER_PANICKED, 1]
+    assert "injected by fixture.panic_in" in r["ops"][3]
+    assert r["build"][:3] == [P.CLASS_DEVICE, P.CODE_DEVICE_STICKY, 1]
+    assert "sticky after code 16" in r["build"][3]
+    assert r["health"][0] == 0 and r["health_state"] == [3, 1, 16]
+    assert any(level == 0 and "injected by fixture.panic_in" in msg for level, _, msg in r["log"])
+
+
+def test_a_sticky_device_error_makes_the_provider_sticky():
+    """fixture.device_fault_in makes an entry meet an illegal-address error, as a faulted kernel
+    reports it: Device / DeviceSticky (8), the provider sticky with that code (RFC-0040 ...md:861,
+    933)."""
+    r = sticky_run({"fixture.device_fault_in": "build"})
+    assert r["ops"][0] == 0
+    assert r["build"][:3] == [P.CLASS_DEVICE, P.CODE_DEVICE_STICKY, 1]
+    assert "the provider is sticky" in r["build"][3]
+    assert r["health_state"] == [3, 1, 8]
+    assert any(level == 0 and "fixture.device_fault_in" in msg for level, _, msg in r["log"])
+
+
+def test_no_injection_leaves_the_provider_healthy():
+    r = sticky_run({})
+    assert r["ops"][0] == 0 and r["build"][0] == 0 and r["health_state"] == [0, 0, 0] and r["log"] == []
 
 
 def test_struct_sizes_match_the_reference_layout():
