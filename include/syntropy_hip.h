@@ -123,6 +123,22 @@ int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, uint64_t w_by
                     uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
                     void* stream);
 
+/* ---- RmsNorm and Logits ----------------------------------------------------------------------
+ * syn_rms_norm: y = RmsNorm(x) of each of `rows` rows of n F32 values (n <= 16384), weight g [n]:
+ *   ss = sum of x[i] x[i] in the F32Fixed order, mean = ss / n, scale = 1 / sqrt(mean + eps),
+ *   y[i] = (x[i] scale) g[i], each one IEEE F32 operation (crates/kernels/src/reference/
+ *   norm.rs:39-47; the order crates/kernels/src/reference/reduce.rs:7-20).
+ * syn_logits(_workspace_bytes): the reference's Logits (crates/kernels/src/reference/linear.rs:
+ *   118-161): each row of x [rows, hidden] normalised as syn_rms_norm (g [hidden], eps), then
+ *   the head [vocab, hidden] in `layout` as syn_gemv_layout computes a Gemv, into y [rows, vocab].
+ *   The workspace holds the normalised rows and the Gemv's workspace. */
+int syn_rms_norm(const float* x, const float* g, uint32_t rows, uint32_t n, float eps, float* y, void* stream);
+int syn_logits_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t rows, uint32_t vocab, uint32_t hidden,
+                               uint64_t* bytes);
+int syn_logits(uint32_t layout, int32_t wtype, const void* head, uint64_t head_bytes, uint32_t vocab,
+               uint32_t hidden, const float* g, float eps, const float* x, uint32_t rows, float* y, void* ws,
+               uint64_t ws_bytes, void* stream);
+
 /* ---- Prefill GEMM ---------------------------------------------------------------------------
  * Q4_K weights times many activation rows on the matrix cores, each output bit-identical to
  * syn_gemv (which takes this path itself for Q4_K calls of 32 rows or more).  The reference

@@ -23,6 +23,10 @@
  *                    the hand-computed cases at :407-458, plus the F64 derived bound
  *   or_gate_up_act   or_gemv and or_silu composed; a one-hot Q8_0 gate/up pair pins the row
  *                    order (gate rows first) and the product against the activation codes
+ *   or_rms_norm      the edge cases of norm.rs's docs (zeros, eps 0, NaN, infinity), a hand
+ *                    case whose bits follow from the operation order, and an F64 bound
+ *   or_logits        or_rms_norm and or_gemv composed; rows whose norm is an exact halving pin
+ *                    that the norm comes first and that g scales its own column
  *   or_moe_*         packing against brute force; MoE slot = expert FFN of the row alone
  *                    (moe/tests.rs:315); combine against its definition; route ids against a
  *                    brute-force sort.  MoeRoute and MoeCombine have no reference code: their
@@ -940,6 +944,38 @@ int or_gemv_threads(int ty, const uint8_t* w, size_t n_out, size_t k, const floa
 /* and the gated product is the MoE FFN's (crates/kernels-cpu/src/moe.rs:529-551): silu with  */
 /* the software exp, the product rounded once.                                              */
 /* ===================================================================================== */
+
+/* ===================================================================================== */
+/* RmsNorm and Logits: crates/kernels/src/reference/norm.rs:39-47 (Norm::row) and           */
+/* crates/kernels/src/reference/linear.rs:118-161 (logits: each row normalised, then the head */
+/* as Gemv).  The head product is the CPU provider's Gemv (or_gemv), as a provider computes */
+/* its Gemv-class ops.                                                                        */
+/* ===================================================================================== */
+
+/* ss = sum of x[i] x[i] in the F32Fixed order; mean = ss / n; scale = 1 / sqrt(mean + eps);
+ * y[i] = (x[i] scale) g[i]: each step one IEEE F32 operation */
+void or_rms_norm_row(const float* x, const float* g, size_t n, float eps, float* y) {
+    const float ss = or_dot(x, x, n);
+    const float mean = ss / (float)n;
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (size_t i = 0; i < n; ++i) y[i] = (x[i] * scale) * g[i];
+}
+
+int or_rms_norm(const float* x, const float* g, size_t rows, size_t n, float eps, float* y) {
+    if (n == 0) return 0;
+    for (size_t r = 0; r < rows; ++r) or_rms_norm_row(x + r * n, g, n, eps, y + r * n);
+    return 0;
+}
+
+int or_logits(int ty, const uint8_t* head, size_t vocab, size_t hidden, const float* g, float eps,
+              const float* x, size_t rows, float* y, int threads) {
+    float* h = (float*)malloc(rows * hidden * sizeof(float) + 1);
+    if (!h) return -1;
+    or_rms_norm(x, g, rows, hidden, eps, h);
+    const int rc = or_gemv_threads(ty, head, vocab, hidden, h, rows, y, threads);
+    free(h);
+    return rc;
+}
 
 int or_gate_up_act(int ty, const uint8_t* w, size_t n_out, size_t k, const float* x, size_t rows,
                    float* y, int threads) {

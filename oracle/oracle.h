@@ -86,6 +86,13 @@ int or_gate_up_act(int ty, const uint8_t* w, size_t n_out, size_t k, const float
                    float* y, int threads);
 void or_partition(int ty, size_t n_out, size_t k, size_t parts, size_t* starts, size_t* ends);
 
+/* ---- RmsNorm (crates/kernels/src/reference/norm.rs:39-47) and Logits
+ *      (crates/kernels/src/reference/linear.rs:118-161): rows normalised, then the head as Gemv ---- */
+void or_rms_norm_row(const float* x, const float* g, size_t n, float eps, float* y);
+int or_rms_norm(const float* x, const float* g, size_t rows, size_t n, float eps, float* y);
+int or_logits(int ty, const uint8_t* head, size_t vocab, size_t hidden, const float* g, float eps,
+              const float* x, size_t rows, float* y, int threads);
+
 /* ---- MoE (crates/kernels-cpu/src/moe.rs:402-551) ---- */
 size_t or_moe_workspace_bytes(size_t n_experts, size_t top_k, size_t hidden, size_t inter,
                               size_t rows);

@@ -77,6 +77,8 @@ def lib():
         L.or_gemv_threads.argtypes = [i32, vp, sz, sz, vp, sz, vp, i32]
         L.or_gate_up_act.argtypes = [i32, vp, sz, sz, vp, sz, vp, i32]
         L.or_partition.argtypes = [i32, sz, sz, sz, vp, vp]
+        L.or_rms_norm.argtypes = [vp, vp, sz, sz, C.c_float, vp]
+        L.or_logits.argtypes = [i32, vp, sz, sz, vp, C.c_float, vp, sz, vp, i32]
         L.or_moe_workspace_bytes.restype = sz
         L.or_moe_workspace_bytes.argtypes = [sz, sz, sz, sz, sz]
         L.or_moe_pack.argtypes = [vp, sz, sz, sz, vp, vp]
@@ -247,6 +249,28 @@ def gate_up_act(ty: int, w, n_out: int, k: int, x, rows: int, threads: int = 1) 
     if lib().or_gate_up_act(ty, _p(w), n_out, k, _p(x), rows, _p(y), threads):
         raise ValueError("gate_up_act refused")
     return y.reshape(rows, n_out)
+
+
+def rms_norm(x, g, eps: float) -> np.ndarray:
+    """RmsNorm of each row of x [rows, n] with weight g [n] (oracle.c or_rms_norm)."""
+    x = _f32(x)
+    rows, n = x.shape
+    g = _f32(g).ravel()
+    assert g.size == n
+    y = np.full((rows, n), np.nan, dtype=np.float32)
+    assert lib().or_rms_norm(_p(x), _p(g), rows, n, eps, _p(y)) == 0
+    return y
+
+
+def logits(ty: int, head, vocab: int, hidden: int, g, eps: float, x, rows: int, threads: int = 1):
+    """Logits: each row of x normalised by (g, eps), then the head [vocab, hidden] as Gemv."""
+    head = np.ascontiguousarray(head, dtype=np.uint8)
+    x, g = _f32(x).ravel(), _f32(g).ravel()
+    assert head.size == vocab * row_bytes(ty, hidden) and g.size == hidden and x.size >= rows * hidden
+    y = np.full(rows * vocab, np.nan, dtype=np.float32)
+    if lib().or_logits(ty, _p(head), vocab, hidden, _p(g), eps, _p(x), rows, _p(y), threads):
+        raise ValueError("logits refused")
+    return y.reshape(rows, vocab)
 
 
 def partition(ty: int, n_out: int, k: int, parts: int):

@@ -600,6 +600,61 @@ SYN_EXPORT int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, ui
     return syn_gate_up_act_rows(layout, wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, ws_bytes, stream, nullptr);
 }
 
+// ---- RmsNorm and Logits ------------------------------------------------------------------
+
+SYN_EXPORT int syn_rms_norm(const float* x, const float* g, uint32_t rows, uint32_t n, float eps, float* y,
+                            void* stream) {
+    const char* W = "syn_rms_norm";
+    if (n > (uint32_t)syn::NORM_MAX_COLS) return fail(SYN_E_UNSUPPORTED, "%s: rows of %u values (at most %d)", W, n, syn::NORM_MAX_COLS);
+    if (rows == 0 || n == 0) return SYN_OK;
+    if (!x || !g || !y) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!aligned(x, 4) || !aligned(g, 4) || !aligned(y, 4)) return fail(SYN_E_INVALID, "%s: operands must be 4-byte aligned", W);
+    syn::launch_rms_norm(x, g, (int)rows, (int)n, eps, y, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_logits_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t rows, uint32_t vocab,
+                                          uint32_t hidden, uint64_t* bytes) {
+    const char* W = "syn_logits_workspace_bytes";
+    if (!bytes) return fail(SYN_E_INVALID, "%s: null output", W);
+    (void)vocab;
+    uint64_t g = 0;
+    if (int rc = syn_gemv_layout_workspace_bytes(layout, wtype, rows, hidden, &g)) return rc;
+    // the normalised rows [rows][hidden] F32, then the head product's workspace
+    *bytes = syn::align_up(4ull * rows * hidden, 256) + g;
+    return SYN_OK;
+}
+
+int syn_logits_rows(uint32_t layout, int32_t wtype, const void* head, uint64_t head_bytes, uint32_t vocab,
+                    uint32_t hidden, const float* g, float eps, const float* x, uint32_t rows, float* y, void* ws,
+                    uint64_t ws_bytes, void* stream, const uint32_t* active) {
+    const char* W = "syn_logits";
+    uint64_t need = 0;
+    if (int rc = syn_logits_workspace_bytes(layout, wtype, rows, vocab, hidden, &need)) return rc;
+    if (hidden > (uint32_t)syn::NORM_MAX_COLS)
+        return fail(SYN_E_UNSUPPORTED, "%s: hidden %u (at most %d)", W, hidden, syn::NORM_MAX_COLS);
+    if (rows == 0 || vocab == 0) return SYN_OK;
+    if (!x || !g || !ws) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (ws_bytes < need)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)need);
+    if (!aligned(ws, 256) || !aligned(x, 4) || !aligned(g, 4))
+        return fail(SYN_E_INVALID, "%s: the workspace must be 256-byte, x and g 4-byte aligned", W);
+    float* h = (float*)ws;
+    const uint64_t hb = syn::align_up(4ull * rows * hidden, 256);
+    syn::launch_rms_norm(x, g, (int)rows, (int)hidden, eps, h, (hipStream_t)stream, active);
+    if (int rc = check_launch(W)) return rc;
+    return syn_gemv_layout_rows(layout, wtype, head, head_bytes, vocab, hidden, h, rows, y, (uint8_t*)ws + hb,
+                                ws_bytes - hb, stream, active);
+}
+
+SYN_EXPORT int syn_logits(uint32_t layout, int32_t wtype, const void* head, uint64_t head_bytes, uint32_t vocab,
+                          uint32_t hidden, const float* g, float eps, const float* x, uint32_t rows, float* y,
+                          void* ws, uint64_t ws_bytes, void* stream) {
+    return syn_logits_rows(layout, wtype, head, head_bytes, vocab, hidden, g, eps, x, rows, y, ws, ws_bytes, stream,
+                           nullptr);
+}
+
 SYN_EXPORT int syn_quantize(int32_t wtype, const float* x, uint64_t n, void* out,
                             uint64_t out_bytes, void* stream) {
     const char* W = "syn_quantize";

@@ -15,6 +15,9 @@ int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
 int syn_gate_up_act_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
                          uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
                          void* stream, const uint32_t* active);
+int syn_logits_rows(uint32_t layout, int32_t wtype, const void* head, uint64_t head_bytes, uint32_t vocab,
+                    uint32_t hidden, const float* g, float eps, const float* x, uint32_t rows, float* y, void* ws,
+                    uint64_t ws_bytes, void* stream, const uint32_t* active);
 int syn_moe_route_rows(const float* router, const float* x, uint32_t rows, uint32_t hidden, uint32_t n_experts,
                        uint32_t top_k, int32_t renormalize, int32_t* ids, float* w, float* probs, void* stream,
                        const uint32_t* active);

@@ -38,6 +38,10 @@ void launch_gemv_q4k_batch_f32(const uint8_t* const* W, int np, const int* n_out
 void launch_q4k_x8(const uint8_t* src, uint8_t* dst, uint64_t nblocks, int inverse, hipStream_t stream);
 void launch_act_quant_batch(int np, const float* const* x, const int* k, uint8_t* const* ws,
                             hipStream_t stream);
+// norm.hip: RmsNorm rows of at most NORM_MAX_COLS values
+constexpr int NORM_MAX_COLS = 16384;
+void launch_rms_norm(const float* x, const float* g, int rows, int n, float eps, float* y, hipStream_t stream,
+                     const uint32_t* active = nullptr);
 // moe.hip
 bool moe_route_supported(int hidden);
 void launch_moe_route(const float* router, const float* x, int rows, int hidden, int n_experts,

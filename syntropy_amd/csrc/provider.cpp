@@ -443,6 +443,10 @@ bool plan_of(const Key& k, const Shape& s, Plan& p) {
             if (n_out > (1u << 29) ||
                 syn_gate_up_act_workspace_bytes(k.layout, k.weight, s.rows, n_out, k_in, &ws) != SYN_OK)
                 return false;
+        } else if (k.op == Op::Logits) {
+            // room for the normalised rows too (the two-weight binding normalises first)
+            if (k_in > 16384 || syn_logits_workspace_bytes(k.layout, k.weight, s.rows, n_out, k_in, &ws) != SYN_OK)
+                return false;
         } else if (syn_gemv_layout_workspace_bytes(k.layout, k.weight, s.rows, k_in, &ws) != SYN_OK) {
             return false;
         }
@@ -742,8 +746,17 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         const bool gated = p.op == Op::GateUpAct;
         const char* name = gated ? "GateUpAct" : p.op == Op::Gemm ? "Gemm" : p.op == Op::Logits ? "Logits" : "Gemv";
         const uint32_t n_out = p.dims[0], k_in = p.dims[1];
-        if (a.n_inputs != 1 || a.n_outputs != 1 || a.n_weights != 1 || a.n_statics != 0)
+        // Logits also takes the final norm (linear.rs:118-161): weight 1 is its F32 [hidden]
+        // weight and constant 0 its F32 eps.  With the head alone it is the product of the
+        // already-normalised input (the graph's RmsNorm -> Logits, crates/graph/src/blocks/
+        // embed.rs:98-135).
+        const bool normed = p.op == Op::Logits && a.n_weights == 2;
+        if (normed) {
+            if (a.n_inputs != 1 || a.n_outputs != 1 || a.n_statics != 1 || a.statics[0].tag != 0)
+                internal("Logits with its norm binds one input, one output, the head, the norm weight and an F32 eps");
+        } else if (a.n_inputs != 1 || a.n_outputs != 1 || a.n_weights != 1 || a.n_statics != 0) {
             internal(std::string(name) + " binds one input, one output, one weight and no constants");
+        }
         const uint8_t* x = tensor(c, a.inputs[0], 0, rows, k_in, 1, 4, "x");
         uint8_t* y = tensor(c, a.outputs[0], 0, rows, n_out, 1, 4, "y");
         const bool fl = p.weight == SYN_F16 || p.weight == SYN_BF16;
@@ -753,7 +766,15 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         const uint64_t wbytes = (uint64_t)k_in / be * bb * n_out * (gated ? 2 : 1);
         const SynBufferView& w = weight(a, 0, wbytes, name);
         uint8_t* ws = workspace_of(c, a, p);
-        if (gated)
+        if (normed) {
+            const SynBufferView& g = weight(a, 1, 4ull * k_in, "Logits norm");
+            float eps;
+            std::memcpy(&eps, &a.statics[0].bits, 4);
+            check_syn(syn_logits_rows(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in,
+                                      (const float*)g.addr, eps, (const float*)x, rows, (float*)y, ws,
+                                      p.workspace - 256, st, active),
+                      name);
+        } else if (gated)
             check_syn(syn_gate_up_act_rows(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in,
                                            (const float*)x, rows, (float*)y, ws, p.workspace - 256, st, active),
                       name);

@@ -174,6 +174,33 @@ def gate_up_act(w: Weights, x: torch.Tensor, rows: int, y: torch.Tensor | None =
     return y
 
 
+def rms_norm(x: torch.Tensor, g: torch.Tensor, eps: float, rows: int, y: torch.Tensor | None = None,
+             stream=None) -> torch.Tensor:
+    """RmsNorm of each row of x F32 [rows, n] (crates/kernels/src/reference/norm.rs:39-47)."""
+    n = g.numel()
+    _check_x(x, rows, n)
+    if y is None:
+        y = torch.empty(rows, n, dtype=torch.float32, device=x.device)
+    call("syn_rms_norm", x.data_ptr(), g.data_ptr(), rows, n, C.c_float(eps), y.data_ptr(), _stream(stream))
+    return y
+
+
+def logits(head: Weights, g: torch.Tensor, eps: float, x: torch.Tensor, rows: int,
+           y: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Logits (crates/kernels/src/reference/linear.rs:118-161): each row of x [rows, hidden]
+    normalised by (g, eps), then y F32 [rows, vocab] = head x as the Gemv op computes it."""
+    _check_x(x, rows, head.k_in)
+    if y is None:
+        y = torch.empty(rows, head.n_out, dtype=torch.float32, device=x.device)
+    need = C.c_uint64()
+    call("syn_logits_workspace_bytes", head.layout, int(head.ty), rows, head.n_out, head.k_in, C.byref(need))
+    ws = torch.empty(max(need.value, 256), dtype=torch.uint8, device=x.device)
+    call("syn_logits", head.layout, int(head.ty), head.bytes.data_ptr(), head.bytes.numel(), head.n_out,
+         head.k_in, g.data_ptr(), C.c_float(eps), x.data_ptr(), rows, y.data_ptr(), ws.data_ptr(), ws.numel(),
+         _stream(stream))
+    return y
+
+
 class GemvBatch:
     """Up to 8 independent single-row Q4_K Gemv ops launched together (one batched Q8_K
     quantization, one grouped GEMV): each y[i] equals gemv(ws[i], x[i], 1) bit for bit.  The
