@@ -29,44 +29,12 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x,
     const bool live = blk < nblk;
     float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) v4 = reinterpret_cast<const float4*>(x + blk * 32)[sub];
-    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    int bad = !(finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]));
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float a = __builtin_fabsf(v[i]);
-        amax = amax > a ? amax : a;
-    }
-#pragma unroll
-    for (int off = 4; off >= 1; off >>= 1) {
-        float o = __shfl_xor(amax, off);
-        amax = amax > o ? amax : o;
-        bad |= __shfl_xor(bad, off);
-    }
-    int q[4] = {0, 0, 0, 0};
-    float dused;
-    if (bad) {
-        dused = __builtin_nanf("");
-    } else {
-        const float d = amax / 127.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        if (finite_f(id)) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) q[i] = (int)__builtin_rintf(v[i] * id);
-        }
-        dused = f16_to_f32(f16_bits(d));
-    }
+    const Q8_0Lane r = q8_0_block_lane(v4);
     if (!live) return;
-    uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
-                      ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
-    reinterpret_cast<uint32_t*>(codes + blk * 32)[sub] = packed;
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
+    reinterpret_cast<uint32_t*>(codes + blk * 32)[sub] = r.packed;
     if (sub == 0) {
-        sums[blk] = s;
-        dout[blk] = dused;
+        sums[blk] = r.sum;
+        dout[blk] = r.d;
     }
 }
 

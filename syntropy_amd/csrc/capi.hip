@@ -746,12 +746,50 @@ MoeWs moe_ws(uint32_t n_experts, uint32_t top_k, uint32_t hidden, uint32_t inter
     return m;
 }
 
+// Q8_0 experts: the workspace after the packing's words: the entries' x rows in Q8_0 (codes
+// [entries][hidden], scales [entries][hidden / 32]), h F32 [entries][inter], h in Q8_0.
+struct MoeQ8Ws {
+    uint64_t xq, xd, h, hq, hd, bytes;
+};
+MoeQ8Ws moe_q8_ws(const MoeWs& head, uint32_t top_k, uint32_t hidden, uint32_t inter, uint32_t rows) {
+    MoeQ8Ws m{};
+    const uint64_t ent = (uint64_t)rows * top_k;
+    uint64_t o = head.xq;
+    m.xq = o;
+    o = syn::align_up(o + ent * hidden, 256);
+    m.xd = o;
+    o = syn::align_up(o + 4 * ent * (hidden / 32), 256);
+    m.h = o;
+    o = syn::align_up(o + 4 * ent * inter, 256);
+    m.hq = o;
+    o = syn::align_up(o + ent * inter, 256);
+    m.hd = o;
+    o = syn::align_up(o + 4 * ent * (inter / 32), 256);
+    m.bytes = o;
+    return m;
+}
+
+// The packing's words of the workspace (offsets, slots, the error word), as moe_ws lays them.
+MoeWs moe_head(uint32_t n_experts, uint32_t top_k, uint32_t rows) {
+    MoeWs m{};
+    uint64_t o = 0;
+    m.offsets = o;
+    o = syn::align_up(o + 4ull * (n_experts + 1), 256);
+    m.slots = o;
+    o = syn::align_up(o + 4ull * rows * top_k, 256);
+    m.err = o;
+    o = syn::align_up(o + 8, 256);
+    m.xq = o;
+    return m;
+}
+
 int check_moe_shape(const char* W, uint32_t n_experts, uint32_t top_k, uint32_t hidden,
-                    uint32_t inter, uint32_t rows) {
+                    uint32_t inter, uint32_t rows, int32_t wtype = SYN_Q4_K) {
     if (n_experts == 0 || n_experts > 256) return fail(SYN_E_UNSUPPORTED, "%s: n_experts %u (1..256)", W, n_experts);
     if (top_k == 0 || top_k > n_experts || top_k > 32) return fail(SYN_E_UNSUPPORTED, "%s: top_k %u (1..min(n_experts, 32))", W, top_k);
-    if (hidden % 256 || inter % 256 || hidden == 0 || inter == 0)
-        return fail(SYN_E_INVALID, "%s: hidden %u and inter %u must be whole 256-weight blocks", W, hidden, inter);
+    const uint32_t be = wtype == SYN_Q8_0 ? 32 : 256;
+    if (hidden % be || inter % be || hidden == 0 || inter == 0)
+        return fail(SYN_E_INVALID, "%s: hidden %u and inter %u must be whole %u-weight blocks", W, hidden, inter, be);
     if (hidden > 65536 || inter > 65536) return fail(SYN_E_UNSUPPORTED, "%s: hidden/inter above 65536", W);
     if ((uint64_t)rows * top_k > 65536) return fail(SYN_E_UNSUPPORTED, "%s: rows * top_k above 65536", W);
     // the expert kernels address the entries' codes with 32-bit offsets
@@ -799,12 +837,63 @@ SYN_EXPORT int syn_moe_grouped_workspace_bytes(int32_t wtype, uint32_t n_experts
                                                uint32_t hidden, uint32_t inter, uint32_t rows,
                                                uint64_t* bytes) {
     const char* W = "syn_moe_grouped_workspace_bytes";
-    if (wtype != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: expert weight type %d (Q4_K)", W, wtype);
-    if (int rc = check_moe_shape(W, n_experts, top_k, hidden, inter, rows)) return rc;
+    if (wtype != SYN_Q4_K && wtype != SYN_Q8_0)
+        return fail(SYN_E_UNSUPPORTED, "%s: expert weight type %d (Q4_K or Q8_0)", W, wtype);
+    if (int rc = check_moe_shape(W, n_experts, top_k, hidden, inter, rows, wtype)) return rc;
     if (!bytes) return fail(SYN_E_INVALID, "%s: null output", W);
-    *bytes = moe_ws(n_experts, top_k, hidden, inter, rows).bytes;
+    *bytes = wtype == SYN_Q8_0 ? moe_q8_ws(moe_head(n_experts, top_k, rows), top_k, hidden, inter, rows).bytes
+                               : moe_ws(n_experts, top_k, hidden, inter, rows).bytes;
     return SYN_OK;
 }
+
+namespace {
+
+// MoeGrouped over Q8_0 experts: pack, Q8_0 of the entries' rows, gate/up + silu, Q8_0 of h, down.
+int moe_grouped_q8_0(const void* gate, const void* up, const void* down, uint64_t expert_bytes_each,
+                     uint32_t n_experts, uint32_t top_k, uint32_t hidden, uint32_t inter, const float* x,
+                     const int32_t* ids, const int32_t* site, uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
+                     uint32_t* status, void* stream, const uint32_t* active, uint32_t* report) {
+    const char* W = "syn_moe_grouped";
+    const uint64_t mat = (uint64_t)inter * (hidden / 32) * 34;  // gate/up; down is the same size
+    if (expert_bytes_each < mat * n_experts)
+        return fail(SYN_E_INVALID, "%s: each stacked matrix holds %llu bytes, the experts need %llu", W,
+                    (unsigned long long)expert_bytes_each, (unsigned long long)(mat * n_experts));
+    const MoeWs head = moe_head(n_experts, top_k, rows);
+    const MoeQ8Ws m = moe_q8_ws(head, top_k, hidden, inter, rows);
+    if (ws_bytes < m.bytes)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)m.bytes);
+    if (!gate || !up || !down || !x || !ids || !out || !ws) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (site && !aligned(site, 4)) return fail(SYN_E_INVALID, "%s: the site mask must be 4-byte aligned", W);
+    if (!aligned(gate, 2) || !aligned(up, 2) || !aligned(down, 2) || !aligned(x, 16) || !aligned(ws, 256) ||
+        !aligned(out, 4))
+        return fail(SYN_E_INVALID, "%s: x must be 16-byte, the workspace 256-byte aligned", W);
+    uint8_t* base = (uint8_t*)ws;
+    uint32_t* offsets = (uint32_t*)(base + head.offsets);
+    uint32_t* slots = (uint32_t*)(base + head.slots);
+    uint32_t* err = (uint32_t*)(base + head.err);
+    const int ent = (int)(rows * top_k);
+    hipStream_t st = (hipStream_t)stream;
+    int8_t* xq = (int8_t*)(base + m.xq);
+    float* xd = (float*)(base + m.xd);
+    float* h = (float*)(base + m.h);
+    int8_t* hq = (int8_t*)(base + m.hq);
+    float* hd = (float*)(base + m.hd);
+    syn::launch_moe_pack(ids, ent, (int)n_experts, offsets, slots, err, st, active, (int)top_k, site, report);
+    syn::launch_moe_gather_q8_0(x, slots, ent, (int)top_k, (int)hidden, err, xq, xd, 1, offsets + n_experts, st);
+    syn::launch_moe_q8(0, (const uint8_t*)gate, (const uint8_t*)up, mat, (int)n_experts, (int)inter, (int)hidden,
+                       offsets, slots, err, xq, xd, h, st);
+    syn::launch_moe_gather_q8_0(h, slots, ent, (int)top_k, (int)inter, err, hq, hd, 0, offsets + n_experts, st);
+    syn::launch_moe_q8(1, (const uint8_t*)down, nullptr, mat, (int)n_experts, (int)hidden, (int)inter, offsets,
+                       slots, err, hq, hd, out, st);
+    if (status) {
+        hipError_t e = hipMemcpyAsync(status, err, 4, hipMemcpyDeviceToDevice, st);
+        if (e != hipSuccess) return fail(SYN_E_DEVICE, "%s: status copy: %s", W, hipGetErrorString(e));
+    }
+    return check_launch(W);
+}
+
+}  // namespace
 
 int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const void* down,
                                uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k,
@@ -812,9 +901,13 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
                                const int32_t* site, uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
                                uint32_t* status, void* stream, const uint32_t* active, uint32_t* report) {
     const char* W = "syn_moe_grouped";
-    if (wtype != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: expert weight type %d (Q4_K)", W, wtype);
-    if (int rc = check_moe_shape(W, n_experts, top_k, hidden, inter, rows)) return rc;
+    if (wtype != SYN_Q4_K && wtype != SYN_Q8_0)
+        return fail(SYN_E_UNSUPPORTED, "%s: expert weight type %d (Q4_K or Q8_0)", W, wtype);
+    if (int rc = check_moe_shape(W, n_experts, top_k, hidden, inter, rows, wtype)) return rc;
     if (rows == 0) return SYN_OK;
+    if (wtype == SYN_Q8_0)
+        return moe_grouped_q8_0(gate, up, down, expert_bytes_each, n_experts, top_k, hidden, inter, x, ids, site,
+                                rows, out, ws, ws_bytes, status, stream, active, report);
     const uint64_t mat = (uint64_t)inter * (hidden / 256) * 144;  // gate/up; down is the same size
     if (expert_bytes_each < mat * n_experts)
         return fail(SYN_E_INVALID, "%s: each stacked matrix holds %llu bytes, the experts need %llu", W,

@@ -195,6 +195,54 @@ SYN_DEV Q8KLane q8k_block_lane(const float* __restrict__ xb, int lane) {
     return r;
 }
 
+// Q8_0 of one 32-value block (crates/kernels-cpu/src/gemv/act.rs:323-342): d = amax / 127,
+// id = 1 / d, codes rounded to nearest even, the scale used the F16-rounded d; a non-finite
+// block gets scale NaN and codes 0.  Eight lanes per block (every lane of the group of eight
+// active): `sub` = lane & 7 holds values 4 sub .. 4 sub + 3 and gets their packed codes, the
+// block's code sum and the scale.
+struct Q8_0Lane {
+    uint32_t packed;
+    int sum;
+    float d;
+};
+SYN_DEV Q8_0Lane q8_0_block_lane(float4 v4) {
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    int bad = !(finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]));
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = __builtin_fabsf(v[i]);
+        amax = amax > a ? amax : a;
+    }
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(amax, off);
+        amax = amax > o ? amax : o;
+        bad |= __shfl_xor(bad, off);
+    }
+    int q[4] = {0, 0, 0, 0};
+    Q8_0Lane r;
+    if (bad) {
+        r.d = __builtin_nanf("");
+    } else {
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        if (finite_f(id)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = (int)__builtin_rintf(v[i] * id);
+        }
+        r.d = f16_to_f32(f16_bits(d));
+    }
+    r.packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
+               ((uint32_t)(q[3] & 0xFF) << 24);
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    r.sum = s;
+    return r;
+}
+
 // The same block in the row layout of the GEMV workspace: codes in order, the eight 32-value
 // sums, the scale.
 SYN_DEV void q8k_block_wave(const float* __restrict__ xb, int8_t* __restrict__ codes,

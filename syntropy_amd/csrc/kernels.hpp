@@ -38,6 +38,13 @@ void launch_gemv_q4k_batch_f32(const uint8_t* const* W, int np, const int* n_out
 void launch_q4k_x8(const uint8_t* src, uint8_t* dst, uint64_t nblocks, int inverse, hipStream_t stream);
 void launch_act_quant_batch(int np, const float* const* x, const int* k, uint8_t* const* ws,
                             hipStream_t stream);
+// moe_q8.hip: MoeGrouped over Q8_0 experts (Q8_0 entries' rows, gate/up + silu, down)
+void launch_moe_gather_q8_0(const float* x, const uint32_t* slots, int nentries, int top_k, int k,
+                            const uint32_t* err, int8_t* codes, float* d, int gather, const uint32_t* total,
+                            hipStream_t stream);
+void launch_moe_q8(int mode, const uint8_t* w0, const uint8_t* w1, uint64_t mat_bytes, int n_experts, int n_out,
+                   int k, const uint32_t* offsets, const uint32_t* slots, const uint32_t* err, const int8_t* aq,
+                   const float* ad, float* y, hipStream_t stream);
 // norm.hip: RmsNorm rows of at most NORM_MAX_COLS values
 constexpr int NORM_MAX_COLS = 16384;
 void launch_rms_norm(const float* x, const float* g, int rows, int n, float eps, float* y, hipStream_t stream,

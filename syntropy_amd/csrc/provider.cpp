@@ -462,7 +462,8 @@ bool plan_of(const Key& k, const Shape& s, Plan& p) {
         return true;
     }
     case Op::MoeGrouped: {
-        if (k.weight != SYN_Q4_K || k.n_schemes > 3 || s.dims.size() != 4) return false;
+        // Q4_K or Q8_0 experts (crates/kernels-cpu/src/moe/entry.rs:50-55)
+        if ((k.weight != SYN_Q4_K && k.weight != SYN_Q8_0) || k.n_schemes > 3 || s.dims.size() != 4) return false;
         uint64_t ws = 0;
         if (syn_moe_grouped_workspace_bytes(k.weight, s.dims[0], s.dims[1], s.dims[2], s.dims[3],
                                             s.rows, &ws) != SYN_OK)
@@ -470,8 +471,8 @@ bool plan_of(const Key& k, const Shape& s, Plan& p) {
         p.weight = k.weight;
         for (int i = 0; i < 4; ++i) p.dims[i] = s.dims[i];
         p.workspace = round_up(ws, 64) + 256;
-        p.max_block = 256;
-        p.act_in = 3;
+        p.max_block = k.weight == SYN_Q4_K ? 256 : 32;
+        p.act_in = k.weight == SYN_Q4_K ? 3 : 2;
         return true;
     }
     case Op::MoeRoute: {
@@ -533,6 +534,7 @@ std::string ops_json() {
             }
     out +=
         "{\"op\":\"MoeGrouped\",\"schemes\":[{\"Ggml\":\"Q4_K\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
+        "{\"op\":\"MoeGrouped\",\"schemes\":[{\"Ggml\":\"Q8_0\"},{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
         "{\"op\":{\"MoeRoute\":{\"norm\":\"Softmax\"}},\"schemes\":[{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0},"
         "{\"op\":\"MoeCombine\",\"schemes\":[{\"Plain\":\"F32\"}],\"layout\":0,\"variant\":0}"
         "]";
@@ -793,7 +795,8 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         // input 2, the site mask: packed I32 [n_experts, 1], nonzero = computed here
         const uint8_t* site = a.n_inputs == 3 ? tensor(c, a.inputs[2], 7, e, 1, 1, 4, "MoeGrouped site") : nullptr;
         uint8_t* out = tensor(c, a.outputs[0], 0, rows, top_k, hidden, 4, "MoeGrouped out");
-        const uint64_t mat = (uint64_t)inter * (hidden / 256) * 144 * e;
+        const uint64_t mat = p.weight == SYN_Q4_K ? (uint64_t)inter * (hidden / 256) * 144 * e
+                                                  : (uint64_t)inter * (hidden / 32) * 34 * e;
         const SynBufferView& g = weight(a, 0, mat, "MoeGrouped gate");
         const SynBufferView& u = weight(a, 1, mat, "MoeGrouped up");
         const SynBufferView& d = weight(a, 2, mat, "MoeGrouped down");

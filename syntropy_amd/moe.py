@@ -42,9 +42,9 @@ class Experts:
 
     def check(self, s: MoeShape):
         ty = WeightType(self.ty)
-        if ty is not WeightType.Q4K:
-            raise MoeError("MoeGrouped on the GPU takes Q4_K experts")
-        need = s.n_experts * s.inter * (s.hidden // 256) * 144
+        if ty not in (WeightType.Q4K, WeightType.Q8_0):
+            raise MoeError("MoeGrouped takes Q4_K or Q8_0 experts (crates/kernels-cpu/src/moe/entry.rs:50-55)")
+        need = s.n_experts * s.inter * (s.hidden // ty.block_elems()) * ty.block_bytes()
         for name, t in (("gate", self.gate), ("up", self.up), ("down", self.down)):
             if t.dtype != torch.uint8 or t.numel() != need:
                 raise MoeError(f"`{name}` holds {t.numel()} bytes, the experts need {need}")
@@ -101,7 +101,8 @@ def moe_grouped(s: MoeShape, experts: Experts, x: torch.Tensor, ids: torch.Tenso
     if out is None:
         out = torch.empty(rows, s.top_k, s.hidden, dtype=torch.float32, device=x.device)
     if ws is None:
-        ws = torch.empty(max(workspace_bytes(s, rows), 256), dtype=torch.uint8, device=x.device)
+        ws = torch.empty(max(workspace_bytes(s, rows, WeightType(experts.ty)), 256), dtype=torch.uint8,
+                         device=x.device)
     call("syn_moe_grouped", int(experts.ty), experts.gate.data_ptr(), experts.up.data_ptr(),
          experts.down.data_ptr(), experts.gate.numel(), s.n_experts, s.top_k, s.hidden, s.inter,
          x.data_ptr(), ids.data_ptr(), site.data_ptr() if site is not None else None, rows,
@@ -126,7 +127,7 @@ class MoeLayer:
 
     def __init__(self, s: MoeShape, router: torch.Tensor, experts: Experts, max_rows: int):
         self.s, self.router, self.experts = s, router, experts
-        self.ws = torch.empty(max(workspace_bytes(s, max_rows), 256), dtype=torch.uint8,
+        self.ws = torch.empty(max(workspace_bytes(s, max_rows, WeightType(experts.ty)), 256), dtype=torch.uint8,
                               device=router.device)
         self.max_rows = max_rows
 

@@ -161,7 +161,7 @@ def test_build_and_ops_json(pr):
                ('{"Ggml": "F16"}', 0), ('{"Ggml": "BF16"}', 0), ('{"Plain": "F16"}', 0), ('{"Plain": "BF16"}', 0)]
     dense = {(op, w, l) for op in ('"Gemv"', '"Gemm"', '"Logits"', '{"GateUpAct": {"act": "Silu"}}')
              for w, l in weights}
-    assert got == dense | {('"MoeGrouped"', '{"Ggml": "Q4_K"}', 0),
+    assert got == dense | {('"MoeGrouped"', '{"Ggml": "Q4_K"}', 0), ('"MoeGrouped"', '{"Ggml": "Q8_0"}', 0),
                            ('{"MoeRoute": {"norm": "Softmax"}}', '{"Plain": "F32"}', 0),
                            ('"MoeCombine"', '{"Plain": "F32"}', 0)}
     assert len(ops) == len(got)
