@@ -38,6 +38,8 @@
  *                    byte example of moe/tests.rs:938-961; the route list against a brute-force
  *                    count of the ids
  */
+/* The weight quantizers restate ggml (Copyright (c) 2023-2026 The ggml authors, MIT License;
+ * the notice is in THIRD_PARTY.md at the repository root). */
 #include "oracle.h"
 
 #include <math.h>

@@ -1,5 +1,8 @@
 // Weight quantizers and exact dequantizers on gfx950.
 //
+// The quantizers follow ggml (Copyright (c) 2023-2026 The ggml authors, MIT License; the notice
+// is in THIRD_PARTY.md at the repository root).
+//
 // The quantizers are ggml's reference routines (third_party/ggml/src/ggml-quants.c:113-140
 // quantize_row_q4_0_ref, :276-297 quantize_row_q8_0_ref, :799-878 make_qkx2_quants,
 // :1458-1528 quantize_row_q4_K_ref), one block per thread, operation for operation: every
