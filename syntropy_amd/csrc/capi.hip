@@ -585,6 +585,17 @@ int syn_gate_up_act_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
                     (unsigned long long)ws_bytes, (unsigned long long)need);
     if (!ws || !aligned(ws, 256) || !y || !aligned(y, 4))
         return fail(SYN_E_INVALID, "%s: the workspace must be 256-byte and y 4-byte aligned", W);
+    if (layout == SYN_LAYOUT_X8 && wtype == SYN_Q4_K && rows == 1 && syn::gemv_q4k_batch_fusable((int)k_in)) {
+        // one launch: the row quantized in every workgroup, gate and up rows side by side, silu(g) u
+        const uint64_t need_w = 2ull * n_out * (k_in / 256) * 144;
+        if (!w || !x) return fail(SYN_E_INVALID, "%s: null operand", W);
+        if (w_bytes < need_w)
+            return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
+                        (unsigned long long)w_bytes, (unsigned long long)need_w);
+        if (!aligned(w, 16) || !aligned(x, 16)) return fail(SYN_E_INVALID, "%s: w and x must be 16-byte aligned", W);
+        syn::launch_gate_up_q4k_f32((const uint8_t*)w, (int)n_out, (int)k_in, x, y, (hipStream_t)stream, active);
+        return check_launch(W);
+    }
     uint64_t g = 0;
     (void)syn_gemv_layout_workspace_bytes(layout, wtype, rows, k_in, &g);
     float* y2 = (float*)((uint8_t*)ws + syn::align_up(g, 256));

@@ -303,13 +303,18 @@ constexpr int FUSE_PIECES = 2;
 template <int LAYOUT, int FUSE>
 constexpr int dec_occupancy() { return FUSE ? 4 : 6; }
 
-template <int LAYOUT, int FUSE>
+// GATED = 1 (GateUpAct{Silu}, one fused launch): the matrix stacks n_out gate rows, then n_out
+// up rows; the first half of the wavefronts computes gate rows and the second half the same up
+// rows, and y[i] = silu(g_i) * u_i (crates/kernels/src/reference/linear.rs:75-112 with the
+// Gemv values, the product rounded once) is formed after one LDS exchange.
+template <int LAYOUT, int FUSE, int GATED>
 __global__ __launch_bounds__(64 * dec_waves<LAYOUT>())
 __attribute__((amdgpu_waves_per_eu(dec_occupancy<LAYOUT, FUSE>())))
 void k_gemv_q4k_batch(DecBatch bt) {
     if (active_rows(bt.active, 0, 1) == 0) return;  // a step with no active row
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int WAVES = dec_waves<LAYOUT>();
+    constexpr int RW = GATED ? WAVES / 2 : WAVES;  // wavefronts per set of output rows
     int p = 0;
     while (p + 1 < bt.np && (int)blockIdx.x >= bt.wg_begin[p + 1]) ++p;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -317,7 +322,9 @@ void k_gemv_q4k_batch(DecBatch bt) {
     const int n_out = bt.n_out[p], nb = bt.nb[p];
     const int P = lanes_per_row(nb);
     const int rows_per_wave = 64 / P;
-    const int row = (((int)blockIdx.x - bt.wg_begin[p]) * WAVES + wave) * rows_per_wave + lane / P;
+    const int row = (((int)blockIdx.x - bt.wg_begin[p]) * RW + wave % RW) * rows_per_wave + lane / P;
+    const bool up_half = GATED && wave >= RW;
+    const int mrow = up_half ? n_out + row : row;  // the matrix row
     const int b = lane % P;
     const bool ok = row < n_out && b < nb;
     static_assert(!FUSE || LAYOUT == LAYOUT_X8, "the fused form reads X8 weights");
@@ -350,14 +357,14 @@ void k_gemv_q4k_batch(DecBatch bt) {
     // the lane's block
     v4u A[9];
     if constexpr (LAYOUT == LAYOUT_X8) {
-        const uint64_t nblocks = (uint64_t)n_out * (uint64_t)nb;
-        const uint64_t g = ok ? (uint64_t)row * nb + b : 0;
+        const uint64_t nblocks = (uint64_t)(GATED ? 2 : 1) * n_out * (uint64_t)nb;
+        const uint64_t g = ok ? (uint64_t)mrow * nb + b : 0;
         const uint8_t* src = W + x8_chunk_offset(g, 0, nblocks);
         const uint32_t step = 16u * x8_group_blocks(g, nblocks);
 #pragma unroll
         for (int i = 0; i < 9; ++i) A[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(src + step * i));
     } else {
-        const uint8_t* src = ok ? W + (int64_t)row * nb * 144 + (int64_t)b * 144 : W;
+        const uint8_t* src = ok ? W + (int64_t)mrow * nb * 144 + (int64_t)b * 144 : W;
 #pragma unroll
         for (int i = 0; i < 9; ++i) A[i] = *reinterpret_cast<const v4u*>(src + 16 * i);
     }
@@ -384,9 +391,9 @@ void k_gemv_q4k_batch(DecBatch bt) {
     float* terms = reinterpret_cast<float*>(lds + align_up(q4k_dec_lds(nb), 16)) + wave * 64;
     terms[lane] = ok ? t : 0.0f;
     wave_lds_sync();
+    float acc = 0.0f;
     if (b == 0 && row < n_out) {
         const float4* tv = reinterpret_cast<const float4*>(terms + lane);
-        float acc = 0.0f;
         for (int q = 0; q < P / 4; ++q) {
             const float4 v = tv[q];
             acc = acc + v.x;
@@ -394,7 +401,14 @@ void k_gemv_q4k_batch(DecBatch bt) {
             acc = acc + v.z;
             acc = acc + v.w;
         }
-        bt.y[p][row] = acc;
+        if constexpr (!GATED) bt.y[p][row] = acc;
+    }
+    if constexpr (GATED) {
+        // the gate sums to the up wavefronts holding the same rows
+        float* gsum = reinterpret_cast<float*>(lds + align_up(q4k_dec_lds(nb), 16)) + WAVES * 64;
+        if (!up_half && b == 0) gsum[(wave % RW) * 64 + lane] = acc;
+        lds_barrier();
+        if (up_half && b == 0 && row < n_out) bt.y[p][row] = ref_silu(gsum[(wave % RW) * 64 + lane]) * acc;
     }
 }
 
@@ -437,11 +451,12 @@ void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* w
                   reinterpret_cast<const int32_t*>(ws + L.sums), y, stream);
 }
 
-template <int LAYOUT, int FUSE>
+template <int LAYOUT, int FUSE, int GATED = 0>
 static void launch_batch(int np, const uint8_t* const* W, const int* n_out, const int* k,
                          const uint8_t* const* ws, const float* const* x, float* const* y,
                          hipStream_t stream, const uint32_t* active = nullptr) {
     constexpr int WAVES = dec_waves<LAYOUT>();
+    constexpr int RW = GATED ? WAVES / 2 : WAVES;
     DecBatch bt{};
     bt.np = np;
     bt.active = active;
@@ -455,15 +470,15 @@ static void launch_batch(int np, const uint8_t* const* W, const int* n_out, cons
         bt.nb[p] = k[p] / 256;
         bt.wg_begin[p] = wg;
         const int nb = bt.nb[p];
-        const int rows_per_wg = WAVES * (64 / (nb <= 16 ? 16 : nb <= 32 ? 32 : 64));
+        const int rows_per_wg = RW * (64 / (nb <= 16 ? 16 : nb <= 32 ? 32 : 64));
         wg += (n_out[p] + rows_per_wg - 1) / rows_per_wg;
         if (nb > max_nb) max_nb = nb;
     }
     bt.wg_begin[np] = wg;
     if (wg == 0) return;
-    // the activation row, then 64 fold terms per wavefront
-    hipLaunchKernelGGL((k_gemv_q4k_batch<LAYOUT, FUSE>), dim3(wg), dim3(64 * WAVES),
-                       align_up(q4k_dec_lds(max_nb), 16) + WAVES * 64 * 4, stream, bt);
+    // the activation row, then 64 fold terms per wavefront (and the gate sums when GATED)
+    hipLaunchKernelGGL((k_gemv_q4k_batch<LAYOUT, FUSE, GATED>), dim3(wg), dim3(64 * WAVES),
+                       align_up(q4k_dec_lds(max_nb), 16) + (GATED ? 2 : 1) * WAVES * 64 * 4, stream, bt);
 }
 
 void launch_gemv_q4k_batch(int layout, int np, const uint8_t* const* W, const int* n_out, const int* k,
@@ -480,6 +495,11 @@ void launch_gemv_q4k_batch_f32(const uint8_t* const* W, int np, const int* n_out
                                const float* const* x, float* const* y, hipStream_t stream,
                                const uint32_t* active) {
     launch_batch<LAYOUT_X8, 1>(np, W, n_out, k, nullptr, x, y, stream, active);
+}
+
+void launch_gate_up_q4k_f32(const uint8_t* W, int n, int k, const float* x, float* y, hipStream_t stream,
+                            const uint32_t* active) {
+    launch_batch<LAYOUT_X8, 1, 1>(1, &W, &n, &k, nullptr, &x, &y, stream, active);
 }
 
 // ---- the x8 repack: a permutation of whole 16-byte chunks --------------------------------------

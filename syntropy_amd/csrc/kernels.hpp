@@ -31,6 +31,9 @@ void launch_gemv_float(int ty, const uint8_t* W, int n_out, int k, const float* 
 void launch_silu_mul(const float* y2, int rows, int n, float* y, hipStream_t stream, const uint32_t* active = nullptr);
 // The same over X8 weights with the F32 rows quantized inside the grouped launch (k <= 16384).
 bool gemv_q4k_batch_fusable(int k);
+// GateUpAct{Silu} at one row over a stacked [gate; up] X8 matrix of 2 n rows: y[i] = silu(g_i) * u_i
+void launch_gate_up_q4k_f32(const uint8_t* W, int n, int k, const float* x, float* y, hipStream_t stream,
+                            const uint32_t* active = nullptr);
 void launch_gemv_q4k_batch_f32(const uint8_t* const* W, int np, const int* n_out, const int* k,
                                const float* const* x, float* const* y, hipStream_t stream,
                                const uint32_t* active = nullptr);

@@ -342,6 +342,12 @@ class Provider:
     def record(self, ctx: int, s: int, e: int):
         self._ok("record", self.vt.record(self.vt.slf, ctx, s, e), ctx)
 
+    def elapsed(self, ctx: int, start: int, end: int):
+        """Nanoseconds between two recorded events, or None when they hold no timing."""
+        present, ns = u32(0), u64(0)
+        self._ok("elapsed", self.vt.elapsed(self.vt.slf, ctx, start, end, C.byref(present), C.byref(ns)), ctx)
+        return ns.value if present.value else None
+
     def poll(self, ctx: int, e: int) -> bool:
         d = u32(0)
         self._ok("poll", self.vt.poll(self.vt.slf, ctx, e, C.byref(d)), ctx)

@@ -346,6 +346,21 @@ def test_gate_up_act_x8_layout(S):
         assert_same(got, o.gate_up_act(o.Q4_K, w, n, k, x, rows, threads=8), f"x8 rows {rows}")
 
 
+@pytest.mark.parametrize("n,k", [(14336, 4096), (37, 4096), (500, 14336), (129, 8192), (3, 256)])
+def test_gate_up_act_x8_one_row_fused(S, n, k):
+    """One row over X8 weights runs gate, up and silu(g) u in one launch (the gate and up rows of
+    an output side by side): the Llama-3-8B FFN shape, ragged row counts, and 16-, 32- and
+    64-lane rows."""
+    from test_gpu_gemm import random_q4k
+    rs = np.random.default_rng(n + k)
+    w = random_q4k(rs, 2 * n, k)
+    x = o.normal(0x6A7E + n, 1.0, k)
+    W = S.repack(S.Weights(S.WeightType.Q4K, dev(w), 2 * n, k))
+    announce(f"gate_up_act x8 fused n={n} k={k}")
+    got = host(S.gate_up_act(W, dev(x), 1))
+    assert_same(got, o.gate_up_act(o.Q4_K, w, n, k, x, 1, threads=16), "fused gate_up_act")
+
+
 # ---- F16 / BF16 weights: 32 FMA accumulators and the halving fold (portable.rs:30-45) ----------
 @pytest.mark.parametrize("ty", [o.F16, o.BF16])
 @pytest.mark.parametrize("rows,n_out,k", [(1, 4096, 4096), (3, 1000, 1024), (9, 64, 4096),
