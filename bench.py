@@ -3,47 +3,56 @@
 
 Headline workload: one Q4_K decode layer's matmuls at Llama-3-8B shapes, batch 1 (QKV
 6144x4096, O 4096x4096, gate and up 14336x4096, down 4096x14336).  One step quantizes each
-GEMV's F32 activation row to Q8_K and runs the five GEMVs: the reference's `Gemv` op five
-times.  Weights are N(0, 0.02) quantized by the GPU Q4_K packer (byte-identical to ggml's),
-then repacked once to the X8 layout (the provider's repack: a permutation of the bytes), in
-COPIES distinct copies that the steps rotate through, so the weights come from HBM and not
-from the 256 MB Infinity Cache.
+GEMV's F32 activation row to Q8_K and runs the five GEMVs.  Weights are N(0, 0.02) quantized by
+the GPU Q4_K packer (byte-identical to ggml's), then repacked once to the X8 layout (the
+provider's repack: a permutation of the bytes), in COPIES distinct copies that the steps rotate
+through, so the weights come from HBM and not from the 256 MB Infinity Cache.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only layer|copy] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only PART] [--no-cpu]
 
-Prints one JSON line: whole-step weight GB/s (value), the roofline of the GEMV kernel from
-HIP events on its stream, and the CPU oracle timed on this host's cores; beside it the MoE layer
-at 64 decode tokens ("moe") and the 2048-token prefill ("prefill": the dense GEMMs on the matrix
-cores and the skewed MoE layer).
+Prints one JSON line: whole-step weight GB/s (value), the roofline of the GEMV kernel from HIP
+events on its stream, and the CPU oracle timed on this host's cores; beside it:
+  * provider_path: the same layer as the reference's executor issues it through the provider
+    table (Gemv QKV, Gemv O, GateUpAct over the stacked gate/up matrix, Gemv down), captured once
+    per weight copy and replayed;
+  * cfg1 (Q4_0 4096x4096 at one row), cfg2 (Q8_0 14336x4096 at 1, 8, 32 and 128 rows) and
+    rows_2_8 (Q4_K at 2, 4 and 8 rows against one row);
+  * moe (the MoE layer at 64 decode tokens) and prefill (the 2048-token dense GEMMs on the matrix
+    cores and the skewed MoE layer).
+--only runs one part (for the profiler); `copy` and `calib` run the counter calibration kernels.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
-
-import numpy as np
 import os
+import subprocess
 import sys
 import time
+
+import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "Q4_K GEMV weight GB/s (% HBM peak); MoE layer tokens/s at 64-token decode"
 HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0
 LAYER = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate", 14336, 4096), ("up", 14336, 4096),
          ("down", 4096, 14336)]
-Q4K = 12
+Q4K, Q8_0, Q4_0 = 12, 8, 2
 COPIES = 5
+MALL_BYTES = 256 << 20
+PARTS = ["layer", "provider", "cfgs", "rows", "moe", "prefill"]
 
 
 def q4k_bytes(n_out, k):
     return n_out * (k // 256) * 144
 
 
-def act_bytes(k):
-    # Q8_K codes + one F32 scale per 256 + one I32 sum per 32, read by the GEMV
-    return k + 4 * (k // 256) + 4 * (k // 32)
+def row_bytes(ty, k):
+    return {Q4K: k // 256 * 144, Q8_0: k // 32 * 34, Q4_0: k // 32 * 18}[ty]
 
 
 def parse():
@@ -51,7 +60,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=["layer", "copy"], default=None)
+    p.add_argument("--only", choices=PARTS + ["copy", "calib"], default=None)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=8.0)
     p.add_argument("--no-moe", action="store_true")
@@ -59,6 +68,50 @@ def parse():
     return p.parse_args()
 
 
+def S_lib():
+    from syntropy_amd._lib import lib
+    return lib()
+
+
+def gpu_us(torch, fn, n):
+    """Average GPU time of fn(i) for i < n, launched back to back on the current stream: a spin
+    kernel first, so every launch is queued before the GPU reaches it and the event pair times
+    the kernels (launch gaps included), not the host's rate."""
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(4e7))
+    e0.record()
+    for i in range(n):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n * 1e3
+
+
+def host_info():
+    """This host's CPU as lscpu reports it, and the cores this process may use."""
+    info = {"cpus_visible": os.cpu_count(), "cpus_in_affinity": len(os.sched_getaffinity(0))}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        want = {"Model name": "model", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+                "Thread(s) per core": "threads_per_core", "CPU(s)": "cpus"}
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in want:
+                info[want[k.strip()]] = v.strip()
+        flags = next((ln for ln in out.splitlines() if ln.startswith("Flags:")), "")
+        info["isa"] = "avx512" if "avx512f" in flags else "avx2" if "avx2" in flags else "baseline"
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
+
+
+def cpu_threads():
+    # a one-GPU box's CPU share is 16 threads; no more than the process may use
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+# ---- the headline: the decode layer ---------------------------------------------------------------
 def build_layer(torch, S, seed_base):
     gen = torch.Generator(device="cuda")
     copies = []
@@ -71,10 +124,8 @@ def build_layer(torch, S, seed_base):
             del w
         copies.append(mats)
     gen.manual_seed(seed_base + 7)
-    xs = {name: torch.randn(k, generator=gen, device="cuda", dtype=torch.float32)
-          for name, _, k in LAYER}
+    xs = {name: torch.randn(k, generator=gen, device="cuda", dtype=torch.float32) for name, _, k in LAYER}
     ys = {name: torch.empty(n_out, device="cuda", dtype=torch.float32) for name, n_out, _ in LAYER}
-    import ctypes as C
     wss = {}
     for name, _, k in LAYER:
         need = C.c_uint64()
@@ -83,35 +134,93 @@ def build_layer(torch, S, seed_base):
     return copies, xs, ys, wss
 
 
-def run_step_batched(batch, stream):
-    """One decode layer as one grouped launch pair (batched Q8_K quantization + grouped GEMV)."""
-    batch(stream=stream)
-
-
-def run_step(S, mats, xs, ys, wss, stream, events=None):
+def run_step(S, mats, xs, ys, wss, stream):
     """One decode layer: five Gemv ops (F32 row in, Q8_K quantization fused, F32 row out)."""
-    for name, _, k in LAYER:
-        if events is not None:
-            events[name][0].record()
-        S.gemv(mats[name], xs[name], 1, y=ys[name], ws=wss[name], stream=stream)
-        if events is not None:
-            events[name][1].record()
-
-
-def S_lib():
-    from syntropy_amd._lib import lib
-    return lib()
-
-
-def cpu_baseline(torch, copies, xs, seconds):
-    """The oracle (C restatement of crates/kernels-cpu, multi-threaded by the reference's row
-    partition) over the same layer: bounded sample of `seconds` of repeated layers."""
-    from oracle import oracle as o
-    threads = min(16, os.cpu_count() or 1)
-    mats = copies[0]
-    # the oracle reads the GGUF order: undo the X8 repack on the host
-    w = {}
     for name, _, _ in LAYER:
+        S.gemv(mats[name], xs[name], 1, y=ys[name], ws=wss[name], stream=stream)
+
+
+def bench_layer(torch, S, a, copies, xs, ys, wss):
+    stream = torch.cuda.current_stream()
+    names = [name for name, _, _ in LAYER]
+    batches = [S.GemvBatch([c[n] for n in names], [xs[n] for n in names], [ys[n] for n in names])
+               for c in copies]
+    weight_bytes = sum(q4k_bytes(n, k) for _, n, k in LAYER)
+    # the layer's five Gemv ops as one grouped launch pair per step (syn_gemv_batch_layout)
+    for i in range(a.warmup):
+        batches[i % COPIES](stream=stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        batches[i % COPIES](stream=stream)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    value = weight_bytes * a.steps / dt / 1e9
+    # the same five ops launched one by one (one launch each, quantization fused)
+    for i in range(a.warmup):
+        run_step(S, copies[i % COPIES], xs, ys, wss, stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for i in range(a.steps):
+        run_step(S, copies[i % COPIES], xs, ys, wss, stream)
+    torch.cuda.synchronize()
+    dt_ops = time.perf_counter() - t1
+    nrep = max(20, min(a.steps, 100))
+    # the grouped GEMV launch (the dominant kernel) alone, back to back on its stream
+    for b in batches:
+        b.quantize(stream)
+    batch_us = gpu_us(torch, lambda i: batches[i % COPIES].gemv_quantized(stream), nrep)
+    per = {name: gpu_us(torch, lambda i, name=name: S.gemv(copies[i % COPIES][name], xs[name], 1, y=ys[name],
+                                                             ws=wss[name], stream=stream), nrep)
+           for name, _, _ in LAYER}
+    # algorithmic bytes of one grouped launch: the weights, each Q8_K row once (codes, 32-value
+    # sums, scales) and the F32 outputs
+    alg_bytes = sum(q4k_bytes(n, k) + k + k // 8 + k // 64 + 4 * n for _, n, k in LAYER)
+    achieved = alg_bytes / (batch_us * 1e-6) / 1e9
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "traffic_q4k_gemv_decode_layer.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+    return {
+        "value": round(value, 2),
+        "ms_per_step": round(dt / a.steps * 1e3, 5),
+        "config": {
+            "workload": "Q4_K decode layer matmuls, Llama-3-8B shapes, batch 1: QKV 6144x4096, "
+                        "O 4096x4096, gate/up 14336x4096, down 4096x14336; Q8_K act quant + "
+                        "5 GEMVs per step",
+            "launch": "grouped: one batched Q8_K quantization + one grouped GEMV (syn_gemv_batch_layout)",
+            "weight_layout": "X8 (runs of 8 Q4_K super-blocks stored chunk-major; repacked once at load)",
+            "weight_bytes_per_step": weight_bytes,
+            "weight_copies_rotated": COPIES,
+            "hbm_fraction_of_peak": round(value / HBM_PEAK_GBS, 4),
+            "one_op_per_launch_gbs": round(weight_bytes * a.steps / dt_ops / 1e9, 2),
+            "one_op_per_launch_us": {k: round(v, 3) for k, v in per.items()},
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_gemv_q4k_batch<X8> (syn_gemv_batch_quantized_layout: the grouped GEMV on Q8_K rows)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "traffic_source": "profiles/traffic_q4k_gemv_decode_layer.json (rocprofv3 --pmc FETCH_SIZE, "
+                              "WRITE_SIZE, scaled by the calibration kernels)",
+            "alg_bytes_per_launch": alg_bytes,
+            "avg_launch_us": round(batch_us, 3),
+        },
+    }
+
+
+def cpu_layer_baseline(copies, xs, seconds):
+    """The oracle (C restatement of crates/kernels-cpu, multi-threaded by the reference's row
+    partition) over the same layer: a bounded sample of `seconds` of repeated layers, then one
+    layer at one thread (a reference launch runs on the calling thread)."""
+    from oracle import oracle as o
+    threads = cpu_threads()
+    mats = copies[0]
+    w = {}
+    for name, _, _ in LAYER:  # the oracle reads the GGUF order: undo the X8 repack on the host
         b = mats[name].bytes.cpu().numpy()
         src = np.empty_like(b)
         S_lib().syn_q4k_repack_host(1, b.ctypes.data, src.ctypes.data, b.size, 1)
@@ -119,35 +228,202 @@ def cpu_baseline(torch, copies, xs, seconds):
     x = {name: xs[name].cpu().numpy() for name, _, _ in LAYER}
     total_w = sum(q4k_bytes(n, k) for _, n, k in LAYER)
 
-    def layer():
+    def layer(t):
         for name, n_out, k in LAYER:
-            o.gemv(o.Q4_K, w[name], n_out, k, x[name], 1, threads=threads)
+            o.gemv(o.Q4_K, w[name], n_out, k, x[name], 1, threads=t)
 
-    layer()
+    layer(threads)
     n, t0 = 0, time.perf_counter()
     while True:
-        layer()
+        layer(threads)
         n += 1
         dt = time.perf_counter() - t0
         if dt >= seconds:
             break
     t1 = time.perf_counter()
-    layer_single = None
-    for name, n_out, k in LAYER:  # one pass at one thread, for reference
-        o.gemv(o.Q4_K, w[name], n_out, k, x[name], 1, threads=1)
-    layer_single = time.perf_counter() - t1
+    reps1 = 0
+    while reps1 < 3 or time.perf_counter() - t1 < 1.0:
+        layer(1)
+        reps1 += 1
+    one = (time.perf_counter() - t1) / reps1
     return {
         "value": round(total_w * n / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n} Q4_K decode layers (5 GEMVs incl. Q8_K activation quantization) in "
-                  f"{dt:.1f} s on {threads} threads; one layer at 1 thread: "
-                  f"{layer_single * 1e3:.1f} ms",
+        "sample": f"{n} Q4_K decode layers (5 GEMVs incl. Q8_K activation quantization) in {dt:.1f} s on "
+                  f"{threads} threads (this box's CPU share for one GPU); one layer at 1 thread: "
+                  f"{one * 1e3:.2f} ms = {total_w / one / 1e9:.2f} GB/s",
         "ms_per_layer": round(dt / n * 1e3, 3),
+        "one_thread_gbs": round(total_w / one / 1e9, 3),
+        "host": host_info(),
     }
 
 
+# ---- the layer through the provider table ----------------------------------------------------------
+def bench_provider(torch, S, a, copies, xs):
+    """QKV Gemv, O Gemv, GateUpAct{Silu} over the stacked [gate; up] matrix and down Gemv, the
+    reference's dense lowering (crates/graph/src/blocks/ffn.rs:39-60), each a prepared op of the
+    provider table (X8 weights), captured once per weight copy and replayed."""
+    from syntropy_amd import provider as P
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipMemcpy.restype = C.c_int
+    pr = P.Provider()
+    ctx = pr.open(0)
+    try:
+        s = pr.stream(ctx)
+        # the stacked [gate; up] matrix: gate holds whole 8-block X8 runs, so its X8 form is the two
+        # X8 matrices one after the other
+        gateup = [torch.cat([c["gate"].bytes, c["up"].bytes]) for c in copies]
+        ops = [("qkv", "Gemv", 6144, 4096), ("o", "Gemv", 4096, 4096), ("gateup", {"GateUpAct": {"act": "Silu"}},
+                                                                      14336, 4096), ("down", "Gemv", 4096, 14336)]
+        prepared = []
+        for name, op, n, k in ops:
+            key = {"op": op, "schemes": [{"Ggml": "Q4_K"}, {"Plain": "F32"}, {"Plain": "F32"}], "layout": 1,
+                   "variant": 0}
+            po = pr.prepare(ctx, key, {"class": "Decode", "rows": 1, "dims": [n, k]})
+            xb, yb, ws = pr.alloc(ctx, 4 * k), pr.alloc(ctx, 4 * n), pr.alloc(ctx, po.workspace)
+            xh = xs["gate" if name == "gateup" else name].cpu().numpy()
+            assert hip.hipMemcpy(xb.addr, xh.ctypes.data, xh.nbytes, 1) == 0
+            per_copy = []
+            for c in range(COPIES):
+                wt = gateup[c] if name == "gateup" else copies[c][name].bytes
+                per_copy.append(P.op_args([P.packed(xb, P.DT_F32, [1, k])], [P.packed(yb, P.DT_F32, [1, n])],
+                                          [P.view(wt.data_ptr(), wt.numel())], P.Slice(ws.handle, 0, po.workspace)))
+            prepared.append((name, po, per_copy))
+        weight_bytes = sum(q4k_bytes(n * (2 if nm == "gateup" else 1), k) for nm, _, n, k in ops)
+        e0, e1 = pr.event(ctx), pr.event(ctx)
+
+        def graphs_of(names):
+            gs = []
+            for c in range(COPIES):
+                pr.begin_capture(ctx, s)
+                for name, po, per_copy in prepared:
+                    if name in names:
+                        pr.launch(ctx, s, po, per_copy[c])
+                gs.append(pr.end_capture(ctx, s))
+            for g in gs:
+                pr.replay(ctx, s, g)
+            pr.synchronize(ctx, s)
+            return gs
+
+        def replay_us(gs, n):
+            pr.synchronize(ctx, s)
+            pr.record(ctx, s, e0)
+            for i in range(n):
+                pr.replay(ctx, s, gs[i % COPIES])
+            pr.record(ctx, s, e1)
+            pr.synchronize(ctx, s)
+            return pr.elapsed(ctx, e0, e1) / n / 1e3
+
+        layer_graphs = graphs_of([nm for nm, _, _, _ in ops])
+        step_us = replay_us(layer_graphs, a.steps)
+        per_op = {nm: round(replay_us(graphs_of([nm]), max(20, a.steps // 2)), 3) for nm, _, _, _ in ops}
+        gbs = weight_bytes / (step_us * 1e-6) / 1e9
+        return {
+            "workload": "the decode layer through the provider table: Gemv QKV 6144x4096, Gemv O "
+                        "4096x4096, GateUpAct{Silu} 2x14336x4096 (stacked gate/up), Gemv down 4096x14336; "
+                        "X8 weights; one captured graph per weight copy, replayed",
+            "weight_bytes_per_step": weight_bytes,
+            "us_per_step": round(step_us, 3),
+            "gbs": round(gbs, 1),
+            "hbm_fraction_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "per_op_graph_us": per_op,
+            "per_op_gbs": {nm: round(q4k_bytes(n * (2 if nm == "gateup" else 1), k) / (per_op[nm] * 1e-6) / 1e9, 1)
+                           for nm, _, n, k in ops},
+        }
+    finally:
+        pr.close(ctx)
+
+
+# ---- Cfg1, Cfg2 and rows 2-8 ------------------------------------------------------------------------
+def weight_set(torch, S, ty, n, k, seed, layout=0):
+    """Copies of one N(0, 0.02) matrix quantized by the GPU packer, enough to exceed the MALL."""
+    wty = {Q4K: S.WeightType.Q4K, Q8_0: S.WeightType.Q8_0, Q4_0: S.WeightType.Q4_0}[ty]
+    ncopies = max(COPIES, -(-2 * MALL_BYTES // (n * row_bytes(ty, k))))
+    gen = torch.Generator(device="cuda")
+    out = []
+    for c in range(ncopies):
+        gen.manual_seed(seed + c)
+        w = torch.randn(n * k, generator=gen, device="cuda") * 0.02
+        W = S.Weights(wty, S.quantize(wty, w), n, k)
+        out.append(S.repack(W) if layout == 1 else W)
+    return out
+
+
+def gemv_case(torch, S, ws_list, rows, n, k, nrep):
+    """(step us: quantization + GEMV, kernel us: the GEMV on quantized rows) at `rows` rows."""
+    ty = ws_list[0].ty
+    x = torch.randn(rows, k, device="cuda")
+    y = torch.empty(rows, n, device="cuda")
+    lay = ws_list[0].layout
+    need = C.c_uint64()
+    S_lib().syn_gemv_layout_workspace_bytes(lay, int(ty), rows, k, C.byref(need))
+    ws = torch.empty(max(need.value, 256), dtype=torch.uint8, device="cuda")
+    step = gpu_us(torch, lambda i: S.gemv(ws_list[i % len(ws_list)], x, rows, y=y, ws=ws), nrep)
+    kern = None
+    if lay == 0:
+        qws = S.new_workspace(ty, rows, k)
+        S.quantize_into(ty, x, rows, k, qws)
+        kern = gpu_us(torch, lambda i: S.gemv_quantized(ws_list[i % len(ws_list)], qws, rows, y), nrep)
+    return step, kern
+
+
+def bench_cfgs(torch, S, a):
+    nrep = max(20, min(a.steps, 100))
+    res = {}
+    # Cfg1: Q4_0 4096 x 4096 at one row
+    n, k = 4096, 4096
+    wl = weight_set(torch, S, Q4_0, n, k, 0x51A10001)
+    step, kern = gemv_case(torch, S, wl, 1, n, k, nrep)
+    wb = n * row_bytes(Q4_0, k)
+    alg = wb + k + 4 * (k // 32) * 2 + 4 * n
+    res["cfg1"] = {"workload": "Q4_0 4096x4096 Gemv, one F32 row (Q8_0 activation quantization + GEMV)",
+                   "weight_bytes": wb, "copies_rotated": len(wl), "step_us": round(step, 3),
+                   "weight_gbs": round(wb / (step * 1e-6) / 1e9, 1),
+                   "roofline": {"bound": "hbm", "kernel": "k_gemv<Q4_0>", "achieved": round(alg / (kern * 1e-6) / 1e9, 1),
+                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(alg / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                "alg_bytes_per_launch": alg, "avg_launch_us": round(kern, 3)}}
+    del wl
+    # Cfg2: Q8_0 14336 x 4096 at 1, 8, 32 and 128 rows
+    n, k = 14336, 4096
+    wl = weight_set(torch, S, Q8_0, n, k, 0x51A10002)
+    wb = n * row_bytes(Q8_0, k)
+    rows_res = {}
+    for T in (1, 8, 32, 128):
+        step, kern = gemv_case(torch, S, wl, T, n, k, max(10, nrep // (1 + T // 32)))
+        alg = wb + T * (k + 8 * (k // 32)) + 4 * T * n
+        rows_res[str(T)] = {"step_us": round(step, 3), "weight_gbs": round(wb / (step * 1e-6) / 1e9, 1),
+                            "kernel_us": round(kern, 3), "kernel_alg_gbs": round(alg / (kern * 1e-6) / 1e9, 1),
+                            "kernel_frac": round(alg / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                            "tflops": round(2.0 * T * n * k / (step * 1e-6) / 1e12, 2)}
+    res["cfg2"] = {"workload": "Q8_0 14336x4096 (Llama-3-8B FFN up) Gemv at T rows, Q8_0 activations",
+                   "weight_bytes": wb, "copies_rotated": len(wl), "rows": rows_res}
+    del wl
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_rows(torch, S, a):
+    """RFC-0040 9 row 2: rows 2-8 at most 1.10 x the one-row time (Q4_K 14336x4096, both layouts)."""
+    nrep = max(20, min(a.steps, 100))
+    n, k = 14336, 4096
+    out = {"target": "time(rows) <= 1.10 x time(rows = 1) (RFC-0040 9, row 2)", "shape": [n, k]}
+    for layout in (0, 1):
+        wl = weight_set(torch, S, Q4K, n, k, 0x51A10004, layout)
+        t = {}
+        for rows in (1, 2, 4, 8):
+            t[rows], _ = gemv_case(torch, S, wl, rows, n, k, nrep)
+        out["x8" if layout else "source"] = {"us": {str(r): round(v, 3) for r, v in t.items()},
+                                             "ratio": {str(r): round(t[r] / t[1], 3) for r in (2, 4, 8)}}
+        del wl
+        torch.cuda.empty_cache()
+    return out
+
+
+# ---- MoE at 64 decode tokens ------------------------------------------------------------------------
 MOE = dict(n_experts=128, top_k=8, hidden=4096, inter=1536, tokens=64)
 
 
@@ -206,7 +482,7 @@ def bench_moe(torch, S, M, steps, warmup, cpu_seconds):
     }
     if cpu_seconds > 0:
         from oracle import oracle as o
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         ex = layer.experts
         g, u, d = ex.gate.cpu().numpy(), ex.up.cpu().numpy(), ex.down.cpu().numpy()
         r, xh = layer.router.cpu().numpy(), x.cpu().numpy()
@@ -231,12 +507,12 @@ def bench_moe(torch, S, M, steps, warmup, cpu_seconds):
     return res
 
 
+# ---- prefill at 2048 tokens ---------------------------------------------------------------------------
 PREFILL = dict(tokens=2048, dense=[("gate", 14336, 4096), ("down", 4096, 14336)], skew_rows=(3, 50, 97),
                skew_scale=3.0)
-F16_MFMA_PEAK_TFLOPS = 2500.0
 
 
-def bench_prefill(torch, S, M, steps, warmup, cpu_seconds, moe_layer_parts=None):
+def bench_prefill(torch, S, M, steps, warmup, cpu_seconds):
     """Prefill at 2048 tokens: the dense Q4_K GEMMs (2048x4096 activations, BF16-valued, times
     gate 14336x4096 and down 4096x14336) on the matrix cores, and the MoE layer at 2048 tokens
     with three router rows scaled so their experts take several times the average load."""
@@ -269,18 +545,16 @@ def bench_prefill(torch, S, M, steps, warmup, cpu_seconds, moe_layer_parts=None)
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / steps
     flops = sum(2.0 * T * n * k for _, n, k in c["dense"])
-    # the GEMM kernel alone, HIP events on its stream
     per = {}
-    for name, _, k in c["dense"]:
+    for name, _, k in c["dense"]:  # the GEMM kernel alone, HIP events on its stream
         S.gemm_quantize_into(xs[name], T, k, wss[name], stream=stream)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(steps):
-            S.gemm_quantized(mats[name], wss[name], T, ys[name], stream=stream)
-        e1.record()
-        torch.cuda.synchronize()
-        per[name] = e0.elapsed_time(e1) / steps  # ms
-    gemm_s = sum(per.values()) * 1e-3
+        per[name] = gpu_us(torch, lambda i, name=name: S.gemm_quantized(mats[name], wss[name], T, ys[name],
+                                                                        stream=stream), steps)
+    gemm_s = sum(per.values()) * 1e-6
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "traffic_prefill_gemm_2048tok.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
     res = {
         "workload": "prefill, 2048 tokens: X 2048x4096 (BF16 values) x Q4_K gate 14336x4096, "
                     "X' 2048x14336 x Q4_K down 4096x14336; Q8_K activation quantization + GEMM each",
@@ -290,13 +564,14 @@ def bench_prefill(torch, S, M, steps, warmup, cpu_seconds, moe_layer_parts=None)
         "roofline": {"bound": "mfma", "kernel": "k_gemm_q4k (F16 MFMA, exact integer sums)",
                      "achieved": round(flops / gemm_s / 1e12, 1), "peak": F16_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / gemm_s / 1e12 / F16_MFMA_PEAK_TFLOPS, 4),
-                     "traffic": None, "avg_launch_us": {k: round(v * 1e3, 1) for k, v in per.items()}},
+                     "traffic": traffic,
+                     "traffic_source": "profiles/traffic_prefill_gemm_2048tok.json (rocprofv3 --pmc)",
+                     "avg_launch_us": {k: round(v, 1) for k, v in per.items()}},
     }
     del mats, xs, wss, ys
     torch.cuda.empty_cache()
-    # MoE at 2048 tokens, skewed
     mc = MOE
-    layer, _ = build_moe(torch, S, M, 0x51A40000) if moe_layer_parts is None else moe_layer_parts
+    layer, _ = build_moe(torch, S, M, 0x51A40000)
     router = layer.router.clone()
     for r in c["skew_rows"]:
         router[r] *= c["skew_scale"]
@@ -321,9 +596,8 @@ def bench_prefill(torch, S, M, steps, warmup, cpu_seconds, moe_layer_parts=None)
                   "skew": f"router rows {list(c['skew_rows'])} scaled by {c['skew_scale']}"}
     if cpu_seconds > 0:
         from oracle import oracle as o
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         rows = 16
-        gen.manual_seed(0x51A10005)
         sample = []
         for i, (name, n_out, k) in enumerate(c["dense"]):
             gen.manual_seed(0x51A10005 + i)
@@ -345,11 +619,36 @@ def bench_prefill(torch, S, M, steps, warmup, cpu_seconds, moe_layer_parts=None)
     return res
 
 
+# ---- counter calibration kernels --------------------------------------------------------------------
+def calibrate(torch, only):
+    """`copy`: a plain 512 MiB device copy (reads and writes 512 MiB each); `calib`: 512 MiB read
+    once by syn_hbm_read_probe with the decode GEMV's load pattern.  Five launches each."""
+    nbytes = 512 << 20
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    if only == "copy":
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        written = nbytes
+    else:
+        f = S_lib().syn_hbm_read_probe_sink_words
+        f.argtypes, f.restype = [C.c_uint64], C.c_uint64
+        words = f(nbytes)
+        sink = torch.empty(words, dtype=torch.int32, device="cuda")
+        for _ in range(5):
+            rc = S_lib().syn_hbm_read_probe(src.data_ptr(), nbytes, sink.data_ptr(),
+                                            torch.cuda.current_stream().cuda_stream)
+            assert rc == 0
+        written = 4 * words
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel": only, "bytes_read_per_launch": nbytes, "bytes_written_per_launch": written,
+                      "launches": 5}))
+
+
 def main():
     a = parse()
     if a.gpus != 1:
-        print(f"bench.py measures one MI355X; --gpus {a.gpus} is not supported "
-              "(one GPU only)", file=sys.stderr)
+        print(f"bench.py measures one MI355X; --gpus {a.gpus} is not supported (one GPU only)", file=sys.stderr)
         sys.exit(2)
     import torch
     import syntropy_amd.gemv as S
@@ -357,124 +656,39 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     torch.cuda.set_device(0)
-    stream = torch.cuda.current_stream()
-
-    if a.only == "copy":
-        # a plain copy of known size: calibrates the HBM byte counters
-        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes": src.numel(), "launches": 5}))
+    if a.only in ("copy", "calib"):
+        calibrate(torch, a.only)
         return
-
-    copies, xs, ys, wss = build_layer(torch, S, 0x51A10003)
-    names = [name for name, _, _ in LAYER]
-    batches = [S.GemvBatch([c[n] for n in names], [xs[n] for n in names], [ys[n] for n in names])
-               for c in copies]
-    weight_bytes = sum(q4k_bytes(n, k) for _, n, k in LAYER)
-
-    # Headline: the layer's five Gemv ops as one grouped launch pair per step.
-    for i in range(a.warmup):
-        run_step_batched(batches[i % COPIES], stream)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(a.steps):
-        run_step_batched(batches[i % COPIES], stream)
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    value = weight_bytes * a.steps / dt / 1e9
-
-    # The same five ops launched one by one (one launch each, quantization fused).
-    for i in range(a.warmup):
-        run_step(S, copies[i % COPIES], xs, ys, wss, stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    for i in range(a.steps):
-        run_step(S, copies[i % COPIES], xs, ys, wss, stream)
-    torch.cuda.synchronize()
-    dt_ops = time.perf_counter() - t1
-
-    # Per-launch durations from HIP events on the launching stream: the grouped GEMV launch
-    # (the dominant kernel) and, for the one-by-one path, each Gemv op.
-    nrep = max(20, min(a.steps, 100))
-    for b in batches:
-        b.quantize(stream)  # each copy's rows in Q8_K once, outside the timed launches
-    for i in range(5):
-        batches[i % COPIES].gemv_quantized(stream)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    # a spin kernel first, so every launch below is queued before the GPU reaches it and the
-    # event pair times the kernels back to back (launch gaps included), not the host's rate
-    torch.cuda._sleep(int(4e7))
-    e0.record()
-    for i in range(nrep):
-        batches[i % COPIES].gemv_quantized(stream)  # k_gemv_q4k_batch alone, back to back
-    e1.record()
-    torch.cuda.synchronize()
-    batch_ms = e0.elapsed_time(e1) / nrep
-    ev = [{name: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for name, _, _ in LAYER} for _ in range(nrep)]
-    for i in range(nrep):
-        run_step(S, copies[i % COPIES], xs, ys, wss, stream, events=ev[i])
-    torch.cuda.synchronize()
-    per = {name: sum(ev[i][name][0].elapsed_time(ev[i][name][1]) for i in range(nrep)) / nrep
-           for name, _, _ in LAYER}  # ms
-    # algorithmic bytes of one k_gemv_q4k_batch launch: the weights, each Q8_K row once (codes,
-    # 32-value sums, scales) and the F32 outputs
-    alg_bytes = sum(q4k_bytes(n, k) + k + k // 8 + k // 64 + 4 * n for _, n, k in LAYER)
-    achieved = alg_bytes / (batch_ms * 1e-3) / 1e9
-
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", "traffic_q4k_gemv_decode_layer.json")
-    if os.path.exists(tfile):
-        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
-
-    out = {
-        "metric": METRIC,
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
-        "ms_per_step": round(dt / a.steps * 1e3, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "i8xi8->i32, f32 terms",
-        "data": "synthetic: W ~ N(0,0.02) -> Q4_K (GPU packer, ggml-exact); x ~ N(0,1) F32",
-        "config": {
-            "workload": "Q4_K decode layer matmuls, Llama-3-8B shapes, batch 1: QKV 6144x4096, "
-                        "O 4096x4096, gate/up 14336x4096, down 4096x14336; Q8_K act quant + "
-                        "5 GEMVs per step",
-            "launch": "grouped: one batched Q8_K quantization + one grouped GEMV (syn_gemv_batch_layout)",
-            "weight_layout": "X8 (runs of 8 Q4_K super-blocks stored chunk-major; repacked once at load)",
-            "weight_bytes_per_step": weight_bytes,
-            "weight_copies_rotated": COPIES,
-            "hbm_fraction_of_peak": round(value / HBM_PEAK_GBS, 4),
-            "one_op_per_launch_gbs": round(weight_bytes * a.steps / dt_ops / 1e9, 2),
-            "one_op_per_launch_us": {k: round(v * 1e3, 3) for k, v in per.items()},
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "k_gemv_q4k_batch<X8> (syn_gemv_batch_quantized_layout: the grouped GEMV on Q8_K rows)",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "alg_bytes_per_launch": alg_bytes,
-            "avg_launch_us": round(batch_ms * 1e3, 3),
-        },
-    }
-    if not a.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(torch, copies, xs, a.cpu_seconds)
-    del copies, batches
-    if not a.no_moe:
+    want = set(PARTS) if a.only is None else {a.only}
+    if a.no_moe:
+        want.discard("moe")
+    if a.no_prefill:
+        want.discard("prefill")
+    out = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+           "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "i8xi8->i32, f32 terms",
+           "data": "synthetic: W ~ N(0,0.02) -> Q4_K (GPU packer, ggml-exact); x ~ N(0,1) F32"}
+    if want & {"layer", "provider"}:
+        copies, xs, ys, wss = build_layer(torch, S, 0x51A10003)
+        if "layer" in want:
+            lay = bench_layer(torch, S, a, copies, xs, ys, wss)
+            out["value"], out["ms_per_step"] = lay["value"], lay["ms_per_step"]
+            out["config"], out["roofline"] = lay["config"], lay["roofline"]
+            if not a.no_cpu:
+                out["cpu_baseline"] = cpu_layer_baseline(copies, xs, a.cpu_seconds)
+        if "provider" in want:
+            out["provider_path"] = bench_provider(torch, S, a, copies, xs)
+        del copies, xs, ys, wss
+        torch.cuda.empty_cache()
+    if "cfgs" in want:
+        out.update(bench_cfgs(torch, S, a))
+    if "rows" in want:
+        out["rows_2_8"] = bench_rows(torch, S, a)
+    if "moe" in want:
         torch.cuda.empty_cache()
         out["moe"] = bench_moe(torch, S, M, max(10, a.steps // 4), max(3, a.warmup // 4),
                                0 if a.no_cpu else a.cpu_seconds)
-    if not a.no_prefill:
+    if "prefill" in want:
         torch.cuda.empty_cache()
         out["prefill"] = bench_prefill(torch, S, M, max(5, a.steps // 20), max(2, a.warmup // 10),
                                        0 if a.no_cpu else min(a.cpu_seconds, 5.0))

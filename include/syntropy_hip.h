@@ -123,6 +123,14 @@ int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, uint64_t w_by
                     uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
                     void* stream);
 
+/* ---- Measurement (not on the op path) ----------------------------------------------------------
+ * syn_hbm_read_probe: reads `bytes` (a multiple of 16, src 16-byte aligned) once with the decode
+ * GEMV's load pattern (16-byte non-temporal loads, nine per lane) and writes one word per
+ * workgroup to sink (syn_hbm_read_probe_sink_words(bytes) words): a kernel of known HBM traffic
+ * against which the HBM byte counters are calibrated.  No counterpart in the reference. */
+uint64_t syn_hbm_read_probe_sink_words(uint64_t bytes);
+int syn_hbm_read_probe(const void* src, uint64_t bytes, uint32_t* sink, void* stream);
+
 /* ---- RmsNorm and Logits ----------------------------------------------------------------------
  * syn_rms_norm: y = RmsNorm(x) of each of `rows` rows of n F32 values (n <= 16384), weight g [n]:
  *   ss = sum of x[i] x[i] in the F32Fixed order, mean = ss / n, scale = 1 / sqrt(mean + eps),

@@ -611,6 +611,19 @@ SYN_EXPORT int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, ui
     return syn_gate_up_act_rows(layout, wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, ws_bytes, stream, nullptr);
 }
 
+// ---- measurement ----------------------------------------------------------------------------
+
+SYN_EXPORT uint64_t syn_hbm_read_probe_sink_words(uint64_t bytes) { return (bytes / 16 + 256 * 9 - 1) / (256 * 9); }
+
+SYN_EXPORT int syn_hbm_read_probe(const void* src, uint64_t bytes, uint32_t* sink, void* stream) {
+    const char* W = "syn_hbm_read_probe";
+    if (bytes % 16) return fail(SYN_E_INVALID, "%s: %llu bytes are not whole 16-byte chunks", W, (unsigned long long)bytes);
+    if (bytes && (!src || !sink)) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!aligned(src, 16) || !aligned(sink, 4)) return fail(SYN_E_INVALID, "%s: src must be 16-byte aligned", W);
+    syn::launch_hbm_read_probe((const uint8_t*)src, bytes, sink, (hipStream_t)stream);
+    return check_launch(W);
+}
+
 // ---- RmsNorm and Logits ------------------------------------------------------------------
 
 SYN_EXPORT int syn_rms_norm(const float* x, const float* g, uint32_t rows, uint32_t n, float eps, float* y,

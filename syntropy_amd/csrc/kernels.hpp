@@ -48,6 +48,8 @@ void launch_moe_gather_q8_0(const float* x, const uint32_t* slots, int nentries,
 void launch_moe_q8(int mode, const uint8_t* w0, const uint8_t* w1, uint64_t mat_bytes, int n_experts, int n_out,
                    int k, const uint32_t* offsets, const uint32_t* slots, const uint32_t* err, const int8_t* aq,
                    const float* ad, float* y, hipStream_t stream);
+// probe.hip: a read-only HBM stream with the decode GEMV's load pattern (counter calibration)
+void launch_hbm_read_probe(const uint8_t* src, uint64_t bytes, uint32_t* sink, hipStream_t stream);
 // norm.hip: RmsNorm rows of at most NORM_MAX_COLS values
 constexpr int NORM_MAX_COLS = 16384;
 void launch_rms_norm(const float* x, const float* g, int rows, int n, float eps, float* y, hipStream_t stream,
