@@ -78,8 +78,9 @@ int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uin
  * syn_q4k_repack: on the device (src and dst distinct, 16-byte aligned); inverse = 1 restores
  *   the GGUF order.  syn_q4k_repack_host: the same on host memory.
  * syn_gemv_layout(_workspace_bytes): the Gemv op over a matrix in `layout` (0 is syn_gemv); for
- *   layout 1 one row runs the grouped decode kernel (k_in <= 16384), more rows the matrix-core
- *   GEMM (k_in a multiple of 2048).
+ *   layout 1 one row runs the decode kernel with the row quantized in every workgroup, 2 to 8 rows
+ *   the multi-row decode kernel on rows quantized beforehand (both k_in <= 16384), more rows the
+ *   matrix-core GEMM (k_in a multiple of 2048).
  * syn_gemv_batch_layout / syn_gemv_batch_quantized_layout: the grouped decode of every problem
  *   in `layout`. */
 int syn_q4k_repack(uint32_t layout, const void* src, void* dst, uint64_t bytes, int32_t inverse, void* stream);

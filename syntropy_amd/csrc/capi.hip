@@ -457,6 +457,10 @@ SYN_EXPORT int syn_gemv_layout_workspace_bytes(uint32_t layout, int32_t wtype, u
         *bytes = syn::act_layout(syn::ACT_Q8K, 1, k_in).bytes;
         return SYN_OK;
     }
+    if (syn::gemv_q4k_rows_supported((int)rows, (int)k_in)) {  // 2..8 rows: Q8_K rows, the multi-row decode
+        *bytes = syn::act_layout(syn::ACT_Q8K, rows, k_in).bytes;
+        return SYN_OK;
+    }
     if (k_in % 2048) return fail(SYN_E_UNSUPPORTED, "%s: the layout-1 GEMM takes k_in in multiples of 2048, not %u", W, k_in);
     if (int rc = check_gemm_shape(W, rows, k_in)) return rc;
     *bytes = syn::gemm_act_bytes((int64_t)gemm_tpad(rows), (int)k_in);
@@ -479,6 +483,23 @@ int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
         const int32_t ts[1] = {wtype};
         const uint64_t wb[1] = {w_bytes};
         return gemv_batch_f32(W, layout, 1, ts, ws_, wb, &n_out, &k_in, xs, ys, ws, ws_bytes, stream, true, active);
+    }
+    if (syn::gemv_q4k_rows_supported((int)rows, (int)k_in)) {
+        const uint64_t need_w = (uint64_t)n_out * (k_in / 256) * 144;
+        if (!w || !x || !ws || !y) return fail(SYN_E_INVALID, "%s: null operand", W);
+        if (w_bytes < need_w)
+            return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
+                        (unsigned long long)w_bytes, (unsigned long long)need_w);
+        if (ws_bytes < need)
+            return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                        (unsigned long long)ws_bytes, (unsigned long long)need);
+        if (!aligned(w, 16) || !aligned(x, 16) || !aligned(ws, 256) || !aligned(y, 4))
+            return fail(SYN_E_INVALID, "%s: w and x must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
+        syn::launch_act_quant(syn::ACT_Q8K, x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
+        if (int rc = check_launch(W)) return rc;
+        syn::launch_gemv_q4k_rows((const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows, y,
+                                  (hipStream_t)stream, active);
+        return check_launch(W);
     }
     if (!syn::gemm_q4k_supported((int)n_out, (int)k_in))
         return fail(SYN_E_UNSUPPORTED, "%s: a %u x %u matrix is larger than 4 GiB", W, n_out, k_in);

@@ -112,8 +112,22 @@ def test_gemm_x8_equals_oracle(S, rows, n_out, k):
     assert_same(got, o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=8), "x8 gemm")
 
 
+@pytest.mark.parametrize("rows,n_out,k", [(2, 14336, 4096), (3, 14336, 4096), (8, 4096, 14336), (7, 37, 1536),
+                                          (4, 9, 16384), (5, 300, 256)])
+def test_x8_rows_2_to_8_equal_oracle(S, rows, n_out, k):
+    """2..8 rows over X8 weights: the rows quantized once, one super-block per lane holding its
+    terms for every row (k need not be a multiple of 2048 here)."""
+    rs = np.random.default_rng(rows * 7 + n_out + k)
+    w = random_q4k(rs, n_out, k)
+    x = o.normal(0xF0 + rows, 1.0, rows * k).reshape(rows, k)
+    W = S.repack(S.Weights(S.WeightType.Q4K, dev(w), n_out, k))
+    announce(f"x8 rows={rows} {n_out}x{k}")
+    got = host(S.gemv(W, dev(x), rows))
+    assert_same(got, o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=16), "x8 rows")
+
+
 def test_x8_refusals(S):
     W = S.repack(S.Weights(S.WeightType.Q4K, torch.zeros(64 * 6 * 144, dtype=torch.uint8, device="cuda"), 64, 1536))
-    x = torch.zeros(4, 1536, device="cuda")
-    with pytest.raises(S.SynError):  # the GEMM takes rows of whole 8-block runs only
-        S.gemv(W, x, 4)
+    x = torch.zeros(9, 1536, device="cuda")
+    with pytest.raises(S.SynError):  # from 9 rows the GEMM takes rows of whole 8-block runs only
+        S.gemv(W, x, 9)

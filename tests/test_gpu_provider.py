@@ -224,7 +224,8 @@ def test_query_answers_none_for_unserved_shapes(cx):
     gelu = dense_key({"GateUpAct": {"act": "Gelu"}}, o.Q4_K)
     assert pr.query(cx.ctx, gelu, shape(1, 64, 256)) is None  # no reference form of GELU gating
     assert pr.query(cx.ctx, dict(gemv_key(o.Q8_0), layout=1), shape(1, 64, 256)) is None
-    assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(8, 64, 1536)) is None  # GEMM: k % 2048
+    assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(9, 64, 1536)) is None  # GEMM: k % 2048
+    assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(8, 64, 1536)) is not None  # 2..8 rows
     assert pr.query(cx.ctx, {"op": "Attention", "schemes": [], "layout": 0, "variant": 0},
                     shape(1, 64, 256)) is None
     with pytest.raises(cx.P.ProviderError) as e:
