@@ -42,6 +42,7 @@ F16_MFMA_PEAK_TFLOPS = 2500.0
 LAYER = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate", 14336, 4096), ("up", 14336, 4096),
          ("down", 4096, 14336)]
 Q4K, Q8_0, Q4_0 = 12, 8, 2
+SPLIT = 2  # the weight layout of Q8_0 / Q4_0 matrices after repack (codes, then scales)
 COPIES = 5
 MALL_BYTES = 256 << 20
 PARTS = ["layer", "provider", "cfgs", "rows", "moe", "prefill"]
@@ -348,7 +349,7 @@ def weight_set(torch, S, ty, n, k, seed, layout=0):
         gen.manual_seed(seed + c)
         w = torch.randn(n * k, generator=gen, device="cuda") * 0.02
         W = S.Weights(wty, S.quantize(wty, w), n, k)
-        out.append(S.repack(W) if layout == 1 else W)
+        out.append(S.repack(W) if layout else W)
     return out
 
 
@@ -363,7 +364,7 @@ def gemv_case(torch, S, ws_list, rows, n, k, nrep):
     ws = torch.empty(max(need.value, 256), dtype=torch.uint8, device="cuda")
     step = gpu_us(torch, lambda i: S.gemv(ws_list[i % len(ws_list)], x, rows, y=y, ws=ws), nrep)
     kern = None
-    if lay == 0:
+    if lay in (0, 2):  # the product alone, over rows quantized beforehand
         qws = S.new_workspace(ty, rows, k)
         S.quantize_into(ty, x, rows, k, qws)
         kern = gpu_us(torch, lambda i: S.gemv_quantized(ws_list[i % len(ws_list)], qws, rows, y), nrep)
@@ -375,31 +376,35 @@ def bench_cfgs(torch, S, a):
     res = {}
     # Cfg1: Q4_0 4096 x 4096 at one row
     n, k = 4096, 4096
-    wl = weight_set(torch, S, Q4_0, n, k, 0x51A10001)
+    wl = weight_set(torch, S, Q4_0, n, k, 0x51A10001, SPLIT)
     step, kern = gemv_case(torch, S, wl, 1, n, k, nrep)
     wb = n * row_bytes(Q4_0, k)
     alg = wb + k + 4 * (k // 32) * 2 + 4 * n
-    res["cfg1"] = {"workload": "Q4_0 4096x4096 Gemv, one F32 row (Q8_0 activation quantization + GEMV)",
+    res["cfg1"] = {"workload": "Q4_0 4096x4096 Gemv, one F32 row (Q8_0 activation quantization + GEMV), "
+                               "weights in the SPLIT layout",
                    "weight_bytes": wb, "copies_rotated": len(wl), "step_us": round(step, 3),
                    "weight_gbs": round(wb / (step * 1e-6) / 1e9, 1),
-                   "roofline": {"bound": "hbm", "kernel": "k_gemv<Q4_0>", "achieved": round(alg / (kern * 1e-6) / 1e9, 1),
+                   "roofline": {"bound": "hbm", "kernel": "k_gemv_split<Q4_0,1>",
+                                "achieved": round(alg / (kern * 1e-6) / 1e9, 1),
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": round(alg / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                                 "alg_bytes_per_launch": alg, "avg_launch_us": round(kern, 3)}}
     del wl
     # Cfg2: Q8_0 14336 x 4096 at 1, 8, 32 and 128 rows
     n, k = 14336, 4096
-    wl = weight_set(torch, S, Q8_0, n, k, 0x51A10002)
+    wl = weight_set(torch, S, Q8_0, n, k, 0x51A10002, SPLIT)
     wb = n * row_bytes(Q8_0, k)
     rows_res = {}
     for T in (1, 8, 32, 128):
         step, kern = gemv_case(torch, S, wl, T, n, k, max(10, nrep // (1 + T // 32)))
         alg = wb + T * (k + 8 * (k // 32)) + 4 * T * n
-        rows_res[str(T)] = {"step_us": round(step, 3), "weight_gbs": round(wb / (step * 1e-6) / 1e9, 1),
+        rows_res[str(T)] = {"kernel": "k_gemv_split<Q8_0>" if T <= 8 else "k_gemm_q8_split",
+                            "step_us": round(step, 3), "weight_gbs": round(wb / (step * 1e-6) / 1e9, 1),
                             "kernel_us": round(kern, 3), "kernel_alg_gbs": round(alg / (kern * 1e-6) / 1e9, 1),
                             "kernel_frac": round(alg / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                             "tflops": round(2.0 * T * n * k / (step * 1e-6) / 1e12, 2)}
-    res["cfg2"] = {"workload": "Q8_0 14336x4096 (Llama-3-8B FFN up) Gemv at T rows, Q8_0 activations",
+    res["cfg2"] = {"workload": "Q8_0 14336x4096 (Llama-3-8B FFN up) Gemv at T rows, Q8_0 activations, "
+                               "weights in the SPLIT layout",
                    "weight_bytes": wb, "copies_rotated": len(wl), "rows": rows_res}
     del wl
     torch.cuda.empty_cache()

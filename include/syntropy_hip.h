@@ -38,6 +38,7 @@ extern "C" {
 
 #define SYN_LAYOUT_SOURCE 0 /* the GGUF order */
 #define SYN_LAYOUT_X8 1     /* Q4_K runs of eight super-blocks stored chunk-major */
+#define SYN_LAYOUT_SPLIT 2  /* Q8_0 / Q4_0: every block's codes, then every block's F16 scale */
 
 /* The message of the last failed call on this thread ("" if none). */
 const char* syn_last_error(void);
@@ -77,19 +78,34 @@ int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uin
  * repacked form is the same length).  Decode then reads whole 128-byte lines per load.
  * syn_q4k_repack: on the device (src and dst distinct, 16-byte aligned); inverse = 1 restores
  *   the GGUF order.  syn_q4k_repack_host: the same on host memory.
+ * Layout 2 (SPLIT) of a Q8_0 or Q4_0 matrix: the codes of every block in block order (32 bytes
+ *   a Q8_0 block, 16 a Q4_0 block), then every block's F16 scale in block order; also the same
+ *   length and shape-free.  syn_split_repack(_host) as syn_q4k_repack(_host), for `wtype`.
  * syn_gemv_layout(_workspace_bytes): the Gemv op over a matrix in `layout` (0 is syn_gemv); for
  *   layout 1 one row runs the decode kernel with the row quantized in every workgroup, 2 to 8 rows
  *   the multi-row decode kernel on rows quantized beforehand (both k_in <= 16384), more rows the
- *   matrix-core GEMM (k_in a multiple of 2048).
+ *   matrix-core GEMM (k_in a multiple of 2048).  Layout 2 quantizes the rows to Q8_0 blocks and
+ *   runs the split decode kernel eight rows at a time, or, for Q8_0 and 9 rows or more, the int8
+ *   matrix-core GEMM.
  * syn_gemv_batch_layout / syn_gemv_batch_quantized_layout: the grouped decode of every problem
  *   in `layout`. */
 int syn_q4k_repack(uint32_t layout, const void* src, void* dst, uint64_t bytes, int32_t inverse, void* stream);
 int syn_q4k_repack_host(uint32_t layout, const void* src, void* dst, uint64_t bytes, int32_t inverse);
+int syn_split_repack(uint32_t layout, int32_t wtype, const void* src, void* dst, uint64_t bytes, int32_t inverse,
+                     void* stream);
+int syn_split_repack_host(uint32_t layout, int32_t wtype, const void* src, void* dst, uint64_t bytes,
+                          int32_t inverse);
 int syn_gemv_layout_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t rows, uint32_t k_in,
                                     uint64_t* bytes);
 int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
                     uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
                     void* stream);
+/* syn_gemv_quantized_layout: the product alone over rows syn_act_quantize quantized for the same
+ * wtype (layout 0 is syn_gemv_quantized; layout 2 as syn_gemv_layout without its quantization).
+ * Replaces crates/kernels-cpu/src/gemv.rs:435-492 for a repacked matrix. */
+int syn_gemv_quantized_layout(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
+                              uint32_t k_in, const void* ws, uint64_t ws_bytes, uint32_t rows, float* y,
+                              void* stream);
 /* syn_gemv_layout_noalloc: no counterpart in the reference.  The same Gemv as syn_gemv_layout
  * (same outputs, bit for bit) for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc): the workspace is a

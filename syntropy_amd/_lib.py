@@ -53,6 +53,9 @@ def lib():
         "syn_gemm_q4k_quantized": [vp, u64, u32, u32, vp, u64, u32, vp, vp],
         "syn_q4k_repack": [u32, vp, vp, u64, i32, vp],
         "syn_q4k_repack_host": [u32, vp, vp, u64, i32],
+        "syn_split_repack": [u32, i32, vp, vp, u64, i32, vp],
+        "syn_gemv_quantized_layout": [u32, i32, vp, u64, u32, u32, vp, u64, u32, vp, vp],
+        "syn_split_repack_host": [u32, i32, vp, vp, u64, i32],
         "syn_gemv_layout_workspace_bytes": [u32, i32, u32, u32, C.POINTER(C.c_uint64)],
         "syn_gemv_layout": [u32, i32, vp, u64, u32, u32, vp, u32, vp, vp, u64, vp],
         "syn_gate_up_act_workspace_bytes": [u32, i32, u32, u32, u32, vp],

@@ -443,12 +443,79 @@ SYN_EXPORT int syn_q4k_repack_host(uint32_t layout, const void* src, void* dst, 
     return SYN_OK;
 }
 
-// Gemv over Q4_K weights in a repacked layout: one row runs the grouped decode kernel, more rows
-// the matrix-core GEMM (which needs rows of whole 8-block runs: k_in a multiple of 2048).
+namespace {
+int check_split_repack(const char* W, uint32_t layout, int32_t wtype, const void* src, void* dst, uint64_t bytes) {
+    if (layout != SYN_LAYOUT_SPLIT) return fail(SYN_E_UNSUPPORTED, "%s: layout %u (2: SPLIT)", W, layout);
+    if (wtype != SYN_Q8_0 && wtype != SYN_Q4_0)
+        return fail(SYN_E_UNSUPPORTED, "%s: weight type %d (the SPLIT layout holds Q8_0 or Q4_0)", W, wtype);
+    const uint64_t bb = (uint64_t)syn::split_code_bytes(wtype) + 2;
+    if (bytes % bb)
+        return fail(SYN_E_INVALID, "%s: %llu bytes are not whole %llu-byte blocks", W, (unsigned long long)bytes,
+                    (unsigned long long)bb);
+    if (bytes && (!src || !dst)) return fail(SYN_E_INVALID, "%s: null buffer", W);
+    if (bytes && src == dst) return fail(SYN_E_INVALID, "%s: the repack is not in place", W);
+    return SYN_OK;
+}
+}  // namespace
+
+SYN_EXPORT int syn_split_repack(uint32_t layout, int32_t wtype, const void* src, void* dst, uint64_t bytes,
+                                int32_t inverse, void* stream) {
+    const char* W = "syn_split_repack";
+    if (int rc = check_split_repack(W, layout, wtype, src, dst, bytes)) return rc;
+    syn::launch_split_repack(wtype, (const uint8_t*)src, (uint8_t*)dst, bytes, inverse != 0, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_split_repack_host(uint32_t layout, int32_t wtype, const void* src, void* dst, uint64_t bytes,
+                                     int32_t inverse) {
+    const char* W = "syn_split_repack_host";
+    if (int rc = check_split_repack(W, layout, wtype, src, dst, bytes)) return rc;
+    const uint64_t cb = (uint64_t)syn::split_code_bytes(wtype), nblocks = bytes / (cb + 2);
+    const uint8_t* s = (const uint8_t*)src;
+    uint8_t* d = (uint8_t*)dst;
+    for (uint64_t g = 0; g < nblocks; ++g) {
+        const uint64_t gguf = g * (cb + 2), codes = g * cb, scale = cb * nblocks + 2 * g;
+        if (!inverse) {
+            memcpy(d + codes, s + gguf + 2, cb);
+            memcpy(d + scale, s + gguf, 2);
+        } else {
+            memcpy(d + gguf + 2, s + codes, cb);
+            memcpy(d + gguf, s + scale, 2);
+        }
+    }
+    return SYN_OK;
+}
+
+// Gemv over weights in a repacked layout.  Q4_K in X8: one row runs the grouped decode kernel,
+// 2 to 8 rows the multi-row decode kernel, more rows the matrix-core GEMM (which needs rows of
+// whole 8-block runs: k_in a multiple of 2048).  Q8_0 / Q4_0 in SPLIT: Q8_0 activation rows, the
+// split decode kernel for up to 8 rows at a time, the int8 matrix-core GEMM for Q8_0 and more.
+constexpr uint32_t SPLIT_GEMM_MIN_ROWS = 9;
+constexpr uint32_t SPLIT_GEMM_MAX_ROWS = 65535u * 32u;  // the GEMM grid's token tiles
+
+namespace {
+// The products over a SPLIT matrix from rows already quantized to Q8_0 blocks in ws.
+void split_products(int32_t wtype, const void* w, uint32_t n_out, uint32_t k_in, const void* ws, uint32_t rows,
+                    float* y, void* stream, const uint32_t* active) {
+    if (wtype == SYN_Q8_0 && rows >= SPLIT_GEMM_MIN_ROWS)
+        syn::launch_gemm_q8_split((const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows, y,
+                                  (hipStream_t)stream, active);
+    else
+        syn::launch_gemv_split(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows, y,
+                               (hipStream_t)stream, active);
+}
+}  // namespace
 SYN_EXPORT int syn_gemv_layout_workspace_bytes(uint32_t layout, int32_t wtype, uint32_t rows, uint32_t k_in,
                                                uint64_t* bytes) {
     const char* W = "syn_gemv_layout_workspace_bytes";
     if (layout == SYN_LAYOUT_SOURCE) return syn_gemv_workspace_bytes(wtype, rows, k_in, bytes);
+    if (layout == SYN_LAYOUT_SPLIT && (wtype == SYN_Q8_0 || wtype == SYN_Q4_0)) {
+        if (int rc = check_gemv_shape(W, wtype, rows, k_in)) return rc;
+        if (!bytes) return fail(SYN_E_INVALID, "%s: null output", W);
+        if (k_in / 32 > (1u << 24)) return fail(SYN_E_UNSUPPORTED, "%s: k_in %u too large", W, k_in);
+        *bytes = syn::act_layout(syn::ACT_Q8_0, rows, k_in).bytes;
+        return SYN_OK;
+    }
     if (layout != SYN_LAYOUT_X8 || wtype != SYN_Q4_K)
         return fail(SYN_E_UNSUPPORTED, "%s: layout %u of weight type %d", W, layout, wtype);
     if (!bytes) return fail(SYN_E_INVALID, "%s: null output", W);
@@ -476,6 +543,27 @@ int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
     uint64_t need = 0;
     if (int rc = syn_gemv_layout_workspace_bytes(layout, wtype, rows, k_in, &need)) return rc;
     if (rows == 0 || n_out == 0) return SYN_OK;
+    if (layout == SYN_LAYOUT_SPLIT) {
+        const uint64_t need_w = (uint64_t)n_out * (k_in / 32) * (syn::split_code_bytes(wtype) + 2);
+        if (!w || !y || (k_in && (!x || !ws))) return fail(SYN_E_INVALID, "%s: null operand", W);
+        if (w_bytes < need_w)
+            return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
+                        (unsigned long long)w_bytes, (unsigned long long)need_w);
+        if (ws_bytes < need)
+            return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                        (unsigned long long)ws_bytes, (unsigned long long)need);
+        if (!aligned(w, 16) || (k_in && (!aligned(x, 16) || !aligned(ws, 256))) || !aligned(y, 4))
+            return fail(SYN_E_INVALID, "%s: w and x must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
+        if ((uint64_t)n_out * rows > (1ull << 40)) return fail(SYN_E_INVALID, "%s: rows * n_out too large", W);
+        if (wtype == SYN_Q8_0 && rows >= SPLIT_GEMM_MIN_ROWS && rows > SPLIT_GEMM_MAX_ROWS)
+            return fail(SYN_E_UNSUPPORTED, "%s: %u rows (the GEMM takes %u)", W, rows, SPLIT_GEMM_MAX_ROWS);
+        if (k_in) {
+            syn::launch_act_quant(syn::ACT_Q8_0, x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
+            if (int rc = check_launch(W)) return rc;
+        }
+        split_products(wtype, w, n_out, k_in, ws, rows, y, stream, active);
+        return check_launch(W);
+    }
     if (rows == 1) {
         const float* xs[1] = {x};
         float* ys[1] = {y};
@@ -525,6 +613,36 @@ SYN_EXPORT int syn_gemv_layout(uint32_t layout, int32_t wtype, const void* w, ui
                                uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
                                void* stream) {
     return syn_gemv_layout_rows(layout, wtype, w, w_bytes, n_out, k_in, x, rows, y, ws, ws_bytes, stream, nullptr);
+}
+
+// The product alone, over rows syn_act_quantize already quantized (Q8_0 blocks for the SPLIT
+// layout's Q8_0 and Q4_0 matrices).
+SYN_EXPORT int syn_gemv_quantized_layout(uint32_t layout, int32_t wtype, const void* w, uint64_t w_bytes,
+                                         uint32_t n_out, uint32_t k_in, const void* ws, uint64_t ws_bytes,
+                                         uint32_t rows, float* y, void* stream) {
+    const char* W = "syn_gemv_quantized_layout";
+    if (layout == SYN_LAYOUT_SOURCE)
+        return syn_gemv_quantized(wtype, w, w_bytes, n_out, k_in, ws, ws_bytes, rows, y, stream);
+    if (layout != SYN_LAYOUT_SPLIT)
+        return fail(SYN_E_UNSUPPORTED, "%s: layout %u (0: SOURCE, 2: SPLIT)", W, layout);
+    uint64_t need = 0;
+    if (int rc = syn_gemv_layout_workspace_bytes(layout, wtype, rows, k_in, &need)) return rc;
+    if (rows == 0 || n_out == 0) return SYN_OK;
+    const uint64_t need_w = (uint64_t)n_out * (k_in / 32) * (syn::split_code_bytes(wtype) + 2);
+    if (!w || !y || (k_in && !ws)) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (w_bytes < need_w)
+        return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
+                    (unsigned long long)w_bytes, (unsigned long long)need_w);
+    if (ws_bytes < need)
+        return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
+                    (unsigned long long)ws_bytes, (unsigned long long)need);
+    if (!aligned(w, 16) || (k_in && !aligned(ws, 256)) || !aligned(y, 4))
+        return fail(SYN_E_INVALID, "%s: w must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
+    if ((uint64_t)n_out * rows > (1ull << 40)) return fail(SYN_E_INVALID, "%s: rows * n_out too large", W);
+    if (wtype == SYN_Q8_0 && rows >= SPLIT_GEMM_MIN_ROWS && rows > SPLIT_GEMM_MAX_ROWS)
+        return fail(SYN_E_UNSUPPORTED, "%s: %u rows (the GEMM takes %u)", W, rows, SPLIT_GEMM_MAX_ROWS);
+    split_products(wtype, w, n_out, k_in, ws, rows, y, stream, nullptr);
+    return check_launch(W);
 }
 
 // ---- syn_gemv_layout without a caller workspace ---------------------------------------------

@@ -72,7 +72,11 @@ SYN_HD inline ActLayout act_layout(int kind, uint64_t rows, uint64_t k) {
 //    chunk-major: 16-byte chunk q of the run's block i at 128 q + 16 i.  A final run of m < 8
 //    blocks is stored the same way with stride 16 m.  Shape-free (a permutation of the matrix
 //    bytes), so a repack needs only the byte count.
-enum : int { LAYOUT_SOURCE = 0, LAYOUT_X8 = 1 };
+//  2 SPLIT (Q8_0 and Q4_0 matrices): the codes of every block in block order (32 bytes a block
+//    for Q8_0, 16 for Q4_0), then every block's F16 scale in block order.  Also shape-free: block
+//    g's codes sit at cb g and its scale at cb nblocks + 2 g (cb = 32 or 16).
+enum : int { LAYOUT_SOURCE = 0, LAYOUT_X8 = 1, LAYOUT_SPLIT = 2 };
+SYN_HD inline int split_code_bytes(int ty) { return ty == T_Q8_0 ? 32 : 16; }
 SYN_HD inline uint32_t x8_group_blocks(uint64_t g, uint64_t nblocks) {
     const uint64_t first = g & ~(uint64_t)7;
     return nblocks - first < 8 ? (uint32_t)(nblocks - first) : 8u;

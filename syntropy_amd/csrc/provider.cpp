@@ -419,14 +419,20 @@ struct Plan {
 
 uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
+// The layout repack gives a dense product's weights of this type (0: they stay in GGUF order).
+uint32_t repacked_layout(int weight) {
+    return weight == SYN_Q4_K ? SYN_LAYOUT_X8 : weight == SYN_Q8_0 || weight == SYN_Q4_0 ? SYN_LAYOUT_SPLIT : 0;
+}
+
 // The plan of a key and shape this provider serves, or false (query answers None).  Gemv and
 // MoeGrouped follow the reference's bindings (kernels-cpu/src/gemv/entry.rs:35-66,
 // moe/entry.rs:33-56); MoeRoute and MoeCombine their IR signatures
 // (crates/graph/src/ir/signature.rs:149,153).
 bool plan_of(const Key& k, const Shape& s, Plan& p) {
     if (k.variant != 0 || !k.rest_plain_f32) return false;
-    // layout 1 (X8, from repack) is served for the dense products' Q4_K weights only
-    if (k.layout != 0 && !(k.layout == SYN_LAYOUT_X8 && dense(k.op) && k.weight == SYN_Q4_K)) return false;
+    // the repacked layouts are served for the dense products' weights only: 1 (X8) for Q4_K,
+    // 2 (SPLIT) for Q8_0 and Q4_0
+    if (k.layout != 0 && !(dense(k.op) && k.layout == repacked_layout(k.weight))) return false;
     p.op = k.op;
     p.rows = s.rows;
     p.layout = k.layout;
@@ -526,8 +532,10 @@ std::string ops_json() {
                              "{\"Plain\":\"BF16\"}"};
     for (const char* op : dense_ops)
         for (const char* w : weights)
-            for (int layout = 0; layout < 2; ++layout) {
-                if (layout == 1 && std::string(w) != "{\"Ggml\":\"Q4_K\"}") continue;
+            for (int layout = 0; layout < 3; ++layout) {
+                const std::string ws(w);
+                if (layout == 1 && ws != "{\"Ggml\":\"Q4_K\"}") continue;
+                if (layout == 2 && ws != "{\"Ggml\":\"Q8_0\"}" && ws != "{\"Ggml\":\"Q4_0\"}") continue;
                 out += std::string("{\"op\":") + op + ",\"schemes\":[" + w +
                        ",{\"Plain\":\"F32\"},{\"Plain\":\"F32\"}],\"layout\":" + std::to_string(layout) +
                        ",\"variant\":0},";
@@ -1075,12 +1083,14 @@ SynStatus e_set_resident(void*, uint64_t ctx, const SynBuffer*, size_t, uint32_t
     return call("set_resident", false, [&] { ctx_of(ctx); });
 }
 
-// Gemv's Q4_K weights are repacked to layout 1 (X8: each run of eight super-blocks stored
-// chunk-major, a permutation of the bytes, so the same length); every other op's weights keep
-// their GGUF layout (LayoutVersion SOURCE, `present` 0).
-bool repacks(const uint8_t* op, size_t op_len) {
+// The dense products' Q4_K weights are repacked to layout 1 (X8: each run of eight super-blocks
+// stored chunk-major), their Q8_0 and Q4_0 weights to layout 2 (SPLIT: every block's codes, then
+// every block's F16 scale).  Both are permutations of the bytes, so the same length.  Every other
+// op's weights keep their GGUF layout (LayoutVersion SOURCE, `present` 0).
+uint32_t repack_target(const uint8_t* op, size_t op_len, int* weight) {
     const Key k = parse_key(op, op_len);
-    return dense(k.op) && k.weight == SYN_Q4_K && k.layout == 0;
+    *weight = k.weight;
+    return dense(k.op) && k.layout == 0 ? repacked_layout(k.weight) : 0;
 }
 SynStatus e_repack(void*, const uint8_t* op, size_t op_len, const uint8_t* src, size_t src_len, uint8_t* dst,
                    size_t dst_len, uint32_t* present, uint32_t* layout) {
@@ -1088,18 +1098,27 @@ SynStatus e_repack(void*, const uint8_t* op, size_t op_len, const uint8_t* src, 
         if (!present || !layout) internal("repack: null output");
         *present = 0;
         *layout = 0;
-        if (!repacks(op, op_len)) return;
-        if (src_len % 144) fail(SYN_CLASS_INVALID_REQUEST, 0, "repack: the bytes are not whole Q4_K super-blocks");
+        int weight = 0;
+        const uint32_t to = repack_target(op, op_len, &weight);
+        if (to == 0) return;
         if (dst_len < src_len) fail(SYN_CLASS_INVALID_REQUEST, 0, "repack: the destination is shorter than the source");
-        check_syn(syn_q4k_repack_host(SYN_LAYOUT_X8, src, dst, src_len, 0), "repack");
+        if (to == SYN_LAYOUT_X8) {
+            if (src_len % 144) fail(SYN_CLASS_INVALID_REQUEST, 0, "repack: the bytes are not whole Q4_K super-blocks");
+            check_syn(syn_q4k_repack_host(SYN_LAYOUT_X8, src, dst, src_len, 0), "repack");
+        } else {
+            if (src_len % (weight == SYN_Q8_0 ? 34 : 18))
+                fail(SYN_CLASS_INVALID_REQUEST, 0, "repack: the bytes are not whole 32-value blocks");
+            check_syn(syn_split_repack_host(SYN_LAYOUT_SPLIT, weight, src, dst, src_len, 0), "repack");
+        }
         *present = 1;
-        *layout = SYN_LAYOUT_X8;
+        *layout = to;
     });
 }
 SynStatus e_repacked_len(void*, const uint8_t* op, size_t op_len, uint64_t src, uint32_t* present, uint64_t* out) {
     return call("repacked_len", false, [&] {
         if (!present || !out) internal("repacked_len: null output");
-        *present = repacks(op, op_len) ? 1 : 0;
+        int weight = 0;
+        *present = repack_target(op, op_len, &weight) != 0 ? 1 : 0;
         *out = *present ? src : 0;
     });
 }

@@ -46,14 +46,15 @@ class GemvError(ValueError):
         self.kind = kind
 
 
-LAYOUT_SOURCE, LAYOUT_X8 = 0, 1
+LAYOUT_SOURCE, LAYOUT_X8, LAYOUT_SPLIT = 0, 1, 2
 
 
 @dataclass
 class Weights:
     """`n_out` rows of `k_in` weights of type `ty` in GGUF block layout, in device memory
     (gemv.rs:157-224).  `bytes` is a uint8 device tensor holding exactly the matrix; `layout` is
-    LAYOUT_SOURCE (the GGUF order) or, for Q4_K, LAYOUT_X8 (see repack)."""
+    LAYOUT_SOURCE (the GGUF order), for Q4_K LAYOUT_X8, for Q8_0 and Q4_0 LAYOUT_SPLIT (see
+    repack)."""
 
     ty: WeightType
     bytes: torch.Tensor
@@ -114,18 +115,27 @@ def gemv_quantized(w: Weights, ws: torch.Tensor, rows: int, y: torch.Tensor, str
     need = rows * w.n_out
     if y.numel() < need:
         raise GemvError("Len", f"`y` holds {y.numel()} values, the op needs {need}")
-    call("syn_gemv_quantized", int(w.ty), w.bytes.data_ptr(), w.bytes.numel(), w.n_out, w.k_in,
-         ws.data_ptr(), ws.numel(), rows, y.data_ptr(), _stream(stream))
+    call("syn_gemv_quantized_layout", w.layout, int(w.ty), w.bytes.data_ptr(), w.bytes.numel(), w.n_out,
+         w.k_in, ws.data_ptr(), ws.numel(), rows, y.data_ptr(), _stream(stream))
 
 
-def repack(w: Weights, layout: int = LAYOUT_X8, stream=None) -> Weights:
+def repack(w: Weights, layout: int | None = None, stream=None) -> Weights:
     """The matrix in another layout (a permutation of its bytes, crates/kernels/src/provider.rs:
     326-336 repack): LAYOUT_X8 stores each run of eight Q4_K super-blocks chunk-major, so the
-    decode kernel reads whole 128-byte lines."""
-    if w.ty is not WeightType.Q4K or layout != LAYOUT_X8 or w.layout != LAYOUT_SOURCE:
-        raise GemvError("Activations", "repack takes Q4_K weights in the source layout to LAYOUT_X8")
+    decode kernel reads whole 128-byte lines; LAYOUT_SPLIT stores every Q8_0 / Q4_0 block's codes
+    first and every block's F16 scale after them, so the codes stream in 16-byte loads."""
+    if layout is None:
+        layout = LAYOUT_X8 if w.ty is WeightType.Q4K else LAYOUT_SPLIT
+    if w.layout != LAYOUT_SOURCE:
+        raise GemvError("Activations", "repack takes weights in the source layout")
     out = torch.empty_like(w.bytes)
-    call("syn_q4k_repack", layout, w.bytes.data_ptr(), out.data_ptr(), w.bytes.numel(), 0, _stream(stream))
+    if w.ty is WeightType.Q4K and layout == LAYOUT_X8:
+        call("syn_q4k_repack", layout, w.bytes.data_ptr(), out.data_ptr(), w.bytes.numel(), 0, _stream(stream))
+    elif w.ty in (WeightType.Q8_0, WeightType.Q4_0) and layout == LAYOUT_SPLIT:
+        call("syn_split_repack", layout, int(w.ty), w.bytes.data_ptr(), out.data_ptr(), w.bytes.numel(), 0,
+             _stream(stream))
+    else:
+        raise GemvError("Activations", "repack takes Q4_K to LAYOUT_X8 and Q8_0 / Q4_0 to LAYOUT_SPLIT")
     return Weights(w.ty, out, w.n_out, w.k_in, layout)
 
 
@@ -300,6 +310,6 @@ def dequantize(ty: WeightType, src: torch.Tensor, stream=None) -> torch.Tensor:
 
 
 __all__ = ["WeightType", "Weights", "GemvError", "SynError", "GemvBatch", "workspace_bytes", "quantize_into",
-           "repack", "LAYOUT_SOURCE", "LAYOUT_X8",
+           "repack", "LAYOUT_SOURCE", "LAYOUT_X8", "LAYOUT_SPLIT",
            "gemv_quantized", "gemv", "quantize", "dequantize", "new_workspace", "gemm_workspace",
            "gemm_quantize_into", "gemm_quantized", "gate_up_act", "lib"]

@@ -91,3 +91,27 @@ def test_x8_host_repack_is_its_definition_and_inverts():
         assert (back == b).all()
     assert lib.syn_q4k_repack_host(2, b.ctypes.data, got.ctypes.data, b.size, 0) == 2
     assert lib.syn_q4k_repack_host(1, b.ctypes.data, got.ctypes.data, 100, 0) == 1
+
+
+def test_split_host_repack_is_its_definition_and_inverts():
+    """The host repack of the SPLIT layout (every block's codes, then every block's F16 scale)
+    against its definition, and the inverse, for Q8_0 (34-byte blocks) and Q4_0 (18)."""
+    import numpy as np
+    import torch  # noqa: F401
+    lib = ctypes.CDLL(LIB)
+    lib.syn_split_repack_host.argtypes = [ctypes.c_uint32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+                                          ctypes.c_uint64, ctypes.c_int32]
+    for ty, bb in ((8, 34), (2, 18)):
+        for nblk in (1, 7, 64, 129):
+            b = np.random.default_rng(nblk + ty).integers(0, 256, nblk * bb, dtype=np.uint8)
+            blocks = b.reshape(nblk, bb)
+            want = np.concatenate([blocks[:, 2:].ravel(), blocks[:, :2].ravel()])
+            got = np.empty_like(b)
+            assert lib.syn_split_repack_host(2, ty, b.ctypes.data, got.ctypes.data, b.size, 0) == 0
+            assert (got == want).all()
+            back = np.empty_like(b)
+            assert lib.syn_split_repack_host(2, ty, got.ctypes.data, back.ctypes.data, b.size, 1) == 0
+            assert (back == b).all()
+        assert lib.syn_split_repack_host(1, ty, b.ctypes.data, got.ctypes.data, b.size, 0) == 2
+        assert lib.syn_split_repack_host(2, ty, b.ctypes.data, got.ctypes.data, b.size - 1, 0) == 1
+    assert lib.syn_split_repack_host(2, 12, b.ctypes.data, got.ctypes.data, 144, 0) == 2

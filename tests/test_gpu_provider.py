@@ -107,26 +107,30 @@ def test_gemv_through_the_provider(cx, ty, rows, n_out, k):
     assert_same(got, o.gemv(ty, w, n_out, k, x, rows, threads=8), "provider gemv")
 
 
-@pytest.mark.parametrize("rows,n_out,k", [(1, 4096, 4096), (1, 1000, 14336), (64, 256, 4096)])
-def test_gemv_x8_layout_through_the_provider(cx, rows, n_out, k):
-    """The core's path for repacked weights: repacked_len / repack on the host bytes, then the
-    Gemv key with the layout repack returned; outputs equal the oracle on the source bytes."""
+@pytest.mark.parametrize("ty,rows,n_out,k,want_layout", [
+    (o.Q4_K, 1, 4096, 4096, 1), (o.Q4_K, 1, 1000, 14336, 1), (o.Q4_K, 64, 256, 4096, 1),
+    (o.Q8_0, 1, 4096, 4096, 2), (o.Q8_0, 5, 1000, 14336, 2), (o.Q8_0, 40, 300, 4096, 2),
+    (o.Q4_0, 1, 4096, 4096, 2), (o.Q4_0, 11, 513, 1024, 2)])
+def test_gemv_repacked_layout_through_the_provider(cx, ty, rows, n_out, k, want_layout):
+    """The core's path for repacked weights: repacked_len / repack on the host bytes (Q4_K to
+    layout 1, Q8_0 and Q4_0 to layout 2), then the Gemv key with the layout repack returned;
+    outputs equal the oracle on the source bytes."""
     P, pr = cx.P, cx.pr
-    rng = GemvRng(rows * 7 + n_out)
-    w = gemv_weights(rng, o.Q4_K, n_out, k, o.f16_bits, o.round_bf16)
+    rng = GemvRng(rows * 7 + n_out + ty)
+    w = gemv_weights(rng, ty, n_out, k, o.f16_bits, o.round_bf16)
     x = gemv_activations(rng, rows, k)
-    src_key = gemv_key(o.Q4_K)
+    src_key = gemv_key(ty)
     kb = json.dumps(src_key).encode()
     kbuf = (C.c_uint8 * len(kb)).from_buffer_copy(kb)
     present, layout = C.c_uint32(), C.c_uint32()
     dst = np.zeros_like(w)
     st = pr.vt.repack(pr.vt.slf, kbuf, len(kb), w.ctypes.data_as(C.POINTER(C.c_uint8)), w.size,
                       dst.ctypes.data_as(C.POINTER(C.c_uint8)), dst.size, C.byref(present), C.byref(layout))
-    assert st.cls == 0 and (present.value, layout.value) == (1, 1)
+    assert st.cls == 0 and (present.value, layout.value) == (1, want_layout)
     key = dict(src_key, layout=layout.value)
-    announce(f"provider gemv x8 rows={rows} n_out={n_out} k={k}")
+    announce(f"provider gemv layout {want_layout} ty={ty} rows={rows} n_out={n_out} k={k}")
     caps = pr.query(cx.ctx, key, shape(rows, n_out, k))
-    assert caps is not None and caps["layout"] == 1
+    assert caps is not None and caps["layout"] == want_layout
     op = pr.prepare(cx.ctx, key, shape(rows, n_out, k))
     wd = dev(dst)
     xb, yb = cx.put(x.astype(np.float32)), cx.empty(4 * rows * n_out)
@@ -134,7 +138,7 @@ def test_gemv_x8_layout_through_the_provider(cx, rows, n_out, k):
                      [P.view(wd.data_ptr(), dst.nbytes)], cx.workspace(op))
     pr.launch(cx.ctx, cx.s, op, args)
     got = cx.get(yb, np.float32, (rows, n_out))
-    assert_same(got, o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=8), "provider gemv x8")
+    assert_same(got, o.gemv(ty, w, n_out, k, x, rows, threads=8), f"provider gemv layout {want_layout}")
 
 
 def dense_key(op, ty, layout=0):
@@ -165,7 +169,8 @@ def test_gemm_and_logits_keys_take_the_gemv_binding(cx, op, ty, rows, n_out, k):
 
 @pytest.mark.parametrize("ty,rows,n,k,layout", [(o.Q4_K, 1, 1536, 4096, 0), (o.Q4_K, 40, 512, 2048, 0),
                                                 (o.Q4_K, 1, 1024, 4096, 1), (o.Q8_0, 3, 700, 1024, 0),
-                                                (o.Q4_0, 1, 256, 512, 0)])
+                                                (o.Q4_0, 1, 256, 512, 0), (o.Q8_0, 1, 700, 1024, 2),
+                                                (o.Q8_0, 12, 300, 2048, 2), (o.Q4_0, 4, 256, 512, 2)])
 def test_gate_up_act_through_the_provider(cx, ty, rows, n, k, layout):
     """GateUpAct{Silu}: one weight of 2 n rows, gate then up (mapping.rs:31); y [rows, n]."""
     P, pr = cx.P, cx.pr
@@ -180,7 +185,7 @@ def test_gate_up_act_through_the_provider(cx, ty, rows, n, k, layout):
         present, lay = C.c_uint32(), C.c_uint32()
         st = pr.vt.repack(pr.vt.slf, kbuf, len(kb), w.ctypes.data_as(C.POINTER(C.c_uint8)), w.size,
                           wl.ctypes.data_as(C.POINTER(C.c_uint8)), wl.size, C.byref(present), C.byref(lay))
-        assert st.cls == 0 and (present.value, lay.value) == (1, 1)
+        assert st.cls == 0 and (present.value, lay.value) == (1, layout)
     key = dense_key({"GateUpAct": {"act": "Silu"}}, ty, layout)
     announce(f"provider gate_up_act ty={ty} rows={rows} n={n} k={k} layout={layout}")
     assert pr.query(cx.ctx, key, shape(rows, n, k)) is not None
@@ -224,6 +229,8 @@ def test_query_answers_none_for_unserved_shapes(cx):
     gelu = dense_key({"GateUpAct": {"act": "Gelu"}}, o.Q4_K)
     assert pr.query(cx.ctx, gelu, shape(1, 64, 256)) is None  # no reference form of GELU gating
     assert pr.query(cx.ctx, dict(gemv_key(o.Q8_0), layout=1), shape(1, 64, 256)) is None
+    assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=2), shape(1, 64, 256)) is None
+    assert pr.query(cx.ctx, dict(gemv_key(o.Q8_0), layout=2), shape(130, 64, 256)) is not None
     assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(9, 64, 1536)) is None  # GEMM: k % 2048
     assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(8, 64, 1536)) is not None  # 2..8 rows
     assert pr.query(cx.ctx, {"op": "Attention", "schemes": [], "layout": 0, "variant": 0},

@@ -96,6 +96,32 @@ def test_x8_single_row_rows_active(cx, active):
     check_rows(got, want, active, "x8")
 
 
+@pytest.mark.parametrize("ty,bucket,active", [(o.Q8_0, 1, 0), (o.Q8_0, 12, 9), (o.Q8_0, 40, 17),
+                                              (o.Q8_0, 40, 3), (o.Q4_0, 12, 10)])
+def test_split_layout_rows_active(cx, ty, bucket, active):
+    """Layout 2 (SPLIT): the split decode kernel in eight-row launches and the int8 GEMM."""
+    import ctypes as C
+    import json
+    P, pr = cx.P, cx.pr
+    rng = GemvRng(77 * ty + bucket + active)
+    n_out, k = 200, 1024
+    w = gemv_weights(rng, ty, n_out, k, o.f16_bits, o.round_bf16)
+    x = gemv_activations(rng, bucket, k).reshape(bucket, k)
+    kb = json.dumps(gemv_key(ty)).encode()
+    kbuf = (C.c_uint8 * len(kb)).from_buffer_copy(kb)
+    present, lay = C.c_uint32(), C.c_uint32()
+    wl = np.zeros_like(w)
+    pr.vt.repack(pr.vt.slf, kbuf, len(kb), w.ctypes.data_as(C.POINTER(C.c_uint8)), w.size,
+                 wl.ctypes.data_as(C.POINTER(C.c_uint8)), wl.size, C.byref(present), C.byref(lay))
+    assert lay.value == 2
+    _, step = step_desc(cx, active)
+    announce(f"rows_active split ty={ty} bucket={bucket} active={active}")
+    got = dense_launch(cx, dict(gemv_key(ty), layout=2), bucket, n_out, k, wl, x, step)
+    a = min(active, bucket)
+    want = o.gemv(ty, w, n_out, k, x[:a], a, threads=8) if a else None
+    check_rows(got, want, active, f"split ty={ty}")
+
+
 def test_gate_up_act_rows_active(cx):
     rng = GemvRng(515)
     n, k, bucket, active = 300, 1024, 4, 2

@@ -158,6 +158,7 @@ def test_build_and_ops_json(pr):
     ops = pr.ops()
     got = {(json.dumps(k["op"]), json.dumps(k["schemes"][0]), k["layout"]) for k in ops}
     weights = [('{"Ggml": "Q4_K"}', 0), ('{"Ggml": "Q4_K"}', 1), ('{"Ggml": "Q8_0"}', 0), ('{"Ggml": "Q4_0"}', 0),
+               ('{"Ggml": "Q8_0"}', 2), ('{"Ggml": "Q4_0"}', 2),
                ('{"Ggml": "F16"}', 0), ('{"Ggml": "BF16"}', 0), ('{"Plain": "F16"}', 0), ('{"Plain": "BF16"}', 0)]
     dense = {(op, w, l) for op in ('"Gemv"', '"Gemm"', '"Logits"', '{"GateUpAct": {"act": "Silu"}}')
              for w, l in weights}
@@ -245,7 +246,8 @@ def test_repack_of_q4k_gemv_is_the_x8_permutation(pr):
         db = (C.c_uint8 * len(kd)).from_buffer_copy(kd)
         assert pr.vt.repacked_len(pr.vt.slf, db, len(kd), src.size, C.byref(present), C.byref(n)).cls == 0
         assert (present.value, n.value) == (1, src.size)
-    for other in (_key("Gemv", "Q8_0"), _key("MoeGrouped", "Q4_K"), _key("MoeCombine", None)):
+    for other in (_key("Gemv", "F16"), _key("MoeGrouped", "Q4_K"), _key("MoeGrouped", "Q8_0"),
+                  _key("MoeCombine", None)):
         ob = (C.c_uint8 * len(other)).from_buffer_copy(other)
         assert pr.vt.repacked_len(pr.vt.slf, ob, len(other), 144, C.byref(present), C.byref(n)).cls == 0
         assert (present.value, n.value) == (0, 0)
@@ -253,6 +255,32 @@ def test_repack_of_q4k_gemv_is_the_x8_permutation(pr):
         assert (present.value, layout.value) == (0, 0)
     bad = pr.vt.repack(pr.vt.slf, kb, len(key), sp, 100, dp, 100, C.byref(present), C.byref(layout))
     assert bad.cls == 1 and "super-blocks" in pr.message()
+
+
+@pytest.mark.parametrize("wname,bb", [("Q8_0", 34), ("Q4_0", 18)])
+def test_repack_of_q8_0_and_q4_0_dense_weights_is_the_split_layout(pr, wname, bb):
+    """The dense products' Q8_0 and Q4_0 weights repack to layout 2 (every block's codes, then
+    every block's F16 scale, the same length)."""
+    import numpy as np
+    nblk = 37
+    src = np.random.default_rng(bb).integers(0, 256, nblk * bb, dtype=np.uint8)
+    blocks = src.reshape(nblk, bb)
+    want = np.concatenate([blocks[:, 2:].ravel(), blocks[:, :2].ravel()])
+    present, layout, n = C.c_uint32(7), C.c_uint32(7), C.c_uint64(7)
+    sp = src.ctypes.data_as(C.POINTER(C.c_uint8))
+    for op in ("Gemv", "Gemm", "Logits", {"GateUpAct": {"act": "Silu"}}):
+        key = _key(op, wname)
+        kb = (C.c_uint8 * len(key)).from_buffer_copy(key)
+        assert pr.vt.repacked_len(pr.vt.slf, kb, len(key), src.size, C.byref(present), C.byref(n)).cls == 0
+        assert (present.value, n.value) == (1, src.size)
+        dst = np.zeros_like(src)
+        dp = dst.ctypes.data_as(C.POINTER(C.c_uint8))
+        assert pr.vt.repack(pr.vt.slf, kb, len(key), sp, src.size, dp, dst.size, C.byref(present),
+                            C.byref(layout)).cls == 0
+        assert (present.value, layout.value) == (1, 2)
+        assert (dst == want).all()
+    bad = pr.vt.repack(pr.vt.slf, kb, len(key), sp, src.size - 1, dp, dst.size, C.byref(present), C.byref(layout))
+    assert bad.cls == 1 and "32-value blocks" in pr.message()
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the behaviour on a host without a GPU")
