@@ -1,0 +1,94 @@
+"""The SPLIT weight layout of Q8_0 and Q4_0 matrices (every block's codes, then every block's F16
+scale): the device repack is its definition and inverts exactly, and the split decode kernel
+(1 to 8 rows, eight at a time beyond) and the int8 matrix-core GEMM (Q8_0, 9 rows or more) give
+the oracle's Gemv values bit for bit (crates/kernels-cpu/src/gemv.rs:435-492)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce, assert_same, dev, host, require_gpu
+from oracle import oracle as o
+from refgen import GemvRng, gemv_activations, gemv_weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def S():
+    require_gpu()
+    import syntropy_amd.gemv as S
+    return S
+
+
+WT = {o.Q8_0: "Q8_0", o.Q4_0: "Q4_0"}
+
+
+def split_numpy(b, bb):
+    blocks = b.reshape(-1, bb)
+    return np.concatenate([blocks[:, 2:].ravel(), blocks[:, :2].ravel()])
+
+
+@pytest.mark.parametrize("ty,bb", [(o.Q8_0, 34), (o.Q4_0, 18)])
+@pytest.mark.parametrize("nblk", [1, 255, 256, 257, 4096 + 3])
+def test_split_repack_matches_definition_and_inverts(S, ty, bb, nblk):
+    rs = np.random.default_rng(nblk * ty)
+    b = rs.integers(0, 256, nblk * bb, dtype=np.uint8)
+    W = S.Weights(S.WeightType(ty), dev(b), nblk, 32)
+    announce(f"split repack ty={ty} {nblk} blocks")
+    r = S.repack(W)
+    assert r.layout == S.LAYOUT_SPLIT
+    got = host(r.bytes)
+    assert (got == split_numpy(b, bb)).all()
+    back = torch.empty_like(r.bytes)
+    assert S.lib().syn_split_repack(2, ty, r.bytes.data_ptr(), back.data_ptr(), r.bytes.numel(), 1, None) == 0
+    torch.cuda.synchronize()
+    assert (host(back) == b).all()
+
+
+def check(S, ty, n_out, k, rows, seed, w=None):
+    rng = GemvRng(seed)
+    if w is None:
+        w = gemv_weights(rng, ty, n_out, k, o.f16_bits, o.round_bf16)
+    x = gemv_activations(rng, rows, k)
+    W = S.repack(S.Weights(S.WeightType(ty), dev(w), n_out, k))
+    announce(f"split gemv {WT[ty]} {n_out}x{k} rows={rows}")
+    y = torch.full((rows, n_out), float("nan"), device="cuda")
+    S.gemv(W, dev(x.astype(np.float32)), rows, y=y)
+    want = o.gemv(ty, w, n_out, k, x, rows, threads=8)
+    assert_same(host(y), want, f"{WT[ty]} {n_out}x{k} rows {rows}")
+    if rows in (1, 9):  # the product alone over rows quantized beforehand
+        ws = S.new_workspace(S.WeightType(ty), rows, k)
+        S.quantize_into(S.WeightType(ty), dev(x.astype(np.float32)), rows, k, ws)
+        y.fill_(float("nan"))
+        S.gemv_quantized(W, ws, rows, y)
+        assert_same(host(y), want, f"{WT[ty]} quantized rows {rows}")
+    return w
+
+
+@pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0])
+@pytest.mark.parametrize("n_out,k", [(37, 32), (300, 1024), (41, 3072), (9, 14336), (130, 16384 + 32)])
+def test_split_decode_rows_equal_oracle(S, ty, n_out, k):
+    """1 to 8 rows (staged activations for narrow rows, global reads for wide ones), 9 and 20 rows
+    (eight-row groups for Q4_0, the GEMM for Q8_0); row lengths of 1 to 513 blocks, partial
+    last load groups and row counts not multiples of eight."""
+    w = None
+    for rows in (1, 2, 3, 5, 8, 9, 20):
+        w = check(S, ty, n_out, k, rows, 1000 * rows + n_out + k + ty, w)
+
+
+@pytest.mark.parametrize("ty,n_out,k,rowss", [
+    (o.Q8_0, 14336, 4096, [1, 8, 32, 128]),  # Q8_0 decode and prefill of the 14336 x 4096 matrix
+    (o.Q4_0, 4096, 4096, [1, 4]),            # the Q4_0 4096 x 4096 decode
+])
+def test_split_config_shapes_equal_oracle(S, ty, n_out, k, rowss):
+    x = o.normal(0x5E11 + k, 0.02, n_out * k)
+    w = o.quantize(ty, x)
+    for rows in rowss:
+        check(S, ty, n_out, k, rows, 0x5E12 + rows, w)
+
+
+def test_split_gemm_edges_equal_oracle(S):
+    """The GEMM's clamped tiles: weight rows not multiples of 16 (or 64), token counts not
+    multiples of 32, one-block rows, many tiles of tokens."""
+    for n_out, k, rows in ((1, 32, 9), (17, 64, 33), (63, 96, 31), (65, 256, 100), (200, 2048, 257)):
+        check(S, o.Q8_0, n_out, k, rows, n_out * 31 + rows)
