@@ -12,9 +12,8 @@
 // folds activation row r's terms in block order.
 //
 // 9 or more rows, Q8_0 (k_gemm_q8_split): v_mfma_i32_16x16x32_i8 takes one 32-value block of 16
-// tokens (A) against 16 weight rows (B): the exact I32 sums of 256 outputs, which the lane owning
-// each output scales and folds (one term per block, in block order).  A wavefront covers 16
-// weight rows x 32 tokens.
+// weight rows against 16 tokens: the exact I32 sums of 256 outputs, which the lane owning each
+// output scales and folds (one term per block, in block order).
 #include <type_traits>
 
 #include "common.hpp"
@@ -215,9 +214,93 @@ void launch_gemv_split(int ty, const uint8_t* W, int n_out, int k, const uint8_t
 }
 
 // ---- 9 or more rows, Q8_0: the int8 matrix cores --------------------------------------------------
+//
+// A wavefront owns 16 weight rows x 16 TT tokens.  Per block, v_mfma_i32_16x16x32_i8 takes the
+// rows' codes as A (lane c: row c's 8 codes at 8 p of the block, p = lane / 16) and the tokens'
+// codes as B (lane c: token c's codes at 8 p): lane (c, p) receives the exact sums of rows 4 p + i
+// against token c, scales them by (dw * dx) and adds them to its accumulators in block order.
+// Loads come in groups of four blocks, the next group's issued before the current one's
+// arithmetic; with whole pairs of groups (nb % 8 == 0) a lane reads a row's four scales and a
+// token's four activation scales with one load each.  The workgroup's wavefronts share the 16 rows and take
+// consecutive token tiles, so the rows' codes are fetched once into the caches.
 
-constexpr int GQ_TT = 2;  // 16-token groups per wavefront
+constexpr int GQ_G = 4;  // blocks per load group
 
+template <int TT>
+struct GqGroup {
+    long w[GQ_G];        // row c's codes, 8 bytes of each block
+    uint32_t sc[4][2];   // rows 4 p + i: four F16 scales
+    long a[TT][GQ_G];    // token c of tile tt: 8 codes of each block
+    float dx[TT][GQ_G];  // token c of tile tt: each block's scale
+};
+
+template <int TT, bool VEC>
+__device__ __forceinline__ void gq_load(GqGroup<TT>& g, const uint8_t* wrow, const uint16_t* const* srow,
+                                        const int8_t* const* xa, const float* const* xdt, int b0, int nb) {
+    if constexpr (VEC) {  // a whole group, 8- and 16-byte aligned
+#pragma unroll
+        for (int j = 0; j < GQ_G; ++j) g.w[j] = *reinterpret_cast<const long*>(wrow + 32 * (b0 + j));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint2 v = *reinterpret_cast<const uint2*>(srow[i] + b0);
+            g.sc[i][0] = v.x;
+            g.sc[i][1] = v.y;
+        }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+#pragma unroll
+            for (int j = 0; j < GQ_G; ++j) g.a[t][j] = *reinterpret_cast<const long*>(xa[t] + 32 * (b0 + j));
+            const float4 d = *reinterpret_cast<const float4*>(xdt[t] + b0);
+            g.dx[t][0] = d.x;
+            g.dx[t][1] = d.y;
+            g.dx[t][2] = d.z;
+            g.dx[t][3] = d.w;
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < GQ_G; ++j) {
+        const bool ok = b0 + j < nb;
+        g.w[j] = ok ? *reinterpret_cast<const long*>(wrow + 32 * (b0 + j)) : 0;
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            g.a[t][j] = ok ? *reinterpret_cast<const long*>(xa[t] + 32 * (b0 + j)) : 0;
+            g.dx[t][j] = ok ? xdt[t][b0 + j] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t h[GQ_G];
+#pragma unroll
+        for (int j = 0; j < GQ_G; ++j) h[j] = b0 + j < nb ? srow[i][b0 + j] : 0u;
+        g.sc[i][0] = h[0] | (h[1] << 16);
+        g.sc[i][1] = h[2] | (h[3] << 16);
+    }
+}
+
+// The arithmetic of one group: the group's MFMAs first, then each block's terms in block order.
+template <int TT, bool VEC>
+__device__ __forceinline__ void gq_compute(const GqGroup<TT>& g, float (&acc)[TT][4], int b0, int nb) {
+    const v4i_s z = {0, 0, 0, 0};
+    v4i_s d[GQ_G][TT];
+#pragma unroll
+    for (int j = 0; j < GQ_G; ++j)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) d[j][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(g.w[j], g.a[t][j], z, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < GQ_G; ++j) {
+        if (!VEC && b0 + j >= nb) break;  // uniform
+        float dw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dw[i] = f16_to_f32((uint16_t)(g.sc[i][j >> 1] >> (16 * (j & 1))));
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][i] = acc[t][i] + (dw[i] * g.dx[t][j]) * (float)d[j][t][i];
+    }
+}
+
+template <int TT, bool VEC>
 __global__ __launch_bounds__(256) void k_gemm_q8_split(const uint8_t* __restrict__ W, int n_out, int k,
                                                        const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                        int T, float* __restrict__ y,
@@ -225,76 +308,287 @@ __global__ __launch_bounds__(256) void k_gemm_q8_split(const uint8_t* __restrict
     T = active_rows(active, 0, T);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, p = lane >> 4;
-    const int row0 = ((int)blockIdx.x * 4 + wave) * 16;
-    const int t0 = (int)blockIdx.y * 16 * GQ_TT;
-    if (row0 >= n_out || t0 >= T) return;  // uniform per wavefront; no barrier below
+    const int row0 = (int)blockIdx.x * 16;
+    const int t0 = ((int)blockIdx.y * (int)(blockDim.x >> 6) + wave) * 16 * TT;
+    if (t0 >= T) return;  // uniform per wavefront; no barrier below
     const int nb = k / 32;
     const uint64_t nblocks = (uint64_t)n_out * nb;
-    const int wr = row0 + c < n_out ? row0 + c : n_out - 1;  // B column c: weight row (clamped)
-    const uint8_t* wcodes = W + (uint64_t)wr * nb * 32 + 8 * p;
-    const uint16_t* wsc = reinterpret_cast<const uint16_t*>(W + 32 * nblocks) + (uint64_t)wr * nb;
-    const int8_t* xa[GQ_TT];
-    const float* xdt[GQ_TT][4];
+    const int wr = row0 + c < n_out ? row0 + c : n_out - 1;  // A row c: weight row (clamped)
+    const uint8_t* wrow = W + (uint64_t)wr * nb * 32 + 8 * p;
+    const uint16_t* scales = reinterpret_cast<const uint16_t*>(W + 32 * nblocks);
+    const uint16_t* srow[4];
 #pragma unroll
-    for (int tt = 0; tt < GQ_TT; ++tt) {
-        const int ta = t0 + 16 * tt + c;  // A row c: token (clamped)
-        xa[tt] = xq + (int64_t)(ta < T ? ta : T - 1) * k + 8 * p;
+    for (int i = 0; i < 4; ++i) {
+        const int r = row0 + 4 * p + i;  // the lane's output rows (clamped)
+        srow[i] = scales + (uint64_t)(r < n_out ? r : n_out - 1) * nb;
+    }
+    const int8_t* xa[TT];
+    const float* xdt[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        const int tok = t0 + 16 * t + c;  // B column c: token (clamped)
+        const int tc = tok < T ? tok : T - 1;
+        xa[t] = xq + (int64_t)tc * k + 8 * p;
+        xdt[t] = xd + (int64_t)tc * nb;
+    }
+    float acc[TT][4];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = 0.0f;
+    // two groups in registers, each loaded while the other one's arithmetic runs.  The loads are
+    // unconditional (a group past the row reloads the current one), so that the wait before each
+    // group's arithmetic counts only the other group's loads.
+    // With VEC the row holds whole pairs of groups (nb % 8 == 0) and nothing is conditional.
+    GqGroup<TT> ga, gb;
+    gq_load<TT, VEC>(ga, wrow, srow, xa, xdt, 0, nb);
+    for (int b0 = 0; b0 < nb; b0 += 2 * GQ_G) {
+        const bool second = VEC || b0 + GQ_G < nb;
+        gq_load<TT, VEC>(gb, wrow, srow, xa, xdt, second ? b0 + GQ_G : b0, nb);
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the arithmetic
+        gq_compute<TT, VEC>(ga, acc, b0, nb);
+        __builtin_amdgcn_sched_barrier(0);
+        gq_load<TT, VEC>(ga, wrow, srow, xa, xdt, b0 + 2 * GQ_G < nb ? b0 + 2 * GQ_G : b0, nb);
+        __builtin_amdgcn_sched_barrier(0);
+        if (second) gq_compute<TT, VEC>(gb, acc, b0 + GQ_G, nb);
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        const int tok = t0 + 16 * t + c;
+        if (tok >= T) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int to = t0 + 16 * tt + 4 * p + i;  // the lane's output tokens
-            xdt[tt][i] = xd + (int64_t)(to < T ? to : T - 1) * nb;
+            const int r = row0 + 4 * p + i;
+            if (r < n_out) y[(int64_t)tok * n_out + r] = acc[t][i];
         }
     }
-    float acc[GQ_TT][4];
+}
+
+// ---- the staged GEMM: weights, codes and scales streamed into an LDS ring -------------------------
+//
+// A workgroup takes 32 weight rows (two wavefront row groups of 16) x TW = 16 TT TG tokens (TG
+// token groups of 16 TT), stage by stage: four blocks of every operand are copied into LDS by
+// global_load_lds while earlier stages compute.  Stage layout (bytes):
+//   codes of the rows  [block j][row][32]          4096
+//   codes of the tokens [block j][token][32]       128 TW
+//   row scales         [row][block j] F16          256
+//   token scales       [token][block j] F32        16 TW
+// Each copy instruction moves 1 KB (16 bytes a lane) or, for the scales, 64 lanes of 4 bytes; a
+// wavefront issues the same number of copies every stage, so its wait is a fixed count.
+
+constexpr int QS_S = 4;    // blocks per stage
+constexpr int QS_RW = 32;  // weight rows per workgroup
+
+template <int TT, int TG>
+struct QsCfg {
+    static constexpr int NW = 2 * TG;      // wavefronts
+    static constexpr int TW = 16 * TT * TG;  // tokens
+    static constexpr int W_OFF = 0, A_OFF = QS_RW * QS_S * 32;
+    static constexpr int SC_OFF = A_OFF + TW * QS_S * 32;
+    static constexpr int DX_OFF = SC_OFF + QS_RW * QS_S * 2;
+    static constexpr int STAGE = DX_OFF + TW * QS_S * 4;
+    static constexpr int NS = STAGE * 4 <= 64 * 1024 ? 4 : 3;  // ring stages
+    static constexpr int COPIES = TG == 1 ? 5 : 4;              // copies per wavefront per stage
+};
+
+// The lane's part of its wavefront's copies: per copy a global base (advanced per stage by
+// `step` bytes), the lane's 32-bit offset, the LDS offset in the stage, 16 or 4 bytes, and whether
+// the lane takes part.
+struct QsCopy {
+    const uint8_t* base;
+    uint32_t voff, lds, step;
+    bool wide, on;
+};
+
+template <int TT, int TG>
+__device__ __forceinline__ void qs_plan(QsCopy* cp, const uint8_t* W, const uint8_t* scales,
+                                        const int8_t* xq, const float* xd, int n_out, int nb, int k, int T,
+                                        int row0, int t0, int wave, int lane) {
+    using C = QsCfg<TT, TG>;
+    const uint32_t rb = (uint32_t)nb * 32u;
+    auto wrow = [&](int r) { return (uint32_t)(row0 + r < n_out ? row0 + r : n_out - 1); };
+    auto tok = [&](int t) { return (uint32_t)(t0 + t < T ? t0 + t : T - 1); };
+    // codes of the rows, block j: lane -> row lane / 2, half lane % 2
+    auto wcopy = [&](int j) {
+        return QsCopy{W + 32 * j, wrow(lane >> 1) * rb + 16u * (uint32_t)(lane & 1),
+                      (uint32_t)(C::W_OFF + 1024 * j), 32u * QS_S, true, true};
+    };
+    // codes of the tokens, block j, tokens 32 h ..: lane -> token 32 h + lane / 2
+    auto acopy = [&](int j, int h) {
+        const int t = 32 * h + (lane >> 1);
+        return QsCopy{reinterpret_cast<const uint8_t*>(xq) + 32 * j, tok(t) * (uint32_t)k + 16u * (uint32_t)(lane & 1),
+                      (uint32_t)(C::A_OFF + C::TW * 32 * j + 1024 * h), 32u * QS_S, true, t < C::TW};
+    };
+    // row scales of rows 16 h .. (32 lanes) or all 32 rows (h < 0): lane -> row lane / 2, blocks
+    // 2 (lane % 2), +1
+    auto scopy = [&](int h) {
+        const int r = (h < 0 ? 0 : 16 * h) + (lane >> 1);
+        return QsCopy{scales, wrow(r) * (uint32_t)nb * 2u + 4u * (uint32_t)(lane & 1),
+                      (uint32_t)(C::SC_OFF + (h < 0 ? 0 : 128 * h)), 2u * QS_S, false, h < 0 || lane < 32};
+    };
+    // token scales of tokens 32 h .. (h < 0: all TW <= 64): lane -> token
+    auto dcopy = [&](int h) {
+        const int t = (h < 0 ? 0 : 32 * h) + lane;
+        return QsCopy{reinterpret_cast<const uint8_t*>(xd), tok(t) * (uint32_t)nb * 4u,
+                      (uint32_t)(C::DX_OFF + (h < 0 ? 0 : 512 * h)), 4u * QS_S, true,
+                      (h < 0 ? t < C::TW : lane < 32)};
+    };
+    if constexpr (TG == 1) {  // 10 copies: wave 0 blocks 0, 1 and the row scales, wave 1 blocks 2, 3 and dx
+        const int j0 = 2 * wave;
+        cp[0] = wcopy(j0);
+        cp[1] = wcopy(j0 + 1);
+        cp[2] = acopy(j0, 0);
+        cp[3] = acopy(j0 + 1, 0);
+        cp[4] = wave == 0 ? scopy(-1) : dcopy(-1);
+    } else {  // 16 copies: wave w block w of the rows and of both token halves, and a scale half
+        cp[0] = wcopy(wave);
+        cp[1] = acopy(wave, 0);
+        cp[2] = acopy(wave, 1);
+        cp[3] = wave < 2 ? scopy(wave) : dcopy(wave - 2);
+    }
+}
+
+template <int TT, int TG>
+__device__ __forceinline__ void qs_issue(const QsCopy* cp, uint32_t stage_lds, int s) {
 #pragma unroll
-    for (int tt = 0; tt < GQ_TT; ++tt)
+    for (int u = 0; u < QsCfg<TT, TG>::COPIES; ++u) {
+        const uint8_t* base = cp[u].base + (size_t)cp[u].step * (size_t)s;
+        if (cp[u].on) {
+            if (cp[u].wide)
+                lds_dma16(cp[u].voff, base, stage_lds + cp[u].lds);
+            else
+                lds_dma4(cp[u].voff, base, stage_lds + cp[u].lds);
+        }
+    }
+}
+
+template <int TT, int TG>
+__global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* __restrict__ W, int n_out, int k,
+                                                                 const int8_t* __restrict__ xq,
+                                                                 const float* __restrict__ xd, int T,
+                                                                 float* __restrict__ y,
+                                                                 const uint32_t* __restrict__ active) {
+    using C = QsCfg<TT, TG>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    T = active_rows(active, 0, T);
+    const int row0 = (int)blockIdx.x * QS_RW, t0 = (int)blockIdx.y * C::TW;
+    if (t0 >= T) return;  // uniform per workgroup
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: copy bases in SGPRs
+    const int c = lane & 15, p = lane >> 4;
+    const int rg = wave & 1, tg = wave >> 1;  // the wavefront's row group and token group
+    const int nb = k / 32, nst = nb / QS_S;
+    const uint8_t* scales = W + 32ull * (uint64_t)n_out * (uint64_t)nb;
+    QsCopy cp[C::COPIES];
+    qs_plan<TT, TG>(cp, W, scales, xq, xd, n_out, nb, k, T, row0, t0, wave, lane);
+    const uint32_t ring = lds_addr(lds);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[tt][i] = 0.0f;
+    for (int s = 0; s < C::NS - 1; ++s) qs_issue<TT, TG>(cp, ring + (uint32_t)(C::STAGE * s), s < nst ? s : nst - 1);
+    float acc[TT][4];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = 0.0f;
     const v4i_s z = {0, 0, 0, 0};
-    // the next block's operands are loaded before this block's arithmetic
-    long bw = *reinterpret_cast<const long*>(wcodes);
-    uint16_t dws = wsc[0];
-    long av[GQ_TT];
+    for (int s = 0; s < nst; ++s) {
+        wait_vm<C::COPIES * (C::NS - 2)>();  // this wavefront's copies of stage s have landed
+        lds_barrier();                       // everyone's have, and stage s - 1 is read out
+        const int sn = s + C::NS - 1;
+        qs_issue<TT, TG>(cp, ring + (uint32_t)(C::STAGE * (sn % C::NS)), sn < nst ? sn : nst - 1);
+        const uint8_t* st = lds + C::STAGE * (s % C::NS);
+        // the lane's rows 4 p + i: four scales each, 8 bytes a row
+        const v4u_s sc01 = *reinterpret_cast<const v4u_s*>(st + C::SC_OFF + (16 * rg + 4 * p) * 8);
+        const v4u_s sc23 = *reinterpret_cast<const v4u_s*>(st + C::SC_OFF + (16 * rg + 4 * p) * 8 + 16);
+        const uint32_t scw[4][2] = {{sc01.x, sc01.y}, {sc01.z, sc01.w}, {sc23.x, sc23.y}, {sc23.z, sc23.w}};
+        float dx[TT][QS_S];
 #pragma unroll
-    for (int tt = 0; tt < GQ_TT; ++tt) av[tt] = *reinterpret_cast<const long*>(xa[tt]);
-    for (int b = 0; b < nb; ++b) {
-        const long bw_c = bw;
-        const uint16_t dws_c = dws;
-        long av_c[GQ_TT];
-#pragma unroll
-        for (int tt = 0; tt < GQ_TT; ++tt) av_c[tt] = av[tt];
-        if (b + 1 < nb) {
-            bw = *reinterpret_cast<const long*>(wcodes + 32 * (b + 1));
-            dws = wsc[b + 1];
-#pragma unroll
-            for (int tt = 0; tt < GQ_TT; ++tt) av[tt] = *reinterpret_cast<const long*>(xa[tt] + 32 * (b + 1));
+        for (int t = 0; t < TT; ++t) {
+            const float4 v = *reinterpret_cast<const float4*>(st + C::DX_OFF + (16 * TT * tg + 16 * t + c) * 16);
+            dx[t][0] = v.x;
+            dx[t][1] = v.y;
+            dx[t][2] = v.z;
+            dx[t][3] = v.w;
         }
-        const float dw = f16_to_f32(dws_c);
+        v4i_s d[QS_S][TT];
 #pragma unroll
-        for (int tt = 0; tt < GQ_TT; ++tt) {
-            const v4i_s d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av_c[tt], bw_c, z, 0, 0, 0);
+        for (int j = 0; j < QS_S; ++j) {
+            const long a = *reinterpret_cast<const long*>(st + C::W_OFF + 1024 * j + (16 * rg + c) * 32 + 8 * p);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[tt][i] = acc[tt][i] + (dw * xdt[tt][i][b]) * (float)d[i];
-        }
-    }
-    if (row0 + c < n_out) {
-#pragma unroll
-        for (int tt = 0; tt < GQ_TT; ++tt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int to = t0 + 16 * tt + 4 * p + i;
-                if (to < T) y[(int64_t)to * n_out + row0 + c] = acc[tt][i];
+            for (int t = 0; t < TT; ++t) {
+                const long b = *reinterpret_cast<const long*>(st + C::A_OFF + C::TW * 32 * j +
+                                                              (16 * TT * tg + 16 * t + c) * 32 + 8 * p);
+                d[j][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
             }
+        }
+#pragma unroll
+        for (int j = 0; j < QS_S; ++j) {
+            float dw[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dw[i] = f16_to_f32((uint16_t)(scw[i][j >> 1] >> (16 * (j & 1))));
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] = acc[t][i] + (dw[i] * dx[t][j]) * (float)d[j][t][i];
+        }
     }
+    wait_vm<0>();  // the last (repeated) copies have landed before the workgroup ends
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        const int tk = t0 + 16 * TT * tg + 16 * t + c;
+        if (tk >= T) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = row0 + 16 * rg + 4 * p + i;
+            if (r < n_out) y[(int64_t)tk * n_out + r] = acc[t][i];
+        }
+    }
+}
+
+// Whether the staged GEMM takes the shape: whole stages, 32-bit copy offsets.
+static bool gemm_q8_staged_fits(int n_out, int k, int T) {
+    const uint64_t nb = (uint64_t)k / 32;
+    return nb % QS_S == 0 && nb > 0 && (uint64_t)n_out * nb * 32 < (1ull << 32) && (uint64_t)T * (uint64_t)k < (1ull << 32);
+}
+
+template <int TT, int TG>
+static void launch_q8_staged(const uint8_t* W, int n_out, int k, const int8_t* xq, const float* xd, int T, float* y,
+                             hipStream_t stream, const uint32_t* active) {
+    using C = QsCfg<TT, TG>;
+    const dim3 grid((unsigned)((n_out + QS_RW - 1) / QS_RW), (unsigned)((T + C::TW - 1) / C::TW));
+    hipLaunchKernelGGL((k_gemm_q8_staged<TT, TG>), grid, dim3(64 * C::NW), (size_t)(C::STAGE * C::NS), stream, W, n_out,
+                       k, xq, xd, T, y, active);
 }
 
 void launch_gemm_q8_split(const uint8_t* W, int n_out, int k, const uint8_t* ws, int T, float* y,
                           hipStream_t stream, const uint32_t* active) {
     const ActLayout L = act_layout(ACT_Q8_0, (uint64_t)T, (uint64_t)k);
-    const dim3 grid((unsigned)((n_out + 63) / 64), (unsigned)((T + 16 * GQ_TT - 1) / (16 * GQ_TT)));
-    hipLaunchKernelGGL(k_gemm_q8_split, grid, dim3(256), 0, stream, W, n_out, k,
-                       reinterpret_cast<const int8_t*>(ws + L.codes), reinterpret_cast<const float*>(ws + L.d), T, y,
-                       active);
+    const int8_t* xq = reinterpret_cast<const int8_t*>(ws + L.codes);
+    const float* xd = reinterpret_cast<const float*>(ws + L.d);
+    if (gemm_q8_staged_fits(n_out, k, T)) {
+        if (T <= 16)
+            launch_q8_staged<1, 1>(W, n_out, k, xq, xd, T, y, stream, active);
+        else if (T <= 32)
+            launch_q8_staged<2, 1>(W, n_out, k, xq, xd, T, y, stream, active);
+        else
+            launch_q8_staged<2, 2>(W, n_out, k, xq, xd, T, y, stream, active);
+        return;
+    }
+    // other shapes: the register-staged kernel; up to 64 tokens: 16-token tiles; beyond, 32-token tiles (a token tile per wavefront, up to
+    // four wavefronts on the same 16 rows)
+    const int TT = T <= 64 ? 1 : 2;
+    const int tiles = (T + 16 * TT - 1) / (16 * TT);
+    const int wpw = tiles < 4 ? tiles : 4;
+    const dim3 grid((unsigned)((n_out + 15) / 16), (unsigned)((tiles + wpw - 1) / wpw));
+    const bool vec = (k / 32) % (2 * GQ_G) == 0;
+    const dim3 block(64 * wpw);
+    if (TT == 1 && vec)
+        hipLaunchKernelGGL((k_gemm_q8_split<1, true>), grid, block, 0, stream, W, n_out, k, xq, xd, T, y, active);
+    else if (TT == 1)
+        hipLaunchKernelGGL((k_gemm_q8_split<1, false>), grid, block, 0, stream, W, n_out, k, xq, xd, T, y, active);
+    else if (vec)
+        hipLaunchKernelGGL((k_gemm_q8_split<2, true>), grid, block, 0, stream, W, n_out, k, xq, xd, T, y, active);
+    else
+        hipLaunchKernelGGL((k_gemm_q8_split<2, false>), grid, block, 0, stream, W, n_out, k, xq, xd, T, y, active);
 }
 
 }  // namespace syn

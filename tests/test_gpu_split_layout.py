@@ -92,3 +92,13 @@ def test_split_gemm_edges_equal_oracle(S):
     multiples of 32, one-block rows, many tiles of tokens."""
     for n_out, k, rows in ((1, 32, 9), (17, 64, 33), (63, 96, 31), (65, 256, 100), (200, 2048, 257)):
         check(S, o.Q8_0, n_out, k, rows, n_out * 31 + rows)
+
+
+def test_split_gemm_staged_shapes_equal_oracle(S):
+    """The LDS-staged GEMM (rows of whole 4-block stages): every token-tile variant (16, 32 and
+    64 tokens a workgroup), partial workgroups of rows and tokens, one stage and many."""
+    w = None
+    for rows in (9, 16, 17, 31, 32, 33, 64, 65, 127):
+        w = check(S, o.Q8_0, 50, 512, rows, 7000 + rows, w)
+    for n_out, k, rows in ((33, 128, 40), (96, 4096, 48), (1, 128, 70)):
+        check(S, o.Q8_0, n_out, k, rows, n_out + k + rows)
