@@ -369,15 +369,19 @@ __global__ __launch_bounds__(256) void k_gemm_q8_split(const uint8_t* __restrict
 // A workgroup takes 32 weight rows (two wavefront row groups of 16) x TW = 16 TT TG tokens (TG
 // token groups of 16 TT), stage by stage: four blocks of every operand are copied into LDS by
 // global_load_lds while earlier stages compute.  Stage layout (bytes):
-//   codes of the rows  [block j][row][32]          4096
-//   codes of the tokens [block j][token][32]       128 TW
-//   row scales         [row][block j] F16          256
-//   token scales       [token][block j] F32        16 TW
-// Each copy instruction moves 1 KB (16 bytes a lane) or, for the scales, 64 lanes of 4 bytes; a
-// wavefront issues the same number of copies every stage, so its wait is a fixed count.
+//   codes of the rows   [row][128]      4096   a row's four blocks, swizzled (below)
+//   codes of the tokens [token][128]    128 TW the same
+//   row scales          [row][block] F16  256
+//   token scales        [token][block] F32 16 TW
+// A copy instruction moves 1 KB: eight rows' (or tokens') whole 128-byte lines, 16 bytes a lane.
+// Within a line the 16-byte halves of the four blocks are stored at slot 2 (j ^ ((c >> 1) & 3)) +
+// (h ^ (c >> 3)) for block j, half h of the line's row or token c (mod 16), so that the matrix
+// operand reads (16 lines, one 16-byte half each per half-wavefront) hit 16 distinct bank groups.
+// A wavefront issues the same number of copies every stage, so its wait is a fixed count.
 
 constexpr int QS_S = 4;    // blocks per stage
 constexpr int QS_RW = 32;  // weight rows per workgroup
+constexpr int QS_NS_MAX = 3;
 
 template <int TT, int TG>
 struct QsCfg {
@@ -387,9 +391,16 @@ struct QsCfg {
     static constexpr int SC_OFF = A_OFF + TW * QS_S * 32;
     static constexpr int DX_OFF = SC_OFF + QS_RW * QS_S * 2;
     static constexpr int STAGE = DX_OFF + TW * QS_S * 4;
-    static constexpr int NS = STAGE * 4 <= 64 * 1024 ? 4 : 3;  // ring stages
-    static constexpr int COPIES = TG == 1 ? 5 : 4;              // copies per wavefront per stage
+    // ring stages: as many as 64 KB hold, at most QS_NS_MAX
+    static constexpr int NS = 64 * 1024 / STAGE < QS_NS_MAX ? 64 * 1024 / STAGE : QS_NS_MAX;
+    static constexpr int COPIES = (4 + TW / 8 + (TG == 1 ? 2 : 4)) / NW;  // per wavefront per stage
+    static_assert((4 + TW / 8 + (TG == 1 ? 2 : 4)) % NW == 0, "copies split evenly");
 };
+
+// The LDS byte offset, within its 128-byte line, of block j's 8 bytes at 8 p for line c.
+SYN_DEV int qs_slot(int c, int j, int p) {
+    return 32 * (j ^ ((c >> 1) & 3)) + 16 * ((p >> 1) ^ ((c >> 3) & 1)) + 8 * (p & 1);
+}
 
 // The lane's part of its wavefront's copies: per copy a global base (advanced per stage by
 // `step` bytes), the lane's 32-bit offset, the LDS offset in the stage, 16 or 4 bytes, and whether
@@ -401,23 +412,28 @@ struct QsCopy {
 };
 
 template <int TT, int TG>
-__device__ __forceinline__ void qs_plan(QsCopy* cp, const uint8_t* W, const uint8_t* scales,
-                                        const int8_t* xq, const float* xd, int n_out, int nb, int k, int T,
-                                        int row0, int t0, int wave, int lane) {
+__device__ __forceinline__ void qs_plan(QsCopy* cp, const uint8_t* W, const uint8_t* scales, const int8_t* xq,
+                                        const float* xd, int n_out, int nb, int k, int T, int row0, int t0, int wave,
+                                        int lane) {
     using C = QsCfg<TT, TG>;
     const uint32_t rb = (uint32_t)nb * 32u;
     auto wrow = [&](int r) { return (uint32_t)(row0 + r < n_out ? row0 + r : n_out - 1); };
     auto tok = [&](int t) { return (uint32_t)(t0 + t < T ? t0 + t : T - 1); };
-    // codes of the rows, block j: lane -> row lane / 2, half lane % 2
-    auto wcopy = [&](int j) {
-        return QsCopy{W + 32 * j, wrow(lane >> 1) * rb + 16u * (uint32_t)(lane & 1),
-                      (uint32_t)(C::W_OFF + 1024 * j), 32u * QS_S, true, true};
+    // lane -> line 8 q + lane / 8 of the stage, LDS slot lane % 8, holding the line's bytes at
+    // `src` (the inverse of the swizzle)
+    const int slot = lane & 7, li = lane >> 3;
+    auto src = [&](int c) {
+        const int j = (slot >> 1) ^ ((c >> 1) & 3), h = (slot & 1) ^ ((c >> 3) & 1);
+        return (uint32_t)(32 * j + 16 * h);
     };
-    // codes of the tokens, block j, tokens 32 h ..: lane -> token 32 h + lane / 2
-    auto acopy = [&](int j, int h) {
-        const int t = 32 * h + (lane >> 1);
-        return QsCopy{reinterpret_cast<const uint8_t*>(xq) + 32 * j, tok(t) * (uint32_t)k + 16u * (uint32_t)(lane & 1),
-                      (uint32_t)(C::A_OFF + C::TW * 32 * j + 1024 * h), 32u * QS_S, true, t < C::TW};
+    auto wcopy = [&](int q) {
+        const int r = 8 * q + li;
+        return QsCopy{W, wrow(r) * rb + src(r & 15), (uint32_t)(C::W_OFF + 1024 * q), 32u * QS_S, true, true};
+    };
+    auto acopy = [&](int q) {
+        const int t = 8 * q + li;
+        return QsCopy{reinterpret_cast<const uint8_t*>(xq), tok(t) * (uint32_t)k + src(t & 15),
+                      (uint32_t)(C::A_OFF + 1024 * q), 32u * QS_S, true, true};
     };
     // row scales of rows 16 h .. (32 lanes) or all 32 rows (h < 0): lane -> row lane / 2, blocks
     // 2 (lane % 2), +1
@@ -433,17 +449,21 @@ __device__ __forceinline__ void qs_plan(QsCopy* cp, const uint8_t* W, const uint
                       (uint32_t)(C::DX_OFF + (h < 0 ? 0 : 512 * h)), 4u * QS_S, true,
                       (h < 0 ? t < C::TW : lane < 32)};
     };
-    if constexpr (TG == 1) {  // 10 copies: wave 0 blocks 0, 1 and the row scales, wave 1 blocks 2, 3 and dx
-        const int j0 = 2 * wave;
-        cp[0] = wcopy(j0);
-        cp[1] = wcopy(j0 + 1);
-        cp[2] = acopy(j0, 0);
-        cp[3] = acopy(j0 + 1, 0);
+    if constexpr (TG == 1 && TT == 1) {  // 8 copies: 4 row lines, 2 token lines, the two scale sets
+        cp[0] = wcopy(2 * wave);
+        cp[1] = wcopy(2 * wave + 1);
+        cp[2] = acopy(wave);
+        cp[3] = wave == 0 ? scopy(-1) : dcopy(-1);
+    } else if constexpr (TG == 1) {  // 10 copies: 4 row lines, 4 token lines, the two scale sets
+        cp[0] = wcopy(2 * wave);
+        cp[1] = wcopy(2 * wave + 1);
+        cp[2] = acopy(2 * wave);
+        cp[3] = acopy(2 * wave + 1);
         cp[4] = wave == 0 ? scopy(-1) : dcopy(-1);
-    } else {  // 16 copies: wave w block w of the rows and of both token halves, and a scale half
+    } else {  // 16 copies: 4 row lines, 8 token lines, two halves of each scale set
         cp[0] = wcopy(wave);
-        cp[1] = acopy(wave, 0);
-        cp[2] = acopy(wave, 1);
+        cp[1] = acopy(2 * wave);
+        cp[2] = acopy(2 * wave + 1);
         cp[3] = wave < 2 ? scopy(wave) : dcopy(wave - 2);
     }
 }
@@ -512,11 +532,11 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
         v4i_s d[QS_S][TT];
 #pragma unroll
         for (int j = 0; j < QS_S; ++j) {
-            const long a = *reinterpret_cast<const long*>(st + C::W_OFF + 1024 * j + (16 * rg + c) * 32 + 8 * p);
+            const int o = qs_slot(c, j, p);  // line c's (row or token, mod 16) bytes 8 p of block j
+            const long a = *reinterpret_cast<const long*>(st + C::W_OFF + (16 * rg + c) * 128 + o);
 #pragma unroll
             for (int t = 0; t < TT; ++t) {
-                const long b = *reinterpret_cast<const long*>(st + C::A_OFF + C::TW * 32 * j +
-                                                              (16 * TT * tg + 16 * t + c) * 32 + 8 * p);
+                const long b = *reinterpret_cast<const long*>(st + C::A_OFF + (16 * TT * tg + 16 * t + c) * 128 + o);
                 d[j][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
             }
         }
