@@ -398,7 +398,7 @@ def bench_cfgs(torch, S, a):
     for T in (1, 8, 32, 128):
         step, kern = gemv_case(torch, S, wl, T, n, k, max(10, nrep // (1 + T // 32)))
         alg = wb + T * (k + 8 * (k // 32)) + 4 * T * n
-        rows_res[str(T)] = {"kernel": "k_gemv_split<Q8_0>" if T <= 8 else "k_gemm_q8_split",
+        rows_res[str(T)] = {"kernel": "k_gemv_split<Q8_0>" if T == 1 else "k_gemm_q8_staged",
                             "step_us": round(step, 3), "weight_gbs": round(wb / (step * 1e-6) / 1e9, 1),
                             "kernel_us": round(kern, 3), "kernel_alg_gbs": round(alg / (kern * 1e-6) / 1e9, 1),
                             "kernel_frac": round(alg / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),

@@ -85,8 +85,8 @@ int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uin
  *   layout 1 one row runs the decode kernel with the row quantized in every workgroup, 2 to 8 rows
  *   the multi-row decode kernel on rows quantized beforehand (both k_in <= 16384), more rows the
  *   matrix-core GEMM (k_in a multiple of 2048).  Layout 2 quantizes the rows to Q8_0 blocks and
- *   runs the split decode kernel eight rows at a time, or, for Q8_0 and 9 rows or more, the int8
- *   matrix-core GEMM.
+ *   runs the split decode kernel eight rows at a time, or, for Q8_0, the int8 matrix-core GEMM
+ *   from 2 rows (k_in a multiple of 128) or from 9 rows (other k_in).
  * syn_gemv_batch_layout / syn_gemv_batch_quantized_layout: the grouped decode of every problem
  *   in `layout`. */
 int syn_q4k_repack(uint32_t layout, const void* src, void* dst, uint64_t bytes, int32_t inverse, void* stream);

@@ -489,15 +489,24 @@ SYN_EXPORT int syn_split_repack_host(uint32_t layout, int32_t wtype, const void*
 // Gemv over weights in a repacked layout.  Q4_K in X8: one row runs the grouped decode kernel,
 // 2 to 8 rows the multi-row decode kernel, more rows the matrix-core GEMM (which needs rows of
 // whole 8-block runs: k_in a multiple of 2048).  Q8_0 / Q4_0 in SPLIT: Q8_0 activation rows, the
-// split decode kernel for up to 8 rows at a time, the int8 matrix-core GEMM for Q8_0 and more.
+// split decode kernel for up to 8 rows at a time, the int8 matrix-core GEMM for Q8_0 from 2 rows
+// (rows of whole 4-block stages) or 9.
 constexpr uint32_t SPLIT_GEMM_MIN_ROWS = 9;
 constexpr uint32_t SPLIT_GEMM_MAX_ROWS = 65535u * 32u;  // the GEMM grid's token tiles
 
 namespace {
+// Q8_0 rows on the int8 matrix cores: from 2 rows where the LDS-staged GEMM takes the shape
+// (16-token tiles beat the split decode kernel there), else from 9.
+bool split_gemm(int32_t wtype, uint32_t n_out, uint32_t k_in, uint32_t rows) {
+    if (wtype != SYN_Q8_0) return false;
+    return rows >= SPLIT_GEMM_MIN_ROWS ||
+           (rows >= 2 && syn::gemm_q8_staged_fits((int)n_out, (int)k_in, (int)rows));
+}
+
 // The products over a SPLIT matrix from rows already quantized to Q8_0 blocks in ws.
 void split_products(int32_t wtype, const void* w, uint32_t n_out, uint32_t k_in, const void* ws, uint32_t rows,
                     float* y, void* stream, const uint32_t* active) {
-    if (wtype == SYN_Q8_0 && rows >= SPLIT_GEMM_MIN_ROWS)
+    if (split_gemm(wtype, n_out, k_in, rows))
         syn::launch_gemm_q8_split((const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows, y,
                                   (hipStream_t)stream, active);
     else
@@ -555,7 +564,7 @@ int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
         if (!aligned(w, 16) || (k_in && (!aligned(x, 16) || !aligned(ws, 256))) || !aligned(y, 4))
             return fail(SYN_E_INVALID, "%s: w and x must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
         if ((uint64_t)n_out * rows > (1ull << 40)) return fail(SYN_E_INVALID, "%s: rows * n_out too large", W);
-        if (wtype == SYN_Q8_0 && rows >= SPLIT_GEMM_MIN_ROWS && rows > SPLIT_GEMM_MAX_ROWS)
+        if (split_gemm(wtype, n_out, k_in, rows) && rows > SPLIT_GEMM_MAX_ROWS)
             return fail(SYN_E_UNSUPPORTED, "%s: %u rows (the GEMM takes %u)", W, rows, SPLIT_GEMM_MAX_ROWS);
         if (k_in) {
             syn::launch_act_quant(syn::ACT_Q8_0, x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
@@ -639,7 +648,7 @@ SYN_EXPORT int syn_gemv_quantized_layout(uint32_t layout, int32_t wtype, const v
     if (!aligned(w, 16) || (k_in && !aligned(ws, 256)) || !aligned(y, 4))
         return fail(SYN_E_INVALID, "%s: w must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
     if ((uint64_t)n_out * rows > (1ull << 40)) return fail(SYN_E_INVALID, "%s: rows * n_out too large", W);
-    if (wtype == SYN_Q8_0 && rows >= SPLIT_GEMM_MIN_ROWS && rows > SPLIT_GEMM_MAX_ROWS)
+    if (split_gemm(wtype, n_out, k_in, rows) && rows > SPLIT_GEMM_MAX_ROWS)
         return fail(SYN_E_UNSUPPORTED, "%s: %u rows (the GEMM takes %u)", W, rows, SPLIT_GEMM_MAX_ROWS);
     split_products(wtype, w, n_out, k_in, ws, rows, y, stream, nullptr);
     return check_launch(W);

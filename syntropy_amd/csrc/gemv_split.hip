@@ -565,7 +565,7 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
 }
 
 // Whether the staged GEMM takes the shape: whole stages, 32-bit copy offsets.
-static bool gemm_q8_staged_fits(int n_out, int k, int T) {
+bool gemm_q8_staged_fits(int n_out, int k, int T) {
     const uint64_t nb = (uint64_t)k / 32;
     return nb % QS_S == 0 && nb > 0 && (uint64_t)n_out * nb * 32 < (1ull << 32) && (uint64_t)T * (uint64_t)k < (1ull << 32);
 }
