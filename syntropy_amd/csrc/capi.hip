@@ -59,10 +59,20 @@ bool use_gemm(int32_t wtype, uint32_t rows, uint32_t n_out, uint32_t k_in) {
            gemm_tpad(rows) * (k_in / 256) < (1ull << 31);
 }
 
+// Q4_K Gemv calls of 2 to 31 rows run on the decode expert kernel (the matrix as one expert,
+// the rows as its entries: the int8 matrix cores over four-row groups).
+bool q4k_dense(int32_t wtype, uint32_t rows, uint32_t k_in) {
+    return wtype == SYN_Q4_K && rows >= 2 && rows < GEMM_MIN_ROWS && k_in > 0 && k_in % 256 == 0;
+}
+
 // Workspace of a Gemv call: the larger of the two activation layouts when the call may take
 // the matrix-core path (the bytes do not depend on n_out, which the workspace query lacks).
 uint64_t gemv_ws_bytes(int32_t wtype, uint32_t rows, uint32_t k_in) {
     uint64_t b = syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
+    if (q4k_dense(wtype, rows, k_in)) {
+        const uint64_t m = syn::moe_act_bytes(rows, (int)k_in);
+        if (m > b) b = m;
+    }
     if (use_gemm(wtype, rows, 1, k_in)) {
         const uint64_t g = syn::gemm_act_bytes((int64_t)gemm_tpad(rows), (int)k_in);
         if (g > b) b = g;
@@ -135,6 +145,20 @@ SYN_EXPORT int syn_gemv_quantized(int32_t wtype, const void* w, uint64_t w_bytes
     return check_launch(W);
 }
 
+namespace {
+// Q4_K rows 2..31: the rows to Q8_K in the expert kernels' layout, then the dense expert product
+// (layout 0: GGUF order; 1: X8).  Operands already checked by the caller.
+int q4k_dense_rows(const char* W, int x8, const void* w, uint32_t n_out, uint32_t k_in, const float* x,
+                   uint32_t rows, float* y, void* ws, void* stream, const uint32_t* active) {
+    const syn::MoeAct a = syn::moe_act_at((uint8_t*)ws, rows, (int)k_in);
+    syn::launch_moe_gather_q8k(x, nullptr, (int)rows, 1, (int)k_in, nullptr, a, 0, (hipStream_t)stream, nullptr);
+    if (int rc = check_launch(W)) return rc;
+    syn::launch_q4k_dense_rows((const uint8_t*)w, x8, (int)n_out, (int)k_in, a, (int)rows, y, (hipStream_t)stream,
+                               active);
+    return check_launch(W);
+}
+}  // namespace
+
 int syn_gemv_rows(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out,
                         uint32_t k_in, const float* x, uint32_t rows, float* y, void* ws,
                         uint64_t ws_bytes, void* stream, const uint32_t* active) {
@@ -143,8 +167,10 @@ int syn_gemv_rows(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out
     if (rows == 0 || n_out == 0) return SYN_OK;
     const uint64_t row_bytes = (uint64_t)k_in / syn::block_elems(wtype) * syn::block_bytes(wtype);
     const bool gemm = use_gemm(wtype, rows, n_out, k_in) && aligned(w, 16);
-    const uint64_t need_ws = gemm ? syn::gemm_act_bytes((int64_t)gemm_tpad(rows), (int)k_in)
-                                  : syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
+    uint64_t need_ws = gemm ? syn::gemm_act_bytes((int64_t)gemm_tpad(rows), (int)k_in)
+                            : syn::act_layout(syn::act_kind(wtype), rows, k_in).bytes;
+    if (!gemm && q4k_dense(wtype, rows, k_in) && syn::moe_act_bytes(rows, (int)k_in) > need_ws)
+        need_ws = syn::moe_act_bytes(rows, (int)k_in);
     if (!y || (row_bytes * n_out && !w)) return fail(SYN_E_INVALID, "%s: null operand", W);
     if (w_bytes < row_bytes * n_out)
         return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
@@ -176,6 +202,8 @@ int syn_gemv_rows(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out
                              (hipStream_t)stream, active);
         return check_launch(W);
     }
+    if (q4k_dense(wtype, rows, k_in) && aligned(w, 16) && row_bytes * n_out < (1ull << 32))
+        return q4k_dense_rows(W, 0, w, n_out, k_in, x, rows, y, ws, stream, active);
     if (k_in) {
         syn::launch_act_quant(syn::act_kind(wtype), x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
         if (int rc = check_launch(W)) return rc;
@@ -487,8 +515,8 @@ SYN_EXPORT int syn_split_repack_host(uint32_t layout, int32_t wtype, const void*
 }
 
 // Gemv over weights in a repacked layout.  Q4_K in X8: one row runs the grouped decode kernel,
-// 2 to 8 rows the multi-row decode kernel, more rows the matrix-core GEMM (which needs rows of
-// whole 8-block runs: k_in a multiple of 2048).  Q8_0 / Q4_0 in SPLIT: Q8_0 activation rows, the
+// 2 to 31 rows the decode expert kernel (int8 matrix cores), more rows the matrix-core GEMM (which
+// needs rows of whole 8-block runs: k_in a multiple of 2048).  Q8_0 / Q4_0 in SPLIT: Q8_0 activation rows, the
 // split decode kernel for up to 8 rows at a time, the int8 matrix-core GEMM for Q8_0 from 2 rows
 // (rows of whole 4-block stages) or 9.
 constexpr uint32_t SPLIT_GEMM_MIN_ROWS = 9;
@@ -533,8 +561,8 @@ SYN_EXPORT int syn_gemv_layout_workspace_bytes(uint32_t layout, int32_t wtype, u
         *bytes = syn::act_layout(syn::ACT_Q8K, 1, k_in).bytes;
         return SYN_OK;
     }
-    if (syn::gemv_q4k_rows_supported((int)rows, (int)k_in)) {  // 2..8 rows: Q8_K rows, the multi-row decode
-        *bytes = syn::act_layout(syn::ACT_Q8K, rows, k_in).bytes;
+    if (q4k_dense(wtype, rows, k_in)) {  // 2..31 rows: the decode expert kernel
+        *bytes = syn::moe_act_bytes(rows, (int)k_in);
         return SYN_OK;
     }
     if (k_in % 2048) return fail(SYN_E_UNSUPPORTED, "%s: the layout-1 GEMM takes k_in in multiples of 2048, not %u", W, k_in);
@@ -581,7 +609,7 @@ int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
         const uint64_t wb[1] = {w_bytes};
         return gemv_batch_f32(W, layout, 1, ts, ws_, wb, &n_out, &k_in, xs, ys, ws, ws_bytes, stream, true, active);
     }
-    if (syn::gemv_q4k_rows_supported((int)rows, (int)k_in)) {
+    if (q4k_dense(wtype, rows, k_in)) {
         const uint64_t need_w = (uint64_t)n_out * (k_in / 256) * 144;
         if (!w || !x || !ws || !y) return fail(SYN_E_INVALID, "%s: null operand", W);
         if (w_bytes < need_w)
@@ -592,11 +620,7 @@ int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
                         (unsigned long long)ws_bytes, (unsigned long long)need);
         if (!aligned(w, 16) || !aligned(x, 16) || !aligned(ws, 256) || !aligned(y, 4))
             return fail(SYN_E_INVALID, "%s: w and x must be 16-byte, the workspace 256-byte and y 4-byte aligned", W);
-        syn::launch_act_quant(syn::ACT_Q8K, x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
-        if (int rc = check_launch(W)) return rc;
-        syn::launch_gemv_q4k_rows((const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows, y,
-                                  (hipStream_t)stream, active);
-        return check_launch(W);
+        return q4k_dense_rows(W, 1, w, n_out, k_in, x, rows, y, ws, stream, active);
     }
     if (!syn::gemm_q4k_supported((int)n_out, (int)k_in))
         return fail(SYN_E_UNSUPPORTED, "%s: a %u x %u matrix is larger than 4 GiB", W, n_out, k_in);

@@ -412,121 +412,6 @@ void k_gemv_q4k_batch(DecBatch bt) {
     }
 }
 
-// Rows 2..R over X8 weights (verify windows and small batches): the rows are quantized to Q8_K
-// beforehand (the workspace layout act_layout(ACT_Q8K, rows, k)).  As k_gemv_q4k_batch, one
-// super-block per lane (P lanes per output row) with its nine 16-byte non-temporal loads; the
-// block's scales are decoded once and its R terms read the activation rows from global memory
-// (every row group of a wavefront reads the same columns, so they come from L1/L2); each row's
-// terms are folded in block order through LDS by the row's first lane.
-SYN_DEV float q4k_term_glb(const uint32_t (&wb)[36], const int (&sc)[8], const int (&mn)[8], float d, float dmin,
-                           const int8_t* __restrict__ xc, const int32_t* __restrict__ xs, float dx) {
-    int s1 = 0;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const v4u xl0 = *reinterpret_cast<const v4u*>(xc + 64 * g);
-        const v4u xl1 = *reinterpret_cast<const v4u*>(xc + 64 * g + 16);
-        const v4u xh0 = *reinterpret_cast<const v4u*>(xc + 64 * g + 32);
-        const v4u xh1 = *reinterpret_cast<const v4u*>(xc + 64 * g + 48);
-        const uint32_t xl[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
-        const uint32_t xh[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
-        int lo = 0, hi = 0;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const uint32_t q = wb[4 + 8 * g + t];
-            lo = sdot4(q & 0x0F0F0F0Fu, xl[t], lo);
-            hi = sdot4((q >> 4) & 0x0F0F0F0Fu, xh[t], hi);
-        }
-        s1 += sc[2 * g] * lo + sc[2 * g + 1] * hi;
-    }
-    const int4 sa = reinterpret_cast<const int4*>(xs)[0], sb = reinterpret_cast<const int4*>(xs)[1];
-    const int s2 = mn[0] * sa.x + mn[1] * sa.y + mn[2] * sa.z + mn[3] * sa.w + mn[4] * sb.x + mn[5] * sb.y +
-                   mn[6] * sb.z + mn[7] * sb.w;
-    return (d * dx) * (float)s1 - (dmin * dx) * (float)s2;
-}
-
-constexpr int ROWS_WAVES = 8;
-
-template <int R>
-__global__ __launch_bounds__(64 * ROWS_WAVES) __attribute__((amdgpu_waves_per_eu(4)))
-void k_gemv_q4k_rows(const uint8_t* __restrict__ W, int n_out, int nb, const int8_t* __restrict__ xq,
-                     const float* __restrict__ xd, const int32_t* __restrict__ xs, int rows, float* __restrict__ y,
-                     const uint32_t* __restrict__ active) {
-    rows = active_rows(active, 0, rows);
-    if (rows == 0) return;  // uniform
-    __shared__ __attribute__((aligned(16))) float terms[ROWS_WAVES][R][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int P = lanes_per_row(nb);
-    const int row = ((int)blockIdx.x * ROWS_WAVES + wave) * (64 / P) + lane / P;
-    const int b = lane % P;
-    const bool ok = row < n_out && b < nb;
-    const uint64_t nblocks = (uint64_t)n_out * (uint64_t)nb;
-    const uint64_t g = ok ? (uint64_t)row * nb + b : 0;
-    const uint8_t* src = W + x8_chunk_offset(g, 0, nblocks);
-    const uint32_t step = 16u * x8_group_blocks(g, nblocks);
-    v4u A[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) A[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(src + step * i));
-    uint32_t wb[36];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) {
-        wb[4 * i] = A[i].x;
-        wb[4 * i + 1] = A[i].y;
-        wb[4 * i + 2] = A[i].z;
-        wb[4 * i + 3] = A[i].w;
-    }
-    int sc[8], mn[8];
-    scales_k4(wb[1], wb[2], wb[3], sc, mn);
-    const float d = f16_to_f32(wb[0]), dmin = f16_to_f32(wb[0] >> 16);
-    const int bb = ok ? b : 0;
-    const int64_t k = (int64_t)nb * 256;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (r < rows) {  // uniform
-            const float t = q4k_term_glb(wb, sc, mn, d, dmin, xq + r * k + (int64_t)bb * 256, xs + (r * k + (int64_t)bb * 256) / 32,
-                                         xd[(int64_t)r * nb + bb]);
-            terms[wave][r][lane] = ok ? t : 0.0f;
-        }
-    }
-    wave_lds_sync();
-    if (b == 0 && row < n_out) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r >= rows) break;
-            const float4* tv = reinterpret_cast<const float4*>(&terms[wave][r][lane]);
-            float acc = 0.0f;
-            for (int q = 0; q < P / 4; ++q) {
-                const float4 v = tv[q];
-                acc = acc + v.x;
-                acc = acc + v.y;
-                acc = acc + v.z;
-                acc = acc + v.w;
-            }
-            y[(int64_t)r * n_out + row] = acc;
-        }
-    }
-}
-
-bool gemv_q4k_rows_supported(int rows, int k) { return rows >= 1 && rows <= 8 && k % 256 == 0 && k > 0 && k <= 16384; }
-
-void launch_gemv_q4k_rows(const uint8_t* W, int n_out, int k, const uint8_t* ws, int rows, float* y, hipStream_t stream,
-                          const uint32_t* active) {
-    const int nb = k / 256;
-    const int rpw = 64 / (nb <= 16 ? 16 : nb <= 32 ? 32 : 64);
-    const dim3 grid((unsigned)((n_out + ROWS_WAVES * rpw - 1) / (ROWS_WAVES * rpw)));
-    const ActLayout L = act_layout(ACT_Q8K, (uint64_t)rows, (uint64_t)k);
-    const int8_t* xq = reinterpret_cast<const int8_t*>(ws + L.codes);
-    const float* xd = reinterpret_cast<const float*>(ws + L.d);
-    const int32_t* xs = reinterpret_cast<const int32_t*>(ws + L.sums);
-#define SYN_ROWS(RR) \
-    hipLaunchKernelGGL((k_gemv_q4k_rows<RR>), grid, dim3(64 * ROWS_WAVES), 0, stream, W, n_out, nb, xq, xd, xs, rows, y, active)
-    if (rows <= 2)
-        SYN_ROWS(2);
-    else if (rows <= 4)
-        SYN_ROWS(4);
-    else
-        SYN_ROWS(8);
-#undef SYN_ROWS
-}
 
 // K up to 32768: at most 8 rounds, and the activation row within 41 KB of LDS.
 bool q4k_dec_supported(int k) { return k % 256 == 0 && k > 0 && k <= 32768; }

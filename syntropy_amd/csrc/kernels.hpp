@@ -32,9 +32,6 @@ void launch_silu_mul(const float* y2, int rows, int n, float* y, hipStream_t str
 // The same over X8 weights with the F32 rows quantized inside the grouped launch (k <= 16384).
 bool gemv_q4k_batch_fusable(int k);
 // 2..8 rows over X8 weights, the rows quantized beforehand (act_layout(ACT_Q8K, rows, k) at ws)
-bool gemv_q4k_rows_supported(int rows, int k);
-void launch_gemv_q4k_rows(const uint8_t* W, int n_out, int k, const uint8_t* ws, int rows, float* y, hipStream_t stream,
-                          const uint32_t* active = nullptr);
 // GateUpAct{Silu} at one row over a stacked [gate; up] X8 matrix of 2 n rows: y[i] = silu(g_i) * u_i
 void launch_gate_up_q4k_f32(const uint8_t* W, int n, int k, const float* x, float* y, hipStream_t stream,
                             const uint32_t* active = nullptr);
@@ -93,6 +90,8 @@ void launch_moe_gather_q8k(const float* x, const uint32_t* slots, int nentries, 
 void launch_moe_gateup(const uint8_t* gate, const uint8_t* up, int n_experts, int hidden,
                        int inter, const uint32_t* offsets, int nentries, MoeAct a,
                        const uint32_t* err, float* h, hipStream_t stream);
+void launch_q4k_dense_rows(const uint8_t* W, int x8, int n_out, int k, MoeAct a, int rows, float* y,
+                           hipStream_t stream, const uint32_t* active = nullptr);
 void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
                      const uint32_t* offsets, int nentries, MoeAct a, const uint32_t* slots,
                      const uint32_t* err, float* out, hipStream_t stream);

@@ -643,7 +643,7 @@ __global__ __launch_bounds__(256) void k_moe_gather_q8k(const float* __restrict_
                                                         const uint32_t* __restrict__ err,
                                                         MoeAct a, int gather,
                                                         const uint32_t* __restrict__ total) {
-    if (err[0]) return;
+    if (err && err[0]) return;
     if (total) nentries = (int)(*total < (uint32_t)nentries ? *total : (uint32_t)nentries);  // packed entries
     const int nb = k / 256;
     const int lane = threadIdx.x & 63;
@@ -725,15 +725,32 @@ struct Slot {
     bool on;    // this lane loads
     bool live;  // the slot loads at all (uniform): not padding, not an absent entry group
     int lds;
+    // weights in the X8 layout (a dense matrix): the lane's chunk q of super-block g0 + b, at
+    // x8_chunk_offset from the matrix base `src`, over a matrix of xnb super-blocks
+    bool x8;
+    int xq;
+    uint64_t xg0, xnb;
+};
+
+// The weight rows of an item: its first row (row0, or its byte offset in GGUF order) and, for a
+// dense matrix, the last row (later rows are clamped to it) and the X8 layout.
+struct ItemRows {
+    int row0, row_max;
+    uint32_t row0_off;
+    bool x8;
+    uint64_t nblocks;  // super-blocks of the whole matrix (X8)
 };
 
 template <class C>
-SYN_DEV Slot make_slot(int s, const uint8_t* const (&bases)[C::NM], uint32_t row0_off, uint32_t rb,
+SYN_DEV Slot make_slot(int s, const uint8_t* const (&bases)[C::NM], const ItemRows& ir, uint32_t rb,
                        const MoeAct& a, int k, int ent0, int nent) {
     const int lane = threadIdx.x & 63;
     Slot r;
     r.on = true;
     r.live = s < C::SLOTS;
+    r.x8 = false;
+    r.xq = 0;
+    r.xg0 = r.xnb = 0;
     if (s >= C::SLOTS) s = C::SLOTS - 1;
     if (s < C::WSLOTS) {
         // chunk ci = 64 s + lane of the tiles: matrix ci / (9 ROWS), then row, then part of 9
@@ -741,7 +758,18 @@ SYN_DEV Slot make_slot(int s, const uint8_t* const (&bases)[C::NM], uint32_t row
         r.on = ci0 < C::WCHUNKS;
         const int ci = r.on ? ci0 : 0;
         const int m = ci / (9 * C::ROWS), rem = ci - m * (9 * C::ROWS);
-        r.src = bases[m] + (row0_off + (uint32_t)(rem / 9) * rb + 16u * (uint32_t)(rem % 9));
+        const int rr = rem / 9, q = rem % 9;
+        if (ir.x8) {
+            const int row = ir.row0 + rr < ir.row_max ? ir.row0 + rr : ir.row_max;
+            r.x8 = true;
+            r.xq = q;
+            r.xg0 = (uint64_t)row * (uint64_t)(k / 256);
+            r.xnb = ir.nblocks;
+            r.src = bases[m];
+        } else {
+            const uint32_t rrc = ir.row_max >= 0 && ir.row0 + rr > ir.row_max ? (uint32_t)(ir.row_max - ir.row0) : (uint32_t)rr;
+            r.src = bases[m] + (ir.row0_off + rrc * rb + 16u * (uint32_t)q);
+        }
         r.step = 144u;
         r.lds = s * 1024;
     } else if (s < C::WSLOTS + C::NG) {
@@ -774,7 +802,8 @@ SYN_DEV Slot make_slot(int s, const uint8_t* const (&bases)[C::NM], uint32_t row
 // The explicit waits of the ring order the stages instead.
 SYN_DEV void issue_slot(const Slot& sl, int b, uint8_t* stage) {
     if (sl.live && sl.on) {
-        const uint8_t* src = sl.src + (uint64_t)sl.step * (uint32_t)b;
+        const uint8_t* src = sl.x8 ? sl.src + x8_chunk_offset(sl.xg0 + (uint32_t)b, sl.xq, sl.xnb)
+                                   : sl.src + (uint64_t)sl.step * (uint32_t)b;
         const uint32_t dst = (uint32_t)(uintptr_t)(lds_ptr)(stage + sl.lds);
         // the LDS address is an m0 operand (the compiler sets m0; s_nop is the wait state)
         asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
@@ -869,12 +898,12 @@ SYN_DEV void q4k_super(const uint8_t* st, int wave, int ent0, int ngroups, float
     }
 }
 
-// The item's super-blocks in order through the three-stage LDS ring.  Each wavefront issues the
-// same loads for every stage (the entry groups the item has); before the arithmetic on
-// super-block b it waits until only the loads of b + 1 may still fly, then the barrier makes
-// the stage whole for the workgroup.
-template <class C>
-SYN_DEV void ffn_rows(const uint8_t* const (&bases)[C::NM], uint32_t row0_off, uint32_t rb,
+// The item's super-blocks in order through an NS-stage LDS ring (three for the MoE layer).
+// Each wavefront issues the same loads for every stage (the entry groups the item has); before
+// the arithmetic on super-block b it waits until only the loads of b + 1 .. b + NS - 2 may still
+// fly, then the barrier makes the stage whole for the workgroup.
+template <class C, int NS = MOE_STAGES>
+SYN_DEV void ffn_rows(const uint8_t* const (&bases)[C::NM], const ItemRows& ir, uint32_t rb,
                       const MoeAct& a, int k, int ent0, int nent, int wave, uint8_t* lds,
                       float (&acc)[C::NM][C::NG]) {
     const int nb = k / 256;
@@ -883,27 +912,25 @@ SYN_DEV void ffn_rows(const uint8_t* const (&bases)[C::NM], uint32_t row0_off, u
     int live = 0;  // loads this wavefront issues per stage
 #pragma unroll
     for (int i = 0; i < C::PER_WAVE; ++i) {
-        sl[i] = make_slot<C>(wave + C::WV * i, bases, row0_off, rb, a, k, ent0, nent);
+        sl[i] = make_slot<C>(wave + C::WV * i, bases, ir, rb, a, k, ent0, nent);
         live += sl[i].live ? 1 : 0;
     }
 #pragma unroll
-    for (int i = 0; i < C::PER_WAVE; ++i) issue_slot(sl[i], 0, lds);
-    if (nb > 1) {
+    for (int q = 0; q < NS - 1; ++q)
+        if (q < nb)
 #pragma unroll
-        for (int i = 0; i < C::PER_WAVE; ++i) issue_slot(sl[i], 1, lds + C::BYTES);
-    }
-    int cur = 0;  // stage of super-block b
+            for (int i = 0; i < C::PER_WAVE; ++i) issue_slot(sl[i], q, lds + q * C::BYTES);
 #pragma unroll 1
     for (int b = 0; b < nb; ++b) {
-        wait_vm_n<C::PER_WAVE>(b + 1 < nb ? live : 0);
+        const int ahead = nb - 1 - b < NS - 2 ? nb - 1 - b : NS - 2;
+        wait_vm_n<C::PER_WAVE * (NS - 2)>(ahead * live);
         lds_barrier();
-        if (b + 2 < nb) {
-            const int nxt = cur == 0 ? 2 : cur - 1;  // (cur + 2) % 3
+        const int bn = b + NS - 1;
+        if (bn < nb) {
 #pragma unroll
-            for (int i = 0; i < C::PER_WAVE; ++i) issue_slot(sl[i], b + 2, lds + nxt * C::BYTES);
+            for (int i = 0; i < C::PER_WAVE; ++i) issue_slot(sl[i], bn, lds + (bn % NS) * C::BYTES);
         }
-        q4k_super<C>(lds + cur * C::BYTES, wave, ent0, ngroups, acc);
-        cur = cur == 2 ? 0 : cur + 1;
+        q4k_super<C>(lds + (b % NS) * C::BYTES, wave, ent0, ngroups, acc);
     }
 }
 
@@ -913,13 +940,23 @@ struct MoeItems {
     int n_experts;
     int row_groups;  // weight rows / rows per item
     int chunk;       // entries per item
+    // dense > 0: one matrix (n_experts 1, no offsets) whose entries are its first `dense` rows of
+    // activations, or *active of them when `active` is set (a step descriptor's rows_active)
+    int dense;
+    const uint32_t* active;
 };
+
+SYN_DEV int moe_dense_rows(const MoeItems& it) {
+    if (!it.active) return it.dense;
+    const uint32_t a = *it.active;
+    return a < (uint32_t)it.dense ? (int)a : it.dense;
+}
 
 // Maps a flat item index to (expert, row group, entry chunk); items of an expert with fewer
 // entries are empty.  Items: expert-major, then entry chunk, then row group.  The item space,
 // n_experts * row_groups * max_chunks, is sized on the device from the largest expert.
 SYN_DEV int moe_max_chunks(const MoeItems& it, const uint32_t* err) {
-    const int most = (int)err[1];
+    const int most = it.dense ? moe_dense_rows(it) : (int)err[1];
     return (most + it.chunk - 1) / it.chunk;
 }
 SYN_DEV bool moe_item(const MoeItems& it, int item, int max_chunks, int& e, int& rg, int& ent0,
@@ -930,7 +967,7 @@ SYN_DEV bool moe_item(const MoeItems& it, int item, int max_chunks, int& e, int&
     const int ch = r / it.row_groups;
     rg = r - ch * it.row_groups;
     if (e >= it.n_experts) return false;
-    const int b0 = (int)it.offsets[e], b1 = (int)it.offsets[e + 1];
+    const int b0 = it.dense ? 0 : (int)it.offsets[e], b1 = it.dense ? moe_dense_rows(it) : (int)it.offsets[e + 1];
     ent0 = b0 + ch * it.chunk;
     if (ent0 >= b1) return false;
     nent = b1 - ent0 < it.chunk ? b1 - ent0 : it.chunk;
@@ -958,7 +995,8 @@ __global__ __launch_bounds__(64 * WV) void k_moe_gateup(const uint8_t* __restric
         const int64_t ebytes = (int64_t)inter * rb;
         const uint8_t* const bases[2] = {gate + e * ebytes, up + e * ebytes};
         float acc[2][C::NG] = {};
-        ffn_rows<C>(bases, (uint32_t)(rg * C::ROWS) * rb, rb, a, hidden, ent0, nent, wave, lds, acc);
+        const ItemRows ir{rg * C::ROWS, -1, (uint32_t)(rg * C::ROWS) * rb, false, 0};
+        ffn_rows<C>(bases, ir, rb, a, hidden, ent0, nent, wave, lds, acc);
         const int row = rg * C::ROWS + wave * 16 + (lane & 15);
 #pragma unroll
         for (int g = 0; g < C::NG; ++g)
@@ -969,16 +1007,17 @@ __global__ __launch_bounds__(64 * WV) void k_moe_gateup(const uint8_t* __restric
 }
 
 // down: out[slot][row] = down_row . hq[entry], written to the entry's slot (the reference's
-// scatter, moe.rs:501-515).
-template <int WV, int CH>
+// scatter, moe.rs:501-515).  With it.dense (a dense Gemv of a few rows): one matrix `down` of
+// `hidden` rows (GGUF order, or X8 when x8), out[entry][row], no slots and no error word.
+template <int WV, int CH, int NS = MOE_STAGES>
 __global__ __launch_bounds__(64 * WV) void k_moe_down(const uint8_t* __restrict__ down, int hidden,
                                                       int inter, MoeItems it, MoeAct a,
                                                       const uint32_t* __restrict__ slots,
                                                       const uint32_t* __restrict__ err,
-                                                      float* __restrict__ out) {
+                                                      float* __restrict__ out, int x8) {
     using C = MoeCfg<1, WV, CH>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    if (err[0]) return;
+    if (err && err[0]) return;
     const int max_chunks = moe_max_chunks(it, err);
     const int total = it.n_experts * it.row_groups * max_chunks;
     const int lane = threadIdx.x & 63, p = lane >> 4;
@@ -989,11 +1028,15 @@ __global__ __launch_bounds__(64 * WV) void k_moe_down(const uint8_t* __restrict_
         if (!moe_item(it, item, max_chunks, e, rg, ent0, nent)) continue;  // uniform per workgroup
         const uint8_t* const bases[1] = {down + e * ((int64_t)hidden * rb)};
         float acc[1][C::NG] = {};
-        ffn_rows<C>(bases, (uint32_t)(rg * C::ROWS) * rb, rb, a, inter, ent0, nent, wave, lds, acc);
+        const ItemRows ir{rg * C::ROWS, it.dense ? hidden - 1 : -1, (uint32_t)(rg * C::ROWS) * rb, x8 != 0,
+                          (uint64_t)hidden * (uint64_t)(inter / 256)};
+        ffn_rows<C, NS>(bases, ir, rb, a, inter, ent0, nent, wave, lds, acc);
         const int row = rg * C::ROWS + wave * 16 + (lane & 15);
 #pragma unroll
-        for (int g = 0; g < C::NG; ++g)
-            if (4 * g + p < nent) out[(int64_t)slots[ent0 + 4 * g + p] * hidden + row] = acc[0][g];
+        for (int g = 0; g < C::NG; ++g) {
+            const int ent = ent0 + 4 * g + p;
+            if (4 * g + p < nent && row < hidden) out[(int64_t)(slots ? (int)slots[ent] : ent) * hidden + row] = acc[0][g];
+        }
         lds_barrier();  // the ring is refilled by the next item
     }
 }
@@ -1015,7 +1058,7 @@ void launch_moe_gateup(const uint8_t* gate, const uint8_t* up, int n_experts, in
                        int inter, const uint32_t* offsets, int nentries, MoeAct a,
                        const uint32_t* err, float* h, hipStream_t stream) {
     using C = MoeCfg<2, GU_WV, GU_CH>;
-    const MoeItems it{offsets, n_experts, inter / C::ROWS, C::CH};
+    const MoeItems it{offsets, n_experts, inter / C::ROWS, C::CH, 0, nullptr};
     const int lds = MOE_STAGES * C::BYTES;
     static const hipError_t lds_ok = hipFuncSetAttribute(
         (const void*)k_moe_gateup<GU_WV, GU_CH>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -1028,13 +1071,42 @@ void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
                      const uint32_t* offsets, int nentries, MoeAct a, const uint32_t* slots,
                      const uint32_t* err, float* out, hipStream_t stream) {
     using C = MoeCfg<1, DN_WV, DN_CH>;
-    const MoeItems it{offsets, n_experts, hidden / C::ROWS, C::CH};
+    const MoeItems it{offsets, n_experts, hidden / C::ROWS, C::CH, 0, nullptr};
     const int lds = MOE_STAGES * C::BYTES;
     static const hipError_t lds_ok = hipFuncSetAttribute(
         (const void*)k_moe_down<DN_WV, DN_CH>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     (void)lds_ok;  // a refusal shows as the launch's error
     hipLaunchKernelGGL((k_moe_down<DN_WV, DN_CH>), dim3(moe_grid(it, nentries)), dim3(C::THREADS),
-                       lds, stream, down, hidden, inter, it, a, slots, err, out);
+                       lds, stream, down, hidden, inter, it, a, slots, err, out, 0);
+}
+
+// A dense Q4_K Gemv of 2 to 31 rows on the decode expert kernel: the matrix as one expert, the
+// rows as its entries (quantized by launch_moe_gather_q8k without a gather), y[row][out].
+// Narrow matrices take 16-row items so that the grid still covers the GPU.
+// The dense form streams the whole matrix once through few workgroups, so its ring is deeper
+// (DENSE_STAGES - 1 super-blocks of every row in flight) than the MoE layer's.
+constexpr int DENSE_STAGES = 8;
+
+template <int WV>
+static void launch_dense_wv(const uint8_t* W, int x8, int n_out, int k, MoeAct a, int rows, float* y,
+                            hipStream_t stream, const uint32_t* active) {
+    using C = MoeCfg<1, WV, DN_CH>;
+    const MoeItems it{nullptr, 1, (n_out + C::ROWS - 1) / C::ROWS, C::CH, rows, active};
+    const int lds = DENSE_STAGES * C::BYTES;
+    static const hipError_t lds_ok = hipFuncSetAttribute(
+        (const void*)k_moe_down<WV, DN_CH, DENSE_STAGES>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    (void)lds_ok;  // a refusal shows as the launch's error
+    const unsigned grid = (unsigned)it.row_groups * (unsigned)((rows + C::CH - 1) / C::CH);
+    hipLaunchKernelGGL((k_moe_down<WV, DN_CH, DENSE_STAGES>), dim3(grid), dim3(C::THREADS), lds, stream, W, n_out,
+                       k, it, a, nullptr, nullptr, y, x8);
+}
+
+void launch_q4k_dense_rows(const uint8_t* W, int x8, int n_out, int k, MoeAct a, int rows, float* y,
+                           hipStream_t stream, const uint32_t* active) {
+    if (n_out >= 8192)
+        launch_dense_wv<2>(W, x8, n_out, k, a, rows, y, stream, active);
+    else
+        launch_dense_wv<1>(W, x8, n_out, k, a, rows, y, stream, active);
 }
 
 // ============================================================================================

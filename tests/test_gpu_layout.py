@@ -101,7 +101,7 @@ def test_batch_layer_full_shapes_equal_oracle(S):
                 assert_same(host(y), want[i], f"{name} problem {i} rep {rep}")
 
 
-@pytest.mark.parametrize("rows,n_out,k", [(2, 64, 2048), (64, 300, 4096), (100, 256, 14336)])
+@pytest.mark.parametrize("rows,n_out,k", [(32, 64, 2048), (64, 300, 4096), (100, 256, 14336)])
 def test_gemm_x8_equals_oracle(S, rows, n_out, k):
     rs = np.random.default_rng(rows + n_out + k)
     w = random_q4k(rs, n_out, k)
@@ -113,10 +113,12 @@ def test_gemm_x8_equals_oracle(S, rows, n_out, k):
 
 
 @pytest.mark.parametrize("rows,n_out,k", [(2, 14336, 4096), (3, 14336, 4096), (8, 4096, 14336), (7, 37, 1536),
-                                          (4, 9, 16384), (5, 300, 256)])
-def test_x8_rows_2_to_8_equal_oracle(S, rows, n_out, k):
-    """2..8 rows over X8 weights: the rows quantized once, one super-block per lane holding its
-    terms for every row (k need not be a multiple of 2048 here)."""
+                                          (4, 9, 16384), (5, 300, 256), (16, 8192, 4096), (17, 1000, 2304),
+                                          (31, 33, 1536), (13, 4096, 14336)])
+def test_x8_rows_2_to_31_equal_oracle(S, rows, n_out, k):
+    """2..31 rows over X8 weights on the decode expert kernel: the rows quantized once, four-row
+    groups on the int8 matrix cores, 16- or 32-row items (k need not be a multiple of 2048: the
+    X8 chunk addresses are computed per super-block)."""
     rs = np.random.default_rng(rows * 7 + n_out + k)
     w = random_q4k(rs, n_out, k)
     x = o.normal(0xF0 + rows, 1.0, rows * k).reshape(rows, k)
@@ -128,6 +130,20 @@ def test_x8_rows_2_to_8_equal_oracle(S, rows, n_out, k):
 
 def test_x8_refusals(S):
     W = S.repack(S.Weights(S.WeightType.Q4K, torch.zeros(64 * 6 * 144, dtype=torch.uint8, device="cuda"), 64, 1536))
-    x = torch.zeros(9, 1536, device="cuda")
-    with pytest.raises(S.SynError):  # from 9 rows the GEMM takes rows of whole 8-block runs only
-        S.gemv(W, x, 9)
+    x = torch.zeros(32, 1536, device="cuda")
+    with pytest.raises(S.SynError):  # from 32 rows the GEMM takes rows of whole 8-block runs only
+        S.gemv(W, x, 32)
+
+
+@pytest.mark.parametrize("rows,n_out,k", [(2, 14336, 4096), (8, 4096, 14336), (9, 300, 1536), (31, 37, 256),
+                                          (20, 6144, 4096)])
+def test_source_q4k_rows_2_to_31_equal_oracle(S, rows, n_out, k):
+    """The same kernel over GGUF-order Q4_K weights (syn_gemv)."""
+    rs = np.random.default_rng(rows * 11 + n_out + k)
+    w = random_q4k(rs, n_out, k)
+    x = o.normal(0xF8 + rows, 1.0, rows * k).reshape(rows, k)
+    W = S.Weights(S.WeightType.Q4K, dev(w), n_out, k)
+    announce(f"source q4k rows={rows} {n_out}x{k}")
+    y = torch.full((rows, n_out), float("nan"), device="cuda")
+    S.gemv(W, dev(x), rows, y=y)
+    assert_same(host(y), o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=16), "source rows")

@@ -231,8 +231,8 @@ def test_query_answers_none_for_unserved_shapes(cx):
     assert pr.query(cx.ctx, dict(gemv_key(o.Q8_0), layout=1), shape(1, 64, 256)) is None
     assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=2), shape(1, 64, 256)) is None
     assert pr.query(cx.ctx, dict(gemv_key(o.Q8_0), layout=2), shape(130, 64, 256)) is not None
-    assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(9, 64, 1536)) is None  # GEMM: k % 2048
-    assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(8, 64, 1536)) is not None  # 2..8 rows
+    assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(32, 64, 1536)) is None  # GEMM: k % 2048
+    assert pr.query(cx.ctx, dict(gemv_key(o.Q4_K), layout=1), shape(31, 64, 1536)) is not None  # 2..31 rows
     assert pr.query(cx.ctx, {"op": "Attention", "schemes": [], "layout": 0, "variant": 0},
                     shape(1, 64, 256)) is None
     with pytest.raises(cx.P.ProviderError) as e:
