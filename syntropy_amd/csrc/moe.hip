@@ -1083,9 +1083,9 @@ void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
 // A dense Q4_K Gemv of 2 to 31 rows on the decode expert kernel: the matrix as one expert, the
 // rows as its entries (quantized by launch_moe_gather_q8k without a gather), y[row][out].
 // Narrow matrices take 16-row items so that the grid still covers the GPU.
-// The dense form streams the whole matrix once through few workgroups, so its ring is deeper
-// (DENSE_STAGES - 1 super-blocks of every row in flight) than the MoE layer's.
-constexpr int DENSE_STAGES = 8;
+// The dense form's ring: three stages, as the MoE layer's (eight measured no faster: the
+// launch's fixed cost and the rows' read pattern bound it, not the loads in flight).
+constexpr int DENSE_STAGES = MOE_STAGES;
 
 template <int WV>
 static void launch_dense_wv(const uint8_t* W, int x8, int n_out, int k, MoeAct a, int rows, float* y,
