@@ -82,9 +82,9 @@ int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uin
  *   a Q8_0 block, 16 a Q4_0 block), then every block's F16 scale in block order; also the same
  *   length and shape-free.  syn_split_repack(_host) as syn_q4k_repack(_host), for `wtype`.
  * syn_gemv_layout(_workspace_bytes): the Gemv op over a matrix in `layout` (0 is syn_gemv); for
- *   layout 1 one row runs the decode kernel with the row quantized in every workgroup, 2 to 8 rows
- *   the multi-row decode kernel on rows quantized beforehand (both k_in <= 16384), more rows the
- *   matrix-core GEMM (k_in a multiple of 2048).  Layout 2 quantizes the rows to Q8_0 blocks and
+ *   layout 1 one row runs the decode kernel with the row quantized in every workgroup (k_in <=
+ *   16384), 2 to 31 rows the decode expert kernel on rows quantized beforehand (int8 matrix
+ *   cores, the matrix as one expert), more rows the matrix-core GEMM (k_in a multiple of 2048).  Layout 2 quantizes the rows to Q8_0 blocks and
  *   runs the split decode kernel eight rows at a time, or, for Q8_0, the int8 matrix-core GEMM
  *   from 2 rows (k_in a multiple of 128) or from 9 rows (other k_in).
  * syn_gemv_batch_layout / syn_gemv_batch_quantized_layout: the grouped decode of every problem
