@@ -307,13 +307,15 @@ constexpr int dec_occupancy() { return FUSE ? 4 : 6; }
 // up rows; the first half of the wavefronts computes gate rows and the second half the same up
 // rows, and y[i] = silu(g_i) * u_i (crates/kernels/src/reference/linear.rs:75-112 with the
 // Gemv values, the product rounded once) is formed after one LDS exchange.
-template <int LAYOUT, int FUSE, int GATED>
-__global__ __launch_bounds__(64 * dec_waves<LAYOUT>())
+// WV: wavefronts per workgroup (dec_waves by default; 16 for the fused form at long rows, where
+// every workgroup re-quantizes the row: fewer, larger workgroups quantize it fewer times).
+template <int LAYOUT, int FUSE, int GATED, int WV = dec_waves<LAYOUT>()>
+__global__ __launch_bounds__(64 * WV)
 __attribute__((amdgpu_waves_per_eu(dec_occupancy<LAYOUT, FUSE>())))
 void k_gemv_q4k_batch(DecBatch bt) {
     if (active_rows(bt.active, 0, 1) == 0) return;  // a step with no active row
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int WAVES = dec_waves<LAYOUT>();
+    constexpr int WAVES = WV;
     constexpr int RW = GATED ? WAVES / 2 : WAVES;  // wavefronts per set of output rows
     int p = 0;
     while (p + 1 < bt.np && (int)blockIdx.x >= bt.wg_begin[p + 1]) ++p;
@@ -452,11 +454,11 @@ void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* w
                   reinterpret_cast<const int32_t*>(ws + L.sums), y, stream);
 }
 
-template <int LAYOUT, int FUSE, int GATED = 0>
+template <int LAYOUT, int FUSE, int GATED = 0, int WV = dec_waves<LAYOUT>()>
 static void launch_batch(int np, const uint8_t* const* W, const int* n_out, const int* k,
                          const uint8_t* const* ws, const float* const* x, float* const* y,
                          hipStream_t stream, const uint32_t* active = nullptr) {
-    constexpr int WAVES = dec_waves<LAYOUT>();
+    constexpr int WAVES = WV;
     constexpr int RW = GATED ? WAVES / 2 : WAVES;
     DecBatch bt{};
     bt.np = np;
@@ -478,7 +480,7 @@ static void launch_batch(int np, const uint8_t* const* W, const int* n_out, cons
     bt.wg_begin[np] = wg;
     if (wg == 0) return;
     // the activation row, then 64 fold terms per wavefront (and the gate sums when GATED)
-    hipLaunchKernelGGL((k_gemv_q4k_batch<LAYOUT, FUSE, GATED>), dim3(wg), dim3(64 * WAVES),
+    hipLaunchKernelGGL((k_gemv_q4k_batch<LAYOUT, FUSE, GATED, WV>), dim3(wg), dim3(64 * WAVES),
                        align_up(q4k_dec_lds(max_nb), 16) + (GATED ? 2 : 1) * WAVES * 64 * 4, stream, bt);
 }
 
@@ -495,7 +497,12 @@ bool gemv_q4k_batch_fusable(int k) { return k % 256 == 0 && k > 0 && k <= 64 * 2
 void launch_gemv_q4k_batch_f32(const uint8_t* const* W, int np, const int* n_out, const int* k,
                                const float* const* x, float* const* y, hipStream_t stream,
                                const uint32_t* active) {
-    launch_batch<LAYOUT_X8, 1>(np, W, n_out, k, nullptr, x, y, stream, active);
+    int max_k = 0;
+    for (int p = 0; p < np; ++p) max_k = k[p] > max_k ? k[p] : max_k;
+    if (max_k > 32 * 256)  // rows of more than 32 super-blocks: 16-wavefront workgroups
+        launch_batch<LAYOUT_X8, 1, 0, 16>(np, W, n_out, k, nullptr, x, y, stream, active);
+    else
+        launch_batch<LAYOUT_X8, 1>(np, W, n_out, k, nullptr, x, y, stream, active);
 }
 
 void launch_gate_up_q4k_f32(const uint8_t* W, int n, int k, const float* x, float* y, hipStream_t stream,
