@@ -497,10 +497,16 @@ bool gemv_q4k_batch_fusable(int k) { return k % 256 == 0 && k > 0 && k <= 64 * 2
 void launch_gemv_q4k_batch_f32(const uint8_t* const* W, int np, const int* n_out, const int* k,
                                const float* const* x, float* const* y, hipStream_t stream,
                                const uint32_t* active) {
-    int max_k = 0;
-    for (int p = 0; p < np; ++p) max_k = k[p] > max_k ? k[p] : max_k;
+    int max_k = 0, wg8 = 0;  // wg8: workgroups at eight wavefronts
+    for (int p = 0; p < np; ++p) {
+        max_k = k[p] > max_k ? k[p] : max_k;
+        const int nb = k[p] / 256, rows_per_wg = 8 * (64 / (nb <= 16 ? 16 : nb <= 32 ? 32 : 64));
+        wg8 += (n_out[p] + rows_per_wg - 1) / rows_per_wg;
+    }
     if (max_k > 32 * 256)  // rows of more than 32 super-blocks: 16-wavefront workgroups
         launch_batch<LAYOUT_X8, 1, 0, 16>(np, W, n_out, k, nullptr, x, y, stream, active);
+    else if (wg8 <= 128)  // at most half the CUs busy: 4-wavefront workgroups, twice as many
+        launch_batch<LAYOUT_X8, 1, 0, 4>(np, W, n_out, k, nullptr, x, y, stream, active);
     else
         launch_batch<LAYOUT_X8, 1>(np, W, n_out, k, nullptr, x, y, stream, active);
 }
