@@ -815,38 +815,36 @@ SYN_DEV void issue_slot(const Slot& sl, int b, uint8_t* stage) {
 
 SYN_DEV long pack2(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
 
-// One super-block of the wavefront's 16 rows of NM matrices (gate and up: NM = 2) against the
-// item's entry groups, operands from the stage in LDS.  acc[m][g]: row c, entry 4g + p.
-template <class C>
-SYN_DEV void q4k_super(const uint8_t* st, int wave, int ent0, int ngroups, float (&acc)[C::NM][C::NG]) {
-    constexpr int NM = C::NM;
-    using L = C;
-    const int lane = threadIdx.x & 63, c = lane & 15, p = lane >> 4, jq = c >> 2;
+// One super-block of 16 weight rows of NM matrices, as lane (c, p) holds it: row c's 16-byte
+// header and its codes at 16 + 32 g + 8 p (g = 0..3).
+template <int NM>
+struct WBlock {
     v4u hdr[NM];
+    uint32_t q[NM][8];
+};
+
+// The super-block's arithmetic against the item's entry groups: the entries' codes [CH][256]
+// (chunk-swizzled), their sums [CH][16] and the scale window `dxw`, all in LDS.  acc[m][g]
+// (row c, entry 4g + p) accumulates the super-block's term (gemv.rs:539-547).
+template <int NM, int NG>
+SYN_DEV void q4k_block(const WBlock<NM>& w, const uint8_t* codes, const uint8_t* lhs, const float* dxw, int ent0,
+                       int ngroups, float (&acc)[NM][NG]) {
+    const int lane = threadIdx.x & 63, c = lane & 15, p = lane >> 4, jq = c >> 2;
     long bq[NM][8];  // B operands: the row's codes of sub-block j, k part p
     uint32_t mns[NM][2];
     int sc0[NM], sc1[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-        const uint8_t* row = st + m * L::W + (16 * wave + c) * 144;
-        hdr[m] = *reinterpret_cast<const v4u*>(row);
-        uint32_t q[8];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const uint2 v = *reinterpret_cast<const uint2*>(row + 16 + 32 * g + 8 * p);
-            q[2 * g] = v.x;
-            q[2 * g + 1] = v.y;
-        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const uint32_t lo = q[2 * (j >> 1)], hi = q[2 * (j >> 1) + 1];
+            const uint32_t lo = w.q[m][2 * (j >> 1)], hi = w.q[m][2 * (j >> 1) + 1];
             const uint32_t c0 = (j & 1) ? (lo >> 4) & 0x0F0F0F0Fu : lo & 0x0F0F0F0Fu;
             const uint32_t c1 = (j & 1) ? (hi >> 4) & 0x0F0F0F0Fu : hi & 0x0F0F0F0Fu;
             bq[m][j] = pack2(c0, c1);
         }
         // get_scale_min_k4 (gemv.rs:528-537) on packed bytes: scales of sub-blocks p and 4 + p,
         // mins of sub-blocks 0-3 | 4-7
-        const uint32_t w0 = hdr[m].y, w1 = hdr[m].z, w2 = hdr[m].w;
+        const uint32_t w0 = w.hdr[m].y, w1 = w.hdr[m].z, w2 = w.hdr[m].w;
         const uint32_t sc_lo = w0 & 0x3F3F3F3Fu;
         const uint32_t sc_hi = (w2 & 0x0F0F0F0Fu) | ((w0 >> 2) & 0x30303030u);
         sc0[m] = (int)((sc_lo >> (8 * p)) & 0xFFu);
@@ -856,14 +854,14 @@ SYN_DEV void q4k_super(const uint8_t* st, int wave, int ent0, int ngroups, float
     }
     const v4i z = {0, 0, 0, 0};
 #pragma unroll
-    for (int g = 0; g < C::NG; ++g) {
+    for (int g = 0; g < NG; ++g) {
         if (g >= ngroups) break;  // uniform
         // entry 4g + (c & 3): its codes of sub-blocks jq and jq + 4, k part p
         const int ta = 4 * g + (c & 3);
-        const v4u ap = *reinterpret_cast<const v4u*>(st + L::CODES + ta * 256 + 16 * ((4 * p + jq) ^ (c & 3)));
+        const v4u ap = *reinterpret_cast<const v4u*>(codes + ta * 256 + 16 * ((4 * p + jq) ^ (c & 3)));
         const int to = 4 * g + p;  // the lane's output entry
-        const v4u lh = *reinterpret_cast<const v4u*>(st + L::LH + 16 * to);
-        const float dx = reinterpret_cast<const float*>(st + L::DX)[(ent0 & 3) + to];
+        const v4u lh = *reinterpret_cast<const v4u*>(lhs + 16 * to);
+        const float dx = dxw[(ent0 & 3) + to];
         v4i d0[NM], d1[NM];
 #pragma unroll
         for (int m = 0; m < NM; ++m) d0[m] = d1[m] = z;
@@ -892,10 +890,30 @@ SYN_DEV void q4k_super(const uint8_t* st, int wave, int ent0, int ngroups, float
             const int s1 = (int)r2[0] + (int)r2[1];
             const int s2 = sdot4(mns[m][0], lh.x, sdot4(mns[m][1], lh.y, 0)) +
                            128 * sdot4(mns[m][0], lh.z, sdot4(mns[m][1], lh.w, 0));
-            const float d = f16_to_f32(hdr[m].x), dmin = f16_to_f32(hdr[m].x >> 16);
+            const float d = f16_to_f32(w.hdr[m].x), dmin = f16_to_f32(w.hdr[m].x >> 16);
             acc[m][g] = acc[m][g] + ((d * dx) * (float)s1 - (dmin * dx) * (float)s2);
         }
     }
+}
+
+// One super-block of the wavefront's 16 rows of NM matrices from the stage's weight tiles.
+template <class C>
+SYN_DEV void q4k_super(const uint8_t* st, int wave, int ent0, int ngroups, float (&acc)[C::NM][C::NG]) {
+    const int lane = threadIdx.x & 63, c = lane & 15, p = lane >> 4;
+    WBlock<C::NM> w;
+#pragma unroll
+    for (int m = 0; m < C::NM; ++m) {
+        const uint8_t* row = st + m * C::W + (16 * wave + c) * 144;
+        w.hdr[m] = *reinterpret_cast<const v4u*>(row);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint2 v = *reinterpret_cast<const uint2*>(row + 16 + 32 * g + 8 * p);
+            w.q[m][2 * g] = v.x;
+            w.q[m][2 * g + 1] = v.y;
+        }
+    }
+    q4k_block<C::NM, C::NG>(w, st + C::CODES, st + C::LH, reinterpret_cast<const float*>(st + C::DX), ent0,
+                            ngroups, acc);
 }
 
 // The item's super-blocks in order through an NS-stage LDS ring (three for the MoE layer).
