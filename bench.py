@@ -509,6 +509,7 @@ def bench_moe(torch, S, M, steps, warmup, cpu_seconds):
         res["cpu_baseline"] = {"value": round(c["tokens"] * n / cdt, 1), "unit": "tokens/s",
                                "cores": threads, "kind": "port",
                                "sample": f"{n} MoE layers of 64 tokens in {cdt:.1f} s"}
+        res["speedup_over_cpu"] = round(res["value"] / res["cpu_baseline"]["value"], 1)
     return res
 
 
@@ -621,6 +622,7 @@ def bench_prefill(torch, S, M, steps, warmup, cpu_seconds):
         res["cpu_baseline"] = {"value": round(rows * n / cdt, 1), "unit": "tokens/s (dense gate+down)",
                                "cores": threads, "kind": "port",
                                "sample": f"{n} x {rows} token rows through gate and down in {cdt:.1f} s"}
+        res["speedup_over_cpu"] = round(res["dense_tokens_per_s"] / res["cpu_baseline"]["value"], 1)
     return res
 
 
@@ -681,6 +683,8 @@ def main():
             out["config"], out["roofline"] = lay["config"], lay["roofline"]
             if not a.no_cpu:
                 out["cpu_baseline"] = cpu_layer_baseline(copies, xs, a.cpu_seconds)
+                # the whole GPU step (quantization + GEMVs) against the CPU path's whole layer
+                out["speedup_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
         if "provider" in want:
             out["provider_path"] = bench_provider(torch, S, a, copies, xs)
         del copies, xs, ys, wss
