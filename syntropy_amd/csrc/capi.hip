@@ -516,27 +516,49 @@ SYN_EXPORT int syn_split_repack_host(uint32_t layout, int32_t wtype, const void*
 
 // Gemv over weights in a repacked layout.  Q4_K in X8: one row runs the grouped decode kernel,
 // 2 to 31 rows the decode expert kernel (int8 matrix cores), more rows the matrix-core GEMM (which
-// needs rows of whole 8-block runs: k_in a multiple of 2048).  Q8_0 / Q4_0 in SPLIT: Q8_0 activation rows, the
-// split decode kernel for up to 8 rows at a time, the int8 matrix-core GEMM for Q8_0 from 2 rows
-// (rows of whole 4-block stages) or 9.
+// needs rows of whole 8-block runs: k_in a multiple of 2048).  Q8_0 / Q4_0 in SPLIT: Q8_0 activation
+// rows, the split decode kernel for up to 8 rows at a time, the int8 matrix-core GEMM where its
+// LDS-staged form takes the shape (rows of whole 4-block stages) and is the faster, and for other
+// Q8_0 shapes from 9 rows.
 constexpr uint32_t SPLIT_GEMM_MIN_ROWS = 9;
 constexpr uint32_t SPLIT_GEMM_MAX_ROWS = 65535u * 32u;  // the GEMM grid's token tiles
 
 namespace {
-// Q8_0 rows on the int8 matrix cores: from 2 rows where the LDS-staged GEMM takes the shape
-// (16-token tiles beat the split decode kernel there), else from 9.
+// Whether the staged GEMM beats the split decode kernel at 2 to 16 rows (one 16-token tile), from
+// estimated microseconds fitted on MI355X timings of both kernels (Q8_0 and Q4_0, 4096 to 14336
+// rows of 4096 to 14336 values).  Split decode kernel, per launch of r <= 8 rows over M million
+// weights: 3 + read M + 0.04 M r (read 0.20 for Q8_0, 0.09 for Q4_0: the weights' HBM time).
+// Staged GEMM: 4 + per 4-block stage 0.33 (Q8_0) or 0.40 (Q4_0), 15% more per further workgroup
+// a CU holds.  Each wavefront runs its row group's stages one after another, so the GEMM's time
+// follows the row length, while the decode kernel's grows with the rows; beyond 16 rows the GEMM
+// is always the faster.  Both produce the same bits.
+bool staged_faster(int32_t wtype, uint32_t n_out, uint32_t k_in, uint32_t rows) {
+    if (rows > 16) return true;
+    const double M = (double)n_out * (double)k_in * 1e-6;
+    const double read = wtype == SYN_Q8_0 ? 0.20 : 0.09;
+    double gemv = 0.0;
+    for (uint32_t r0 = 0; r0 < rows; r0 += 8) gemv += 3.0 + read * M + 0.04 * M * (rows - r0 < 8 ? rows - r0 : 8);
+    const double wgs_per_cu = (double)((((uint64_t)n_out + 31) / 32 + 255) / 256);  // 256 CUs
+    const double gemm =
+        4.0 + (wtype == SYN_Q8_0 ? 0.33 : 0.40) * (double)(k_in / 128) * (1.0 + 0.15 * (wgs_per_cu - 1.0));
+    return gemm < gemv;
+}
+
+// Rows on the int8 matrix cores: where the LDS-staged GEMM takes the shape and is the faster
+// (above), else Q8_0 from 9 rows on the register-staged GEMM.
 bool split_gemm(int32_t wtype, uint32_t n_out, uint32_t k_in, uint32_t rows) {
-    if (wtype != SYN_Q8_0) return false;
-    return rows >= SPLIT_GEMM_MIN_ROWS ||
-           (rows >= 2 && syn::gemm_q8_staged_fits((int)n_out, (int)k_in, (int)rows));
+    if (wtype != SYN_Q8_0 && wtype != SYN_Q4_0) return false;
+    if (rows >= 2 && syn::gemm_q8_staged_fits((int)wtype, (int)n_out, (int)k_in, (int)rows))
+        return staged_faster(wtype, n_out, k_in, rows);
+    return wtype == SYN_Q8_0 && rows >= SPLIT_GEMM_MIN_ROWS;
 }
 
 // The products over a SPLIT matrix from rows already quantized to Q8_0 blocks in ws.
 void split_products(int32_t wtype, const void* w, uint32_t n_out, uint32_t k_in, const void* ws, uint32_t rows,
                     float* y, void* stream, const uint32_t* active) {
     if (split_gemm(wtype, n_out, k_in, rows))
-        syn::launch_gemm_q8_split((const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows, y,
-                                  (hipStream_t)stream, active);
+        syn::launch_gemm_q8_split((int)wtype, (const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows,
+                                  y, (hipStream_t)stream, active);
     else
         syn::launch_gemv_split(wtype, (const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows, y,
                                (hipStream_t)stream, active);

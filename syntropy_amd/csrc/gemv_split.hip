@@ -11,9 +11,10 @@
 // rows are staged in LDS once per workgroup.  Each block's term is written to LDS and lane r
 // folds activation row r's terms in block order.
 //
-// 9 or more rows, Q8_0 (k_gemm_q8_split): v_mfma_i32_16x16x32_i8 takes one 32-value block of 16
-// weight rows against 16 tokens: the exact I32 sums of 256 outputs, which the lane owning each
-// output scales and folds (one term per block, in block order).
+// 2 or more rows (k_gemm_q8_staged, Q8_0 and Q4_0, where rows hold whole 4-block stages; else for
+// Q8_0 from 9 rows k_gemm_q8_split): v_mfma_i32_16x16x32_i8 takes one 32-value block of 16 weight
+// rows against 16 tokens: the exact I32 sums of 256 outputs, which the lane owning each output
+// scales and folds (one term per block, in block order).
 #include <type_traits>
 
 #include "common.hpp"
@@ -368,38 +369,63 @@ __global__ __launch_bounds__(256) void k_gemm_q8_split(const uint8_t* __restrict
 //
 // A workgroup takes 32 weight rows (two wavefront row groups of 16) x TW = 16 TT TG tokens (TG
 // token groups of 16 TT), stage by stage: four blocks of every operand are copied into LDS by
-// global_load_lds while earlier stages compute.  Stage layout (bytes):
-//   codes of the rows   [row][128]      4096   a row's four blocks, swizzled (below)
-//   codes of the tokens [token][128]    128 TW the same
+// global_load_lds while earlier stages compute.  Stage layout (bytes), WL = 4 CB (the rows' code
+// bytes per stage: 128 for Q8_0, 64 for Q4_0):
+//   codes of the rows   [row][WL]       32 WL  a row's four blocks, swizzled (below)
+//   codes of the tokens [token][128]    128 TW the same as Q8_0 rows
 //   row scales          [row][block] F16  256
 //   token scales        [token][block] F32 16 TW
-// A copy instruction moves 1 KB: eight rows' (or tokens') whole 128-byte lines, 16 bytes a lane.
-// Within a line the 16-byte halves of the four blocks are stored at slot 2 (j ^ ((c >> 1) & 3)) +
-// (h ^ (c >> 3)) for block j, half h of the line's row or token c (mod 16), so that the matrix
-// operand reads (16 lines, one 16-byte half each per half-wavefront) hit 16 distinct bank groups.
+// A copy instruction moves 1 KB, 16 bytes a lane: eight 128-byte lines (Q8_0 rows, tokens) or
+// sixteen 64-byte Q4_0 row lines.  Within a 128-byte line the 16-byte halves of the four blocks
+// are stored at slot 2 (j ^ ((c >> 1) & 3)) + (h ^ (c >> 3)) for block j, half h of the line's
+// row or token c (mod 16); within a 64-byte Q4_0 line block j sits at slot j ^ ((c >> 2) & 3).
+// Either way a matrix operand read (16 lines, 8 bytes of each for each of two lane quarters per
+// half-wavefront) covers 256 distinct bytes modulo 256: every bank once.
 // A wavefront issues the same number of copies every stage, so its wait is a fixed count.
+//
+// Q4_0: lane (c, p) takes the low nibbles (p < 2) or the high nibbles (p >= 2) of bytes 8 (p & 1)
+// .. +7 of the block's 16: elements 8 p .. 8 p + 7 of the block, the same elements as the token
+// operand's 8 bytes at 8 p.  The nibbles n become the int8 values n - 8 per byte with
+// ((n + 0x78) ^ 0x80), which no byte carries out of, so the sums are the block's exact
+// sum of (n - 8) x.
 
 constexpr int QS_S = 4;    // blocks per stage
 constexpr int QS_RW = 32;  // weight rows per workgroup
 constexpr int QS_NS_MAX = 3;
 
-template <int TT, int TG>
+template <int FMT, int TT, int TG>
 struct QsCfg {
-    static constexpr int NW = 2 * TG;      // wavefronts
-    static constexpr int TW = 16 * TT * TG;  // tokens
-    static constexpr int W_OFF = 0, A_OFF = QS_RW * QS_S * 32;
+    static constexpr int CB = FMT == T_Q8_0 ? 32 : 16;  // code bytes per block
+    static constexpr int WL = QS_S * CB;                 // a row's code bytes per stage
+    static constexpr int NW = 2 * TG;                    // wavefronts
+    static constexpr int TW = 16 * TT * TG;              // tokens
+    static constexpr int W_OFF = 0, A_OFF = QS_RW * WL;
     static constexpr int SC_OFF = A_OFF + TW * QS_S * 32;
     static constexpr int DX_OFF = SC_OFF + QS_RW * QS_S * 2;
     static constexpr int STAGE = DX_OFF + TW * QS_S * 4;
     // ring stages: as many as 64 KB hold, at most QS_NS_MAX
     static constexpr int NS = 64 * 1024 / STAGE < QS_NS_MAX ? 64 * 1024 / STAGE : QS_NS_MAX;
-    static constexpr int COPIES = (4 + TW / 8 + (TG == 1 ? 2 : 4)) / NW;  // per wavefront per stage
-    static_assert((4 + TW / 8 + (TG == 1 ? 2 : 4)) % NW == 0, "copies split evenly");
+    // copies per stage: row codes, token codes, and the two scale sets, each set whole or in
+    // SPARTS / DPARTS parts, so that the count splits evenly over the wavefronts
+    static constexpr int WCOPIES = QS_RW * WL / 1024;
+    static constexpr int SPARTS = TG == 1 || (FMT == T_Q4_0 && TG == 2) ? 1 : 2;
+    static constexpr int DPARTS = TG == 1 ? 1 : FMT == T_Q8_0 ? 2 : TG == 4 ? 4 : 1;
+    static constexpr int TOTAL = WCOPIES + TW / 8 + SPARTS + DPARTS;
+    static constexpr int COPIES = TOTAL / NW;  // per wavefront per stage
+    static_assert(TOTAL % NW == 0, "copies split evenly");
+    static_assert(NS >= 2 && COPIES * (NS - 2) <= 63, "the wait count fits vmcnt");
 };
 
 // The LDS byte offset, within its 128-byte line, of block j's 8 bytes at 8 p for line c.
 SYN_DEV int qs_slot(int c, int j, int p) {
     return 32 * (j ^ ((c >> 1) & 3)) + 16 * ((p >> 1) ^ ((c >> 3) & 1)) + 8 * (p & 1);
+}
+// The same within a 64-byte Q4_0 row line: block j's 8 bytes at 8 (p & 1).
+SYN_DEV int qs_slot4(int c, int j, int p) { return 16 * (j ^ ((c >> 2) & 3)) + 8 * (p & 1); }
+
+// Four Q4_0 code bytes -> the int8 values n - 8 of their low (sh 0) or high (sh 4) nibbles.
+SYN_DEV uint32_t q4_signed(uint32_t v, int sh) {
+    return (((v >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
 }
 
 // The lane's part of its wavefront's copies: per copy a global base (advanced per stage by
@@ -411,12 +437,12 @@ struct QsCopy {
     bool wide, on;
 };
 
-template <int TT, int TG>
+template <int FMT, int TT, int TG>
 __device__ __forceinline__ void qs_plan(QsCopy* cp, const uint8_t* W, const uint8_t* scales, const int8_t* xq,
                                         const float* xd, int n_out, int nb, int k, int T, int row0, int t0, int wave,
                                         int lane) {
-    using C = QsCfg<TT, TG>;
-    const uint32_t rb = (uint32_t)nb * 32u;
+    using C = QsCfg<FMT, TT, TG>;
+    const uint32_t rb = (uint32_t)nb * (uint32_t)C::CB;
     auto wrow = [&](int r) { return (uint32_t)(row0 + r < n_out ? row0 + r : n_out - 1); };
     auto tok = [&](int t) { return (uint32_t)(t0 + t < T ? t0 + t : T - 1); };
     // lane -> line 8 q + lane / 8 of the stage, LDS slot lane % 8, holding the line's bytes at
@@ -427,51 +453,84 @@ __device__ __forceinline__ void qs_plan(QsCopy* cp, const uint8_t* W, const uint
         return (uint32_t)(32 * j + 16 * h);
     };
     auto wcopy = [&](int q) {
-        const int r = 8 * q + li;
-        return QsCopy{W, wrow(r) * rb + src(r & 15), (uint32_t)(C::W_OFF + 1024 * q), 32u * QS_S, true, true};
+        if constexpr (FMT == T_Q8_0) {
+            const int r = 8 * q + li;
+            return QsCopy{W, wrow(r) * rb + src(r & 15), (uint32_t)(C::W_OFF + 1024 * q), (uint32_t)C::WL, true, true};
+        } else {  // lane -> row 16 q + lane / 4, slot lane % 4 holding block (lane % 4) ^ ((row >> 2) & 3)
+            const int r = 16 * q + (lane >> 2);
+            return QsCopy{W, wrow(r) * rb + 16u * (uint32_t)((lane & 3) ^ ((r >> 2) & 3)),
+                          (uint32_t)(C::W_OFF + 1024 * q), (uint32_t)C::WL, true, true};
+        }
     };
     auto acopy = [&](int q) {
         const int t = 8 * q + li;
         return QsCopy{reinterpret_cast<const uint8_t*>(xq), tok(t) * (uint32_t)k + src(t & 15),
                       (uint32_t)(C::A_OFF + 1024 * q), 32u * QS_S, true, true};
     };
-    // row scales of rows 16 h .. (32 lanes) or all 32 rows (h < 0): lane -> row lane / 2, blocks
-    // 2 (lane % 2), +1
-    auto scopy = [&](int h) {
-        const int r = (h < 0 ? 0 : 16 * h) + (lane >> 1);
+    // part h of `parts` of the row scales (32 rows x 8 bytes): lane -> row (32 / parts) h + lane / 2,
+    // blocks 2 (lane % 2), +1, from the lanes below 64 / parts
+    auto scopy = [&](int h, int parts) {
+        const int r = (32 / parts) * h + (lane >> 1);
         return QsCopy{scales, wrow(r) * (uint32_t)nb * 2u + 4u * (uint32_t)(lane & 1),
-                      (uint32_t)(C::SC_OFF + (h < 0 ? 0 : 128 * h)), 2u * QS_S, false, h < 0 || lane < 32};
+                      (uint32_t)(C::SC_OFF + (256 / parts) * h), 2u * QS_S, false, lane < 64 / parts};
     };
-    // token scales of tokens 32 h .. (h < 0: all TW <= 64): lane -> token
-    auto dcopy = [&](int h) {
-        const int t = (h < 0 ? 0 : 32 * h) + lane;
+    // part h of `parts` of the token scales (TW <= 64 tokens x 16 bytes): lane -> token
+    // (TW / parts) h + lane, from the lanes below TW / parts
+    auto dcopy = [&](int h, int parts) {
+        const int t = (C::TW / parts) * h + lane;
         return QsCopy{reinterpret_cast<const uint8_t*>(xd), tok(t) * (uint32_t)nb * 4u,
-                      (uint32_t)(C::DX_OFF + (h < 0 ? 0 : 512 * h)), 4u * QS_S, true,
-                      (h < 0 ? t < C::TW : lane < 32)};
+                      (uint32_t)(C::DX_OFF + 16 * (C::TW / parts) * h), 4u * QS_S, true, lane < C::TW / parts};
     };
-    if constexpr (TG == 1 && TT == 1) {  // 8 copies: 4 row lines, 2 token lines, the two scale sets
+    constexpr int S = C::SPARTS, D = C::DPARTS;
+    if constexpr (FMT == T_Q8_0 && TT == 1 && TG == 1) {  // 8 copies: 4 row, 2 token, two scale sets
         cp[0] = wcopy(2 * wave);
         cp[1] = wcopy(2 * wave + 1);
         cp[2] = acopy(wave);
-        cp[3] = wave == 0 ? scopy(-1) : dcopy(-1);
-    } else if constexpr (TG == 1) {  // 10 copies: 4 row lines, 4 token lines, the two scale sets
+        cp[3] = wave == 0 ? scopy(0, S) : dcopy(0, D);
+    } else if constexpr (FMT == T_Q8_0 && TG == 1) {  // 10 copies: 4 row, 4 token, two scale sets
         cp[0] = wcopy(2 * wave);
         cp[1] = wcopy(2 * wave + 1);
         cp[2] = acopy(2 * wave);
         cp[3] = acopy(2 * wave + 1);
-        cp[4] = wave == 0 ? scopy(-1) : dcopy(-1);
-    } else {  // 16 copies: 4 row lines, 8 token lines, two halves of each scale set
+        cp[4] = wave == 0 ? scopy(0, S) : dcopy(0, D);
+    } else if constexpr (FMT == T_Q8_0 && TT == 2) {  // 16 copies: 4 row, 8 token, halves of the scale sets
         cp[0] = wcopy(wave);
         cp[1] = acopy(2 * wave);
         cp[2] = acopy(2 * wave + 1);
-        cp[3] = wave < 2 ? scopy(wave) : dcopy(wave - 2);
+        cp[3] = wave < 2 ? scopy(wave, S) : dcopy(wave - 2, D);
+    } else if constexpr (FMT == T_Q8_0 && TG == 2) {  // 12 copies: 4 row, 4 token, halves of the scale sets
+        cp[0] = wcopy(wave);
+        cp[1] = acopy(wave);
+        cp[2] = wave < 2 ? scopy(wave, S) : dcopy(wave - 2, D);
+    } else if constexpr (FMT == T_Q8_0) {  // TG 4, 16 copies: 4 row, 8 token, halves of the scale sets
+        cp[0] = acopy(wave);
+        cp[1] = wave < 4 ? wcopy(wave) : wave < 6 ? scopy(wave - 4, S) : dcopy(wave - 6, D);
+    } else if constexpr (TT == 1 && TG == 1) {  // Q4_0, 6 copies: 2 row, 2 token, two scale sets
+        cp[0] = wcopy(wave);
+        cp[1] = acopy(wave);
+        cp[2] = wave == 0 ? scopy(0, S) : dcopy(0, D);
+    } else if constexpr (TG == 1) {  // Q4_0, 8 copies: 2 row, 4 token, two scale sets
+        cp[0] = wcopy(wave);
+        cp[1] = acopy(2 * wave);
+        cp[2] = acopy(2 * wave + 1);
+        cp[3] = wave == 0 ? scopy(0, S) : dcopy(0, D);
+    } else if constexpr (TT == 2) {  // Q4_0, 12 copies: 2 row, 8 token, two scale sets
+        cp[0] = acopy(2 * wave);
+        cp[1] = acopy(2 * wave + 1);
+        cp[2] = wave < 2 ? wcopy(wave) : wave == 2 ? scopy(0, S) : dcopy(0, D);
+    } else if constexpr (TG == 2) {  // Q4_0, 8 copies: 2 row, 4 token, two scale sets
+        cp[0] = acopy(wave);
+        cp[1] = wave < 2 ? wcopy(wave) : wave == 2 ? scopy(0, S) : dcopy(0, D);
+    } else {  // Q4_0, TG 4, 16 copies: 2 row, 8 token, scale halves, token-scale quarters
+        cp[0] = acopy(wave);
+        cp[1] = wave < 2 ? wcopy(wave) : wave < 4 ? scopy(wave - 2, S) : dcopy(wave - 4, D);
     }
 }
 
-template <int TT, int TG>
+template <int FMT, int TT, int TG>
 __device__ __forceinline__ void qs_issue(const QsCopy* cp, uint32_t stage_lds, int s) {
 #pragma unroll
-    for (int u = 0; u < QsCfg<TT, TG>::COPIES; ++u) {
+    for (int u = 0; u < QsCfg<FMT, TT, TG>::COPIES; ++u) {
         const uint8_t* base = cp[u].base + (size_t)cp[u].step * (size_t)s;
         if (cp[u].on) {
             if (cp[u].wide)
@@ -482,13 +541,13 @@ __device__ __forceinline__ void qs_issue(const QsCopy* cp, uint32_t stage_lds, i
     }
 }
 
-template <int TT, int TG>
+template <int FMT, int TT, int TG>
 __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* __restrict__ W, int n_out, int k,
                                                                  const int8_t* __restrict__ xq,
                                                                  const float* __restrict__ xd, int T,
                                                                  float* __restrict__ y,
                                                                  const uint32_t* __restrict__ active) {
-    using C = QsCfg<TT, TG>;
+    using C = QsCfg<FMT, TT, TG>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     T = active_rows(active, 0, T);
     const int row0 = (int)blockIdx.x * QS_RW, t0 = (int)blockIdx.y * C::TW;
@@ -498,12 +557,13 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
     const int c = lane & 15, p = lane >> 4;
     const int rg = wave & 1, tg = wave >> 1;  // the wavefront's row group and token group
     const int nb = k / 32, nst = nb / QS_S;
-    const uint8_t* scales = W + 32ull * (uint64_t)n_out * (uint64_t)nb;
+    const uint8_t* scales = W + (uint64_t)C::CB * (uint64_t)n_out * (uint64_t)nb;
     QsCopy cp[C::COPIES];
-    qs_plan<TT, TG>(cp, W, scales, xq, xd, n_out, nb, k, T, row0, t0, wave, lane);
+    qs_plan<FMT, TT, TG>(cp, W, scales, xq, xd, n_out, nb, k, T, row0, t0, wave, lane);
     const uint32_t ring = lds_addr(lds);
 #pragma unroll
-    for (int s = 0; s < C::NS - 1; ++s) qs_issue<TT, TG>(cp, ring + (uint32_t)(C::STAGE * s), s < nst ? s : nst - 1);
+    for (int s = 0; s < C::NS - 1; ++s)
+        qs_issue<FMT, TT, TG>(cp, ring + (uint32_t)(C::STAGE * s), s < nst ? s : nst - 1);
     float acc[TT][4];
 #pragma unroll
     for (int t = 0; t < TT; ++t)
@@ -514,7 +574,7 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
         wait_vm<C::COPIES * (C::NS - 2)>();  // this wavefront's copies of stage s have landed
         lds_barrier();                       // everyone's have, and stage s - 1 is read out
         const int sn = s + C::NS - 1;
-        qs_issue<TT, TG>(cp, ring + (uint32_t)(C::STAGE * (sn % C::NS)), sn < nst ? sn : nst - 1);
+        qs_issue<FMT, TT, TG>(cp, ring + (uint32_t)(C::STAGE * (sn % C::NS)), sn < nst ? sn : nst - 1);
         const uint8_t* st = lds + C::STAGE * (s % C::NS);
         // the lane's rows 4 p + i: four scales each, 8 bytes a row
         const v4u_s sc01 = *reinterpret_cast<const v4u_s*>(st + C::SC_OFF + (16 * rg + 4 * p) * 8);
@@ -533,7 +593,14 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
 #pragma unroll
         for (int j = 0; j < QS_S; ++j) {
             const int o = qs_slot(c, j, p);  // line c's (row or token, mod 16) bytes 8 p of block j
-            const long a = *reinterpret_cast<const long*>(st + C::W_OFF + (16 * rg + c) * 128 + o);
+            long a;
+            if constexpr (FMT == T_Q8_0) {
+                a = *reinterpret_cast<const long*>(st + C::W_OFF + (16 * rg + c) * C::WL + o);
+            } else {
+                const uint2 v = *reinterpret_cast<const uint2*>(st + C::W_OFF + (16 * rg + c) * C::WL + qs_slot4(c, j, p));
+                const int sh = 4 * (p >> 1);
+                a = (long)(((uint64_t)q4_signed(v.y, sh) << 32) | (uint64_t)q4_signed(v.x, sh));
+            }
 #pragma unroll
             for (int t = 0; t < TT; ++t) {
                 const long b = *reinterpret_cast<const long*>(st + C::A_OFF + (16 * TT * tg + 16 * t + c) * 128 + o);
@@ -564,33 +631,62 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
     }
 }
 
-// Whether the staged GEMM takes the shape: whole stages, 32-bit copy offsets.
-bool gemm_q8_staged_fits(int n_out, int k, int T) {
+// Whether the staged GEMM takes the shape (Q8_0 or Q4_0 rows): whole stages, 32-bit copy offsets.
+bool gemm_q8_staged_fits(int ty, int n_out, int k, int T) {
     const uint64_t nb = (uint64_t)k / 32;
-    return nb % QS_S == 0 && nb > 0 && (uint64_t)n_out * nb * 32 < (1ull << 32) && (uint64_t)T * (uint64_t)k < (1ull << 32);
+    return (ty == T_Q8_0 || ty == T_Q4_0) && nb % QS_S == 0 && nb > 0 &&
+           (uint64_t)n_out * nb * (uint64_t)split_code_bytes(ty) < (1ull << 32) &&
+           (uint64_t)T * (uint64_t)k < (1ull << 32);
 }
 
-template <int TT, int TG>
+template <int FMT, int TT, int TG>
 static void launch_q8_staged(const uint8_t* W, int n_out, int k, const int8_t* xq, const float* xd, int T, float* y,
                              hipStream_t stream, const uint32_t* active) {
-    using C = QsCfg<TT, TG>;
+    using C = QsCfg<FMT, TT, TG>;
     const dim3 grid((unsigned)((n_out + QS_RW - 1) / QS_RW), (unsigned)((T + C::TW - 1) / C::TW));
-    hipLaunchKernelGGL((k_gemm_q8_staged<TT, TG>), grid, dim3(64 * C::NW), (size_t)(C::STAGE * C::NS), stream, W, n_out,
-                       k, xq, xd, T, y, active);
+    hipLaunchKernelGGL((k_gemm_q8_staged<FMT, TT, TG>), grid, dim3(64 * C::NW), (size_t)(C::STAGE * C::NS), stream,
+                       W, n_out, k, xq, xd, T, y, active);
 }
 
-void launch_gemm_q8_split(const uint8_t* W, int n_out, int k, const uint8_t* ws, int T, float* y,
+// Token tiles: up to 16 tokens one 16-token group; up to 32 two (one wavefront pair of 32 tokens,
+// or two pairs of 16); beyond, 64-token workgroups (two pairs of 32 tokens, or four of 16).  A
+// wavefront with one 16-token tile does half the work of one with two, so where the launch would
+// give a SIMD fewer than QS_TT1_WAVES / 1024 wavefronts of two tiles it takes one-tile wavefronts,
+// twice as many.
+constexpr uint64_t QS_TT1_WAVES = 2048;
+
+template <int FMT>
+static void launch_staged_fmt(const uint8_t* W, int n_out, int k, const int8_t* xq, const float* xd, int T, float* y,
+                              hipStream_t stream, const uint32_t* active) {
+    const uint64_t row_wgs = (uint64_t)(n_out + QS_RW - 1) / QS_RW;
+    if (T <= 16) {
+        launch_q8_staged<FMT, 1, 1>(W, n_out, k, xq, xd, T, y, stream, active);
+    } else if (T <= 32) {
+        if (row_wgs * 2 < QS_TT1_WAVES)
+            launch_q8_staged<FMT, 1, 2>(W, n_out, k, xq, xd, T, y, stream, active);
+        else
+            launch_q8_staged<FMT, 2, 1>(W, n_out, k, xq, xd, T, y, stream, active);
+    } else {
+        if (row_wgs * (uint64_t)((T + 63) / 64) * 4 < QS_TT1_WAVES)
+            launch_q8_staged<FMT, 1, 4>(W, n_out, k, xq, xd, T, y, stream, active);
+        else
+            launch_q8_staged<FMT, 2, 2>(W, n_out, k, xq, xd, T, y, stream, active);
+    }
+}
+
+// Q8_0 rows of any shape (the staged GEMM where it fits, else the register-staged one); Q4_0 rows
+// where the staged GEMM fits (gemm_q8_staged_fits).
+void launch_gemm_q8_split(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws, int T, float* y,
                           hipStream_t stream, const uint32_t* active) {
     const ActLayout L = act_layout(ACT_Q8_0, (uint64_t)T, (uint64_t)k);
     const int8_t* xq = reinterpret_cast<const int8_t*>(ws + L.codes);
     const float* xd = reinterpret_cast<const float*>(ws + L.d);
-    if (gemm_q8_staged_fits(n_out, k, T)) {
-        if (T <= 16)
-            launch_q8_staged<1, 1>(W, n_out, k, xq, xd, T, y, stream, active);
-        else if (T <= 32)
-            launch_q8_staged<2, 1>(W, n_out, k, xq, xd, T, y, stream, active);
-        else
-            launch_q8_staged<2, 2>(W, n_out, k, xq, xd, T, y, stream, active);
+    if (ty == T_Q4_0) {
+        launch_staged_fmt<T_Q4_0>(W, n_out, k, xq, xd, T, y, stream, active);
+        return;
+    }
+    if (gemm_q8_staged_fits(T_Q8_0, n_out, k, T)) {
+        launch_staged_fmt<T_Q8_0>(W, n_out, k, xq, xd, T, y, stream, active);
         return;
     }
     // other shapes: the register-staged kernel; up to 64 tokens: 16-token tiles; beyond, 32-token tiles (a token tile per wavefront, up to

@@ -53,9 +53,9 @@ void launch_moe_q8(int mode, const uint8_t* w0, const uint8_t* w1, uint64_t mat_
 void launch_split_repack(int ty, const uint8_t* src, uint8_t* dst, uint64_t bytes, int inverse, hipStream_t stream);
 void launch_gemv_split(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws, int rows, float* y,
                        hipStream_t stream, const uint32_t* active = nullptr);
-void launch_gemm_q8_split(const uint8_t* W, int n_out, int k, const uint8_t* ws, int T, float* y,
+void launch_gemm_q8_split(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws, int T, float* y,
                           hipStream_t stream, const uint32_t* active = nullptr);
-bool gemm_q8_staged_fits(int n_out, int k, int T);
+bool gemm_q8_staged_fits(int ty, int n_out, int k, int T);
 // probe.hip: a read-only HBM stream with the decode GEMV's load pattern (counter calibration)
 void launch_hbm_read_probe(const uint8_t* src, uint64_t bytes, uint32_t* sink, hipStream_t stream);
 // norm.hip: RmsNorm rows of at most NORM_MAX_COLS values

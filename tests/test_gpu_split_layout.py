@@ -69,8 +69,8 @@ def check(S, ty, n_out, k, rows, seed, w=None):
 @pytest.mark.parametrize("n_out,k", [(37, 32), (300, 1024), (41, 3072), (9, 14336), (130, 16384 + 32)])
 def test_split_decode_rows_equal_oracle(S, ty, n_out, k):
     """1 to 8 rows (staged activations for narrow rows, global reads for wide ones), 9 and 20 rows
-    (eight-row groups for Q4_0, the GEMM for Q8_0); row lengths of 1 to 513 blocks, partial
-    last load groups and row counts not multiples of eight."""
+    (eight-row groups, or the GEMM where it is the faster); row lengths of 1 to 513 blocks,
+    partial last load groups and row counts not multiples of eight."""
     w = None
     for rows in (1, 2, 3, 5, 8, 9, 20):
         w = check(S, ty, n_out, k, rows, 1000 * rows + n_out + k + ty, w)
@@ -78,7 +78,7 @@ def test_split_decode_rows_equal_oracle(S, ty, n_out, k):
 
 @pytest.mark.parametrize("ty,n_out,k,rowss", [
     (o.Q8_0, 14336, 4096, [1, 8, 32, 128]),  # Q8_0 decode and prefill of the 14336 x 4096 matrix
-    (o.Q4_0, 4096, 4096, [1, 4]),            # the Q4_0 4096 x 4096 decode
+    (o.Q4_0, 4096, 4096, [1, 4, 32, 128]),   # the Q4_0 4096 x 4096 decode and a few rows
 ])
 def test_split_config_shapes_equal_oracle(S, ty, n_out, k, rowss):
     x = o.normal(0x5E11 + k, 0.02, n_out * k)
@@ -94,11 +94,49 @@ def test_split_gemm_edges_equal_oracle(S):
         check(S, o.Q8_0, n_out, k, rows, n_out * 31 + rows)
 
 
-def test_split_gemm_staged_shapes_equal_oracle(S):
+@pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0])
+def test_split_gemm_staged_shapes_equal_oracle(S, ty):
     """The LDS-staged GEMM (rows of whole 4-block stages): every token-tile variant (16, 32 and
-    64 tokens a workgroup), partial workgroups of rows and tokens, one stage and many."""
+    64 tokens a workgroup; one or two 16-token tiles a wavefront: small launches take one),
+    partial workgroups of rows and tokens, one stage and many; for Q4_0 (64-byte row lines,
+    nibbles widened in registers) and Q8_0."""
     w = None
     for rows in (9, 16, 17, 31, 32, 33, 64, 65, 127):
-        w = check(S, o.Q8_0, 50, 512, rows, 7000 + rows, w)
-    for n_out, k, rows in ((33, 128, 40), (96, 4096, 48), (1, 128, 70)):
-        check(S, o.Q8_0, n_out, k, rows, n_out + k + rows)
+        w = check(S, ty, 50, 512, rows, 7000 + rows + ty, w)
+    # the last three launch enough wavefronts for two-tile wavefronts (32 and 64 tokens)
+    for n_out, k, rows in ((33, 128, 40), (96, 4096, 48), (1, 128, 70), (4097, 256, 5), (32800, 128, 20),
+                           (32770, 128, 31), (4096, 256, 300)):
+        check(S, ty, n_out, k, rows, n_out + k + rows + ty)
+
+
+@pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0])
+def test_split_gemm_few_rows_equal_oracle(S, ty):
+    """2 to 16 rows over 14336-row matrices, where the staged GEMM (one 16-token tile) is the
+    faster from 2 (Q8_0) or 5 (Q4_0) rows: full tiles, a partial last row tile and a partial
+    last row group."""
+    x = o.normal(0xF3 + ty, 0.02, 14336 * 4096)
+    w = o.quantize(ty, x)
+    for rows in (2, 5, 8, 13, 16):
+        check(S, ty, 14336, 4096, rows, 0xF30 + rows + ty, w)
+    cb = 34 if ty == o.Q8_0 else 18
+    check(S, ty, 14329, 4096, 7, 0xF31 + ty, w[:14329 * 128 * cb])
+
+
+def test_split_q4_0_extreme_codes_equal_oracle(S):
+    """Q4_0 codes 0 and 15 (n - 8 = -8 and 7) against activation codes of +-127 in every block:
+    the widened nibbles at both ends, whose exact block sums are as large as Q4_0 makes them."""
+    n_out, k = 64, 1024
+    nb = k // 32
+    rng = np.random.default_rng(0x40E)
+    w = np.zeros((n_out * nb, 18), np.uint8)
+    w[:, 0:2] = np.frombuffer(np.float16(0.0123).tobytes(), np.uint8)
+    w[:, 2:] = rng.choice(np.array([0x00, 0xFF, 0x0F, 0xF0], np.uint8), size=(n_out * nb, 16))
+    w = w.reshape(-1)
+    for rows in (2, 20, 70):
+        x = np.where(rng.random(rows * k) < 0.5, -1.0, 1.0).astype(np.float32)
+        W = S.repack(S.Weights(S.WeightType(o.Q4_0), dev(w), n_out, k))
+        announce(f"split gemv Q4_0 extreme codes {n_out}x{k} rows={rows}")
+        y = torch.full((rows, n_out), float("nan"), device="cuda")
+        S.gemv(W, dev(x), rows, y=y)
+        want = o.gemv(o.Q4_0, w, n_out, k, x, rows, threads=8)
+        assert_same(host(y), want, f"Q4_0 extreme codes rows {rows}")
