@@ -18,7 +18,9 @@ events on its stream, and the CPU oracle timed on this host's cores; beside it:
   * cfg1 (Q4_0 4096x4096 at one row), cfg2 (Q8_0 14336x4096 at 1, 8, 32 and 128 rows) and
     rows_2_8 (Q4_K at 2, 4 and 8 rows against one row);
   * moe (the MoE layer at 64 decode tokens) and prefill (the 2048-token dense GEMMs on the matrix
-    cores and the skewed MoE layer).
+    cores and the skewed MoE layer);
+  * read_floor: a bare read of each decode op's byte count (syn_hbm_read_probe, the decode GEMV's
+    load pattern with no arithmetic), timed like the ops: what one launch of that size costs.
 --only runs one part (for the profiler); `copy` and `calib` run the counter calibration kernels.
 """
 from __future__ import annotations
@@ -45,7 +47,7 @@ Q4K, Q8_0, Q4_0 = 12, 8, 2
 SPLIT = 2  # the weight layout of Q8_0 / Q4_0 matrices after repack (codes, then scales)
 COPIES = 5
 MALL_BYTES = 256 << 20
-PARTS = ["layer", "provider", "cfgs", "rows", "moe", "prefill"]
+PARTS = ["layer", "provider", "cfgs", "rows", "floor", "moe", "prefill"]
 
 
 def q4k_bytes(n_out, k):
@@ -627,6 +629,38 @@ def bench_prefill(torch, S, M, steps, warmup, cpu_seconds):
 
 
 # ---- counter calibration kernels --------------------------------------------------------------------
+def bench_read_floor(torch, nrep):
+    """A bare read (syn_hbm_read_probe) of each decode op's weight bytes, launched back to back
+    over copies that together exceed the Infinity Cache: the time one launch of that many bytes
+    takes with no arithmetic, against which a lone op's time is measured."""
+    f = S_lib().syn_hbm_read_probe_sink_words
+    f.argtypes, f.restype = [C.c_uint64], C.c_uint64
+    sizes = {"O 4096x4096 Q4_K / Cfg1 Q4_0 4096x4096": 4096 * row_bytes(Q4K, 4096),
+             "QKV 6144x4096 Q4_K": 6144 * row_bytes(Q4K, 4096),
+             "gate, up or down Q4_K": 14336 * row_bytes(Q4K, 4096),
+             "Cfg2 Q8_0 14336x4096": 14336 * row_bytes(Q8_0, 4096),
+             "decode layer Q4_K (5 GEMVs)": 122683392,
+             "512 MiB": 512 << 20}
+    out = {}
+    stream = torch.cuda.current_stream().cuda_stream
+    for name, nbytes in sizes.items():
+        nbytes = nbytes // 16 * 16
+        ncopies = max(3, -(-2 * MALL_BYTES // nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(c) for c in range(ncopies)]
+        sink = torch.empty(f(nbytes), dtype=torch.int32, device="cuda")
+
+        def go(i):
+            rc = S_lib().syn_hbm_read_probe(bufs[i % ncopies].data_ptr(), nbytes, sink.data_ptr(), stream)
+            assert rc == 0
+        go(0)
+        us = gpu_us(torch, go, nrep)
+        out[name] = {"bytes": nbytes, "us": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del bufs, sink
+    torch.cuda.empty_cache()
+    return out
+
+
 def calibrate(torch, only):
     """`copy`: a plain 512 MiB device copy (reads and writes 512 MiB each); `calib`: 512 MiB read
     once by syn_hbm_read_probe with the decode GEMV's load pattern.  Five launches each."""
@@ -693,6 +727,8 @@ def main():
         out.update(bench_cfgs(torch, S, a))
     if "rows" in want:
         out["rows_2_8"] = bench_rows(torch, S, a)
+    if "floor" in want:
+        out["read_floor"] = bench_read_floor(torch, max(20, min(a.steps, 100)))
     if "moe" in want:
         torch.cuda.empty_cache()
         out["moe"] = bench_moe(torch, S, M, max(10, a.steps // 4), max(3, a.warmup // 4),

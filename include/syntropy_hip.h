@@ -142,9 +142,10 @@ int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, uint64_t w_by
 
 /* ---- Measurement (not on the op path) ----------------------------------------------------------
  * syn_hbm_read_probe: reads `bytes` (a multiple of 16, src 16-byte aligned) once with the decode
- * GEMV's load pattern (16-byte non-temporal loads, nine per lane) and writes one word per
- * workgroup to sink (syn_hbm_read_probe_sink_words(bytes) words): a kernel of known HBM traffic
- * against which the HBM byte counters are calibrated.  No counterpart in the reference. */
+ * GEMV's load pattern (16-byte non-temporal loads, nine per lane from 256 MiB, one below) and
+ * writes one word per workgroup to sink (syn_hbm_read_probe_sink_words(bytes) words): a kernel
+ * of known HBM traffic against which the HBM byte counters are calibrated, and a bare read to
+ * set a lone op of the same bytes against.  No counterpart in the reference. */
 uint64_t syn_hbm_read_probe_sink_words(uint64_t bytes);
 int syn_hbm_read_probe(const void* src, uint64_t bytes, uint32_t* sink, void* stream);
 

@@ -807,7 +807,7 @@ SYN_EXPORT int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, ui
 
 // ---- measurement ----------------------------------------------------------------------------
 
-SYN_EXPORT uint64_t syn_hbm_read_probe_sink_words(uint64_t bytes) { return (bytes / 16 + 256 * 9 - 1) / (256 * 9); }
+SYN_EXPORT uint64_t syn_hbm_read_probe_sink_words(uint64_t bytes) { return syn::hbm_read_probe_workgroups(bytes); }
 
 SYN_EXPORT int syn_hbm_read_probe(const void* src, uint64_t bytes, uint32_t* sink, void* stream) {
     const char* W = "syn_hbm_read_probe";
