@@ -115,16 +115,17 @@ __global__ __launch_bounds__(64 * SPLIT_WAVES) void k_gemv_split(const uint8_t* 
     const int pieces = FMT == T_Q8_0 ? 2 * nb : nb;  // 16-byte pieces of the row
     float acc = 0.0f;                                // lane r < rows: activation row r's sum
     for (int g0 = 0; g0 < pieces; g0 += 64 * SPLIT_UNROLL) {
-        // SPLIT_UNROLL load instructions in flight before the arithmetic
+        // SPLIT_UNROLL load instructions (and their scales) in flight before the arithmetic: the
+        // loads are unconditional (pieces past the row re-read its last piece, unused) and the
+        // scales stay raw bits until used, so no wait splits the group
         v4u_s wv[SPLIT_UNROLL];
-        float dwv[SPLIT_UNROLL];
+        uint16_t swv[SPLIT_UNROLL];
 #pragma unroll
         for (int u = 0; u < SPLIT_UNROLL; ++u) {
-            const int h = g0 + 64 * u + lane;
-            const bool ok = h < pieces;
-            wv[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const v4u_s*>(codes + 16 * (uint64_t)h))
-                       : v4u_s{0u, 0u, 0u, 0u};
-            dwv[u] = ok ? f16_to_f32(scales[FMT == T_Q8_0 ? h >> 1 : h]) : 0.0f;
+            const int h0 = g0 + 64 * u + lane;
+            const int h = h0 < pieces ? h0 : pieces - 1;
+            wv[u] = __builtin_nontemporal_load(reinterpret_cast<const v4u_s*>(codes + 16 * (uint64_t)h));
+            swv[u] = scales[FMT == T_Q8_0 ? h >> 1 : h];
         }
 #pragma unroll
         for (int u = 0; u < SPLIT_UNROLL; ++u) {
@@ -132,10 +133,10 @@ __global__ __launch_bounds__(64 * SPLIT_WAVES) void k_gemv_split(const uint8_t* 
             if (i0 >= pieces) break;  // uniform
             const int h = i0 + lane;
             const bool ok = h < pieces;
-            const v4u_s w = wv[u];
+            const v4u_s w = ok ? wv[u] : v4u_s{0u, 0u, 0u, 0u};
             const int b = FMT == T_Q8_0 ? h >> 1 : h;  // the block
             const int b0 = FMT == T_Q8_0 ? i0 >> 1 : i0;
-            const float dw = dwv[u];
+            const float dw = ok ? f16_to_f32(swv[u]) : 0.0f;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 if (r >= rows) break;  // uniform
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(64 * SPLIT_WAVES) void k_gemv_split(const uint8_t* 
                     const v4u_s x =
                         ok ? *reinterpret_cast<const v4u_s*>(aq + (size_t)r * k + 16 * h) : v4u_s{0u, 0u, 0u, 0u};
                     s = sdot4(w.x, x.x, sdot4(w.y, x.y, sdot4(w.z, x.z, sdot4(w.w, x.w, 0))));
-                    s += __shfl_xor(s, 1);  // the block's other half (exact)
+                    s += __builtin_amdgcn_mov_dpp(s, 0xB1, 0xF, 0xF, false);  // the block's other half (lane ^ 1; exact)
                 } else {
                     const v4u_s z4 = {0u, 0u, 0u, 0u};
                     const v4u_s x0 = ok ? *reinterpret_cast<const v4u_s*>(aq + (size_t)r * k + 32 * h) : z4;
@@ -171,6 +172,11 @@ __global__ __launch_bounds__(64 * SPLIT_WAVES) void k_gemv_split(const uint8_t* 
 }
 
 static int split_r(int rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8; }
+
+// Whether one launch of `rows` <= 8 rows stages its activation rows in LDS.
+bool gemv_split_staged(int ty, int rows, int k) {
+    return split_act_lds(ty, split_r(rows), k) <= (size_t)SPLIT_STAGE_MAX;
+}
 
 template <int FMT>
 static void launch_split_fmt(const uint8_t* W, int n_out, int k, const uint8_t* ws, int rows, float* y,

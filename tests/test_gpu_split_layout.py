@@ -111,9 +111,9 @@ def test_split_gemm_staged_shapes_equal_oracle(S, ty):
 
 @pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0])
 def test_split_gemm_few_rows_equal_oracle(S, ty):
-    """2 to 16 rows over 14336-row matrices, where the staged GEMM (one 16-token tile) is the
-    faster from 2 (Q8_0) or 5 (Q4_0) rows: full tiles, a partial last row tile and a partial
-    last row group."""
+    """2 to 16 rows over 14336-row matrices, where the staged GEMM (one 16-token tile) takes over
+    from the split decode kernel at a few rows (4 for Q8_0, 7 for Q4_0): full tiles, a partial
+    last row tile and a partial last row group."""
     x = o.normal(0xF3 + ty, 0.02, 14336 * 4096)
     w = o.quantize(ty, x)
     for rows in (2, 5, 8, 13, 16):
