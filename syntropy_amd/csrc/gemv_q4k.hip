@@ -332,10 +332,12 @@ void k_gemv_q4k_batch(DecBatch bt) {
     static_assert(!FUSE || LAYOUT == LAYOUT_X8, "the fused form reads X8 weights");
     float xv[FUSE ? FUSE_PIECES : 1][16];
     if constexpr (FUSE) {
+        // unconditional loads (pieces past the row re-read its last piece, unused): a load in a
+        // branch would make the compiler wait for it before the block's loads below
 #pragma unroll
         for (int i = 0; i < FUSE_PIECES; ++i) {
             const int c = (int)threadIdx.x + i * 64 * WAVES;
-            if (c < nb * 16) load_block16(bt.x[p], c, xv[i]);
+            load_block16(bt.x[p], c < nb * 16 ? c : nb * 16 - 1, xv[i]);
         }
     } else if constexpr (LAYOUT == LAYOUT_X8) {
         // the activation row streams into LDS first, with no registers held (codes column by
