@@ -84,9 +84,10 @@ int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uin
  * syn_gemv_layout(_workspace_bytes): the Gemv op over a matrix in `layout` (0 is syn_gemv); for
  *   layout 1 one row runs the decode kernel with the row quantized in every workgroup (k_in <=
  *   16384), 2 to 31 rows the decode expert kernel on rows quantized beforehand (int8 matrix
- *   cores, the matrix as one expert), more rows the matrix-core GEMM (k_in a multiple of 2048).  Layout 2 quantizes the rows to Q8_0 blocks and
- *   runs the split decode kernel eight rows at a time, or, for Q8_0, the int8 matrix-core GEMM
- *   from 2 rows (k_in a multiple of 128) or from 9 rows (other k_in).
+ *   cores, the matrix as one expert), more rows the matrix-core GEMM (k_in a multiple of 2048).
+ *   Layout 2 quantizes the rows to Q8_0 blocks and runs the split decode kernel eight rows at a
+ *   time, or the int8 matrix-core GEMM: for k_in a multiple of 128 where it is the faster (from
+ *   2 to 9 rows by shape, always beyond 16), and for Q8_0 of other k_in from 9 rows.
  * syn_gemv_batch_layout / syn_gemv_batch_quantized_layout: the grouped decode of every problem
  *   in `layout`. */
 int syn_q4k_repack(uint32_t layout, const void* src, void* dst, uint64_t bytes, int32_t inverse, void* stream);
