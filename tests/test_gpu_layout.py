@@ -101,6 +101,67 @@ def test_batch_layer_full_shapes_equal_oracle(S):
                 assert_same(host(y), want[i], f"{name} problem {i} rep {rep}")
 
 
+def _batch_case(S, shapes, seed):
+    rs = np.random.default_rng(seed)
+    ws, xs, ys, raw = [], [], [], []
+    for n, k in shapes:
+        w = random_q4k(rs, n, k)
+        raw.append(w)
+        ws.append(S.repack(S.Weights(S.WeightType.Q4K, dev(w), n, k)))
+        xs.append(torch.empty(k, device="cuda"))
+        ys.append(torch.full((n,), float("nan"), device="cuda"))
+    return ws, xs, ys, raw
+
+
+def _set_rows(shapes, xs, seed):
+    vals = []
+    for i, (n, k) in enumerate(shapes):
+        x = o.normal(seed + i, 1.0, k)
+        xs[i].copy_(dev(x))
+        vals.append(x)
+    torch.cuda.synchronize()
+    return vals
+
+
+def test_batch_x8_new_rows_each_call(S):
+    """One workspace, six calls with new rows each: every call equals the oracle (nothing of an
+    earlier call's quantized rows stands in for the next call's)."""
+    shapes = [(512, 4096), (300, 14336), (64, 2048)]
+    ws, xs, ys, raw = _batch_case(S, shapes, 0x5180)
+    batch = S.GemvBatch(ws, xs, ys)
+    for call_no in range(6):
+        x = _set_rows(shapes, xs, 0x5190 + 10 * call_no)
+        announce(f"batch call {call_no}")
+        batch()
+        for i, (n, k) in enumerate(shapes):
+            assert_same(host(ys[i]), o.gemv(o.Q4_K, raw[i], n, k, x[i], 1, threads=16), f"call {call_no} problem {i}")
+
+
+def test_batch_x8_captured_replays_equal_oracle(S):
+    """The grouped decode captured into a graph: replays with new rows, eager work and
+    synchronizations between them, each equal the oracle."""
+    shapes = [(640, 4096), (96, 14336)]
+    ws, xs, ys, raw = _batch_case(S, shapes, 0x51A0)
+    batch = S.GemvBatch(ws, xs, ys)
+    _set_rows(shapes, xs, 0x51B0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        batch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        batch()
+    for rep in range(3):
+        x = _set_rows(shapes, xs, 0x51C0 + 10 * rep)
+        announce(f"batch captured replay {rep}")
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (n, k) in enumerate(shapes):
+            assert_same(host(ys[i]), o.gemv(o.Q4_K, raw[i], n, k, x[i], 1, threads=16), f"replay {rep} problem {i}")
+
+
 @pytest.mark.parametrize("rows,n_out,k", [(32, 64, 2048), (64, 300, 4096), (100, 256, 14336)])
 def test_gemm_x8_equals_oracle(S, rows, n_out, k):
     rs = np.random.default_rng(rows + n_out + k)
