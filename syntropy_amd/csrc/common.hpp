@@ -131,6 +131,56 @@ SYN_DEV float rot1(float v) {
     return __builtin_bit_cast(float, i);
 }
 
+// Reductions across lanes without LDS, for operations that are commutative and associative
+// (max, sum, or): the quad steps pair lanes i ^ 1 and i ^ 2; then row_half_mirror pairs lane i
+// of a group of eight with lane 7 - i (the other quad), row_mirror lane i of a row of 16 with
+// lane 15 - i (the other half), and the permlane swaps rows 0-1 / 2-3, then the two halves of
+// the wavefront.  Every lane of the group ends holding the group's result; every lane of the
+// group must be active.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+template <int CTRL>
+SYN_DEV uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+SYN_DEV uint64_t dpp_u64(uint64_t v) {
+    return ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
+}
+SYN_DEV uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+// the maximum over groups of G = 8, 16 or 64 lanes
+template <int G>
+SYN_DEV uint64_t group_max_u64(uint64_t k) {
+    k = umax64(k, dpp_u64<DPP_XOR1>(k));
+    k = umax64(k, dpp_u64<DPP_XOR2>(k));
+    k = umax64(k, dpp_u64<DPP_HALF_MIRROR>(k));
+    if constexpr (G >= 16) k = umax64(k, dpp_u64<DPP_MIRROR>(k));
+    if constexpr (G == 64) {
+        const auto l1 = __builtin_amdgcn_permlane16_swap((uint32_t)k, (uint32_t)k, false, false);
+        const auto h1 = __builtin_amdgcn_permlane16_swap((uint32_t)(k >> 32), (uint32_t)(k >> 32), false, false);
+        k = umax64(((uint64_t)h1[0] << 32) | l1[0], ((uint64_t)h1[1] << 32) | l1[1]);
+        const auto l2 = __builtin_amdgcn_permlane32_swap((uint32_t)k, (uint32_t)k, false, false);
+        const auto h2 = __builtin_amdgcn_permlane32_swap((uint32_t)(k >> 32), (uint32_t)(k >> 32), false, false);
+        k = umax64(((uint64_t)h2[0] << 32) | l2[0], ((uint64_t)h2[1] << 32) | l2[1]);
+    }
+    return k;
+}
+// the sum (or the or: OR = true) over groups of 8 lanes
+template <bool OR = false>
+SYN_DEV int group8_sum(int s) {
+    auto op = [](int a, int b) { return OR ? (a | b) : a + b; };
+    s = op(s, (int)dpp_u32<DPP_XOR1>((uint32_t)s));
+    s = op(s, (int)dpp_u32<DPP_XOR2>((uint32_t)s));
+    return op(s, (int)dpp_u32<DPP_HALF_MIRROR>((uint32_t)s));
+}
+// The key that orders candidates of a signed-maximum search: magnitude bits, then the first
+// index on equal magnitudes, then the sign (one candidate per index).  Non-negative F32 bit
+// patterns order as their values.
+SYN_DEV uint64_t amax_key(float v, int idx) {
+    return ((uint64_t)(f2u(v) & 0x7FFFFFFFu) << 32) | ((uint64_t)(0xFFFF - idx) << 1) | (f2u(v) >> 31);
+}
+SYN_DEV float key_amax(uint64_t k) { return u2f((uint32_t)(k >> 32)); }
+SYN_DEV float key_value(uint64_t k) { return (k & 1) ? -key_amax(k) : key_amax(k); }
+
 // Q8_K of one 256-value block (crates/kernels-cpu/src/gemv/act.rs:351-373): largest
 // magnitude, first index on ties, ggml's nearest_int; non-finite block -> scale NaN, codes 0.
 // One wavefront; lane l holds values 4l..4l+3 and gets their four codes (packed bytes), the
@@ -145,29 +195,13 @@ SYN_DEV Q8KLane q8k_block_lane(const float* __restrict__ xb, int lane) {
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
     const bool fin = finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]);
     const bool all_finite = __all(fin);
-    // Largest magnitude, the first index on a tie: (amax desc, index asc).
-    float amax = 0.0f, mx = 0.0f;
-    int idx = 0x7FFFFFFF;
+    // Largest magnitude, the first index on a tie (amax desc, index asc), as the largest key
+    // (an all-zero block gives amax 0; a non-finite one is decided by all_finite)
+    uint64_t key = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = __builtin_fabsf(v[i]);
-        if (a > amax) {
-            amax = a;
-            mx = v[i];
-            idx = lane * 4 + i;
-        }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float oa = __shfl_xor(amax, off);
-        const float om = __shfl_xor(mx, off);
-        const int oi = __shfl_xor(idx, off);
-        if (oa > amax || (oa == amax && oi < idx)) {
-            amax = oa;
-            mx = om;
-            idx = oi;
-        }
-    }
+    for (int i = 0; i < 4; ++i) key = umax64(key, amax_key(v[i], lane * 4 + i));
+    key = group_max_u64<64>(key);
+    const float amax = key_amax(key), mx = key_value(key);
     float d = 0.0f;
     int q[4] = {0, 0, 0, 0};
     if (!all_finite) {
@@ -186,11 +220,7 @@ SYN_DEV Q8KLane q8k_block_lane(const float* __restrict__ xb, int lane) {
     Q8KLane r;
     r.packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
                ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
-    r.sum32 = s;
+    r.sum32 = group8_sum(q[0] + q[1] + q[2] + q[3]);
     r.d = d;
     return r;
 }
@@ -207,19 +237,17 @@ struct Q8_0Lane {
 };
 SYN_DEV Q8_0Lane q8_0_block_lane(float4 v4) {
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    int bad = !(finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]));
-    float amax = 0.0f;
+    const int bad = group8_sum<true>(!(finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3])));
+    // the largest magnitude by its bits (non-negative F32 patterns order as their values; a
+    // block holding a NaN or an infinity is `bad` and its amax unused)
+    uint32_t ab = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float a = __builtin_fabsf(v[i]);
-        amax = amax > a ? amax : a;
+        const uint32_t a = f2u(v[i]) & 0x7FFFFFFFu;
+        ab = ab > a ? ab : a;
     }
-#pragma unroll
-    for (int off = 4; off >= 1; off >>= 1) {
-        const float o = __shfl_xor(amax, off);
-        amax = amax > o ? amax : o;
-        bad |= __shfl_xor(bad, off);
-    }
+    ab = (uint32_t)(group_max_u64<8>(ab) & 0xFFFFFFFFu);
+    const float amax = u2f(ab);
     int q[4] = {0, 0, 0, 0};
     Q8_0Lane r;
     if (bad) {
@@ -235,11 +263,7 @@ SYN_DEV Q8_0Lane q8_0_block_lane(float4 v4) {
     }
     r.packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
                ((uint32_t)(q[3] & 0xFF) << 24);
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
-    r.sum = s;
+    r.sum = group8_sum(q[0] + q[1] + q[2] + q[3]);
     return r;
 }
 

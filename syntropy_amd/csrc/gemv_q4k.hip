@@ -60,31 +60,16 @@ SYN_DEV void load_block16(const float* __restrict__ x, int c, float (&v)[16]) {
 SYN_DEV void quant16_to_lds(const float (&v)[16], int c, int nb, uint8_t* lds) {
     const int sb = c >> 4, part = c & 15;
     bool fin = true;
-    float amax = 0.0f, mx = 0.0f;
-    int idx = 0x7FFFFFFF;
+    uint64_t key = 0;  // largest magnitude, the first index on a tie (amax_key)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         fin = fin && finite_f(v[i]);
-        const float av = __builtin_fabsf(v[i]);
-        if (av > amax) {
-            amax = av;
-            mx = v[i];
-            idx = part * 16 + i;
-        }
+        key = umax64(key, amax_key(v[i], part * 16 + i));
     }
-    int bad = !fin;
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) {
-        const float oa = __shfl_xor(amax, off);
-        const float om = __shfl_xor(mx, off);
-        const int oi = __shfl_xor(idx, off);
-        bad |= __shfl_xor(bad, off);
-        if (oa > amax || (oa == amax && oi < idx)) {
-            amax = oa;
-            mx = om;
-            idx = oi;
-        }
-    }
+    key = group_max_u64<16>(key);
+    // any non-finite value in the 16 lanes
+    const int bad = (int)(group_max_u64<16>(fin ? 0u : 1u) & 1u);
+    const float amax = key_amax(key), mx = key_value(key);
     float d = 0.0f;
     int q[16];
 #pragma unroll
@@ -112,7 +97,7 @@ SYN_DEV void quant16_to_lds(const float (&v)[16], int c, int nb, uint8_t* lds) {
     }
     v4u pk = {w[0], w[1], w[2], w[3]};
     *reinterpret_cast<v4u*>(lds + sb * COL + part * 16) = pk;
-    s += __shfl_xor(s, 1);  // the two 16-value halves of a 32-value group
+    s += (int)dpp_u32<DPP_XOR1>((uint32_t)s);  // the two 16-value halves of a 32-value group
     if ((part & 1) == 0) reinterpret_cast<int*>(lds + xs_off(nb) + sb * SUMW)[part >> 1] = s;
     if (part == 0) reinterpret_cast<float*>(lds + xd_off(nb))[sb] = d;
 }
