@@ -529,10 +529,9 @@ namespace {
 // rows of 4096 to 14336 values).  Split decode kernel, per launch of r <= 8 rows over M million
 // weights: a + read M + per M r (Q4_0: 2.4, 0.089, 0.038; Q8_0: 3.2, 0.141, 0.034, or 0.070
 // per row and million weights when the activation rows do not fit in LDS and are read from
-// global memory).  Staged GEMM: a + per 4-block stage 0.49 (Q4_0; a 2.4) or 0.40 (Q8_0; a 2.6),
-// 20% more per further workgroup a CU holds.  Each wavefront runs its row group's stages one
-// after another, so the GEMM's time follows the row length, while the decode kernel's grows with
-// the rows; beyond 16 rows the GEMM is always the faster.  Both produce the same bits.
+// global memory).  The GEMM's estimate is gemm_q8_cost_us (gemv_split.hip): flat in the rows up
+// to 16 and following the row length, while the decode kernel's grows with the rows; beyond 16
+// rows the GEMM is always the faster.  All produce the same bits.
 bool staged_faster(int32_t wtype, uint32_t n_out, uint32_t k_in, uint32_t rows) {
     if (rows > 16) return true;
     const bool q8 = wtype == SYN_Q8_0;
@@ -543,9 +542,7 @@ bool staged_faster(int32_t wtype, uint32_t n_out, uint32_t k_in, uint32_t rows) 
         const double per = !q8 ? 0.038 : syn::gemv_split_staged((int)wtype, (int)r, (int)k_in) ? 0.034 : 0.070;
         gemv += (q8 ? 3.2 : 2.4) + (q8 ? 0.141 : 0.089) * M + per * M * (double)r;
     }
-    const double wgs_per_cu = (double)((((uint64_t)n_out + 31) / 32 + 255) / 256);  // 256 CUs
-    const double gemm = (q8 ? 2.6 : 2.4) + (q8 ? 0.40 : 0.49) * (double)(k_in / 128) * (1.0 + 0.2 * (wgs_per_cu - 1.0));
-    return gemm < gemv;
+    return syn::gemm_q8_cost_us((int)wtype, (int)n_out, (int)k_in, (int)rows) < gemv;
 }
 
 // Rows on the int8 matrix cores: where the LDS-staged GEMM takes the shape and is the faster

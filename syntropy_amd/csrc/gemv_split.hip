@@ -11,10 +11,11 @@
 // rows are staged in LDS once per workgroup.  Each block's term is written to LDS and lane r
 // folds activation row r's terms in block order.
 //
-// 2 or more rows (k_gemm_q8_staged, Q8_0 and Q4_0, where rows hold whole 4-block stages; else for
-// Q8_0 from 9 rows k_gemm_q8_split): v_mfma_i32_16x16x32_i8 takes one 32-value block of 16 weight
-// rows against 16 tokens: the exact I32 sums of 256 outputs, which the lane owning each output
-// scales and folds (one term per block, in block order).
+// 2 or more rows (k_gemm_q8_splitk up to 16 rows of whole 16-block stages, k_gemm_q8_staged for
+// more rows or rows of whole 4-block stages, Q8_0 and Q4_0; else for Q8_0 from 9 rows
+// k_gemm_q8_split): v_mfma_i32_16x16x32_i8 takes one 32-value block of 16 weight rows against 16
+// tokens: the exact I32 sums of 256 outputs, which are scaled and folded (one term per block, in
+// block order).
 #include <type_traits>
 
 #include "common.hpp"
@@ -637,6 +638,200 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
     }
 }
 
+// ---- up to 16 rows: the K-split staged GEMM ------------------------------------------------------
+//
+// A workgroup of four wavefronts owns one 16-row x 16-token tile.  A stage holds 16 blocks of
+// every operand; wavefront w takes blocks 4w .. 4w + 3 of it, as a slice laid out like a stage of
+// k_gemm_q8_staged (the same lines and swizzles), computes the terms (dw dx) s of its blocks for
+// the tile's 256 outputs and writes them to LDS.  After the next barrier lane o of the workgroup
+// adds output o's 16 terms of the stage to its sum, in block order: the fold, and every bit, is
+// the one-wavefront kernel's, with four wavefronts on the tile and a quarter of the stages each.
+// Terms of output o sit at [o][16 blocks], wavefront w's four at 16-byte slot w ^ (o & 3).
+constexpr int QK_SLICES = 4;             // wavefronts, one 4-block slice of a stage each
+constexpr int QK_SB = QS_S * QK_SLICES;  // blocks per stage
+constexpr int QK_NS = 2;                 // ring stages
+
+template <int FMT>
+struct QkCfg {
+    static constexpr int CB = FMT == T_Q8_0 ? 32 : 16;
+    static constexpr int WL = QS_S * CB;                        // a row's bytes in a slice
+    static constexpr int W_OFF = 0;                             // [slice][16 rows][WL]
+    static constexpr int A_OFF = QK_SLICES * 16 * WL;           // [slice][16 tokens][128]
+    static constexpr int SC_OFF = A_OFF + QK_SLICES * 16 * 128;  // [16 rows][16 blocks] F16
+    static constexpr int DX_OFF = SC_OFF + 16 * QK_SB * 2;       // [16 tokens][16 blocks] F32
+    static constexpr int STAGE = DX_OFF + 16 * QK_SB * 4;
+    static constexpr int TERMS = 256 * QK_SB * 4;               // [256 outputs][16 blocks] F32
+    static constexpr int LDS = QK_NS * STAGE + 2 * TERMS;
+    static constexpr int WCOP = 16 * WL / 1024;  // row-line copies of a slice: 2 (Q8_0) or 1 (Q4_0)
+    static constexpr int COP = WCOP + 2 + 1;     // + 2 token-line copies + a scale copy (wavefronts 0, 1)
+};
+
+template <int FMT>
+__global__ __launch_bounds__(256) void k_gemm_q8_splitk(const uint8_t* __restrict__ W, int n_out, int k,
+                                                         const int8_t* __restrict__ xq,
+                                                         const float* __restrict__ xd, int T,
+                                                         float* __restrict__ y,
+                                                         const uint32_t* __restrict__ active) {
+    using C = QkCfg<FMT>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    T = active_rows(active, 0, T);
+    const int row0 = (int)blockIdx.x * 16, t0 = (int)blockIdx.y * 16;
+    if (t0 >= T) return;  // uniform per workgroup
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: copy bases in SGPRs
+    const int c = lane & 15, p = lane >> 4;
+    const int nb = k / 32, nst = nb / QK_SB;
+    const uint32_t rb = (uint32_t)nb * (uint32_t)C::CB;
+    const uint8_t* scales = W + (uint64_t)C::CB * (uint64_t)n_out * (uint64_t)nb;
+    auto wrow = [&](int r) { return (uint32_t)(row0 + r < n_out ? row0 + r : n_out - 1); };
+    auto tok = [&](int t) { return (uint32_t)(t0 + t < T ? t0 + t : T - 1); };
+    // this wavefront's copies: its slice's row and token lines, and for wavefronts 0 and 1 the
+    // stage's row scales (32 bytes a row) or token scales (64 bytes a token)
+    QsCopy cp[C::COP];
+    const int slot = lane & 7, li = lane >> 3;
+    auto src128 = [&](int cc) {  // the inverse of the 128-byte line swizzle (qs_slot)
+        const int j = (slot >> 1) ^ ((cc >> 1) & 3), h = (slot & 1) ^ ((cc >> 3) & 1);
+        return (uint32_t)(32 * j + 16 * h);
+    };
+    const uint32_t wslice = (uint32_t)(4 * wave) * (uint32_t)C::CB;  // the slice's first block in a row
+    int ncop = 0;
+#pragma unroll
+    for (int q = 0; q < C::WCOP; ++q) {
+        if constexpr (FMT == T_Q8_0) {
+            const int r = 8 * q + li;
+            cp[ncop++] = QsCopy{W, wrow(r) * rb + wslice + src128(r), (uint32_t)(C::W_OFF + wave * 16 * C::WL + 1024 * q),
+                                (uint32_t)(QK_SB * C::CB), true, true};
+        } else {
+            const int r = lane >> 2;
+            cp[ncop++] = QsCopy{W, wrow(r) * rb + wslice + 16u * (uint32_t)((lane & 3) ^ ((r >> 2) & 3)),
+                                (uint32_t)(C::W_OFF + wave * 16 * C::WL), (uint32_t)(QK_SB * C::CB), true, true};
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int t = 8 * q + li;
+        cp[ncop++] = QsCopy{reinterpret_cast<const uint8_t*>(xq), tok(t) * (uint32_t)k + (uint32_t)(4 * wave * 32) + src128(t),
+                            (uint32_t)(C::A_OFF + wave * 2048 + 1024 * q), (uint32_t)(QK_SB * 32), true, true};
+    }
+    if (wave == 0)
+        cp[ncop++] = QsCopy{scales, wrow(lane >> 1) * (uint32_t)nb * 2u + 16u * (uint32_t)(lane & 1),
+                            (uint32_t)C::SC_OFF, (uint32_t)(QK_SB * 2), true, lane < 32};
+    else if (wave == 1)
+        cp[ncop++] = QsCopy{reinterpret_cast<const uint8_t*>(xd), tok(lane >> 2) * (uint32_t)nb * 4u + 16u * (uint32_t)(lane & 3),
+                            (uint32_t)C::DX_OFF, (uint32_t)(QK_SB * 4), true, true};
+    const uint32_t ring = lds_addr(lds);
+    auto issue = [&](int s) {
+        const uint32_t st = ring + (uint32_t)(C::STAGE * (s % QK_NS));
+#pragma unroll
+        for (int u = 0; u < C::COP; ++u) {
+            if (u < ncop && cp[u].on) lds_dma16(cp[u].voff, cp[u].base + (size_t)cp[u].step * (size_t)s, st + cp[u].lds);
+        }
+    };
+    float* terms = reinterpret_cast<float*>(lds + QK_NS * C::STAGE);
+    float acc = 0.0f;  // output threadIdx.x: row o / 16, token o % 16
+    const int o = (int)threadIdx.x;
+    auto fold = [&](int buf) {
+        const float* tr = terms + buf * (C::TERMS / 4) + o * QK_SB;
+#pragma unroll
+        for (int j = 0; j < QK_SLICES; ++j) {
+            const float4 v = *reinterpret_cast<const float4*>(tr + 4 * (j ^ (o & 3)));
+            acc = (((acc + v.x) + v.y) + v.z) + v.w;
+        }
+    };
+    issue(0);
+    const v4i_s z = {0, 0, 0, 0};
+    for (int s = 0; s < nst; ++s) {
+        wait_vm<0>();    // this wavefront's copies of stage s have landed
+        lds_barrier();   // everyone's have; stage s - 1 and the terms of s - 2 are read out
+        if (s > 0) fold((s - 1) & 1);
+        if (s + 1 < nst) issue(s + 1);
+        const uint8_t* st = lds + C::STAGE * (s % QK_NS);
+        const uint8_t* wsl = st + C::W_OFF + wave * 16 * C::WL;
+        const uint8_t* asl = st + C::A_OFF + wave * 2048;
+        // the lane's rows 4 p + i: the slice's four scales each; token c's four scales
+        uint2 scw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) scw[i] = *reinterpret_cast<const uint2*>(st + C::SC_OFF + ((4 * p + i) * QK_SB + 4 * wave) * 2);
+        const float4 dxv = *reinterpret_cast<const float4*>(st + C::DX_OFF + (c * QK_SB + 4 * wave) * 4);
+        const float dx[4] = {dxv.x, dxv.y, dxv.z, dxv.w};
+        v4i_s d[QS_S];
+#pragma unroll
+        for (int j = 0; j < QS_S; ++j) {
+            const int ob = qs_slot(c, j, p);
+            long a;
+            if constexpr (FMT == T_Q8_0) {
+                a = *reinterpret_cast<const long*>(wsl + c * C::WL + ob);
+            } else {
+                const uint2 v = *reinterpret_cast<const uint2*>(wsl + c * C::WL + qs_slot4(c, j, p));
+                const int sh = 4 * (p >> 1);
+                a = (long)(((uint64_t)q4_signed(v.y, sh) << 32) | (uint64_t)q4_signed(v.x, sh));
+            }
+            const long b = *reinterpret_cast<const long*>(asl + c * 128 + ob);
+            d[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
+        }
+        float* tw = terms + (s & 1) * (C::TERMS / 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = scw[i].x, hi = scw[i].y;
+            float t[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float dw = f16_to_f32((uint16_t)((j < 2 ? lo : hi) >> (16 * (j & 1))));
+                t[j] = (dw * dx[j]) * (float)d[j][i];
+            }
+            const int oo = (4 * p + i) * 16 + c;  // the output: row 4 p + i, token c
+            *reinterpret_cast<float4*>(tw + oo * QK_SB + 4 * (wave ^ (oo & 3))) = make_float4(t[0], t[1], t[2], t[3]);
+        }
+    }
+    lds_barrier();
+    fold((nst - 1) & 1);
+    const int tk = t0 + (o & 15), r = row0 + (o >> 4);
+    if (tk < T && r < n_out) y[(int64_t)tk * n_out + r] = acc;
+}
+
+// Whether the K-split GEMM takes the shape: whole 16-block stages, at most 32 tokens (a second
+// 16-token tile is a second workgroup on the same rows), 32-bit offsets.
+bool gemm_q8_splitk_fits(int ty, int n_out, int k, int T) {
+    return T >= 1 && T <= 32 && (k / 32) % QK_SB == 0 && k % 32 == 0 && gemm_q8_staged_fits(ty, n_out, k, T);
+}
+
+// Estimated microseconds of the int8 GEMMs, fitted on MI355X timings (Q8_0 and Q4_0, 4096 to
+// 14336 rows of 4096 to 14336 values).  K-split: 2.5 + 0.6 per 16-block stage and workgroup per
+// CU (16 rows x 16 tokens a workgroup, 256 CUs).  Staged, up to 32 tokens: a + per 4-block stage
+// 0.49 (Q4_0; a 2.4) or 0.40 (Q8_0; a 2.6), 20% more per further workgroup a CU holds (32 rows a
+// workgroup).  Both follow the row length, not the token count, while a launch leaves SIMDs idle.
+double gemm_splitk_cost_us(int n_out, int k, int T) {
+    return 2.5 + 0.6 * (double)(k / 512) * (double)((n_out + 15) / 16) * (double)((T + 15) / 16) / 256.0;
+}
+double gemm_staged_cost_us(int ty, int n_out, int k) {
+    const double wgs_per_cu = (double)(((n_out + 31) / 32 + 255) / 256);
+    const bool q8 = ty == T_Q8_0;
+    return (q8 ? 2.6 : 2.4) + (q8 ? 0.40 : 0.49) * (double)(k / 128) * (1.0 + 0.2 * (wgs_per_cu - 1.0));
+}
+// The K-split form up to 16 tokens wherever it fits, and at 17 to 32 where it is estimated faster.
+static bool use_splitk(int ty, int n_out, int k, int T) {
+    if (!gemm_q8_splitk_fits(ty, n_out, k, T)) return false;
+    return T <= 16 || gemm_splitk_cost_us(n_out, k, T) < gemm_staged_cost_us(ty, n_out, k);
+}
+double gemm_q8_cost_us(int ty, int n_out, int k, int T) {
+    if (use_splitk(ty, n_out, k, T)) return gemm_splitk_cost_us(n_out, k, T);
+    return gemm_staged_cost_us(ty, n_out, k);
+}
+
+template <int FMT>
+static void launch_splitk(const uint8_t* W, int n_out, int k, const int8_t* xq, const float* xd, int T, float* y,
+                          hipStream_t stream, const uint32_t* active) {
+    using C = QkCfg<FMT>;
+    // once per process and format, thread-safe (a function-local static); a refusal shows as the
+    // launch's error
+    static const hipError_t attr = hipFuncSetAttribute((const void*)k_gemm_q8_splitk<FMT>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+    (void)attr;
+    const dim3 grid((unsigned)((n_out + 15) / 16), (unsigned)((T + 15) / 16));
+    hipLaunchKernelGGL((k_gemm_q8_splitk<FMT>), grid, dim3(256), (size_t)C::LDS, stream, W, n_out, k, xq, xd, T, y,
+                       active);
+}
+
 // Whether the staged GEMM takes the shape (Q8_0 or Q4_0 rows): whole stages, 32-bit copy offsets.
 bool gemm_q8_staged_fits(int ty, int n_out, int k, int T) {
     const uint64_t nb = (uint64_t)k / 32;
@@ -687,6 +882,13 @@ void launch_gemm_q8_split(int ty, const uint8_t* W, int n_out, int k, const uint
     const ActLayout L = act_layout(ACT_Q8_0, (uint64_t)T, (uint64_t)k);
     const int8_t* xq = reinterpret_cast<const int8_t*>(ws + L.codes);
     const float* xd = reinterpret_cast<const float*>(ws + L.d);
+    if (use_splitk(ty, n_out, k, T)) {  // rows of whole 16-block stages, up to 32 tokens
+        if (ty == T_Q4_0)
+            launch_splitk<T_Q4_0>(W, n_out, k, xq, xd, T, y, stream, active);
+        else
+            launch_splitk<T_Q8_0>(W, n_out, k, xq, xd, T, y, stream, active);
+        return;
+    }
     if (ty == T_Q4_0) {
         launch_staged_fmt<T_Q4_0>(W, n_out, k, xq, xd, T, y, stream, active);
         return;

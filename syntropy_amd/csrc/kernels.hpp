@@ -56,6 +56,9 @@ void launch_gemv_split(int ty, const uint8_t* W, int n_out, int k, const uint8_t
 void launch_gemm_q8_split(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws, int T, float* y,
                           hipStream_t stream, const uint32_t* active = nullptr);
 bool gemm_q8_staged_fits(int ty, int n_out, int k, int T);
+bool gemm_q8_splitk_fits(int ty, int n_out, int k, int T);
+// estimated microseconds of the int8 GEMM launch_gemm_q8_split picks (gemv_split.hip)
+double gemm_q8_cost_us(int ty, int n_out, int k, int T);
 bool gemv_split_staged(int ty, int rows, int k);
 // probe.hip: a read-only HBM stream with the decode GEMV's load pattern (counter calibration)
 void launch_hbm_read_probe(const uint8_t* src, uint64_t bytes, uint32_t* sink, hipStream_t stream);

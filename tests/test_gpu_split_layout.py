@@ -96,24 +96,26 @@ def test_split_gemm_edges_equal_oracle(S):
 
 @pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0])
 def test_split_gemm_staged_shapes_equal_oracle(S, ty):
-    """The LDS-staged GEMM (rows of whole 4-block stages): every token-tile variant (16, 32 and
-    64 tokens a workgroup; one or two 16-token tiles a wavefront: small launches take one),
+    """The LDS-staged GEMMs: the K-split form (up to 16 tokens, rows of whole 16-block stages:
+    9 and 16 rows here) and the staged form (more tokens, or rows of whole 4-block stages: every
+    token-tile variant, 16, 32 and 64 tokens a workgroup, one or two 16-token tiles a wavefront),
     partial workgroups of rows and tokens, one stage and many; for Q4_0 (64-byte row lines,
     nibbles widened in registers) and Q8_0."""
     w = None
     for rows in (9, 16, 17, 31, 32, 33, 64, 65, 127):
         w = check(S, ty, 50, 512, rows, 7000 + rows + ty, w)
     # the last three launch enough wavefronts for two-tile wavefronts (32 and 64 tokens)
-    for n_out, k, rows in ((33, 128, 40), (96, 4096, 48), (1, 128, 70), (4097, 256, 5), (32800, 128, 20),
-                           (32770, 128, 31), (4096, 256, 300)):
+    # (160, 14336, 24): the K-split form over two token tiles at long rows
+    for n_out, k, rows in ((33, 128, 40), (96, 4096, 48), (1, 128, 70), (4097, 256, 5), (160, 14336, 24),
+                           (32800, 128, 20), (32770, 128, 31), (4096, 256, 300)):
         check(S, ty, n_out, k, rows, n_out + k + rows + ty)
 
 
 @pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0])
 def test_split_gemm_few_rows_equal_oracle(S, ty):
-    """2 to 16 rows over 14336-row matrices, where the staged GEMM (one 16-token tile) takes over
-    from the split decode kernel at a few rows (4 for Q8_0, 7 for Q4_0): full tiles, a partial
-    last row tile and a partial last row group."""
+    """2 to 16 rows over 14336-row matrices, where the K-split GEMM (one 16-token tile, four
+    wavefronts on it) takes over from the split decode kernel at a few rows (3 for Q8_0, 6 for
+    Q4_0): full tiles, a partial last row tile and a partial last row group."""
     x = o.normal(0xF3 + ty, 0.02, 14336 * 4096)
     w = o.quantize(ty, x)
     for rows in (2, 5, 8, 13, 16):

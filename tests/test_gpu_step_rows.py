@@ -100,8 +100,8 @@ def test_x8_single_row_rows_active(cx, active):
                                               (o.Q8_0, 40, 3), (o.Q4_0, 12, 10), (o.Q4_0, 40, 33),
                                               (o.Q4_0, 40, 0)])
 def test_split_layout_rows_active(cx, ty, bucket, active):
-    """Layout 2 (SPLIT): the split decode kernel (one row, and Q4_0's twelve in eight-row
-    launches) and the staged int8 GEMM (Q8_0's twelve rows, forty rows)."""
+    """Layout 2 (SPLIT): the split decode kernel (one row), the K-split int8 GEMM (twelve rows)
+    and the staged int8 GEMM (forty rows)."""
     import ctypes as C
     import json
     P, pr = cx.P, cx.pr
