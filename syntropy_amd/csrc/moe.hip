@@ -1119,12 +1119,111 @@ static void launch_dense_wv(const uint8_t* W, int x8, int n_out, int k, MoeAct a
                        k, it, a, nullptr, nullptr, y, x8);
 }
 
+// The K-split form over one dense matrix (rows of a multiple of 4 super-blocks): a workgroup of
+// four wavefronts owns 16 weight rows and up to CH (4, 8 or 16) entries; a stage holds 4
+// super-blocks, one per wavefront, each in the one-wavefront expert stage layout (MoeCfg<1, 1,
+// CH>: the same copies and the same super-block arithmetic, q4k_super).  The entry chunk is
+// sized to the rows, so that small ones leave room in LDS for more workgroups per CU.  A wavefront's term of a super-block
+// comes out of q4k_super exactly (its sum starts at -0.0, and -0.0 + t = t); the terms go to LDS
+// at [entry][row][4] and, after the next barrier, lane o of the workgroup adds output o's four
+// in super-block order.  The fold, and every bit, is the one-wavefront kernel's with four
+// wavefronts on the rows.
+constexpr int DK_WAVES = 4;
+
+template <int NS, int CH>
+__global__ __launch_bounds__(64 * DK_WAVES) void k_q4k_rows_splitk(const uint8_t* __restrict__ W, int n_out, int k,
+                                                                   MoeItems it, MoeAct a, float* __restrict__ out,
+                                                                   int x8) {
+    using C = MoeCfg<1, 1, CH>;
+    constexpr int OUTS = 16 * CH;  // outputs of the workgroup: entry o / 16, row o % 16
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int STAGE = DK_WAVES * C::BYTES;
+    const int max_chunks = moe_max_chunks(it, nullptr);
+    const int lane = threadIdx.x & 63, p = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = k / 256, nst = nb / DK_WAVES;
+    const uint32_t rb = (uint32_t)nb * 144u;
+    float* terms = reinterpret_cast<float*>(lds + NS * STAGE);  // [2][OUTS][4]
+    int e, rg, ent0, nent;
+    if (!moe_item(it, (int)blockIdx.x, max_chunks, e, rg, ent0, nent)) return;  // uniform per workgroup
+    const uint8_t* const bases[1] = {W};
+    const ItemRows ir{rg * 16, n_out - 1, (uint32_t)(rg * 16) * rb, x8 != 0, (uint64_t)n_out * (uint64_t)nb};
+    const int ngroups = (nent + 3) >> 2;
+    // every wavefront makes the same slots (its 16 rows, the item's entries) and issues them for
+    // its own super-block of each stage into its own part of the stage
+    Slot sl[C::PER_WAVE];
+    int live = 0;
+#pragma unroll
+    for (int i = 0; i < C::PER_WAVE; ++i) {
+        sl[i] = make_slot<C>(i, bases, ir, rb, a, k, ent0, nent);
+        live += sl[i].live ? 1 : 0;
+    }
+    auto issue = [&](int s) {
+        uint8_t* part = lds + (s % NS) * STAGE + wave * C::BYTES;
+#pragma unroll
+        for (int i = 0; i < C::PER_WAVE; ++i) issue_slot(sl[i], DK_WAVES * s + wave, part);
+    };
+    const int o = (int)threadIdx.x;  // the output this lane folds (o < OUTS)
+    float acc = 0.0f;
+    auto fold = [&](int buf) {
+        if (o < OUTS) {
+            const float4 v = *reinterpret_cast<const float4*>(terms + buf * OUTS * 4 + o * 4);
+            acc = (((acc + v.x) + v.y) + v.z) + v.w;
+        }
+    };
+#pragma unroll
+    for (int q = 0; q < NS - 1; ++q)
+        if (q < nst) issue(q);
+#pragma unroll 1
+    for (int s = 0; s < nst; ++s) {
+        const int ahead = nst - 1 - s < NS - 2 ? nst - 1 - s : NS - 2;
+        wait_vm_n<C::PER_WAVE * (NS - 2)>(ahead * live);
+        lds_barrier();  // stage s whole; stage s - 1 and the terms of s - 2 read out
+        if (s > 0) fold((s - 1) & 1);
+        if (s + NS - 1 < nst) issue(s + NS - 1);
+        float t[1][C::NG];
+#pragma unroll
+        for (int g = 0; g < C::NG; ++g) t[0][g] = -0.0f;
+        q4k_super<C>(lds + (s % NS) * STAGE + wave * C::BYTES, 0, ent0, ngroups, t);
+        float* tw = terms + (s & 1) * OUTS * 4;
+#pragma unroll
+        for (int g = 0; g < C::NG; ++g)
+            if (g < ngroups) tw[((4 * g + p) * 16 + c) * 4 + wave] = t[0][g];
+    }
+    lds_barrier();
+    fold((nst - 1) & 1);
+    const int ent = o >> 4, row = rg * 16 + (o & 15);
+    if (o < OUTS && ent < nent && row < n_out) out[(int64_t)(ent0 + ent) * n_out + row] = acc;
+}
+
+template <int NS, int CH>
+static void launch_dense_splitk(const uint8_t* W, int x8, int n_out, int k, MoeAct a, int rows, float* y,
+                                hipStream_t stream, const uint32_t* active) {
+    using C = MoeCfg<1, 1, CH>;
+    const MoeItems it{nullptr, 1, (n_out + 15) / 16, C::CH, rows, active};
+    const int lds = NS * DK_WAVES * C::BYTES + 2 * 16 * CH * 4 * 4;
+    static const hipError_t lds_ok = hipFuncSetAttribute((const void*)k_q4k_rows_splitk<NS, CH>,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    (void)lds_ok;  // a refusal shows as the launch's error
+    const unsigned grid = (unsigned)it.row_groups * (unsigned)((rows + C::CH - 1) / C::CH);
+    hipLaunchKernelGGL((k_q4k_rows_splitk<NS, CH>), dim3(grid), dim3(64 * DK_WAVES), lds, stream, W, n_out, k, it, a,
+                       y, x8);
+}
+
 void launch_q4k_dense_rows(const uint8_t* W, int x8, int n_out, int k, MoeAct a, int rows, float* y,
                            hipStream_t stream, const uint32_t* active) {
-    if (n_out >= 8192)
+    if ((k / 256) % DK_WAVES == 0) {
+        if (rows <= 4)
+            launch_dense_splitk<2, 4>(W, x8, n_out, k, a, rows, y, stream, active);
+        else if (rows <= 8)
+            launch_dense_splitk<2, 8>(W, x8, n_out, k, a, rows, y, stream, active);
+        else
+            launch_dense_splitk<2, 16>(W, x8, n_out, k, a, rows, y, stream, active);
+    } else if (n_out >= 8192) {
         launch_dense_wv<2>(W, x8, n_out, k, a, rows, y, stream, active);
-    else
+    } else {
         launch_dense_wv<1>(W, x8, n_out, k, a, rows, y, stream, active);
+    }
 }
 
 // ============================================================================================
