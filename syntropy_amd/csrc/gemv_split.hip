@@ -808,10 +808,11 @@ double gemm_staged_cost_us(int ty, int n_out, int k) {
     const bool q8 = ty == T_Q8_0;
     return (q8 ? 2.6 : 2.4) + (q8 ? 0.40 : 0.49) * (double)(k / 128) * (1.0 + 0.2 * (wgs_per_cu - 1.0));
 }
-// The K-split form up to 16 tokens wherever it fits, and at 17 to 32 where it is estimated faster.
+// The K-split form where it fits and is estimated faster than the staged one (at 14336 rows of
+// 4096 values it is not: 896 workgroups at two per CU run in two rounds).
 static bool use_splitk(int ty, int n_out, int k, int T) {
     if (!gemm_q8_splitk_fits(ty, n_out, k, T)) return false;
-    return T <= 16 || gemm_splitk_cost_us(n_out, k, T) < gemm_staged_cost_us(ty, n_out, k);
+    return gemm_splitk_cost_us(n_out, k, T) < gemm_staged_cost_us(ty, n_out, k);
 }
 double gemm_q8_cost_us(int ty, int n_out, int k, int T) {
     if (use_splitk(ty, n_out, k, T)) return gemm_splitk_cost_us(n_out, k, T);

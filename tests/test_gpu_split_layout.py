@@ -113,9 +113,9 @@ def test_split_gemm_staged_shapes_equal_oracle(S, ty):
 
 @pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0])
 def test_split_gemm_few_rows_equal_oracle(S, ty):
-    """2 to 16 rows over 14336-row matrices, where the K-split GEMM (one 16-token tile, four
-    wavefronts on it) takes over from the split decode kernel at a few rows (3 for Q8_0, 6 for
-    Q4_0): full tiles, a partial last row tile and a partial last row group."""
+    """2 to 16 rows over 14336-row matrices, where the staged GEMM (one 16-token tile; at this
+    many rows it is estimated faster than the K-split form) takes over from the split decode
+    kernel at a few rows: full tiles, a partial last row tile and a partial last row group."""
     x = o.normal(0xF3 + ty, 0.02, 14336 * 4096)
     w = o.quantize(ty, x)
     for rows in (2, 5, 8, 13, 16):
