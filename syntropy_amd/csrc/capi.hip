@@ -525,8 +525,8 @@ constexpr uint32_t SPLIT_GEMM_MAX_ROWS = 65535u * 32u;  // the GEMM grid's token
 
 namespace {
 // Whether the staged GEMM beats the split decode kernel at 2 to 16 rows (one 16-token tile), from
-// estimated microseconds fitted on MI355X timings of both kernels (Q8_0 and Q4_0, 4096 to 14336
-// rows of 4096 to 14336 values).  Split decode kernel, per launch of r <= 8 rows over M million
+// estimated microseconds fitted on MI355X timings of both kernels with the weights read from
+// HBM (Q8_0 and Q4_0, 4096 to 14336 rows of 4096 to 14336 values).  Split decode kernel, per launch of r <= 8 rows over M million
 // weights: a + read M + per M r (Q4_0: 2.4, 0.089, 0.038; Q8_0: 3.2, 0.141, 0.034, or 0.070
 // per row and million weights when the activation rows do not fit in LDS and are read from
 // global memory).  The GEMM's estimate is gemm_q8_cost_us (gemv_split.hip): flat in the rows up

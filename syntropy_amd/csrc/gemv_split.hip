@@ -795,13 +795,15 @@ bool gemm_q8_splitk_fits(int ty, int n_out, int k, int T) {
     return T >= 1 && T <= 32 && (k / 32) % QK_SB == 0 && k % 32 == 0 && gemm_q8_staged_fits(ty, n_out, k, T);
 }
 
-// Estimated microseconds of the int8 GEMMs, fitted on MI355X timings (Q8_0 and Q4_0, 4096 to
-// 14336 rows of 4096 to 14336 values).  K-split: 2.5 + 0.6 per 16-block stage and workgroup per
-// CU (16 rows x 16 tokens a workgroup, 256 CUs).  Staged, up to 32 tokens: a + per 4-block stage
-// 0.49 (Q4_0; a 2.4) or 0.40 (Q8_0; a 2.6), 20% more per further workgroup a CU holds (32 rows a
-// workgroup).  Both follow the row length, not the token count, while a launch leaves SIMDs idle.
-double gemm_splitk_cost_us(int n_out, int k, int T) {
-    return 2.5 + 0.6 * (double)(k / 512) * (double)((n_out + 15) / 16) * (double)((T + 15) / 16) / 256.0;
+// Estimated microseconds of the int8 GEMMs, fitted on MI355X timings with the weights read from
+// HBM (Q8_0 and Q4_0, 4096 to 14336 rows of 4096 to 14336 values).  K-split: 4.7 + 0.45 (Q4_0)
+// or 5.1 + 0.49 (Q8_0) per 16-block stage and workgroup per CU (16 rows x 16 tokens a workgroup,
+// 256 CUs).  Staged, up to 32 tokens: a + per 4-block stage 0.49 (Q4_0; a 2.4) or 0.40 (Q8_0;
+// a 2.6), 20% more per further workgroup a CU holds (32 rows a workgroup).  Both follow the row
+// length, not the token count, while a launch leaves SIMDs idle.
+double gemm_splitk_cost_us(int ty, int n_out, int k, int T) {
+    const double x = (double)(k / 512) * (double)((n_out + 15) / 16) * (double)((T + 15) / 16) / 256.0;
+    return ty == T_Q8_0 ? 5.1 + 0.49 * x : 4.7 + 0.45 * x;
 }
 double gemm_staged_cost_us(int ty, int n_out, int k) {
     const double wgs_per_cu = (double)(((n_out + 31) / 32 + 255) / 256);
@@ -812,10 +814,10 @@ double gemm_staged_cost_us(int ty, int n_out, int k) {
 // 4096 values it is not: 896 workgroups at two per CU run in two rounds).
 static bool use_splitk(int ty, int n_out, int k, int T) {
     if (!gemm_q8_splitk_fits(ty, n_out, k, T)) return false;
-    return gemm_splitk_cost_us(n_out, k, T) < gemm_staged_cost_us(ty, n_out, k);
+    return gemm_splitk_cost_us(ty, n_out, k, T) < gemm_staged_cost_us(ty, n_out, k);
 }
 double gemm_q8_cost_us(int ty, int n_out, int k, int T) {
-    if (use_splitk(ty, n_out, k, T)) return gemm_splitk_cost_us(n_out, k, T);
+    if (use_splitk(ty, n_out, k, T)) return gemm_splitk_cost_us(ty, n_out, k, T);
     return gemm_staged_cost_us(ty, n_out, k);
 }
 
