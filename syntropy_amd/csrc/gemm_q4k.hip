@@ -218,8 +218,10 @@ SYN_DEV void gemm_issue(const GemmArgs& g, const GemmSlots& s, int wave, int lan
 }
 
 // The F16 pair (1024 + 16 q0, 1024 + 16 q1) etc. from the nibbles under `mask`.
+// (v & mask) | 0x64006400 is one v_bitop3_b32 (truth table 0xEA = (a & b) | c); written as two
+// operations the compiler issues an AND and an OR.
 SYN_DEV h2 magic_pair(uint32_t v, uint32_t mask) {
-    return __builtin_bit_cast(h2, (v & mask) | 0x64006400u);
+    return __builtin_bit_cast(h2, __builtin_amdgcn_bitop3_b32(v, mask, 0x64006400u, 0xEA));
 }
 
 SYN_DEV h2 bcast(_Float16 v) { return h2{v, v}; }
