@@ -80,6 +80,39 @@ def _link(out: str, objs, extra=()) -> None:
     os.replace(tmp, out)
 
 
+# Host code under AddressSanitizer and UndefinedBehaviorSanitizer (each flag for the host pass
+# only: the kernels' device code is built as always).  The libraries this gives resolve the
+# sanitizer runtime from the program that loads them (tests/sanitize/host_paths.cpp).
+SANITIZE_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                 "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer",
+                 "-Xarch_host", "-g"]
+
+
+def build_host_sanitized(out_dir: str, jobs: int = 8) -> tuple:
+    """Both libraries with sanitized host code, into out_dir; returns their paths."""
+    obj_dir = os.path.join(out_dir, "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    srcs = sources()
+
+    def one(src):
+        obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
+        lang = ["-x", "hip"] if src.endswith(".cpp") else FILE_FLAGS.get(os.path.basename(src), [])
+        r = subprocess.run([HIPCC, *FLAGS, *SANITIZE_HOST, *lang, "-c", src, "-o", obj], capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=min(jobs, len(srcs))) as ex:
+        objs = list(ex.map(one, srcs))
+    provider = [o for o in objs if os.path.basename(o).startswith("provider.")]
+    kernels = [o for o in objs if o not in provider]
+    lib = os.path.join(out_dir, os.path.basename(LIB))
+    plib = os.path.join(out_dir, os.path.basename(PROVIDER_LIB))
+    _link(lib, kernels)
+    _link(plib, objs, [f"-Wl,--version-script={PROVIDER_MAP}", "-Wl,-Bsymbolic"])
+    return lib, plib
+
+
 def build(jobs: int = 8) -> str:
     os.makedirs(OBJ, exist_ok=True)
     srcs = sources()
