@@ -1210,9 +1210,159 @@ static void launch_dense_splitk(const uint8_t* W, int x8, int n_out, int k, MoeA
                        y, x8);
 }
 
+// The K-split form over X8 rows (rows of a multiple of 8 super-blocks, each row whole runs):
+// eight wavefronts on 16 weight rows, a stage holding one run (super-blocks 8s..8s+7) of every
+// row.  The weights are copied along whole 128-byte lines (eight consecutive lanes read one
+// line: chunk q of the run's eight super-blocks) into a shared region in line order, 16-byte
+// chunks [row][q][i ^ ((row >> 1) & 7)] (the XOR spreads 16 rows' reads of one super-block over
+// distinct banks), and wavefront i reads super-block i of the run from it; each wavefront copies
+// its own super-block's entries (codes, sums, scales) as the expert stage does.  The arithmetic
+// (q4k_block), the terms and their fold in super-block order are the four-wavefront form's.
+constexpr int X8R_WV = 8;
+constexpr int X8R_WBYTES = 16 * 9 * 128;  // one run of 16 rows
+constexpr int X8R_WSLOTS = X8R_WBYTES / 1024;
+
+template <class C>
+constexpr int x8r_entry_bytes() { return C::BYTES - C::CODES; }  // codes, sums, scale window
+template <class C>
+constexpr int x8r_stage() { return X8R_WBYTES + X8R_WV * x8r_entry_bytes<C>(); }
+
+// Super-block i of the run, as lane (c, p) holds it, from the line-order region: row c's header is
+// chunk 0, its codes at 16 + 32 g + 8 p are chunk 1 + 2 g + p / 2 at 8 (p & 1).
+SYN_DEV WBlock<1> x8r_block(const uint8_t* wl, int i) {
+    const int lane = threadIdx.x & 63, c = lane & 15, p = lane >> 4;
+    const uint8_t* r = wl + c * (9 * 128) + 16 * (i ^ ((c >> 1) & 7));
+    WBlock<1> w;
+    w.hdr[0] = *reinterpret_cast<const v4u*>(r);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const uint2 v = *reinterpret_cast<const uint2*>(r + (1 + 2 * g + (p >> 1)) * 128 + 8 * (p & 1));
+        w.q[0][2 * g] = v.x;
+        w.q[0][2 * g + 1] = v.y;
+    }
+    return w;
+}
+
+template <int NS, int CH>
+__global__ __launch_bounds__(64 * X8R_WV) void k_q4k_rows_x8(const uint8_t* __restrict__ W, int n_out, int k,
+                                                              MoeItems it, MoeAct a, float* __restrict__ out) {
+    using C = MoeCfg<1, 1, CH>;
+    constexpr int WV = X8R_WV, OUTS = 16 * CH, EB = x8r_entry_bytes<C>(), STAGE = x8r_stage<C>();
+    constexpr int WPER = (X8R_WSLOTS + WV - 1) / WV;  // weight slots per wavefront (at most)
+    constexpr int EPER = C::SLOTS - C::WSLOTS;         // entry slots per wavefront
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int max_chunks = moe_max_chunks(it, nullptr);
+    const int lane = threadIdx.x & 63, p = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = k / 256, nst = nb / 8;
+    const uint32_t rb = (uint32_t)nb * 144u;
+    float* terms = reinterpret_cast<float*>(lds + NS * STAGE);  // [2][OUTS][WV]
+    int e, rg, ent0, nent;
+    if (!moe_item(it, (int)blockIdx.x, max_chunks, e, rg, ent0, nent)) return;  // uniform per workgroup
+    const int ngroups = (nent + 3) >> 2;
+    // weight slots: chunk ci = 64 slot + lane is line ci / 8 (row r = ci / 72, chunk q of the run)
+    // at position ci % 8, which holds super-block (ci % 8) ^ ((r >> 1) & 7) of the run; rows past
+    // the matrix read its last row (their outputs are not written)
+    Slot ws[WPER];
+    int live = 0;
+#pragma unroll
+    for (int u = 0; u < WPER; ++u) {
+        const int slot = wave + WV * u;
+        const int ci = 64 * (slot < X8R_WSLOTS ? slot : 0) + lane;
+        const int line = ci >> 3, r = line / 9, q = line - 9 * r;
+        const int row = rg * 16 + r < n_out ? rg * 16 + r : n_out - 1;
+        ws[u].src = W + ((uint64_t)row * rb + 128u * (uint32_t)q + 16u * (uint32_t)((ci & 7) ^ ((r >> 1) & 7)));
+        ws[u].step = 1152u;  // one run
+        ws[u].on = true;
+        ws[u].live = slot < X8R_WSLOTS;
+        ws[u].x8 = false;
+        ws[u].xq = 0;
+        ws[u].xg0 = ws[u].xnb = 0;
+        ws[u].lds = slot * 1024;
+        live += ws[u].live ? 1 : 0;
+    }
+    // this wavefront's entry slots for its super-block of each run
+    const uint8_t* const bases[1] = {W};
+    const ItemRows ir{rg * 16, n_out - 1, 0u, false, 0};
+    Slot es[EPER];
+#pragma unroll
+    for (int i = 0; i < EPER; ++i) {
+        es[i] = make_slot<C>(C::WSLOTS + i, bases, ir, rb, a, k, ent0, nent);
+        live += es[i].live ? 1 : 0;
+    }
+    auto issue = [&](int s) {
+        uint8_t* st = lds + (s % NS) * STAGE;
+#pragma unroll
+        for (int u = 0; u < WPER; ++u) issue_slot(ws[u], s, st);
+        // make_slot's entry offsets start at C::CODES: shift them to this wavefront's part
+        uint8_t* part = st + X8R_WBYTES + wave * EB - C::CODES;
+#pragma unroll
+        for (int i = 0; i < EPER; ++i) issue_slot(es[i], 8 * s + wave, part);
+    };
+    const int o = (int)threadIdx.x;  // the output this lane folds (o < OUTS)
+    float acc = 0.0f;
+    auto fold = [&](int buf) {
+        if (o < OUTS) {
+#pragma unroll
+            for (int h = 0; h < WV / 4; ++h) {
+                const float4 v = *reinterpret_cast<const float4*>(terms + (buf * OUTS + o) * WV + 4 * h);
+                acc = (((acc + v.x) + v.y) + v.z) + v.w;
+            }
+        }
+    };
+#pragma unroll
+    for (int q = 0; q < NS - 1; ++q)
+        if (q < nst) issue(q);
+#pragma unroll 1
+    for (int s = 0; s < nst; ++s) {
+        const int ahead = nst - 1 - s < NS - 2 ? nst - 1 - s : NS - 2;
+        wait_vm_n<(WPER + EPER) * (NS - 2)>(ahead * live);
+        lds_barrier();  // stage s whole; stage s - 1 and the terms of s - 2 read out
+        if (s > 0) fold((s - 1) & 1);
+        if (s + NS - 1 < nst) issue(s + NS - 1);
+        const uint8_t* st = lds + (s % NS) * STAGE;
+        const uint8_t* part = st + X8R_WBYTES + wave * EB;
+        float t[1][C::NG];
+#pragma unroll
+        for (int g = 0; g < C::NG; ++g) t[0][g] = -0.0f;
+        const WBlock<1> w = x8r_block(st, wave);
+        q4k_block<1, C::NG>(w, part, part + (C::LH - C::CODES), reinterpret_cast<const float*>(part + (C::DX - C::CODES)),
+                            ent0, ngroups, t);
+        float* tw = terms + (s & 1) * OUTS * WV;
+#pragma unroll
+        for (int g = 0; g < C::NG; ++g)
+            if (g < ngroups) tw[((4 * g + p) * 16 + c) * WV + wave] = t[0][g];
+    }
+    lds_barrier();
+    fold((nst - 1) & 1);
+    const int ent = o >> 4, row = rg * 16 + (o & 15);
+    if (o < OUTS && ent < nent && row < n_out) out[(int64_t)(ent0 + ent) * n_out + row] = acc;
+}
+
+template <int NS, int CH>
+static void launch_rows_x8(const uint8_t* W, int n_out, int k, MoeAct a, int rows, float* y, hipStream_t stream,
+                           const uint32_t* active) {
+    using C = MoeCfg<1, 1, CH>;
+    const MoeItems it{nullptr, 1, (n_out + 15) / 16, C::CH, rows, active};
+    const int lds = NS * x8r_stage<C>() + 2 * 16 * CH * X8R_WV * 4;
+    static const hipError_t lds_ok = hipFuncSetAttribute((const void*)k_q4k_rows_x8<NS, CH>,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    (void)lds_ok;  // a refusal shows as the launch's error
+    const unsigned grid = (unsigned)it.row_groups * (unsigned)((rows + C::CH - 1) / C::CH);
+    hipLaunchKernelGGL((k_q4k_rows_x8<NS, CH>), dim3(grid), dim3(64 * X8R_WV), lds, stream, W, n_out, k, it, a, y);
+}
+
 void launch_q4k_dense_rows(const uint8_t* W, int x8, int n_out, int k, MoeAct a, int rows, float* y,
                            hipStream_t stream, const uint32_t* active) {
-    if ((k / 256) % DK_WAVES == 0) {
+    const int nb = k / 256;
+    if (x8 && nb % 8 == 0) {  // X8 rows of whole runs: the line-order form
+        if (rows <= 4)
+            launch_rows_x8<2, 4>(W, n_out, k, a, rows, y, stream, active);
+        else if (rows <= 8)
+            launch_rows_x8<2, 8>(W, n_out, k, a, rows, y, stream, active);
+        else
+            launch_rows_x8<2, 16>(W, n_out, k, a, rows, y, stream, active);
+    } else if (nb % DK_WAVES == 0) {
         if (rows <= 4)
             launch_dense_splitk<2, 4>(W, x8, n_out, k, a, rows, y, stream, active);
         else if (rows <= 8)
