@@ -233,7 +233,9 @@ struct GemmHdr {
 };
 
 // The matrix-core part of one super-block of the wavefront's 64 tokens x 32 rows, from the
-// weights and codes of the stage in LDS: dacc = S1 - 512 X exactly, and the row headers.
+// weights and codes of the stage in LDS: dacc = S1 - 512 X exactly, and the row headers.  Only
+// the first NMT 16-token tiles are computed (a tile of fewer entries leaves the rest empty).
+template <int NMT>
 SYN_DEV void gemm_mfma(const uint8_t* st, int wave, int lane, v4f (&dacc)[GM_MT][GM_NT], GemmHdr& h) {
     const int c = lane & 15, p = lane >> 4;
     const uint8_t* wt = st + (16 * GM_NT * wave) * 144;
@@ -271,7 +273,7 @@ SYN_DEV void gemm_mfma(const uint8_t* st, int wave, int lane, v4f (&dacc)[GM_MT]
     }
 
 #pragma unroll
-    for (int mt = 0; mt < GM_MT; ++mt)
+    for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < GM_NT; ++nt) dacc[mt][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -290,7 +292,7 @@ SYN_DEV void gemm_mfma(const uint8_t* st, int wave, int lane, v4f (&dacc)[GM_MT]
             bq[nt] = v8h{y3.x, y3.y, y2.x, y2.y, y1.x, y1.y, y4.x, y4.y};
         }
 #pragma unroll
-        for (int mt = 0; mt < GM_MT; ++mt) {
+        for (int mt = 0; mt < NMT; ++mt) {
             const int t = 16 * mt + c;
             const v8h a = *reinterpret_cast<const v8h*>(at + t * 512 + (((8 * p + s) ^ c) << 4));
 #pragma unroll
@@ -302,12 +304,13 @@ SYN_DEV void gemm_mfma(const uint8_t* st, int wave, int lane, v4f (&dacc)[GM_MT]
 
 // S2 from the tail's code sums, then the super-block's terms folded into the accumulators in
 // the reference's rounding order.
+template <int NMT>
 SYN_DEV void gemm_fold(const uint8_t* tl, int lane, const v4f (&dacc)[GM_MT][GM_NT], const GemmHdr& h,
                        v4f (&acc)[GM_MT][GM_NT]) {
     const int c = lane & 15, p = lane >> 4;
     const v8h zero8 = {};
 #pragma unroll
-    for (int mt = 0; mt < GM_MT; ++mt) {
+    for (int mt = 0; mt < NMT; ++mt) {
         const v8h as = p < 2 ? *reinterpret_cast<const v8h*>(tl + (16 * mt + c) * 32 + 16 * p) : zero8;
         const v4f dx = *reinterpret_cast<const v4f*>(tl + GM_TT * 32 + (16 * mt + 4 * p) * 4);
         const v4f xs = *reinterpret_cast<const v4f*>(tl + GM_TT * 36 + (16 * mt + 4 * p) * 4);
@@ -337,7 +340,7 @@ static_assert(GM_WA % 16 == 0 && GM_TB % 16 == 0 && GM_LOOP_LDS <= 160 * 1024, "
 // (independent work the wavefront can issue between the products), with the two sets of exact
 // sums alternating by parity.  Super-block 0 has no fold before it, so it is peeled: the loop's
 // products and fold are one straight run of code the scheduler can interleave.
-template <class Issue>
+template <int NMT, class Issue>
 SYN_DEV void gemm_loop(int nb, int live, uint8_t* smem, int wave, int lane, Issue&& issue,
                        v4f (&acc)[GM_MT][GM_NT]) {
     uint8_t* tails = smem + 2 * GM_WA;
@@ -353,9 +356,9 @@ SYN_DEV void gemm_loop(int nb, int live, uint8_t* smem, int wave, int lane, Issu
         // this lane's loads of b have landed once at most those of b + 1 are in flight
         wait_vm_n<GM_PER_WAVE>(b + 1 < nb ? live : 0);
         lds_barrier();
-        gemm_mfma(stage, wave, lane, dc, hc);
+        gemm_mfma<NMT>(stage, wave, lane, dc, hc);
         if constexpr (decltype(fold)::value) {
-            gemm_fold(tails + prev * GM_TB, lane, dp, hp, acc);
+            gemm_fold<NMT>(tails + prev * GM_TB, lane, dp, hp, acc);
         }
         lds_barrier();
         if (b + 2 < nb) issue(b + 2, stage, tails + prev * GM_TB);
@@ -368,9 +371,9 @@ SYN_DEV void gemm_loop(int nb, int live, uint8_t* smem, int wave, int lane, Issu
     }
     const int last = slot == 0 ? 2 : slot - 1;  // the slot of nb - 1
     if (nb & 1)
-        gemm_fold(tails + last * GM_TB, lane, d0, h0, acc);
+        gemm_fold<NMT>(tails + last * GM_TB, lane, d0, h0, acc);
     else
-        gemm_fold(tails + last * GM_TB, lane, d1, h1, acc);
+        gemm_fold<NMT>(tails + last * GM_TB, lane, d1, h1, acc);
 }
 
 __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_q4k(GemmArgs g) {
@@ -388,9 +391,14 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_q4k(GemmArgs g) {
 #pragma unroll
         for (int nt = 0; nt < GM_NT; ++nt) acc[mt][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    gemm_loop(g.nb, live, smem, wave, lane,
-              [&](int b, uint8_t* stage, uint8_t* tail) { gemm_issue(g, sl, wave, lane, b, t0, stage, tail); },
-              acc);
+    auto issue = [&](int b, uint8_t* stage, uint8_t* tail) { gemm_issue(g, sl, wave, lane, b, t0, stage, tail); };
+    // the 16-token tiles holding active rows (a last tile of fewer rows computes only those)
+    switch ((T - t0 < GM_TT ? T - t0 + 15 : GM_TT) / 16) {
+        case 1: gemm_loop<1>(g.nb, live, smem, wave, lane, issue, acc); break;
+        case 2: gemm_loop<2>(g.nb, live, smem, wave, lane, issue, acc); break;
+        case 3: gemm_loop<3>(g.nb, live, smem, wave, lane, issue, acc); break;
+        default: gemm_loop<GM_MT>(g.nb, live, smem, wave, lane, issue, acc); break;
+    }
 
     const int c = lane & 15, p = lane >> 4;
 #pragma unroll
@@ -624,7 +632,14 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
     for (int mt = 0; mt < GM_MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < GM_NT; ++nt) acc[mt][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_loop(g.nb, live, smem, wave, lane, issue, acc);
+    // the 16-token tiles holding entries (the padding of an expert's last tile is not computed;
+    // its outputs are dropped)
+    switch ((nvalid + 15) / 16) {
+        case 1: gemm_loop<1>(g.nb, live, smem, wave, lane, issue, acc); break;
+        case 2: gemm_loop<2>(g.nb, live, smem, wave, lane, issue, acc); break;
+        case 3: gemm_loop<3>(g.nb, live, smem, wave, lane, issue, acc); break;
+        default: gemm_loop<GM_MT>(g.nb, live, smem, wave, lane, issue, acc); break;
+    }
     const int c = lane & 15, p = lane >> 4;
     if constexpr (MODE == 0) {
         // u (wavefronts 4-7) through LDS to the wavefronts holding g of the same outputs
