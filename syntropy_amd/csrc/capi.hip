@@ -617,6 +617,12 @@ int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
         if ((uint64_t)n_out * rows > (1ull << 40)) return fail(SYN_E_INVALID, "%s: rows * n_out too large", W);
         if (split_gemm(wtype, n_out, k_in, rows) && rows > SPLIT_GEMM_MAX_ROWS)
             return fail(SYN_E_UNSUPPORTED, "%s: %u rows (the GEMM takes %u)", W, rows, SPLIT_GEMM_MAX_ROWS);
+        if (rows == 1 && k_in && !split_gemm(wtype, n_out, k_in, rows) && syn::gemv_split_fused_fits((int)wtype, (int)k_in)) {
+            // one row: quantized inside the product's workgroups, one launch
+            syn::launch_gemv_split_fused((int)wtype, (const uint8_t*)w, (int)n_out, (int)k_in, x, y, (hipStream_t)stream,
+                                         active);
+            return check_launch(W);
+        }
         if (k_in) {
             syn::launch_act_quant(syn::ACT_Q8_0, x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
             if (int rc = check_launch(W)) return rc;

@@ -8,8 +8,10 @@
 // 1 to 8 rows (k_gemv_split): one weight row per wavefront, eight per workgroup.  Each wavefront
 // load instruction reads 1 KB of the row's codes, 16 bytes a lane: half a Q8_0 block (the pair
 // of lanes adds its two exact halves with a lane swap) or a whole Q4_0 block.  The activation
-// rows are staged in LDS once per workgroup.  Each block's term is written to LDS and lane r
-// folds activation row r's terms in block order.
+// rows are staged in LDS once per workgroup; a single F32 row can instead be quantized there by
+// every workgroup (the same Q8_0 blocks the quantization kernel writes), under the first weight
+// loads, which saves the separate quantization launch.  Each block's term is written to LDS and
+// lane r folds activation row r's terms in block order.
 //
 // 2 or more rows (k_gemm_q8_splitk up to 16 rows of whole 16-block stages, k_gemm_q8_staged for
 // more rows or rows of whole 4-block stages, Q8_0 and Q4_0; else for Q8_0 from 9 rows
@@ -60,6 +62,9 @@ void launch_split_repack(int ty, const uint8_t* src, uint8_t* dst, uint64_t byte
 // ---- 1 to 8 rows ---------------------------------------------------------------------------------
 
 constexpr int SPLIT_WAVES = 8;
+// wavefronts of a workgroup that quantizes its row itself: sixteen quantize the row half as often
+// as eight (Q4_0 4096 x 4096: 5.9 against 6.8 us a call)
+constexpr int FUSE_WAVES = 16;
 constexpr int SPLIT_UNROLL = 4;  // 16-byte weight loads a lane has in flight
 constexpr int SPLIT_STAGE_MAX = 48 * 1024;  // LDS bytes of staged activation rows at most
 
@@ -70,16 +75,19 @@ SYN_HD inline size_t split_act_lds(int ty, int R, int k) {
     return (size_t)R * k + (size_t)R * nb * 4 * (ty == T_Q4_0 ? 2 : 1);
 }
 // per wavefront, the terms of one load instruction: [R][64 blocks]
-SYN_HD inline size_t split_fold_lds(int R) { return (size_t)SPLIT_WAVES * R * 64 * 4; }
+SYN_HD inline size_t split_fold_lds(int R, int waves = SPLIT_WAVES) { return (size_t)waves * R * 64 * 4; }
 
-// STAGED: the activation rows are copied to LDS first (when they fit), else read from global.
-template <int FMT, int R, int STAGED>
-__global__ __launch_bounds__(64 * SPLIT_WAVES) void k_gemv_split(const uint8_t* __restrict__ W, int n_out, int k,
+// STAGED 1: the activation rows are copied to LDS first (when they fit), 0: read from global;
+// 2 (R = 1): the F32 row xf is quantized to Q8_0 blocks in LDS by the workgroup.
+template <int FMT, int R, int STAGED, int WVS = STAGED == 2 ? FUSE_WAVES : SPLIT_WAVES>
+__global__ __launch_bounds__(64 * WVS) void k_gemv_split(const uint8_t* __restrict__ W, int n_out, int k,
                                                                   const int8_t* __restrict__ xq,
                                                                   const float* __restrict__ xd,
                                                                   const int32_t* __restrict__ xs, int rows,
                                                                   float* __restrict__ y,
-                                                                  const uint32_t* __restrict__ active, int first) {
+                                                                  const uint32_t* __restrict__ active, int first,
+                                                                  const float* __restrict__ xf) {
+    static_assert(STAGED != 2 || R == 1, "one row quantized in the workgroup");
     rows = active_rows(active, first, rows);
     if (rows == 0) return;  // uniform
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -87,18 +95,52 @@ __global__ __launch_bounds__(64 * SPLIT_WAVES) void k_gemv_split(const uint8_t* 
     constexpr int BPI = FMT == T_Q8_0 ? 32 : 64;  // blocks per wavefront load instruction
     const int nb = k / 32;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = (int)blockIdx.x * SPLIT_WAVES + wave;
+    const int row = (int)blockIdx.x * WVS + wave;
+    const uint64_t nblocks = (uint64_t)n_out * nb;
+    const int rowc = row < n_out ? row : n_out - 1;  // a wavefront past the matrix loads its last row, unused
+    const uint8_t* codes = W + (uint64_t)rowc * nb * CB;
+    const uint16_t* scales = reinterpret_cast<const uint16_t*>(W + (uint64_t)CB * nblocks) + (uint64_t)rowc * nb;
+    const int pieces = FMT == T_Q8_0 ? 2 * nb : nb;  // 16-byte pieces of the row
+    // SPLIT_UNROLL load instructions (and their scales) in flight before the arithmetic: the
+    // loads are unconditional (pieces past the row re-read its last piece, unused) and the
+    // scales stay raw bits until used, so no wait splits the group.  The first group is issued
+    // before the activation rows are staged.
+    v4u_s wv[SPLIT_UNROLL];
+    uint16_t swv[SPLIT_UNROLL];
+    auto load_group = [&](int g0) {
+#pragma unroll
+        for (int u = 0; u < SPLIT_UNROLL; ++u) {
+            const int h0 = g0 + 64 * u + lane;
+            const int h = h0 < pieces ? h0 : pieces - 1;
+            wv[u] = __builtin_nontemporal_load(reinterpret_cast<const v4u_s*>(codes + 16 * (uint64_t)h));
+            swv[u] = scales[FMT == T_Q8_0 ? h >> 1 : h];
+        }
+    };
+    // STAGED 2: the row's first values are loaded before the weights, so that quantizing them
+    // waits for them alone (loads retire in order) while the weight loads fly
+    constexpr int XPRE = 16 / WVS > 0 ? 16 / WVS : 1;  // passes of 64 WVS lanes (k <= 4096)
+    float4 xv[XPRE];
+    if constexpr (STAGED == 2) {
+#pragma unroll
+        for (int q = 0; q < XPRE; ++q) {
+            const int t = (int)threadIdx.x + 64 * WVS * q;
+            const int tc = t < nb * 8 ? t : 0;
+            xv[q] = reinterpret_cast<const float4*>(xf)[tc];  // block tc / 8, values 4 (tc % 8) ..
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weights'
+    }
+    load_group(0);
     const int8_t* aq = xq;
     const float* ad = xd;
     const int32_t* as = xs;
     size_t fold_off = 0;
-    if constexpr (STAGED) {
+    if constexpr (STAGED == 1) {
         int8_t* lq = reinterpret_cast<int8_t*>(lds);
         float* ld = reinterpret_cast<float*>(lds + (size_t)R * k);
         int32_t* ls = reinterpret_cast<int32_t*>(lds + (size_t)R * k + (size_t)R * nb * 4);
-        for (int i = threadIdx.x; i < rows * k / 16; i += 64 * SPLIT_WAVES)
+        for (int i = threadIdx.x; i < rows * k / 16; i += 64 * WVS)
             reinterpret_cast<v4u_s*>(lq)[i] = reinterpret_cast<const v4u_s*>(xq)[i];
-        for (int i = threadIdx.x; i < rows * nb; i += 64 * SPLIT_WAVES) {
+        for (int i = threadIdx.x; i < rows * nb; i += 64 * WVS) {
             ld[i] = xd[i];
             if constexpr (FMT == T_Q4_0) ls[i] = xs[i];
         }
@@ -107,27 +149,40 @@ __global__ __launch_bounds__(64 * SPLIT_WAVES) void k_gemv_split(const uint8_t* 
         as = ls;
         fold_off = align_up(split_act_lds(FMT, R, k), 16);
         __syncthreads();
+    } else if constexpr (STAGED == 2) {
+        // q8_0_block_lane over eight lanes a block: the blocks of a pass are whole groups of
+        // eight lanes, active or not together
+        int8_t* lq = reinterpret_cast<int8_t*>(lds);
+        float* ld = reinterpret_cast<float*>(lds + (size_t)k);
+        int32_t* ls = reinterpret_cast<int32_t*>(lds + (size_t)k + (size_t)nb * 4);
+        // lane t % 8 of block t / 8 (values 4 (t % 8) ..); computed by every lane of the pass, so
+        // that the preloaded values are used where they were loaded, written where t is a block's
+        auto quant = [&](float4 v, int t) {
+            const int blk = t >> 3, sub = t & 7;
+            const Q8_0Lane q = q8_0_block_lane(v);
+            if (t < nb * 8) {
+                reinterpret_cast<uint32_t*>(lq + (size_t)blk * 32)[sub] = q.packed;
+                if (sub == 0) {
+                    ld[blk] = q.d;
+                    if constexpr (FMT == T_Q4_0) ls[blk] = q.sum;
+                }
+            }
+        };
+#pragma unroll
+        for (int q = 0; q < XPRE; ++q) quant(xv[q], (int)threadIdx.x + 64 * WVS * q);
+        for (int t = (int)threadIdx.x + 64 * WVS * XPRE; t < nb * 8; t += 64 * WVS)
+            quant(reinterpret_cast<const float4*>(xf)[t], t);
+        aq = lq;
+        ad = ld;
+        as = ls;
+        fold_off = align_up(split_act_lds(FMT, R, k), 16);
+        lds_barrier();  // the LDS rows whole; the weight loads stay in flight
     }
     float* buf = reinterpret_cast<float*>(lds + fold_off) + (size_t)wave * R * 64;
     if (row >= n_out) return;  // uniform per wavefront; no workgroup barrier below
-    const uint64_t nblocks = (uint64_t)n_out * nb;
-    const uint8_t* codes = W + (uint64_t)row * nb * CB;
-    const uint16_t* scales = reinterpret_cast<const uint16_t*>(W + (uint64_t)CB * nblocks) + (uint64_t)row * nb;
-    const int pieces = FMT == T_Q8_0 ? 2 * nb : nb;  // 16-byte pieces of the row
-    float acc = 0.0f;                                // lane r < rows: activation row r's sum
+    float acc = 0.0f;          // lane r < rows: activation row r's sum
     for (int g0 = 0; g0 < pieces; g0 += 64 * SPLIT_UNROLL) {
-        // SPLIT_UNROLL load instructions (and their scales) in flight before the arithmetic: the
-        // loads are unconditional (pieces past the row re-read its last piece, unused) and the
-        // scales stay raw bits until used, so no wait splits the group
-        v4u_s wv[SPLIT_UNROLL];
-        uint16_t swv[SPLIT_UNROLL];
-#pragma unroll
-        for (int u = 0; u < SPLIT_UNROLL; ++u) {
-            const int h0 = g0 + 64 * u + lane;
-            const int h = h0 < pieces ? h0 : pieces - 1;
-            wv[u] = __builtin_nontemporal_load(reinterpret_cast<const v4u_s*>(codes + 16 * (uint64_t)h));
-            swv[u] = scales[FMT == T_Q8_0 ? h >> 1 : h];
-        }
+        if (g0) load_group(g0);
 #pragma unroll
         for (int u = 0; u < SPLIT_UNROLL; ++u) {
             const int i0 = g0 + 64 * u;
@@ -194,10 +249,10 @@ static void launch_split_fmt(const uint8_t* W, int n_out, int k, const uint8_t* 
         if (stage <= (size_t)SPLIT_STAGE_MAX) {
             const size_t lds = align_up(stage, 16) + split_fold_lds(RR);
             hipLaunchKernelGGL((k_gemv_split<FMT, RR, 1>), grid, dim3(64 * SPLIT_WAVES), lds, stream, W, n_out, k, xq,
-                               xd, xs, rows, yr, active, first);
+                               xd, xs, rows, yr, active, first, nullptr);
         } else {
             hipLaunchKernelGGL((k_gemv_split<FMT, RR, 0>), grid, dim3(64 * SPLIT_WAVES), split_fold_lds(RR), stream, W,
-                               n_out, k, xq, xd, xs, rows, yr, active, first);
+                               n_out, k, xq, xd, xs, rows, yr, active, first, nullptr);
         }
     };
     switch (split_r(rows)) {
@@ -206,6 +261,22 @@ static void launch_split_fmt(const uint8_t* W, int n_out, int k, const uint8_t* 
     case 4: go(std::integral_constant<int, 4>{}); break;
     default: go(std::integral_constant<int, 8>{}); break;
     }
+}
+
+// One F32 row quantized inside the product's workgroups (no workspace): where its Q8_0 blocks fit
+// the LDS staging area.
+bool gemv_split_fused_fits(int ty, int k) { return split_act_lds(ty, 1, k) <= (size_t)SPLIT_STAGE_MAX; }
+
+void launch_gemv_split_fused(int ty, const uint8_t* W, int n_out, int k, const float* x, float* y, hipStream_t stream,
+                             const uint32_t* active) {
+    const dim3 grid((unsigned)((n_out + FUSE_WAVES - 1) / FUSE_WAVES));
+    const size_t lds = align_up(split_act_lds(ty, 1, k), 16) + split_fold_lds(1, FUSE_WAVES);
+    if (ty == T_Q8_0)
+        hipLaunchKernelGGL((k_gemv_split<T_Q8_0, 1, 2>), grid, dim3(64 * FUSE_WAVES), lds, stream, W, n_out, k, nullptr,
+                           nullptr, nullptr, 1, y, active, 0, x);
+    else
+        hipLaunchKernelGGL((k_gemv_split<T_Q4_0, 1, 2>), grid, dim3(64 * FUSE_WAVES), lds, stream, W, n_out, k, nullptr,
+                           nullptr, nullptr, 1, y, active, 0, x);
 }
 
 // y[r][o] over a SPLIT matrix from rows quantized to Q8_0 in `ws` (act_layout(ACT_Q8_0, rows, k)),

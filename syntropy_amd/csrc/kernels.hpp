@@ -60,6 +60,9 @@ bool gemm_q8_splitk_fits(int ty, int n_out, int k, int T);
 // estimated microseconds of the int8 GEMM launch_gemm_q8_split picks (gemv_split.hip)
 double gemm_q8_cost_us(int ty, int n_out, int k, int T);
 bool gemv_split_staged(int ty, int rows, int k);
+bool gemv_split_fused_fits(int ty, int k);
+void launch_gemv_split_fused(int ty, const uint8_t* W, int n_out, int k, const float* x, float* y, hipStream_t stream,
+                             const uint32_t* active);
 // probe.hip: a read-only HBM stream with the decode GEMV's load pattern (counter calibration)
 void launch_hbm_read_probe(const uint8_t* src, uint64_t bytes, uint32_t* sink, hipStream_t stream);
 uint64_t hbm_read_probe_workgroups(uint64_t bytes);
