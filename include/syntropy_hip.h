@@ -85,8 +85,8 @@ int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uin
  *   layout 1 one row runs the decode kernel with the row quantized in every workgroup (k_in <=
  *   16384), 2 to 31 rows the decode expert kernel on rows quantized beforehand (int8 matrix
  *   cores, the matrix as one expert), more rows the matrix-core GEMM (k_in a multiple of 2048).
- *   Layout 2 at one row (k_in <= 40960) is one launch whose workgroups quantize the row to Q8_0
- *   blocks themselves; otherwise it quantizes the rows to Q8_0 blocks and runs the split decode
+ *   Layout 2 at one row (k_in up to 39296 for Q4_0, 43680 for Q8_0) is one launch whose
+ *   workgroups quantize the row to Q8_0 blocks themselves; otherwise it quantizes the rows to Q8_0 blocks and runs the split decode
  *   kernel eight rows at a time, or the int8 matrix-core GEMM: for k_in a multiple of 128 where
  *   it is the faster (from 2 to 9 rows by shape, always beyond 16), and for Q8_0 of other k_in
  *   from 9 rows.
