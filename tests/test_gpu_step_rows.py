@@ -96,12 +96,12 @@ def test_x8_single_row_rows_active(cx, active):
     check_rows(got, want, active, "x8")
 
 
-@pytest.mark.parametrize("ty,bucket,active", [(o.Q8_0, 1, 0), (o.Q8_0, 12, 9), (o.Q8_0, 40, 17),
-                                              (o.Q8_0, 40, 3), (o.Q4_0, 12, 10), (o.Q4_0, 40, 33),
+@pytest.mark.parametrize("ty,bucket,active", [(o.Q8_0, 1, 0), (o.Q8_0, 1, 1), (o.Q4_0, 1, 1), (o.Q8_0, 12, 9),
+                                              (o.Q8_0, 40, 17), (o.Q8_0, 40, 3), (o.Q4_0, 12, 10), (o.Q4_0, 40, 33),
                                               (o.Q4_0, 40, 0)])
 def test_split_layout_rows_active(cx, ty, bucket, active):
-    """Layout 2 (SPLIT): the split decode kernel (one row), the K-split int8 GEMM (twelve rows)
-    and the staged int8 GEMM (forty rows)."""
+    """Layout 2 (SPLIT): the split decode kernel quantizing its one row in its workgroups, the
+    K-split int8 GEMM (twelve rows) and the staged int8 GEMM (forty rows)."""
     import ctypes as C
     import json
     P, pr = cx.P, cx.pr
