@@ -475,6 +475,8 @@ void launch_moe_route(const float* router, const float* x, int rows, int hidden,
 // ============================================================================================
 // err[0]: 1 when an id is out of range, else 0; err[1]: the largest expert's entry count.
 
+constexpr int PACK_BATCH = 8;  // chunks of 64 ids a wavefront loads at once
+
 // One workgroup of 1024 threads; wave w owns the contiguous slot range [w*per, (w+1)*per).
 // Pass 1 counts per (wave, expert) in LDS; pass 2 scans to per-(wave, expert) bases; pass 3
 // places each wave's slots in order (64 at a time, ranks among equal experts by ballots).
@@ -498,12 +500,24 @@ __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ i
     __shared__ uint32_t bad;  // the first slot whose id names no expert, or ~0
     if (tid == 0) bad = ~0u;
     __syncthreads();
-    for (int s = s_begin + lane; s < s_end; s += 64) {
-        const int e = ids[s];
-        if (e < 0 || e >= n_experts)
-            atomicMin(&bad, (uint32_t)s);
-        else if (!site || site[e] != 0)
-            atomicAdd(&cnt[wave * n_experts + e], 1u);
+    // the wave's ids PACK_BATCH chunks of 64 at a time, their loads in flight together
+    for (int c0 = s_begin; c0 < s_end; c0 += 64 * PACK_BATCH) {
+        int ev[PACK_BATCH];
+#pragma unroll
+        for (int u = 0; u < PACK_BATCH; ++u) {
+            const int s = c0 + 64 * u + lane;
+            ev[u] = s < s_end ? ids[s] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < PACK_BATCH; ++u) {
+            const int s = c0 + 64 * u + lane;
+            if (s >= s_end) continue;
+            const int e = ev[u];
+            if (e < 0 || e >= n_experts)
+                atomicMin(&bad, (uint32_t)s);
+            else if (!site || site[e] != 0)
+                atomicAdd(&cnt[wave * n_experts + e], 1u);
+        }
     }
     __syncthreads();
     if (bad != ~0u) {
@@ -578,9 +592,19 @@ __global__ __launch_bounds__(1024) void k_moe_pack(const int32_t* __restrict__ i
     }
     __syncthreads();
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int ev[PACK_BATCH];
     for (int c0 = s_begin; c0 < s_end; c0 += 64) {
+        const int u = ((c0 - s_begin) >> 6) % PACK_BATCH;  // uniform
+        if (u == 0)  // the next PACK_BATCH chunks' ids, loaded together
+#pragma unroll
+            for (int v = 0; v < PACK_BATCH; ++v) {
+                const int sv = c0 + 64 * v + lane;
+                ev[v] = sv < s_end ? ids[sv] : -1;
+            }
         const int s = c0 + lane;
-        const int e = s < s_end ? ids[s] : -1;
+        int e = -1;
+#pragma unroll
+        for (int v = 0; v < PACK_BATCH; ++v) e = v == u ? ev[v] : e;
         const bool live = e >= 0 && (!site || site[e] != 0);
         // lanes holding the same expert
         uint64_t same = __ballot(live);
