@@ -355,8 +355,9 @@ def weight_set(torch, S, ty, n, k, seed, layout=0):
     return out
 
 
-def gemv_case(torch, S, ws_list, rows, n, k, nrep):
-    """(step us: quantization + GEMV, kernel us: the GEMV on quantized rows) at `rows` rows."""
+def gemv_case(torch, S, ws_list, rows, n, k, nrep, kernel=True):
+    """(step us: quantization + GEMV, kernel us: the GEMV on quantized rows, or None when not
+    asked for) at `rows` rows."""
     ty = ws_list[0].ty
     x = torch.randn(rows, k, device="cuda")
     y = torch.empty(rows, n, device="cuda")
@@ -366,7 +367,7 @@ def gemv_case(torch, S, ws_list, rows, n, k, nrep):
     ws = torch.empty(max(need.value, 256), dtype=torch.uint8, device="cuda")
     step = gpu_us(torch, lambda i: S.gemv(ws_list[i % len(ws_list)], x, rows, y=y, ws=ws), nrep)
     kern = None
-    if lay in (0, 2):  # the product alone, over rows quantized beforehand
+    if kernel and lay in (0, 2):  # the product alone, over rows quantized beforehand
         qws = S.new_workspace(ty, rows, k)
         S.quantize_into(ty, x, rows, k, qws)
         kern = gpu_us(torch, lambda i: S.gemv_quantized(ws_list[i % len(ws_list)], qws, rows, y), nrep)
@@ -429,7 +430,7 @@ def bench_rows(torch, S, a):
         wl = weight_set(torch, S, Q4K, n, k, 0x51A10004, layout)
         t = {}
         for rows in (1, 2, 4, 8):
-            t[rows], _ = gemv_case(torch, S, wl, rows, n, k, nrep)
+            t[rows], _ = gemv_case(torch, S, wl, rows, n, k, nrep, kernel=False)
         out["x8" if layout else "source"] = {"us": {str(r): round(v, 3) for r, v in t.items()},
                                              "ratio": {str(r): round(t[r] / t[1], 3) for r in (2, 4, 8)}}
         del wl
