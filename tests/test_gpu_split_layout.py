@@ -66,11 +66,13 @@ def check(S, ty, n_out, k, rows, seed, w=None):
 
 
 @pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0])
-@pytest.mark.parametrize("n_out,k", [(37, 32), (300, 1024), (41, 3072), (9, 14336), (130, 16384 + 32)])
+@pytest.mark.parametrize("n_out,k", [(37, 32), (300, 1024), (41, 3072), (9, 14336), (130, 16384 + 32), (9, 45056)])
 def test_split_decode_rows_equal_oracle(S, ty, n_out, k):
     """1 to 8 rows (staged activations for narrow rows, global reads for wide ones), 9 and 20 rows
-    (eight-row groups, or the GEMM where it is the faster); row lengths of 1 to 513 blocks,
-    partial last load groups and row counts not multiples of eight."""
+    (eight-row groups, or the GEMM where it is the faster); row lengths of 1 to 1408 blocks,
+    partial last load groups and row counts not multiples of eight.  One row is one launch that
+    quantizes its row in LDS up to 39,296 (Q4_0) or 43,680 (Q8_0) values; 45,056 takes the
+    quantization launch first."""
     w = None
     for rows in (1, 2, 3, 5, 8, 9, 20):
         w = check(S, ty, n_out, k, rows, 1000 * rows + n_out + k + ty, w)
