@@ -334,6 +334,22 @@ def test_gate_up_act_equals_oracle(S, ty, rows, n, k):
     assert_same(got, o.gate_up_act(ty, w, n, k, x, rows, threads=8), "gate_up_act")
 
 
+@pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0])
+@pytest.mark.parametrize("n,k", [(700, 4096), (64, 45056)])
+def test_gate_up_act_split_layout(S, ty, n, k):
+    """GateUpAct over SPLIT weights: one row (one launch that quantizes the row in LDS at 4096
+    values; the quantization launch first at 45,056), a few rows and the GEMM's row counts."""
+    rng = GemvRng(ty * 31 + n + k)
+    w = gemv_weights(rng, ty, 2 * n, k, o.f16_bits, o.round_bf16)
+    W = S.repack(S.Weights(ty, dev(w), 2 * n, k))
+    assert W.layout == S.LAYOUT_SPLIT
+    for rows in (1, 3, 12):
+        x = gemv_activations(rng, rows, k)
+        announce(f"gate_up_act split ty={ty} rows={rows} n={n} k={k}")
+        got = host(S.gate_up_act(W, dev(x.astype(np.float32)), rows))
+        assert_same(got, o.gate_up_act(ty, w, n, k, x, rows, threads=8), f"split rows {rows}")
+
+
 def test_gate_up_act_x8_layout(S):
     rng = GemvRng(4242)
     n, k = 1024, 4096

@@ -64,10 +64,11 @@ def head_weights(S, ty, seed):
 
 
 @pytest.mark.parametrize("ty,layout,rows", [(o.Q4_K, 0, 1), (o.Q4_K, 1, 1), (o.Q4_K, 0, 3), (o.Q4_K, 1, 64),
-                                            (o.Q8_0, 0, 2)])
+                                            (o.Q8_0, 0, 2), (o.Q8_0, 2, 1), (o.Q8_0, 2, 5)])
 def test_logits_vocab_head(S, ty, layout, rows):
-    """A 128256 x 4096 head: one decode row on the GEMV kernels (both layouts), a few rows, and 64
-    rows on the matrix-core GEMM (X8)."""
+    """A 128256 x 4096 head: one decode row on the GEMV kernels (Q4_K in both layouts; Q8_0 SPLIT
+    in one launch that quantizes the row in LDS), a few rows, and 64 rows on the matrix-core GEMM
+    (X8)."""
     w = head_weights(S, ty, 0x10 + ty)
     rs = np.random.default_rng(rows)
     x = (rs.standard_normal((rows, HIDDEN)) * 3).astype(np.float32)
@@ -75,8 +76,8 @@ def test_logits_vocab_head(S, ty, layout, rows):
     want = o.logits(ty, w, VOCAB, HIDDEN, g, 1e-5, x, rows, threads=16)
     wty = {o.Q4_K: S.WeightType.Q4K, o.Q8_0: S.WeightType.Q8_0}[ty]
     W = S.Weights(wty, dev(w), VOCAB, HIDDEN)
-    if layout == 1:
-        W = S.repack(W)
+    if layout:
+        W = S.repack(W, layout)
     announce(f"logits head {VOCAB}x{HIDDEN} ty={ty} layout={layout} rows={rows}")
     got = host(S.logits(W, dev(g), 1e-5, dev(x), rows))
     assert_same(got, want, "logits")
