@@ -245,6 +245,28 @@ def test_grouped_skewed_loads(M):
     assert_same(got, want)
 
 
+def test_grouped_decode_path_heavy_expert(M):
+    """The decode kernels (few entries per expert on average) with one expert holding 35 of 80
+    entries: its entries span several work items of the gate/up (16 entries) and down (12
+    entries) kernels, the last one partial and starting off a multiple of four."""
+    s = M.MoeShape(16, 2, 512, 768)
+    gate, up, down = random_q4k_experts(21, s.n_experts, s.hidden, s.inter)
+    rows = 40
+    rng = MoeRng(23)
+    x = moe_activations(rng, rows * s.hidden).reshape(rows, s.hidden)
+    ids = moe_route_ids(rng, rows, s.top_k, s.n_experts)
+    ids[:35, 0] = 3
+    ids[:35, 1] = np.where(ids[:35, 1] == 3, 11, ids[:35, 1])
+    ids[35] = [0, 2]
+    counts = np.bincount(ids.ravel(), minlength=s.n_experts)
+    assert counts[3] == 35 and counts[:3].sum() % 4 == 2  # expert 3's entries start at 6
+    announce("grouped decode path heavy expert")
+    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, 16, 2, 512, 768, gate, up, down, x, ids)
+    assert st == 0
+    assert_same(got, want)
+
+
 def test_grouped_row_permutation(M):
     """moe/tests.rs:497-539: permuting rows permutes the per-slot and combined outputs."""
     s = M.MoeShape(6, 2, 256, 512)
