@@ -504,6 +504,117 @@ void launch_gate_up_q4k_f32(const uint8_t* W, int n, int k, const float* x, floa
 }
 
 // ---- the x8 repack: a permutation of whole 16-byte chunks --------------------------------------
+// Two or three rows over X8 weights: the one-row decode kernel's loads and its one block per
+// lane, with the NR activation rows (Q8_K, quantized beforehand) side by side in LDS, so the
+// weights stream once and each lane computes its block's term against every row; each row's
+// terms are folded in block order by the row's first lane, as at one row.  Rows of up to 64
+// super-blocks; rows past the step's active rows are neither computed nor written.
+constexpr int XR_WAVES = 8;
+
+SYN_HD inline size_t xr_row_lds(int nb) { return align_up(q4k_dec_lds(nb) + 16, 16); }  // + the scales' 16-byte tail
+
+template <int NR>
+__global__ __launch_bounds__(64 * XR_WAVES) void k_gemv_q4k_x8_rows(const uint8_t* __restrict__ W, int n_out, int nb,
+                                                                  const uint8_t* __restrict__ ws, int rows_ws, int rows,
+                                                                  float* __restrict__ y,
+                                                                  const uint32_t* __restrict__ active) {
+    rows = active_rows(active, 0, rows);
+    if (rows == 0) return;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int P = lanes_per_row(nb);
+    const int row = ((int)blockIdx.x * XR_WAVES + wave) * (64 / P) + lane / P;
+    const int b = lane % P;
+    const bool ok = row < n_out && b < nb;
+    const int RB = (int)xr_row_lds(nb);
+    // the activation rows stream into LDS first (as the one-row kernel's), then the block
+    const ActLayout L = act_layout(ACT_Q8K, (uint64_t)rows_ws, (uint64_t)nb * 256);
+    const uint32_t l0 = lds_addr(lds);
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        if (r >= rows) break;  // uniform
+        const uint8_t* codes = ws + L.codes + (size_t)r * nb * 256;
+        const uint32_t lr = l0 + (uint32_t)(r * RB);
+        for (int c = wv; c < nb; c += XR_WAVES)
+            if (lane < 16) lds_dma16(16u * (uint32_t)lane, codes + (size_t)c * 256, lr + (uint32_t)(c * COL));
+        if (wv == 0) {
+            const uint8_t* sums = ws + L.sums + (size_t)r * nb * 32;
+            for (int u = 0; u * 64 < nb * 2; ++u)
+                if (u * 64 + lane < nb * 2)
+                    lds_dma16(16u * (uint32_t)lane, sums + (size_t)u * 1024, lr + (uint32_t)(xs_off(nb) + u * 1024));
+            // up to 12 bytes past the row's scales: the next row's, or the sums after them
+            if (lane * 4 < nb) lds_dma16(16u * (uint32_t)lane, ws + L.d + (size_t)r * nb * 4, lr + (uint32_t)xd_off(nb));
+        }
+    }
+    v4u A[9];
+    {
+        const uint64_t nblocks = (uint64_t)n_out * (uint64_t)nb;
+        const uint64_t g = ok ? (uint64_t)row * nb + b : 0;
+        const uint8_t* src = W + x8_chunk_offset(g, 0, nblocks);
+        const uint32_t step = 16u * x8_group_blocks(g, nblocks);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) A[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(src + step * i));
+    }
+    wait_vm<9>();  // this wavefront's row loads, all older than the block's nine
+    lds_barrier();
+    float* terms = reinterpret_cast<float*>(lds + (size_t)NR * RB) + wave * 64;
+    float t[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) t[r] = r < rows ? q4k_term_lds(A, lds + r * RB, nb, ok ? b : 0) : 0.0f;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) terms[r * XR_WAVES * 64 + lane] = ok ? t[r] : 0.0f;
+    wave_lds_sync();
+    if (b == 0 && row < n_out) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            if (r >= rows) break;
+            const float4* tv = reinterpret_cast<const float4*>(terms + r * XR_WAVES * 64 + lane);
+            float acc = 0.0f;
+            for (int q = 0; q < P / 4; ++q) {
+                const float4 v = tv[q];
+                acc = acc + v.x;
+                acc = acc + v.y;
+                acc = acc + v.z;
+                acc = acc + v.w;
+            }
+            y[(int64_t)r * n_out + row] = acc;
+        }
+    }
+}
+
+// Where it is the faster form (measured against the K-split expert kernel over X8 runs, 14336 x
+// 4096, 4096 x 14336 and 4096 x 4096): two rows of up to 64 super-blocks (10.7 against 13.2 us
+// at 14336 x 4096, level elsewhere); three rows only where every CU holds a workgroup and the
+// rows are at most 16 super-blocks (12.0 against 13.2 us at 14336 x 4096; 13-14 % slower at 4096
+// rows, where a row's extra terms no longer hide under the weight stream).
+bool gemv_q4k_x8_rows_pick(int n_out, int k, int rows) {
+    if (k % 256 || k <= 0 || k > 64 * 256) return false;
+    const int nb = k / 256;
+    return rows == 2 || (rows == 3 && nb <= 16 && (n_out + 31) / 32 >= 256);
+}
+
+void launch_gemv_q4k_x8_rows(const uint8_t* W, int n_out, int k, const uint8_t* ws, int rows, float* y,
+                             hipStream_t stream, const uint32_t* active) {
+    const int nb = k / 256;
+    const int rows_per_wg = XR_WAVES * (64 / (nb <= 16 ? 16 : nb <= 32 ? 32 : 64));
+    const dim3 grid((unsigned)((n_out + rows_per_wg - 1) / rows_per_wg));
+#define SYN_XR(NR)                                                                                          \
+    do {                                                                                                     \
+        const size_t lds = (size_t)NR * xr_row_lds(nb) + (size_t)NR * XR_WAVES * 64 * 4;                     \
+        static const hipError_t lds_ok = hipFuncSetAttribute((const void*)k_gemv_q4k_x8_rows<NR>,             \
+                                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024); \
+        (void)lds_ok; /* a refusal shows as the launch's error */                                            \
+        hipLaunchKernelGGL((k_gemv_q4k_x8_rows<NR>), grid, dim3(64 * XR_WAVES), lds, stream, W, n_out, nb, ws, rows, \
+                           rows, y, active);                                                                 \
+    } while (0)
+    if (rows <= 2)
+        SYN_XR(2);
+    else
+        SYN_XR(3);
+#undef SYN_XR
+}
+
 __global__ __launch_bounds__(256) void k_q4k_x8(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
                                                 uint64_t nblocks, int inverse) {
     const uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;  // source chunk (GGUF order)

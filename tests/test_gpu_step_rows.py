@@ -74,15 +74,18 @@ def test_gemv_rows_active(cx, ty, bucket, n_out, k, active):
     check_rows(got, want, active, f"gemv ty={ty}")
 
 
-@pytest.mark.parametrize("active", [0, 1])
-def test_x8_single_row_rows_active(cx, active):
+@pytest.mark.parametrize("bucket,n_out,active", [(1, 1024, 0), (1, 1024, 1), (2, 1024, 0), (2, 1024, 1),
+                                                 (3, 8200, 2), (3, 8200, 3)])
+def test_x8_rows_active(cx, bucket, n_out, active):
+    """X8 weights at one row (the fused decode kernel) and at two and three rows (the decode
+    kernel over rows side by side in LDS), with fewer rows active than the bucket."""
     import ctypes as C
     import json
     P, pr = cx.P, cx.pr
-    rng = GemvRng(991)
-    n_out, k = 1024, 4096
+    rng = GemvRng(991 + bucket)
+    k = 4096
     w = gemv_weights(rng, o.Q4_K, n_out, k, o.f16_bits, o.round_bf16)
-    x = gemv_activations(rng, 1, k).reshape(1, k)
+    x = gemv_activations(rng, bucket, k).reshape(bucket, k)
     kb = json.dumps(gemv_key(o.Q4_K)).encode()
     kbuf = (C.c_uint8 * len(kb)).from_buffer_copy(kb)
     present, lay = C.c_uint32(), C.c_uint32()
@@ -90,9 +93,10 @@ def test_x8_single_row_rows_active(cx, active):
     pr.vt.repack(pr.vt.slf, kbuf, len(kb), w.ctypes.data_as(C.POINTER(C.c_uint8)), w.size,
                  wl.ctypes.data_as(C.POINTER(C.c_uint8)), wl.size, C.byref(present), C.byref(lay))
     _, step = step_desc(cx, active)
-    announce(f"rows_active x8 active={active}")
-    got = dense_launch(cx, dict(gemv_key(o.Q4_K), layout=1), 1, n_out, k, wl, x, step)
-    want = o.gemv(o.Q4_K, w, n_out, k, x, 1, threads=8) if active else None
+    announce(f"rows_active x8 bucket={bucket} n_out={n_out} active={active}")
+    got = dense_launch(cx, dict(gemv_key(o.Q4_K), layout=1), bucket, n_out, k, wl, x, step)
+    a = min(active, bucket)
+    want = o.gemv(o.Q4_K, w, n_out, k, x[:a], a, threads=8) if a else None
     check_rows(got, want, active, "x8")
 
 
