@@ -151,10 +151,15 @@ namespace {
 int q4k_dense_rows(const char* W, int x8, const void* w, uint32_t n_out, uint32_t k_in, const float* x,
                    uint32_t rows, float* y, void* ws, void* stream, const uint32_t* active) {
     if (x8 && syn::gemv_q4k_x8_rows_pick((int)n_out, (int)k_in, (int)rows)) {  // the one-row kernel's loads
+        if (syn::gemv_q4k_x8_rows_fused((int)k_in, (int)rows)) {  // one launch: the rows quantized in its workgroups
+            syn::launch_gemv_q4k_x8_rows((const uint8_t*)w, (int)n_out, (int)k_in, nullptr, x, (int)rows, y,
+                                         (hipStream_t)stream, active);
+            return check_launch(W);
+        }
         syn::launch_act_quant(syn::ACT_Q8K, x, rows, k_in, (uint8_t*)ws, (hipStream_t)stream);
         if (int rc = check_launch(W)) return rc;
-        syn::launch_gemv_q4k_x8_rows((const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, (int)rows, y,
-                                     (hipStream_t)stream, active);
+        syn::launch_gemv_q4k_x8_rows((const uint8_t*)w, (int)n_out, (int)k_in, (const uint8_t*)ws, nullptr, (int)rows,
+                                     y, (hipStream_t)stream, active);
         return check_launch(W);
     }
     const syn::MoeAct a = syn::moe_act_at((uint8_t*)ws, rows, (int)k_in);

@@ -508,14 +508,19 @@ void launch_gate_up_q4k_f32(const uint8_t* W, int n, int k, const float* x, floa
 // lane, with the NR activation rows (Q8_K, quantized beforehand) side by side in LDS, so the
 // weights stream once and each lane computes its block's term against every row; each row's
 // terms are folded in block order by the row's first lane, as at one row.  Rows of up to 64
-// super-blocks; rows past the step's active rows are neither computed nor written.
+// super-blocks; rows past the step's active rows are neither computed nor written.  FUSE = 1
+// (two rows of at most 16 super-blocks): the workgroup quantizes the F32 rows to Q8_K in LDS
+// itself, as the one-row kernel does, the rows' loads issued before the block's: one launch
+// (14336 x 4096: 10.2 against 10.7 us; 4096 x 4096: 6.4 against 7.8 us; at three rows the
+// separate quantization is the faster, 12.3 against 12.6 us).
 constexpr int XR_WAVES = 8;
 
 SYN_HD inline size_t xr_row_lds(int nb) { return align_up(q4k_dec_lds(nb) + 16, 16); }  // + the scales' 16-byte tail
 
-template <int NR>
+template <int NR, int FUSE>
 __global__ __launch_bounds__(64 * XR_WAVES) void k_gemv_q4k_x8_rows(const uint8_t* __restrict__ W, int n_out, int nb,
                                                                   const uint8_t* __restrict__ ws, int rows_ws, int rows,
+                                                                  const float* __restrict__ x,
                                                                   float* __restrict__ y,
                                                                   const uint32_t* __restrict__ active) {
     rows = active_rows(active, 0, rows);
@@ -527,13 +532,26 @@ __global__ __launch_bounds__(64 * XR_WAVES) void k_gemv_q4k_x8_rows(const uint8_
     const int b = lane % P;
     const bool ok = row < n_out && b < nb;
     const int RB = (int)xr_row_lds(nb);
+    // FUSE: 16-value pieces of the rows (task = row * 16 nb + piece), loaded unconditionally (a
+    // task past the last re-reads it, unused) before the block's loads
+    constexpr int PIECES = FUSE ? (NR * 256 + 64 * XR_WAVES - 1) / (64 * XR_WAVES) : 1;
+    float xv[PIECES][16];
+    if constexpr (FUSE) {
+        const int ntask = NR * nb * 16;
+#pragma unroll
+        for (int i = 0; i < PIECES; ++i) {
+            const int tk0 = (int)threadIdx.x + i * 64 * XR_WAVES, tk = tk0 < ntask ? tk0 : ntask - 1;
+            const int r = tk / (nb * 16);
+            load_block16(x + (int64_t)r * nb * 256, tk - r * nb * 16, xv[i]);
+        }
+    }
     // the activation rows stream into LDS first (as the one-row kernel's), then the block
     const ActLayout L = act_layout(ACT_Q8K, (uint64_t)rows_ws, (uint64_t)nb * 256);
     const uint32_t l0 = lds_addr(lds);
     const int wv = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        if (r >= rows) break;  // uniform
+        if (FUSE || r >= rows) break;  // uniform
         const uint8_t* codes = ws + L.codes + (size_t)r * nb * 256;
         const uint32_t lr = l0 + (uint32_t)(r * RB);
         for (int c = wv; c < nb; c += XR_WAVES)
@@ -556,8 +574,17 @@ __global__ __launch_bounds__(64 * XR_WAVES) void k_gemv_q4k_x8_rows(const uint8_
 #pragma unroll
         for (int i = 0; i < 9; ++i) A[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(src + step * i));
     }
-    wait_vm<9>();  // this wavefront's row loads, all older than the block's nine
-    lds_barrier();
+    if constexpr (FUSE) {
+#pragma unroll
+        for (int i = 0; i < PIECES; ++i) {
+            const int tk = (int)threadIdx.x + i * 64 * XR_WAVES, r = tk / (nb * 16);
+            if (r < NR && r < rows) quant16_to_lds(xv[i], tk - r * nb * 16, nb, lds + r * RB);  // 16-lane groups stay whole
+        }
+        lds_barrier();
+    } else {
+        wait_vm<9>();  // this wavefront's row loads, all older than the block's nine
+        lds_barrier();
+    }
     float* terms = reinterpret_cast<float*>(lds + (size_t)NR * RB) + wave * 64;
     float t[NR];
 #pragma unroll
@@ -594,24 +621,29 @@ bool gemv_q4k_x8_rows_pick(int n_out, int k, int rows) {
     return rows == 2 || (rows == 3 && nb <= 16 && (n_out + 31) / 32 >= 256);
 }
 
-void launch_gemv_q4k_x8_rows(const uint8_t* W, int n_out, int k, const uint8_t* ws, int rows, float* y,
-                             hipStream_t stream, const uint32_t* active) {
+bool gemv_q4k_x8_rows_fused(int k, int rows) { return rows == 2 && k % 256 == 0 && k > 0 && k <= 16 * 256; }
+
+void launch_gemv_q4k_x8_rows(const uint8_t* W, int n_out, int k, const uint8_t* ws, const float* x, int rows,
+                             float* y, hipStream_t stream, const uint32_t* active) {
     const int nb = k / 256;
     const int rows_per_wg = XR_WAVES * (64 / (nb <= 16 ? 16 : nb <= 32 ? 32 : 64));
     const dim3 grid((unsigned)((n_out + rows_per_wg - 1) / rows_per_wg));
-#define SYN_XR(NR)                                                                                          \
+#define SYN_XR(NR, FUSE)                                                                                    \
     do {                                                                                                     \
         const size_t lds = (size_t)NR * xr_row_lds(nb) + (size_t)NR * XR_WAVES * 64 * 4;                     \
-        static const hipError_t lds_ok = hipFuncSetAttribute((const void*)k_gemv_q4k_x8_rows<NR>,             \
+        static const hipError_t lds_ok = hipFuncSetAttribute((const void*)k_gemv_q4k_x8_rows<NR, FUSE>,       \
                                                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024); \
         (void)lds_ok; /* a refusal shows as the launch's error */                                            \
-        hipLaunchKernelGGL((k_gemv_q4k_x8_rows<NR>), grid, dim3(64 * XR_WAVES), lds, stream, W, n_out, nb, ws, rows, \
-                           rows, y, active);                                                                 \
+        hipLaunchKernelGGL((k_gemv_q4k_x8_rows<NR, FUSE>), grid, dim3(64 * XR_WAVES), lds, stream, W, n_out, nb, ws, \
+                           rows, rows, x, y, active);                                                        \
     } while (0)
-    if (rows <= 2)
-        SYN_XR(2);
-    else
-        SYN_XR(3);
+    if (x) {  // two rows quantized in the workgroups (gemv_q4k_x8_rows_fused)
+        SYN_XR(2, 1);
+    } else if (rows <= 2) {
+        SYN_XR(2, 0);
+    } else {
+        SYN_XR(3, 0);
+    }
 #undef SYN_XR
 }
 

@@ -19,8 +19,11 @@ bool q4k_dec_supported(int k);
 // Q4_K at 2 or 3 rows over X8 weights, where gemv_q4k_x8_rows_pick finds it the faster form, on
 // Q8_K rows quantized by launch_act_quant
 bool gemv_q4k_x8_rows_pick(int n_out, int k, int rows);
-void launch_gemv_q4k_x8_rows(const uint8_t* W, int n_out, int k, const uint8_t* ws, int rows, float* y,
-                             hipStream_t stream, const uint32_t* active);
+// with x (F32 rows, not ws) where gemv_q4k_x8_rows_fused(k, rows): the rows quantized in the
+// workgroups
+bool gemv_q4k_x8_rows_fused(int k, int rows);
+void launch_gemv_q4k_x8_rows(const uint8_t* W, int n_out, int k, const uint8_t* ws, const float* x, int rows,
+                             float* y, hipStream_t stream, const uint32_t* active);
 void launch_gemv_q4k_dec_f32(const uint8_t* W, int n_out, int k, const float* x, float* y,
                              hipStream_t stream, const uint32_t* active = nullptr);
 void launch_gemv_q4k_dec_ws(const uint8_t* W, int n_out, int k, const uint8_t* ws, float* y,
