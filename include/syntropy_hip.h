@@ -258,6 +258,17 @@ int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, const void*
 int syn_moe_combine(const float* out, const int32_t* ids, const float* w, uint32_t rows,
                     uint32_t top_k, uint32_t hidden, float* y, void* stream);
 
+/* MoeCombine as the graph binds it: inputs [per_expert, weights, shared...], dims [top_k,
+ * n_shared, hidden] (crates/kernels/src/op/kind.rs:244; crates/graph/src/ir/signature.rs:153;
+ * crates/graph/src/blocks/ffn.rs:189-200).  The binding carries no expert ids, so the slots of
+ * out F32 [rows, top_k, hidden] are added in rank order (slot j = rank j, the order MoeRoute
+ * writes; plan/rfcs/RFC-0042-quantization-and-numerical-fidelity.md:233), then each of the
+ * n_shared <= 8 shared outputs F32 [rows, hidden] (shared: a host array of device pointers):
+ * y = 0.0, y += w_j * v_j, y += shared_s, in F32 without fused multiply-add. */
+int syn_moe_combine_ranked(const float* out, const float* w, uint32_t n_shared,
+                           const float* const* shared, uint32_t rows, uint32_t top_k, uint32_t hidden,
+                           float* y, void* stream);
+
 /* ---- MoE residency split --------------------------------------------------------------------
  * The doorbell layer a router op writes and the split rule every site evaluates from it
  * (plan/rfcs/RFC-0040-kernel-providers-and-backends.md:380-403; RFC-0023 sections 2 and 6).

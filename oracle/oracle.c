@@ -28,8 +28,9 @@
  *   or_logits        or_rms_norm and or_gemv composed; rows whose norm is an exact halving pin
  *                    that the norm comes first and that g scales its own column
  *   or_moe_*         packing against brute force; MoE slot = expert FFN of the row alone
- *                    (moe/tests.rs:315); combine against its definition; route ids against a
- *                    brute-force sort.  MoeRoute and MoeCombine have no reference code: their
+ *                    (moe/tests.rs:315); combine against its definition; the rank-order
+ *                    combine equal to it on rows whose ids ascend, and on order-sensitive hand
+ *                    cases; route ids against a brute-force sort.  MoeRoute and MoeCombine have no reference code: their
  *                    values are pinned by the specification and invariants only.
  *   or_moe_assign    the reference's generated split rule (moe_assign.h), compiled into
  *                    oracle/_ref, on 10^6 generated inputs; the hand-worked cases of
@@ -1212,6 +1213,35 @@ int or_moe_combine(const float* out, const int32_t* ids, const float* w, size_t 
             const float* slot = out + (r * top_k + j) * hidden;
             float wj = w[r * top_k + j];
             for (size_t i = 0; i < hidden; ++i) yr[i] += wj * slot[i];
+        }
+    }
+    return 0;
+}
+
+/* ===================================================================================== */
+/* MoeCombine as the IR binds it: inputs [per_expert, weights, shared...], dims            */
+/* [top_k, n_shared, hidden] (crates/kernels/src/op/kind.rs:244;                           */
+/* crates/graph/src/ir/signature.rs:153; crates/graph/src/blocks/ffn.rs:189-200).  The      */
+/* binding carries no expert ids, so the routed slots are added in rank order, as          */
+/* plan/rfcs/RFC-0042-quantization-and-numerical-fidelity.md:233 states (slot j = rank j),  */
+/* then the shared experts' outputs in input order (RFC-0040 ...md:296): y = 0.0,          */
+/* y += w_j * v_j (product rounded, then the sum), y += shared_s, in F32, no FMA.          */
+/* shared: n_shared arrays of [rows, hidden], contiguous ([n_shared][rows][hidden]).        */
+/* ===================================================================================== */
+
+int or_moe_combine_ranked(const float* out, const float* w, const float* shared, size_t n_shared,
+                          size_t rows, size_t top_k, size_t hidden, float* y) {
+    for (size_t r = 0; r < rows; ++r) {
+        float* yr = y + r * hidden;
+        for (size_t i = 0; i < hidden; ++i) yr[i] = 0.0f;
+        for (size_t j = 0; j < top_k; ++j) {
+            const float* slot = out + (r * top_k + j) * hidden;
+            const float wj = w[r * top_k + j];
+            for (size_t i = 0; i < hidden; ++i) yr[i] += wj * slot[i];
+        }
+        for (size_t s = 0; s < n_shared; ++s) {
+            const float* sh = shared + (s * rows + r) * hidden;
+            for (size_t i = 0; i < hidden; ++i) yr[i] += sh[i];
         }
     }
     return 0;

@@ -113,6 +113,11 @@ int or_moe_route(const float* router, const float* x, size_t rows, size_t hidden
 /* ---- MoeCombine (crates/kernels-cpu/src/moe/tests.rs:541-556) ---- */
 int or_moe_combine(const float* out, const int32_t* ids, const float* w, size_t rows,
                    size_t top_k, size_t hidden, float* y);
+/* ---- MoeCombine as the IR binds it (crates/kernels/src/op/kind.rs:244;
+ * crates/graph/src/ir/signature.rs:153): slots in rank order, then the shared experts'
+ * outputs ([n_shared][rows][hidden]); RFC-0042 ...md:233 ---- */
+int or_moe_combine_ranked(const float* out, const float* w, const float* shared, size_t n_shared,
+                          size_t rows, size_t top_k, size_t hidden, float* y);
 
 /* ---- The residency split: doorbell layer and split rule
  * (crates/kernels/include/syntropy/moe_doorbell.h, moe_assign.h; RFC-0040 ...md:380-403) ---- */

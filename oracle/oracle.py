@@ -85,6 +85,7 @@ def lib():
         L.or_moe_grouped.argtypes = [i32, i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, vp, i32]
         L.or_moe_route.argtypes = [vp, vp, sz, sz, sz, sz, i32, vp, vp, vp]
         L.or_moe_combine.argtypes = [vp, vp, vp, sz, sz, sz, vp]
+        L.or_moe_combine_ranked.argtypes = [vp, vp, vp, sz, sz, sz, sz, vp]
         L.or_moe_assign.argtypes = [vp, C.c_uint32, vp, C.c_uint32, C.c_uint32, u64, C.c_uint32, vp]
         L.or_moe_assign.restype = None
         L.or_moe_doorbell.argtypes = [vp, sz, sz, C.c_uint32, vp, C.c_uint32, C.c_uint32, vp]
@@ -325,6 +326,18 @@ def moe_combine(out, ids, w) -> np.ndarray:
     rows, top_k, hidden = out.shape
     y = np.zeros((rows, hidden), dtype=np.float32)
     assert lib().or_moe_combine(_p(out), _p(ids), _p(w), rows, top_k, hidden, _p(y)) == 0
+    return y
+
+
+def moe_combine_ranked(out, w, shared=()) -> np.ndarray:
+    """MoeCombine as the IR binds it: slots in rank order, then each shared output [rows, hidden]."""
+    out, w = _f32(out), _f32(w)
+    rows, top_k, hidden = out.shape
+    sh = np.ascontiguousarray(np.stack([_f32(a).reshape(rows, hidden) for a in shared])) if len(shared) \
+        else np.zeros((0, rows, hidden), np.float32)
+    y = np.zeros((rows, hidden), dtype=np.float32)
+    assert lib().or_moe_combine_ranked(_p(out), _p(w), _p(sh) if len(shared) else None, len(shared), rows,
+                                       top_k, hidden, _p(y)) == 0
     return y
 
 

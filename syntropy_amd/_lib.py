@@ -75,6 +75,7 @@ def lib():
         "syn_moe_assign_layer": [vp, u32, vp, u32, vp, u64, u32, vp, vp],
         "syn_moe_site_mask": [vp, u32, vp, u32, i32, vp, vp],
         "syn_moe_combine": [vp, vp, vp, u32, u32, u32, vp, vp],
+        "syn_moe_combine_ranked": [vp, vp, u32, vp, u32, u32, u32, vp, vp],
     }
     for name, args in sigs.items():
         f = getattr(L, name)

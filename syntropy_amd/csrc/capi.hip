@@ -35,6 +35,23 @@ int check_launch(const char* what) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+// The weight view of a matrix of need_w bytes (nblocks blocks) in `layout`.  A SOURCE view may run
+// past the matrix.  The repacks are shape-free and place bytes by the total length they were
+// given (SPLIT's scale section starts after every block's codes; X8's final run of fewer than 8
+// super-blocks has its own stride), so a repacked view must be the repack of this matrix alone:
+// exactly need_w bytes for SPLIT, and for X8 when the block count is not a multiple of 8.
+int check_view(const char* W, uint32_t layout, uint64_t w_bytes, uint64_t need_w, uint64_t nblocks) {
+    if (w_bytes < need_w)
+        return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
+                    (unsigned long long)w_bytes, (unsigned long long)need_w);
+    const bool exact = layout == SYN_LAYOUT_SPLIT || (layout == SYN_LAYOUT_X8 && nblocks % 8 != 0);
+    if (exact && w_bytes != need_w)
+        return fail(SYN_E_INVALID,
+                    "%s: a layout-%u weight view must be the repack of the matrix alone: %llu bytes, not %llu", W,
+                    layout, (unsigned long long)need_w, (unsigned long long)w_bytes);
+    return SYN_OK;
+}
+
 bool gemv_type(int32_t t) { return t == SYN_Q4_0 || t == SYN_Q8_0 || t == SYN_Q4_K; }
 bool float_type(int32_t t) { return t == SYN_F16 || t == SYN_BF16; }
 
@@ -297,7 +314,7 @@ SYN_EXPORT int syn_gemv_batch_workspace_bytes(uint32_t n, const uint32_t* k_in, 
 namespace {
 
 // Shared checks of the grouped entry points: problem i's quantized row sits at ws + off[i].
-int batch_setup(const char* W, uint32_t n, const int32_t* wtypes, const void* const* w,
+int batch_setup(const char* W, uint32_t layout, uint32_t n, const int32_t* wtypes, const void* const* w,
                 const uint64_t* w_bytes, const uint32_t* n_out, const uint32_t* k_in, void* ws,
                 uint64_t ws_bytes, uint64_t* off) {
     if (n > SYN_BATCH) return fail(SYN_E_UNSUPPORTED, "%s: at most %d problems", W, SYN_BATCH);
@@ -315,7 +332,7 @@ int batch_setup(const char* W, uint32_t n, const int32_t* wtypes, const void* co
             if (wtypes[i] != SYN_Q4_K) return fail(SYN_E_UNSUPPORTED, "%s: problem %u is not Q4_K", W, i);
             if (n_out[i] == 0 || n_out[i] > (1u << 28)) return fail(SYN_E_INVALID, "%s: n_out[%u] = %u", W, i, n_out[i]);
             const uint64_t need_w = (uint64_t)k_in[i] / 256 * 144 * n_out[i];
-            if (w_bytes[i] < need_w) return fail(SYN_E_INVALID, "%s: weight %u holds %llu bytes, the matrix %llu", W, i, (unsigned long long)w_bytes[i], (unsigned long long)need_w);
+            if (int rc = check_view(W, layout, w_bytes[i], need_w, need_w / 144)) return rc;
             if (!w[i] || !aligned(w[i], 16)) return fail(SYN_E_INVALID, "%s: problem %u: W must be a 16-byte aligned pointer", W, i);
         }
         off[i] = o;
@@ -368,7 +385,7 @@ SYN_EXPORT int syn_act_quantize_batch(uint32_t n, const uint32_t* k_in, const fl
     if (n == 0) return SYN_OK;
     if (!x) return fail(SYN_E_INVALID, "%s: null argument array", W);
     uint64_t off[SYN_BATCH];
-    if (int rc = batch_setup(W, n, nullptr, nullptr, nullptr, nullptr, k_in, ws, ws_bytes, off)) return rc;
+    if (int rc = batch_setup(W, SYN_LAYOUT_SOURCE, n, nullptr, nullptr, nullptr, nullptr, k_in, ws, ws_bytes, off)) return rc;
     return batch_quantize(W, n, k_in, x, (uint8_t*)ws, off, (hipStream_t)stream);
 }
 
@@ -380,7 +397,7 @@ SYN_EXPORT int syn_gemv_batch_quantized_layout(uint32_t layout, uint32_t n, cons
     if (n == 0) return SYN_OK;
     if (!w || !y) return fail(SYN_E_INVALID, "%s: null argument array", W);
     uint64_t off[SYN_BATCH];
-    if (int rc = batch_setup(W, n, wtypes, w, w_bytes, n_out, k_in, (void*)ws, ws_bytes, off)) return rc;
+    if (int rc = batch_setup(W, layout, n, wtypes, w, w_bytes, n_out, k_in, (void*)ws, ws_bytes, off)) return rc;
     return batch_gemv(W, (int)layout, n, w, n_out, k_in, (const uint8_t*)ws, off, y, (hipStream_t)stream);
 }
 
@@ -407,7 +424,7 @@ int gemv_batch_f32(const char* W, uint32_t layout, uint32_t n, const int32_t* wt
     if (layout != SYN_LAYOUT_SOURCE && layout != SYN_LAYOUT_X8)
         return fail(SYN_E_UNSUPPORTED, "%s: weight layout %u", W, layout);
     uint64_t off[SYN_BATCH];
-    if (int rc = batch_setup(W, n, wtypes, w, w_bytes, n_out, k_in, ws, ws_bytes, off)) return rc;
+    if (int rc = batch_setup(W, layout, n, wtypes, w, w_bytes, n_out, k_in, ws, ws_bytes, off)) return rc;
     if (!fuse || layout != SYN_LAYOUT_X8) {
         if (int rc = batch_quantize(W, n, k_in, x, (uint8_t*)ws, off, (hipStream_t)stream)) return rc;
         return batch_gemv(W, (int)layout, n, w, n_out, k_in, (const uint8_t*)ws, off, y, (hipStream_t)stream);
@@ -618,9 +635,7 @@ int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
     if (layout == SYN_LAYOUT_SPLIT) {
         const uint64_t need_w = (uint64_t)n_out * (k_in / 32) * (syn::split_code_bytes(wtype) + 2);
         if (!w || !y || (k_in && (!x || !ws))) return fail(SYN_E_INVALID, "%s: null operand", W);
-        if (w_bytes < need_w)
-            return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
-                        (unsigned long long)w_bytes, (unsigned long long)need_w);
+        if (int rc = check_view(W, layout, w_bytes, need_w, (uint64_t)n_out * (k_in / 32))) return rc;
         if (ws_bytes < need)
             return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
                         (unsigned long long)ws_bytes, (unsigned long long)need);
@@ -653,9 +668,7 @@ int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
     if (q4k_dense(wtype, rows, k_in)) {
         const uint64_t need_w = (uint64_t)n_out * (k_in / 256) * 144;
         if (!w || !x || !ws || !y) return fail(SYN_E_INVALID, "%s: null operand", W);
-        if (w_bytes < need_w)
-            return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
-                        (unsigned long long)w_bytes, (unsigned long long)need_w);
+        if (int rc = check_view(W, layout, w_bytes, need_w, need_w / 144)) return rc;
         if (ws_bytes < need)
             return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
                         (unsigned long long)ws_bytes, (unsigned long long)need);
@@ -667,9 +680,7 @@ int syn_gemv_layout_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
         return fail(SYN_E_UNSUPPORTED, "%s: a %u x %u matrix is larger than 4 GiB", W, n_out, k_in);
     const uint64_t need_w = (uint64_t)n_out * (k_in / 256) * 144;
     if (!w || !x || !ws || !y) return fail(SYN_E_INVALID, "%s: null operand", W);
-    if (w_bytes < need_w)
-        return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
-                    (unsigned long long)w_bytes, (unsigned long long)need_w);
+    if (int rc = check_view(W, layout, w_bytes, need_w, need_w / 144)) return rc;
     if (ws_bytes < need)
         return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
                     (unsigned long long)ws_bytes, (unsigned long long)need);
@@ -704,9 +715,7 @@ SYN_EXPORT int syn_gemv_quantized_layout(uint32_t layout, int32_t wtype, const v
     if (rows == 0 || n_out == 0) return SYN_OK;
     const uint64_t need_w = (uint64_t)n_out * (k_in / 32) * (syn::split_code_bytes(wtype) + 2);
     if (!w || !y || (k_in && !ws)) return fail(SYN_E_INVALID, "%s: null operand", W);
-    if (w_bytes < need_w)
-        return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
-                    (unsigned long long)w_bytes, (unsigned long long)need_w);
+    if (int rc = check_view(W, layout, w_bytes, need_w, (uint64_t)n_out * (k_in / 32))) return rc;
     if (ws_bytes < need)
         return fail(SYN_E_WORKSPACE, "%s: the workspace holds %llu bytes, the call needs %llu", W,
                     (unsigned long long)ws_bytes, (unsigned long long)need);
@@ -802,9 +811,7 @@ int syn_gate_up_act_rows(uint32_t layout, int32_t wtype, const void* w, uint64_t
         // one launch: the row quantized in every workgroup, gate and up rows side by side, silu(g) u
         const uint64_t need_w = 2ull * n_out * (k_in / 256) * 144;
         if (!w || !x) return fail(SYN_E_INVALID, "%s: null operand", W);
-        if (w_bytes < need_w)
-            return fail(SYN_E_INVALID, "%s: the weight view holds %llu bytes, the matrix %llu", W,
-                        (unsigned long long)w_bytes, (unsigned long long)need_w);
+        if (int rc = check_view(W, layout, w_bytes, need_w, need_w / 144)) return rc;
         if (!aligned(w, 16) || !aligned(x, 16)) return fail(SYN_E_INVALID, "%s: w and x must be 16-byte aligned", W);
         syn::launch_gate_up_q4k_f32((const uint8_t*)w, (int)n_out, (int)k_in, x, y, (hipStream_t)stream, active);
         return check_launch(W);
@@ -1223,6 +1230,31 @@ int syn_moe_combine_rows(const float* out, const int32_t* ids, const float* w, u
 SYN_EXPORT int syn_moe_combine(const float* out, const int32_t* ids, const float* w, uint32_t rows,
                                uint32_t top_k, uint32_t hidden, float* y, void* stream) {
     return syn_moe_combine_rows(out, ids, w, rows, top_k, hidden, y, stream, nullptr);
+}
+
+int syn_moe_combine_ranked_rows(const float* out, const float* w, uint32_t n_shared, const float* const* shared,
+                                uint32_t rows, uint32_t top_k, uint32_t hidden, float* y, void* stream,
+                                const uint32_t* active) {
+    const char* W = "syn_moe_combine_ranked";
+    if (top_k == 0 || top_k > 64) return fail(SYN_E_UNSUPPORTED, "%s: top_k %u (1..64)", W, top_k);
+    if (n_shared > (uint32_t)syn::MAX_SHARED)
+        return fail(SYN_E_UNSUPPORTED, "%s: %u shared experts (at most %d)", W, n_shared, syn::MAX_SHARED);
+    if (rows == 0 || hidden == 0) return SYN_OK;
+    if (!out || !w || !y || (n_shared && !shared)) return fail(SYN_E_INVALID, "%s: null operand", W);
+    syn::SharedOuts sh{};
+    sh.n = (int)n_shared;
+    for (uint32_t i = 0; i < n_shared; ++i) {
+        if (!shared[i]) return fail(SYN_E_INVALID, "%s: null shared output %u", W, i);
+        sh.p[i] = shared[i];
+    }
+    syn::launch_moe_combine_ranked(out, w, sh, (int)rows, (int)top_k, (int)hidden, y, (hipStream_t)stream, active);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_moe_combine_ranked(const float* out, const float* w, uint32_t n_shared,
+                                      const float* const* shared, uint32_t rows, uint32_t top_k, uint32_t hidden,
+                                      float* y, void* stream) {
+    return syn_moe_combine_ranked_rows(out, w, n_shared, shared, rows, top_k, hidden, y, stream, nullptr);
 }
 
 // ============================================================================================

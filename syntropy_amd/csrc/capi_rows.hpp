@@ -29,3 +29,6 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
                          uint32_t* report = nullptr);
 int syn_moe_combine_rows(const float* out, const int32_t* ids, const float* w, uint32_t rows, uint32_t top_k,
                          uint32_t hidden, float* y, void* stream, const uint32_t* active);
+int syn_moe_combine_ranked_rows(const float* out, const float* w, uint32_t n_shared, const float* const* shared,
+                                uint32_t rows, uint32_t top_k, uint32_t hidden, float* y, void* stream,
+                                const uint32_t* active);

@@ -113,6 +113,14 @@ void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
                      const uint32_t* err, float* out, hipStream_t stream);
 void launch_moe_combine(const float* out, const int32_t* ids, const float* w, int rows, int top_k,
                         int hidden, float* y, hipStream_t stream, const uint32_t* active = nullptr);
+// The shared experts' outputs MoeCombine adds after the routed slots, [rows, hidden] each.
+constexpr int MAX_SHARED = 8;
+struct SharedOuts {
+    const float* p[MAX_SHARED];
+    int n;
+};
+void launch_moe_combine_ranked(const float* out, const float* w, const SharedOuts& sh, int rows, int top_k,
+                               int hidden, float* y, hipStream_t stream, const uint32_t* active = nullptr);
 // moe_split.hip: the residency split (doorbell layer, split rule, site masks)
 void launch_moe_assign(const uint8_t* route, uint32_t n_route, const uint32_t* eligible, uint32_t n_experts,
                        uint32_t b_copy, uint64_t expert_bytes, uint32_t copy_slots, uint32_t* out,

@@ -1472,4 +1472,61 @@ void launch_moe_combine(const float* out, const int32_t* ids, const float* w, in
                        dim3(256), 0, stream, out, ids, w, top_k, hidden, vec, y, active);
 }
 
+// MoeCombine as the IR binds it (crates/kernels/src/op/kind.rs:244, crates/graph/src/ir/
+// signature.rs:153): per row, the routed slots in rank order (slot j is rank j; the binding carries
+// no expert ids), then the shared experts' outputs in input order, y = 0.0, y += w_j * v_j, y +=
+// shared_s, in F32 without fused multiply-add.  One workgroup per (row, 1024 columns), four
+// columns a thread.
+__global__ __launch_bounds__(256) void k_moe_combine_ranked(const float* __restrict__ out,
+                                                            const float* __restrict__ w, SharedOuts sh,
+                                                            int top_k, int hidden, int vec,
+                                                            float* __restrict__ y,
+                                                            const uint32_t* __restrict__ active) {
+    __shared__ float sw[64];
+    const int r = blockIdx.y, tid = threadIdx.x;
+    if (r >= active_rows(active, 0, (int)gridDim.y)) return;  // uniform: a row past the active ones
+    if (tid < top_k) sw[tid] = w[(int64_t)r * top_k + tid];
+    __syncthreads();
+    const int c = blockIdx.x * 1024 + 4 * tid;
+    if (c >= hidden) return;
+    const float* base = out + (int64_t)r * top_k * hidden;
+    if (vec) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int j = 0; j < top_k; ++j) {
+            const float wj = sw[j];
+            const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)j * hidden + c);
+            acc.x = acc.x + wj * v.x;
+            acc.y = acc.y + wj * v.y;
+            acc.z = acc.z + wj * v.z;
+            acc.w = acc.w + wj * v.w;
+        }
+        for (int s2 = 0; s2 < sh.n; ++s2) {
+            const float4 v = *reinterpret_cast<const float4*>(sh.p[s2] + (int64_t)r * hidden + c);
+            acc.x = acc.x + v.x;
+            acc.y = acc.y + v.y;
+            acc.z = acc.z + v.z;
+            acc.w = acc.w + v.w;
+        }
+        *reinterpret_cast<float4*>(y + (int64_t)r * hidden + c) = acc;
+    } else {
+        const int n = hidden - c < 4 ? hidden - c : 4;
+        for (int q = 0; q < n; ++q) {
+            float acc = 0.0f;
+            for (int j = 0; j < top_k; ++j) acc = acc + sw[j] * base[(int64_t)j * hidden + c + q];
+            for (int s2 = 0; s2 < sh.n; ++s2) acc = acc + sh.p[s2][(int64_t)r * hidden + c + q];
+            y[(int64_t)r * hidden + c + q] = acc;
+        }
+    }
+}
+
+void launch_moe_combine_ranked(const float* out, const float* w, const SharedOuts& sh, int rows, int top_k,
+                               int hidden, float* y, hipStream_t stream, const uint32_t* active) {
+    if (rows == 0 || hidden == 0) return;
+    uintptr_t align = reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(y);
+    for (int i = 0; i < sh.n; ++i) align |= reinterpret_cast<uintptr_t>(sh.p[i]);
+    const int vec = hidden % 4 == 0 && align % 16 == 0;
+    hipLaunchKernelGGL(k_moe_combine_ranked, dim3((unsigned)((hidden + 1023) / 1024), (unsigned)rows),
+                       dim3(256), 0, stream, out, w, sh, top_k, hidden, vec, y, active);
+}
+
 }  // namespace syn

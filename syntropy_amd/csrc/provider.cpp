@@ -494,10 +494,11 @@ bool plan_of(const Key& k, const Shape& s, Plan& p) {
         return true;
     }
     case Op::MoeCombine: {
-        // dims [top_k, hidden]
-        if (k.weight != -1 || s.dims.size() != 2 || s.dims[0] == 0 || s.dims[0] > 64) return false;
-        p.dims[0] = s.dims[0];
-        p.dims[1] = s.dims[1];
+        // dims [top_k, n_shared, hidden] (crates/kernels/src/op/kind.rs:244)
+        if (k.weight != -1 || s.dims.size() != 3) return false;
+        const uint32_t top_k = s.dims[0], n_shared = s.dims[1], hidden = s.dims[2];
+        if (top_k == 0 || top_k > 64 || n_shared > 8 || hidden == 0) return false;
+        for (int i = 0; i < 3; ++i) p.dims[i] = s.dims[i];
         p.workspace = 0;
         return true;
     }
@@ -561,14 +562,18 @@ struct Buf {
     uint64_t bytes;
     uint32_t kind;
     uint32_t first_page;  // HostMapped: the number of its first doorbell page
+    uint32_t numbered;    // HostMapped: how many of its pages carry numbers (0: none)
 };
 
 // Doorbell flags (RFC-0040 ...md:545-547 and its 2026-11-07 revision at :594): a HostFlag
 // {page, slot} names the 4-byte word `slot` of a 4 KiB page of the tier manager's HostMapped
 // buffers.  Their pages are numbered in allocation order on the context, from 0, and a number
 // is never reused, as the CUDA provider numbers them (crates/kernels-cuda/src/memory.rs:44-49,
-// 544-583).  A HostMapped buffer is pinned, mapped and coherent host memory whose device
-// address is its host address (ROCm's unified addressing, checked at alloc).
+// 544-583): a buffer of n bytes takes ceil(n / 4096) numbers (none for 0 bytes); a buffer whose
+// pages would pass number 65535 is still allocated, with no numbers (its words hold no flags),
+// and does not advance the count.  A HostMapped buffer is pinned, mapped and coherent host
+// memory whose device address is its host address (ROCm's unified addressing, checked at
+// alloc).
 constexpr uint64_t DOORBELL_PAGE = 4096;
 constexpr uint32_t MAX_DOORBELL_PAGES = 1u << 16;
 constexpr uint64_t DEFAULT_SPIN_US = 2000000;
@@ -775,21 +780,24 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         // GateUpAct's weight stacks the gate rows, then the up rows
         const uint64_t wbytes = (uint64_t)k_in / be * bb * n_out * (gated ? 2 : 1);
         const SynBufferView& w = weight(a, 0, wbytes, name);
+        // the view's own length: a repacked view must be the repack of this matrix alone
+        // (checked by the entry points), a SOURCE view may run past it
+        const uint64_t wlen = w.len;
         uint8_t* ws = workspace_of(c, a, p);
         if (normed) {
             const SynBufferView& g = weight(a, 1, 4ull * k_in, "Logits norm");
             float eps;
             std::memcpy(&eps, &a.statics[0].bits, 4);
-            check_syn(syn_logits_rows(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in,
+            check_syn(syn_logits_rows(p.layout, p.weight, (const void*)w.addr, wlen, n_out, k_in,
                                       (const float*)g.addr, eps, (const float*)x, rows, (float*)y, ws,
                                       p.workspace - 256, st, active),
                       name);
         } else if (gated)
-            check_syn(syn_gate_up_act_rows(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in,
+            check_syn(syn_gate_up_act_rows(p.layout, p.weight, (const void*)w.addr, wlen, n_out, k_in,
                                            (const float*)x, rows, (float*)y, ws, p.workspace - 256, st, active),
                       name);
         else
-            check_syn(syn_gemv_layout_rows(p.layout, p.weight, (const void*)w.addr, wbytes, n_out, k_in,
+            check_syn(syn_gemv_layout_rows(p.layout, p.weight, (const void*)w.addr, wlen, n_out, k_in,
                                            (const float*)x, rows, (float*)y, ws, p.workspace - 256, st, active),
                       name);
         return;
@@ -839,15 +847,21 @@ void launch_op(Ctx& c, hipStream_t st, const Plan& p, const SynOpArgs& a) {
         return;
     }
     case Op::MoeCombine: {
-        const uint32_t top_k = p.dims[0], hidden = p.dims[1];
-        if (a.n_inputs != 3 || a.n_outputs != 1)
-            internal("MoeCombine binds the per-slot outputs, their weights and ids, and one output");
+        // inputs [per_expert F32 [rows, top_k, hidden], weights F32 [rows, top_k], then each shared
+        // expert's output F32 [rows, hidden]] (crates/graph/src/ir/signature.rs:153,
+        // crates/graph/src/blocks/ffn.rs:189-200); slots added in rank order, then the shared
+        // outputs
+        const uint32_t top_k = p.dims[0], n_shared = p.dims[1], hidden = p.dims[2];
+        if (a.n_inputs != 2 + (size_t)n_shared || a.n_outputs != 1 || a.n_weights != 0 || a.n_statics != 0)
+            internal("MoeCombine binds the per-expert outputs, their weights, n_shared shared outputs and one output");
         const uint8_t* per = tensor(c, a.inputs[0], 0, rows, top_k, hidden, 4, "MoeCombine outputs");
         const uint8_t* w = tensor(c, a.inputs[1], 0, rows, top_k, 1, 4, "MoeCombine weights");
-        const uint8_t* ids = tensor(c, a.inputs[2], 7, rows, top_k, 1, 4, "MoeCombine ids");
+        const float* shared[8] = {};
+        for (uint32_t i = 0; i < n_shared; ++i)
+            shared[i] = (const float*)tensor(c, a.inputs[2 + i], 0, rows, hidden, 1, 4, "MoeCombine shared output");
         uint8_t* y = tensor(c, a.outputs[0], 0, rows, hidden, 1, 4, "MoeCombine y");
-        check_syn(syn_moe_combine_rows((const float*)per, (const int32_t*)ids, (const float*)w, rows, top_k,
-                                       hidden, (float*)y, st, active),
+        check_syn(syn_moe_combine_ranked_rows((const float*)per, (const float*)w, n_shared, shared, rows, top_k,
+                                              hidden, (float*)y, st, active),
                   "MoeCombine");
         return;
     }
@@ -1011,16 +1025,14 @@ SynStatus e_alloc(void*, uint64_t ctx, const SynAllocRequest* req, SynBuffer* ou
         if (req->kind == KIND_HOST_MAPPED && req->align > DOORBELL_PAGE)
             unsupported("alloc: HostMapped memory is aligned to 4 KiB pages");
         void* p = nullptr;
-        uint32_t first_page = 0;
+        uint32_t first_page = 0, numbered = 0;
         if (req->kind == KIND_DEVICE) {
             if (hipMalloc(&p, req->bytes ? req->bytes : 1) != hipSuccess)
                 fail(SYN_CLASS_CAPACITY, SYN_CODE_ALLOC_FAILED, "alloc: " + std::to_string(req->bytes) + " bytes");
         } else {
-            const uint64_t pages = req->bytes ? (req->bytes + DOORBELL_PAGE - 1) / DOORBELL_PAGE : 1;
-            if (c.pages.size() + pages > MAX_DOORBELL_PAGES)
-                fail(SYN_CLASS_CAPACITY, SYN_CODE_ALLOC_FAILED,
-                     "alloc: the context has numbered all 65536 doorbell pages");
-            if (hipHostMalloc(&p, pages * DOORBELL_PAGE, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+            const uint64_t pages = (req->bytes + DOORBELL_PAGE - 1) / DOORBELL_PAGE;
+            if (hipHostMalloc(&p, (pages ? pages : 1) * DOORBELL_PAGE, hipHostMallocMapped | hipHostMallocCoherent) !=
+                hipSuccess)
                 fail(SYN_CLASS_CAPACITY, SYN_CODE_ALLOC_FAILED,
                      "alloc: " + std::to_string(req->bytes) + " bytes of host-mapped memory");
             void* d = nullptr;
@@ -1028,18 +1040,21 @@ SynStatus e_alloc(void*, uint64_t ctx, const SynAllocRequest* req, SynBuffer* ou
                 (void)hipHostFree(p);
                 fail(SYN_CLASS_DEVICE, 0, "alloc: host-mapped memory whose device address is not its host address");
             }
-            std::memset(p, 0, pages * DOORBELL_PAGE);
+            std::memset(p, 0, (pages ? pages : 1) * DOORBELL_PAGE);
             first_page = (uint32_t)c.pages.size();
-            for (uint64_t i = 0; i < pages; ++i) {
-                DoorbellPage pg;
-                pg.addr = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p) + i * DOORBELL_PAGE);
-                pg.bytes = req->bytes > i * DOORBELL_PAGE ? req->bytes - i * DOORBELL_PAGE : 0;
-                pg.live = true;
-                c.pages.push_back(pg);
+            if (first_page + pages <= MAX_DOORBELL_PAGES) {  // else the buffer carries no numbers
+                numbered = (uint32_t)pages;
+                for (uint64_t i = 0; i < pages; ++i) {
+                    DoorbellPage pg;
+                    pg.addr = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p) + i * DOORBELL_PAGE);
+                    pg.bytes = req->bytes - i * DOORBELL_PAGE;
+                    pg.live = true;
+                    c.pages.push_back(pg);
+                }
             }
         }
         const uint64_t h = c.handle();
-        c.bufs[h] = Buf{p, req->bytes, req->kind, first_page};
+        c.bufs[h] = Buf{p, req->bytes, req->kind, first_page, numbered};
         SynBuffer b{};
         b.addr = reinterpret_cast<uint64_t>(p);
         b.bytes = req->bytes;
@@ -1057,8 +1072,7 @@ SynStatus e_free(void*, uint64_t ctx, const SynBuffer* buf) {
         if (it == c.bufs.end()) internal("free: unknown buffer " + std::to_string(buf->handle));
         const Buf b = it->second;
         if (b.kind == KIND_HOST_MAPPED) {  // its page numbers retire, never renaming another flag
-            const uint64_t pages = b.bytes ? (b.bytes + DOORBELL_PAGE - 1) / DOORBELL_PAGE : 1;
-            for (uint64_t i = 0; i < pages; ++i) c.pages[b.first_page + i].live = false;
+            for (uint32_t i = 0; i < b.numbered; ++i) c.pages[b.first_page + i].live = false;
             check_hip(hipHostFree(b.ptr), "hipHostFree");
         } else {
             check_hip(hipFree(b.ptr), "hipFree");

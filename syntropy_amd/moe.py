@@ -122,8 +122,27 @@ def combine(out: torch.Tensor, ids: torch.Tensor, w: torch.Tensor, y: torch.Tens
     return y
 
 
+def combine_ranked(out: torch.Tensor, w: torch.Tensor, shared=(), y: torch.Tensor | None = None,
+                   stream=None) -> torch.Tensor:
+    """MoeCombine as the graph binds it (crates/graph/src/blocks/ffn.rs:189-200): the slots of out
+    F32 [rows, top_k, hidden] in rank order, then each shared output F32 [rows, hidden]."""
+    rows, top_k, hidden = out.shape
+    if len(shared) > 8:
+        raise MoeError("at most 8 shared outputs")
+    for t in shared:
+        if t.shape != (rows, hidden) or t.dtype != torch.float32 or not t.is_contiguous():
+            raise MoeError("each shared output is contiguous F32 [rows, hidden]")
+    if y is None:
+        y = torch.empty(rows, hidden, dtype=torch.float32, device=out.device)
+    ptrs = (C.c_void_p * max(1, len(shared)))(*[t.data_ptr() for t in shared])
+    call("syn_moe_combine_ranked", out.data_ptr(), w.data_ptr(), len(shared), ptrs if shared else None, rows,
+         top_k, hidden, y.data_ptr(), _stream(stream))
+    return y
+
+
 class MoeLayer:
-    """route -> MoeGrouped -> combine for one layer, with its workspace held."""
+    """route -> MoeGrouped -> MoeCombine for one layer, as the graph binds them (the combine in
+    rank order), with its workspace held."""
 
     def __init__(self, s: MoeShape, router: torch.Tensor, experts: Experts, max_rows: int):
         self.s, self.router, self.experts = s, router, experts
@@ -137,7 +156,7 @@ class MoeLayer:
             raise MoeError(f"{rows} rows above the layer's {self.max_rows}")
         ids, w = route(self.router, x, self.s.top_k, True, stream=stream)
         out = moe_grouped(self.s, self.experts, x, ids, ws=self.ws, stream=stream)
-        return combine(out, ids, w, stream=stream), ids, w, out
+        return combine_ranked(out, w, stream=stream), ids, w, out
 
 
 # ---- the residency split (doorbell layer, split rule, site masks) ------------------------------
@@ -199,5 +218,5 @@ def site_mask(layer: torch.Tensor, max_union: int, codes: torch.Tensor, n_expert
 
 
 __all__ = ["MoeShape", "MoeError", "Experts", "route", "pack", "workspace_bytes", "moe_grouped",
-           "combine", "MoeLayer", "GemvError", "doorbell", "doorbell_bytes", "assign", "assign_layer",
+           "combine", "combine_ranked", "MoeLayer", "GemvError", "doorbell", "doorbell_bytes", "assign", "assign_layer",
            "site_mask", "HIT", "COPY", "CPU"]

@@ -26,6 +26,7 @@ DT_F32, DT_I32 = 0, 7
 # MemKind (crates/kernels/src/memory.rs:33-40); doorbell pages are 4 KiB of HostMapped buffers
 KIND_DEVICE, KIND_HOST_MAPPED = 0, 1
 DOORBELL_PAGE = 4096
+MAX_DOORBELL_PAGES = 1 << 16  # page numbers are 16 bits (HostFlag = page << 16 | slot)
 # status classes and Kernels-domain codes (RFC-0040 13)
 CLASS_DEVICE, CLASS_TIMEOUT, CLASS_INTERNAL = 6, 10, 13
 CODE_DEVICE_STICKY, CODE_DOORBELL_TIMEOUT, CODE_PROVIDER_PANICKED = 8, 11, 16
@@ -321,9 +322,12 @@ class Provider:
         self._ok("alloc", self.vt.alloc(self.vt.slf, ctx, C.byref(AllocRequest(nbytes, align, kind, 0)),
                                         C.byref(b)), ctx)
         if kind == KIND_HOST_MAPPED:  # the core numbers the doorbell pages in allocation order
-            n = self._pages.get(ctx, 0)
-            b.first_page = n
-            self._pages[ctx] = n + max(1, -(-nbytes // DOORBELL_PAGE))
+            n, pages = self._pages.get(ctx, 0), -(-nbytes // DOORBELL_PAGE)
+            if n + pages <= MAX_DOORBELL_PAGES:
+                b.first_page = n
+                self._pages[ctx] = n + pages
+            else:  # allocated with no page numbers: its words hold no flags
+                b.first_page = None
         return b
 
     def free(self, ctx: int, b: Buffer):
@@ -397,6 +401,8 @@ def host_flag(buf: Buffer, offset: int):
     """(page, slot) of the doorbell flag at byte `offset` of a HostMapped buffer, and the host's
     c_uint32 over it (the buffer's addr is also its host address)."""
     assert offset % 4 == 0 and 0 <= offset < buf.bytes
+    if buf.first_page is None:
+        raise ValueError("the buffer's pages carry no doorbell numbers")
     page = buf.first_page + offset // DOORBELL_PAGE
     slot = offset % DOORBELL_PAGE // 4
     return page, slot, u32.from_address(buf.addr + offset)

@@ -282,6 +282,38 @@ def test_pages_are_numbered_in_allocation_order(cx):
     pr.free(cx.ctx, nxt)
 
 
+def test_page_numbers_run_out_without_failing_alloc():
+    """A HostMapped buffer of n bytes takes ceil(n / 4096) page numbers, none for 0 bytes; one
+    whose pages would pass number 65535 is still allocated, with no numbers, and leaves the count
+    where it was (crates/kernels-cuda/src/memory.rs:546-559).  On a context of its own: it spends
+    every number."""
+    cx = Ctx()
+    P, pr = cx.P, cx.pr
+    empty = pr.alloc(cx.ctx, 0, kind=P.KIND_HOST_MAPPED)
+    one = pr.alloc(cx.ctx, 4096, kind=P.KIND_HOST_MAPPED)
+    assert one.first_page == empty.first_page  # the empty buffer took no number
+    nxt = one.first_page + 1
+    announce("doorbell page numbers past 65535")
+    too_big = pr.alloc(cx.ctx, (65536 - nxt + 1) * 4096, kind=P.KIND_HOST_MAPPED)  # one page too many
+    assert too_big.first_page is None and too_big.addr % 4096 == 0
+    with pytest.raises(P.ProviderError):
+        pr.signal_host(cx.ctx, cx.s, nxt, 0, 1)  # no page took that number
+    pr.free(cx.ctx, too_big)
+    fits = pr.alloc(cx.ctx, (65536 - nxt) * 4096, kind=P.KIND_HOST_MAPPED)  # exactly the rest
+    assert fits.first_page == nxt
+    page, slot, w = P.host_flag(fits, fits.bytes - 4)
+    assert (page, slot) == (65535, 1023)
+    w.value = 0
+    pr.signal_host(cx.ctx, cx.s, page, slot, 5)
+    pr.synchronize(cx.ctx, cx.s)
+    assert w.value == 5
+    after = pr.alloc(cx.ctx, 4096, kind=P.KIND_HOST_MAPPED)  # numbers spent: still allocated
+    assert after.first_page is None and after.addr != 0
+    for b in (empty, one, fits, after):
+        pr.free(cx.ctx, b)
+    cx.close()
+
+
 def test_a_wait_past_its_spin_limit_ends_and_is_reported():
     """A context opened with kernels.spin_kernel_max_us = 2000: a wait the host never answers
     gives up on its own, writes no reset, lets the stream run on (the next flag rises), and

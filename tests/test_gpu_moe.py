@@ -424,3 +424,31 @@ def test_combine_bit_exact(M, rows, k, hidden):
     flat[1:] = dev(out).reshape(-1)
     view = flat[1:].view(rows, k, hidden)
     assert_same(host(M.combine(view, dev(ids), dev(w))), o.moe_combine(out, ids, w), "unaligned")
+
+
+@pytest.mark.parametrize("rows,k,hidden,n_shared", [(33, 8, 1000, 0), (5, 8, 1001, 1), (64, 8, 4096, 0),
+                                                    (3, 64, 130, 3), (7, 1, 4096, 8), (2, 3, 2050, 2)])
+def test_combine_ranked_bit_exact(M, rows, k, hidden, n_shared):
+    """MoeCombine as the graph binds it: slots in rank order, then the shared outputs; float4
+    columns and the scalar tail, top_k 1 to 64, 0 to 8 shared outputs."""
+    rs = np.random.default_rng(rows * 37 + hidden + n_shared)
+    out = rs.standard_normal((rows, k, hidden)).astype(np.float32)
+    w = rs.random((rows, k)).astype(np.float32)
+    shared = [rs.standard_normal((rows, hidden)).astype(np.float32) for _ in range(n_shared)]
+    announce(f"combine ranked rows={rows} k={k} hidden={hidden} shared={n_shared}")
+    want = o.moe_combine_ranked(out, w, shared)
+    got = M.combine_ranked(dev(out), dev(w), [dev(a) for a in shared])
+    assert_same(host(got), want)
+    # views 4 bytes into their buffers take the scalar path
+    flat = torch.zeros(rows * k * hidden + 1, device="cuda")
+    flat[1:] = dev(out).reshape(-1)
+    view = flat[1:].view(rows, k, hidden)
+    assert_same(host(M.combine_ranked(view, dev(w), [dev(a) for a in shared])), want, "unaligned")
+
+
+def test_combine_ranked_refusals(M):
+    out, w = torch.zeros(2, 3, 8, device="cuda"), torch.zeros(2, 3, device="cuda")
+    with pytest.raises(M.MoeError):
+        M.combine_ranked(out, w, [torch.zeros(2, 8, device="cuda")] * 9)
+    with pytest.raises(M.MoeError):
+        M.combine_ranked(out, w, [torch.zeros(2, 9, device="cuda")])

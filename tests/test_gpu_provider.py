@@ -264,17 +264,42 @@ def test_launch_checks_workspace_and_arguments(cx):
     assert (cx.get(yb, np.uint8, 4 * rows * n_out) == 0x7F).all()
 
 
-def test_moe_layer_through_the_provider(cx):
-    """Route, grouped experts, combine: three prepared ops on one stream, every output bit-exact."""
+def fast_q4k_experts(seed, n_experts, hidden, inter):
+    """Stacked Q4_K experts: random codes, F16 scales in [2^-10, 2^-5) (the distribution of
+    crates/kernels-cpu/src/moe/tests.rs:40-74, generated vectorized for the layer-size case)."""
+    rs = np.random.default_rng(seed)
+
+    def mat(n_out, k):
+        nb = n_out * k // 256
+        b = np.frombuffer(rs.bytes(nb * 144), np.uint8).reshape(nb, 144).copy()
+        h = ((rs.integers(5, 10, (nb, 2), dtype=np.uint16) << 10)
+             | rs.integers(0, 1024, (nb, 2), dtype=np.uint16)).astype(np.uint16)
+        b[:, 0:4] = h.view(np.uint8).reshape(nb, 4)
+        return b.ravel()
+
+    return mat(n_experts * inter, hidden), mat(n_experts * inter, hidden), mat(n_experts * hidden, inter)
+
+
+@pytest.mark.parametrize("E,top_k,hidden,inter,rows,n_shared", [
+    (16, 4, 512, 256, 37, 2),
+    (128, 8, 4096, 1536, 64, 0)])  # the Qwen3-235B-A22B MoE shape at 64 decode tokens
+def test_moe_layer_through_the_provider(cx, E, top_k, hidden, inter, rows, n_shared):
+    """Route, grouped experts, combine: three prepared ops on one stream under the reference's
+    keys and bindings (MoeCombine: dims [top_k, n_shared, hidden], inputs [per_expert, weights,
+    shared...], crates/kernels/src/op/kind.rs:244, crates/graph/src/blocks/ffn.rs:189-200), every
+    output bit-exact."""
     P, pr = cx.P, cx.pr
-    E, top_k, hidden, inter, rows = 16, 4, 512, 256, 37
-    rng = MoeRng(77)
-    gate = moe_matrix(rng, o.Q4_K, E * inter, hidden, o.f16_bits)
-    up = moe_matrix(rng, o.Q4_K, E * inter, hidden, o.f16_bits)
-    down = moe_matrix(rng, o.Q4_K, E * hidden, inter, o.f16_bits)
+    if E == 128:
+        gate, up, down = fast_q4k_experts(7, E, hidden, inter)
+    else:
+        rng = MoeRng(77)
+        gate = moe_matrix(rng, o.Q4_K, E * inter, hidden, o.f16_bits)
+        up = moe_matrix(rng, o.Q4_K, E * inter, hidden, o.f16_bits)
+        down = moe_matrix(rng, o.Q4_K, E * hidden, inter, o.f16_bits)
     router = o.normal(0x51A30004, 0.02, E * hidden).reshape(E, hidden)
     x = o.normal(0x51A20004, 1.0, rows * hidden).reshape(rows, hidden)
-    announce(f"provider moe E={E} k={top_k} hidden={hidden} inter={inter} rows={rows}")
+    shared = [o.normal(0x51A50000 + i, 1.0, rows * hidden).reshape(rows, hidden) for i in range(n_shared)]
+    announce(f"provider moe E={E} k={top_k} hidden={hidden} inter={inter} rows={rows} shared={n_shared}")
 
     route_key = {"op": {"MoeRoute": {"norm": "Softmax"}}, "schemes": [{"Plain": "F32"}, {"Plain": "F32"}],
                  "layout": 0, "variant": 0}
@@ -283,9 +308,11 @@ def test_moe_layer_through_the_provider(cx):
     combine_key = {"op": "MoeCombine", "schemes": [{"Plain": "F32"}], "layout": 0, "variant": 0}
     caps = pr.query(cx.ctx, route_key, shape(rows, E, top_k, hidden))
     assert caps["numerics"]["softmax_f32"]
+    ccaps = pr.query(cx.ctx, combine_key, shape(rows, top_k, n_shared, hidden))
+    assert ccaps["workspace"] == 0 and ccaps["deterministic"]
     r_op = pr.prepare(cx.ctx, route_key, shape(rows, E, top_k, hidden))
     g_op = pr.prepare(cx.ctx, grouped_key, shape(rows, E, top_k, hidden, inter))
-    c_op = pr.prepare(cx.ctx, combine_key, shape(rows, top_k, hidden))
+    c_op = pr.prepare(cx.ctx, combine_key, shape(rows, top_k, n_shared, hidden))
 
     rd, gd, ud, dd = dev(router), dev(gate), dev(up), dev(down)
     xb = cx.put(x)
@@ -296,18 +323,41 @@ def test_moe_layer_through_the_provider(cx):
     w_arg = P.packed(w_b, P.DT_F32, [rows, top_k])
     per_arg = P.packed(per_b, P.DT_F32, [rows, top_k, hidden])
     y_arg = P.packed(y_b, P.DT_F32, [rows, hidden])
+    sh_args = [P.packed(cx.put(a), P.DT_F32, [rows, hidden]) for a in shared]
     pr.launch(cx.ctx, cx.s, r_op, P.op_args([x_arg], [ids_arg, w_arg], [P.view(rd.data_ptr(), router.nbytes)],
                                             cx.workspace(r_op), [P.Scalar(1, 1)]))
     views = [P.view(t.data_ptr(), t.numel()) for t in (gd, ud, dd)]
     pr.launch(cx.ctx, cx.s, g_op, P.op_args([x_arg, ids_arg], [per_arg], views, cx.workspace(g_op)))
-    pr.launch(cx.ctx, cx.s, c_op, P.op_args([per_arg, w_arg, ids_arg], [y_arg], []))
+    pr.launch(cx.ctx, cx.s, c_op, P.op_args([per_arg, w_arg, *sh_args], [y_arg], []))
 
     wids, ww, _ = o.moe_route(router, x, E, top_k, True)
     assert (cx.get(ids_b, np.int32, (rows, top_k)) == wids).all()
     assert_same(cx.get(w_b, np.float32, (rows, top_k)), ww, "route weights")
-    want = o.moe_grouped(o.Q4_K, o.Q4_K, E, top_k, hidden, inter, gate, up, down, x, wids, threads=8)
+    want = o.moe_grouped(o.Q4_K, o.Q4_K, E, top_k, hidden, inter, gate, up, down, x, wids, threads=16)
     assert_same(cx.get(per_b, np.float32, (rows, top_k, hidden)), want, "grouped")
-    assert_same(cx.get(y_b, np.float32, (rows, hidden)), o.moe_combine(want, wids, ww), "combined")
+    assert_same(cx.get(y_b, np.float32, (rows, hidden)), o.moe_combine_ranked(want, ww, shared), "combined")
+    del gd, ud, dd
+    torch.cuda.empty_cache()
+
+
+def test_moe_combine_binding_refusals(cx):
+    """MoeCombine's query answers None for shapes outside [top_k 1..64, n_shared 0..8, hidden];
+    a launch with a shared-output count other than the plan's is refused."""
+    P, pr = cx.P, cx.pr
+    key = {"op": "MoeCombine", "schemes": [{"Plain": "F32"}], "layout": 0, "variant": 0}
+    for dims in ([0, 0, 64], [65, 0, 64], [2, 9, 64], [2, 0, 0], [2, 64], [2, 0, 64, 1]):
+        assert pr.query(cx.ctx, key, shape(4, *dims)) is None, dims
+    assert pr.query(cx.ctx, key, shape(4, 2, 0, 64)) is not None  # the ggml mapping test's key
+    rows, top_k, hidden = 4, 2, 64
+    op = pr.prepare(cx.ctx, key, shape(rows, top_k, 1, hidden))
+    per = P.packed(cx.empty(4 * rows * top_k * hidden), P.DT_F32, [rows, top_k, hidden])
+    w = P.packed(cx.empty(4 * rows * top_k), P.DT_F32, [rows, top_k])
+    yb = cx.empty(4 * rows * hidden)
+    y = P.packed(yb, P.DT_F32, [rows, hidden])
+    with pytest.raises(P.ProviderError) as e:
+        pr.launch(cx.ctx, cx.s, op, P.op_args([per, w], [y], []))
+    assert "shared" in e.value.message
+    assert (cx.get(yb, np.uint8, 4 * rows * hidden) == 0x7F).all()
 
 
 def test_moe_grouped_site_input_through_the_provider(cx):

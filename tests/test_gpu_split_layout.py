@@ -2,6 +2,8 @@
 scale): the device repack is its definition and inverts exactly, and the split decode kernel
 (1 to 8 rows, eight at a time beyond) and the int8 matrix-core GEMM (Q8_0, 9 rows or more) give
 the oracle's Gemv values bit for bit (crates/kernels-cpu/src/gemv.rs:435-492)."""
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -144,3 +146,36 @@ def test_split_q4_0_extreme_codes_equal_oracle(S):
         S.gemv(W, dev(x), rows, y=y)
         want = o.gemv(o.Q4_0, w, n_out, k, x, rows, threads=8)
         assert_same(host(y), want, f"Q4_0 extreme codes rows {rows}")
+
+
+@pytest.mark.parametrize("ty,n_out,k,layout,ok", [
+    (o.Q8_0, 64, 512, 2, False),   # SPLIT: the scale section sits after every block's codes
+    (o.Q4_0, 64, 512, 2, False),
+    (o.Q4_K, 3, 256, 1, False),    # X8 with a final run of 3 super-blocks
+    (o.Q4_K, 16, 512, 1, True)])   # X8 in whole runs of 8: a longer view reads the same bytes
+def test_repacked_view_longer_than_the_matrix(S, ty, n_out, k, layout, ok):
+    """A repacked view must be the repack of its matrix alone where the layout places bytes by the
+    total length; a longer view is refused before anything runs (or, in whole X8 runs, computes the
+    same values)."""
+    rng = GemvRng(4242 + ty)
+    w = gemv_weights(rng, ty, n_out, k, o.f16_bits, o.round_bf16)
+    x = gemv_activations(rng, 2, k).astype(np.float32)
+    W = S.repack(S.Weights(S.WeightType(ty), dev(w), n_out, k))
+    assert W.layout == layout
+    longer = torch.zeros(W.bytes.numel() + 256, dtype=torch.uint8, device="cuda")
+    longer[:W.bytes.numel()] = W.bytes
+    y = torch.full((2, n_out), float("nan"), device="cuda")
+    need = C.c_uint64(0)
+    assert S.lib().syn_gemv_layout_workspace_bytes(layout, ty, 2, k, C.byref(need)) == 0
+    ws = torch.empty(max(need.value, 256), dtype=torch.uint8, device="cuda")
+    announce(f"longer view ty={ty} {n_out}x{k} layout={layout}")
+    args = (layout, ty, longer.data_ptr(), longer.numel(), n_out, k, dev(x).data_ptr(), 2, y.data_ptr(),
+            ws.data_ptr(), ws.numel(), None)
+    rc = S.lib().syn_gemv_layout(*args)
+    if ok:
+        assert rc == 0
+        assert_same(host(y), o.gemv(ty, w, n_out, k, x, 2), "whole X8 runs")
+    else:
+        assert rc != 0 and b"repack of the matrix alone" in S.lib().syn_last_error()
+        torch.cuda.synchronize()
+        assert torch.isnan(y).all()

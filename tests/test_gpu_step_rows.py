@@ -162,7 +162,7 @@ def test_moe_rows_active(cx, E, top_k, hidden, inter, bucket, active):
     combine_key = {"op": "MoeCombine", "schemes": [{"Plain": "F32"}], "layout": 0, "variant": 0}
     r_op = pr.prepare(cx.ctx, route_key, shape(bucket, E, top_k, hidden))
     g_op = pr.prepare(cx.ctx, grouped_key, shape(bucket, E, top_k, hidden, inter))
-    c_op = pr.prepare(cx.ctx, combine_key, shape(bucket, top_k, hidden))
+    c_op = pr.prepare(cx.ctx, combine_key, shape(bucket, top_k, 0, hidden))
     rd, gd, ud, dd = dev(router), dev(gate), dev(up), dev(down)
     xb = cx.put(x)
     ids0 = np.full((bucket, top_k), 999, np.int32)  # out of range past rows_active
@@ -177,7 +177,7 @@ def test_moe_rows_active(cx, E, top_k, hidden, inter, bucket, active):
                                             cx.workspace(r_op), [P.Scalar(1, 1)], step=step))
     views = [P.view(t.data_ptr(), t.numel()) for t in (gd, ud, dd)]
     pr.launch(cx.ctx, cx.s, g_op, P.op_args([x_arg, ids_arg], [per_arg], views, cx.workspace(g_op), step=step))
-    pr.launch(cx.ctx, cx.s, c_op, P.op_args([per_arg, w_arg, ids_arg], [y_arg], [], step=step))
+    pr.launch(cx.ctx, cx.s, c_op, P.op_args([per_arg, w_arg], [y_arg], [], step=step))
 
     xa = x[:active]
     wids, ww, _ = o.moe_route(router, xa, E, top_k, True)
@@ -187,7 +187,7 @@ def test_moe_rows_active(cx, E, top_k, hidden, inter, bucket, active):
     want_per = o.moe_grouped(o.Q4_K, o.Q4_K, E, top_k, hidden, inter, gate, up, down, xa, wids, threads=8)
     per = cx.get(per_b, np.float32, (bucket, top_k * hidden))
     check_rows(per, want_per.reshape(active, top_k * hidden), active, "grouped")
-    want_y = o.moe_combine(want_per.reshape(active, top_k, hidden), wids, ww)
+    want_y = o.moe_combine_ranked(want_per.reshape(active, top_k, hidden), ww)
     check_rows(cx.get(y_b, np.float32, (bucket, hidden)), want_y, active, "combine")
 
 

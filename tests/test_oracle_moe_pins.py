@@ -182,6 +182,86 @@ def test_combine_catches_planted_mistakes():
     assert not check_combine(ordered(ascending, by_rank=True))
 
 
+# ---- combine as the graph binds it: [per_expert, weights, shared...], rank order ---------------
+# (crates/graph/src/ir/signature.rs:153, crates/graph/src/blocks/ffn.rs:189-200; RFC-0042 ...md:233)
+def ranked_hand_cases():
+    """(out [rows, k, hidden], w, shared list, want [rows, hidden]) derived by hand."""
+    cases = []
+    # Rank order 0, 1, 2 sums (2^27 + 1) - 2^27 = 0 (2^27 + 1 rounds to 2^27); ascending expert
+    # order of ids [5, 1, 3] would give 1 (the helper's first hand case), reversed order 1 too.
+    out = np.array([[[2.0 ** 27], [1.0], [-(2.0 ** 27)]]], f32)
+    cases.append((out, np.ones((1, 3), f32), [], np.array([[0.0]], f32)))
+    # Each product rounded before its add: rank 0 gives -1, rank 1 adds fl(a * a) = 1 + 2^-11,
+    # y = 2^-11; a fused multiply-add would keep the 2^-24.
+    a = f32(1 + 2.0 ** -12)
+    out = np.array([[[-1.0], [a]]], f32)
+    cases.append((out, np.array([[1.0, a]], f32), [], np.array([[2.0 ** -11]], f32)))
+    # The shared outputs come after the routed slots and carry no weight: the slot gives
+    # 4 * 2^25 = 2^27, then each shared 8 is half an ulp of 2^27 (a tie, to even: lost), y = 2^27;
+    # shared first would give 8 + 8 = 16, then 2^27 + 16 exactly; weighting them by 4 would give
+    # 2^27 + 32 + 32.
+    out = np.array([[[2.0 ** 25]]], f32)
+    cases.append((out, np.array([[4.0]], f32), [np.array([[8.0]], f32), np.array([[8.0]], f32)],
+                  np.array([[2.0 ** 27]], f32)))
+    return cases
+
+
+def ranked_exact_case(seed, rows=13, k=8, hidden=64, n_shared=2):
+    rs = np.random.default_rng(seed)
+    out = rs.integers(-1000, 1001, (rows, k, hidden)).astype(f32)
+    w = (2.0 ** rs.integers(-3, 4, (rows, k))).astype(f32)
+    shared = [rs.integers(-1000, 1001, (rows, hidden)).astype(f32) for _ in range(n_shared)]
+    want = (out.astype(np.float64) * w[:, :, None]).sum(axis=1) + sum(a.astype(np.float64) for a in shared)
+    return out, w, shared, want.astype(f32)
+
+
+def check_ranked(fn):
+    cases = ranked_hand_cases() + [ranked_exact_case(s) for s in (4, 5)]
+    ok = all(np.array_equal(bits(fn(out, w, sh)), bits(want)) for out, w, sh, want in cases)
+    # rows whose ids ascend: the rank-order sum is the helper's ascending-expert sum
+    rs = np.random.default_rng(6)
+    out = rs.standard_normal((9, 8, 48)).astype(f32)
+    w = rs.random((9, 8)).astype(f32)
+    ids = np.sort(np.stack([rs.permutation(128)[:8] for _ in range(9)]), axis=1).astype(np.int32)
+    return ok and np.array_equal(bits(fn(out, w, [])), bits(o.moe_combine(out, ids, w)))
+
+
+def test_combine_ranked_matches_hand_exact_and_ascending_cases():
+    assert check_ranked(o.moe_combine_ranked)
+
+
+def test_combine_ranked_catches_planted_mistakes():
+    def variant(order=lambda k: range(k), fused=False, shared_first=False, shared_weight=1.0):
+        def fn(out, w, shared):
+            rows, k, hidden = out.shape
+            y = np.zeros((rows, hidden), f32)
+            for r in range(rows):
+                def routed():
+                    for j in order(k):
+                        if fused:
+                            y[r] = (y[r].astype(np.float64) + np.float64(w[r, j]) * out[r, j]).astype(f32)
+                        else:
+                            y[r] = y[r] + f32(w[r, j]) * out[r, j]
+
+                def sh():
+                    for a in shared:
+                        y[r] = y[r] + f32(shared_weight) * a[r]
+                if shared_first:
+                    sh()
+                    routed()
+                else:
+                    routed()
+                    sh()
+            return y
+        return fn
+
+    assert check_ranked(variant())  # the definition itself passes
+    assert not check_ranked(variant(order=lambda k: reversed(range(k))))
+    assert not check_ranked(variant(fused=True))
+    assert not check_ranked(variant(shared_first=True))
+    assert not check_ranked(variant(shared_weight=4.0))
+
+
 # ---- MoeRoute{Softmax}: RFC-0042 ...md:232-233; reference.rs:56-59 -----------------------------
 def route_logits(logits):
     """A router and a one-hot token that make the F32Fixed logits exactly `logits`."""
