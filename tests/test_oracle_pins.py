@@ -391,6 +391,52 @@ def test_moe_every_slot_is_its_experts_ffn_of_the_row_alone():
                 assert (bits(out[r, j]) == bits(want)).all(), (rows, r, j)
 
 
+def q8_0_layer(seed):
+    e, _, hidden, inter = MOE
+    rng = MoeRng(seed)
+    gate = moe_matrix(rng, o.Q8_0, e * inter, hidden, o.f16_bits)
+    up = moe_matrix(rng, o.Q8_0, e * inter, hidden, o.f16_bits)
+    down = moe_matrix(rng, o.Q8_0, e * hidden, inter, o.f16_bits)
+    return rng, gate, up, down
+
+
+def ffn_alone_q8_0(gate, up, down, e, x, h_q8k=False, swap=False):
+    """The Q8_0-expert form of moe/tests.rs:300-313: gate/up Gemv on the row's Q8_0 blocks,
+    silu(g) * u, h requantized as the down matrix's activation kind (Q8_0, act.rs:31-39), down
+    Gemv.  h_q8k and swap plant mistakes: h through Q8_K first, or silu taken of the up row."""
+    _, _, hidden, inter = MOE
+    gb, db = inter * o.row_bytes(o.Q8_0, hidden), hidden * o.row_bytes(o.Q8_0, inter)
+    g = o.gemv(o.Q8_0, gate[e * gb:(e + 1) * gb], inter, hidden, x, 1)[0]
+    u = o.gemv(o.Q8_0, up[e * gb:(e + 1) * gb], inter, hidden, x, 1)[0]
+    if swap:
+        g, u = u, g
+    h = np.array([np.float32(o.silu(float(a))) * b for a, b in zip(g, u)], np.float32)
+    if h_q8k:
+        d, _, codes = o.act_quantize(o.ACT_Q8K, h, 1, inter)
+        h = (codes.astype(np.float32).reshape(-1, 256) * d[:, None]).astype(np.float32).ravel()
+    return o.gemv(o.Q8_0, down[e * db:(e + 1) * db], hidden, inter, h, 1)[0]
+
+
+def test_moe_q8_0_experts_every_slot_is_its_experts_ffn_of_the_row_alone():
+    """moe/tests.rs:315-337 on Q8_0 experts (moe/entry.rs:50-55): every slot of the oracle's
+    grouped FFN equals its expert's FFN of its row alone, bit for bit; the same check rejects an
+    h requantized as Q8_K (the Q4_K experts' kind) and gate and up swapped."""
+    rng, gate, up, down = q8_0_layer(11)
+    n_experts, top_k, hidden, inter = MOE
+    for rows in [1, 3, 8]:
+        x = moe_activations(rng, rows * hidden).reshape(rows, hidden)
+        ids = moe_route_ids(rng, rows, top_k, n_experts)
+        out = o.moe_grouped(o.Q8_0, o.Q8_0, n_experts, top_k, hidden, inter, gate, up, down, x, ids)
+        for r in range(rows):
+            for j in range(top_k):
+                e = int(ids[r, j])
+                want = ffn_alone_q8_0(gate, up, down, e, x[r])
+                assert (bits(out[r, j]) == bits(want)).all(), (rows, r, j)
+                # planted mistakes, each caught by the same bit comparison
+                assert not (bits(ffn_alone_q8_0(gate, up, down, e, x[r], h_q8k=True)) == bits(want)).all()
+                assert not (bits(ffn_alone_q8_0(gate, up, down, e, x[r], swap=True)) == bits(want)).all()
+
+
 def test_moe_slots_of_other_sites_keep_their_values():
     """moe/tests.rs:559-590: with the site mask on the even experts, their slots equal the
     unmasked call's and every other slot keeps its bits; the odd experts' call on the same output
