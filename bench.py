@@ -115,6 +115,24 @@ def cpu_threads():
 
 
 # ---- the headline: the decode layer ---------------------------------------------------------------
+def timed_reps(fn, seconds):
+    """(repetitions, seconds) of fn run back to back for at least `seconds` (one call first, untimed)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            return n, dt
+
+
+# The CPU baseline is the reference's own x86 level of kernels-cpu restated in C
+# (crates/kernels-cpu/src/gemv/x86.rs: AVX2 block sums, 8 activation rows a weight pass), the
+# same bits as the portable restatement, which is timed beside it for a shorter sample.
+CPU_LEVEL, PORTABLE_SECONDS = 1, 2.0
+
+
 def build_layer(torch, S, seed_base):
     gen = torch.Generator(device="cuda")
     copies = []
@@ -231,34 +249,26 @@ def cpu_layer_baseline(copies, xs, seconds):
     x = {name: xs[name].cpu().numpy() for name, _, _ in LAYER}
     total_w = sum(q4k_bytes(n, k) for _, n, k in LAYER)
 
-    def layer(t):
+    def layer(t, level=CPU_LEVEL):
         for name, n_out, k in LAYER:
-            o.gemv(o.Q4_K, w[name], n_out, k, x[name], 1, threads=t)
+            o.gemv(o.Q4_K, w[name], n_out, k, x[name], 1, threads=t, level=level)
 
-    layer(threads)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        layer(threads)
-        n += 1
-        dt = time.perf_counter() - t0
-        if dt >= seconds:
-            break
-    t1 = time.perf_counter()
-    reps1 = 0
-    while reps1 < 3 or time.perf_counter() - t1 < 1.0:
-        layer(1)
-        reps1 += 1
-    one = (time.perf_counter() - t1) / reps1
+    n, dt = timed_reps(lambda: layer(threads), seconds)
+    reps1, dt1 = timed_reps(lambda: layer(1), 1.0)
+    one = dt1 / reps1
+    np_, dtp = timed_reps(lambda: layer(threads, 0), PORTABLE_SECONDS)
     return {
         "value": round(total_w * n / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
+        "level": "x86 (AVX2 block sums, crates/kernels-cpu/src/gemv/x86.rs)",
         "sample": f"{n} Q4_K decode layers (5 GEMVs incl. Q8_K activation quantization) in {dt:.1f} s on "
                   f"{threads} threads (this box's CPU share for one GPU); one layer at 1 thread: "
                   f"{one * 1e3:.2f} ms = {total_w / one / 1e9:.2f} GB/s",
         "ms_per_layer": round(dt / n * 1e3, 3),
         "one_thread_gbs": round(total_w / one / 1e9, 3),
+        "portable_gbs": round(total_w * np_ / dtp / 1e9, 3),
         "host": host_info(),
     }
 
@@ -502,23 +512,20 @@ def bench_moe(torch, S, M, steps, warmup, cpu_seconds):
         g, u, d = ex.gate.cpu().numpy(), ex.up.cpu().numpy(), ex.down.cpu().numpy()
         r, xh = layer.router.cpu().numpy(), x.cpu().numpy()
 
-        def step():
+        def step(level=CPU_LEVEL):
             ids_c, w_c, _ = o.moe_route(r, xh, c["n_experts"], c["top_k"], True)
             out_c = o.moe_grouped(o.Q4_K, o.Q4_K, c["n_experts"], c["top_k"], c["hidden"],
-                                  c["inter"], g, u, d, xh, ids_c, threads=threads)
-            return o.moe_combine(out_c, ids_c, w_c)
+                                  c["inter"], g, u, d, xh, ids_c, threads=threads, level=level)
+            return o.moe_combine_ranked(out_c, w_c)
 
-        step()
-        n, t1 = 0, time.perf_counter()
-        while True:
-            step()
-            n += 1
-            if time.perf_counter() - t1 >= cpu_seconds:
-                break
-        cdt = time.perf_counter() - t1
+        n, cdt = timed_reps(step, cpu_seconds)
+        np_, dtp = timed_reps(lambda: step(0), PORTABLE_SECONDS)
         res["cpu_baseline"] = {"value": round(c["tokens"] * n / cdt, 1), "unit": "tokens/s",
                                "cores": threads, "kind": "port",
-                               "sample": f"{n} MoE layers of 64 tokens in {cdt:.1f} s"}
+                               "level": "x86 (AVX2 block sums, crates/kernels-cpu/src/gemv/x86.rs)",
+                               "sample": f"{n} MoE layers of 64 tokens in {cdt:.1f} s (experts split over "
+                                         f"{threads} threads)",
+                               "portable_tokens_per_s": round(c["tokens"] * np_ / dtp, 1)}
         res["speedup_over_cpu"] = round(res["value"] / res["cpu_baseline"]["value"], 1)
     return res
 
@@ -621,17 +628,18 @@ def bench_prefill(torch, S, M, steps, warmup, cpu_seconds):
             wb = S.quantize(S.WeightType.Q4K, w).cpu().numpy()
             xh = torch.randn(rows, k, device="cuda").cpu().numpy()
             sample.append((wb, n_out, k, xh))
-        n, t1 = 0, time.perf_counter()
-        while True:
+        def dense(level=CPU_LEVEL):
             for wb, n_out, k, xh in sample:
-                o.gemv(o.Q4_K, wb, n_out, k, xh, rows, threads=threads)
-            n += 1
-            if time.perf_counter() - t1 >= cpu_seconds:
-                break
-        cdt = time.perf_counter() - t1
+                o.gemv(o.Q4_K, wb, n_out, k, xh, rows, threads=threads, level=level)
+
+        n, cdt = timed_reps(dense, cpu_seconds)
+        np_, dtp = timed_reps(lambda: dense(0), PORTABLE_SECONDS)
         res["cpu_baseline"] = {"value": round(rows * n / cdt, 1), "unit": "tokens/s (dense gate+down)",
                                "cores": threads, "kind": "port",
-                               "sample": f"{n} x {rows} token rows through gate and down in {cdt:.1f} s"}
+                               "level": "x86 (AVX2 block sums, 8 rows a weight pass, "
+                                        "crates/kernels-cpu/src/gemv/x86.rs, gemv.rs:83)",
+                               "sample": f"{n} x {rows} token rows through gate and down in {cdt:.1f} s",
+                               "portable_tokens_per_s": round(rows * np_ / dtp, 1)}
         res["speedup_over_cpu"] = round(res["dense_tokens_per_s"] / res["cpu_baseline"]["value"], 1)
     return res
 

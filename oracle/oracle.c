@@ -856,13 +856,121 @@ static void int_rows(int ty, const uint8_t* w, size_t n_out, size_t k, const uin
     }
 }
 
-int or_gemv_ws(int ty, const uint8_t* w, size_t n_out, size_t k, const uint8_t* ws,
-               const float* xf, size_t rows, size_t o0, size_t o1, float* y) {
+/* ===================================================================================== */
+/* The reference's x86 level of the same kernel (crates/kernels-cpu/src/gemv/x86.rs:74-153;  */
+/* portable.rs:114-190 int_rows with gemv.rs:83 ROW_GROUP = 8): a block's weights are loaded */
+/* once for up to 8 activation rows, and each exact block sum comes from AVX2 byte products: */
+/* |w| as unsigned bytes times x * sign(w) as signed bytes (vpmaddubsw cannot saturate:       */
+/* |w| <= 128, |x| <= 127), pairs summed by vpmaddwd, then a horizontal add.  The sums are     */
+/* exact, the F32 terms and their order are int_rows', so the outputs are its bits (the tests */
+/* compare them).  This is the timed CPU baseline; the portable form above is the checker.   */
+/* ===================================================================================== */
+#include <immintrin.h>
+
+#define OR_ROW_GROUP 8
+
+static inline int32_t x86_hsum(__m256i v) {
+    __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0x4E));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xB1));
+    return _mm_cvtsi128_si32(s);
+}
+/* sum over 32 signed byte pairs, exact */
+static inline int32_t x86_dot_i8(__m256i w, __m256i x) {
+    const __m256i p = _mm256_maddubs_epi16(_mm256_sign_epi8(w, w), _mm256_sign_epi8(x, w));
+    return x86_hsum(_mm256_madd_epi16(p, _mm256_set1_epi16(1)));
+}
+/* sum over 32 pairs of unsigned bytes n <= 15 and signed bytes x, exact */
+static inline int32_t x86_dot_u4(__m256i n, __m256i x) {
+    return x86_hsum(_mm256_madd_epi16(_mm256_maddubs_epi16(n, x), _mm256_set1_epi16(1)));
+}
+static inline __m256i x86_load32(const void* p) { return _mm256_loadu_si256((const __m256i*)p); }
+
+static void int_rows_x86(int ty, const uint8_t* w, size_t n_out, size_t k, const uint8_t* ws,
+                         size_t rows, size_t o0, size_t o1, float* y) {
+    int kind = or_act_kind(ty);
+    size_t n = rows * k, c, s, m;
+    act_counts(kind, n, &c, &s, &m);
+    const float* xd = (const float*)ws;
+    const int32_t* xs = (const int32_t*)(ws + 4 * s);
+    const int8_t* xq = (const int8_t*)(ws + 4 * (s + m));
+    size_t be = (size_t)or_block_elems(ty), bb = (size_t)or_block_bytes(ty);
+    size_t nb = k / be, row_bytes = nb * bb;
+    const __m256i low4 = _mm256_set1_epi8(0x0F);
+    for (size_t r0 = 0; r0 < rows; r0 += OR_ROW_GROUP) {
+        const size_t nr = rows - r0 < OR_ROW_GROUP ? rows - r0 : OR_ROW_GROUP;
+        for (size_t o = o0; o < o1; ++o) {
+            const uint8_t* wr = w + o * row_bytes;
+            float acc[OR_ROW_GROUP];
+            for (size_t i = 0; i < nr; ++i) acc[i] = 0.0f;
+            for (size_t b = 0; b < nb; ++b) {
+                const uint8_t* blk = wr + b * bb;
+                if (ty == OR_Q8_0 || ty == OR_Q4_0) {
+                    __m256i wv;
+                    if (ty == OR_Q8_0) {
+                        wv = x86_load32(blk + 2);
+                    } else { /* the 16 code bytes: low nibbles are values 0-15, high 16-31, minus 8 */
+                        const __m128i q = _mm_loadu_si128((const __m128i*)(blk + 2));
+                        const __m128i m4 = _mm_set1_epi8(0x0F);
+                        wv = _mm256_sub_epi8(_mm256_set_m128i(_mm_and_si128(_mm_srli_epi16(q, 4), m4),
+                                                              _mm_and_si128(q, m4)),
+                                             _mm256_set1_epi8(8));
+                    }
+                    const float dw = half_at(blk);
+                    for (size_t i = 0; i < nr; ++i) {
+                        const int32_t sum = x86_dot_i8(wv, x86_load32(xq + (r0 + i) * k + b * 32));
+                        acc[i] += q32_term(dw, xd[(r0 + i) * nb + b], sum);
+                    }
+                } else { /* Q4_K: four groups of 64 values, low nibbles sub-block 2g, high 2g + 1 */
+                    int32_t sb[OR_ROW_GROUP][8];
+                    for (int g = 0; g < 4; ++g) {
+                        const __m256i q = x86_load32(blk + 16 + 32 * g);
+                        const __m256i lo = _mm256_and_si256(q, low4);
+                        const __m256i hi = _mm256_and_si256(_mm256_srli_epi16(q, 4), low4);
+                        for (size_t i = 0; i < nr; ++i) {
+                            const int8_t* xb = xq + (r0 + i) * k + b * 256 + 64 * g;
+                            sb[i][2 * g] = x86_dot_u4(lo, x86_load32(xb));
+                            sb[i][2 * g + 1] = x86_dot_u4(hi, x86_load32(xb + 32));
+                        }
+                    }
+                    int32_t sc[8], mn[8];
+                    for (int j = 0; j < 8; ++j) {
+                        uint8_t a, mm;
+                        scale_min_k4(j, blk + 4, &a, &mm);
+                        sc[j] = a;
+                        mn[j] = mm;
+                    }
+                    const float d = half_at(blk), dmin = half_at(blk + 2);
+                    for (size_t i = 0; i < nr; ++i) {
+                        const int32_t* sx = xs + (r0 + i) * (k / 32) + b * 8;
+                        int32_t s1 = 0, s2 = 0;
+                        for (int j = 0; j < 8; ++j) {
+                            s1 += sc[j] * sb[i][j];
+                            s2 += mn[j] * sx[j];
+                        }
+                        acc[i] += q4k_term(d, dmin, xd[(r0 + i) * nb + b], s1, s2);
+                    }
+                }
+            }
+            for (size_t i = 0; i < nr; ++i) y[(r0 + i) * n_out + o] = acc[i];
+        }
+    }
+}
+
+/* level 0: the portable kernels; 1: the x86 level (integer types; the float types have one form) */
+static int gemv_ws_level(int level, int ty, const uint8_t* w, size_t n_out, size_t k, const uint8_t* ws,
+                         const float* xf, size_t rows, size_t o0, size_t o1, float* y) {
     if (!or_block_elems(ty) || k % (size_t)or_block_elems(ty) || o1 > n_out) return -1;
     if (rows == 0 || o0 >= o1) return 0;
     if (ty == OR_F16 || ty == OR_BF16) float_rows(ty, w, n_out, k, xf, rows, o0, o1, y);
+    else if (level == 1) int_rows_x86(ty, w, n_out, k, ws, rows, o0, o1, y);
     else int_rows(ty, w, n_out, k, ws, rows, o0, o1, y);
     return 0;
+}
+
+int or_gemv_ws(int ty, const uint8_t* w, size_t n_out, size_t k, const uint8_t* ws,
+               const float* xf, size_t rows, size_t o0, size_t o1, float* y) {
+    return gemv_ws_level(0, ty, w, n_out, k, ws, xf, rows, o0, o1, y);
 }
 
 int or_gemv(int ty, const uint8_t* w, size_t n_out, size_t k, const float* x, size_t rows,
@@ -892,7 +1000,7 @@ void or_partition(int ty, size_t n_out, size_t k, size_t parts, size_t* starts, 
 }
 
 struct gemv_job {
-    int ty;
+    int level, ty;
     const uint8_t* w;
     size_t n_out, k, rows, o0, o1;
     const uint8_t* ws;
@@ -902,12 +1010,25 @@ struct gemv_job {
 
 static void* gemv_worker(void* p) {
     struct gemv_job* j = (struct gemv_job*)p;
-    or_gemv_ws(j->ty, j->w, j->n_out, j->k, j->ws, j->x, j->rows, j->o0, j->o1, j->y);
+    gemv_ws_level(j->level, j->ty, j->w, j->n_out, j->k, j->ws, j->x, j->rows, j->o0, j->o1, j->y);
     return NULL;
 }
 
+static int gemv_threads_level(int level, int ty, const uint8_t* w, size_t n_out, size_t k, const float* x,
+                              size_t rows, float* y, int threads);
+
 int or_gemv_threads(int ty, const uint8_t* w, size_t n_out, size_t k, const float* x,
                     size_t rows, float* y, int threads) {
+    return gemv_threads_level(0, ty, w, n_out, k, x, rows, y, threads);
+}
+
+int or_gemv_x86(int ty, const uint8_t* w, size_t n_out, size_t k, const float* x, size_t rows, float* y,
+                int threads) {
+    return gemv_threads_level(1, ty, w, n_out, k, x, rows, y, threads);
+}
+
+static int gemv_threads_level(int level, int ty, const uint8_t* w, size_t n_out, size_t k, const float* x,
+                              size_t rows, float* y, int threads) {
     if (!or_block_elems(ty) || k % (size_t)or_block_elems(ty)) return -1;
     int kind = or_act_kind(ty);
     size_t wsb = or_act_workspace_bytes(kind, rows, k);
@@ -919,7 +1040,7 @@ int or_gemv_threads(int ty, const uint8_t* w, size_t n_out, size_t k, const floa
     }
     if (threads < 1) threads = 1;
     if (threads == 1) {
-        int rc = or_gemv_ws(ty, w, n_out, k, ws, x, rows, 0, n_out, y);
+        int rc = gemv_ws_level(level, ty, w, n_out, k, ws, x, rows, 0, n_out, y);
         free(ws);
         return rc;
     }
@@ -928,7 +1049,7 @@ int or_gemv_threads(int ty, const uint8_t* w, size_t n_out, size_t k, const floa
     pthread_t* tid = (pthread_t*)calloc((size_t)threads, sizeof *tid);
     or_partition(ty, n_out, k, (size_t)threads, st, st + threads);
     for (int t = 0; t < threads; ++t) {
-        jobs[t] = (struct gemv_job){ty, w, n_out, k, rows, st[t], st[threads + t], ws, x, y};
+        jobs[t] = (struct gemv_job){level, ty, w, n_out, k, rows, st[t], st[threads + t], ws, x, y};
         pthread_create(&tid[t], NULL, gemv_worker, &jobs[t]);
     }
     for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
@@ -1042,6 +1163,7 @@ struct moe_ctx {
     float* out;
     const uint32_t *offsets, *slots;
     size_t e_begin, e_end, stride; /* experts e_begin, e_begin+stride, ... */
+    int level;                     /* the Gemv kernels' level (gemv_ws_level) */
 };
 
 /* moe.rs:470-517: one expert's pass: gather distinct rows, quantize, gate/up + silu, requant h,
@@ -1063,11 +1185,11 @@ static int moe_expert(const struct moe_ctx* c, size_t e, float* xg, float* g, fl
         n++;
     }
     if (or_act_quantize(or_act_kind(c->gate_ty), xg, n, H, xq)) return -1;
-    or_gemv_ws(c->gate_ty, gw, I, H, xq, xg, n, 0, I, g);
-    or_gemv_ws(c->gate_ty, uw, I, H, xq, xg, n, 0, I, u);
+    gemv_ws_level(c->level, c->gate_ty, gw, I, H, xq, xg, n, 0, I, g);
+    gemv_ws_level(c->level, c->gate_ty, uw, I, H, xq, xg, n, 0, I, u);
     for (size_t i = 0; i < n * I; ++i) g[i] = or_silu(g[i]) * u[i];
     if (or_act_quantize(or_act_kind(c->down_ty), g, n, I, hq)) return -1;
-    or_gemv_ws(c->down_ty, dw, H, I, hq, g, n, 0, H, yd);
+    gemv_ws_level(c->level, c->down_ty, dw, H, I, hq, g, n, 0, H, yd);
     size_t row_i = 0;
     for (size_t i = g0; i < g1; ++i) {
         size_t r = c->slots[i] / K;
@@ -1095,10 +1217,31 @@ static void* moe_worker(void* p) {
     return NULL;
 }
 
+static int moe_grouped_level(int level, int gate_ty, int down_ty, size_t n_experts, size_t top_k, size_t hidden,
+                             size_t inter, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                             const float* x, const int32_t* ids, const int32_t* site, size_t rows,
+                             float* out, int threads);
+
 int or_moe_grouped(int gate_ty, int down_ty, size_t n_experts, size_t top_k, size_t hidden,
                    size_t inter, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
                    const float* x, const int32_t* ids, const int32_t* site, size_t rows,
                    float* out, int threads) {
+    return moe_grouped_level(0, gate_ty, down_ty, n_experts, top_k, hidden, inter, gate, up, down, x, ids, site,
+                             rows, out, threads);
+}
+
+int or_moe_grouped_x86(int gate_ty, int down_ty, size_t n_experts, size_t top_k, size_t hidden,
+                       size_t inter, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                       const float* x, const int32_t* ids, const int32_t* site, size_t rows,
+                       float* out, int threads) {
+    return moe_grouped_level(1, gate_ty, down_ty, n_experts, top_k, hidden, inter, gate, up, down, x, ids, site,
+                             rows, out, threads);
+}
+
+static int moe_grouped_level(int level, int gate_ty, int down_ty, size_t n_experts, size_t top_k, size_t hidden,
+                             size_t inter, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                             const float* x, const int32_t* ids, const int32_t* site, size_t rows,
+                             float* out, int threads) {
     if ((gate_ty != OR_Q4_K && gate_ty != OR_Q8_0) || (down_ty != OR_Q4_K && down_ty != OR_Q8_0))
         return -1;
     if (hidden % (size_t)or_block_elems(gate_ty) || inter % (size_t)or_block_elems(down_ty))
@@ -1113,7 +1256,7 @@ int or_moe_grouped(int gate_ty, int down_ty, size_t n_experts, size_t top_k, siz
     }
     if (threads < 1) threads = 1;
     struct moe_ctx base = {gate_ty, down_ty, n_experts, top_k, hidden, inter, rows, gate, up,
-                           down, x, site, out, offsets, slots, 0, n_experts, 1};
+                           down, x, site, out, offsets, slots, 0, n_experts, 1, level};
     if (threads == 1) {
         moe_worker(&base);
     } else {

@@ -97,6 +97,14 @@ int or_logits(int ty, const uint8_t* head, size_t vocab, size_t hidden, const fl
 size_t or_moe_workspace_bytes(size_t n_experts, size_t top_k, size_t hidden, size_t inter,
                               size_t rows);
 /* Counting-sort packing: offsets[n_experts+1], slots[rows*top_k].  -1 on a bad id. */
+/* The reference's x86 level (crates/kernels-cpu/src/gemv/x86.rs; ROW_GROUP = 8 rows a weight
+ * pass): the same outputs as or_gemv_threads / or_moe_grouped, timed as the CPU baseline. */
+int or_gemv_x86(int ty, const uint8_t* w, size_t n_out, size_t k, const float* x, size_t rows, float* y,
+                int threads);
+int or_moe_grouped_x86(int gate_ty, int down_ty, size_t n_experts, size_t top_k, size_t hidden,
+                       size_t inter, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                       const float* x, const int32_t* ids, const int32_t* site, size_t rows,
+                       float* out, int threads);
 int or_moe_pack(const int32_t* ids, size_t rows, size_t top_k, size_t n_experts,
                 uint32_t* offsets, uint32_t* slots);
 /* site: NULL (every expert) or n_experts ints, nonzero = computed here. */

@@ -75,6 +75,8 @@ def lib():
         L.or_gemv_ws.argtypes = [i32, vp, sz, sz, vp, vp, sz, sz, sz, vp]
         L.or_gemv.argtypes = [i32, vp, sz, sz, vp, sz, vp]
         L.or_gemv_threads.argtypes = [i32, vp, sz, sz, vp, sz, vp, i32]
+        L.or_gemv_x86.argtypes = [i32, vp, sz, sz, vp, sz, vp, i32]
+        L.or_moe_grouped_x86.argtypes = [i32, i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, vp, i32]
         L.or_gate_up_act.argtypes = [i32, vp, sz, sz, vp, sz, vp, i32]
         L.or_partition.argtypes = [i32, sz, sz, sz, vp, vp]
         L.or_rms_norm.argtypes = [vp, vp, sz, sz, C.c_float, vp]
@@ -231,12 +233,15 @@ def act_quantize(kind: int, x, rows: int, k: int):
 
 
 # ---- GEMV ----------------------------------------------------------------------------------
-def gemv(ty: int, w, n_out: int, k: int, x, rows: int, threads: int = 1) -> np.ndarray:
+def gemv(ty: int, w, n_out: int, k: int, x, rows: int, threads: int = 1, level: int = 0) -> np.ndarray:
+    """level 0: the portable kernels (the checker); 1: the reference's x86 level (8-row groups,
+    AVX2 block sums), the same bits, timed as the CPU baseline."""
     w = np.ascontiguousarray(w, dtype=np.uint8)
     x = _f32(x).ravel()
     assert w.size == n_out * row_bytes(ty, k) and x.size >= rows * k
     y = np.full(rows * n_out, np.nan, dtype=np.float32)
-    if lib().or_gemv_threads(ty, _p(w), n_out, k, _p(x), rows, _p(y), threads):
+    fn = lib().or_gemv_x86 if level == 1 else lib().or_gemv_threads
+    if fn(ty, _p(w), n_out, k, _p(x), rows, _p(y), threads):
         raise ValueError("gemv refused")
     return y.reshape(rows, n_out)
 
@@ -293,7 +298,7 @@ def moe_pack(ids, n_experts: int):
 
 
 def moe_grouped(gate_ty, down_ty, n_experts, top_k, hidden, inter, gate, up, down, x, ids,
-                site=None, threads: int = 1, out=None) -> np.ndarray:
+                site=None, threads: int = 1, out=None, level: int = 0) -> np.ndarray:
     x = _f32(x)
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     rows = ids.shape[0]
@@ -301,8 +306,9 @@ def moe_grouped(gate_ty, down_ty, n_experts, top_k, hidden, inter, gate, up, dow
         out = np.full(rows * top_k * hidden, np.nan, dtype=np.float32)
     gate, up, down = (np.ascontiguousarray(a, dtype=np.uint8) for a in (gate, up, down))
     s = None if site is None else np.ascontiguousarray(site, dtype=np.int32)
-    rc = lib().or_moe_grouped(gate_ty, down_ty, n_experts, top_k, hidden, inter, _p(gate),
-                              _p(up), _p(down), _p(x), _p(ids), _p(s), rows, _p(out), threads)
+    fn = lib().or_moe_grouped_x86 if level == 1 else lib().or_moe_grouped
+    rc = fn(gate_ty, down_ty, n_experts, top_k, hidden, inter, _p(gate), _p(up), _p(down), _p(x), _p(ids), _p(s),
+            rows, _p(out), threads)
     if rc:
         raise ValueError(f"moe_grouped refused ({rc})")
     return out.reshape(rows, top_k, hidden)

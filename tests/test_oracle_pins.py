@@ -460,3 +460,40 @@ def test_moe_slots_of_other_sites_keep_their_values():
     assert (ids % 2 == 1).any() and (ids % 2 == 0).any()
     done = o.moe_grouped(*args, site=(~even).astype(np.int32), out=out)
     assert (bits(done) == bits(every)).all()
+
+
+# ---- the reference's x86 level (the timed CPU baseline) ---------------------------------------
+@pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0, o.Q4_K])
+def test_x86_level_gives_the_portable_bits(ty):
+    """crates/kernels-cpu/src/gemv/x86.rs's block sums with portable.rs's 8-row groups give the
+    portable kernels' bits (x86.rs module docs: the sums are exact): row counts across the group
+    edges, threaded by the reference's partition, and seeded extreme codes."""
+    k = 1024 if ty == o.Q4_K else 512
+    for n_out, rows, threads in ((37, 1, 1), (64, 7, 3), (65, 8, 2), (33, 9, 4), (40, 17, 5)):
+        rng = GemvRng(n_out * 131 + rows + ty)
+        w = gemv_weights(rng, ty, n_out, k, o.f16_bits, o.round_bf16)
+        x = gemv_activations(rng, rows, k)
+        want = o.gemv(ty, w, n_out, k, x, rows)
+        got = o.gemv(ty, w, n_out, k, x, rows, threads=threads, level=1)
+        assert (bits(got) == bits(want)).all(), (n_out, rows, threads)
+    # all-extreme codes: 0x80 (-128) and 0x7F weight bytes, activations of +-127
+    nb = k // o.BLOCK_ELEMS[ty]
+    wb = np.frombuffer(np.random.default_rng(ty).bytes(16 * nb * o.BLOCK_BYTES[ty]), np.uint8).copy()
+    blocks = wb.reshape(16 * nb, o.BLOCK_BYTES[ty])
+    hdr = 4 if ty == o.Q4_K else 2
+    blocks[:, :2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+    if ty == o.Q4_K:
+        blocks[:, 2:4] = np.frombuffer(np.float16(0.02).tobytes(), np.uint8)
+    blocks[:, hdr:] = np.where(blocks[:, hdr:] & 1, 0x80, 0x7F) if ty == o.Q8_0 else blocks[:, hdr:]
+    x = np.where(np.random.default_rng(7).random(3 * k) < 0.5, -1.0, 1.0).astype(np.float32)
+    assert (bits(o.gemv(ty, wb, 16, k, x, 3, level=1)) == bits(o.gemv(ty, wb, 16, k, x, 3))).all()
+
+
+@pytest.mark.parametrize("ty", [o.Q4_K, o.Q8_0])
+def test_x86_level_moe_gives_the_portable_bits(ty):
+    n_experts, top_k, hidden, inter = MOE
+    rng, gate, up, down = moe_layer(21) if ty == o.Q4_K else q8_0_layer(21)
+    x = moe_activations(rng, 11 * hidden).reshape(11, hidden)
+    ids = moe_route_ids(rng, 11, top_k, n_experts)
+    args = (ty, ty, n_experts, top_k, hidden, inter, gate, up, down, x, ids)
+    assert (bits(o.moe_grouped(*args, threads=3, level=1)) == bits(o.moe_grouped(*args))).all()
