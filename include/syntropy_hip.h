@@ -39,6 +39,7 @@ extern "C" {
 #define SYN_LAYOUT_SOURCE 0 /* the GGUF order */
 #define SYN_LAYOUT_X8 1     /* Q4_K runs of eight super-blocks stored chunk-major */
 #define SYN_LAYOUT_SPLIT 2  /* Q8_0 / Q4_0: every block's codes, then every block's F16 scale */
+#define SYN_LAYOUT_TILE64 3 /* Q4_K rows in runs of 64, each run stored super-block-major */
 
 /* The message of the last failed call on this thread ("" if none). */
 const char* syn_last_error(void);
@@ -250,6 +251,24 @@ int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, const void*
                     uint32_t hidden, uint32_t inter, const float* x, const int32_t* ids,
                     const int32_t* site, uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
                     uint32_t* status, void* stream);
+
+/* Layout 3 (TILE64) of Q4_K rows of k_in values, in whole runs of 64 rows (a matrix, or a stack
+ * of matrices such as an MoE layer's experts, of a multiple of 64 rows): within each run, the
+ * 144-byte super-block b of the run's row r sits at 144 (64 b + r) from the run's start, so the
+ * run's block b is one contiguous 9,216-byte piece.  A permutation of the bytes (the same
+ * length, as crates/kernels/src/provider.rs:326-336 asks of a repack), but one that needs k_in:
+ * the reference's repack hook receives only the OpKey and the bytes, so the provider keeps MoE
+ * experts in GGUF order and this layout is the direct API's.
+ * syn_q4k_tile64_repack: on the device (src and dst distinct, 16-byte aligned); inverse = 1
+ *   restores the GGUF order.  syn_q4k_tile64_repack_host: the same on host memory.
+ * syn_moe_grouped_layout: MoeGrouped over experts in `layout` (0 is syn_moe_grouped; 3 for Q4_K
+ *   experts stacked as there, each stack repacked whole), the same bits as over GGUF experts. */
+int syn_q4k_tile64_repack(const void* src, void* dst, uint64_t bytes, uint32_t k_in, int32_t inverse, void* stream);
+int syn_q4k_tile64_repack_host(const void* src, void* dst, uint64_t bytes, uint32_t k_in, int32_t inverse);
+int syn_moe_grouped_layout(uint32_t layout, int32_t wtype, const void* gate, const void* up, const void* down,
+                           uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k, uint32_t hidden,
+                           uint32_t inter, const float* x, const int32_t* ids, const int32_t* site, uint32_t rows,
+                           float* out, void* ws, uint64_t ws_bytes, uint32_t* status, void* stream);
 
 /* MoeCombine: y F32 [rows, hidden] = per row, the slots of out F32 [rows, top_k, hidden] in
  * ascending expert id, y += w * v from +0.0 without fused multiply-add

@@ -70,6 +70,10 @@ def lib():
         "syn_moe_pack": [vp, u32, u32, u32, vp, vp, vp, vp],
         "syn_moe_grouped_workspace_bytes": [i32, u32, u32, u32, u32, u32, C.POINTER(C.c_uint64)],
         "syn_moe_grouped": [i32, vp, vp, vp, u64, u32, u32, u32, u32, vp, vp, vp, u32, vp, vp, u64, vp, vp],
+        "syn_moe_grouped_layout": [u32, i32, vp, vp, vp, u64, u32, u32, u32, u32, vp, vp, vp, u32, vp, vp, u64, vp,
+                                   vp],
+        "syn_q4k_tile64_repack": [vp, vp, u64, u32, i32, vp],
+        "syn_q4k_tile64_repack_host": [vp, vp, u64, u32, i32],
         "syn_moe_doorbell": [vp, u32, u32, u32, vp, vp, u32, vp, u32, vp, vp],
         "syn_moe_assign": [vp, u32, vp, u32, u32, u64, u32, vp, vp],
         "syn_moe_assign_layer": [vp, u32, vp, u32, vp, u64, u32, vp, vp],

@@ -501,6 +501,43 @@ SYN_EXPORT int syn_q4k_repack_host(uint32_t layout, const void* src, void* dst, 
 }
 
 namespace {
+int check_tile64(const char* W, const void* src, void* dst, uint64_t bytes, uint32_t k_in) {
+    if (k_in == 0 || k_in % 256 || k_in > 65536)
+        return fail(SYN_E_INVALID, "%s: k_in %u must be whole super-blocks, at most 65536", W, k_in);
+    const uint64_t run = (uint64_t)syn::TILE64_ROWS * (k_in / 256) * 144;
+    if (bytes % run)
+        return fail(SYN_E_INVALID, "%s: %llu bytes are not whole runs of 64 rows of %u values", W,
+                    (unsigned long long)bytes, k_in);
+    if (bytes && (!src || !dst)) return fail(SYN_E_INVALID, "%s: null buffer", W);
+    if (bytes && src == dst) return fail(SYN_E_INVALID, "%s: the repack is not in place", W);
+    return SYN_OK;
+}
+}  // namespace
+
+SYN_EXPORT int syn_q4k_tile64_repack(const void* src, void* dst, uint64_t bytes, uint32_t k_in, int32_t inverse,
+                                     void* stream) {
+    const char* W = "syn_q4k_tile64_repack";
+    if (int rc = check_tile64(W, src, dst, bytes, k_in)) return rc;
+    if (!aligned(src, 16) || !aligned(dst, 16)) return fail(SYN_E_INVALID, "%s: buffers must be 16-byte aligned", W);
+    syn::launch_tile64_repack((const uint8_t*)src, (uint8_t*)dst, bytes, (int)k_in, inverse != 0, (hipStream_t)stream);
+    return check_launch(W);
+}
+
+SYN_EXPORT int syn_q4k_tile64_repack_host(const void* src, void* dst, uint64_t bytes, uint32_t k_in, int32_t inverse) {
+    const char* W = "syn_q4k_tile64_repack_host";
+    if (int rc = check_tile64(W, src, dst, bytes, k_in)) return rc;
+    const uint64_t rb = (uint64_t)(k_in / 256) * 144, rows = bytes / rb;
+    const uint8_t* s = (const uint8_t*)src;
+    uint8_t* d = (uint8_t*)dst;
+    for (uint64_t r = 0; r < rows; ++r)
+        for (uint64_t b = 0; b < k_in / 256; ++b) {
+            const uint64_t g = r * rb + 144 * b, t = syn::tile64_row_offset(r, rb) + (uint64_t)syn::TILE64_ROWS * 144 * b;
+            memcpy(d + (inverse ? g : t), s + (inverse ? t : g), 144);
+        }
+    return SYN_OK;
+}
+
+namespace {
 int check_split_repack(const char* W, uint32_t layout, int32_t wtype, const void* src, void* dst, uint64_t bytes) {
     if (layout != SYN_LAYOUT_SPLIT) return fail(SYN_E_UNSUPPORTED, "%s: layout %u (2: SPLIT)", W, layout);
     if (wtype != SYN_Q8_0 && wtype != SYN_Q4_0)
@@ -1143,10 +1180,13 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
                                uint64_t expert_bytes_each, uint32_t n_experts, uint32_t top_k,
                                uint32_t hidden, uint32_t inter, const float* x, const int32_t* ids,
                                const int32_t* site, uint32_t rows, float* out, void* ws, uint64_t ws_bytes,
-                               uint32_t* status, void* stream, const uint32_t* active, uint32_t* report) {
+                               uint32_t* status, void* stream, const uint32_t* active, uint32_t* report,
+                               uint32_t layout) {
     const char* W = "syn_moe_grouped";
     if (wtype != SYN_Q4_K && wtype != SYN_Q8_0)
         return fail(SYN_E_UNSUPPORTED, "%s: expert weight type %d (Q4_K or Q8_0)", W, wtype);
+    if (layout != SYN_LAYOUT_SOURCE && !(layout == SYN_LAYOUT_TILE64 && wtype == SYN_Q4_K))
+        return fail(SYN_E_UNSUPPORTED, "%s: experts of type %d in layout %u (0, or 3 for Q4_K)", W, wtype, layout);
     if (int rc = check_moe_shape(W, n_experts, top_k, hidden, inter, rows, wtype)) return rc;
     if (rows == 0) return SYN_OK;
     if (wtype == SYN_Q8_0)
@@ -1182,10 +1222,10 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
         syn::launch_moe_tiles(offsets, (int)n_experts, err, mt, st);
         syn::launch_gemm_act(x, (int)rows, (int)hidden, gx, st, active);
         syn::launch_moe_gemm(0, (const uint8_t*)gate, (const uint8_t*)up, (int)n_experts, (int)inter, (int)hidden,
-                             gx, m.max_tiles, offsets, mt, err, slots, h, st, (int)top_k);
+                             gx, m.max_tiles, offsets, mt, err, slots, h, st, (int)top_k, (int)layout);
         syn::launch_moe_gemm_act(h, (int)inter, offsets, mt, err, gh, st);
         syn::launch_moe_gemm(1, (const uint8_t*)down, nullptr, (int)n_experts, (int)hidden, (int)inter, gh,
-                             m.max_tiles, offsets, mt, err, slots, out, st, (int)top_k);
+                             m.max_tiles, offsets, mt, err, slots, out, st, (int)top_k, (int)layout);
         if (status) {
             hipError_t e = hipMemcpyAsync(status, err, 4, hipMemcpyDeviceToDevice, st);
             if (e != hipSuccess) return fail(SYN_E_DEVICE, "%s: status copy: %s", W, hipGetErrorString(e));
@@ -1197,10 +1237,10 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
     syn::launch_moe_gather_q8k(x, slots, ent, (int)top_k, (int)hidden, err, ax, 1, st, offsets + n_experts);
     float* h = (float*)(base + m.h);
     syn::launch_moe_gateup((const uint8_t*)gate, (const uint8_t*)up, (int)n_experts, (int)hidden, (int)inter,
-                           offsets, ent, ax, err, h, st);
+                           offsets, ent, ax, err, h, st, (int)layout);
     syn::launch_moe_gather_q8k(h, slots, ent, (int)top_k, (int)inter, err, ah, 0, st, offsets + n_experts);
     syn::launch_moe_down((const uint8_t*)down, (int)n_experts, (int)hidden, (int)inter, offsets, ent, ah,
-                         slots, err, out, st);
+                         slots, err, out, st, (int)layout);
     if (status) {
         hipError_t e = hipMemcpyAsync(status, err, 4, hipMemcpyDeviceToDevice, st);
         if (e != hipSuccess) return fail(SYN_E_DEVICE, "%s: status copy: %s", W, hipGetErrorString(e));
@@ -1215,6 +1255,15 @@ SYN_EXPORT int syn_moe_grouped(int32_t wtype, const void* gate, const void* up, 
                                uint32_t* status, void* stream) {
     return syn_moe_grouped_rows(wtype, gate, up, down, expert_bytes_each, n_experts, top_k, hidden, inter, x, ids,
                                 site, rows, out, ws, ws_bytes, status, stream, nullptr);
+}
+
+SYN_EXPORT int syn_moe_grouped_layout(uint32_t layout, int32_t wtype, const void* gate, const void* up,
+                                      const void* down, uint64_t expert_bytes_each, uint32_t n_experts,
+                                      uint32_t top_k, uint32_t hidden, uint32_t inter, const float* x,
+                                      const int32_t* ids, const int32_t* site, uint32_t rows, float* out, void* ws,
+                                      uint64_t ws_bytes, uint32_t* status, void* stream) {
+    return syn_moe_grouped_rows(wtype, gate, up, down, expert_bytes_each, n_experts, top_k, hidden, inter, x, ids,
+                                site, rows, out, ws, ws_bytes, status, stream, nullptr, nullptr, layout);
 }
 
 int syn_moe_combine_rows(const float* out, const int32_t* ids, const float* w, uint32_t rows,

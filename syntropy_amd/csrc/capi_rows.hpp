@@ -4,7 +4,7 @@
 // the value the host writes before each replay; rows past it are neither computed nor written.
 // syn_moe_grouped_rows' `report`, when given, is three words of host-visible memory: the first
 // refused launch (an id that names no expert) writes 1 + the slot, the id and top_k, if word 0
-// is clear.
+// is clear.  Its `layout` is the experts' (0 GGUF order, 3 TILE64 for Q4_K).
 #pragma once
 
 #include <stdint.h>
@@ -26,7 +26,7 @@ int syn_moe_grouped_rows(int32_t wtype, const void* gate, const void* up, const 
                          uint32_t inter, const float* x, const int32_t* ids, const int32_t* site, uint32_t rows,
                          float* out, void* ws,
                          uint64_t ws_bytes, uint32_t* status, void* stream, const uint32_t* active,
-                         uint32_t* report = nullptr);
+                         uint32_t* report = nullptr, uint32_t layout = 0);
 int syn_moe_combine_rows(const float* out, const int32_t* ids, const float* w, uint32_t rows, uint32_t top_k,
                          uint32_t hidden, float* y, void* stream, const uint32_t* active);
 int syn_moe_combine_ranked_rows(const float* out, const float* w, uint32_t n_shared, const float* const* shared,

@@ -151,7 +151,7 @@ static_assert(GM_WB % 1024 == 0 && GM_AB % 1024 == 0, "wavefront-sized weight an
 
 struct GemmArgs {
     const uint8_t* W;
-    int layout;  // LAYOUT_SOURCE or LAYOUT_X8 (rows of whole 8-block runs)
+    int layout;  // LAYOUT_SOURCE, LAYOUT_X8 (rows of whole 8-block runs) or LAYOUT_TILE64 (the experts)
     const uint8_t* codes;
     const uint8_t* tail;
     float* y;
@@ -177,8 +177,10 @@ SYN_DEV GemmSlots gemm_slots(const GemmArgs& g, int wave, int lane, int n0, int 
         const int gs = wave + GM_WAVES * u;
         const int ci = 64 * gs + lane, row = ci / 9, part = ci - 9 * (ci / 9);
         const int r = n0 + row < g.N ? n0 + row : g.N - 1;
-        // chunk `part` of the row's block: 16 bytes on in GGUF order, 128 (a run's chunk row) in X8
-        s.woff[u] = (uint32_t)r * g.rb + (g.layout == LAYOUT_X8 ? 128u : 16u) * (uint32_t)part;
+        // chunk `part` of the row's block: 16 bytes on in GGUF order and TILE64, 128 (a run's chunk
+        // row) in X8
+        s.woff[u] = g.layout == LAYOUT_TILE64 ? (uint32_t)tile64_row_offset((uint32_t)r, g.rb) + 16u * (uint32_t)part
+                                               : (uint32_t)r * g.rb + (g.layout == LAYOUT_X8 ? 128u : 16u) * (uint32_t)part;
         if (gs < GM_WSLOT) s.nw = u + 1;
     }
     // tail slot: wave w takes tail part w if it exists
@@ -529,6 +531,7 @@ struct MoeGemmArgs {
     const uint32_t* slots;
     float* out;         // h [entries][cols] (MODE 0) or out [slots][cols] (MODE 1)
     int cols;           // inter (MODE 0) or hidden (MODE 1)
+    int layout;         // LAYOUT_SOURCE or LAYOUT_TILE64 (the row tiles are whole 64-row runs)
     int top_k;          // MODE 0: act holds the tokens' rows, position p of a tile reads its
                         // entry's token slots[i] / top_k
 };
@@ -553,7 +556,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
     // the weight tile's 256 rows: MODE 0 rows 0-127 of b0 then rows 0-127 of b1 (slots
     // 0..GM_WSLOT/2-1 hold exactly the first 128 rows: 128 * 9 chunks = 18 slots of 64)
     GemmArgs ga{};
-    ga.layout = LAYOUT_SOURCE;
+    ga.layout = g.layout;
     ga.N = GM_ROWS;
     ga.rb = g.rb;
     ga.codes = g.act.codes;
@@ -594,9 +597,11 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
         }
     }
     const int live = sl.nw + GM_ASLOT / GM_WAVES + (MODE == 0 ? (wave < 4 ? 1 : 0) : sl.nt);
+    // super-block b of the tile's rows: 144 b on in GGUF order, 64 rows' blocks on in TILE64
+    const size_t bstep = g.layout == LAYOUT_TILE64 ? (size_t)TILE64_ROWS * 144 : 144;
     auto issue = [&](int b, uint8_t* stage, uint8_t* tail) {
-        const uint8_t* w0 = b0 + 144 * (size_t)b;
-        const uint8_t* w1 = b1 + 144 * (size_t)b;
+        const uint8_t* w0 = b0 + bstep * (size_t)b;
+        const uint8_t* w1 = b1 + bstep * (size_t)b;
         const uint32_t st = lds_addr(stage);
 #pragma unroll
         for (int u = 0; u < GM_WPW; ++u)
@@ -683,9 +688,11 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
 
 void launch_moe_gemm(int mode, const uint8_t* w0, const uint8_t* w1, int n_experts, int rows, int k,
                      GemmAct act, int max_tiles, const uint32_t* offsets, MoeTiles mt, const uint32_t* err,
-                     const uint32_t* slots, float* out, hipStream_t stream, int top_k) {
+                     const uint32_t* slots, float* out, hipStream_t stream, int top_k, int layout) {
+    static_assert(GM_ROWS % (2 * TILE64_ROWS) == 0, "row tiles of whole TILE64 runs");
     MoeGemmArgs g;
     g.top_k = top_k;
+    g.layout = layout == LAYOUT_TILE64 ? (int)LAYOUT_TILE64 : (int)LAYOUT_SOURCE;
     g.W0 = w0;
     g.W1 = w1;
     g.nb = k / 256;

@@ -105,12 +105,12 @@ void launch_moe_gather_q8k(const float* x, const uint32_t* slots, int nentries, 
                            const uint32_t* err, MoeAct a, int gather, hipStream_t stream, const uint32_t* total = nullptr);
 void launch_moe_gateup(const uint8_t* gate, const uint8_t* up, int n_experts, int hidden,
                        int inter, const uint32_t* offsets, int nentries, MoeAct a,
-                       const uint32_t* err, float* h, hipStream_t stream);
+                       const uint32_t* err, float* h, hipStream_t stream, int layout);
 void launch_q4k_dense_rows(const uint8_t* W, int x8, int n_out, int k, MoeAct a, int rows, float* y,
                            hipStream_t stream, const uint32_t* active = nullptr);
 void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
                      const uint32_t* offsets, int nentries, MoeAct a, const uint32_t* slots,
-                     const uint32_t* err, float* out, hipStream_t stream);
+                     const uint32_t* err, float* out, hipStream_t stream, int layout);
 void launch_moe_combine(const float* out, const int32_t* ids, const float* w, int rows, int top_k,
                         int hidden, float* y, hipStream_t stream, const uint32_t* active = nullptr);
 // The shared experts' outputs MoeCombine adds after the routed slots, [rows, hidden] each.
@@ -165,10 +165,13 @@ void launch_moe_tiles(const uint32_t* offsets, int n_experts, const uint32_t* er
 void launch_moe_gemm_act(const float* h, int k, const uint32_t* offsets, MoeTiles mt, const uint32_t* err,
                          GemmAct a, hipStream_t stream);
 // mode 0 (gate/up): act holds the tokens' rows (launch_gemm_act of x), gathered per position;
-// mode 1 (down): act holds the entries' h rows at their padded positions.
+// mode 1 (down): act holds the entries' h rows at their padded positions.  The experts in GGUF
+// order or TILE64 (`layout`).
 void launch_moe_gemm(int mode, const uint8_t* w0, const uint8_t* w1, int n_experts, int rows, int k,
                      GemmAct act, int max_tiles, const uint32_t* offsets, MoeTiles mt, const uint32_t* err,
-                     const uint32_t* slots, float* out, hipStream_t stream, int top_k);
+                     const uint32_t* slots, float* out, hipStream_t stream, int top_k, int layout);
+// TILE64 <-> GGUF order of `bytes` of Q4_K rows of k values (whole 64-row runs).
+void launch_tile64_repack(const uint8_t* src, uint8_t* dst, uint64_t bytes, int k, int inverse, hipStream_t stream);
 // quant.hip
 void launch_quantize(int ty, const float* x, uint64_t n, uint8_t* out, hipStream_t stream);
 void launch_dequantize(int ty, const uint8_t* src, uint64_t n, float* out, hipStream_t stream);

@@ -75,7 +75,16 @@ SYN_HD inline ActLayout act_layout(int kind, uint64_t rows, uint64_t k) {
 //  2 SPLIT (Q8_0 and Q4_0 matrices): the codes of every block in block order (32 bytes a block
 //    for Q8_0, 16 for Q4_0), then every block's F16 scale in block order.  Also shape-free: block
 //    g's codes sit at cb g and its scale at cb nblocks + 2 g (cb = 32 or 16).
-enum : int { LAYOUT_SOURCE = 0, LAYOUT_X8 = 1, LAYOUT_SPLIT = 2 };
+//  3 TILE64 (Q4_K matrices of whole 64-row runs, and stacks of them such as an MoE layer's
+//    experts): within each run of 64 consecutive rows, super-block b of the run's row r sits at
+//    144 (64 b + r) from the run's start, so the 64 rows' block b is one contiguous 9,216-byte
+//    piece.  A permutation of the matrix bytes that needs the row length besides the byte count.
+enum : int { LAYOUT_SOURCE = 0, LAYOUT_X8 = 1, LAYOUT_SPLIT = 2, LAYOUT_TILE64 = 3 };
+constexpr int TILE64_ROWS = 64;
+// Byte offset of row r's super-block 0 in a TILE64 matrix of rb-byte rows (block b adds 9216 b).
+SYN_HD inline uint64_t tile64_row_offset(uint64_t r, uint64_t rb) {
+    return (r / TILE64_ROWS) * TILE64_ROWS * rb + (r % TILE64_ROWS) * 144;
+}
 SYN_HD inline int split_code_bytes(int ty) { return ty == T_Q8_0 ? 32 : 16; }
 SYN_HD inline uint32_t x8_group_blocks(uint64_t g, uint64_t nblocks) {
     const uint64_t first = g & ~(uint64_t)7;

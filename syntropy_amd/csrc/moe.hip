@@ -696,6 +696,30 @@ void launch_moe_gather_q8k(const float* x, const uint32_t* slots, int nentries, 
 }
 
 // ============================================================================================
+// TILE64 repack of Q4_K rows (whole 64-row runs of nb super-blocks): one thread per 16-byte chunk
+// ============================================================================================
+
+__global__ __launch_bounds__(256) void k_tile64_repack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                       uint64_t chunks, int nb, int inverse) {
+    const uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= chunks) return;
+    const uint64_t blk = c / 9;  // the block in GGUF order: row blk / nb, super-block blk % nb
+    const uint32_t q = (uint32_t)(c - blk * 9);
+    const uint64_t row = blk / (uint64_t)nb, b = blk - row * (uint64_t)nb;
+    const uint64_t at = (row / TILE64_ROWS) * TILE64_ROWS * (uint64_t)nb + b * TILE64_ROWS + row % TILE64_ROWS;
+    const uint64_t g_off = blk * 144 + 16 * q, t_off = at * 144 + 16 * q;
+    const uint64_t from = inverse ? t_off : g_off, to = inverse ? g_off : t_off;
+    *reinterpret_cast<uint4*>(dst + to) = *reinterpret_cast<const uint4*>(src + from);
+}
+
+void launch_tile64_repack(const uint8_t* src, uint8_t* dst, uint64_t bytes, int k, int inverse, hipStream_t stream) {
+    const uint64_t chunks = bytes / 16;
+    if (chunks == 0) return;
+    hipLaunchKernelGGL(k_tile64_repack, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, src, dst, chunks,
+                       k / 256, inverse);
+}
+
+// ============================================================================================
 // Grouped Q4_K product on the int8 matrix cores
 // ============================================================================================
 //
@@ -763,6 +787,7 @@ struct ItemRows {
     uint32_t row0_off;
     bool x8;
     uint64_t nblocks;  // super-blocks of the whole matrix (X8)
+    bool tiled = false;  // TILE64: block b of the item's 64 rows is one piece (row0 a multiple of 64)
 };
 
 template <class C>
@@ -792,9 +817,9 @@ SYN_DEV Slot make_slot(int s, const uint8_t* const (&bases)[C::NM], const ItemRo
             r.src = bases[m];
         } else {
             const uint32_t rrc = ir.row_max >= 0 && ir.row0 + rr > ir.row_max ? (uint32_t)(ir.row_max - ir.row0) : (uint32_t)rr;
-            r.src = bases[m] + (ir.row0_off + rrc * rb + 16u * (uint32_t)q);
+            r.src = bases[m] + (ir.row0_off + rrc * (ir.tiled ? 144u : rb) + 16u * (uint32_t)q);
         }
-        r.step = 144u;
+        r.step = ir.tiled ? (uint32_t)C::ROWS * 144u : 144u;
         r.lds = s * 1024;
     } else if (s < C::WSLOTS + C::NG) {
         // entries 4j..4j+3: position q of entry t holds its chunk q ^ (t & 3)
@@ -1022,8 +1047,9 @@ __global__ __launch_bounds__(64 * WV) void k_moe_gateup(const uint8_t* __restric
                                                         const uint8_t* __restrict__ up, int inter,
                                                         int hidden, MoeItems it, MoeAct a,
                                                         const uint32_t* __restrict__ err,
-                                                        float* __restrict__ h) {
+                                                        float* __restrict__ h, int tiled) {
     using C = MoeCfg<2, WV, CH>;
+    static_assert(C::ROWS == TILE64_ROWS, "an item's rows are one TILE64 run");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     if (err[0]) return;
     const int max_chunks = moe_max_chunks(it, err);
@@ -1037,7 +1063,8 @@ __global__ __launch_bounds__(64 * WV) void k_moe_gateup(const uint8_t* __restric
         const int64_t ebytes = (int64_t)inter * rb;
         const uint8_t* const bases[2] = {gate + e * ebytes, up + e * ebytes};
         float acc[2][C::NG] = {};
-        const ItemRows ir{rg * C::ROWS, -1, (uint32_t)(rg * C::ROWS) * rb, false, 0};
+        ItemRows ir{rg * C::ROWS, -1, (uint32_t)(rg * C::ROWS) * rb, false, 0};
+        ir.tiled = tiled != 0;
         ffn_rows<C>(bases, ir, rb, a, hidden, ent0, nent, wave, lds, acc);
         const int row = rg * C::ROWS + wave * 16 + (lane & 15);
 #pragma unroll
@@ -1049,14 +1076,15 @@ __global__ __launch_bounds__(64 * WV) void k_moe_gateup(const uint8_t* __restric
 }
 
 // down: out[slot][row] = down_row . hq[entry], written to the entry's slot (the reference's
-// scatter, moe.rs:501-515).  With it.dense (a dense Gemv of a few rows): one matrix `down` of
-// `hidden` rows (GGUF order, or X8 when x8), out[entry][row], no slots and no error word.
+// scatter, moe.rs:501-515); the experts in GGUF order or, with 64-row items, TILE64 (`layout`).
+// With it.dense (a dense Gemv of a few rows): one matrix `down` of `hidden` rows (GGUF order, or
+// X8), out[entry][row], no slots and no error word.
 template <int WV, int CH, int NS = MOE_STAGES>
 __global__ __launch_bounds__(64 * WV) void k_moe_down(const uint8_t* __restrict__ down, int hidden,
                                                       int inter, MoeItems it, MoeAct a,
                                                       const uint32_t* __restrict__ slots,
                                                       const uint32_t* __restrict__ err,
-                                                      float* __restrict__ out, int x8) {
+                                                      float* __restrict__ out, int layout) {
     using C = MoeCfg<1, WV, CH>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     if (err && err[0]) return;
@@ -1070,8 +1098,9 @@ __global__ __launch_bounds__(64 * WV) void k_moe_down(const uint8_t* __restrict_
         if (!moe_item(it, item, max_chunks, e, rg, ent0, nent)) continue;  // uniform per workgroup
         const uint8_t* const bases[1] = {down + e * ((int64_t)hidden * rb)};
         float acc[1][C::NG] = {};
-        const ItemRows ir{rg * C::ROWS, it.dense ? hidden - 1 : -1, (uint32_t)(rg * C::ROWS) * rb, x8 != 0,
-                          (uint64_t)hidden * (uint64_t)(inter / 256)};
+        ItemRows ir{rg * C::ROWS, it.dense ? hidden - 1 : -1, (uint32_t)(rg * C::ROWS) * rb, layout == LAYOUT_X8,
+                    (uint64_t)hidden * (uint64_t)(inter / 256)};
+        ir.tiled = layout == LAYOUT_TILE64;
         ffn_rows<C, NS>(bases, ir, rb, a, inter, ent0, nent, wave, lds, acc);
         const int row = rg * C::ROWS + wave * 16 + (lane & 15);
 #pragma unroll
@@ -1101,7 +1130,7 @@ constexpr int DN_WV = 4, DN_CH = 12;
 
 void launch_moe_gateup(const uint8_t* gate, const uint8_t* up, int n_experts, int hidden,
                        int inter, const uint32_t* offsets, int nentries, MoeAct a,
-                       const uint32_t* err, float* h, hipStream_t stream) {
+                       const uint32_t* err, float* h, hipStream_t stream, int layout) {
     using C = MoeCfg<2, GU_WV, GU_CH>;
     const MoeItems it{offsets, n_experts, inter / C::ROWS, C::CH, 0, nullptr};
     const int lds = MOE_STAGES * C::BYTES;
@@ -1109,20 +1138,22 @@ void launch_moe_gateup(const uint8_t* gate, const uint8_t* up, int n_experts, in
         (const void*)k_moe_gateup<GU_WV, GU_CH>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     (void)lds_ok;  // a refusal shows as the launch's error
     hipLaunchKernelGGL((k_moe_gateup<GU_WV, GU_CH>), dim3(moe_grid(it, nentries)), dim3(C::THREADS),
-                       lds, stream, gate, up, inter, hidden, it, a, err, h);
+                       lds, stream, gate, up, inter, hidden, it, a, err, h, layout == LAYOUT_TILE64 ? 1 : 0);
 }
 
 void launch_moe_down(const uint8_t* down, int n_experts, int hidden, int inter,
                      const uint32_t* offsets, int nentries, MoeAct a, const uint32_t* slots,
-                     const uint32_t* err, float* out, hipStream_t stream) {
+                     const uint32_t* err, float* out, hipStream_t stream, int layout) {
     using C = MoeCfg<1, DN_WV, DN_CH>;
+    static_assert(C::ROWS == TILE64_ROWS, "an item's rows are one TILE64 run");
     const MoeItems it{offsets, n_experts, hidden / C::ROWS, C::CH, 0, nullptr};
     const int lds = MOE_STAGES * C::BYTES;
     static const hipError_t lds_ok = hipFuncSetAttribute(
         (const void*)k_moe_down<DN_WV, DN_CH>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     (void)lds_ok;  // a refusal shows as the launch's error
     hipLaunchKernelGGL((k_moe_down<DN_WV, DN_CH>), dim3(moe_grid(it, nentries)), dim3(C::THREADS),
-                       lds, stream, down, hidden, inter, it, a, slots, err, out, 0);
+                       lds, stream, down, hidden, inter, it, a, slots, err, out,
+                       layout == LAYOUT_TILE64 ? (int)LAYOUT_TILE64 : (int)LAYOUT_SOURCE);
 }
 
 // A dense Q4_K Gemv of 2 to 31 rows on the decode expert kernel: the matrix as one expert, the
@@ -1143,7 +1174,7 @@ static void launch_dense_wv(const uint8_t* W, int x8, int n_out, int k, MoeAct a
     (void)lds_ok;  // a refusal shows as the launch's error
     const unsigned grid = (unsigned)it.row_groups * (unsigned)((rows + C::CH - 1) / C::CH);
     hipLaunchKernelGGL((k_moe_down<WV, DENSE_CH, DENSE_STAGES>), dim3(grid), dim3(C::THREADS), lds, stream, W, n_out,
-                       k, it, a, nullptr, nullptr, y, x8);
+                       k, it, a, nullptr, nullptr, y, x8 ? (int)LAYOUT_X8 : (int)LAYOUT_SOURCE);
 }
 
 // The K-split form over one dense matrix (rows of a multiple of 4 super-blocks): a workgroup of

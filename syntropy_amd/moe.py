@@ -29,25 +29,51 @@ class MoeError(ValueError):
     """Why a MoE call refused its inputs (moe.rs:148-166).  A refused call writes nothing."""
 
 
+LAYOUT_SOURCE, LAYOUT_TILE64 = 0, 3
+
+
 @dataclass
 class Experts:
-    """One layer's experts in GGUF block layout, stacked by expert (ffn_gate_exps,
-    ffn_up_exps, ffn_down_exps): gate/up [n_experts][inter, hidden], down
-    [n_experts][hidden, inter], uint8 device tensors of one weight type."""
+    """One layer's experts stacked by expert (ffn_gate_exps, ffn_up_exps, ffn_down_exps):
+    gate/up [n_experts][inter, hidden], down [n_experts][hidden, inter], uint8 device tensors of
+    one weight type, in GGUF block layout (`layout` 0) or, for Q4_K, TILE64 (3: each run of 64
+    rows stored super-block-major; `tile64` makes it)."""
 
     ty: WeightType
     gate: torch.Tensor
     up: torch.Tensor
     down: torch.Tensor
+    layout: int = LAYOUT_SOURCE
 
     def check(self, s: MoeShape):
         ty = WeightType(self.ty)
         if ty not in (WeightType.Q4K, WeightType.Q8_0):
             raise MoeError("MoeGrouped takes Q4_K or Q8_0 experts (crates/kernels-cpu/src/moe/entry.rs:50-55)")
+        if self.layout not in (LAYOUT_SOURCE, LAYOUT_TILE64) or (self.layout == LAYOUT_TILE64 and ty != WeightType.Q4K):
+            raise MoeError(f"experts of {ty.name} in layout {self.layout} (0, or 3 for Q4_K)")
         need = s.n_experts * s.inter * (s.hidden // ty.block_elems()) * ty.block_bytes()
         for name, t in (("gate", self.gate), ("up", self.up), ("down", self.down)):
             if t.dtype != torch.uint8 or t.numel() != need:
                 raise MoeError(f"`{name}` holds {t.numel()} bytes, the experts need {need}")
+
+
+def tile64_repack(w: torch.Tensor, k: int, inverse: bool = False, stream=None) -> torch.Tensor:
+    """Q4_K rows of k values, whole runs of 64 rows, GGUF order -> TILE64 (or back)."""
+    if w.dtype != torch.uint8 or not w.is_contiguous():
+        raise MoeError("the rows must be contiguous uint8")
+    out = torch.empty_like(w)
+    call("syn_q4k_tile64_repack", w.data_ptr(), out.data_ptr(), w.numel(), k, 1 if inverse else 0, _stream(stream))
+    return out
+
+
+def tile64(experts: Experts, s: MoeShape, stream=None) -> Experts:
+    """The experts repacked to TILE64 (new tensors; the GGUF ones are left as they are)."""
+    experts.check(s)
+    if experts.layout == LAYOUT_TILE64:
+        return experts
+    return Experts(experts.ty, tile64_repack(experts.gate, s.hidden, stream=stream),
+                   tile64_repack(experts.up, s.hidden, stream=stream),
+                   tile64_repack(experts.down, s.inter, stream=stream), LAYOUT_TILE64)
 
 
 def route(router: torch.Tensor, x: torch.Tensor, top_k: int, renormalize: bool = True,
@@ -86,7 +112,8 @@ def moe_grouped(s: MoeShape, experts: Experts, x: torch.Tensor, ids: torch.Tenso
                 out: torch.Tensor | None = None, ws: torch.Tensor | None = None,
                 status: torch.Tensor | None = None, stream=None,
                 site: torch.Tensor | None = None) -> torch.Tensor:
-    """MoeGrouped (moe.rs:402-518): out F32 [rows, top_k, hidden].  site (I32 [n_experts],
+    """MoeGrouped (moe.rs:402-518): out F32 [rows, top_k, hidden], the same bits in either expert
+    layout.  site (I32 [n_experts],
     optional): experts marked zero are not computed and their slots of out keep their values
     (moe/entry.rs:13-16, 297-300)."""
     experts.check(s)
@@ -103,7 +130,7 @@ def moe_grouped(s: MoeShape, experts: Experts, x: torch.Tensor, ids: torch.Tenso
     if ws is None:
         ws = torch.empty(max(workspace_bytes(s, rows, WeightType(experts.ty)), 256), dtype=torch.uint8,
                          device=x.device)
-    call("syn_moe_grouped", int(experts.ty), experts.gate.data_ptr(), experts.up.data_ptr(),
+    call("syn_moe_grouped_layout", experts.layout, int(experts.ty), experts.gate.data_ptr(), experts.up.data_ptr(),
          experts.down.data_ptr(), experts.gate.numel(), s.n_experts, s.top_k, s.hidden, s.inter,
          x.data_ptr(), ids.data_ptr(), site.data_ptr() if site is not None else None, rows,
          out.data_ptr(), ws.data_ptr(), ws.numel(),
@@ -217,6 +244,6 @@ def site_mask(layer: torch.Tensor, max_union: int, codes: torch.Tensor, n_expert
     return site
 
 
-__all__ = ["MoeShape", "MoeError", "Experts", "route", "pack", "workspace_bytes", "moe_grouped",
+__all__ = ["MoeShape", "MoeError", "Experts", "LAYOUT_SOURCE", "LAYOUT_TILE64", "tile64", "tile64_repack", "route", "pack", "workspace_bytes", "moe_grouped",
            "combine", "combine_ranked", "MoeLayer", "GemvError", "doorbell", "doorbell_bytes", "assign", "assign_layer",
            "site_mask", "HIT", "COPY", "CPU"]

@@ -225,6 +225,33 @@ static void capi_paths() {
     CHECK(syn_split_repack_host(2, SYN_Q4_0, a.data(), nullptr, 18, 0) != 0);
     CHECK(std::strlen(syn_last_error()) > 0);
 
+    // TILE64: two runs of 64 rows of 3 super-blocks; block b of row r lands at 144 (64 b + r)
+    // of its run, and the inverse restores the rows
+    {
+        const uint32_t k = 768;
+        const size_t rb = 3 * 144, bytes = 128 * rb;
+        std::vector<uint8_t> src(bytes), t(bytes), back(bytes);
+        std::mt19937_64 r64(11);
+        for (auto& v : src) v = (uint8_t)r64();
+        CHECK(syn_q4k_tile64_repack_host(src.data(), t.data(), bytes, k, 0) == 0);
+        bool placed = true;
+        for (size_t row = 0; row < 128; ++row)
+            for (size_t blk = 0; blk < 3; ++blk)
+                placed = placed && std::memcmp(t.data() + (row / 64) * 64 * rb + 144 * (64 * blk + row % 64),
+                                               src.data() + row * rb + 144 * blk, 144) == 0;
+        CHECK(placed);
+        CHECK(syn_q4k_tile64_repack_host(t.data(), back.data(), bytes, k, 1) == 0 && back == src);
+        CHECK(syn_q4k_tile64_repack_host(src.data(), t.data(), bytes - rb, k, 0) != 0);  // 127 rows
+        CHECK(syn_q4k_tile64_repack_host(src.data(), t.data(), bytes, 700, 0) != 0);
+        CHECK(syn_q4k_tile64_repack_host(src.data(), src.data(), bytes, k, 0) != 0);
+        CHECK(syn_q4k_tile64_repack_host(nullptr, t.data(), bytes, k, 0) != 0);
+        float xs[256] = {};
+        CHECK(syn_moe_grouped_layout(3, SYN_Q8_0, a.data(), a.data(), a.data(), 0, 4, 2, 256, 256, xs,
+                                     nullptr, nullptr, 1, nullptr, nullptr, 0, nullptr, nullptr) != 0);
+        CHECK(syn_moe_grouped_layout(1, SYN_Q4_K, a.data(), a.data(), a.data(), 0, 4, 2, 256, 256, xs,
+                                     nullptr, nullptr, 1, nullptr, nullptr, 0, nullptr, nullptr) != 0);
+    }
+
     // the device entry points refuse malformed arguments (on a host without a GPU, or before
     // any launch): they must return an error, not read the null buffers
     float y[4];

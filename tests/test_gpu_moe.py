@@ -156,24 +156,37 @@ def test_pack_refuses_bad_ids(M):
 
 
 # ---- grouped expert FFN ------------------------------------------------------------------------
-def run_grouped(M, shape, gate, up, down, x, ids):
+LAYOUTS = (0, 3)  # the experts in GGUF order and in TILE64
+
+
+def tile64_numpy(w, k):
+    """TILE64 by its definition: each run of 64 rows of k / 256 super-blocks, block-major."""
+    return w.reshape(-1, 64, k // 256, 144).transpose(0, 2, 1, 3).ravel()
+
+
+def run_grouped(M, shape, gate, up, down, x, ids, layout=0):
     ex = M.Experts(12, dev(gate), dev(up), dev(down))
+    if layout:
+        ex = M.tile64(ex, shape)
+        assert ex.layout == layout
     out = torch.full((ids.shape[0], shape.top_k, shape.hidden), float("nan"), device="cuda")
     st = torch.full((1,), 7, dtype=torch.int32, device="cuda")
     M.moe_grouped(shape, ex, dev(x), dev(ids), out=out, status=st)
     return host(out), int(host(st)[0])
 
 
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("rows", [1, 2, 5, 8, 9, 17, 40])
-def test_grouped_equals_oracle_reference_shape(M, rows):
-    """crates/kernels-cpu/src/moe/tests.rs:227-236 shape: 6 experts, top-2, hidden 256, inter 512."""
+def test_grouped_equals_oracle_reference_shape(M, rows, layout):
+    """crates/kernels-cpu/src/moe/tests.rs:227-236 shape: 6 experts, top-2, hidden 256, inter 512;
+    the experts in GGUF order and in TILE64."""
     s = M.MoeShape(6, 2, 256, 512)
     gate, up, down = random_q4k_experts(1, s.n_experts, s.hidden, s.inter)
     rng = MoeRng(100 + rows)
     x = moe_activations(rng, rows * s.hidden).reshape(rows, s.hidden)
     ids = moe_route_ids(rng, rows, s.top_k, s.n_experts)
-    announce(f"grouped ref-shape rows={rows}")
-    got, st = run_grouped(M, s, gate, up, down, x, ids)
+    announce(f"grouped ref-shape rows={rows} layout={layout}")
+    got, st = run_grouped(M, s, gate, up, down, x, ids, layout)
     want = o.moe_grouped(o.Q4_K, o.Q4_K, 6, 2, 256, 512, gate, up, down, x, ids)
     assert st == 0
     assert_same(got, want, f"rows {rows}")
@@ -191,10 +204,12 @@ def test_grouped_layer_shape_64_tokens(M):
     ids = host(ids_d)
     wids, ww, _ = o.moe_route(router, x, s.n_experts, s.top_k, True)
     assert (ids == wids).all()
-    got, st = run_grouped(M, s, gate, up, down, x, ids)
-    assert st == 0
     want = o.moe_grouped(o.Q4_K, o.Q4_K, 128, 8, 4096, 1536, gate, up, down, x, ids, threads=16)
-    assert_same(got, want, "layer slots")
+    for layout in LAYOUTS:
+        announce(f"grouped layer shape 64 tokens layout={layout}")
+        got, st = run_grouped(M, s, gate, up, down, x, ids, layout)
+        assert st == 0
+        assert_same(got, want, f"layer slots, layout {layout}")
     y = host(M.combine(dev(got), dev(ids), dev(ww)))
     assert_same(y, o.moe_combine(want, ids, ww), "combined")
 
@@ -218,11 +233,12 @@ def test_moe_layer_2048_skewed_tokens(M):
     assert_same(host(w_d), ww, "weights")
     loads = np.sort(np.bincount(ids.ravel(), minlength=s.n_experts))[::-1]
     assert (loads[:3] >= 4 * T * s.top_k / s.n_experts).all(), loads[:4]
-    announce("moe layer 2048 skewed tokens: grouped")
-    got, st = run_grouped(M, s, gate, up, down, x, ids)
-    assert st == 0
     want = o.moe_grouped(o.Q4_K, o.Q4_K, 128, 8, 4096, 1536, gate, up, down, x, ids, threads=16)
-    assert_same(got, want, "slots")
+    for layout in LAYOUTS:
+        announce(f"moe layer 2048 skewed tokens: grouped, layout={layout}")
+        got, st = run_grouped(M, s, gate, up, down, x, ids, layout)
+        assert st == 0
+        assert_same(got, want, f"slots, layout {layout}")
     announce("moe layer 2048 skewed tokens: combine")
     y = host(M.combine(dev(got), dev(ids), dev(ww)))
     assert_same(y, o.moe_combine(want, ids, ww), "combined")
@@ -260,11 +276,12 @@ def test_grouped_decode_path_heavy_expert(M):
     ids[35] = [0, 2]
     counts = np.bincount(ids.ravel(), minlength=s.n_experts)
     assert counts[3] == 35 and counts[:3].sum() % 4 == 2  # expert 3's entries start at 6
-    announce("grouped decode path heavy expert")
-    got, st = run_grouped(M, s, gate, up, down, x, ids)
     want = o.moe_grouped(o.Q4_K, o.Q4_K, 16, 2, 512, 768, gate, up, down, x, ids)
-    assert st == 0
-    assert_same(got, want)
+    for layout in LAYOUTS:
+        announce(f"grouped decode path heavy expert layout={layout}")
+        got, st = run_grouped(M, s, gate, up, down, x, ids, layout)
+        assert st == 0
+        assert_same(got, want, f"layout {layout}")
 
 
 def test_grouped_row_permutation(M):
@@ -297,11 +314,12 @@ def test_grouped_gemm_path_equals_oracle(M, rows):
     rng = MoeRng(300 + rows)
     x = moe_activations(rng, rows * s.hidden).reshape(rows, s.hidden)
     ids = moe_route_ids(rng, rows, s.top_k, s.n_experts)
-    announce(f"grouped gemm path rows={rows}")
-    got, st = run_grouped(M, s, gate, up, down, x, ids)
     want = o.moe_grouped(o.Q4_K, o.Q4_K, 6, 2, 256, 512, gate, up, down, x, ids)
-    assert st == 0
-    assert_same(got, want, f"rows {rows}")
+    for layout in LAYOUTS:
+        announce(f"grouped gemm path rows={rows} layout={layout}")
+        got, st = run_grouped(M, s, gate, up, down, x, ids, layout)
+        assert st == 0
+        assert_same(got, want, f"rows {rows}, layout {layout}")
 
 
 def test_grouped_gemm_path_skewed_and_empty_experts(M):
@@ -320,11 +338,12 @@ def test_grouped_gemm_path_skewed_and_empty_experts(M):
                 ids[r, j] = next(e for e in range(12) if e not in ids[r])
     cnt = np.bincount(ids.ravel(), minlength=16)
     assert cnt[3] >= 150 and (cnt[12:] == 0).all()
-    announce("grouped gemm path skewed")
-    got, st = run_grouped(M, s, gate, up, down, x, ids)
     want = o.moe_grouped(o.Q4_K, o.Q4_K, 16, 4, 1024, 512, gate, up, down, x, ids, threads=8)
-    assert st == 0
-    assert_same(got, want, "skewed")
+    for layout in LAYOUTS:
+        announce(f"grouped gemm path skewed layout={layout}")
+        got, st = run_grouped(M, s, gate, up, down, x, ids, layout)
+        assert st == 0
+        assert_same(got, want, f"skewed, layout {layout}")
 
 
 def test_grouped_gemm_path_refusal_writes_nothing(M):
@@ -334,10 +353,11 @@ def test_grouped_gemm_path_refusal_writes_nothing(M):
     x = np.ones((rows, 256), np.float32)
     ids = np.tile(np.array([[0, 1]], np.int32), (rows, 1))
     ids[41, 1] = 4
-    announce("grouped gemm path bad id")
-    got, st = run_grouped(M, s, gate, up, down, x, ids)
-    assert st == 1
-    assert np.isnan(got).all()
+    for layout in LAYOUTS:
+        announce(f"grouped gemm path bad id layout={layout}")
+        got, st = run_grouped(M, s, gate, up, down, x, ids, layout)
+        assert st == 1
+        assert np.isnan(got).all()
 
 
 def test_grouped_refusal_writes_nothing(M):
@@ -345,10 +365,11 @@ def test_grouped_refusal_writes_nothing(M):
     gate, up, down = random_q4k_experts(3, s.n_experts, s.hidden, s.inter)
     x = np.ones((3, 256), np.float32)
     ids = np.array([[0, 1], [2, 6], [3, 4]], np.int32)
-    announce("grouped bad id")
-    got, st = run_grouped(M, s, gate, up, down, x, ids)
-    assert st == 1
-    assert np.isnan(got).all()
+    for layout in LAYOUTS:
+        announce(f"grouped bad id layout={layout}")
+        got, st = run_grouped(M, s, gate, up, down, x, ids, layout)
+        assert st == 1
+        assert np.isnan(got).all()
 
 
 @pytest.mark.parametrize("rows,n_experts,top_k", [(3, 256, 1), (40, 256, 8), (300, 4, 1)])
@@ -387,21 +408,55 @@ def test_grouped_site_mask(M, rows, n_experts, top_k, hidden, inter):
     site = (rs.random(n_experts) < 0.5).astype(np.int32)
     site[ids[0, 0]] = 1
     site[ids[0, 1]] = 0
-    ex = M.Experts(12, dev(gate), dev(up), dev(down))
-    out = torch.full((rows, top_k, hidden), SENTINEL, dtype=torch.int32, device="cuda").view(torch.float32)
-    st = torch.full((1,), 7, dtype=torch.int32, device="cuda")
-    announce(f"grouped site rows={rows} E={n_experts} k={top_k} hidden={hidden} inter={inter}")
-    M.moe_grouped(s, ex, dev(x), dev(ids), out=out, status=st, site=dev(site))
-    got = host(out)
-    assert int(host(st)[0]) == 0
     args = (o.Q4_K, o.Q4_K, n_experts, top_k, hidden, inter, gate, up, down, x, ids)
     want = o.moe_grouped(*args, site=site, threads=8,
                          out=np.full(rows * top_k * hidden, SENTINEL, np.uint32).view(np.float32))
-    assert_same(got, want, "masked")
+    want_all = o.moe_grouped(*args, threads=8)
     kept = site[ids] == 0
-    assert (got[kept].view(np.uint32) == SENTINEL).all()
-    M.moe_grouped(s, ex, dev(x), dev(ids), out=out, status=st, site=dev(1 - site))
-    assert_same(host(out), o.moe_grouped(*args, threads=8), "both sites")
+    ex0 = M.Experts(12, dev(gate), dev(up), dev(down))
+    for ex in (ex0, M.tile64(ex0, s)):
+        out = torch.full((rows, top_k, hidden), SENTINEL, dtype=torch.int32, device="cuda").view(torch.float32)
+        st = torch.full((1,), 7, dtype=torch.int32, device="cuda")
+        announce(f"grouped site rows={rows} E={n_experts} k={top_k} hidden={hidden} inter={inter} "
+                 f"layout={ex.layout}")
+        M.moe_grouped(s, ex, dev(x), dev(ids), out=out, status=st, site=dev(site))
+        got = host(out)
+        assert int(host(st)[0]) == 0
+        assert_same(got, want, f"masked, layout {ex.layout}")
+        assert (got[kept].view(np.uint32) == SENTINEL).all()
+        M.moe_grouped(s, ex, dev(x), dev(ids), out=out, status=st, site=dev(1 - site))
+        assert_same(host(out), want_all, f"both sites, layout {ex.layout}")
+
+
+# ---- the TILE64 expert layout ---------------------------------------------------------------------
+@pytest.mark.parametrize("rows,k", [(64, 256), (128, 768), (3 * 1536, 4096)])
+def test_tile64_repack_matches_definition_and_inverts(M, rows, k):
+    """The device repack places each run's block b of row r at 144 (64 b + r), as the host repack
+    does, and its inverse restores the GGUF rows (one stack of 3 experts' gate rows last)."""
+    rs = np.random.default_rng(rows + k)
+    w = np.frombuffer(rs.bytes(rows * k // 256 * 144), np.uint8).copy()
+    announce(f"tile64 repack rows={rows} k={k}")
+    t = M.tile64_repack(dev(w), k)
+    want = tile64_numpy(w, k)
+    assert (host(t) == want).all()
+    from syntropy_amd._lib import lib
+    viahost = np.empty_like(w)
+    assert lib().syn_q4k_tile64_repack_host(w.ctypes.data, viahost.ctypes.data, w.size, k, 0) == 0
+    assert (viahost == want).all()
+    assert (host(M.tile64_repack(t, k, inverse=True)) == w).all()
+
+
+def test_tile64_refusals(M):
+    """Rows that are not whole 64-row runs, and TILE64 for Q8_0 experts, are refused before any
+    launch."""
+    w = torch.zeros(100 * 144, dtype=torch.uint8, device="cuda")
+    with pytest.raises(Exception, match="whole runs of 64 rows"):
+        M.tile64_repack(w, 256)
+    s = M.MoeShape(4, 2, 256, 256)
+    q8 = torch.zeros(4 * 256 * 8 * 34, dtype=torch.uint8, device="cuda")
+    with pytest.raises(M.MoeError, match="layout 3"):
+        M.moe_grouped(s, M.Experts(8, q8, q8, q8, M.LAYOUT_TILE64), torch.zeros(1, 256, device="cuda"),
+                      torch.zeros(1, 2, dtype=torch.int32, device="cuda"))
 
 
 # ---- combine ------------------------------------------------------------------------------------
