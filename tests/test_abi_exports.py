@@ -115,3 +115,30 @@ def test_split_host_repack_is_its_definition_and_inverts():
         assert lib.syn_split_repack_host(1, ty, b.ctypes.data, got.ctypes.data, b.size, 0) == 2
         assert lib.syn_split_repack_host(2, ty, b.ctypes.data, got.ctypes.data, b.size - 1, 0) == 1
     assert lib.syn_split_repack_host(2, 12, b.ctypes.data, got.ctypes.data, 144, 0) == 2
+
+
+def test_tile64_host_repack_is_its_definition_and_inverts():
+    """The host repack of the TILE64 layout (within each run of 64 rows, super-block b of row r at
+    144 (64 b + r)) against an element-wise placement loop, and the inverse; stacks of one and
+    three runs, rows of 1, 6 and 16 super-blocks; lengths that are not whole runs are refused."""
+    import numpy as np
+    import torch  # noqa: F401
+    lib = ctypes.CDLL(LIB)
+    lib.syn_q4k_tile64_repack_host.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                               ctypes.c_uint32, ctypes.c_int32]
+    for nb, runs in ((1, 1), (6, 3), (16, 2)):
+        rows, rb = 64 * runs, nb * 144
+        b = np.random.default_rng(nb * 10 + runs).integers(0, 256, rows * rb, dtype=np.uint8)
+        want = np.empty_like(b)
+        for r in range(rows):
+            for j in range(nb):
+                at = (r // 64) * 64 * rb + 144 * (64 * j + r % 64)
+                want[at:at + 144] = b[r * rb + 144 * j:r * rb + 144 * (j + 1)]
+        got = np.empty_like(b)
+        assert lib.syn_q4k_tile64_repack_host(b.ctypes.data, got.ctypes.data, b.size, 256 * nb, 0) == 0
+        assert (got == want).all()
+        back = np.empty_like(b)
+        assert lib.syn_q4k_tile64_repack_host(got.ctypes.data, back.ctypes.data, b.size, 256 * nb, 1) == 0
+        assert (back == b).all()
+    assert lib.syn_q4k_tile64_repack_host(b.ctypes.data, got.ctypes.data, b.size - rb, 256 * nb, 0) == 1
+    assert lib.syn_q4k_tile64_repack_host(b.ctypes.data, got.ctypes.data, b.size, 300, 0) == 1
