@@ -19,8 +19,9 @@ events on its stream, and the CPU oracle timed on this host's cores; beside it:
     rows_2_8 (Q4_K at 2, 4 and 8 rows against one row);
   * moe (the MoE layer at 64 decode tokens) and prefill (the 2048-token dense GEMMs on the matrix
     cores and the skewed MoE layer);
-  * read_floor: a bare read of each decode op's byte count (syn_hbm_read_probe, the decode GEMV's
-    load pattern with no arithmetic), timed like the ops: what one launch of that size costs.
+  * read_floor: a bare read of each decode op's byte count (the fastest of three read shapes, two of
+    them the decode GEMV's own wavefront pattern with no arithmetic), timed like the ops: what one
+    launch of that size costs.
 --only runs one part (for the profiler); `copy` and `calib` run the counter calibration kernels.
 """
 from __future__ import annotations
@@ -682,11 +683,15 @@ def bench_prefill(torch, S, M, steps, warmup, cpu_seconds):
 
 # ---- counter calibration kernels --------------------------------------------------------------------
 def bench_read_floor(torch, nrep):
-    """A bare read (syn_hbm_read_probe) of each decode op's weight bytes, launched back to back
-    over copies that together exceed the Infinity Cache: the time one launch of that many bytes
-    takes with no arithmetic, against which a lone op's time is measured."""
+    """A bare read of each decode op's weight bytes, launched back to back over copies that
+    together exceed the Infinity Cache, in three shapes: syn_hbm_read_probe (one 16-byte load a
+    lane, 4 KB a workgroup) and syn_hbm_read_runs at 1 and 8 wavefronts a workgroup (the X8 decode
+    GEMV's own wavefront pattern, 9 KB a wavefront).  The fastest is the time one launch of that
+    many bytes takes with no arithmetic, against which an op's time is measured."""
     f = S_lib().syn_hbm_read_probe_sink_words
     f.argtypes, f.restype = [C.c_uint64], C.c_uint64
+    g = S_lib().syn_hbm_read_runs_sink_words
+    g.argtypes, g.restype = [C.c_uint64], C.c_uint64
     sizes = {"O 4096x4096 Q4_K / Cfg1 Q4_0 4096x4096": 4096 * row_bytes(Q4K, 4096),
              "QKV 6144x4096 Q4_K": 6144 * row_bytes(Q4K, 4096),
              "gate, up or down Q4_K": 14336 * row_bytes(Q4K, 4096),
@@ -699,15 +704,23 @@ def bench_read_floor(torch, nrep):
         nbytes = nbytes // 16 * 16
         ncopies = max(3, -(-2 * MALL_BYTES // nbytes))
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(c) for c in range(ncopies)]
-        sink = torch.empty(f(nbytes), dtype=torch.int32, device="cuda")
-
-        def go(i):
-            rc = S_lib().syn_hbm_read_probe(bufs[i % ncopies].data_ptr(), nbytes, sink.data_ptr(), stream)
-            assert rc == 0
-        go(0)
-        us = gpu_us(torch, go, nrep)
-        out[name] = {"bytes": nbytes, "us": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-                     "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        sink = torch.empty(max(f(nbytes), g(nbytes)), dtype=torch.int32, device="cuda")
+        shapes = {}
+        for shape in ("probe", "runs1", "runs8"):
+            def go(i, shape=shape):
+                src = bufs[i % ncopies].data_ptr()
+                if shape == "probe":
+                    rc = S_lib().syn_hbm_read_probe(src, nbytes, sink.data_ptr(), stream)
+                else:
+                    rc = S_lib().syn_hbm_read_runs(1 if shape == "runs1" else 8, src, nbytes, sink.data_ptr(), stream)
+                assert rc == 0
+            go(0)
+            shapes[shape] = round(gpu_us(torch, go, nrep), 3)
+        best = min(shapes, key=shapes.get)
+        us = shapes[best]
+        out[name] = {"bytes": nbytes, "us": us, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "shape": best,
+                     "us_by_shape": shapes}
         del bufs, sink
     torch.cuda.empty_cache()
     return out

@@ -155,6 +155,13 @@ int syn_gate_up_act(uint32_t layout, int32_t wtype, const void* w, uint64_t w_by
  * set a lone op of the same bytes against.  No counterpart in the reference. */
 uint64_t syn_hbm_read_probe_sink_words(uint64_t bytes);
 int syn_hbm_read_probe(const void* src, uint64_t bytes, uint32_t* sink, void* stream);
+/* syn_hbm_read_runs: reads `bytes` once with the X8 decode GEMV's wavefront pattern (a wavefront
+ * per 9,216 bytes: nine 16-byte non-temporal loads a lane, instruction i reading line i of eight
+ * 1,152-byte runs), `waves` (1 or 8) wavefronts a workgroup; one word per wavefront to sink
+ * (syn_hbm_read_runs_sink_words(bytes) words).  The bare read a lone op or the grouped GEMV is
+ * set against, beside syn_hbm_read_probe.  No counterpart in the reference. */
+uint64_t syn_hbm_read_runs_sink_words(uint64_t bytes);
+int syn_hbm_read_runs(uint32_t waves, const void* src, uint64_t bytes, uint32_t* sink, void* stream);
 
 /* ---- RmsNorm and Logits ----------------------------------------------------------------------
  * syn_rms_norm: y = RmsNorm(x) of each of `rows` rows of n F32 values (n <= 16384), weight g [n]:

@@ -881,6 +881,18 @@ SYN_EXPORT int syn_hbm_read_probe(const void* src, uint64_t bytes, uint32_t* sin
     return check_launch(W);
 }
 
+SYN_EXPORT uint64_t syn_hbm_read_runs_sink_words(uint64_t bytes) { return syn::hbm_read_runs_units(bytes); }
+
+SYN_EXPORT int syn_hbm_read_runs(uint32_t waves, const void* src, uint64_t bytes, uint32_t* sink, void* stream) {
+    const char* W = "syn_hbm_read_runs";
+    if (waves != 1 && waves != 8) return fail(SYN_E_UNSUPPORTED, "%s: %u wavefronts a workgroup (1 or 8)", W, waves);
+    if (bytes % 16) return fail(SYN_E_INVALID, "%s: %llu bytes are not whole 16-byte chunks", W, (unsigned long long)bytes);
+    if (bytes && (!src || !sink)) return fail(SYN_E_INVALID, "%s: null operand", W);
+    if (!aligned(src, 16) || !aligned(sink, 4)) return fail(SYN_E_INVALID, "%s: src must be 16-byte aligned", W);
+    syn::launch_hbm_read_runs((int)waves, (const uint8_t*)src, bytes, sink, (hipStream_t)stream);
+    return check_launch(W);
+}
+
 // ---- RmsNorm and Logits ------------------------------------------------------------------
 
 SYN_EXPORT int syn_rms_norm(const float* x, const float* g, uint32_t rows, uint32_t n, float eps, float* y,

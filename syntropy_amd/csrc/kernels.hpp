@@ -74,6 +74,8 @@ void launch_gemv_split_fused(int ty, const uint8_t* W, int n_out, int k, const f
 // probe.hip: a read-only HBM stream with the decode GEMV's load pattern (counter calibration)
 void launch_hbm_read_probe(const uint8_t* src, uint64_t bytes, uint32_t* sink, hipStream_t stream);
 uint64_t hbm_read_probe_workgroups(uint64_t bytes);
+uint64_t hbm_read_runs_units(uint64_t bytes);
+void launch_hbm_read_runs(int waves, const uint8_t* src, uint64_t bytes, uint32_t* sink, hipStream_t stream);
 // norm.hip: RmsNorm rows of at most NORM_MAX_COLS values
 constexpr int NORM_MAX_COLS = 16384;
 void launch_rms_norm(const float* x, const float* g, int rows, int n, float eps, float* y, hipStream_t stream,

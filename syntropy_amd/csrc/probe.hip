@@ -34,6 +34,41 @@ __global__ __launch_bounds__(256) void k_hbm_read_probe(const uint8_t* __restric
     if (threadIdx.x == 0) sink[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
 
+// The decode GEMV's wavefront pattern over X8 weights: a wavefront reads 9,216 bytes (eight
+// 1,152-byte runs) with nine loads a lane, instruction i reading line i of every run; WAVES
+// wavefronts a workgroup.  Each wavefront writes one word (its unit's) to sink.
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_hbm_read_runs(const uint8_t* __restrict__ src, uint64_t bytes,
+                                                              uint32_t* __restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t unit = (uint64_t)blockIdx.x * WAVES + (threadIdx.x >> 6);
+    const uint64_t base = unit * 9216 + (uint64_t)(lane >> 3) * 1152 + 16 * (uint64_t)(lane & 7);
+    uint32_t acc = 0;
+    v4u_p v[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+        const uint64_t off = base + 128 * (uint64_t)i;
+        v[i] = off < bytes ? __builtin_nontemporal_load(reinterpret_cast<const v4u_p*>(src + off)) : v4u_p{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < 9; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, m);
+    if (lane == 0 && unit * 9216 < bytes) sink[unit] = acc;
+}
+
+uint64_t hbm_read_runs_units(uint64_t bytes) { return (bytes + 9215) / 9216; }
+
+void launch_hbm_read_runs(int waves, const uint8_t* src, uint64_t bytes, uint32_t* sink, hipStream_t stream) {
+    const uint64_t units = hbm_read_runs_units(bytes);
+    if (units == 0) return;
+    if (waves == 1)
+        hipLaunchKernelGGL(k_hbm_read_runs<1>, dim3((unsigned)units), dim3(64), 0, stream, src, bytes, sink);
+    else
+        hipLaunchKernelGGL(k_hbm_read_runs<8>, dim3((unsigned)((units + 7) / 8)), dim3(512), 0, stream, src, bytes,
+                           sink);
+}
+
 int hbm_read_probe_loads(uint64_t bytes) { return bytes >= (256ull << 20) ? 9 : 1; }
 
 uint64_t hbm_read_probe_workgroups(uint64_t bytes) {
