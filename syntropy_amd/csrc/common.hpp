@@ -142,28 +142,52 @@ template <int CTRL>
 SYN_DEV uint32_t dpp_u32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
 }
-template <int CTRL>
-SYN_DEV uint64_t dpp_u64(uint64_t v) {
-    return ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
-}
-SYN_DEV uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-// the maximum over groups of G = 8, 16 or 64 lanes
-template <int G>
-SYN_DEV uint64_t group_max_u64(uint64_t k) {
-    k = umax64(k, dpp_u64<DPP_XOR1>(k));
-    k = umax64(k, dpp_u64<DPP_XOR2>(k));
-    k = umax64(k, dpp_u64<DPP_HALF_MIRROR>(k));
-    if constexpr (G >= 16) k = umax64(k, dpp_u64<DPP_MIRROR>(k));
+// the maximum / minimum of 32-bit words over groups of G = 8, 16 or 64 lanes
+template <int G, bool MIN>
+SYN_DEV uint32_t group_ext_u32(uint32_t k) {
+    auto op = [](uint32_t a, uint32_t b) { return MIN ? (a < b ? a : b) : (a > b ? a : b); };
+    k = op(k, dpp_u32<DPP_XOR1>(k));
+    k = op(k, dpp_u32<DPP_XOR2>(k));
+    k = op(k, dpp_u32<DPP_HALF_MIRROR>(k));
+    if constexpr (G >= 16) k = op(k, dpp_u32<DPP_MIRROR>(k));
     if constexpr (G == 64) {
-        const auto l1 = __builtin_amdgcn_permlane16_swap((uint32_t)k, (uint32_t)k, false, false);
-        const auto h1 = __builtin_amdgcn_permlane16_swap((uint32_t)(k >> 32), (uint32_t)(k >> 32), false, false);
-        k = umax64(((uint64_t)h1[0] << 32) | l1[0], ((uint64_t)h1[1] << 32) | l1[1]);
-        const auto l2 = __builtin_amdgcn_permlane32_swap((uint32_t)k, (uint32_t)k, false, false);
-        const auto h2 = __builtin_amdgcn_permlane32_swap((uint32_t)(k >> 32), (uint32_t)(k >> 32), false, false);
-        k = umax64(((uint64_t)h2[0] << 32) | l2[0], ((uint64_t)h2[1] << 32) | l2[1]);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(k, k, false, false);
+        k = op(s1[0], s1[1]);
+        const auto s2 = __builtin_amdgcn_permlane32_swap(k, k, false, false);
+        k = op(s2[0], s2[1]);
     }
     return k;
 }
+template <int G>
+SYN_DEV uint32_t group_max_u32(uint32_t k) { return group_ext_u32<G, false>(k); }
+template <int G>
+SYN_DEV uint32_t group_min_u32(uint32_t k) { return group_ext_u32<G, true>(k); }
+
+// The signed maximum of a Q8_K block held N values a lane by G lanes (value i of the lane is the
+// block's value G0 + i): the largest magnitude, the first index on equal magnitudes, and that
+// value's sign.  Magnitudes compare as their bits (non-negative F32 patterns order as their
+// values); `bad` is a NaN or an infinity anywhere in the block (its magnitude bits are the
+// largest).  The first index is the smallest (index << 1 | sign) among the values of the
+// largest magnitude.
+template <int G, int N>
+SYN_DEV void block_signed_amax(const float (&v)[N], int i0, float& amax, float& mx, bool& bad) {
+    uint32_t mag[N], m = 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        mag[i] = f2u(v[i]) & 0x7FFFFFFFu;
+        m = m > mag[i] ? m : mag[i];
+    }
+    m = group_max_u32<G>(m);
+    uint32_t key = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = N - 1; i >= 0; --i)
+        key = mag[i] == m ? (((uint32_t)(i0 + i) << 1) | (f2u(v[i]) >> 31)) : key;
+    key = group_min_u32<G>(key);
+    bad = m >= 0x7F800000u;
+    amax = u2f(m);
+    mx = (key & 1u) ? -amax : amax;
+}
+
 // the sum (or the or: OR = true) over groups of 8 lanes
 template <bool OR = false>
 SYN_DEV int group8_sum(int s) {
@@ -172,14 +196,6 @@ SYN_DEV int group8_sum(int s) {
     s = op(s, (int)dpp_u32<DPP_XOR2>((uint32_t)s));
     return op(s, (int)dpp_u32<DPP_HALF_MIRROR>((uint32_t)s));
 }
-// The key that orders candidates of a signed-maximum search: magnitude bits, then the first
-// index on equal magnitudes, then the sign (one candidate per index).  Non-negative F32 bit
-// patterns order as their values.
-SYN_DEV uint64_t amax_key(float v, int idx) {
-    return ((uint64_t)(f2u(v) & 0x7FFFFFFFu) << 32) | ((uint64_t)(0xFFFF - idx) << 1) | (f2u(v) >> 31);
-}
-SYN_DEV float key_amax(uint64_t k) { return u2f((uint32_t)(k >> 32)); }
-SYN_DEV float key_value(uint64_t k) { return (k & 1) ? -key_amax(k) : key_amax(k); }
 
 // Q8_K of one 256-value block (crates/kernels-cpu/src/gemv/act.rs:351-373): largest
 // magnitude, first index on ties, ggml's nearest_int; non-finite block -> scale NaN, codes 0.
@@ -193,18 +209,13 @@ struct Q8KLane {
 SYN_DEV Q8KLane q8k_block_lane(const float* __restrict__ xb, int lane) {
     const float4 v4 = reinterpret_cast<const float4*>(xb)[lane];
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    const bool fin = finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3]);
-    const bool all_finite = __all(fin);
-    // Largest magnitude, the first index on a tie (amax desc, index asc), as the largest key
-    // (an all-zero block gives amax 0; a non-finite one is decided by all_finite)
-    uint64_t key = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) key = umax64(key, amax_key(v[i], lane * 4 + i));
-    key = group_max_u64<64>(key);
-    const float amax = key_amax(key), mx = key_value(key);
+    // largest magnitude, the first index on a tie (an all-zero block gives amax 0)
+    float amax, mx;
+    bool bad;
+    block_signed_amax<64>(v, lane * 4, amax, mx, bad);
     float d = 0.0f;
     int q[4] = {0, 0, 0, 0};
-    if (!all_finite) {
+    if (bad) {
         d = __builtin_nanf("");
     } else if (amax != 0.0f) {
         const float iscale = -127.0f / mx;
@@ -237,16 +248,16 @@ struct Q8_0Lane {
 };
 SYN_DEV Q8_0Lane q8_0_block_lane(float4 v4) {
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    const int bad = group8_sum<true>(!(finite_f(v[0]) && finite_f(v[1]) && finite_f(v[2]) && finite_f(v[3])));
-    // the largest magnitude by its bits (non-negative F32 patterns order as their values; a
-    // block holding a NaN or an infinity is `bad` and its amax unused)
+    // the largest magnitude by its bits (non-negative F32 patterns order as their values); a
+    // NaN or an infinity has the largest bits, so the block is `bad` and its amax unused
     uint32_t ab = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t a = f2u(v[i]) & 0x7FFFFFFFu;
         ab = ab > a ? ab : a;
     }
-    ab = (uint32_t)(group_max_u64<8>(ab) & 0xFFFFFFFFu);
+    ab = group_max_u32<8>(ab);
+    const bool bad = ab >= 0x7F800000u;
     const float amax = u2f(ab);
     int q[4] = {0, 0, 0, 0};
     Q8_0Lane r;

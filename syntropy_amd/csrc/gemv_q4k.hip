@@ -59,17 +59,10 @@ SYN_DEV void load_block16(const float* __restrict__ x, int c, float (&v)[16]) {
 
 SYN_DEV void quant16_to_lds(const float (&v)[16], int c, int nb, uint8_t* lds) {
     const int sb = c >> 4, part = c & 15;
-    bool fin = true;
-    uint64_t key = 0;  // largest magnitude, the first index on a tie (amax_key)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        fin = fin && finite_f(v[i]);
-        key = umax64(key, amax_key(v[i], part * 16 + i));
-    }
-    key = group_max_u64<16>(key);
-    // any non-finite value in the 16 lanes
-    const int bad = (int)(group_max_u64<16>(fin ? 0u : 1u) & 1u);
-    const float amax = key_amax(key), mx = key_value(key);
+    // largest magnitude, the first index on a tie; any non-finite value in the 16 lanes
+    float amax, mx;
+    bool bad;
+    block_signed_amax<16>(v, part * 16, amax, mx, bad);
     float d = 0.0f;
     int q[16];
 #pragma unroll
