@@ -206,8 +206,7 @@ struct Q8KLane {
     int sum32;
     float d;
 };
-SYN_DEV Q8KLane q8k_block_lane(const float* __restrict__ xb, int lane) {
-    const float4 v4 = reinterpret_cast<const float4*>(xb)[lane];
+SYN_DEV Q8KLane q8k_block_lane(float4 v4, int lane) {
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
     // largest magnitude, the first index on a tie (an all-zero block gives amax 0)
     float amax, mx;
@@ -234,6 +233,9 @@ SYN_DEV Q8KLane q8k_block_lane(const float* __restrict__ xb, int lane) {
     r.sum32 = group8_sum(q[0] + q[1] + q[2] + q[3]);
     r.d = d;
     return r;
+}
+SYN_DEV Q8KLane q8k_block_lane(const float* __restrict__ xb, int lane) {
+    return q8k_block_lane(reinterpret_cast<const float4*>(xb)[lane], lane);
 }
 
 // Q8_0 of one 32-value block (crates/kernels-cpu/src/gemv/act.rs:323-342): d = amax / 127,

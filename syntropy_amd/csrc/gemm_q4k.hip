@@ -72,15 +72,15 @@ GemmAct gemm_act_at(uint8_t* base, int64_t tpad, int k) {
 }
 
 // One wavefront per (super-block b, token t): the Q8_K block of crates/kernels-cpu/src/gemv/
-// act.rs:351-373 (q8k_block_lane), written in the GEMM order.  Lane l holds values 4l..4l+3:
-// sub-block j = l / 8, k part p = l / 16, nibble half h = (l / 8) & 1, dword s = l & 7.
-// A null row writes zeros (padding).
-SYN_DEV void gemm_act_block(const float* __restrict__ row, int b, int t, GemmAct a, int lane) {
+// act.rs:351-373 (q8k_block_lane), written in the GEMM order.  Lane l holds values 4l..4l+3
+// (v4, loaded by the caller): sub-block j = l / 8, k part p = l / 16, nibble half h = (l / 8) & 1,
+// dword s = l & 7.  A padding position (live false) writes zeros.
+SYN_DEV void gemm_act_block(float4 v4, bool live, int b, int t, GemmAct a, int lane) {
     uint32_t q = 0;
     int sum32 = 0, xsum = 0;
     float d = 0.0f;
-    if (row) {  // uniform over the wavefront
-        const Q8KLane r = q8k_block_lane(row + (int64_t)b * 256, lane);
+    if (live) {  // uniform over the wavefront
+        const Q8KLane r = q8k_block_lane(v4, lane);
         q = r.packed;
         sum32 = r.sum32;
         d = r.d;
@@ -113,20 +113,56 @@ SYN_DEV void gemm_act_block(const float* __restrict__ row, int b, int t, GemmAct
     }
 }
 
+// A wavefront takes BPW consecutive super-blocks of one row, their loads issued together before
+// any is quantized: at many blocks (ACT_WIDE_ITEMS or more) four a wavefront, which keeps more
+// bytes in flight per wavefront (14336-wide rows at 2048 tokens: 45 against 50 us; the MoE layer's
+// h: 43 against 56 us); below that one, which keeps more wavefronts (4096-wide: 15 against
+// 17 us).  Item = (block group g, position t), t fastest.
+constexpr int64_t ACT_WIDE_ITEMS = 65536;
+
+template <int BPW, class RowOf>
+SYN_DEV void gemm_act_blocks(int nb, int64_t item, GemmAct a, int lane, RowOf row_of) {
+    const int ng = (nb + BPW - 1) / BPW;
+    if (item >= (int64_t)ng * a.tpad) return;
+    const int g = (int)(item / a.tpad), t = (int)(item - (int64_t)g * a.tpad);
+    const float* row = row_of(t);  // null: a padding position
+    float4 v[BPW];
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        const int b = g * BPW + j;
+        v[j] = row && b < nb ? reinterpret_cast<const float4*>(row + (int64_t)b * 256)[lane] : float4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        const int b = g * BPW + j;
+        if (b < nb) gemm_act_block(v[j], row != nullptr, b, t, a, lane);  // uniform
+    }
+}
+
+// Blocks a wavefront for nb super-blocks at tpad positions, and the wavefronts that takes.
+SYN_HD inline int gemm_act_bpw(int nb, int64_t tpad) { return (int64_t)nb * tpad >= ACT_WIDE_ITEMS ? 4 : 1; }
+SYN_HD inline int64_t gemm_act_items(int nb, int64_t tpad) {
+    const int bpw = gemm_act_bpw(nb, tpad);
+    return (int64_t)((nb + bpw - 1) / bpw) * tpad;
+}
+
+template <int BPW>
 __global__ __launch_bounds__(256) void k_gemm_act(const float* __restrict__ x, int T, int k, GemmAct a,
                                                   const uint32_t* __restrict__ active) {
     T = active_rows(active, 0, T);  // inactive rows are written as padding
-    const int nb = k / 256, lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63;
     const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= (int64_t)nb * a.tpad) return;
-    const int b = (int)(item / a.tpad), t = (int)(item - (int64_t)b * a.tpad);
-    gemm_act_block(t < T ? x + (int64_t)t * k : nullptr, b, t, a, lane);
+    gemm_act_blocks<BPW>(k / 256, item, a, lane, [&](int t) { return t < T ? x + (int64_t)t * k : nullptr; });
 }
 
 void launch_gemm_act(const float* x, int T, int k, GemmAct a, hipStream_t stream, const uint32_t* active) {
-    const int64_t items = (int64_t)(k / 256) * a.tpad;
+    const int64_t items = gemm_act_items(k / 256, a.tpad);
     if (items == 0) return;
-    hipLaunchKernelGGL(k_gemm_act, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, x, T, k, a, active);
+    const dim3 grid((unsigned)((items + 3) / 4));
+    if (gemm_act_bpw(k / 256, a.tpad) == 4)
+        hipLaunchKernelGGL(k_gemm_act<4>, grid, dim3(256), 0, stream, x, T, k, a, active);
+    else
+        hipLaunchKernelGGL(k_gemm_act<1>, grid, dim3(256), 0, stream, x, T, k, a, active);
 }
 
 // ============================================================================================
@@ -494,27 +530,33 @@ void launch_moe_tiles(const uint32_t* offsets, int n_experts, const uint32_t* er
 
 // The entries' h rows at their padded positions (row i of h for entry i).  Positions in tiles
 // past the used ones are not written (no workgroup reads them).
+template <int BPW>
 __global__ __launch_bounds__(256) void k_moe_gemm_act(const float* __restrict__ h, int k,
                                                       const uint32_t* __restrict__ offsets, MoeTiles mt,
                                                       const uint32_t* __restrict__ err, GemmAct a) {
     if (err[0]) return;
-    const int nb = k / 256, lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63;
     const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= (int64_t)nb * a.tpad) return;
-    const int b = (int)(item / a.tpad), pos = (int)(item - (int64_t)b * a.tpad);
-    const uint32_t tile = (uint32_t)pos / 64u;
-    if (tile >= mt.n_tiles[0]) return;
-    const uint32_t e = mt.tile_e[tile];
-    const uint32_t i = offsets[e] + ((uint32_t)pos - mt.pad_off[e]);
-    gemm_act_block(i < offsets[e + 1] ? h + (int64_t)i * k : nullptr, b, pos, a, lane);
+    const int64_t ng = (k / 256 + BPW - 1) / BPW;
+    if (item >= ng * a.tpad) return;
+    const uint32_t tile = (uint32_t)(item - (item / a.tpad) * a.tpad) / 64u;
+    if (tile >= mt.n_tiles[0]) return;  // a tile past the used ones: nothing reads it
+    gemm_act_blocks<BPW>(k / 256, item, a, lane, [&](int pos) {
+        const uint32_t e = mt.tile_e[tile];
+        const uint32_t i = offsets[e] + ((uint32_t)pos - mt.pad_off[e]);
+        return i < offsets[e + 1] ? h + (int64_t)i * k : nullptr;
+    });
 }
 
 void launch_moe_gemm_act(const float* h, int k, const uint32_t* offsets, MoeTiles mt, const uint32_t* err,
                          GemmAct a, hipStream_t stream) {
-    const int64_t items = (int64_t)(k / 256) * a.tpad;
+    const int64_t items = gemm_act_items(k / 256, a.tpad);
     if (items == 0) return;
-    hipLaunchKernelGGL(k_moe_gemm_act, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, h, k, offsets, mt,
-                       err, a);
+    const dim3 grid((unsigned)((items + 3) / 4));
+    if (gemm_act_bpw(k / 256, a.tpad) == 4)
+        hipLaunchKernelGGL(k_moe_gemm_act<4>, grid, dim3(256), 0, stream, h, k, offsets, mt, err, a);
+    else
+        hipLaunchKernelGGL(k_moe_gemm_act<1>, grid, dim3(256), 0, stream, h, k, offsets, mt, err, a);
 }
 
 struct MoeGemmArgs {
