@@ -502,10 +502,9 @@ void launch_gate_up_q4k_f32(const uint8_t* W, int n, int k, const float* x, floa
 // weights stream once and each lane computes its block's term against every row; each row's
 // terms are folded in block order by the row's first lane, as at one row.  Rows of up to 64
 // super-blocks; rows past the step's active rows are neither computed nor written.  FUSE = 1
-// (two rows of at most 16 super-blocks): the workgroup quantizes the F32 rows to Q8_K in LDS
-// itself, as the one-row kernel does, the rows' loads issued before the block's: one launch
-// (14336 x 4096: 10.2 against 10.7 us; 4096 x 4096: 6.4 against 7.8 us; at three rows the
-// separate quantization is the faster, 12.3 against 12.6 us).
+// (two or three rows of at most 16 super-blocks): the workgroup quantizes the F32 rows to Q8_K in
+// LDS itself, as the one-row kernel does, the rows' loads issued before the block's: one launch
+// (two rows, 14336 x 4096: 10.2 against 10.7 us; 4096 x 4096: 6.4 against 7.8 us).
 constexpr int XR_WAVES = 8;
 
 SYN_HD inline size_t xr_row_lds(int nb) { return align_up(q4k_dec_lds(nb) + 16, 16); }  // + the scales' 16-byte tail
@@ -605,16 +604,18 @@ __global__ __launch_bounds__(64 * XR_WAVES) void k_gemv_q4k_x8_rows(const uint8_
 
 // Where it is the faster form (measured against the K-split expert kernel over X8 runs, 14336 x
 // 4096, 4096 x 14336 and 4096 x 4096): two rows of up to 64 super-blocks (10.7 against 13.2 us
-// at 14336 x 4096, level elsewhere); three rows only where every CU holds a workgroup and the
-// rows are at most 16 super-blocks (12.0 against 13.2 us at 14336 x 4096; 13-14 % slower at 4096
-// rows, where a row's extra terms no longer hide under the weight stream).
+// at 14336 x 4096, level elsewhere); three rows of at most 16 super-blocks in the fused form
+// (14336, 6144 and 4096 rows of 4096: 11.7, 7.3 and 6.9 us against 11.8, 8.7 and 7.8 for the
+// separate quantization before this kernel or the expert kernel).  Four rows fused were slower
+// than the expert kernel at 14336 and 4096 rows (13.8 and 8.4 against 13.1 and 7.9 us).
 bool gemv_q4k_x8_rows_pick(int n_out, int k, int rows) {
     if (k % 256 || k <= 0 || k > 64 * 256) return false;
     const int nb = k / 256;
-    return rows == 2 || (rows == 3 && nb <= 16 && (n_out + 31) / 32 >= 256);
+    (void)n_out;
+    return rows == 2 || (rows == 3 && nb <= 16);
 }
 
-bool gemv_q4k_x8_rows_fused(int k, int rows) { return rows == 2 && k % 256 == 0 && k > 0 && k <= 16 * 256; }
+bool gemv_q4k_x8_rows_fused(int k, int rows) { return (rows == 2 || rows == 3) && k % 256 == 0 && k > 0 && k <= 16 * 256; }
 
 void launch_gemv_q4k_x8_rows(const uint8_t* W, int n_out, int k, const uint8_t* ws, const float* x, int rows,
                              float* y, hipStream_t stream, const uint32_t* active) {
@@ -630,8 +631,11 @@ void launch_gemv_q4k_x8_rows(const uint8_t* W, int n_out, int k, const uint8_t* 
         hipLaunchKernelGGL((k_gemv_q4k_x8_rows<NR, FUSE>), grid, dim3(64 * XR_WAVES), lds, stream, W, n_out, nb, ws, \
                            rows, rows, x, y, active);                                                        \
     } while (0)
-    if (x) {  // two rows quantized in the workgroups (gemv_q4k_x8_rows_fused)
-        SYN_XR(2, 1);
+    if (x) {  // the rows quantized in the workgroups (gemv_q4k_x8_rows_fused)
+        if (rows <= 2)
+            SYN_XR(2, 1);
+        else
+            SYN_XR(3, 1);
     } else if (rows <= 2) {
         SYN_XR(2, 0);
     } else {
