@@ -11,7 +11,10 @@
 // rows are staged in LDS once per workgroup; a single F32 row can instead be quantized there by
 // every workgroup (the same Q8_0 blocks the quantization kernel writes), under the first weight
 // loads, which saves the separate quantization launch.  Each block's term is written to LDS and
-// lane r folds activation row r's terms in block order.
+// lane r folds activation row r's terms in block order.  At one activation row the workgroup's
+// rows are folded together, lane w of the first wavefront adding wavefront w's terms, a chunk of
+// 128 blocks at a time: one fold instruction serves every row of the workgroup (a lane-0-only
+// fold per wavefront costs as many instructions as all the row's other arithmetic together).
 //
 // 2 or more rows (k_gemm_q8_splitk up to 16 rows of whole 16-block stages, k_gemm_q8_staged for
 // more rows or rows of whole 4-block stages, Q8_0 and Q4_0; else for Q8_0 from 9 rows
@@ -63,8 +66,12 @@ void launch_split_repack(int ty, const uint8_t* src, uint8_t* dst, uint64_t byte
 
 constexpr int SPLIT_WAVES = 8;
 // wavefronts of a workgroup that quantizes its row itself: sixteen quantize the row half as often
-// as eight (Q4_0 4096 x 4096: 5.9 against 6.8 us a call)
+// as eight (Q4_0 4096 x 4096: 5.15 against 5.74 us a call, Q4_0 4096 x 14336: 12.4 against 14.5),
+// where the matrix has rows for a workgroup of sixteen on each of gfx950's 256 CUs; below that,
+// eight (Q8_0 1024 x 4096: 4.65 against 5.52 us)
 constexpr int FUSE_WAVES = 16;
+constexpr int FUSE_WAVES_FEW = 8;
+constexpr int GFX950_CUS = 256;
 constexpr int SPLIT_UNROLL = 4;  // 16-byte weight loads a lane has in flight
 constexpr int SPLIT_STAGE_MAX = 48 * 1024;  // LDS bytes of staged activation rows at most
 
@@ -76,11 +83,19 @@ SYN_HD inline size_t split_act_lds(int ty, int R, int k) {
 }
 // per wavefront, the terms of one load instruction: [R][64 blocks]
 SYN_HD inline size_t split_fold_lds(int R, int waves = SPLIT_WAVES) { return (size_t)waves * R * 64 * 4; }
+// one activation row: the terms of FOLD_CHUNK blocks of each of the workgroup's rows, a row's
+// F32 words padded to a multiple of four plus four, so that the folding lanes' 16-byte reads
+// start in different banks
+constexpr int FOLD_CHUNK = 128;
+SYN_HD inline int wg_fold_stride(int nb) { return ((nb < FOLD_CHUNK ? nb : FOLD_CHUNK) + 3) / 4 * 4 + 4; }
+SYN_HD inline size_t wg_fold_lds(int nb, int waves) { return (size_t)waves * wg_fold_stride(nb) * 4; }
 
 // STAGED 1: the activation rows are copied to LDS first (when they fit), 0: read from global;
 // 2 (R = 1): the F32 row xf is quantized to Q8_0 blocks in LDS by the workgroup.
+// One activation row: eight wavefronts a SIMD (64 VGPRs at most), two workgroups of sixteen or
+// four of eight resident on a CU.
 template <int FMT, int R, int STAGED, int WVS = STAGED == 2 ? FUSE_WAVES : SPLIT_WAVES>
-__global__ __launch_bounds__(64 * WVS) void k_gemv_split(const uint8_t* __restrict__ W, int n_out, int k,
+__global__ __launch_bounds__(64 * WVS, R == 1 ? 8 : 1) void k_gemv_split(const uint8_t* __restrict__ W, int n_out, int k,
                                                                   const int8_t* __restrict__ xq,
                                                                   const float* __restrict__ xd,
                                                                   const int32_t* __restrict__ xs, int rows,
@@ -88,6 +103,7 @@ __global__ __launch_bounds__(64 * WVS) void k_gemv_split(const uint8_t* __restri
                                                                   const uint32_t* __restrict__ active, int first,
                                                                   const float* __restrict__ xf) {
     static_assert(STAGED != 2 || R == 1, "one row quantized in the workgroup");
+    constexpr bool WGF = R == 1;  // the workgroup's rows folded together
     rows = active_rows(active, first, rows);
     if (rows == 0) return;  // uniform
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -179,8 +195,15 @@ __global__ __launch_bounds__(64 * WVS) void k_gemv_split(const uint8_t* __restri
         lds_barrier();  // the LDS rows whole; the weight loads stay in flight
     }
     float* buf = reinterpret_cast<float*>(lds + fold_off) + (size_t)wave * R * 64;
-    if (row >= n_out) return;  // uniform per wavefront; no workgroup barrier below
-    float acc = 0.0f;          // lane r < rows: activation row r's sum
+    // WGF: the terms [wavefront][blocks cb ..], the workgroup's rows folded by the first wavefront;
+    // a wavefront past the matrix goes on (it reaches the barriers) over its clamped row, unused
+    float* terms = reinterpret_cast<float*>(lds + fold_off);
+    const int fst = wg_fold_stride(nb);
+    int cb = 0;
+    if constexpr (!WGF) {
+        if (row >= n_out) return;  // uniform per wavefront; no workgroup barrier below
+    }
+    float acc = 0.0f;  // lane r < rows: activation row r's sum (WGF: lane w of wavefront 0, row w's)
     for (int g0 = 0; g0 < pieces; g0 += 64 * SPLIT_UNROLL) {
         if (g0) load_group(g0);
 #pragma unroll
@@ -213,18 +236,50 @@ __global__ __launch_bounds__(64 * WVS) void k_gemv_split(const uint8_t* __restri
                     if (ok) s -= 8 * as[r * nb + b];  // (n - 8) codes, exact
                 }
                 const bool writer = ok && (FMT != T_Q8_0 || (h & 1) == 0);
-                if (writer) buf[r * 64 + (b - b0)] = (dw * ad[r * nb + b]) * (float)s;
+                const float term = (dw * ad[r * nb + b]) * (float)s;
+                if constexpr (WGF) {
+                    if (writer) terms[wave * fst + (b - cb)] = term;
+                } else {
+                    if (writer) buf[r * 64 + (b - b0)] = term;
+                }
             }
-            wave_lds_sync();
-            if (lane < rows) {  // this instruction's blocks, in order, into row `lane`'s sum
-                const int nbi = nb - b0 < BPI ? nb - b0 : BPI;
-                const float* t = buf + lane * 64;
-                for (int j = 0; j < nbi; ++j) acc = acc + t[j];
+            if constexpr (WGF) {
+                const int done = nb - b0 < BPI ? nb : b0 + BPI;  // blocks through this instruction
+                if (done - cb == FOLD_CHUNK || done == nb) {      // uniform
+                    lds_barrier();
+                    if (wave == 0 && lane < WVS) {  // blocks cb .. done - 1 of row `lane`, in order
+                        const float* t = terms + lane * fst;
+                        const int cnt = done - cb;
+                        int j = 0;
+                        for (; j + 32 <= cnt; j += 32) {  // eight reads in flight
+                            float4 v[8];
+#pragma unroll
+                            for (int q = 0; q < 8; ++q) v[q] = reinterpret_cast<const float4*>(t + j)[q];
+#pragma unroll
+                            for (int q = 0; q < 8; ++q) acc = (((acc + v[q].x) + v[q].y) + v[q].z) + v[q].w;
+                        }
+                        for (; j < cnt; ++j) acc = acc + t[j];
+                    }
+                    cb = done;
+                    if (done < nb) lds_barrier();  // read out before the next chunk's terms
+                }
+            } else {
+                wave_lds_sync();
+                if (lane < rows) {  // this instruction's blocks, in order, into row `lane`'s sum
+                    const int nbi = nb - b0 < BPI ? nb - b0 : BPI;
+                    const float* t = buf + lane * 64;
+                    for (int j = 0; j < nbi; ++j) acc = acc + t[j];
+                }
+                wave_lds_sync();
             }
-            wave_lds_sync();
         }
     }
-    if (lane < rows) y[(int64_t)lane * n_out + row] = acc;
+    if constexpr (WGF) {
+        const int orow = (int)blockIdx.x * WVS + lane;
+        if (wave == 0 && lane < WVS && orow < n_out) y[orow] = acc;
+    } else if (lane < rows) {
+        y[(int64_t)lane * n_out + row] = acc;
+    }
 }
 
 static int split_r(int rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8; }
@@ -246,12 +301,13 @@ static void launch_split_fmt(const uint8_t* W, int n_out, int k, const uint8_t* 
     auto go = [&](auto rt) {
         constexpr int RR = decltype(rt)::value;
         const size_t stage = split_act_lds(FMT, RR, k);
+        const size_t fold = RR == 1 ? wg_fold_lds(k / 32, SPLIT_WAVES) : split_fold_lds(RR);
         if (stage <= (size_t)SPLIT_STAGE_MAX) {
-            const size_t lds = align_up(stage, 16) + split_fold_lds(RR);
+            const size_t lds = align_up(stage, 16) + fold;
             hipLaunchKernelGGL((k_gemv_split<FMT, RR, 1>), grid, dim3(64 * SPLIT_WAVES), lds, stream, W, n_out, k, xq,
                                xd, xs, rows, yr, active, first, nullptr);
         } else {
-            hipLaunchKernelGGL((k_gemv_split<FMT, RR, 0>), grid, dim3(64 * SPLIT_WAVES), split_fold_lds(RR), stream, W,
+            hipLaunchKernelGGL((k_gemv_split<FMT, RR, 0>), grid, dim3(64 * SPLIT_WAVES), fold, stream, W,
                                n_out, k, xq, xd, xs, rows, yr, active, first, nullptr);
         }
     };
@@ -269,14 +325,21 @@ bool gemv_split_fused_fits(int ty, int k) { return split_act_lds(ty, 1, k) <= (s
 
 void launch_gemv_split_fused(int ty, const uint8_t* W, int n_out, int k, const float* x, float* y, hipStream_t stream,
                              const uint32_t* active) {
-    const dim3 grid((unsigned)((n_out + FUSE_WAVES - 1) / FUSE_WAVES));
-    const size_t lds = align_up(split_act_lds(ty, 1, k), 16) + split_fold_lds(1, FUSE_WAVES);
-    if (ty == T_Q8_0)
-        hipLaunchKernelGGL((k_gemv_split<T_Q8_0, 1, 2>), grid, dim3(64 * FUSE_WAVES), lds, stream, W, n_out, k, nullptr,
-                           nullptr, nullptr, 1, y, active, 0, x);
+    auto go = [&](auto wt) {
+        constexpr int WV = decltype(wt)::value;
+        const dim3 grid((unsigned)((n_out + WV - 1) / WV));
+        const size_t lds = align_up(split_act_lds(ty, 1, k), 16) + wg_fold_lds(k / 32, WV);
+        if (ty == T_Q8_0)
+            hipLaunchKernelGGL((k_gemv_split<T_Q8_0, 1, 2, WV>), grid, dim3(64 * WV), lds, stream, W, n_out, k,
+                               nullptr, nullptr, nullptr, 1, y, active, 0, x);
+        else
+            hipLaunchKernelGGL((k_gemv_split<T_Q4_0, 1, 2, WV>), grid, dim3(64 * WV), lds, stream, W, n_out, k,
+                               nullptr, nullptr, nullptr, 1, y, active, 0, x);
+    };
+    if (n_out >= FUSE_WAVES * GFX950_CUS)
+        go(std::integral_constant<int, FUSE_WAVES>{});
     else
-        hipLaunchKernelGGL((k_gemv_split<T_Q4_0, 1, 2>), grid, dim3(64 * FUSE_WAVES), lds, stream, W, n_out, k, nullptr,
-                           nullptr, nullptr, 1, y, active, 0, x);
+        go(std::integral_constant<int, FUSE_WAVES_FEW>{});
 }
 
 // y[r][o] over a SPLIT matrix from rows quantized to Q8_0 in `ws` (act_layout(ACT_Q8_0, rows, k)),

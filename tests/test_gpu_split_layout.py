@@ -91,6 +91,16 @@ def test_split_config_shapes_equal_oracle(S, ty, n_out, k, rowss):
         check(S, ty, n_out, k, rows, 0x5E12 + rows, w)
 
 
+@pytest.mark.parametrize("ty", [o.Q8_0, o.Q4_0])
+@pytest.mark.parametrize("n_out,k", [(4096 + 37, 1024), (4096 + 5, 14336 + 32), (2048 + 9, 4096)])
+def test_split_one_row_workgroup_fold_equal_oracle(S, ty, n_out, k):
+    """One row quantized in the product's workgroups, whose rows are folded together: workgroups
+    of sixteen rows (4096 rows or more) and of eight, the last one partly past the matrix; rows of
+    one to four 128-block fold chunks, the last one partial."""
+    w = o.quantize(ty, o.normal(0x5E21 + n_out + k, 0.02, n_out * k))
+    check(S, ty, n_out, k, 1, 0x5E22 + n_out, w)
+
+
 def test_split_gemm_edges_equal_oracle(S):
     """The GEMM's clamped tiles: weight rows not multiples of 16 (or 64), token counts not
     multiples of 32, one-block rows, many tiles of tokens."""
