@@ -162,6 +162,12 @@ int syn_hbm_read_probe(const void* src, uint64_t bytes, uint32_t* sink, void* st
  * set against, beside syn_hbm_read_probe.  No counterpart in the reference. */
 uint64_t syn_hbm_read_runs_sink_words(uint64_t bytes);
 int syn_hbm_read_runs(uint32_t waves, const void* src, uint64_t bytes, uint32_t* sink, void* stream);
+/* syn_div_forms_check: compares, over every F32 bit pattern but the NaNs, the quantizers' short
+ * forms of their correctly rounded divisions (amax / 127 for finite amax >= 0, 1 / b, -127 / b) and of
+ * the F32 -> F16 -> F32 rounding against the compiler's correctly rounded division and the
+ * integer F16 conversion; adds each form's count of differing results to counts[0..3] (device
+ * memory, 4 words, zero on entry).  A self-check with no counterpart in the reference. */
+int syn_div_forms_check(unsigned long long* counts, void* stream);
 
 /* ---- RmsNorm and Logits ----------------------------------------------------------------------
  * syn_rms_norm: y = RmsNorm(x) of each of `rows` rows of n F32 values (n <= 16384), weight g [n]:

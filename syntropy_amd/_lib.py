@@ -64,6 +64,7 @@ def lib():
         "syn_gemv_batch_quantized_layout": [u32, u32, vp, vp, vp, vp, vp, vp, u64, vp, vp],
         "syn_hbm_read_probe": [vp, u64, vp, vp],
         "syn_hbm_read_runs": [u32, vp, u64, vp, vp],
+        "syn_div_forms_check": [vp, vp],
         "syn_rms_norm": [vp, vp, u32, u32, C.c_float, vp, vp],
         "syn_logits_workspace_bytes": [u32, i32, u32, u32, u32, C.POINTER(C.c_uint64)],
         "syn_logits": [u32, i32, vp, u64, u32, u32, vp, C.c_float, vp, u32, vp, vp, u64, vp],

@@ -881,6 +881,13 @@ SYN_EXPORT int syn_hbm_read_probe(const void* src, uint64_t bytes, uint32_t* sin
     return check_launch(W);
 }
 
+SYN_EXPORT int syn_div_forms_check(unsigned long long* counts, void* stream) {
+    const char* W = "syn_div_forms_check";
+    if (!counts || !aligned(counts, 8)) return fail(SYN_E_INVALID, "%s: counts must be 8-byte aligned device memory", W);
+    syn::launch_div_forms_check(counts, (hipStream_t)stream);
+    return check_launch(W);
+}
+
 SYN_EXPORT uint64_t syn_hbm_read_runs_sink_words(uint64_t bytes) { return syn::hbm_read_runs_units(bytes); }
 
 SYN_EXPORT int syn_hbm_read_runs(uint32_t waves, const void* src, uint64_t bytes, uint32_t* sink, void* stream) {

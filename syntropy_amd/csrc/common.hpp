@@ -54,6 +54,40 @@ SYN_DEV uint32_t f16_bits(float x) {
 }
 
 // ggml's nearest_int (ggml-quants.c:621-626; kernels-cpu/src/gemv/act.rs:345-348).
+// The quantizers' correctly rounded F32 divisions in fewer instructions than the compiler's
+// general sequence (about ten each).  Each form equals the division bit for bit over its whole
+// domain on gfx950; syn_div_forms_check compares them over every F32 pattern.
+//  div127(a), a finite and >= 0: RN(a * RN(1/127)) and one fma residual step (Markstein).
+SYN_DEV float div127(float a) {
+    const float y = 1.0f / 127.0f;
+    const float q = a * y;
+    return __builtin_fmaf(__builtin_fmaf(-q, 127.0f, a), y, q);
+}
+//  recip_rn(b): v_rcp_f32 and one fma Newton step where 2^-126 <= |b| < 2^126, else the division.
+SYN_DEV float recip_rn(float b) {
+    const uint32_t m = f2u(b) & 0x7FFFFFFFu;
+    if (m >= 0x00800000u && m < 0x7E800000u) {
+        const float y = __builtin_amdgcn_rcpf(b);
+        return __builtin_fmaf(__builtin_fmaf(-b, y, 1.0f), y, y);
+    }
+    return 1.0f / b;
+}
+//  neg127_div(b) = -127 / b: RN(-127 * recip) and one fma residual step where 2^-120 <= |b| <
+//  2^126, else the division.
+SYN_DEV float neg127_div(float b) {
+    const uint32_t m = f2u(b) & 0x7FFFFFFFu;
+    if (m >= 0x03800000u && m < 0x7E800000u) {
+        const float y = __builtin_amdgcn_rcpf(b);
+        const float r = __builtin_fmaf(__builtin_fmaf(-b, y, 1.0f), y, y);
+        const float q = -127.0f * r;
+        return __builtin_fmaf(__builtin_fmaf(-q, b, -127.0f), r, q);
+    }
+    return -127.0f / b;
+}
+// F32 -> F16 -> F32 by the hardware conversions (round to nearest even, F16 subnormals kept):
+// f16_to_f32(f16_bits(x)) for every non-NaN x (also checked by syn_div_forms_check).
+SYN_DEV float f16_round(float x) { return (float)(_Float16)x; }
+
 SYN_DEV int nearest_int(float f) {
     float v = f + 12582912.f;
     return (int)(f2u(v) & 0x007FFFFFu) - 0x00400000;
@@ -217,7 +251,7 @@ SYN_DEV Q8KLane q8k_block_lane(float4 v4, int lane) {
     if (bad) {
         d = __builtin_nanf("");
     } else if (amax != 0.0f) {
-        const float iscale = -127.0f / mx;
+        const float iscale = neg127_div(mx);
         if (finite_f(iscale)) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -225,7 +259,7 @@ SYN_DEV Q8KLane q8k_block_lane(float4 v4, int lane) {
                 q[i] = t < 127 ? t : 127;
             }
         }
-        d = 1.0f / iscale;
+        d = recip_rn(iscale);
     }
     Q8KLane r;
     r.packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
@@ -266,13 +300,13 @@ SYN_DEV Q8_0Lane q8_0_block_lane(float4 v4) {
     if (bad) {
         r.d = __builtin_nanf("");
     } else {
-        const float d = amax / 127.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const float d = div127(amax);
+        const float id = d != 0.0f ? recip_rn(d) : 0.0f;
         if (finite_f(id)) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) q[i] = (int)__builtin_rintf(v[i] * id);
         }
-        r.d = f16_to_f32(f16_bits(d));
+        r.d = f16_round(d);
     }
     r.packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
                ((uint32_t)(q[3] & 0xFF) << 24);

@@ -70,7 +70,7 @@ SYN_DEV void quant16_to_lds(const float (&v)[16], int c, int nb, uint8_t* lds) {
     if (bad) {
         d = __builtin_nanf("");
     } else if (amax != 0.0f) {
-        const float iscale = -127.0f / mx;
+        const float iscale = neg127_div(mx);
         if (finite_f(iscale)) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -78,7 +78,7 @@ SYN_DEV void quant16_to_lds(const float (&v)[16], int c, int nb, uint8_t* lds) {
                 q[i] = n < 127 ? n : 127;
             }
         }
-        d = 1.0f / iscale;
+        d = recip_rn(iscale);
     }
     uint32_t w[4];
     int s = 0;

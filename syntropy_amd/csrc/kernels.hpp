@@ -76,6 +76,7 @@ void launch_hbm_read_probe(const uint8_t* src, uint64_t bytes, uint32_t* sink, h
 uint64_t hbm_read_probe_workgroups(uint64_t bytes);
 uint64_t hbm_read_runs_units(uint64_t bytes);
 void launch_hbm_read_runs(int waves, const uint8_t* src, uint64_t bytes, uint32_t* sink, hipStream_t stream);
+void launch_div_forms_check(unsigned long long* counts, hipStream_t stream);
 // norm.hip: RmsNorm rows of at most NORM_MAX_COLS values
 constexpr int NORM_MAX_COLS = 16384;
 void launch_rms_norm(const float* x, const float* g, int rows, int n, float eps, float* y, hipStream_t stream,

@@ -52,12 +52,29 @@ def crafted_row(k, seed, nonfinite=None):
         x[7 * 256:8 * 256] = 0.0
         x[7 * 256 + 9] = np.float32(-1e-39)           # subnormal maximum: the inverse scale overflows
         x[8 * 256:9 * 256] *= np.float32(1e-40)       # every value subnormal
+    if nb > 10:
+        # the quantizers' short division forms hand over to the division at their range ends:
+        # a block of normal values whose Q8_0 scale is subnormal and whose Q8_K inverse scale
+        # overflows, and one whose maximum passes 2^126
+        x[9 * 256:10 * 256] *= np.float32(1e-37)
+        x[10 * 256:11 * 256] *= np.float32(3e37)
     if nonfinite is not None:
         x[nb // 2 * 256 + 77] = np.float32(nonfinite)
     return x
 
 
 ROWS = [(4096, 11), (8192, 12), (14336, 13), (2048, 14)]
+
+
+def test_division_forms_equal_the_division_everywhere(S):
+    """The quantizers' short forms of amax / 127, 1 / b, -127 / b and the F16 rounding of the
+    scale equal the correctly rounded division and the integer F16 conversion for every F32 bit
+    pattern but the NaNs (one launch over all 2^32)."""
+    counts = torch.zeros(4, dtype=torch.int64, device="cuda")
+    announce("division forms over every F32 pattern")
+    assert S.lib().syn_div_forms_check(counts.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    assert counts.tolist() == [0, 0, 0, 0]
 
 
 @pytest.mark.parametrize("k,seed", ROWS)
