@@ -163,10 +163,11 @@ int syn_hbm_read_probe(const void* src, uint64_t bytes, uint32_t* sink, void* st
 uint64_t syn_hbm_read_runs_sink_words(uint64_t bytes);
 int syn_hbm_read_runs(uint32_t waves, const void* src, uint64_t bytes, uint32_t* sink, void* stream);
 /* syn_div_forms_check: compares, over every F32 bit pattern but the NaNs, the quantizers' short
- * forms of their correctly rounded divisions (amax / 127 for finite amax >= 0, 1 / b, -127 / b) and of
- * the F32 -> F16 -> F32 rounding against the compiler's correctly rounded division and the
- * integer F16 conversion; adds each form's count of differing results to counts[0..3] (device
- * memory, 4 words, zero on entry).  A self-check with no counterpart in the reference. */
+ * forms of their correctly rounded divisions (amax / 127 for finite amax >= 0, 1 / b, -127 / b),
+ * of the F32 -> F16 -> F32 rounding and of ggml's nearest_int (|x| < 2^21) against the
+ * compiler's correctly rounded division, the integer F16 conversion and nearest_int's own
+ * arithmetic; adds each form's count of differing results to counts[0..4] (device memory, 5
+ * words, zero on entry).  A self-check with no counterpart in the reference. */
 int syn_div_forms_check(unsigned long long* counts, void* stream);
 
 /* ---- RmsNorm and Logits ----------------------------------------------------------------------

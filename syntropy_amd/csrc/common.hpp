@@ -92,6 +92,10 @@ SYN_DEV int nearest_int(float f) {
     float v = f + 12582912.f;
     return (int)(f2u(v) & 0x007FFFFFu) - 0x00400000;
 }
+// nearest_int(f) for |f| < 2^21 (where f + 1.5 * 2^23 rounds f to the nearest even integer, in
+// its low bits; just below 2^22 the sum rounds up to 2^24 and the two part): v_rndne_f32 and a
+// conversion (syn_div_forms_check compares the two over every such f).
+SYN_DEV int nearest_int_small(float f) { return (int)__builtin_rintf(f); }
 
 // get_scale_min_k4 (crates/kernels-cpu/src/gemv.rs:528-537) from the 12 packed bytes held in
 // three little-endian words.
@@ -211,11 +215,14 @@ SYN_DEV void block_signed_amax(const float (&v)[N], int i0, float& amax, float& 
         mag[i] = f2u(v[i]) & 0x7FFFFFFFu;
         m = m > mag[i] ? m : mag[i];
     }
+    const uint32_t lm = m;  // the lane's own largest magnitude
     m = group_max_u32<G>(m);
-    uint32_t key = 0xFFFFFFFFu;
+    // the lane's first value of the largest magnitude (the scan runs backwards: the first wins);
+    // lanes hold consecutive index ranges, so (i0 << 1 | its sign) orders as its (index << 1 | sign)
+    uint32_t first = 0;
 #pragma unroll
-    for (int i = N - 1; i >= 0; --i)
-        key = mag[i] == m ? (((uint32_t)(i0 + i) << 1) | (f2u(v[i]) >> 31)) : key;
+    for (int i = N - 1; i >= 0; --i) first = mag[i] == m ? f2u(v[i]) : first;
+    uint32_t key = lm == m ? (((uint32_t)i0 << 1) | (first >> 31)) : 0xFFFFFFFFu;
     key = group_min_u32<G>(key);
     bad = m >= 0x7F800000u;
     amax = u2f(m);
@@ -252,10 +259,10 @@ SYN_DEV Q8KLane q8k_block_lane(float4 v4, int lane) {
         d = __builtin_nanf("");
     } else if (amax != 0.0f) {
         const float iscale = neg127_div(mx);
-        if (finite_f(iscale)) {
+        if (finite_f(iscale)) {  // |iscale v| <= 127 (to a rounding): nearest_int_small's range
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int t = nearest_int(iscale * v[i]);
+                const int t = nearest_int_small(iscale * v[i]);
                 q[i] = t < 127 ? t : 127;
             }
         }
@@ -264,7 +271,7 @@ SYN_DEV Q8KLane q8k_block_lane(float4 v4, int lane) {
     Q8KLane r;
     r.packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
                ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
-    r.sum32 = group8_sum(q[0] + q[1] + q[2] + q[3]);
+    r.sum32 = group8_sum(sdot4(r.packed, 0x01010101u, 0));
     r.d = d;
     return r;
 }
@@ -310,7 +317,7 @@ SYN_DEV Q8_0Lane q8_0_block_lane(float4 v4) {
     }
     r.packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
                ((uint32_t)(q[3] & 0xFF) << 24);
-    r.sum = group8_sum(q[0] + q[1] + q[2] + q[3]);
+    r.sum = group8_sum(sdot4(r.packed, 0x01010101u, 0));
     return r;
 }
 

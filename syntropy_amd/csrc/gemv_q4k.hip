@@ -71,10 +71,10 @@ SYN_DEV void quant16_to_lds(const float (&v)[16], int c, int nb, uint8_t* lds) {
         d = __builtin_nanf("");
     } else if (amax != 0.0f) {
         const float iscale = neg127_div(mx);
-        if (finite_f(iscale)) {
+        if (finite_f(iscale)) {  // |iscale v| <= 127 (to a rounding): nearest_int_small's range
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int n = nearest_int(iscale * v[i]);
+                const int n = nearest_int_small(iscale * v[i]);
                 q[i] = n < 127 ? n : 127;
             }
         }
@@ -86,7 +86,7 @@ SYN_DEV void quant16_to_lds(const float (&v)[16], int c, int nb, uint8_t* lds) {
     for (int k = 0; k < 4; ++k) {
         w[k] = (uint32_t)(q[4 * k] & 0xFF) | ((uint32_t)(q[4 * k + 1] & 0xFF) << 8) |
                ((uint32_t)(q[4 * k + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * k + 3] & 0xFF) << 24);
-        s += q[4 * k] + q[4 * k + 1] + q[4 * k + 2] + q[4 * k + 3];
+        s = sdot4(w[k], 0x01010101u, s);  // the four codes' sum, exact
     }
     v4u pk = {w[0], w[1], w[2], w[3]};
     *reinterpret_cast<v4u*>(lds + sb * COL + part * 16) = pk;

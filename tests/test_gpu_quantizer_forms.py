@@ -67,14 +67,15 @@ ROWS = [(4096, 11), (8192, 12), (14336, 13), (2048, 14)]
 
 
 def test_division_forms_equal_the_division_everywhere(S):
-    """The quantizers' short forms of amax / 127, 1 / b, -127 / b and the F16 rounding of the
-    scale equal the correctly rounded division and the integer F16 conversion for every F32 bit
-    pattern but the NaNs (one launch over all 2^32)."""
-    counts = torch.zeros(4, dtype=torch.int64, device="cuda")
+    """The quantizers' short forms of amax / 127, 1 / b, -127 / b, the F16 rounding of the
+    scale and the rounding of scaled values to codes equal the correctly rounded division, the
+    integer F16 conversion and ggml's nearest_int for every F32 bit pattern but the NaNs (one
+    launch over all 2^32)."""
+    counts = torch.zeros(5, dtype=torch.int64, device="cuda")
     announce("division forms over every F32 pattern")
     assert S.lib().syn_div_forms_check(counts.data_ptr(), None) == 0
     torch.cuda.synchronize()
-    assert counts.tolist() == [0, 0, 0, 0]
+    assert counts.tolist() == [0, 0, 0, 0, 0]
 
 
 @pytest.mark.parametrize("k,seed", ROWS)
