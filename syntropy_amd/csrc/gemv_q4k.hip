@@ -275,6 +275,9 @@ constexpr int dec_waves() { return LAYOUT == LAYOUT_X8 ? 8 : 4; }
 // For a whole layer the separate quantization launch is faster (each workgroup re-quantizing
 // its row costs more than the launch it saves).
 constexpr int FUSE_PIECES = 2;
+// a wavefront's 64 fold terms in LDS, padded by four words so that the rows' 16-byte reads of a
+// workgroup fold start in different banks
+constexpr int DEC_TS = 68;
 
 // Resident wavefronts per SIMD: 6 (80 registers); the fused form holds the row pieces too
 // (4: 128 registers, no spills).
@@ -370,10 +373,29 @@ void k_gemv_q4k_batch(DecBatch bt) {
     const float t = q4k_term_lds(A, lds, nb, ok ? b : 0);
     // in-order fold: the row's P terms (+0.0 past its nb blocks, which leaves a sum that
     // started from +0.0 unchanged) added by the row's first lane
-    float* terms = reinterpret_cast<float*>(lds + align_up(q4k_dec_lds(nb), 16)) + wave * 64;
+    float* terms0 = reinterpret_cast<float*>(lds + align_up(q4k_dec_lds(nb), 16));
+    float* terms = terms0 + wave * DEC_TS;
     terms[lane] = ok ? t : 0.0f;
-    wave_lds_sync();
     float acc = 0.0f;
+    if (!GATED && P == 64) {  // uniform per workgroup
+        // one row a wavefront: the workgroup's rows folded together, lane w of wavefront 0
+        // adding wavefront w's terms (one instruction stream for every row, not one per row)
+        lds_barrier();
+        const int frow = ((int)blockIdx.x - bt.wg_begin[p]) * RW + lane;
+        if (wave == 0 && lane < WAVES && frow < n_out) {
+            const float4* tv = reinterpret_cast<const float4*>(terms0 + lane * DEC_TS);
+            for (int q = 0; q < (nb + 3) / 4; ++q) {
+                const float4 v = tv[q];
+                acc = acc + v.x;
+                acc = acc + v.y;
+                acc = acc + v.z;
+                acc = acc + v.w;
+            }
+            bt.y[p][frow] = acc;
+        }
+        return;
+    }
+    wave_lds_sync();
     if (b == 0 && row < n_out) {
         const float4* tv = reinterpret_cast<const float4*>(terms + lane);
         for (int q = 0; q < P / 4; ++q) {
@@ -387,7 +409,7 @@ void k_gemv_q4k_batch(DecBatch bt) {
     }
     if constexpr (GATED) {
         // the gate sums to the up wavefronts holding the same rows
-        float* gsum = reinterpret_cast<float*>(lds + align_up(q4k_dec_lds(nb), 16)) + WAVES * 64;
+        float* gsum = terms0 + WAVES * DEC_TS;
         if (!up_half && b == 0) gsum[(wave % RW) * 64 + lane] = acc;
         lds_barrier();
         if (up_half && b == 0 && row < n_out) bt.y[p][row] = ref_silu(gsum[(wave % RW) * 64 + lane]) * acc;
@@ -459,9 +481,9 @@ static void launch_batch(int np, const uint8_t* const* W, const int* n_out, cons
     }
     bt.wg_begin[np] = wg;
     if (wg == 0) return;
-    // the activation row, then 64 fold terms per wavefront (and the gate sums when GATED)
+    // the activation row, then the fold terms per wavefront (and the gate sums when GATED)
     hipLaunchKernelGGL((k_gemv_q4k_batch<LAYOUT, FUSE, GATED, WV>), dim3(wg), dim3(64 * WAVES),
-                       align_up(q4k_dec_lds(max_nb), 16) + (GATED ? 2 : 1) * WAVES * 64 * 4, stream, bt);
+                       align_up(q4k_dec_lds(max_nb), 16) + (GATED ? 2 : 1) * WAVES * DEC_TS * 4, stream, bt);
 }
 
 void launch_gemv_q4k_batch(int layout, int np, const uint8_t* const* W, const int* n_out, const int* k,
