@@ -253,24 +253,27 @@ SYN_DEV Q8KLane q8k_block_lane(float4 v4, int lane) {
     float amax, mx;
     bool bad;
     block_signed_amax<64>(v, lane * 4, amax, mx, bad);
-    float d = 0.0f;
-    int q[4] = {0, 0, 0, 0};
+    // codes of is v: is 0 where the codes are all 0 (an all-zero block, an infinite inverse
+    // scale), which leaves finite values' codes 0; a block with a NaN or an infinity is zeroed
+    // after the arithmetic (straight-line code)
+    float d = 0.0f, is = 0.0f;
     if (bad) {
         d = __builtin_nanf("");
     } else if (amax != 0.0f) {
         const float iscale = neg127_div(mx);
-        if (finite_f(iscale)) {  // |iscale v| <= 127 (to a rounding): nearest_int_small's range
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = nearest_int_small(iscale * v[i]);
-                q[i] = t < 127 ? t : 127;
-            }
-        }
+        is = finite_f(iscale) ? iscale : 0.0f;  // |iscale v| <= 127 (to a rounding): nearest_int_small's range
         d = recip_rn(iscale);
+    }
+    int q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = nearest_int_small(is * v[i]);
+        q[i] = t < 127 ? t : 127;
     }
     Q8KLane r;
     r.packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
                ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
+    r.packed = bad ? 0u : r.packed;
     r.sum32 = group8_sum(sdot4(r.packed, 0x01010101u, 0));
     r.d = d;
     return r;
@@ -302,21 +305,24 @@ SYN_DEV Q8_0Lane q8_0_block_lane(float4 v4) {
     ab = group_max_u32<8>(ab);
     const bool bad = ab >= 0x7F800000u;
     const float amax = u2f(ab);
-    int q[4] = {0, 0, 0, 0};
+    // codes of is v, is 0 where the codes are all 0 (d 0, an infinite inverse); a bad block is
+    // zeroed after the arithmetic (straight-line code)
     Q8_0Lane r;
+    float is = 0.0f;
     if (bad) {
         r.d = __builtin_nanf("");
     } else {
         const float d = div127(amax);
         const float id = d != 0.0f ? recip_rn(d) : 0.0f;
-        if (finite_f(id)) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) q[i] = (int)__builtin_rintf(v[i] * id);
-        }
+        is = finite_f(id) ? id : 0.0f;
         r.d = f16_round(d);
     }
+    int q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = (int)__builtin_rintf(v[i] * is);
     r.packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
                ((uint32_t)(q[3] & 0xFF) << 24);
+    r.packed = bad ? 0u : r.packed;
     r.sum = group8_sum(sdot4(r.packed, 0x01010101u, 0));
     return r;
 }

@@ -63,22 +63,22 @@ SYN_DEV void quant16_to_lds(const float (&v)[16], int c, int nb, uint8_t* lds) {
     float amax, mx;
     bool bad;
     block_signed_amax<16>(v, part * 16, amax, mx, bad);
-    float d = 0.0f;
-    int q[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) q[i] = 0;
+    // codes of is v: is 0 where the codes are all 0 (an all-zero block, an infinite inverse
+    // scale), which leaves finite values' codes 0; a block with a NaN or an infinity (`bad`) is
+    // zeroed whole after the arithmetic (straight-line code: no branch around the 16 values)
+    float d = 0.0f, is = 0.0f;
     if (bad) {
         d = __builtin_nanf("");
     } else if (amax != 0.0f) {
         const float iscale = neg127_div(mx);
-        if (finite_f(iscale)) {  // |iscale v| <= 127 (to a rounding): nearest_int_small's range
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int n = nearest_int_small(iscale * v[i]);
-                q[i] = n < 127 ? n : 127;
-            }
-        }
+        is = finite_f(iscale) ? iscale : 0.0f;  // |iscale v| <= 127 (to a rounding): nearest_int_small's range
         d = recip_rn(iscale);
+    }
+    int q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int n = nearest_int_small(is * v[i]);
+        q[i] = n < 127 ? n : 127;
     }
     uint32_t w[4];
     int s = 0;
@@ -86,6 +86,7 @@ SYN_DEV void quant16_to_lds(const float (&v)[16], int c, int nb, uint8_t* lds) {
     for (int k = 0; k < 4; ++k) {
         w[k] = (uint32_t)(q[4 * k] & 0xFF) | ((uint32_t)(q[4 * k + 1] & 0xFF) << 8) |
                ((uint32_t)(q[4 * k + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * k + 3] & 0xFF) << 24);
+        w[k] = bad ? 0u : w[k];
         s = sdot4(w[k], 0x01010101u, s);  // the four codes' sum, exact
     }
     v4u pk = {w[0], w[1], w[2], w[3]};
