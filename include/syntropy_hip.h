@@ -85,8 +85,8 @@ int syn_gemv(int32_t wtype, const void* w, uint64_t w_bytes, uint32_t n_out, uin
  * syn_gemv_layout(_workspace_bytes): the Gemv op over a matrix in `layout` (0 is syn_gemv); for
  *   layout 1 one row runs the decode kernel with the row quantized in every workgroup (k_in <=
  *   16384), 2 to 31 rows the decode expert kernel on rows quantized beforehand (int8 matrix
- *   cores, the matrix as one expert) except 2 rows (k_in <= 16384) and 3 rows (k_in <= 4096),
- *   which run the decode kernel over the rows side by side in LDS (with k_in <= 4096 in one
+ *   cores, the matrix as one expert) except 2 rows (k_in <= 16384) and 3 or 4 rows (k_in <=
+ *   4096), which run the decode kernel over the rows side by side in LDS (with k_in <= 4096 in one
  *   launch that quantizes them in its workgroups); more rows the
  *   matrix-core GEMM (k_in a multiple of 2048).
  *   Layout 2 at one row (k_in up to 39296 for Q4_0, 43680 for Q8_0) is one launch whose

@@ -520,15 +520,17 @@ void launch_gate_up_q4k_f32(const uint8_t* W, int n, int k, const float* x, floa
 }
 
 // ---- the x8 repack: a permutation of whole 16-byte chunks --------------------------------------
-// Two or three rows over X8 weights: the one-row decode kernel's loads and its one block per
+// Two to four rows over X8 weights: the one-row decode kernel's loads and its one block per
 // lane, with the NR activation rows (Q8_K, quantized beforehand) side by side in LDS, so the
-// weights stream once and each lane computes its block's term against every row; each row's
-// terms are folded in block order by the row's first lane, as at one row.  Rows of up to 64
-// super-blocks; rows past the step's active rows are neither computed nor written.  FUSE = 1
-// (two or three rows of at most 16 super-blocks): the workgroup quantizes the F32 rows to Q8_K in
-// LDS itself, as the one-row kernel does, the rows' loads issued before the block's: one launch
-// (two rows, 14336 x 4096: 10.2 against 10.7 us; 4096 x 4096: 6.4 against 7.8 us).
+// weights stream once and each lane computes its block's term against every row; the terms of
+// each (weight row, activation row) pair of a wavefront are folded in block order by a lane of
+// their own, one stream of adds for all the pairs.  Rows of up to 64 super-blocks; rows past the
+// step's active rows are neither computed nor written.  FUSE = 1 (rows of at most 16
+// super-blocks): the workgroup quantizes the F32 rows to Q8_K in LDS itself, as the one-row
+// kernel does, the rows' loads issued before the block's: one launch (two rows, 14336 x 4096:
+// 10.2 against 10.7 us; 4096 x 4096: 6.4 against 7.8 us, before the shared fold).
 constexpr int XR_WAVES = 8;
+constexpr int XR_TS = XR_WAVES * 64 + 4;  // one activation row's terms in LDS, padded
 
 SYN_HD inline size_t xr_row_lds(int nb) { return align_up(q4k_dec_lds(nb) + 16, 16); }  // + the scales' 16-byte tail
 
@@ -600,45 +602,46 @@ __global__ __launch_bounds__(64 * XR_WAVES) void k_gemv_q4k_x8_rows(const uint8_
         wait_vm<9>();  // this wavefront's row loads, all older than the block's nine
         lds_barrier();
     }
-    float* terms = reinterpret_cast<float*>(lds + (size_t)NR * RB) + wave * 64;
+    // terms [activation row r][wavefront][lane], a row's set padded by four words
+    float* terms = reinterpret_cast<float*>(lds + (size_t)NR * RB);
     float t[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) t[r] = r < rows ? q4k_term_lds(A, lds + r * RB, nb, ok ? b : 0) : 0.0f;
 #pragma unroll
-    for (int r = 0; r < NR; ++r) terms[r * XR_WAVES * 64 + lane] = ok ? t[r] : 0.0f;
+    for (int r = 0; r < NR; ++r) terms[r * XR_TS + wave * 64 + lane] = ok ? t[r] : 0.0f;
     wave_lds_sync();
-    if (b == 0 && row < n_out) {
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            if (r >= rows) break;
-            const float4* tv = reinterpret_cast<const float4*>(terms + r * XR_WAVES * 64 + lane);
-            float acc = 0.0f;
-            for (int q = 0; q < P / 4; ++q) {
-                const float4 v = tv[q];
-                acc = acc + v.x;
-                acc = acc + v.y;
-                acc = acc + v.z;
-                acc = acc + v.w;
-            }
-            y[(int64_t)r * n_out + row] = acc;
+    // lane j + rpw r folds the wavefront's weight row j against activation row r: one stream of
+    // P adds for every (row, activation row) pair of the wavefront
+    const int rpw = 64 / P, fr = lane % rpw, ar = lane / rpw;
+    const int frow = ((int)blockIdx.x * XR_WAVES + wave) * rpw + fr;
+    if (ar < rows && ar < NR && frow < n_out) {
+        const float4* tv = reinterpret_cast<const float4*>(terms + ar * XR_TS + wave * 64 + fr * P);
+        float acc = 0.0f;
+        for (int q = 0; q < P / 4; ++q) {
+            const float4 v = tv[q];
+            acc = acc + v.x;
+            acc = acc + v.y;
+            acc = acc + v.z;
+            acc = acc + v.w;
         }
+        y[(int64_t)ar * n_out + frow] = acc;
     }
 }
 
-// Where it is the faster form (measured against the K-split expert kernel over X8 runs, 14336 x
-// 4096, 4096 x 14336 and 4096 x 4096): two rows of up to 64 super-blocks (10.7 against 13.2 us
-// at 14336 x 4096, level elsewhere); three rows of at most 16 super-blocks in the fused form
-// (14336, 6144 and 4096 rows of 4096: 11.7, 7.3 and 6.9 us against 11.8, 8.7 and 7.8 for the
-// separate quantization before this kernel or the expert kernel).  Four rows fused were slower
-// than the expert kernel at 14336 and 4096 rows (13.8 and 8.4 against 13.1 and 7.9 us).
+// Where it is the faster form (measured against the line-order expert kernel over X8 runs,
+// 14336 x 4096, 6144 x 4096, 4096 x 4096 and 4096 x 14336): two rows of up to 64 super-blocks
+// (9.35 against 13.2 us at 14336 x 4096, level elsewhere); three and four rows of at most 16
+// super-blocks in the fused form (14336, 6144 and 4096 rows of 4096: three rows 11.1, 6.8 and
+// 6.5 us against 12.0, 7.5 and 7.1 before the shared fold; four rows 13.1, 8.1 and 7.8 against
+// 13.2, 8.8 and 7.8 for the expert kernel).
 bool gemv_q4k_x8_rows_pick(int n_out, int k, int rows) {
     if (k % 256 || k <= 0 || k > 64 * 256) return false;
     const int nb = k / 256;
     (void)n_out;
-    return rows == 2 || (rows == 3 && nb <= 16);
+    return rows == 2 || ((rows == 3 || rows == 4) && nb <= 16);
 }
 
-bool gemv_q4k_x8_rows_fused(int k, int rows) { return (rows == 2 || rows == 3) && k % 256 == 0 && k > 0 && k <= 16 * 256; }
+bool gemv_q4k_x8_rows_fused(int k, int rows) { return rows >= 2 && rows <= 4 && k % 256 == 0 && k > 0 && k <= 16 * 256; }
 
 void launch_gemv_q4k_x8_rows(const uint8_t* W, int n_out, int k, const uint8_t* ws, const float* x, int rows,
                              float* y, hipStream_t stream, const uint32_t* active) {
@@ -647,7 +650,7 @@ void launch_gemv_q4k_x8_rows(const uint8_t* W, int n_out, int k, const uint8_t* 
     const dim3 grid((unsigned)((n_out + rows_per_wg - 1) / rows_per_wg));
 #define SYN_XR(NR, FUSE)                                                                                    \
     do {                                                                                                     \
-        const size_t lds = (size_t)NR * xr_row_lds(nb) + (size_t)NR * XR_WAVES * 64 * 4;                     \
+        const size_t lds = (size_t)NR * xr_row_lds(nb) + (size_t)NR * XR_TS * 4;                             \
         static const hipError_t lds_ok = hipFuncSetAttribute((const void*)k_gemv_q4k_x8_rows<NR, FUSE>,       \
                                                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024); \
         (void)lds_ok; /* a refusal shows as the launch's error */                                            \
@@ -657,12 +660,16 @@ void launch_gemv_q4k_x8_rows(const uint8_t* W, int n_out, int k, const uint8_t* 
     if (x) {  // the rows quantized in the workgroups (gemv_q4k_x8_rows_fused)
         if (rows <= 2)
             SYN_XR(2, 1);
-        else
+        else if (rows == 3)
             SYN_XR(3, 1);
+        else
+            SYN_XR(4, 1);
     } else if (rows <= 2) {
         SYN_XR(2, 0);
-    } else {
+    } else if (rows == 3) {
         SYN_XR(3, 0);
+    } else {
+        SYN_XR(4, 0);
     }
 #undef SYN_XR
 }

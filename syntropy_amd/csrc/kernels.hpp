@@ -16,7 +16,7 @@ void launch_gemv_q(int ty, const uint8_t* W, int n_out, int k, const uint8_t* ws
                    float* y, hipStream_t stream, const uint32_t* active = nullptr);
 // gemv_q4k.hip: the Q4_K single-row decode kernel (activation row in LDS)
 bool q4k_dec_supported(int k);
-// Q4_K at 2 or 3 rows over X8 weights, where gemv_q4k_x8_rows_pick finds it the faster form, on
+// Q4_K at 2 to 4 rows over X8 weights, where gemv_q4k_x8_rows_pick finds it the faster form, on
 // Q8_K rows quantized by launch_act_quant
 bool gemv_q4k_x8_rows_pick(int n_out, int k, int rows);
 // with x (F32 rows, not ws) where gemv_q4k_x8_rows_fused(k, rows): the rows quantized in the

@@ -177,12 +177,14 @@ def test_gemm_x8_equals_oracle(S, rows, n_out, k):
                                           (4, 9, 16384), (5, 300, 256), (16, 8192, 4096), (17, 1000, 2304),
                                           (31, 33, 1536), (13, 4096, 14336), (2, 37, 1536), (2, 4096, 14336),
                                           (2, 9, 16384), (3, 8200, 2304), (3, 4096, 4096), (3, 6144, 4096),
-                                          (3, 37, 1536), (3, 300, 14336), (4, 14336, 4096)])
+                                          (3, 37, 1536), (3, 300, 14336), (4, 14336, 4096), (4, 6144, 4096),
+                                          (4, 37, 1536), (4, 300, 2304), (2, 300, 8192)])
 def test_x8_rows_2_to_31_equal_oracle(S, rows, n_out, k):
-    """2..31 rows over X8 weights: at two rows, and three of at most 16 super-blocks, the decode
-    kernel with the rows side by side in LDS (16, 32 or 64 lanes a row, lanes past the row's
-    blocks, a partial last workgroup; up to 16 super-blocks the rows quantized in its
-    workgroups); otherwise the decode expert kernel: the rows quantized once,
+    """2..31 rows over X8 weights: at two rows, and three or four of at most 16 super-blocks, the
+    decode kernel with the rows side by side in LDS (16, 32 or 64 lanes a row, lanes past the
+    row's blocks, a partial last workgroup, one fold lane per weight row and activation row; up
+    to 16 super-blocks the rows quantized in its workgroups); otherwise the decode expert kernel:
+    the rows quantized once,
     four-row groups on the int8 matrix cores, 16- or 32-row items (k need not be a multiple of
     2048: the X8 chunk addresses are computed per super-block)."""
     rs = np.random.default_rng(rows * 7 + n_out + k)
