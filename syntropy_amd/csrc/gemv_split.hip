@@ -564,6 +564,18 @@ SYN_DEV int qs_slot(int c, int j, int p) {
 // The same within a 64-byte Q4_0 row line: block j's 8 bytes at 8 (p & 1).
 SYN_DEV int qs_slot4(int c, int j, int p) { return 16 * (j ^ ((c >> 2) & 3)) + 8 * (p & 1); }
 
+// RN(h * x) for the F16 half `hi` of word w and an F32 x: v_fma_mix_f32 converts the half inside
+// the instruction (exactly) and adds +0.0, which rounds the product once; only a zero product's
+// sign can differ from a multiply (+0.0 for -0.0), which a sum that starts from +0.0 does not see.
+SYN_DEV float f16_mul_f32(uint32_t w, int hi, float x) {
+    float p;
+    if (hi)
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(p) : "v"(w), "v"(x));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(p) : "v"(w), "v"(x));
+    return p;
+}
+
 // Four Q4_0 code bytes -> the int8 values n - 8 of their low (sh 0) or high (sh 4) nibbles.
 SYN_DEV uint32_t q4_signed(uint32_t v, int sh) {
     return (((v >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
@@ -750,13 +762,19 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
         }
 #pragma unroll
         for (int j = 0; j < QS_S; ++j) {
-            float dw[4];
+            if constexpr (TT == 1) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dw[i] = f16_to_f32((uint16_t)(scw[i][j >> 1] >> (16 * (j & 1))));
+                for (int i = 0; i < 4; ++i)
+                    acc[0][i] = acc[0][i] + f16_mul_f32(scw[i][j >> 1], j & 1, dx[0][j]) * (float)d[j][0][i];
+            } else {
+                float dw[4];
 #pragma unroll
-            for (int t = 0; t < TT; ++t)
+                for (int i = 0; i < 4; ++i) dw[i] = f16_to_f32((uint16_t)(scw[i][j >> 1] >> (16 * (j & 1))));
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t][i] = acc[t][i] + (dw[i] * dx[t][j]) * (float)d[j][t][i];
+                for (int t = 0; t < TT; ++t)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[t][i] = acc[t][i] + (dw[i] * dx[t][j]) * (float)d[j][t][i];
+            }
         }
     }
     wait_vm<0>();  // the last (repeated) copies have landed before the workgroup ends
@@ -910,8 +928,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8_splitk(const uint8_t* __restric
             float t[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float dw = f16_to_f32((uint16_t)((j < 2 ? lo : hi) >> (16 * (j & 1))));
-                t[j] = (dw * dx[j]) * (float)d[j][i];
+                t[j] = f16_mul_f32(j < 2 ? lo : hi, j & 1, dx[j]) * (float)d[j][i];
             }
             const int oo = (4 * p + i) * 16 + c;  // the output: row 4 p + i, token c
             *reinterpret_cast<float4*>(tw + oo * QK_SB + 4 * (wave ^ (oo & 3))) = make_float4(t[0], t[1], t[2], t[3]);

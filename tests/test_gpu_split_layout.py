@@ -158,6 +158,45 @@ def test_split_q4_0_extreme_codes_equal_oracle(S):
         assert_same(host(y), want, f"Q4_0 extreme codes rows {rows}")
 
 
+# F16 weight scales across the range: subnormal (both signs), the largest finite, zeros of both
+# signs, ones, and ordinary values; the products dw * dx then run from subnormal F32 to large
+SCALE_BITS = np.array([0x0001, 0x0200, 0x03FF, 0x8001, 0x83FF, 0x7BFF, 0xFBFF, 0x0000, 0x8000,
+                       0x3C00, 0xBC00, 0x2E66, 0x1400, 0x0400, 0x5640, 0xD0F0], np.uint16)
+
+
+@pytest.mark.parametrize("ty,bb", [(o.Q8_0, 34), (o.Q4_0, 18)])
+@pytest.mark.parametrize("n_out,k", [(64, 2048), (300, 1024)])
+def test_split_extreme_scales_equal_oracle(S, ty, bb, n_out, k):
+    """Weights whose F16 scales span subnormals, the largest finite F16 and signed zeros,
+    against activation blocks of magnitudes 1e-6 to 1e4, at one row (the workgroups' quantization,
+    and the product on a quantized row) and at 2 to 128 rows (the split decode kernel, the int8
+    matrix-core GEMMs): the scale products dw * dx from subnormal F16 operands, each rounded once
+    as the reference rounds it."""
+    nb = k // 32
+    rng = np.random.default_rng(0x5CA1E + n_out + ty)
+    w = rng.integers(0, 256, (n_out * nb, bb), dtype=np.uint8)
+    sc = rng.choice(SCALE_BITS, size=n_out * nb)
+    w[:, 0] = (sc & 0xFF).astype(np.uint8)
+    w[:, 1] = (sc >> 8).astype(np.uint8)
+    w = w.reshape(-1)
+    W = S.repack(S.Weights(S.WeightType(ty), dev(w), n_out, k))
+    for rows in (1, 2, 8, 16, 32, 128):
+        # a magnitude per 32-value block, 1e-6 to 1e4: activation scales from F16 subnormals up
+        mag = np.repeat(np.float32(10.0) ** rng.integers(-6, 5, rows * k // 32).astype(np.float32), 32)
+        x = (rng.standard_normal(rows * k).astype(np.float32) * mag).astype(np.float32)
+        announce(f"split gemv {WT[ty]} extreme scales {n_out}x{k} rows={rows}")
+        y = torch.full((rows, n_out), float("nan"), device="cuda")
+        S.gemv(W, dev(x), rows, y=y)
+        want = o.gemv(ty, w, n_out, k, x, rows, threads=8)
+        assert_same(host(y), want, f"{WT[ty]} extreme scales rows {rows}")
+        if rows in (1, 8, 32):
+            ws = S.new_workspace(S.WeightType(ty), rows, k)
+            S.quantize_into(S.WeightType(ty), dev(x), rows, k, ws)
+            y.fill_(float("nan"))
+            S.gemv_quantized(W, ws, rows, y)
+            assert_same(host(y), want, f"{WT[ty]} extreme scales quantized rows {rows}")
+
+
 @pytest.mark.parametrize("ty,n_out,k,layout,ok", [
     (o.Q8_0, 64, 512, 2, False),   # SPLIT: the scale section sits after every block's codes
     (o.Q4_0, 64, 512, 2, False),
