@@ -65,10 +65,11 @@ void launch_split_repack(int ty, const uint8_t* src, uint8_t* dst, uint64_t byte
 // ---- 1 to 8 rows ---------------------------------------------------------------------------------
 
 constexpr int SPLIT_WAVES = 8;
-// wavefronts of a workgroup that quantizes its row itself: sixteen quantize the row half as often
-// as eight (Q4_0 4096 x 4096: 5.15 against 5.74 us a call, Q4_0 4096 x 14336: 12.4 against 14.5),
-// where the matrix has rows for a workgroup of sixteen on each of gfx950's 256 CUs; below that,
-// eight (Q8_0 1024 x 4096: 4.65 against 5.52 us)
+// wavefronts of a workgroup that quantizes its row itself: for Q4_0 sixteen quantize the row half
+// as often as eight (4096 x 4096: 5.03 against 5.38 us a call, 8192 x 4096: 6.39 against 7.08,
+// 4096 x 14336: 11.9 against 12.7) where the matrix has rows for a workgroup of sixteen on each
+// of gfx950's 256 CUs; below that, and for Q8_0, whose rows carry twice the bytes, eight
+// (Q8_0 14336 x 4096: 12.75 against 13.75 us, 4096 x 14336: 16.5 against 17.2)
 constexpr int FUSE_WAVES = 16;
 constexpr int FUSE_WAVES_FEW = 8;
 constexpr int GFX950_CUS = 256;
@@ -336,7 +337,7 @@ void launch_gemv_split_fused(int ty, const uint8_t* W, int n_out, int k, const f
             hipLaunchKernelGGL((k_gemv_split<T_Q4_0, 1, 2, WV>), grid, dim3(64 * WV), lds, stream, W, n_out, k,
                                nullptr, nullptr, nullptr, 1, y, active, 0, x);
     };
-    if (n_out >= FUSE_WAVES * GFX950_CUS)
+    if (ty == T_Q4_0 && n_out >= FUSE_WAVES * GFX950_CUS)
         go(std::integral_constant<int, FUSE_WAVES>{});
     else
         go(std::integral_constant<int, FUSE_WAVES_FEW>{});

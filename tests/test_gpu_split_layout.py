@@ -95,8 +95,8 @@ def test_split_config_shapes_equal_oracle(S, ty, n_out, k, rowss):
 @pytest.mark.parametrize("n_out,k", [(4096 + 37, 1024), (4096 + 5, 14336 + 32), (2048 + 9, 4096)])
 def test_split_one_row_workgroup_fold_equal_oracle(S, ty, n_out, k):
     """One row quantized in the product's workgroups, whose rows are folded together: workgroups
-    of sixteen rows (4096 rows or more) and of eight, the last one partly past the matrix; rows of
-    one to four 128-block fold chunks, the last one partial."""
+    of sixteen rows (Q4_0 at 4096 rows or more) and of eight, the last one partly past the
+    matrix; rows of one to four 128-block fold chunks, the last one partial."""
     w = o.quantize(ty, o.normal(0x5E21 + n_out + k, 0.02, n_out * k))
     check(S, ty, n_out, k, 1, 0x5E22 + n_out, w)
 
