@@ -545,8 +545,11 @@ struct QsCfg {
     static constexpr int SC_OFF = A_OFF + TW * QS_S * 32;
     static constexpr int DX_OFF = SC_OFF + QS_RW * QS_S * 2;
     static constexpr int STAGE = DX_OFF + TW * QS_S * 4;
-    // ring stages: as many as 64 KB hold, at most QS_NS_MAX
-    static constexpr int NS = 64 * 1024 / STAGE < QS_NS_MAX ? 64 * 1024 / STAGE : QS_NS_MAX;
+    // stages a barrier step consumes: two for one token tile a wavefront pair (few tokens), else one
+    static constexpr int SPI = TT == 1 && TG == 1 ? 2 : 1;
+    // ring stages: as many as 64 KB hold, at most QS_NS_MAX (three stages a step beyond one)
+    static constexpr int NSM = SPI == 2 ? 6 : QS_NS_MAX;
+    static constexpr int NS = 64 * 1024 / STAGE < NSM ? 64 * 1024 / STAGE : NSM;
     // copies per stage: row codes, token codes, and the two scale sets, each set whole or in
     // SPARTS / DPARTS parts, so that the count splits evenly over the wavefronts
     static constexpr int WCOPIES = QS_RW * WL / 1024;
@@ -555,7 +558,7 @@ struct QsCfg {
     static constexpr int TOTAL = WCOPIES + TW / 8 + SPARTS + DPARTS;
     static constexpr int COPIES = TOTAL / NW;  // per wavefront per stage
     static_assert(TOTAL % NW == 0, "copies split evenly");
-    static_assert(NS >= 2 && COPIES * (NS - 2) <= 63, "the wait count fits vmcnt");
+    static_assert(NS >= 2 * SPI && COPIES * (NS - 2 * SPI) <= 63, "the wait count fits vmcnt");
 };
 
 // The LDS byte offset, within its 128-byte line, of block j's 8 bytes at 8 p for line c.
@@ -716,7 +719,7 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
     qs_plan<FMT, TT, TG>(cp, W, scales, xq, xd, n_out, nb, k, T, row0, t0, wave, lane);
     const uint32_t ring = lds_addr(lds);
 #pragma unroll
-    for (int s = 0; s < C::NS - 1; ++s)
+    for (int s = 0; s < C::NS - C::SPI; ++s)
         qs_issue<FMT, TT, TG>(cp, ring + (uint32_t)(C::STAGE * s), s < nst ? s : nst - 1);
     float acc[TT][4];
 #pragma unroll
@@ -724,11 +727,7 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[t][i] = 0.0f;
     const v4i_s z = {0, 0, 0, 0};
-    for (int s = 0; s < nst; ++s) {
-        wait_vm<C::COPIES * (C::NS - 2)>();  // this wavefront's copies of stage s have landed
-        lds_barrier();                       // everyone's have, and stage s - 1 is read out
-        const int sn = s + C::NS - 1;
-        qs_issue<FMT, TT, TG>(cp, ring + (uint32_t)(C::STAGE * (sn % C::NS)), sn < nst ? sn : nst - 1);
+    auto body = [&](int s) __attribute__((always_inline)) {
         const uint8_t* st = lds + C::STAGE * (s % C::NS);
         // the lane's rows 4 p + i: four scales each, 8 bytes a row
         const v4u_s sc01 = *reinterpret_cast<const v4u_s*>(st + C::SC_OFF + (16 * rg + 4 * p) * 8);
@@ -777,6 +776,20 @@ __global__ __launch_bounds__(64 * 2 * TG) void k_gemm_q8_staged(const uint8_t* _
                     for (int i = 0; i < 4; ++i) acc[t][i] = acc[t][i] + (dw[i] * dx[t][j]) * (float)d[j][t][i];
             }
         }
+    };
+    // SPI stages a barrier: their copies have landed (the NS - 2 SPI after them may fly), the
+    // previous step's are read out, and the next SPI go into those slots
+    for (int s = 0; s < nst; s += C::SPI) {
+        wait_vm<C::COPIES * (C::NS - 2 * C::SPI)>();
+        lds_barrier();
+#pragma unroll
+        for (int u = 0; u < C::SPI; ++u) {
+            const int sn = s + C::NS - C::SPI + u;
+            qs_issue<FMT, TT, TG>(cp, ring + (uint32_t)(C::STAGE * (sn % C::NS)), sn < nst ? sn : nst - 1);
+        }
+#pragma unroll
+        for (int u = 0; u < C::SPI; ++u)
+            if (s + u < nst) body(s + u);  // uniform
     }
     wait_vm<0>();  // the last (repeated) copies have landed before the workgroup ends
 #pragma unroll
