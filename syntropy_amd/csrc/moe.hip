@@ -182,21 +182,54 @@ __global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ ro
     }
 }
 
-// Logits at many tokens: one workgroup per 16 tokens x 16 experts, one (token, expert) pair per
-// thread, so a wavefront's lanes read 4 token rows and 16 router rows (LDS broadcasts).  The
-// rows stream through LDS in chunks of 8 blocks (1 KB a row, padded by 16 bytes so the 16 router
-// rows of a read fall in distinct banks), double-buffered by DMA.  Each thread sums its pair's
-// 32-term blocks in order and keeps the pairwise tree as a binary stack: block j's sum merges
-// with the completed subtrees left of it (level L when bit L of j is set, left + right), and at
-// the end the subtrees of the set bits of nblk fold from the smallest up (left + right).  That is
+// Logits at many tokens: one workgroup per 32 tokens x 16 experts, two (token, expert) pairs per
+// thread (tokens 2g and 2g + 1 against one expert), so each router value a thread reads serves
+// two tokens: a wavefront's lanes read 8 token rows and 16 router rows (LDS broadcasts), 12
+// distinct 16-byte chunks per pair and step against 20 at one pair a thread.  The rows stream
+// through LDS in chunks of 4 blocks (512 bytes a row, padded by 16 bytes so the 16 router rows of
+// a read fall in distinct banks), double-buffered by DMA.  Each thread sums each pair's 32-term
+// blocks in order and keeps its pairwise tree as a binary stack: block j's sum merges with the
+// completed subtrees left of it (level L when bit L of j is set, left + right), and at the end
+// the subtrees of the set bits of nblk fold from the smallest up (left + right).  That is
 // reduce.rs's level-by-level tree with the odd value carried: the tree over n values is the tree
 // over the first 2^m (the largest power of two below n) plus the tree over the rest.
-constexpr int LT_T = 16, LT_E = 16, LT_CB = 8;
-constexpr int LT_ROW = LT_CB * 128 + 16;          // a row's chunk in LDS: 1,040 bytes
-constexpr int LT_STAGE = (LT_T + LT_E) * LT_ROW;  // 33,280 bytes; two stages
+constexpr int LT_T = 32, LT_E = 16, LT_CB = 4;
+constexpr int LT_ROW = LT_CB * 128 + 16;          // a row's chunk in LDS: 528 bytes
+constexpr int LT_NR = LT_T + LT_E;                // rows a stage holds
+constexpr int LT_STAGE = LT_NR * LT_ROW;          // 25,344 bytes
+constexpr int LT_NS = 3;                           // ring stages: two chunks in flight
+constexpr int LT_CPW = LT_NR / 4;                 // copies per wavefront per chunk: one row each
 constexpr int LT_LEVELS = 9;                      // nblk <= 256
 
-__global__ __launch_bounds__(256) void k_moe_logits_tile(const float* __restrict__ router,
+// one pair's block sum pushed onto its tree stack (block j, in block order)
+SYN_DEV void lt_push(float (&st)[LT_LEVELS], float v, int j) {
+    bool carry = true;
+#pragma unroll
+    for (int L = 0; L < LT_LEVELS; ++L) {
+        if (carry) {
+            if ((j >> L) & 1) {
+                v = st[L] + v;
+            } else {
+                st[L] = v;
+                carry = false;
+            }
+        }
+    }
+}
+SYN_DEV float lt_total(const float (&st)[LT_LEVELS], int nblk) {
+    float total = 0.0f;
+    bool have = false;
+#pragma unroll
+    for (int L = 0; L < LT_LEVELS; ++L) {
+        if ((nblk >> L) & 1) {
+            total = have ? st[L] + total : st[L];
+            have = true;
+        }
+    }
+    return total;
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_moe_logits_tile(const float* __restrict__ router,
                                                          const float* __restrict__ x, int rows, int hidden,
                                                          int n_experts, float* __restrict__ logits,
                                                          const uint32_t* __restrict__ active) {
@@ -207,13 +240,13 @@ __global__ __launch_bounds__(256) void k_moe_logits_tile(const float* __restrict
     rows = active_rows(active, 0, rows);
     if (t0 >= rows) return;  // uniform: tokens past the step's active rows
     const int nblk = hidden / 32;
-    // wavefront w copies stage rows 8w .. 8w + 7 (tokens 0-15, then experts 0-15): lane l the
-    // 16 bytes l of the row's chunk, one copy per row (8 per chunk per wavefront)
+    // wavefront w copies stage rows 12w .. 12w + 11 (tokens 0-31, then experts 0-15): lane l < 32
+    // the 16 bytes l of the row's chunk, one copy per row
     auto issue = [&](int c0, uint8_t* stage) {
         const int nb = nblk - c0 < LT_CB ? nblk - c0 : LT_CB;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = 8 * wave + i;
+        for (int i = 0; i < LT_CPW; ++i) {
+            const int r = LT_CPW * wave + i;
             const float* base;
             if (r < LT_T) {
                 const int t = t0 + r < rows ? t0 + r : rows - 1;
@@ -225,73 +258,59 @@ __global__ __launch_bounds__(256) void k_moe_logits_tile(const float* __restrict
             if (lane < 8 * nb) lds_dma16(16u * (uint32_t)lane + 128u * (uint32_t)c0, base, lds_addr(stage + r * LT_ROW));
         }
     };
-    const int tt = 4 * wave + (lane >> 4), ee = lane & 15;
-    float st[LT_LEVELS];
+    const int tg = 4 * wave + (lane >> 4), ee = lane & 15;  // tokens 2 tg, 2 tg + 1; expert ee
+    float st0[LT_LEVELS], st1[LT_LEVELS];
 #pragma unroll
-    for (int L = 0; L < LT_LEVELS; ++L) st[L] = 0.0f;
+    for (int L = 0; L < LT_LEVELS; ++L) st0[L] = st1[L] = 0.0f;
     issue(0, lt_lds);
-    for (int c0 = 0, cur = 0; c0 < nblk; c0 += LT_CB, cur ^= 1) {
-        if (c0 + LT_CB < nblk) {
-            issue(c0 + LT_CB, lt_lds + (cur ^ 1) * LT_STAGE);
-            wait_vm<8>();  // this wavefront's copies of the current chunk, older than the next's
-        } else {
+    if (LT_CB < nblk) issue(LT_CB, lt_lds + LT_STAGE);
+    for (int c0 = 0, cur = 0; c0 < nblk; c0 += LT_CB, cur = cur == LT_NS - 1 ? 0 : cur + 1) {
+        if (c0 + LT_CB < nblk)
+            wait_vm<LT_CPW>();  // this wavefront's copies of the current chunk, older than the next's
+        else
             wait_vm<0>();
-        }
-        lds_barrier();
+        lds_barrier();  // everyone's copies of this chunk landed, and the chunk before is read out
+        if (c0 + 2 * LT_CB < nblk)  // into the slot of the chunk before
+            issue(c0 + 2 * LT_CB, lt_lds + (cur == 0 ? LT_NS - 1 : cur - 1) * LT_STAGE);
         const uint8_t* stage = lt_lds + cur * LT_STAGE;
-        const float4* xr = reinterpret_cast<const float4*>(stage + tt * LT_ROW);
+        const float4* xr0 = reinterpret_cast<const float4*>(stage + (2 * tg) * LT_ROW);
+        const float4* xr1 = reinterpret_cast<const float4*>(stage + (2 * tg + 1) * LT_ROW);
         const float4* wr = reinterpret_cast<const float4*>(stage + (LT_T + ee) * LT_ROW);
         const int nb = nblk - c0 < LT_CB ? nblk - c0 : LT_CB;
-        // four blocks' sums at a time (independent chains), pushed in block order: block j's sum
-        // merges with the left subtrees its set low bits complete
-        for (int b4 = 0; b4 < nb; b4 += 4) {
-            float acc[4];
+        // the chunk's block sums (independent chains), pushed in block order
+        float acc0[LT_CB], acc1[LT_CB];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) acc[u] = 0.0f;
+        for (int u = 0; u < LT_CB; ++u) acc0[u] = acc1[u] = 0.0f;
+#pragma unroll 2
+        for (int q = 0; q < 8; ++q) {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int bb = b4 + u < nb ? b4 + u : b4;  // past the chunk: a valid block, unused
-                    const float4 xv = xr[8 * bb + q], wv = wr[8 * bb + q];
-                    acc[u] = acc[u] + wv.x * xv.x;
-                    acc[u] = acc[u] + wv.y * xv.y;
-                    acc[u] = acc[u] + wv.z * xv.z;
-                    acc[u] = acc[u] + wv.w * xv.w;
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if (b4 + u < nb) {
-                    const int j = c0 + b4 + u;
-                    float v = acc[u];
-                    bool carry = true;
-#pragma unroll
-                    for (int L = 0; L < LT_LEVELS; ++L) {
-                        if (carry) {
-                            if ((j >> L) & 1) {
-                                v = st[L] + v;
-                            } else {
-                                st[L] = v;
-                                carry = false;
-                            }
-                        }
-                    }
-                }
+            for (int u = 0; u < LT_CB; ++u) {
+                const int bb = u < nb ? u : 0;  // past the chunk: a valid block, unused
+                const float4 wv = wr[8 * bb + q], xa = xr0[8 * bb + q], xb = xr1[8 * bb + q];
+                acc0[u] = acc0[u] + wv.x * xa.x;
+                acc0[u] = acc0[u] + wv.y * xa.y;
+                acc0[u] = acc0[u] + wv.z * xa.z;
+                acc0[u] = acc0[u] + wv.w * xa.w;
+                acc1[u] = acc1[u] + wv.x * xb.x;
+                acc1[u] = acc1[u] + wv.y * xb.y;
+                acc1[u] = acc1[u] + wv.z * xb.z;
+                acc1[u] = acc1[u] + wv.w * xb.w;
             }
         }
-        lds_barrier();  // this stage is refilled two chunks on
-    }
-    float total = 0.0f;
-    bool have = false;
 #pragma unroll
-    for (int L = 0; L < LT_LEVELS; ++L) {
-        if ((nblk >> L) & 1) {
-            total = have ? st[L] + total : st[L];
-            have = true;
+        for (int u = 0; u < LT_CB; ++u) {
+            if (u < nb) {
+                lt_push(st0, acc0[u], c0 + u);
+                lt_push(st1, acc1[u], c0 + u);
+            }
         }
     }
-    if (t0 + tt < rows && e0 + ee < n_experts) logits[(int64_t)(t0 + tt) * n_experts + e0 + ee] = total;
+    const float tot0 = lt_total(st0, nblk), tot1 = lt_total(st1, nblk);
+    const int ta = t0 + 2 * tg, tb = ta + 1;
+    if (e0 + ee < n_experts) {
+        if (ta < rows) logits[(int64_t)ta * n_experts + e0 + ee] = tot0;
+        if (tb < rows) logits[(int64_t)tb * n_experts + e0 + ee] = tot1;
+    }
 }
 
 // The many-token logits kernel from this many rows on (fewer: too few workgroups to fill the
@@ -444,10 +463,10 @@ void launch_moe_route(const float* router, const float* x, int rows, int hidden,
     (void)lds_ok4;
     if (rows >= LT_MIN_ROWS && ((uintptr_t)x & 15) == 0 && ((uintptr_t)router & 15) == 0) {
         static const hipError_t lt_ok = hipFuncSetAttribute((const void*)k_moe_logits_tile,
-                                                            hipFuncAttributeMaxDynamicSharedMemorySize, 2 * LT_STAGE);
+                                                            hipFuncAttributeMaxDynamicSharedMemorySize, LT_NS * LT_STAGE);
         (void)lt_ok;  // a refusal shows as the launch's error
         const dim3 lg((rows + LT_T - 1) / LT_T, (n_experts + LT_E - 1) / LT_E);
-        hipLaunchKernelGGL(k_moe_logits_tile, lg, dim3(256), 2 * LT_STAGE, stream, router, x, rows, hidden, n_experts,
+        hipLaunchKernelGGL(k_moe_logits_tile, lg, dim3(256), LT_NS * LT_STAGE, stream, router, x, rows, hidden, n_experts,
                            logits, active);
     } else if (((uintptr_t)x & 15) == 0)
         hipLaunchKernelGGL(k_moe_logits<true>, grid, dim3(256), lds, stream, router, x, rows, hidden, n_experts, logits,
