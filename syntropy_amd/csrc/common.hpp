@@ -153,6 +153,24 @@ SYN_DEV int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// a * b + c for operands of at most 24 significant bits (|a|, |b| < 2^23): one full-rate
+// v_mad_i32_i24 instead of the quarter-rate 32-bit multiply.  Exact while the result fits 32 bits.
+SYN_DEV int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
+// The Q4_K super-block's exact S2 = sum_j m_j * s_j: 6-bit minimums m_j against the 32-value
+// code sums s_j (|s_j| <= 32 * 128), every operand within 24 bits.  (S1 = sum_j sc_j * D_j takes
+// mad24 the same way: |D_j| <= 32 * 15 * 128 < 2^16.)
+SYN_DEV int q4k_s2(const int (&mn)[8], int4 sa, int4 sb) {
+    int s2 = __mul24(mn[0], sa.x);
+    s2 = mad24(mn[1], sa.y, s2);
+    s2 = mad24(mn[2], sa.z, s2);
+    s2 = mad24(mn[3], sa.w, s2);
+    s2 = mad24(mn[4], sb.x, s2);
+    s2 = mad24(mn[5], sb.y, s2);
+    s2 = mad24(mn[6], sb.z, s2);
+    return mad24(mn[7], sb.w, s2);
+}
+
 // Lane rotation by one inside groups of P lanes (the in-order fold hands its running sum to
 // the next lane of the group): quad_perm [3,0,1,2], row_ror:1, or wave_ror:1.
 template <int P>

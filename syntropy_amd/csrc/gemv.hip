@@ -82,11 +82,10 @@ SYN_DEV float q4k_term(const uint32_t* wb, const ActPtrs& a, int r, int64_t b) {
             lo = sdot4(q & 0x0F0F0F0Fu, xl[t], lo);
             hi = sdot4((q >> 4) & 0x0F0F0F0Fu, xh[t], hi);
         }
-        s1 += sc[2 * g] * lo + sc[2 * g + 1] * hi;
+        s1 = mad24(sc[2 * g + 1], hi, mad24(sc[2 * g], lo, s1));
     }
     const int4 sa = xs4[0], sb = xs4[1];
-    const int s2 = mn[0] * sa.x + mn[1] * sa.y + mn[2] * sa.z + mn[3] * sa.w + mn[4] * sb.x +
-                   mn[5] * sb.y + mn[6] * sb.z + mn[7] * sb.w;
+    const int s2 = q4k_s2(mn, sa, sb);
     return (d * dx) * (float)s1 - (dmin * dx) * (float)s2;
 }
 

@@ -154,13 +154,12 @@ SYN_DEV float q4k_term_lds(const v4u* wv, const uint8_t* lds, int nb, int b) {
             lo = sdot4(q & 0x0F0F0F0Fu, xl[t], lo);
             hi = sdot4((q >> 4) & 0x0F0F0F0Fu, xh[t], hi);
         }
-        s1 += sc[2 * g] * lo + sc[2 * g + 1] * hi;
+        s1 = mad24(sc[2 * g + 1], hi, mad24(sc[2 * g], lo, s1));
     }
     const int4 sa = *reinterpret_cast<const int4*>(lds + xs_off(nb) + b * SUMW);
     const int4 sb = *reinterpret_cast<const int4*>(lds + xs_off(nb) + b * SUMW + 16);
     const float dx = reinterpret_cast<const float*>(lds + xd_off(nb))[b];
-    const int s2 = mn[0] * sa.x + mn[1] * sa.y + mn[2] * sa.z + mn[3] * sa.w + mn[4] * sb.x +
-                   mn[5] * sb.y + mn[6] * sb.z + mn[7] * sb.w;
+    const int s2 = q4k_s2(mn, sa, sb);
     return (d * dx) * (float)s1 - (dmin * dx) * (float)s2;
 }
 
