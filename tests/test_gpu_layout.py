@@ -196,6 +196,24 @@ def test_x8_rows_2_to_31_equal_oracle(S, rows, n_out, k):
     assert_same(got, o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=16), "x8 rows")
 
 
+@pytest.mark.parametrize("n_out,k", [(14336, 4096), (4096 + 9, 2048), (37, 4096), (16 * 257 + 3, 4096),
+                                     (16 * 512, 2048)])
+def test_x8_rows_whole_runs_equal_oracle(S, n_out, k):
+    """2 to 8 rows over X8 rows of whole 8-block runs: the decode kernel with the rows quantized in
+    its workgroups (2 and 3 rows) and the quantization launch then the line-order expert kernel
+    (5, 7, 8 rows), at one and two runs a row, a partial last 16-row group, and thousands of row
+    groups."""
+    rs = np.random.default_rng(n_out * 3 + k)
+    w = random_q4k(rs, n_out, k)
+    W = S.repack(S.Weights(S.WeightType.Q4K, dev(w), n_out, k))
+    for rows in (2, 3, 5, 7, 8):
+        x = o.normal(0xF1 + rows + n_out, 1.0, rows * k).reshape(rows, k)
+        announce(f"x8 whole-run rows={rows} {n_out}x{k}")
+        y = torch.full((rows, n_out), float("nan"), device="cuda")
+        S.gemv(W, dev(x), rows, y=y)
+        assert_same(host(y), o.gemv(o.Q4_K, w, n_out, k, x, rows, threads=16), f"x8 whole-run rows {rows}")
+
+
 def test_x8_refusals(S):
     W = S.repack(S.Weights(S.WeightType.Q4K, torch.zeros(64 * 6 * 144, dtype=torch.uint8, device="cuda"), 64, 1536))
     x = torch.zeros(32, 1536, device="cuda")
