@@ -42,6 +42,9 @@ sys.path.insert(0, ROOT)
 METRIC = "Q4_K GEMV weight GB/s (% HBM peak); MoE layer tokens/s at 64-token decode"
 HBM_PEAK_GBS = 8000.0
 F16_MFMA_PEAK_TFLOPS = 2500.0
+# Non-packed F32 VALU issue: 256 CUs x 4 SIMDs x 16 lanes at the 2.4 GHz peak engine clock, in
+# tera lane-operations per second (a wave64 VALU instruction holds a 16-lane SIMD four cycles)
+VALU_PEAK_TOPS = 256 * 4 * 16 * 2.4e9 / 1e12
 LAYER = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate", 14336, 4096), ("up", 14336, 4096),
          ("down", 4096, 14336)]
 Q4K, Q8_0, Q4_0 = 12, 8, 2
@@ -422,6 +425,14 @@ def bench_cfgs(torch, S, a):
                             "kernel_us": round(kt, 3), "kernel_alg_gbs": round(alg / (kt * 1e-6) / 1e9, 1),
                             "kernel_frac": round(alg / (kt * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                             "tflops": round(2.0 * T * n * k / (step * 1e-6) / 1e12, 2)}
+        if T > 1:
+            # the F32 term of every (output, block): convert, two multiplies, add (gemv.rs:539-547),
+            # one VALU lane-operation each, against the VALU issue peak
+            ops = 4.0 * T * n * (k // 32)
+            rows_res[str(T)]["valu_roofline"] = {
+                "bound": "valu", "ops_per_launch": int(ops), "unit": "T lane-ops/s",
+                "achieved": round(ops / (kt * 1e-6) / 1e12, 2), "peak": round(VALU_PEAK_TOPS, 2),
+                "frac": round(ops / (kt * 1e-6) / 1e12 / VALU_PEAK_TOPS, 4)}
         if T == 1:
             rows_res["1"]["product_on_a_quantized_row_us"] = round(kern, 3)
     res["cfg2"] = {"workload": "Q8_0 14336x4096 (Llama-3-8B FFN up) Gemv at T rows, Q8_0 activations, "
