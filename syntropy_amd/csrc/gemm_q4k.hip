@@ -374,39 +374,55 @@ constexpr int GM_LOOP_LDS = 2 * GM_WA + 3 * GM_TB;
 static_assert(GM_WA % 16 == 0 && GM_TB % 16 == 0 && GM_LOOP_LDS <= 160 * 1024, "GEMM LDS");
 
 // The super-block loop of both GEMM kernels.  `issue(b, stage, tail)` issues the wavefront's
-// `live` loads of super-block b.  Super-block b's products run first, then b - 1's fold
-// (independent work the wavefront can issue between the products), with the two sets of exact
-// sums alternating by parity.  Super-block 0 has no fold before it, so it is peeled: the loop's
-// products and fold are one straight run of code the scheduler can interleave.
-template <int NMT, class Issue>
+// loads of super-block b.  Super-block b's products run first, then b - 1's fold (independent
+// work the wavefront can issue between the products), with the two sets of exact sums
+// alternating by parity.  Super-block 0 has no fold before it, so it is peeled: the loop's
+// products and fold are one straight run of code the scheduler can interleave.  Two schedules
+// of the loads, each a super-block ahead of the products:
+//   AHEAD: two barriers a super-block; once every wavefront has left b's stage, b + 2's loads go
+//     to it at the end of b's step, before the wait for b + 1's, so both may be in flight (the
+//     dense GEMM: 425-434 against 438-444 us a launch at 2048 tokens);
+//   otherwise one barrier a super-block; once every wavefront's loads of b have landed and every
+//     wavefront has left b - 1's products and b - 2's fold, b + 1's loads go to b - 1's stage
+//     and b - 2's tail slot (the MoE layer at 2048 tokens: 1.56 against 1.60 ms).
+// On return every wavefront is done with the two stages (the caller may reuse them); the tail
+// ring may still be read.
+template <int NMT, bool AHEAD, class Issue>
 SYN_DEV void gemm_loop(int nb, int live, uint8_t* smem, int wave, int lane, Issue&& issue,
                        v4f (&acc)[GM_MT][GM_NT]) {
     uint8_t* tails = smem + 2 * GM_WA;
     issue(0, smem, tails);
-    if (nb > 1) issue(1, smem + GM_WA, tails + GM_TB);
+    if (AHEAD && nb > 1) issue(1, smem + GM_WA, tails + GM_TB);
     v4f d0[GM_MT][GM_NT], d1[GM_MT][GM_NT];
     GemmHdr h0, h1;
     int slot = 0;  // tail ring slot of b
     auto step = [&](auto fold, int b, v4f (&dc)[GM_MT][GM_NT], GemmHdr& hc, const v4f (&dp)[GM_MT][GM_NT],
                     const GemmHdr& hp) __attribute__((always_inline)) {
-        uint8_t* stage = smem + (b & 1) * GM_WA;
-        const int prev = slot == 0 ? 2 : slot - 1;  // the slot of b - 1, and of b + 2 after the fold
-        // this lane's loads of b have landed once at most those of b + 1 are in flight
-        wait_vm_n<GM_PER_WAVE>(b + 1 < nb ? live : 0);
+        const int prev = slot == 0 ? 2 : slot - 1;  // the slot of b - 1 (b + 2's after the fold)
+        const int next = slot == 2 ? 0 : slot + 1;  // the slot of b + 1 (b - 2's)
+        if constexpr (AHEAD) {
+            wait_vm_n<GM_PER_WAVE>(b + 1 < nb ? live : 0);  // at most b + 1's loads in flight
+        } else {
+            wait_vm<0>();  // b's loads, the only ones in flight
+        }
         lds_barrier();
-        gemm_mfma<NMT>(stage, wave, lane, dc, hc);
+        if (!AHEAD && b + 1 < nb) issue(b + 1, smem + ((b + 1) & 1) * GM_WA, tails + next * GM_TB);
+        gemm_mfma<NMT>(smem + (b & 1) * GM_WA, wave, lane, dc, hc);
         if constexpr (decltype(fold)::value) {
             gemm_fold<NMT>(tails + prev * GM_TB, lane, dp, hp, acc);
         }
-        lds_barrier();
-        if (b + 2 < nb) issue(b + 2, stage, tails + prev * GM_TB);
-        slot = slot == 2 ? 0 : slot + 1;
+        if constexpr (AHEAD) {
+            lds_barrier();
+            if (b + 2 < nb) issue(b + 2, smem + (b & 1) * GM_WA, tails + prev * GM_TB);
+        }
+        slot = next;
     };
     step(std::false_type{}, 0, d0, h0, d1, h1);
     for (int b = 1; b < nb; b += 2) {
         step(std::true_type{}, b, d1, h1, d0, h0);
         if (b + 1 < nb) step(std::true_type{}, b + 1, d0, h0, d1, h1);
     }
+    if constexpr (!AHEAD) lds_barrier();
     const int last = slot == 0 ? 2 : slot - 1;  // the slot of nb - 1
     if (nb & 1)
         gemm_fold<NMT>(tails + last * GM_TB, lane, d0, h0, acc);
@@ -432,10 +448,10 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_q4k(GemmArgs g) {
     auto issue = [&](int b, uint8_t* stage, uint8_t* tail) { gemm_issue(g, sl, wave, lane, b, t0, stage, tail); };
     // the 16-token tiles holding active rows (a last tile of fewer rows computes only those)
     switch ((T - t0 < GM_TT ? T - t0 + 15 : GM_TT) / 16) {
-        case 1: gemm_loop<1>(g.nb, live, smem, wave, lane, issue, acc); break;
-        case 2: gemm_loop<2>(g.nb, live, smem, wave, lane, issue, acc); break;
-        case 3: gemm_loop<3>(g.nb, live, smem, wave, lane, issue, acc); break;
-        default: gemm_loop<GM_MT>(g.nb, live, smem, wave, lane, issue, acc); break;
+        case 1: gemm_loop<1, true>(g.nb, live, smem, wave, lane, issue, acc); break;
+        case 2: gemm_loop<2, true>(g.nb, live, smem, wave, lane, issue, acc); break;
+        case 3: gemm_loop<3, true>(g.nb, live, smem, wave, lane, issue, acc); break;
+        default: gemm_loop<GM_MT, true>(g.nb, live, smem, wave, lane, issue, acc); break;
     }
 
     const int c = lane & 15, p = lane >> 4;
@@ -638,7 +654,6 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
             toff = tp * (wave == 2 ? 32u : 36u) + token_of(lane) * 4u;
         }
     }
-    const int live = sl.nw + GM_ASLOT / GM_WAVES + (MODE == 0 ? (wave < 4 ? 1 : 0) : sl.nt);
     // super-block b of the tile's rows: 144 b on in GGUF order, 64 rows' blocks on in TILE64
     const size_t bstep = g.layout == LAYOUT_TILE64 ? (size_t)TILE64_ROWS * 144 : 144;
     auto issue = [&](int b, uint8_t* stage, uint8_t* tail) {
@@ -682,10 +697,10 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_moe_gemm(MoeGemmArgs g) {
     // the 16-token tiles holding entries (the padding of an expert's last tile is not computed;
     // its outputs are dropped)
     switch ((nvalid + 15) / 16) {
-        case 1: gemm_loop<1>(g.nb, live, smem, wave, lane, issue, acc); break;
-        case 2: gemm_loop<2>(g.nb, live, smem, wave, lane, issue, acc); break;
-        case 3: gemm_loop<3>(g.nb, live, smem, wave, lane, issue, acc); break;
-        default: gemm_loop<GM_MT>(g.nb, live, smem, wave, lane, issue, acc); break;
+        case 1: gemm_loop<1, false>(g.nb, 0, smem, wave, lane, issue, acc); break;
+        case 2: gemm_loop<2, false>(g.nb, 0, smem, wave, lane, issue, acc); break;
+        case 3: gemm_loop<3, false>(g.nb, 0, smem, wave, lane, issue, acc); break;
+        default: gemm_loop<GM_MT, false>(g.nb, 0, smem, wave, lane, issue, acc); break;
     }
     const int c = lane & 15, p = lane >> 4;
     if constexpr (MODE == 0) {
