@@ -114,7 +114,7 @@ def host_info():
 
 
 def cpu_threads():
-    # a one-GPU box's CPU share is 16 threads; no more than the process may use
+    # one GPU's share of the host is 16 threads; no more than the process may use
     return max(1, min(16, len(os.sched_getaffinity(0))))
 
 

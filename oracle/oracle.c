@@ -863,7 +863,8 @@ static void int_rows(int ty, const uint8_t* w, size_t n_out, size_t k, const uin
 /* |w| as unsigned bytes times x * sign(w) as signed bytes (vpmaddubsw cannot saturate:       */
 /* |w| <= 128, |x| <= 127), pairs summed by vpmaddwd, then a horizontal add.  The sums are     */
 /* exact, the F32 terms and their order are int_rows', so the outputs are its bits (the tests */
-/* compare them).  This is the timed CPU baseline; the portable form above is the checker.   */
+/* compare them).  This is the timed CPU baseline; the portable form above is the reference  */
+/* restatement the tests compare the GPU outputs with.                                        */
 /* ===================================================================================== */
 #include <immintrin.h>
 

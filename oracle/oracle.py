@@ -234,8 +234,8 @@ def act_quantize(kind: int, x, rows: int, k: int):
 
 # ---- GEMV ----------------------------------------------------------------------------------
 def gemv(ty: int, w, n_out: int, k: int, x, rows: int, threads: int = 1, level: int = 0) -> np.ndarray:
-    """level 0: the portable kernels (the checker); 1: the reference's x86 level (8-row groups,
-    AVX2 block sums), the same bits, timed as the CPU baseline."""
+    """level 0: the portable kernels (what the GPU outputs are compared with); 1: the reference's
+    x86 level (8-row groups, AVX2 block sums), the same bits, timed as the CPU baseline."""
     w = np.ascontiguousarray(w, dtype=np.uint8)
     x = _f32(x).ravel()
     assert w.size == n_out * row_bytes(ty, k) and x.size >= rows * k
