@@ -268,7 +268,7 @@ def cpu_layer_baseline(copies, xs, seconds):
         "kind": "port",
         "level": "x86 (AVX2 block sums, crates/kernels-cpu/src/gemv/x86.rs)",
         "sample": f"{n} Q4_K decode layers (5 GEMVs incl. Q8_K activation quantization) in {dt:.1f} s on "
-                  f"{threads} threads (this box's CPU share for one GPU); one layer at 1 thread: "
+                  f"{threads} threads (the host's CPU share for one GPU); one layer at 1 thread: "
                   f"{one * 1e3:.2f} ms = {total_w / one / 1e9:.2f} GB/s",
         "ms_per_layer": round(dt / n * 1e3, 3),
         "one_thread_gbs": round(total_w / one / 1e9, 3),
